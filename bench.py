@@ -1,0 +1,256 @@
+"""Benchmark of the fused metric path on one MI355X; prints ONE JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+
+Headline (``value``): SSIM forward throughput on configs[1] of BASELINE.json,
+an 8x3x1080x1920 uint8 pair (a ~ U{0..255}, b = clip(a + round(N(0, 8)))),
+counted as N*C*H*W samples of one input per second (Gpixel/s).  A "step" is
+one ``fa.ssim(a, b, data_range=255)`` call (fused kernel + finalize) over one
+batch; K steps are timed between device synchronisations, cycling through 4
+distinct resident pairs (398 MB) so the 256 MB Infinity Cache cannot serve the
+inputs.
+
+Also reported: PSNR on configs[2] (8x3x2160x3840 uint8), as achieved GB/s at 2
+bytes per sample and its fraction of the 8 TB/s HBM peak.
+
+``roofline`` is measured live for the dominant kernel (the SSIM strip kernel):
+its launches are bracketed with HIP events on the stream they run on, through
+the C ABI with no finalize sinks, so the average is that kernel alone.  The
+algorithmic bytes are 2 B per input sample; the kernel is VALU-bound, so its
+FP32 work is reported beside the HBM figure.  ``traffic`` is filled from the
+committed rocprofv3 PMC summary when present.
+
+``cpu_baseline`` times the reference's own CPU kernels (oracle/_ref, compiled
+from the reference sources) on a bounded sample of the same workload, on all
+host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X vector FP32 (packed); unpacked issue is half of it
+BASELINE_GPIXS = 25.6     # reference SSIM Gpixel/s, RTX 3090 (README.md:61)
+SSIM_SHAPE = (8, 3, 1080, 1920)
+PSNR_SHAPE = (8, 3, 2160, 3840)
+# FP32 operations per SSIM output pixel of this kernel at K=11 (fused multiply-
+# adds counted as 2): vertical 4 planes x 11 taps, horizontal 4 x 11, moments
+# 4 (x', y', x'y', (x'-y')^2 from 2 loads), epilogue 18.
+SSIM_FLOP_PER_PIXEL = 2 * 44 + 2 * 44 + 8 + 18
+PROFILE_PMC = REPO / "profiles" / "ssim_fwd_1080p8_pmc.txt"
+
+
+def _pairs(torch, shape, sigma, count, dev, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    out = []
+    for _ in range(count):
+        a = torch.randint(0, 256, shape, dtype=torch.uint8, device=dev, generator=g)
+        n = torch.round(torch.randn(shape, device=dev, generator=g) * sigma)
+        b = (a.to(torch.int16) + n.to(torch.int16)).clamp(0, 255).to(torch.uint8)
+        del n
+        out.append((a, b))
+    return out
+
+
+def _time_steps(torch, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def _kernel_ms(torch, launch, iters):
+    """Average duration of `launch` (one kernel) from HIP events on the
+    current stream, which is the stream the C ABI launches on."""
+    st = torch.cuda.current_stream()
+    launch(0)
+    st.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(iters):
+        launch(i)
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def _pmc_traffic():
+    """HBM bytes per launch of the SSIM kernel from the committed PMC summary."""
+    if not PROFILE_PMC.exists():
+        return None
+    for line in PROFILE_PMC.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(seconds=12.0):
+    """Reference CPU SSIM (oracle/_ref) on 1x3x1080x1920 uint8 pairs, all cores."""
+    import numpy as np
+
+    from oracle import ref_cpu
+
+    if not ref_cpu.available():
+        return None
+    cores = os.cpu_count() or 1
+    ref_cpu.load(threads=cores)
+    rng = np.random.default_rng(0)
+    shape = (1,) + SSIM_SHAPE[1:]
+    a = rng.integers(0, 256, shape, dtype=np.uint8)
+    b = np.clip(a.astype(np.int16) + np.round(rng.normal(0, 8, shape)).astype(np.int16),
+                0, 255).astype(np.uint8)
+    ref_cpu.ssim_per_image(a, b)  # warm the pool
+    best = float("inf")
+    t_end = time.perf_counter() + seconds
+    reps = 0
+    while reps < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        ref_cpu.ssim_per_image(a, b)
+        best = min(best, time.perf_counter() - t0)
+        reps += 1
+    samples = a.size
+    return {"value": round(samples / best / 1e9, 4), "unit": "Gpixel/s", "cores": cores,
+            "kind": "reference",
+            "sample": f"reference fa_cpu_ssim (oracle/_ref, -O3 -mavx2 -mfma -ffast-math) on "
+                      f"1x3x1080x1920 uint8, best of {reps} calls over ~{seconds:.0f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the per-shard kernel is the single-GPU one; see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import frame_analytics_amd as fa
+    from frame_analytics_amd import backend
+
+    dev = torch.device("cuda:0")
+    ext = backend.load()
+    assert ext is not None and ext.has_gpu, "gfx950 kernel library did not load"
+    lib = ext.gpu
+
+    # ---------------- SSIM, configs[1] ---------------------------------- #
+    pairs = _pairs(torch, SSIM_SHAPE, 8.0, 4, dev, seed=1)
+    n, c, h, w = SSIM_SHAPE
+    samples = n * c * h * w
+
+    def ssim_step(i):
+        a, b = pairs[i % len(pairs)]
+        return fa.ssim(a, b, data_range=255.0)
+
+    elapsed = _time_steps(torch, ssim_step, args.steps, args.warmup)
+    ms_per_step = elapsed / args.steps * 1e3
+    gpix = samples * args.steps / elapsed / 1e9
+
+    # dominant kernel alone: the C ABI with no finalize sinks launches only it
+    win = fa.gaussian_window_1d(11, 1.5, device=dev, dtype=torch.float32)
+    bpp = backend._ssim_workspace(ext, h, w, 11)
+    partial = torch.empty((n * c, bpp), dtype=torch.float64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def ssim_kernel(i):
+        a, b = pairs[i % len(pairs)]
+        rc = lib.fa_gpu_ssim(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, win.data_ptr(), 11,
+                             127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, None,
+                             partial.data_ptr(), bpp, None, None, 0, stream)
+        assert rc == 0, rc
+
+    k_ms = _kernel_ms(torch, ssim_kernel, max(50, args.steps // 2))
+    bytes_per_launch = 2.0 * samples
+    achieved = bytes_per_launch / (k_ms * 1e-3) / 1e9
+    out_px = n * c * (h - 10) * (w - 10)
+    tflops = out_px * SSIM_FLOP_PER_PIXEL / (k_ms * 1e-3) / 1e12
+    del pairs, partial
+    torch.cuda.empty_cache()
+
+    # ---------------- PSNR, configs[2] ---------------------------------- #
+    ppairs = _pairs(torch, PSNR_SHAPE, 4.0, 2, dev, seed=2)
+    pn = PSNR_SHAPE[0]
+    per = ppairs[0][0].numel() // pn
+
+    def psnr_step(i):
+        a, b = ppairs[i % len(ppairs)]
+        return fa.psnr(a, b, data_range=255.0)
+
+    p_el = _time_steps(torch, psnr_step, args.steps, args.warmup)
+    p_ms = p_el / args.steps * 1e3
+    pbytes = 2.0 * ppairs[0][0].numel()
+    bpi = backend._pixel_workspace(ext, pn, per, 0)
+    ppart = torch.empty((pn, bpi), dtype=torch.float64, device=dev)
+
+    def psnr_kernel(i):
+        a, b = ppairs[i % len(ppairs)]
+        rc = lib.fa_gpu_pixel_reduce(a.data_ptr(), b.data_ptr(), 0, pn, per, 0, 0.0, -1e300,
+                                     ppart.data_ptr(), bpi, None, None, None, None, 0, stream)
+        assert rc == 0, rc
+
+    pk_ms = _kernel_ms(torch, psnr_kernel, max(50, args.steps // 2))
+    del ppairs, ppart
+    torch.cuda.empty_cache()
+
+    line = {
+        "metric": "SSIM Gpixel/s at 1080p x8 uint8 (configs[1]); PSNR 4K x8 HBM GB/s beside it",
+        "value": round(gpix, 3),
+        "unit": "Gpixel/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(gpix / BASELINE_GPIXS, 3),
+        "dtype": "f32",
+        "data": "synthetic uint8 (BASELINE.json generator, 4 resident pairs rotated)",
+        "config": {"workload": "ssim_fwd 8x3x1080x1920 uint8, reduction=mean, 11x11 gaussian",
+                   "batch": n, "channels": c, "height": h, "width": w},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": _pmc_traffic(),
+            "kernel": "ssim_kernel<uint8,float,REDUCE,11>",
+            "kernel_ms": round(k_ms, 4),
+            "valu_tflops": round(tflops, 2),
+            "valu_frac_of_fp32_peak": round(tflops / FP32_PEAK_TFLOPS, 4),
+        },
+        "psnr": {
+            "workload": "psnr 8x3x2160x3840 uint8 (configs[2]), 2 resident pairs rotated",
+            "ms_per_step": round(p_ms, 4),
+            "GBps_end_to_end": round(pbytes / (p_ms * 1e-3) / 1e9, 1),
+            "kernel": "pix_u8_kernel<MSE,16>",
+            "kernel_ms": round(pk_ms, 4),
+            "GBps_kernel": round(pbytes / (pk_ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(pbytes / (pk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        },
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

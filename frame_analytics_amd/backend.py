@@ -1,0 +1,452 @@
+"""Dispatch to the gfx950 kernels: tensors in, raw pointers across the C ABI.
+
+Counterpart of the reference's ``frame_analytics/backend.py``.  Shapes and
+dtypes become ints, tensors become device pointers, and every buffer the
+kernels write -- scratch included -- is allocated here through torch's caching
+allocator, so no call ever allocates inside the library and every call stays
+legal inside a HIP graph capture (reference backend.py:145-153).
+
+Failure policy (deliberately stricter than the reference, which warns once and
+falls back to PyTorch, backend.py:215-224):
+
+* on a machine with a GPU the kernel library must load; if it cannot, the
+  first call raises.  ``FA_NATIVE=0`` is the explicit opt-out.
+* a kernel that returns a non-zero status raises :class:`KernelError`; there is
+  no silent retry on another path.
+* ``try_*`` return ``None`` only when the native path does not apply to the
+  call by design (a CPU tensor, a gradient that the kernel cannot give, a
+  window width without a kernel); the caller then takes the portable path,
+  exactly where the reference would.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Any, Optional
+
+import torch
+
+from ._cabi import KernelError, status_text  # noqa: F401
+
+_SUPPORTED = (torch.uint8, torch.float16, torch.bfloat16, torch.float32, torch.float64)
+
+# mirrors the dtype codes of include/fa_abi.h (reference backend.py:37-43)
+_DTYPE_CODE = {
+    torch.uint8: 0,
+    torch.float16: 1,
+    torch.bfloat16: 2,
+    torch.float32: 3,
+    torch.float64: 4,
+}
+
+_PSNR_NONE = -1.0e300
+_OP_MSE = 0
+_WINDOWS = (3, 5, 7, 9, 11)
+
+
+class _Native:
+    """What :func:`load` hands back: the kernel library and where it came from."""
+
+    def __init__(self) -> None:
+        self.gpu: Any = None
+        self.gpu_origin: Optional[str] = None
+        self.gpu_error: Optional[str] = None
+
+    @property
+    def has_gpu(self) -> bool:
+        return self.gpu is not None
+
+
+_ext: Optional[_Native] = None
+_load_error: Optional[str] = None
+
+
+def _disabled() -> bool:
+    return os.environ.get("FA_NATIVE", "auto").lower() in ("0", "off", "false", "no")
+
+
+def load(force: bool = False) -> Optional[_Native]:
+    """Load the kernel library (building it in-tree first if it is missing).
+
+    Returns ``None`` when native kernels are disabled (``FA_NATIVE=0``) or when
+    the machine has no GPU.  On a machine with a GPU a library that will not
+    load raises: a GPU call must never quietly run somewhere else.
+    """
+    global _ext, _load_error
+    if _ext is not None and not force:
+        return _ext
+    if _disabled():
+        _load_error = "disabled via FA_NATIVE"
+        return None
+    if not torch.cuda.is_available():
+        _load_error = "no GPU visible"
+        return None
+    from . import _cabi
+
+    native = _Native()
+    try:
+        native.gpu, native.gpu_origin = _cabi.load_gpu()
+    except Exception as exc:
+        _load_error = f"{type(exc).__name__}: {exc}"
+        raise RuntimeError(
+            "frame_analytics_amd: the gfx950 kernel library failed to load "
+            f"({_load_error}); set FA_NATIVE=0 to run the portable PyTorch "
+            "path on purpose") from exc
+    _load_error = None
+    _ext = native
+    return _ext
+
+
+def status() -> dict:
+    try:
+        ext = load()
+    except RuntimeError:
+        ext = None
+    path = None
+    if ext is not None:
+        from . import _build
+
+        path = str(_build.library_path())
+    return {
+        "available": ext is not None,
+        "gpu": bool(ext is not None and ext.has_gpu),
+        "error": _load_error,
+        "gpu_source": None if ext is None else ext.gpu_origin,
+        "gpu_library": path,
+    }
+
+
+# --------------------------------------------------------------------------- #
+# marshalling helpers
+# --------------------------------------------------------------------------- #
+
+
+def _f64(device, *shape) -> torch.Tensor:
+    return torch.empty(shape, device=device, dtype=torch.float64)
+
+
+def _contig(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _dev(t: torch.Tensor) -> int:
+    i = t.device.index
+    return torch.cuda.current_device() if i is None else int(i)
+
+
+def _stream(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check(code: int, ext: _Native) -> None:
+    if code != 0:
+        raise KernelError(status_text(code, ext.gpu))
+
+
+_win_cache: dict = {}
+
+
+def _win_f32(win: torch.Tensor) -> torch.Tensor:
+    """The window as contiguous float32, cast once per cached window."""
+    if win.dtype == torch.float32:
+        return _contig(win)
+    key = (id(win), str(win.device))
+    hit = _win_cache.get(key)
+    if hit is not None and hit[0] is win:
+        return hit[1]
+    w = win.to(torch.float32).contiguous()
+    _win_cache[key] = (win, w)
+    return w
+
+
+def _usable(x: torch.Tensor, y: torch.Tensor) -> bool:
+    """Inference-only kernels serve a call unless a gradient is actually wanted
+    (reference backend.py:227-244)."""
+    grad_wanted = torch.is_grad_enabled() and (x.requires_grad or y.requires_grad)
+    return x.dtype in _SUPPORTED and x.dtype == y.dtype and not grad_wanted
+
+
+def _gpu_ext(x: torch.Tensor) -> Optional[_Native]:
+    """The loaded library when ``x`` lives on the GPU, else ``None``."""
+    if not x.is_cuda:
+        return None
+    ext = load()
+    if ext is None or not ext.has_gpu:
+        return None
+    return ext
+
+
+# Workspace sizes depend on the shape only; caching them keeps the runtime
+# query out of graph capture (reference backend.py:247-286).
+_ws_cache: dict = {}
+
+
+def _pixel_workspace(ext: _Native, n_images: int, n_per_image: int, dev: int) -> int:
+    key = ("pix", n_images, n_per_image, dev)
+    hit = _ws_cache.get(key)
+    if hit is None:
+        out = ctypes.c_int(0)
+        _check(ext.gpu.fa_gpu_pixel_workspace(n_images, n_per_image, dev, ctypes.byref(out)), ext)
+        hit = _ws_cache[key] = int(out.value)
+    return hit
+
+
+def _ssim_workspace(ext: _Native, h: int, w: int, k: int) -> int:
+    key = ("ssim", h, w, k)
+    hit = _ws_cache.get(key)
+    if hit is None:
+        out = ctypes.c_int(0)
+        _check(ext.gpu.fa_gpu_ssim_workspace(h, w, k, ctypes.byref(out)), ext)
+        hit = _ws_cache[key] = int(out.value)
+    return hit
+
+
+def _gmsd_workspace(ext: _Native, h: int, w: int, downsample: bool) -> int:
+    key = ("gmsd", h, w, bool(downsample))
+    hit = _ws_cache.get(key)
+    if hit is None:
+        out = ctypes.c_int(0)
+        _check(ext.gpu.fa_gpu_gmsd_workspace(h, w, int(downsample), ctypes.byref(out)), ext)
+        hit = _ws_cache[key] = int(out.value)
+    return hit
+
+
+# --------------------------------------------------------------------------- #
+# pixel losses
+# --------------------------------------------------------------------------- #
+
+
+def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
+              param: float, per_image: bool, psnr_bias: float) -> torch.Tensor:
+    """One fused reduction; exactly one output tensor is allocated."""
+    n = int(x.shape[0])
+    per = x.numel() // n
+    dev = _dev(x)
+    bpi = _pixel_workspace(ext, n, per, dev)
+    partial = _f64(x.device, n, bpi)
+    want_psnr = psnr_bias != _PSNR_NONE
+    out = _f64(x.device, n) if per_image else _f64(x.device)
+    sinks: list = [None, None, None, None]
+    sinks[(2 if want_psnr else 0) + (0 if per_image else 1)] = out
+    _check(ext.gpu.fa_gpu_pixel_reduce(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op, float(param),
+        float(psnr_bias), _ptr(partial), bpi,
+        _ptr(sinks[0]), _ptr(sinks[1]), _ptr(sinks[2]), _ptr(sinks[3]),
+        dev, _stream(x)), ext)
+    return out
+
+
+def try_mse(x: torch.Tensor, y: torch.Tensor, *, per_image: bool,
+            dtype: torch.dtype, psnr_bias: Optional[float] = None) -> Optional[torch.Tensor]:
+    """Squared-error reduction, or PSNR when ``psnr_bias`` (= 10 log10 L^2) is given."""
+    ext = _gpu_ext(x)
+    if ext is None or not _usable(x, y):
+        return None
+    bias = psnr_bias if psnr_bias is not None else _PSNR_NONE
+    out = pixel_gpu(ext, _contig(x), _contig(y), op=_OP_MSE, param=0.0,
+                    per_image=per_image, psnr_bias=bias)
+    return out if dtype == torch.float64 else out.to(dtype)
+
+
+def try_pixel(x: torch.Tensor, y: torch.Tensor, *, op: int, param: float,
+              per_image: bool, dtype: torch.dtype) -> Optional[torch.Tensor]:
+    """L1 / Charbonnier / Huber reduction; ``None`` if no kernel applies."""
+    ext = _gpu_ext(x)
+    if ext is None or not _usable(x, y):
+        return None
+    out = pixel_gpu(ext, _contig(x), _contig(y), op=op, param=param,
+                    per_image=per_image, psnr_bias=_PSNR_NONE)
+    return out if dtype == torch.float64 else out.to(dtype)
+
+
+# --------------------------------------------------------------------------- #
+# SSIM
+# --------------------------------------------------------------------------- #
+
+
+def ssim_autograd_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> bool:
+    """Can the differentiable native SSIM path serve this call?"""
+    return (
+        x.is_cuda
+        and x.dtype == torch.float32
+        and y.dtype == torch.float32
+        and x.shape == y.shape
+        and x.dim() == 4
+        and win_size in _WINDOWS
+        and not torch.cuda.is_current_stream_capturing()
+        and _gpu_ext(x) is not None
+    )
+
+
+ssim_cs_autograd_available = ssim_autograd_available
+
+
+def ssim_fused(x: torch.Tensor, y: torch.Tensor, win: torch.Tensor,
+               shift: float, C1: float, C2: float, want_map: bool):
+    """Forward half of the differentiable SSIM: ``[per_image, total(, map)]``."""
+    ext = load()
+    x, y = _contig(x), _contig(y)
+    winf = _win_f32(win)
+    n, c, h, w = x.shape
+    k = int(winf.numel())
+    bpp = _ssim_workspace(ext, h, w, k)
+    partial = _f64(x.device, n * c, bpp)
+    per_image = _f64(x.device, n)
+    total = _f64(x.device)
+    smap = (torch.empty((n, c, h - k + 1, w - k + 1), device=x.device, dtype=torch.float32)
+            if want_map else None)
+    _check(ext.gpu.fa_gpu_ssim(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
+        float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
+        _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
+    return [per_image, total, smap] if want_map else [per_image, total]
+
+
+def ssim_backward(x, y, dL_dmap, grad_scalar, win, shift, C1, C2, need_dx, need_dy):
+    ext = load()
+    x, y = _contig(x), _contig(y)
+    winf = _win_f32(win)
+    n, c, h, w = x.shape
+    k = int(winf.numel())
+    hout, wout = h - k + 1, w - k + 1
+    has_map = dL_dmap is not None and dL_dmap.numel() > 0
+    dmap = dL_dmap.to(torch.float32).contiguous() if has_map else None
+    gscalar = None if has_map else grad_scalar.to(torch.float32).contiguous().reshape(1)
+    aux = torch.empty((4 if need_dy else 3, n * c, hout, wout), device=x.device,
+                      dtype=torch.float32)
+    dx = torch.empty_like(x) if need_dx else None
+    dy = torch.empty_like(y) if need_dy else None
+    _check(ext.gpu.fa_gpu_ssim_backward(
+        _ptr(x), _ptr(y), _ptr(dmap), _ptr(gscalar), _ptr(winf), k, n, c, h, w,
+        float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
+        _dev(x), _stream(x)), ext)
+    return dx, dy
+
+
+def try_ssim(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
+             shift: float, C1: float, C2: float, reduction: str,
+             return_map: bool, dtype: torch.dtype) -> Optional[torch.Tensor]:
+    """SSIM on the GPU; ``None`` when the native path does not apply.
+
+    Float64 input runs a float64 kernel.  A float64 *map* still takes the
+    portable path, because the C ABI's map buffer is float32.
+    """
+    ext = _gpu_ext(x)
+    if ext is None or not _usable(x, y) or win_size not in _WINDOWS:
+        return None
+    if dtype == torch.float64 and (x.dtype != torch.float64 or return_map):
+        return None
+    from .functional import gaussian_window_1d
+
+    win = _win_f32(gaussian_window_1d(win_size, sigma, device=x.device, dtype=torch.float32))
+    n, c = int(x.shape[0]), int(x.shape[1])
+    h, w = int(x.shape[-2]), int(x.shape[-1])
+    hout, wout = h - win_size + 1, w - win_size + 1
+    x, y = _contig(x), _contig(y)
+    bpp = _ssim_workspace(ext, h, w, win_size)
+    partial = _f64(x.device, n * c, bpp)
+    smap = per_image = total = None
+    if return_map:
+        smap = torch.empty((n, c, hout, wout), device=x.device, dtype=torch.float32)
+    elif reduction == "none":
+        per_image = _f64(x.device, n)
+    else:
+        total = _f64(x.device)
+    _check(ext.gpu.fa_gpu_ssim(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), win_size,
+        float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
+        _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
+    if return_map:
+        return smap if dtype == torch.float32 else smap.to(dtype)
+    return per_image if reduction == "none" else total
+
+
+# --------------------------------------------------------------------------- #
+# MS-SSIM's per-scale primitive
+# --------------------------------------------------------------------------- #
+
+
+def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2):
+    n, c, h, w = x.shape
+    k = int(winf.numel())
+    planes = n * c
+    bpp = _ssim_workspace(ext, h, w, k)
+    partial = _f64(x.device, planes, bpp)
+    partial_cs = _f64(x.device, planes, bpp)
+    out_s = _f64(x.device, planes)
+    out_cs = _f64(x.device, planes)
+    _check(ext.gpu.fa_gpu_ssim_cs(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
+        float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
+        bpp, _ptr(out_s), _ptr(out_cs), _dev(x), _stream(x)), ext)
+    return out_s, out_cs
+
+
+def ssim_cs_forward(x, y, win, shift, C1, C2):
+    """``(ssim, cs)`` plane means from the differentiable native path."""
+    ext = load()
+    return _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2)
+
+
+def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy):
+    ext = load()
+    x, y = _contig(x), _contig(y)
+    winf = _win_f32(win)
+    n, c, h, w = x.shape
+    k = int(winf.numel())
+    hout, wout = h - k + 1, w - k + 1
+    gsf = gs.to(torch.float32).contiguous().reshape(-1)
+    gcsf = gcs.to(torch.float32).contiguous().reshape(-1)
+    aux = torch.empty((4 if need_dy else 3, n * c, hout, wout), device=x.device,
+                      dtype=torch.float32)
+    dx = torch.empty_like(x) if need_dx else None
+    dy = torch.empty_like(y) if need_dy else None
+    _check(ext.gpu.fa_gpu_ssim_cs_backward(
+        _ptr(x), _ptr(y), _ptr(gsf), _ptr(gcsf), _ptr(winf), k, n, c, h, w,
+        float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
+        _dev(x), _stream(x)), ext)
+    return dx, dy
+
+
+def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
+                shift: float, C1: float, C2: float):
+    """``(ssim, cs)`` per plane, shaped ``(N, C)``; ``None`` if unavailable."""
+    ext = _gpu_ext(x)
+    if ext is None or not _usable(x, y):
+        return None
+    k = int(win.numel())
+    if k not in _WINDOWS or x.shape[-2] < k or x.shape[-1] < k:
+        return None
+    n, c = int(x.shape[0]), int(x.shape[1])
+    s, cs = _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2)
+    return s.view(n, c), cs.view(n, c)
+
+
+# --------------------------------------------------------------------------- #
+# GMSD
+# --------------------------------------------------------------------------- #
+
+
+def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsample: bool):
+    """``(gms_mean, gmsd)`` per image, float64; ``None`` if unavailable."""
+    ext = _gpu_ext(x)
+    if ext is None or not _usable(x, y):
+        return None
+    n, c = int(x.shape[0]), int(x.shape[1])
+    h, w = int(x.shape[-2]), int(x.shape[-1])
+    x, y = _contig(x), _contig(y)
+    bpp = _gmsd_workspace(ext, h, w, downsample)
+    psum = _f64(x.device, n * c, bpp)
+    psumsq = _f64(x.device, n * c, bpp)
+    mean = _f64(x.device, n)
+    dev = _f64(x.device, n)
+    _check(ext.gpu.fa_gpu_gmsd(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
+        int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
+        _dev(x), _stream(x)), ext)
+    return mean, dev

@@ -1,0 +1,170 @@
+// Shared device helpers for the gfx950 metric kernels.
+//
+// Everything here is written for CDNA4: 64-lane wavefronts, 256-thread
+// workgroups (4 waves), full-rate FP64 vector arithmetic.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "fa_abi.h"
+
+namespace fa {
+
+constexpr int WAVE = 64;
+constexpr int BLOCK = 256;  // threads per workgroup for every kernel here
+constexpr int WAVES_PER_BLOCK = BLOCK / WAVE;
+
+// --------------------------------------------------------------------------
+// element types
+//
+// The narrow float types travel as raw 16-bit patterns; bfloat16 widens by a
+// shift and half through the hardware conversion.
+// --------------------------------------------------------------------------
+struct half_t { uint16_t bits; };
+struct bf16_t { uint16_t bits; };
+
+template <typename T> struct Elem;
+template <> struct Elem<uint8_t> {
+  __device__ static inline float f(uint8_t v) { return static_cast<float>(v); }
+  __device__ static inline double d(uint8_t v) { return static_cast<double>(v); }
+};
+template <> struct Elem<float> {
+  __device__ static inline float f(float v) { return v; }
+  __device__ static inline double d(float v) { return static_cast<double>(v); }
+};
+template <> struct Elem<double> {
+  __device__ static inline float f(double v) { return static_cast<float>(v); }
+  __device__ static inline double d(double v) { return v; }
+};
+template <> struct Elem<half_t> {
+  __device__ static inline float f(half_t v) {
+    __half_raw r;
+    r.x = v.bits;
+    return __half2float(__half(r));
+  }
+  __device__ static inline double d(half_t v) { return static_cast<double>(f(v)); }
+};
+template <> struct Elem<bf16_t> {
+  __device__ static inline float f(bf16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+  }
+  __device__ static inline double d(bf16_t v) { return static_cast<double>(f(v)); }
+};
+
+// Load one element at working precision CT (float or double).
+template <typename CT, typename T>
+__device__ inline CT load_as(const T* p, int64_t i) {
+  if constexpr (sizeof(CT) == 8) return Elem<T>::d(p[i]);
+  else return Elem<T>::f(p[i]);
+}
+
+// --------------------------------------------------------------------------
+// wave64 / workgroup reductions
+//
+// A butterfly over all 64 lanes, then one slot per wave in LDS; the result is
+// valid in thread 0 only.  The order of additions is fixed, so every sum in
+// this library is deterministic run to run.
+// --------------------------------------------------------------------------
+template <typename V>
+__device__ inline V wave_sum(V v) {
+#pragma unroll
+  for (int off = WAVE / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+template <typename V>
+__device__ inline V block_sum(V v, V* smem /* >= WAVES_PER_BLOCK */) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  if (lane == 0) smem[wave] = v;
+  __syncthreads();
+  V out = V(0);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < WAVES_PER_BLOCK; ++i) out += smem[i];
+  }
+  return out;
+}
+
+// Two independent sums in one pass; smem holds 2 * WAVES_PER_BLOCK slots.
+template <typename V>
+__device__ inline void block_sum2(V a, V b, V* smem, V* oa, V* ob) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  if (lane == 0) {
+    smem[wave] = a;
+    smem[WAVES_PER_BLOCK + wave] = b;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    V sa = V(0), sb = V(0);
+#pragma unroll
+    for (int i = 0; i < WAVES_PER_BLOCK; ++i) {
+      sa += smem[i];
+      sb += smem[WAVES_PER_BLOCK + i];
+    }
+    *oa = sa;
+    *ob = sb;
+  }
+}
+
+}  // namespace fa
+
+// --------------------------------------------------------------------------
+// host-side plumbing shared by the entry points
+// --------------------------------------------------------------------------
+#define FA_HIP_TRY(EXPR)                                                 \
+  do {                                                                   \
+    const hipError_t e_ = (EXPR);                                        \
+    if (e_ != hipSuccess) return -static_cast<int>(e_);                  \
+  } while (0)
+
+#define FA_LAUNCH_CHECK()                                                \
+  do {                                                                   \
+    const hipError_t e_ = hipGetLastError();                             \
+    if (e_ != hipSuccess) return -static_cast<int>(e_);                  \
+  } while (0)
+
+namespace fa {
+
+// Makes `dev` current for the duration of one entry point and restores the
+// caller's device afterwards (the caller's notion of "current" is torch's).
+struct DeviceScope {
+  int prev = -1;
+  bool changed = false;
+  hipError_t status = hipSuccess;
+  explicit DeviceScope(int dev) {
+    status = hipGetDevice(&prev);
+    if (status == hipSuccess && dev >= 0 && dev != prev) {
+      status = hipSetDevice(dev);
+      changed = (status == hipSuccess);
+    }
+  }
+  ~DeviceScope() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+// Compute-unit count of `device`, cached: the attribute query costs as much
+// as a small kernel.
+int cu_count(int device);
+
+// Launches the per-row / total mean reduction over a [nrows, ncols] array of
+// 8-byte partials (uint64 when `exact`, float64 otherwise).  Skipped when every
+// sink is null.  Defined in fa_pixel.hip.
+int launch_finalize(const void* partial, bool exact, int nrows, int ncols,
+                    double n_per_row, double n_total, double psnr_bias,
+                    double* out_per_row, double* out_total,
+                    double* out_psnr_per_row, double* out_psnr_total,
+                    hipStream_t st);
+
+}  // namespace fa
+
+#define FA_DEVICE_SCOPE(DEV)                                             \
+  fa::DeviceScope guard_(DEV);                                           \
+  if (guard_.status != hipSuccess) return -static_cast<int>(guard_.status)

@@ -1,0 +1,586 @@
+// SSIM family on gfx950: forward (mean / per-image / map), the MS-SSIM
+// per-scale primitive (SSIM and cs plane means), and the analytic backward.
+//
+// Semantics follow the reference (fa_cuda.cu:389-784, 1158-1414):
+//   * inputs are shifted by `shift` (= L/2) before filtering; the shift cancels
+//     out of every variance term and is added back to the means
+//   * four blurred moment planes x', y', x'y', (x'-y')^2 -- sigma_x^2+sigma_y^2
+//     is recovered as E[(x'-y')^2] + 2 sigma_xy - (mu_x - mu_y)^2, which keeps
+//     every intermediate the size of the answer
+//   * SSIM = (2 mu_x mu_y + C1)(2 sigma_xy + C2) / ((mu_x^2+mu_y^2+C1)(sigma_x^2+sigma_y^2+C2))
+//   * cs = (2 sigma_xy + C2) / (sigma_x^2 + sigma_y^2 + C2)
+//   * backward: per output pixel b = g dS/dsigma_xx, c = g dS/dsigma_xy,
+//     t_x = g dS/dmu_x - 2 b mu_x' - c mu_y'; then
+//     dx = 2 x' (w * b) + y' (w * c) + (w * t_x) on the full grid.
+//
+// The MI355X-specific choices:
+//   * every kernel is the register-ring / LDS strip engine of fa_strip.h
+//   * the backward computes in float64 throughout (moments, coefficients,
+//     scatter): CDNA4 retires FP64 FMA at the unpacked FP32 rate, so exact-ish
+//     gradients cost registers, not time.  Only the aux maps and dx are stored
+//     as float32, as the C ABI prescribes.
+//   * float64 inputs get a float64 forward instead of a refusal.
+//   * the block partial sums are float64 and reduced in a fixed order.
+#include "fa_strip.h"
+
+#include <algorithm>
+
+namespace fa {
+
+enum { MODE_REDUCE = 0, MODE_MAP = 1, MODE_CS = 2, MODE_PREP = 3, MODE_PREP_CS = 4 };
+
+// Output rows per workgroup.  Part of the partial-buffer geometry, so it is a
+// property of the library, reported through the *_workspace queries.
+constexpr int SSIM_TH = 64;
+
+struct SsimArgs {
+  const void* x;
+  const void* y;
+  int H, W, Hout, Wout, TH, strips, bpp;
+  double shift, C1, C2;
+  const float* win;
+  float* map;           // MODE_MAP
+  double* partial;      // MODE_REDUCE / MAP / CS
+  double* partial_cs;   // MODE_CS
+  const float* dmap;    // MODE_PREP: full upstream map, or null
+  const float* gscalar; // MODE_PREP: device scalar used when dmap is null
+  double gnorm;         // MODE_PREP(_CS): 1/(npix*planes) or 1/npix
+  const float* gs;      // MODE_PREP_CS: per-plane dL/d(mean ssim)
+  const float* gcs;     // MODE_PREP_CS: per-plane dL/d(mean cs)
+  float* ob;
+  float* oc;
+  float* otx;
+  float* oty;
+};
+
+template <typename T, typename CTy, int MODE>
+struct SsimPol {
+  static constexpr int NP = 4;
+  using CT = CTy;
+  struct Raw {
+    CT x, y;
+  };
+
+  const T* __restrict__ x;
+  const T* __restrict__ y;
+  int64_t in_off;
+  int H, W;
+  CT shift, C1, C2;
+  int64_t out_off;
+  int Wout;
+  float* __restrict__ map;
+  float* __restrict__ ob;
+  float* __restrict__ oc;
+  float* __restrict__ otx;
+  float* __restrict__ oty;
+  const float* __restrict__ dmap;
+  CT g_uniform, gS, gCS;
+  double acc_s, acc_cs;
+
+  __device__ inline Raw load(int row, int col) const {
+    // the forward's tap origin is 0, so row and col are never negative
+    if (row < H && col < W) {
+      const int64_t o = in_off + static_cast<int64_t>(row) * W + col;
+      return Raw{load_as<CT>(x, o), load_as<CT>(y, o)};
+    }
+    return Raw{shift, shift};
+  }
+
+  __device__ inline void moments(const Raw& r, CT* m) const {
+    const CT xs = r.x - shift;
+    const CT ys = r.y - shift;
+    const CT d = xs - ys;
+    m[0] = xs;
+    m[1] = ys;
+    m[2] = xs * ys;
+    m[3] = d * d;
+  }
+
+  __device__ inline void emit(int orow, int ocol, const CT* v) {
+    const CT ux = v[0];
+    const CT uy = v[1];
+    const CT mx = ux + shift;
+    const CT my = uy + shift;
+    const CT sxy = v[2] - ux * uy;
+    const CT du = ux - uy;
+    const CT sxx_syy = v[3] + CT(2) * sxy - du * du;
+    const CT A1 = CT(2) * mx * my + C1;
+    const CT A2 = CT(2) * sxy + C2;
+    const CT B1 = mx * mx + my * my + C1;
+    const CT B2 = sxx_syy + C2;
+    if constexpr (MODE == MODE_REDUCE || MODE == MODE_MAP) {
+      const CT s = (A1 * A2) / (B1 * B2);
+      if constexpr (MODE == MODE_MAP)
+        map[out_off + static_cast<int64_t>(orow) * Wout + ocol] = static_cast<float>(s);
+      acc_s += static_cast<double>(s);
+    } else if constexpr (MODE == MODE_CS) {
+      const CT inv = CT(1) / (B1 * B2);
+      acc_s += static_cast<double>(A1 * A2 * inv);
+      acc_cs += static_cast<double>(A2 * B1 * inv);
+    } else {
+      const CT iB1 = CT(1) / B1;
+      const CT iB2 = CT(1) / B2;
+      const CT S = A1 * A2 * iB1 * iB2;
+      const CT k = CT(2) * A2 * iB1 * iB2;
+      const CT dmux = k * (my - mx * A1 * iB1);
+      const CT dmuy = k * (mx - my * A1 * iB1);
+      const int64_t idx = out_off + static_cast<int64_t>(orow) * Wout + ocol;
+      CT b, c, gm;
+      if constexpr (MODE == MODE_PREP) {
+        gm = dmap ? static_cast<CT>(dmap[idx]) : g_uniform;
+        b = -gm * S * iB2;
+        c = CT(2) * gm * A1 * iB1 * iB2;
+      } else {
+        const CT CS = A2 * iB2;
+        gm = gS;
+        b = -(gS * S + gCS * CS) * iB2;
+        c = CT(2) * (gS * A1 * iB1 + gCS) * iB2;
+      }
+      ob[idx] = static_cast<float>(b);
+      oc[idx] = static_cast<float>(c);
+      otx[idx] = static_cast<float>(gm * dmux - CT(2) * b * ux - c * uy);
+      if (oty) oty[idx] = static_cast<float>(gm * dmuy - CT(2) * b * uy - c * ux);
+    }
+  }
+};
+
+template <typename T, typename CT, int MODE, int KW>
+__global__ __launch_bounds__(BLOCK) void ssim_kernel(SsimArgs a) {
+  __shared__ CT sbuf[2][PH][4][HROW];
+  __shared__ double sred[2 * WAVES_PER_BLOCK];
+
+  const int plane = blockIdx.x / a.bpp;
+  const int tile = blockIdx.x - plane * a.bpp;
+  const int chunk = tile / a.strips;
+  const int strip = tile - chunk * a.strips;
+
+  SsimPol<T, CT, MODE> pol;
+  pol.x = static_cast<const T*>(a.x);
+  pol.y = static_cast<const T*>(a.y);
+  pol.in_off = static_cast<int64_t>(plane) * a.H * a.W;
+  pol.H = a.H;
+  pol.W = a.W;
+  pol.shift = static_cast<CT>(a.shift);
+  pol.C1 = static_cast<CT>(a.C1);
+  pol.C2 = static_cast<CT>(a.C2);
+  pol.out_off = static_cast<int64_t>(plane) * a.Hout * a.Wout;
+  pol.Wout = a.Wout;
+  pol.map = a.map;
+  pol.ob = a.ob;
+  pol.oc = a.oc;
+  pol.otx = a.otx;
+  pol.oty = a.oty;
+  pol.dmap = a.dmap;
+  pol.g_uniform = CT(0);
+  pol.gS = CT(0);
+  pol.gCS = CT(0);
+  if constexpr (MODE == MODE_PREP) {
+    if (!a.dmap) pol.g_uniform = static_cast<CT>(a.gscalar[0]) * static_cast<CT>(a.gnorm);
+  }
+  if constexpr (MODE == MODE_PREP_CS) {
+    pol.gS = static_cast<CT>(a.gs[plane]) * static_cast<CT>(a.gnorm);
+    pol.gCS = static_cast<CT>(a.gcs[plane]) * static_cast<CT>(a.gnorm);
+  }
+  pol.acc_s = 0.0;
+  pol.acc_cs = 0.0;
+
+  strip_engine<SsimPol<T, CT, MODE>, KW>(pol, a.win, 0, a.Hout, a.Wout, a.TH, strip,
+                                         chunk, sbuf);
+
+  const int64_t slot = static_cast<int64_t>(plane) * a.bpp + tile;
+  if constexpr (MODE == MODE_REDUCE || MODE == MODE_MAP) {
+    const double s = block_sum(pol.acc_s, sred);
+    if (threadIdx.x == 0) a.partial[slot] = s;
+  } else if constexpr (MODE == MODE_CS) {
+    double s = 0.0, scs = 0.0;
+    block_sum2(pol.acc_s, pol.acc_cs, sred, &s, &scs);
+    if (threadIdx.x == 0) {
+      a.partial[slot] = s;
+      a.partial_cs[slot] = scs;
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// backward scatter: the coefficient maps correlated back onto the full grid
+// (zero outside the valid Hout x Wout support) and combined with x', y'.
+// --------------------------------------------------------------------------
+struct ScatterArgs {
+  const float* x;
+  const float* y;
+  const float* ab;
+  const float* ac;
+  const float* atx;
+  const float* aty;
+  float* dx;
+  float* dy;
+  const float* win;
+  int H, W, Hout, Wout, TH, strips, bpp;
+  double shift;
+};
+
+template <bool DY>
+struct ScatterPol {
+  static constexpr int NP = DY ? 4 : 3;
+  using CT = double;
+  struct Raw {
+    float v[NP];
+  };
+
+  const float* __restrict__ aux[4];
+  int64_t aux_off;
+  int Hout, Wout;
+  const float* __restrict__ x;
+  const float* __restrict__ y;
+  int64_t img_off;
+  int W;
+  double shift;
+  float* __restrict__ dx;
+  float* __restrict__ dy;
+
+  __device__ inline Raw load(int row, int col) const {
+    Raw r;
+    if (row >= 0 && row < Hout && col >= 0 && col < Wout) {
+      const int64_t o = aux_off + static_cast<int64_t>(row) * Wout + col;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) r.v[p] = aux[p][o];
+    } else {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) r.v[p] = 0.0f;
+    }
+    return r;
+  }
+
+  __device__ inline void moments(const Raw& r, double* m) const {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) m[p] = static_cast<double>(r.v[p]);
+  }
+
+  __device__ inline void emit(int orow, int ocol, const double* v) {
+    const int64_t o = img_off + static_cast<int64_t>(orow) * W + ocol;
+    const double xv = static_cast<double>(x[o]) - shift;
+    const double yv = static_cast<double>(y[o]) - shift;
+    if (dx) dx[o] = static_cast<float>(2.0 * xv * v[0] + yv * v[1] + v[2]);
+    if constexpr (DY) dy[o] = static_cast<float>(2.0 * yv * v[0] + xv * v[1] + v[3]);
+  }
+};
+
+template <int KW, bool DY>
+__global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
+  constexpr int NP = ScatterPol<DY>::NP;
+  __shared__ double sbuf[2][PH][NP][HROW];
+
+  const int plane = blockIdx.x / a.bpp;
+  const int tile = blockIdx.x - plane * a.bpp;
+  const int chunk = tile / a.strips;
+  const int strip = tile - chunk * a.strips;
+
+  ScatterPol<DY> pol;
+  pol.aux[0] = a.ab;
+  pol.aux[1] = a.ac;
+  pol.aux[2] = a.atx;
+  pol.aux[3] = a.aty;
+  pol.aux_off = static_cast<int64_t>(plane) * a.Hout * a.Wout;
+  pol.Hout = a.Hout;
+  pol.Wout = a.Wout;
+  pol.x = a.x;
+  pol.y = a.y;
+  pol.img_off = static_cast<int64_t>(plane) * a.H * a.W;
+  pol.W = a.W;
+  pol.shift = a.shift;
+  pol.dx = a.dx;
+  pol.dy = a.dy;
+  strip_engine<ScatterPol<DY>, KW>(pol, a.win, -(KW - 1), a.H, a.W, a.TH, strip, chunk, sbuf);
+}
+
+// Per-plane means of two partial arrays (MS-SSIM keeps planes apart).
+__global__ __launch_bounds__(BLOCK) void planes2_kernel(const double* __restrict__ pa,
+                                                        const double* __restrict__ pb,
+                                                        int ncols, double npix,
+                                                        double* __restrict__ oa,
+                                                        double* __restrict__ ob) {
+  __shared__ double smem[2 * WAVES_PER_BLOCK];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * ncols;
+  double a = 0.0, b = 0.0;
+  for (int i = threadIdx.x; i < ncols; i += BLOCK) {
+    a += pa[base + i];
+    b += pb[base + i];
+  }
+  double sa = 0.0, sb = 0.0;
+  block_sum2(a, b, smem, &sa, &sb);
+  if (threadIdx.x == 0) {
+    oa[blockIdx.x] = sa / npix;
+    ob[blockIdx.x] = sb / npix;
+  }
+}
+
+// --------------------------------------------------------------------------
+// host dispatch
+// --------------------------------------------------------------------------
+template <typename T, typename CT, int MODE>
+static int launch_ssim_k(int K, dim3 grid, hipStream_t st, const SsimArgs& a) {
+  switch (K) {
+    case 3: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 3>), grid, dim3(BLOCK), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 5>), grid, dim3(BLOCK), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 7>), grid, dim3(BLOCK), 0, st, a); break;
+    case 9: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 9>), grid, dim3(BLOCK), 0, st, a); break;
+    case 11: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 11>), grid, dim3(BLOCK), 0, st, a); break;
+    default: return FA_E_WINDOW;
+  }
+  FA_LAUNCH_CHECK();
+  return FA_OK;
+}
+
+template <int MODE>
+static int launch_ssim(int dtype, int K, dim3 grid, hipStream_t st, const SsimArgs& a) {
+  switch (dtype) {
+    case FA_U8: return launch_ssim_k<uint8_t, float, MODE>(K, grid, st, a);
+    case FA_F16: return launch_ssim_k<half_t, float, MODE>(K, grid, st, a);
+    case FA_BF16: return launch_ssim_k<bf16_t, float, MODE>(K, grid, st, a);
+    case FA_F32: return launch_ssim_k<float, float, MODE>(K, grid, st, a);
+    case FA_F64: return launch_ssim_k<double, double, MODE>(K, grid, st, a);
+    default: return FA_E_DTYPE;
+  }
+}
+
+template <bool DY>
+static int launch_scatter_k(int K, dim3 grid, hipStream_t st, const ScatterArgs& a) {
+  switch (K) {
+    case 3: hipLaunchKernelGGL((scatter_kernel<3, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((scatter_kernel<5, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((scatter_kernel<7, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 9: hipLaunchKernelGGL((scatter_kernel<9, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 11: hipLaunchKernelGGL((scatter_kernel<11, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    default: return FA_E_WINDOW;
+  }
+  FA_LAUNCH_CHECK();
+  return FA_OK;
+}
+
+// Validates the common SSIM arguments and derives the output geometry.
+static int ssim_shape(int N, int C, int H, int W, int K, int* Hout, int* Wout) {
+  if (N <= 0 || C <= 0 || H <= 0 || W <= 0) return FA_E_SHAPE;
+  if (K < 3 || K > FA_MAX_WIN || (K & 1) == 0) return FA_E_WINDOW;
+  *Hout = H - K + 1;
+  *Wout = W - K + 1;
+  if (*Hout <= 0 || *Wout <= 0) return FA_E_SHAPE;
+  return FA_OK;
+}
+
+// Workgroups of a strip-engine launch over `planes` planes; the grid is 1-D.
+static int grid_of(int64_t planes, int64_t per_plane, dim3* grid) {
+  const int64_t total = planes * per_plane;
+  if (total <= 0 || total > (static_cast<int64_t>(INT32_MAX) / BLOCK)) return FA_E_SHAPE;
+  *grid = dim3(static_cast<unsigned>(total));
+  return FA_OK;
+}
+
+// The coefficient pass plus the scatter, shared by both backward entry points.
+template <int MODE>
+static int ssim_backward_impl(const float* x, const float* y, const float* dmap,
+                              const float* gscalar, const float* gs,
+                              const float* gcs, const float* win, int K, int N,
+                              int C, int H, int W, double shift, double C1,
+                              double C2, float* aux, float* dx, float* dy,
+                              hipStream_t st) {
+  int Hout = 0, Wout = 0;
+  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  const int64_t npix = static_cast<int64_t>(Hout) * Wout;
+  const int64_t aux_stride = planes * npix;
+
+  SsimArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.H = H;
+  a.W = W;
+  a.Hout = Hout;
+  a.Wout = Wout;
+  a.TH = SSIM_TH;
+  int chunks = 0;
+  strip_grid(Hout, Wout, K, SSIM_TH, &a.strips, &chunks);
+  a.bpp = a.strips * chunks;
+  a.shift = shift;
+  a.C1 = C1;
+  a.C2 = C2;
+  a.win = win;
+  a.dmap = dmap;
+  a.gscalar = gscalar;
+  a.gs = gs;
+  a.gcs = gcs;
+  a.gnorm = MODE == MODE_PREP ? 1.0 / (static_cast<double>(npix) * static_cast<double>(planes))
+                              : 1.0 / static_cast<double>(npix);
+  a.ob = aux;
+  a.oc = aux + aux_stride;
+  a.otx = aux + 2 * aux_stride;
+  a.oty = dy ? aux + 3 * aux_stride : nullptr;
+  dim3 grid;
+  rc = grid_of(planes, a.bpp, &grid);
+  if (rc != FA_OK) return rc;
+  rc = launch_ssim_k<float, double, MODE>(K, grid, st, a);
+  if (rc != FA_OK) return rc;
+
+  ScatterArgs s = {};
+  s.x = x;
+  s.y = y;
+  s.ab = a.ob;
+  s.ac = a.oc;
+  s.atx = a.otx;
+  s.aty = a.oty;
+  s.dx = dx;
+  s.dy = dy;
+  s.win = win;
+  s.H = H;
+  s.W = W;
+  s.Hout = Hout;
+  s.Wout = Wout;
+  s.TH = SSIM_TH;
+  strip_grid(H, W, K, SSIM_TH, &s.strips, &chunks);
+  s.bpp = s.strips * chunks;
+  s.shift = shift;
+  rc = grid_of(planes, s.bpp, &grid);
+  if (rc != FA_OK) return rc;
+  return dy ? launch_scatter_k<true>(K, grid, st, s) : launch_scatter_k<false>(K, grid, st, s);
+}
+
+}  // namespace fa
+
+using namespace fa;
+
+extern "C" {
+
+// reference: fa_cuda.cu:1158-1165 (fa_cuda_ssim_workspace)
+FA_API int fa_gpu_ssim_workspace(int H, int W, int K, int* out_bpp) {
+  if (!out_bpp) return FA_E_ARG;
+  int Hout = 0, Wout = 0;
+  const int rc = ssim_shape(1, 1, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  int strips = 0, chunks = 0;
+  strip_grid(Hout, Wout, K, SSIM_TH, &strips, &chunks);
+  *out_bpp = strips * chunks;
+  return FA_OK;
+}
+
+// reference: fa_cuda.cu:1167-1223 (fa_cuda_ssim)
+FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
+                       int H, int W, const float* win, int K, double shift,
+                       double C1, double C2, float* map_out, double* partial,
+                       int bpp, double* out_per_image, double* out_total,
+                       int device, void* stream) {
+  if (!x || !y || !win || !partial) return FA_E_ARG;
+  int Hout = 0, Wout = 0;
+  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  int strips = 0, chunks = 0;
+  strip_grid(Hout, Wout, K, SSIM_TH, &strips, &chunks);
+  if (bpp != strips * chunks) return FA_E_ARG;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  SsimArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.H = H;
+  a.W = W;
+  a.Hout = Hout;
+  a.Wout = Wout;
+  a.TH = SSIM_TH;
+  a.strips = strips;
+  a.bpp = bpp;
+  a.shift = shift;
+  a.C1 = C1;
+  a.C2 = C2;
+  a.win = win;
+  a.map = map_out;
+  a.partial = partial;
+  dim3 grid;
+  rc = grid_of(static_cast<int64_t>(N) * C, bpp, &grid);
+  if (rc != FA_OK) return rc;
+  rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, grid, st, a)
+               : launch_ssim<MODE_REDUCE>(dtype, K, grid, st, a);
+  if (rc != FA_OK) return rc;
+
+  // each image owns C consecutive plane rows of `partial`
+  const double npix = static_cast<double>(Hout) * Wout;
+  return launch_finalize(partial, false, N, C * bpp, npix * C,
+                         npix * C * static_cast<double>(N), FA_PSNR_NONE,
+                         out_per_image, out_total, nullptr, nullptr, st);
+}
+
+// reference: fa_cuda.cu:1235-1283 (fa_cuda_ssim_cs)
+FA_API int fa_gpu_ssim_cs(const void* x, const void* y, int dtype, int N,
+                          int C, int H, int W, const float* win, int K,
+                          double shift, double C1, double C2, double* partial,
+                          double* partial_cs, int bpp, double* out_s,
+                          double* out_cs, int device, void* stream) {
+  if (!x || !y || !win || !partial || !partial_cs || !out_s || !out_cs) return FA_E_ARG;
+  int Hout = 0, Wout = 0;
+  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  int strips = 0, chunks = 0;
+  strip_grid(Hout, Wout, K, SSIM_TH, &strips, &chunks);
+  if (bpp != strips * chunks) return FA_E_ARG;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  SsimArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.H = H;
+  a.W = W;
+  a.Hout = Hout;
+  a.Wout = Wout;
+  a.TH = SSIM_TH;
+  a.strips = strips;
+  a.bpp = bpp;
+  a.shift = shift;
+  a.C1 = C1;
+  a.C2 = C2;
+  a.win = win;
+  a.partial = partial;
+  a.partial_cs = partial_cs;
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  dim3 grid;
+  rc = grid_of(planes, bpp, &grid);
+  if (rc != FA_OK) return rc;
+  rc = launch_ssim<MODE_CS>(dtype, K, grid, st, a);
+  if (rc != FA_OK) return rc;
+  hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
+                     partial, partial_cs, bpp, static_cast<double>(Hout) * Wout, out_s, out_cs);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
+}
+
+// reference: fa_cuda.cu:1299-1353 (fa_cuda_ssim_backward)
+FA_API int fa_gpu_ssim_backward(const float* x, const float* y,
+                                const float* dL_dmap, const float* grad_scalar,
+                                const float* win, int K, int N, int C, int H,
+                                int W, double shift, double C1, double C2,
+                                float* aux, float* dx, float* dy, int device,
+                                void* stream) {
+  if (!x || !y || !win || !aux) return FA_E_ARG;
+  if (!dx && !dy) return FA_E_ARG;
+  if (!dL_dmap && !grad_scalar) return FA_E_ARG;
+  FA_DEVICE_SCOPE(device);
+  return ssim_backward_impl<MODE_PREP>(x, y, dL_dmap, grad_scalar, nullptr, nullptr, win, K,
+                                       N, C, H, W, shift, C1, C2, aux, dx, dy,
+                                       static_cast<hipStream_t>(stream));
+}
+
+// reference: fa_cuda.cu:1365-1414 (fa_cuda_ssim_cs_backward)
+FA_API int fa_gpu_ssim_cs_backward(const float* x, const float* y,
+                                   const float* gs, const float* gcs,
+                                   const float* win, int K, int N, int C,
+                                   int H, int W, double shift, double C1,
+                                   double C2, float* aux, float* dx,
+                                   float* dy, int device, void* stream) {
+  if (!x || !y || !gs || !gcs || !win || !aux) return FA_E_ARG;
+  if (!dx && !dy) return FA_E_ARG;
+  FA_DEVICE_SCOPE(device);
+  return ssim_backward_impl<MODE_PREP_CS>(x, y, nullptr, nullptr, gs, gcs, win, K, N, C, H, W,
+                                          shift, C1, C2, aux, dx, dy,
+                                          static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,164 @@
+// The separable-window strip engine behind every SSIM-family kernel.
+//
+// One workgroup of 256 lanes owns a strip of 256 consecutive *input* columns
+// and a chunk of TH output rows of one plane.  Each lane owns exactly one input
+// column and walks down it:
+//
+//   vertical pass (registers).  The lane turns every input row it loads into
+//     NP "moment" values and keeps the last RS rows of them in a register ring.
+//     Every phase it loads PH new rows and forms the KW-tap vertical sum of
+//     PH output rows -- no LDS traffic, no bank conflicts, and because the ring
+//     slot of every row is a compile-time constant after unrolling one ring
+//     cycle, no register moves either.
+//
+//   horizontal pass (LDS).  The PH x NP vertical sums of all 256 columns go to
+//     one of two LDS buffers; after a single barrier wave i takes phase row i
+//     and lane g takes output columns 4g..4g+3, reading the 16 values it needs
+//     per plane with ds_read_b128 (consecutive lanes, consecutive 16-byte
+//     chunks: conflict free).  Double buffering means one barrier per phase.
+//
+// A strip yields 256 - (KW-1) output columns; neighbouring strips overlap by
+// KW-1 input columns, and neighbouring row chunks by KW-1 input rows.
+//
+// What the lane loads, which moments it forms and what happens to each output
+// pixel is a policy (see fa_ssim.hip): the SSIM forward (4 moments, float32 or
+// float64), the backward coefficient pass, and the backward scatter (the
+// coefficient maps filtered back onto the full grid, which is the same
+// correlation with the input origin moved back by KW-1 and zero padding).
+#pragma once
+
+#include "fa_common.h"
+
+namespace fa {
+
+constexpr int STRIP_COLS = BLOCK;  // input columns per workgroup, one per lane
+constexpr int PH = WAVES_PER_BLOCK;  // output rows per phase: one per wave
+constexpr int HROW = STRIP_COLS + 16;  // LDS row pitch, room for the last 16-wide read
+constexpr int COLS_PER_LANE = 4;       // horizontal outputs per lane per phase
+
+template <int KW>
+struct StripGeom {
+  static constexpr int OUTW = STRIP_COLS - (KW - 1);        // output columns per strip
+  static constexpr int RS = ((KW - 1 + PH + PH - 1) / PH) * PH;  // ring rows
+  static constexpr int NCYC = RS / PH;                        // phases per ring cycle
+};
+
+// Strip / chunk counts of an out_H x out_W output grid.
+inline void strip_grid(int out_H, int out_W, int K, int TH, int* strips, int* chunks) {
+  const int outw = STRIP_COLS - (K - 1);
+  *strips = (out_W + outw - 1) / outw;
+  *chunks = (out_H + TH - 1) / TH;
+}
+
+template <typename CT>
+struct LdsVec;  // 16-byte LDS vector of CT
+template <> struct LdsVec<float> { using type = float4; static constexpr int N = 4; };
+template <> struct LdsVec<double> { using type = double2; static constexpr int N = 2; };
+
+// Runs the whole strip for one (plane, strip, chunk) workgroup.
+//   in_H, in_W : input grid (values outside it are whatever Pol::load returns)
+//   off        : input row/column of tap 0 for output (0, 0): 0 for a valid
+//                correlation, -(KW-1) for the transposed (scatter) one
+//   out_H,out_W: output grid
+template <class Pol, int KW>
+__device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
+                                    int off, int out_H, int out_W, int TH,
+                                    int strip, int chunk,
+                                    typename Pol::CT (*sbuf)[PH][Pol::NP][HROW]) {
+  using CT = typename Pol::CT;
+  using Raw = typename Pol::Raw;
+  constexpr int NP = Pol::NP;
+  constexpr int OUTW = StripGeom<KW>::OUTW;
+  constexpr int RS = StripGeom<KW>::RS;
+  constexpr int NCYC = StripGeom<KW>::NCYC;
+  using V16 = typename LdsVec<CT>::type;
+  constexpr int VN = LdsVec<CT>::N;
+  constexpr int NREAD = 16 / VN;  // 16-byte LDS reads per plane per lane
+
+  CT w[KW];
+#pragma unroll
+  for (int j = 0; j < KW; ++j) w[j] = static_cast<CT>(win[j]);
+
+  const int lane = threadIdx.x;
+  const int col0 = strip * OUTW;          // first output column of the strip
+  const int in_col = col0 + off + lane;   // this lane's input column
+  const int r0 = chunk * TH;              // first output row of the chunk
+  const int rows_here = min(TH, out_H - r0);
+  const int in_row0 = r0 + off;           // input row of tap 0 for output row r0
+  const int nph = (rows_here + PH - 1) / PH;
+
+  CT ring[RS][NP];
+#pragma unroll
+  for (int i = 0; i < KW - 1; ++i) pol.moments(pol.load(in_row0 + i, in_col), ring[i]);
+
+  Raw pend[PH];
+#pragma unroll
+  for (int i = 0; i < PH; ++i) pend[i] = pol.load(in_row0 + KW - 1 + i, in_col);
+
+  const int hrow = threadIdx.x / WAVE;          // phase row of this wave
+  const int oc_l = COLS_PER_LANE * (threadIdx.x % WAVE);  // strip-local output column
+
+  for (int qc = 0; qc < nph; qc += NCYC) {
+#pragma unroll
+    for (int u = 0; u < NCYC; ++u) {
+      const int q = qc + u;
+      if (q < nph) {  // uniform across the workgroup
+#pragma unroll
+        for (int i = 0; i < PH; ++i) pol.moments(pend[i], ring[(KW - 1 + u * PH + i) % RS]);
+        if (q + 1 < nph) {
+#pragma unroll
+          for (int i = 0; i < PH; ++i)
+            pend[i] = pol.load(in_row0 + KW - 1 + (q + 1) * PH + i, in_col);
+        }
+
+        // ---- vertical taps, from the register ring ----------------------
+        CT (*dst)[NP][HROW] = sbuf[q & 1];
+#pragma unroll
+        for (int i = 0; i < PH; ++i) {
+          CT v[NP];
+#pragma unroll
+          for (int p = 0; p < NP; ++p) v[p] = CT(0);
+#pragma unroll
+          for (int j = 0; j < KW; ++j) {
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+              v[p] = fma(w[j], ring[(u * PH + i + j) % RS][p], v[p]);
+          }
+#pragma unroll
+          for (int p = 0; p < NP; ++p) dst[i][p][lane] = v[p];
+        }
+        __syncthreads();
+
+        // ---- horizontal taps, from LDS ----------------------------------
+        const int orow_l = q * PH + hrow;
+        if (orow_l < rows_here && oc_l < OUTW) {
+          CT h[COLS_PER_LANE][NP];
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            CT in[16];
+            const V16* src = reinterpret_cast<const V16*>(&dst[hrow][p][oc_l]);
+#pragma unroll
+            for (int r = 0; r < NREAD; ++r) {
+              const V16 t = src[r];
+              __builtin_memcpy(&in[r * VN], &t, sizeof(V16));
+            }
+#pragma unroll
+            for (int k = 0; k < COLS_PER_LANE; ++k) {
+              CT a = CT(0);
+#pragma unroll
+              for (int j = 0; j < KW; ++j) a = fma(w[j], in[k + j], a);
+              h[k][p] = a;
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < COLS_PER_LANE; ++k) {
+            const int oc = col0 + oc_l + k;
+            if (oc_l + k < OUTW && oc < out_W) pol.emit(r0 + orow_l, oc, h[k]);
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace fa

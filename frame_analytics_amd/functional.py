@@ -1,0 +1,658 @@
+"""MSE / PSNR / SSIM / MS-SSIM / GMSD / pixel losses -- the public functions.
+
+Same names, signatures, defaults and error behaviour as the reference's
+``frame_analytics/functional.py``; ``import frame_analytics_amd as fa`` is a
+drop-in for ``import frame_analytics as fa`` on these entry points.
+
+Routing for a GPU tensor: the gfx950 kernels behind ``include/fa_abi.h``
+(through :mod:`frame_analytics_amd.backend`).  The portable PyTorch path below
+runs only where the reference runs it too -- CPU tensors,
+``backend_hint="torch"``, a window width without a kernel, the GMS map, a
+float64 working dtype for GMSD, and pixel losses that need a gradient -- and
+it is plain eager PyTorch: no ``torch.compile`` (on ROCm that would emit
+Triton).  ``backend_hint="native"`` raises instead of taking it.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "mse",
+    "psnr",
+    "ssim",
+    "ms_ssim",
+    "gmsd",
+    "gms",
+    "l1",
+    "charbonnier",
+    "huber",
+    "rgb_to_luma",
+    "gaussian_window_1d",
+    "set_compile_enabled",
+    "MS_SSIM_WEIGHTS",
+]
+
+def set_compile_enabled(flag: bool) -> None:
+    """Kept for API compatibility (reference functional.py:55-59).
+
+    This build never compiles the portable path -- on ROCm ``torch.compile``
+    lowers to Triton -- so the flag changes nothing.
+    """
+    del flag
+
+
+# --------------------------------------------------------------------------- #
+# input handling (reference functional.py:141-271)
+# --------------------------------------------------------------------------- #
+
+
+def _infer_data_range(t: torch.Tensor) -> float:
+    if t.dtype == torch.uint8:
+        return 255.0
+    if t.dtype in (torch.int16, torch.int32) or t.dtype == getattr(torch, "uint16", None):
+        return 65535.0
+    return 1.0
+
+
+def _as_nchw(t: torch.Tensor) -> torch.Tensor:
+    """(H,W), (C,H,W) or (N,C,H,W) -> 4-D view."""
+    if t.ndim == 4:
+        return t
+    if t.ndim == 3:
+        return t.unsqueeze(0)
+    if t.ndim == 2:
+        return t.unsqueeze(0).unsqueeze(0)
+    raise ValueError(f"expected 2/3/4-D tensor, got shape {tuple(t.shape)}")
+
+
+def _check_pair(x: torch.Tensor, y: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    if x.shape != y.shape:
+        raise ValueError(f"shape mismatch: {tuple(x.shape)} vs {tuple(y.shape)}")
+    if x.device != y.device:
+        raise ValueError(f"device mismatch: {x.device} vs {y.device}")
+    return _as_nchw(x), _as_nchw(y)
+
+
+def _work_dtype(x: torch.Tensor, dtype: Optional[torch.dtype]) -> torch.dtype:
+    if dtype is not None:
+        return dtype
+    return torch.float64 if x.dtype == torch.float64 else torch.float32
+
+
+# (r, g, b, offset as a fraction of the data range)
+LUMA_COEFFS = {
+    "bt601": (0.299, 0.587, 0.114, 0.0),
+    "bt709": (0.2126, 0.7152, 0.0722, 0.0),
+    "matlab": (65.481 / 255.0, 128.553 / 255.0, 24.966 / 255.0, 16.0 / 255.0),
+}
+
+
+def _resolve_luma(luma) -> Optional[str]:
+    if luma is None or luma is False:
+        return None
+    if luma is True:
+        return "bt601"
+    if isinstance(luma, str):
+        if luma not in LUMA_COEFFS:
+            raise ValueError(f"unknown luma mode {luma!r}; expected one of {sorted(LUMA_COEFFS)}")
+        return luma
+    raise TypeError(f"luma must be None, a bool or a string, got {type(luma).__name__}")
+
+
+def rgb_to_luma(t: torch.Tensor, mode: str = "bt601", *,
+                data_range: Optional[float] = None,
+                dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``(N,3,H,W)`` RGB -> ``(N,1,H,W)`` luma in the input's own units."""
+    t4 = _as_nchw(t)
+    if t4.shape[1] != 3:
+        raise ValueError(f"luma needs a 3-channel image, got {t4.shape[1]} channels")
+    m = _resolve_luma(mode)
+    if m is None:
+        raise ValueError("rgb_to_luma needs a luma convention, not None/False")
+    kr, kg, kb, off = LUMA_COEFFS[m]
+    L = float(data_range) if data_range is not None else _infer_data_range(t4)
+    v = t4.to(_work_dtype(t4, dtype))
+    out = kr * v[:, 0:1] + kg * v[:, 1:2] + kb * v[:, 2:3]
+    return out + off * L if off else out
+
+
+def _crop_border(t: torch.Tensor, b: int) -> torch.Tensor:
+    if not b:
+        return t
+    if b < 0:
+        raise ValueError(f"crop_border must be >= 0, got {b}")
+    h, w = t.shape[-2], t.shape[-1]
+    if h <= 2 * b or w <= 2 * b:
+        raise ValueError(f"crop_border={b} removes the whole {h}x{w} image")
+    return t[..., b:h - b, b:w - b]
+
+
+def _prep(x, y, luma, crop_border: int, data_range: Optional[float]):
+    """Shape check, data range, luma mode, border crop (a view)."""
+    x4, y4 = _check_pair(x, y)
+    L = float(data_range) if data_range is not None else _infer_data_range(x4)
+    mode = _resolve_luma(luma)
+    return _crop_border(x4, crop_border), _crop_border(y4, crop_border), L, mode
+
+
+def _apply_luma(x4, y4, mode, L, dtype):
+    if mode is None:
+        return x4, y4
+    return (rgb_to_luma(x4, mode, data_range=L, dtype=dtype),
+            rgb_to_luma(y4, mode, data_range=L, dtype=dtype))
+
+
+def _no_autocast(t: torch.Tensor):
+    """Convolutions of the portable path run at the tensor's own dtype."""
+    return torch.autocast(device_type=t.device.type, enabled=False)
+
+
+def _check_reduction(reduction: str) -> None:
+    if reduction not in ("mean", "none"):
+        raise ValueError(f"reduction must be 'mean' or 'none', got {reduction!r}")
+
+
+# --------------------------------------------------------------------------- #
+# MSE / PSNR
+# --------------------------------------------------------------------------- #
+
+
+def _sum_sq(x, y, dtype, per_image):
+    d = x.to(dtype) - y.to(dtype)
+    if per_image:
+        return (d * d).sum(dim=(1, 2, 3), dtype=torch.float64) / d[0].numel()
+    return (d * d).sum(dtype=torch.float64) / d.numel()
+
+
+def mse(x: torch.Tensor, y: torch.Tensor, *, reduction: str = "mean",
+        dtype: Optional[torch.dtype] = None, out_dtype: torch.dtype = torch.float64,
+        luma=None, crop_border: int = 0) -> torch.Tensor:
+    """Mean squared error; ``reduction="none"`` gives one value per image.
+
+    uint8 pairs are reduced in exact integer arithmetic on the GPU.
+    """
+    x4, y4, L, mode = _prep(x, y, luma, crop_border, None)
+    wdt = _work_dtype(x4, dtype)
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    _check_reduction(reduction)
+    per_image = reduction == "none"
+    from . import backend
+
+    fast = backend.try_mse(x4, y4, per_image=per_image, dtype=out_dtype)
+    if fast is not None:
+        return fast
+    return _sum_sq(x4, y4, wdt, per_image).to(out_dtype)
+
+
+def psnr(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None,
+         reduction: str = "mean", dtype: Optional[torch.dtype] = None,
+         out_dtype: torch.dtype = torch.float64, eps: float = 0.0, luma=None,
+         crop_border: int = 0) -> torch.Tensor:
+    """Peak signal-to-noise ratio in dB; identical inputs give ``+inf`` unless ``eps``."""
+    _check_reduction(reduction)
+    x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
+    x4, y4 = _apply_luma(x4, y4, mode, L, _work_dtype(x4, dtype))
+    bias = 10.0 * math.log10(L * L)
+    from . import backend
+
+    if not eps:
+        # the dB conversion happens inside the reduction's finalize kernel
+        fast = backend.try_mse(x4, y4, per_image=reduction == "none", dtype=out_dtype,
+                               psnr_bias=bias)
+        if fast is not None:
+            return fast
+    m = mse(x4, y4, reduction=reduction, dtype=dtype, out_dtype=out_dtype)
+    if eps:
+        m = m.clamp_min(eps)
+    # a host constant minus a device term: no H2D copy, capture-safe
+    return bias - 10.0 * torch.log10(m)
+
+
+# --------------------------------------------------------------------------- #
+# SSIM
+# --------------------------------------------------------------------------- #
+
+_window_cache: dict = {}
+
+
+def gaussian_window_1d(win_size: int = 11, sigma: float = 1.5, *, device=None,
+                       dtype=torch.float32) -> torch.Tensor:
+    """1-D factor of MATLAB's ``fspecial('gaussian', win_size, sigma)``.
+
+    Normalised in float64, then cast; its outer product with itself is the
+    normalised 2-D window.  Cached per (size, sigma, device, dtype) so that no
+    call after the first performs a host-to-device copy.
+    """
+    key = (int(win_size), float(sigma), str(device), dtype)
+    w = _window_cache.get(key)
+    if w is None:
+        half = (win_size - 1) / 2.0
+        t = torch.arange(win_size, dtype=torch.float64) - half
+        g = torch.exp(-(t * t) / (2.0 * sigma * sigma))
+        w = (g / g.sum()).to(device=device, dtype=dtype)
+        _window_cache[key] = w
+    return w
+
+
+def _moments_filtered(x4, y4, win, wdt, shift):
+    """Separable 'valid' Gaussian of [x', y', x'^2, y'^2, x'y'], x' = x - shift.
+
+    Returns a tuple of five (N, C, H-K+1, W-K+1) tensors.
+    """
+    xs = x4.to(wdt) - shift
+    ys = y4.to(wdt) - shift
+    planes = torch.stack([xs, ys, xs * xs, ys * ys, xs * ys])  # (5, N, C, H, W)
+    five, n, c, h, w = planes.shape
+    k = win.numel()
+    flat = planes.reshape(five * n * c, 1, h, w)
+    wv = win.to(wdt)
+    with _no_autocast(flat):
+        flat = F.conv2d(flat, wv.view(1, 1, 1, k))
+        flat = F.conv2d(flat, wv.view(1, 1, k, 1))
+    return tuple(flat.reshape(five, n, c, h - k + 1, w - k + 1).unbind(0))
+
+
+def _ssim_and_cs_maps(mom, shift, C1, C2):
+    ux, uy, exx, eyy, exy = mom
+    mx, my = ux + shift, uy + shift
+    sxx = exx - ux * ux
+    syy = eyy - uy * uy
+    sxy = exy - ux * uy
+    cs = (2.0 * sxy + C2) / (sxx + syy + C2)
+    lum = (2.0 * mx * my + C1) / (mx * mx + my * my + C1)
+    return lum * cs, cs
+
+
+def _reject_double_backward() -> None:
+    """The fused backward is a kernel, not an autograd graph: refuse
+    ``create_graph=True`` instead of returning a silently-zero second
+    derivative (reference functional.py:496-518)."""
+    if torch.is_grad_enabled():
+        raise RuntimeError(
+            "frame_analytics_amd's fused SSIM backward is not twice differentiable, "
+            "so create_graph=True (gradient penalties, Hessian-vector products, "
+            "torch.func.hessian, MAML-style inner loops) cannot use it. For a "
+            "second derivative use the portable path:\n"
+            "    ...(x, y, backend_hint='torch')")
+
+
+class _FusedSSIM(torch.autograd.Function):
+    """Differentiable native SSIM: only x, y and the window are saved; the
+    backward recomputes the moments (reference functional.py:521-572)."""
+
+    @staticmethod
+    def forward(ctx, x, y, win, shift, C1, C2, want_map):
+        from . import backend
+
+        res = backend.ssim_fused(x, y, win, shift, C1, C2, want_map)
+        ctx.save_for_backward(x, y, win)
+        ctx.consts = (shift, C1, C2)
+        ctx.want_map = want_map
+        return res[2] if want_map else res[1]
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        from . import backend
+
+        _reject_double_backward()
+        x, y, win = ctx.saved_tensors
+        shift, C1, C2 = ctx.consts
+        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_dx or need_dy):
+            return (None,) * 7
+        empty = torch.empty(0, device=x.device, dtype=torch.float32)
+        if ctx.want_map:
+            dmap, gscalar = grad_out.contiguous(), empty
+        else:
+            # a 1-element device tensor: reading it on the host would sync
+            dmap, gscalar = empty, grad_out.reshape(1)
+        dx, dy = backend.ssim_backward(x, y, dmap, gscalar, win, shift, C1, C2,
+                                       need_dx, need_dy)
+        return (dx if need_dx else None, dy if need_dy else None,
+                None, None, None, None, None)
+
+
+def _matlab_downsample(x: torch.Tensor, f: int) -> torch.Tensor:
+    """MATLAB ``ssim.m``'s automatic f x f box downsample (replicate padding,
+    every f-th sample), reference functional.py:575-586."""
+    if f <= 1:
+        return x
+    n, c, h, w = x.shape
+    pad = f // 2
+    xp = F.pad(x.reshape(n * c, 1, h, w), (pad, pad, pad, pad), mode="replicate")
+    ker = x.new_full((1, 1, f, f), 1.0 / (f * f))
+    with _no_autocast(xp):
+        lp = F.conv2d(xp, ker)
+    return lp.reshape(n, c, lp.shape[-2], lp.shape[-1])[:, :, ::f, ::f].contiguous()
+
+
+def ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None,
+         win_size: int = 11, sigma: float = 1.5, K: Sequence[float] = (0.01, 0.03),
+         reduction: str = "mean", return_map: bool = False,
+         dtype: Optional[torch.dtype] = None, downsample: bool = False,
+         backend_hint: str = "auto", luma=None, crop_border: int = 0) -> torch.Tensor:
+    """Structural similarity (Wang et al. 2004), ``ssim_index.m`` defaults:
+    11x11 Gaussian window, sigma 1.5, K = (0.01, 0.03), 'valid' support."""
+    _check_reduction(reduction)
+    x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
+    wdt = _work_dtype(x4, dtype)
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    C1 = (float(K[0]) * L) ** 2
+    C2 = (float(K[1]) * L) ** 2
+    if downsample:
+        f = max(1, int(round(min(x4.shape[-2], x4.shape[-1]) / 256.0)))
+        if f > 1:
+            x4 = _matlab_downsample(x4.to(wdt), f)
+            y4 = _matlab_downsample(y4.to(wdt), f)
+    if x4.shape[-2] < win_size or x4.shape[-1] < win_size:
+        raise ValueError(f"image {tuple(x4.shape[-2:])} smaller than window {win_size}x{win_size}")
+    shift = 0.5 * L
+    from . import backend
+
+    if (backend_hint != "torch" and (x4.requires_grad or y4.requires_grad)
+            and torch.is_grad_enabled() and reduction == "mean" and not downsample
+            and backend.ssim_autograd_available(x4, y4, win_size)):
+        win = gaussian_window_1d(win_size, sigma, device=x4.device, dtype=torch.float32)
+        return _FusedSSIM.apply(x4, y4, win, shift, C1, C2, return_map)
+
+    if backend_hint != "torch":
+        fast = backend.try_ssim(x4, y4, win_size=win_size, sigma=sigma, shift=shift,
+                                C1=C1, C2=C2, reduction=reduction, return_map=return_map,
+                                dtype=wdt)
+        if fast is not None:
+            return fast
+        if backend_hint == "native":
+            raise RuntimeError("native SSIM backend unavailable for these inputs")
+
+    win = gaussian_window_1d(win_size, sigma, device=x4.device, dtype=wdt)
+    smap, _ = _ssim_and_cs_maps(_moments_filtered(x4, y4, win, wdt, shift), shift, C1, C2)
+    if return_map:
+        return smap
+    if reduction == "none":
+        return smap.mean(dim=(1, 2, 3), dtype=torch.float64)
+    return smap.mean(dtype=torch.float64)
+
+
+# --------------------------------------------------------------------------- #
+# MS-SSIM
+# --------------------------------------------------------------------------- #
+
+# Wang et al. 2003, table 1
+MS_SSIM_WEIGHTS = (0.0448, 0.2856, 0.3001, 0.2363, 0.1333)
+
+_ms_weight_cache: dict = {}
+
+
+def _ms_weights(w, device) -> torch.Tensor:
+    """Scale weights as a cached ``(M, 1, 1)`` float64 device tensor."""
+    key = (w, str(device))
+    t = _ms_weight_cache.get(key)
+    if t is None:
+        t = torch.tensor(w, dtype=torch.float64, device=device).view(-1, 1, 1)
+        _ms_weight_cache[key] = t
+    return t
+
+
+class _FusedSSIMCS(torch.autograd.Function):
+    """Differentiable native ``(ssim, cs)`` plane means, MS-SSIM's per-scale
+    primitive (reference functional.py:749-783)."""
+
+    @staticmethod
+    def forward(ctx, x, y, win, shift, C1, C2):
+        from . import backend
+
+        s, cs = backend.ssim_cs_forward(x, y, win, shift, C1, C2)
+        ctx.save_for_backward(x, y, win)
+        ctx.consts = (shift, C1, C2)
+        return s, cs
+
+    @staticmethod
+    def backward(ctx, g_s, g_cs):
+        from . import backend
+
+        _reject_double_backward()
+        x, y, win = ctx.saved_tensors
+        shift, C1, C2 = ctx.consts
+        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_dx or need_dy):
+            return (None,) * 6
+        if g_s is None:
+            g_s = torch.zeros(x.shape[0] * x.shape[1], device=x.device)
+        if g_cs is None:
+            g_cs = torch.zeros(x.shape[0] * x.shape[1], device=x.device)
+        dx, dy = backend.ssim_cs_backward(x, y, g_s, g_cs, win, shift, C1, C2,
+                                          need_dx, need_dy)
+        return (dx if need_dx else None, dy if need_dy else None, None, None, None, None)
+
+
+def _ssim_cs_pair(x4, y4, win, wdt, shift, C1, C2, backend_hint):
+    """``(ssim, cs)`` plane means, each ``(N, C)``."""
+    from . import backend
+
+    n, c = x4.shape[0], x4.shape[1]
+    if (backend_hint != "torch" and (x4.requires_grad or y4.requires_grad)
+            and torch.is_grad_enabled()
+            and backend.ssim_cs_autograd_available(x4, y4, win.numel())):
+        s, cs = _FusedSSIMCS.apply(x4, y4, win, shift, C1, C2)
+        return s.view(n, c), cs.view(n, c)
+    if backend_hint != "torch":
+        fast = backend.try_ssim_cs(x4, y4, win=win, shift=shift, C1=C1, C2=C2)
+        if fast is not None:
+            return fast
+        if backend_hint == "native":
+            raise RuntimeError("native SSIM/CS backend unavailable for these inputs")
+    smap, cs = _ssim_and_cs_maps(_moments_filtered(x4, y4, win, wdt, shift), shift, C1, C2)
+    return (smap.mean(dim=(2, 3), dtype=torch.float64),
+            cs.mean(dim=(2, 3), dtype=torch.float64))
+
+
+def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None,
+            win_size: int = 11, sigma: float = 1.5, K: Sequence[float] = (0.01, 0.03),
+            weights: Optional[Sequence[float]] = None, reduction: str = "mean",
+            dtype: Optional[torch.dtype] = None, backend_hint: str = "auto",
+            luma=None, crop_border: int = 0) -> torch.Tensor:
+    """Multi-scale SSIM (Wang, Simoncelli, Bovik 2003).
+
+    ``prod_j cs_j^{w_j}`` with the full SSIM at the coarsest scale, scales
+    separated by a non-overlapping 2x2 mean (odd trailing row/column dropped),
+    factors clamped at zero, channels averaged after the product.  Needs
+    ``win_size * 2**(scales-1)`` pixels on a side.
+    """
+    _check_reduction(reduction)
+    w = tuple(float(v) for v in (weights if weights is not None else MS_SSIM_WEIGHTS))
+    if not w:
+        raise ValueError("weights must not be empty")
+    x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
+    wdt = _work_dtype(x4, dtype)
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    C1 = (float(K[0]) * L) ** 2
+    C2 = (float(K[1]) * L) ** 2
+    shift = 0.5 * L
+    scales = len(w)
+    need = win_size * (1 << (scales - 1))
+    if min(x4.shape[-2], x4.shape[-1]) < need:
+        raise ValueError(
+            f"image {tuple(x4.shape[-2:])} is too small for {scales} scales with a "
+            f"{win_size}x{win_size} window; needs at least {need} px on a side")
+
+    win = gaussian_window_1d(win_size, sigma, device=x4.device, dtype=wdt)
+    cx, cy = x4, y4
+    terms = []
+    for i in range(scales):
+        if i:
+            cx = F.avg_pool2d(cx.to(wdt), 2)
+            cy = F.avg_pool2d(cy.to(wdt), 2)
+        s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
+        terms.append(s if i == scales - 1 else cs)
+    # a fractional power of a negative factor is not real: clamp at zero
+    per_plane = torch.stack(terms).clamp_min(0.0).pow(_ms_weights(w, x4.device)).prod(dim=0)
+    per_image = per_plane.mean(dim=1)
+    return per_image if reduction == "none" else per_image.mean()
+
+
+# --------------------------------------------------------------------------- #
+# GMSD / GMS
+# --------------------------------------------------------------------------- #
+
+_prewitt_cache: dict = {}
+
+
+def _prewitt_pair(device, dtype) -> torch.Tensor:
+    """``(2, 1, 3, 3)``: horizontal and vertical Prewitt taps, scaled by 1/3."""
+    key = (str(device), dtype)
+    k = _prewitt_cache.get(key)
+    if k is None:
+        gx = torch.tensor([[1.0, 0.0, -1.0]] * 3, dtype=torch.float64) / 3.0
+        k = torch.stack([gx, gx.t().contiguous()]).unsqueeze(1).to(device=device, dtype=dtype)
+        _prewitt_cache[key] = k
+    return k
+
+
+def _gms_map(x4, y4, wdt, T, eps, downsample):
+    xf, yf = x4.to(wdt), y4.to(wdt)
+    if downsample:
+        xf, yf = F.avg_pool2d(xf, 2), F.avg_pool2d(yf, 2)
+    n, c, h, w = xf.shape
+    if h < 3 or w < 3:
+        raise ValueError(f"image {h}x{w} is smaller than the 3x3 Prewitt window")
+    both = torch.cat([xf, yf], dim=0).reshape(2 * n * c, 1, h, w)
+    with _no_autocast(both):
+        g = F.conv2d(both, _prewitt_pair(xf.device, wdt))  # (2NC, 2, H-2, W-2)
+    g1 = torch.sqrt((g[: n * c] ** 2).sum(dim=1) + eps)
+    g2 = torch.sqrt((g[n * c:] ** 2).sum(dim=1) + eps)
+    q = (2.0 * g1 * g2 + T) / (g1 * g1 + g2 * g2 + T)
+    return q.reshape(n, c, h - 2, w - 2)
+
+
+def _gmsd_common(x, y, data_range, T, eps, downsample, dtype, luma, crop_border,
+                 reduction, return_map, backend_hint):
+    """``(map, None)`` or ``(None, (gms_mean, gmsd))`` per image."""
+    _check_reduction(reduction)
+    x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
+    wdt = _work_dtype(x4, dtype)
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    Tv = float(T) if T is not None else 170.0 * (L / 255.0) ** 2
+    ev = float(eps) if eps is not None else (1e-6 * L) ** 2
+    if backend_hint != "torch":
+        from . import backend
+
+        # the kernel never writes the map and computes in float32
+        native_ok = not return_map and wdt != torch.float64
+        fast = (backend.try_gmsd(x4, y4, T=Tv, eps=ev, downsample=downsample)
+                if native_ok else None)
+        if fast is not None:
+            return None, fast
+        if backend_hint == "native":
+            raise RuntimeError("native GMSD backend unavailable for these inputs"
+                               + (" (return_map=True has no native kernel)" if return_map else ""))
+    q = _gms_map(x4, y4, wdt, Tv, ev, downsample)
+    if return_map:
+        return q, None
+    # widen before the variance: q sits within ~1e-3 of 1 on a good match
+    f = q.reshape(q.shape[0], -1).double()
+    return None, (f.mean(dim=1), f.var(dim=1, correction=0).clamp_min(0.0).sqrt())
+
+
+def gms(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None,
+        T: Optional[float] = None, eps: Optional[float] = None, downsample: bool = True,
+        reduction: str = "mean", return_map: bool = False,
+        dtype: Optional[torch.dtype] = None, luma=None, crop_border: int = 0,
+        backend_hint: str = "auto") -> torch.Tensor:
+    """Mean gradient-magnitude similarity; higher is better, 1.0 is identical."""
+    q, stats = _gmsd_common(x, y, data_range, T, eps, downsample, dtype, luma,
+                            crop_border, reduction, return_map, backend_hint)
+    if q is not None:
+        return q
+    return stats[0] if reduction == "none" else stats[0].mean()
+
+
+def gmsd(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None,
+         T: Optional[float] = None, eps: Optional[float] = None, downsample: bool = True,
+         reduction: str = "mean", return_map: bool = False,
+         dtype: Optional[torch.dtype] = None, luma=None, crop_border: int = 0,
+         backend_hint: str = "auto") -> torch.Tensor:
+    """Gradient magnitude similarity deviation (Xue et al. 2014); lower is better."""
+    q, stats = _gmsd_common(x, y, data_range, T, eps, downsample, dtype, luma,
+                            crop_border, reduction, return_map, backend_hint)
+    if q is not None:
+        return q
+    return stats[1] if reduction == "none" else stats[1].mean()
+
+
+# --------------------------------------------------------------------------- #
+# pixel losses
+# --------------------------------------------------------------------------- #
+
+# op codes of include/fa_abi.h
+_OP_MSE = 0
+_OP_L1 = 1
+_OP_CHARB = 2
+_OP_HUBER = 3
+
+
+def _pixel_terms(name, d, param):
+    if name == "l1":
+        return d.abs()
+    if name == "charbonnier":
+        return torch.sqrt(d * d + param)
+    a = d.abs()
+    return torch.where(a <= param, 0.5 * a * a, param * (a - 0.5 * param))
+
+
+_PIXEL_OPS = {"l1": _OP_L1, "charbonnier": _OP_CHARB, "huber": _OP_HUBER}
+
+
+def _pixel_loss(name, x, y, param, reduction, dtype, out_dtype, luma, crop_border,
+                backend_hint):
+    _check_reduction(reduction)
+    x4, y4, L, mode = _prep(x, y, luma, crop_border, None)
+    wdt = _work_dtype(x4, dtype)
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    per_image = reduction == "none"
+    from . import backend
+
+    if backend_hint != "torch":
+        fast = backend.try_pixel(x4, y4, op=_PIXEL_OPS[name], param=param,
+                                 per_image=per_image, dtype=out_dtype)
+        if fast is not None:
+            return fast
+        if backend_hint == "native":
+            raise RuntimeError(f"native {name} backend unavailable for these inputs")
+    t = _pixel_terms(name, x4.to(wdt) - y4.to(wdt), param)
+    if per_image:
+        out = t.sum(dim=(1, 2, 3), dtype=torch.float64) / t[0].numel()
+    else:
+        out = t.sum(dtype=torch.float64) / t.numel()
+    return out.to(out_dtype)
+
+
+def l1(x: torch.Tensor, y: torch.Tensor, *, reduction: str = "mean",
+       dtype: Optional[torch.dtype] = None, out_dtype: torch.dtype = torch.float64,
+       luma=None, crop_border: int = 0, backend_hint: str = "auto") -> torch.Tensor:
+    """Mean absolute error, in the input's own units."""
+    return _pixel_loss("l1", x, y, 0.0, reduction, dtype, out_dtype, luma, crop_border,
+                       backend_hint)
+
+
+def charbonnier(x: torch.Tensor, y: torch.Tensor, *, eps: float = 1e-3,
+                reduction: str = "mean", dtype: Optional[torch.dtype] = None,
+                out_dtype: torch.dtype = torch.float64, luma=None, crop_border: int = 0,
+                backend_hint: str = "auto") -> torch.Tensor:
+    """``mean sqrt((x - y)^2 + eps^2)``; ``eps`` has the units of the residual."""
+    return _pixel_loss("charbonnier", x, y, float(eps) ** 2, reduction, dtype, out_dtype,
+                       luma, crop_border, backend_hint)
+
+
+def huber(x: torch.Tensor, y: torch.Tensor, *, delta: float = 1.0, reduction: str = "mean",
+          dtype: Optional[torch.dtype] = None, out_dtype: torch.dtype = torch.float64,
+          luma=None, crop_border: int = 0, backend_hint: str = "auto") -> torch.Tensor:
+    """Huber loss, term for term ``torch.nn.HuberLoss``."""
+    if delta <= 0:
+        raise ValueError(f"delta must be > 0, got {delta}")
+    return _pixel_loss("huber", x, y, float(delta), reduction, dtype, out_dtype, luma,
+                       crop_border, backend_hint)

@@ -1,0 +1,167 @@
+/*
+ * frame_analytics_amd -- C ABI of the MI355X (gfx950) metric kernels.
+ *
+ * This is the drop-in boundary for the GPU half of NevermindNilas/frame_analytics.
+ * Every entry point below replaces one `fa_cuda_*` entry point of the reference's
+ * C ABI (reference: frame_analytics/csrc/fa_abi.h) with the same argument list,
+ * the same argument meaning and the same status codes.  Only the prefix differs:
+ * `fa_gpu_` instead of `fa_cuda_`, because the library behind it is hand-written
+ * HIP for CDNA4 and links nothing from CUDA.
+ *
+ * Conventions (identical to the reference, fa_abi.h:12-21):
+ *   - every entry point returns an int status; FA_OK (0) is success
+ *   - a negative status is a HIP runtime error, negated (see fa_gpu_error_string)
+ *   - the caller owns every buffer, scratch included.  Python allocates them
+ *     through torch's caching allocator, which keeps calls legal inside a HIP
+ *     graph capture
+ *   - shapes travel as ints, dtypes as an int code, streams as an opaque
+ *     hipStream_t handle; the device ordinal is explicit on every call
+ *   - nothing here allocates device memory and nothing synchronises
+ */
+#ifndef FRAME_ANALYTICS_AMD_ABI_H
+#define FRAME_ANALYTICS_AMD_ABI_H
+
+#include <stdint.h>
+
+#define FA_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Bumped whenever a signature below changes meaning (reference fa_abi.h:41). */
+#define FA_ABI_VERSION 1
+
+/* dtype codes (reference fa_abi.h:44-48) */
+#define FA_U8 0
+#define FA_F16 1
+#define FA_BF16 2
+#define FA_F32 3
+#define FA_F64 4
+
+/* pixel-loss selector (reference fa_abi.h:51-54) */
+#define FA_OP_MSE 0
+#define FA_OP_L1 1
+#define FA_OP_CHARB 2 /* param = eps^2 */
+#define FA_OP_HUBER 3 /* param = delta */
+
+/* status codes (reference fa_abi.h:57-64); negative = -(hipError_t) */
+#define FA_OK 0
+#define FA_E_DTYPE 1
+#define FA_E_SHAPE 2
+#define FA_E_WINDOW 3
+#define FA_E_OP 4
+#define FA_E_ARG 5
+#define FA_E_INTERNAL 6
+#define FA_E_NOGPU 7
+
+/* "not an MSE reduction, skip the dB conversion" (reference fa_abi.h:67) */
+#define FA_PSNR_NONE (-1.0e300)
+
+/* Largest supported Gaussian window; odd widths 3..11 (reference fa_abi.h:71). */
+#define FA_MAX_WIN 11
+
+/* Replaces fa_cuda_abi_version (reference fa_abi.h:131). */
+FA_API int fa_gpu_abi_version(void);
+
+/* Replaces fa_cuda_error_string (reference fa_abi.h:132). */
+FA_API const char* fa_gpu_error_string(int code);
+
+/* Replaces fa_cuda_device_count (reference fa_abi.h:133). */
+FA_API int fa_gpu_device_count(int* out_count);
+
+/*
+ * Replaces fa_cuda_pixel_workspace (reference fa_abi.h:135-136).
+ * out_bpi: workgroups per image of fa_gpu_pixel_reduce; `partial` must hold
+ * n_images * bpi 8-byte slots.
+ */
+FA_API int fa_gpu_pixel_workspace(int64_t n_images, int64_t n_per_image,
+                                  int device, int* out_bpi);
+
+/*
+ * Replaces fa_cuda_pixel_reduce (reference fa_abi.h:140-147).
+ * partial: [n_images, bpi] 8-byte scratch (uint64 bit patterns for the exact
+ * uint8 MSE/L1 sums, float64 otherwise).  Any of the four sinks may be null;
+ * the psnr sinks are written only when psnr_bias != FA_PSNR_NONE.
+ */
+FA_API int fa_gpu_pixel_reduce(const void* a, const void* b, int dtype,
+                               int64_t n_images, int64_t n_per_image, int op,
+                               double param, double psnr_bias, double* partial,
+                               int bpi, double* out_per_image,
+                               double* out_total, double* out_psnr_per_image,
+                               double* out_psnr_total, int device,
+                               void* stream);
+
+/*
+ * Replaces fa_cuda_ssim_workspace (reference fa_abi.h:149).
+ * out_bpp: partial slots per plane of fa_gpu_ssim / fa_gpu_ssim_cs.
+ */
+FA_API int fa_gpu_ssim_workspace(int H, int W, int K, int* out_bpp);
+
+/*
+ * Replaces fa_cuda_ssim (reference fa_abi.h:152-159).
+ * partial: [N*C, bpp] float64.  map_out: optional [N, C, H-K+1, W-K+1] float32.
+ * out_per_image: N float64 (may be null).  out_total: 1 float64 (may be null).
+ */
+FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
+                       int H, int W, const float* win, int K, double shift,
+                       double C1, double C2, float* map_out, double* partial,
+                       int bpp, double* out_per_image, double* out_total,
+                       int device, void* stream);
+
+/*
+ * Replaces fa_cuda_ssim_cs (reference fa_abi.h:162-168).
+ * out_s / out_cs: N*C float64 each, per-plane means of the SSIM map and of its
+ * contrast-structure factor.
+ */
+FA_API int fa_gpu_ssim_cs(const void* x, const void* y, int dtype, int N,
+                          int C, int H, int W, const float* win, int K,
+                          double shift, double C1, double C2, double* partial,
+                          double* partial_cs, int bpp, double* out_s,
+                          double* out_cs, int device, void* stream);
+
+/*
+ * Replaces fa_cuda_ssim_backward (reference fa_abi.h:174-181).
+ * aux: (dy ? 4 : 3) * N*C * (H-K+1) * (W-K+1) float32 scratch.  Exactly one of
+ * dL_dmap (full map gradient) and grad_scalar (1-element device tensor, the
+ * gradient of the batch-mean SSIM) must be non-null.
+ */
+FA_API int fa_gpu_ssim_backward(const float* x, const float* y,
+                                const float* dL_dmap, const float* grad_scalar,
+                                const float* win, int K, int N, int C, int H,
+                                int W, double shift, double C1, double C2,
+                                float* aux, float* dx, float* dy, int device,
+                                void* stream);
+
+/*
+ * Replaces fa_cuda_ssim_cs_backward (reference fa_abi.h:184-190).
+ * gs / gcs: N*C float32 device scalars, dL/d(plane-mean SSIM) and
+ * dL/d(plane-mean cs).
+ */
+FA_API int fa_gpu_ssim_cs_backward(const float* x, const float* y,
+                                   const float* gs, const float* gcs,
+                                   const float* win, int K, int N, int C,
+                                   int H, int W, double shift, double C1,
+                                   double C2, float* aux, float* dx,
+                                   float* dy, int device, void* stream);
+
+/*
+ * Replaces fa_cuda_gmsd_workspace (reference fa_abi.h:192).
+ * out_bpp: partial slots per plane of fa_gpu_gmsd.
+ */
+FA_API int fa_gpu_gmsd_workspace(int H, int W, int downsample, int* out_bpp);
+
+/*
+ * Replaces fa_cuda_gmsd (reference fa_abi.h:195-200).
+ * psum / psumsq: [N*C, bpp] float64.  out_mean / out_std: N float64 each.
+ */
+FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
+                       int H, int W, double Tc, double eps, int downsample,
+                       double* psum, double* psumsq, int bpp, double* out_mean,
+                       double* out_std, int device, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* FRAME_ANALYTICS_AMD_ABI_H */

@@ -1,0 +1,87 @@
+"""The C-ABI library: builds, loads, exports exactly what include/fa_abi.h
+declares, with the ctypes prototypes the binder uses.  No compute calls (these
+run without a GPU); the status and workspace queries used here are pure host
+arithmetic."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from frame_analytics_amd import _build, _cabi
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "fa_abi.h"
+
+
+def _declared():
+    """name -> number of parameters, for every FA_API function in the header."""
+    txt = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"FA_API\s+[\w\s\*]+?\b(fa_\w+)\s*\(([^)]*)\)\s*;", txt, flags=re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    path = _build.library_path()
+    if not path.exists():
+        _build.build()
+    return _cabi.bind(ctypes.CDLL(str(path)))
+
+
+def test_header_and_binder_agree():
+    decl = _declared()
+    assert len(decl) == 12
+    assert set(decl) == set(_cabi.SIGNATURES)
+    for name, n in decl.items():
+        assert len(_cabi.SIGNATURES[name][0]) == n, name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.fa_gpu_abi_version() == _cabi.FA_ABI_VERSION
+    assert lib.fa_gpu_error_string(0) == b"ok"
+    assert lib.fa_gpu_error_string(3) == b"unsupported window size"
+    assert b"GPU" in lib.fa_gpu_error_string(7)
+
+
+def test_workspace_queries(lib):
+    out = ctypes.c_int(0)
+    assert lib.fa_gpu_ssim_workspace(1080, 1920, 11, ctypes.byref(out)) == 0
+    # 246 output columns per 256-lane strip, 64 output rows per workgroup
+    assert out.value == 8 * 17
+    assert lib.fa_gpu_ssim_workspace(8, 8, 11, ctypes.byref(out)) == 2  # FA_E_SHAPE
+    assert lib.fa_gpu_ssim_workspace(64, 64, 4, ctypes.byref(out)) == 3  # even window
+    assert lib.fa_gpu_ssim_workspace(64, 64, 13, ctypes.byref(out)) == 3
+    assert lib.fa_gpu_ssim_workspace(64, 64, 11, None) == 5  # FA_E_ARG
+    assert lib.fa_gpu_gmsd_workspace(1080, 1920, 1, ctypes.byref(out)) == 0
+    assert out.value == 4 * 9  # 538x958 output: 248-column strips, 64-row chunks
+    assert lib.fa_gpu_gmsd_workspace(5, 5, 1, ctypes.byref(out)) == 2
+
+
+def test_argument_validation_before_any_gpu_work(lib):
+    """Null pointers and bad codes are rejected on the host."""
+    assert lib.fa_gpu_pixel_reduce(None, None, 0, 1, 16, 0, 0.0, -1e300, None, 1,
+                                   None, None, None, None, 0, None) == 5
+    one = ctypes.c_double(0)
+    p = ctypes.addressof(one)
+    assert lib.fa_gpu_pixel_reduce(p, p, 0, 1, 16, 9, 0.0, -1e300, p, 1,
+                                   None, None, None, None, 0, None) == 4  # FA_E_OP
+    assert lib.fa_gpu_pixel_reduce(p, p, 0, 0, 16, 0, 0.0, -1e300, p, 1,
+                                   None, None, None, None, 0, None) == 2
+    assert lib.fa_gpu_ssim(p, p, 0, 1, 1, 64, 64, p, 12, 0.5, 1e-4, 9e-4, None, p, 1,
+                           None, None, 0, None) == 3
+    assert lib.fa_gpu_ssim(p, p, 0, 1, 1, 64, 64, p, 11, 0.5, 1e-4, 9e-4, None, p, 99,
+                           None, None, 0, None) == 5  # bpp mismatch
+    assert lib.fa_gpu_ssim_backward(p, p, None, None, p, 11, 1, 1, 64, 64, 0.5, 1e-4, 9e-4,
+                                    p, p, None, 0, None) == 5  # no upstream gradient
+    assert lib.fa_gpu_gmsd(p, p, 0, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, 99, p, p, 0, None) == 5

@@ -1,0 +1,133 @@
+"""API contract on CPU tensors (the portable eager path) -- runs without a GPU.
+
+These mirror the reference's contract tests (test_metrics.py,
+test_training_metrics.py): argument handling, reductions, luma / crop, error
+behaviour and the module wrappers.  The portable path computes in float32 like
+the reference's, so values are held to the reference's gates (5e-6 SSIM-family,
+exact integer MSE).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import frame_analytics_amd as fa
+from oracle import reference as ref
+from tests.conftest import natural_pair, u8_pair
+
+TOL = 5e-6
+
+
+def test_ssim_mse_psnr_cpu():
+    a, b = natural_pair(97, 131, 7.0, seed=3)
+    x = torch.as_tensor(a, dtype=torch.uint8)
+    y = torch.as_tensor(b, dtype=torch.uint8)
+    assert abs(float(fa.ssim(x, y, data_range=255.0)) - ref.ssim(a[None, None], b[None, None])) < TOL
+    a8, b8 = a.astype(np.uint8)[None, None], b.astype(np.uint8)[None, None]
+    assert float(fa.mse(x, y)) == ref.mse(a8, b8)
+    assert abs(float(fa.psnr(x, y)) - float(ref.psnr(a8, b8))) < 1e-9
+    v2 = float(fa.ssim(x, y, data_range=255.0))
+    assert v2 == float(fa.ssim(x[None], y[None], data_range=255.0)) == float(
+        fa.ssim(x[None, None], y[None, None], data_range=255.0))
+
+
+def test_training_metrics_cpu():
+    a, b = natural_pair(200, 232, 8.0, seed=432)
+    x = torch.as_tensor(a, dtype=torch.uint8)[None, None]
+    y = torch.as_tensor(b, dtype=torch.uint8)[None, None]
+    assert abs(float(fa.ms_ssim(x, y, data_range=255.0)) - ref.ms_ssim(a[None, None], b[None, None])) < TOL
+    m, s = ref.gmsd_stats(a[None, None], b[None, None], 255.0)
+    assert abs(float(fa.gmsd(x, y, data_range=255.0)) - s[0]) < TOL
+    assert abs(float(fa.gms(x, y, data_range=255.0)) - m[0]) < TOL
+    assert abs(float(fa.l1(x, y)) - ref.l1(a, b)) < 1e-9
+    assert abs(float(fa.charbonnier(x, y)) - ref.charbonnier(a, b)) < 1e-6
+    assert abs(float(fa.huber(x, y, delta=4.0)) - ref.huber(a, b, 4.0)) < 1e-9
+
+
+def test_reductions_and_shapes():
+    a, b = u8_pair((5, 1, 64, 64), 20.0, seed=1)
+    x, y = torch.from_numpy(a), torch.from_numpy(b)
+    for fn in (fa.ssim, fa.mse, fa.l1, fa.huber, fa.charbonnier):
+        per = fn(x, y, reduction="none")
+        assert per.shape == (5,)
+    assert fa.psnr(x, y, reduction="none").shape == (5,)
+    assert fa.ssim(x, y, return_map=True).shape == (5, 1, 54, 54)
+    assert abs(float(fa.ssim(x, y, reduction="none").mean()) - float(fa.ssim(x, y))) < 1e-9
+
+
+def test_errors():
+    x = torch.zeros(1, 1, 32, 32)
+    with pytest.raises(ValueError):
+        fa.ssim(x, torch.zeros(1, 1, 32, 33))
+    with pytest.raises(ValueError):
+        fa.ssim(torch.zeros(1, 1, 8, 8), torch.zeros(1, 1, 8, 8))
+    with pytest.raises(ValueError):
+        fa.mse(x, x, reduction="sum")
+    with pytest.raises(ValueError):
+        fa.huber(x, x, delta=0.0)
+    with pytest.raises(ValueError):
+        fa.mse(x, x, crop_border=16)
+    with pytest.raises(ValueError):
+        fa.mse(x, x, crop_border=-1)
+    with pytest.raises(ValueError):
+        fa.psnr(torch.zeros(1, 3, 32, 32), torch.zeros(1, 3, 32, 32), luma="rec2020")
+    with pytest.raises(TypeError):
+        fa.psnr(torch.zeros(1, 3, 32, 32), torch.zeros(1, 3, 32, 32), luma=3)
+    with pytest.raises(ValueError):
+        fa.psnr(torch.zeros(1, 2, 32, 32), torch.zeros(1, 2, 32, 32), luma=True)
+    with pytest.raises(ValueError, match="too small"):
+        fa.ms_ssim(torch.zeros(1, 1, 175, 300), torch.zeros(1, 1, 175, 300), data_range=1.0)
+    with pytest.raises(ValueError):
+        fa.ssim(torch.zeros(2, 2, 2, 16, 16), torch.zeros(2, 2, 2, 16, 16))
+
+
+def test_luma_crop_cpu():
+    rng = np.random.default_rng(12)
+    a = rng.integers(0, 256, (3, 60, 70)).astype(np.float64)
+    b = np.clip(a + 9.0 * rng.standard_normal(a.shape), 0, 255).round()
+    x = torch.from_numpy(a.astype(np.uint8))[None]
+    y = torch.from_numpy(b.astype(np.uint8))[None]
+    for mode in ("bt601", "bt709", "matlab"):
+        ya, yb = ref.crop(ref.rgb_to_luma(a[None], mode), 2), ref.crop(ref.rgb_to_luma(b[None], mode), 2)
+        assert abs(float(fa.ssim(x, y, luma=mode, crop_border=2)) - ref.ssim(ya, yb)) < TOL
+        assert abs(float(fa.psnr(x, y, luma=mode, crop_border=2)) - float(ref.psnr(ya, yb))) < 1e-5
+    assert float(fa.psnr(x, y, luma=True)) == float(fa.psnr(x, y, luma="bt601"))
+
+
+def test_modules_agree_with_functions():
+    a, b = natural_pair(200, 232, 8.0, seed=7)
+    x = torch.as_tensor(a, dtype=torch.uint8)[None, None]
+    y = torch.as_tensor(b, dtype=torch.uint8)[None, None]
+    pairs = [
+        (fa.SSIM(data_range=255.0)(x, y), fa.ssim(x, y, data_range=255.0)),
+        (fa.MSSSIM(data_range=255.0)(x, y), fa.ms_ssim(x, y, data_range=255.0)),
+        (fa.GMSD(data_range=255.0)(x, y), fa.gmsd(x, y, data_range=255.0)),
+        (fa.MSE()(x, y), fa.mse(x, y)),
+        (fa.PSNR()(x, y), fa.psnr(x, y)),
+        (fa.L1()(x, y), fa.l1(x, y)),
+        (fa.Charbonnier(eps=2.0)(x, y), fa.charbonnier(x, y, eps=2.0)),
+        (fa.Huber(delta=3.0)(x, y), fa.huber(x, y, delta=3.0)),
+    ]
+    for got, want in pairs:
+        assert float(got) == float(want)
+    assert abs(float(fa.GMSD(data_range=255.0).loss(x, y))
+               - (1.0 - float(fa.gms(x, y, data_range=255.0)))) < 1e-12
+
+
+def test_gradients_cpu_portable():
+    x = torch.rand(1, 1, 64, 64, requires_grad=True)
+    y = torch.rand(1, 1, 64, 64)
+    fa.SSIM(data_range=1.0).loss(x, y).backward()
+    assert torch.isfinite(x.grad).all() and float(x.grad.abs().sum()) > 0
+    for fn in (fa.l1, fa.charbonnier, fa.huber):
+        z = torch.rand(1, 3, 32, 32, requires_grad=True)
+        fn(z, torch.rand(1, 3, 32, 32)).backward()
+        assert torch.isfinite(z.grad).all()
+
+
+def test_status_without_gpu():
+    st = fa.backend_status()
+    if not torch.cuda.is_available():
+        assert st["available"] is False and st["error"]

@@ -1,0 +1,145 @@
+"""GPU parity of the fused SSIM / SSIM-CS backward.
+
+Bar (north star): dL/dx within 1e-6 relative of float64, measured max-normwise
+(max |g - g_ref| / max |g_ref|), the reference's own gradient metric
+(test_metrics.py:144) at a 200x tighter tolerance.  The reference oracle is the
+float64 closed-form adjoint in oracle/reference.py, itself pinned by central
+differences and float64 autograd in tests/test_oracle.py.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import frame_analytics_amd as fa
+from oracle import reference as ref
+from tests.conftest import float_pair
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-6
+
+
+def _normwise(g, want):
+    return float(np.abs(g - want).max() / max(np.abs(want).max(), 1e-300))
+
+
+def _grads(x0, y0, wrt, **kw):
+    x = x0.clone().requires_grad_("x" in wrt)
+    y = y0.clone().requires_grad_("y" in wrt)
+    (1.0 - fa.ssim(x, y, **kw)).backward()
+    return x.grad, y.grad
+
+
+def test_configs3_full_size(gpu):
+    """16x3x256x256 float32, loss = 1 - ssim(x, y, data_range=1)."""
+    xa, ya = float_pair((16, 3, 256, 256), 0.05, seed=3)
+    x = torch.from_numpy(xa).to(gpu).requires_grad_(True)
+    y = torch.from_numpy(ya).to(gpu)
+    loss = 1.0 - fa.ssim(x, y, data_range=1.0)
+    want_val = ref.ssim(xa.astype(np.float64), ya.astype(np.float64), 1.0)
+    assert abs(float(loss) - (1.0 - want_val)) <= 1e-6 * abs(1.0 - want_val)
+    loss.backward()
+    gx, _ = ref.ssim_mean_grad(xa.astype(np.float64), ya.astype(np.float64), 1.0)
+    err = _normwise(x.grad.double().cpu().numpy(), -gx)
+    assert err <= REL, err
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 64, 64), (1, 1, 97, 131), (2, 3, 80, 120),
+                                   (1, 2, 300, 17)])
+@pytest.mark.parametrize("wrt", [("x",), ("y",), ("x", "y")])
+def test_backward_matches_oracle(gpu, shape, wrt):
+    xa, ya = float_pair(shape, 0.05, seed=sum(shape))
+    gx, gy = _grads(torch.from_numpy(xa).to(gpu), torch.from_numpy(ya).to(gpu), wrt,
+                    data_range=1.0)
+    rx, ry = ref.ssim_mean_grad(xa.astype(np.float64), ya.astype(np.float64), 1.0)
+    if "x" in wrt:
+        assert _normwise(gx.double().cpu().numpy(), -rx) <= REL
+    else:
+        assert gx is None
+    if "y" in wrt:
+        assert _normwise(gy.double().cpu().numpy(), -ry) <= REL
+    else:
+        assert gy is None
+
+
+@pytest.mark.parametrize("win", [3, 5, 7, 9, 11])
+def test_backward_window_sizes(gpu, win):
+    xa, ya = float_pair((1, 2, 70, 90), 0.05, seed=win)
+    gx, gy = _grads(torch.from_numpy(xa).to(gpu), torch.from_numpy(ya).to(gpu), ("x", "y"),
+                    data_range=1.0, win_size=win)
+    rx, ry = ref.ssim_mean_grad(xa.astype(np.float64), ya.astype(np.float64), 1.0, win_size=win)
+    assert _normwise(gx.double().cpu().numpy(), -rx) <= REL
+    assert _normwise(gy.double().cpu().numpy(), -ry) <= REL
+
+
+def test_backward_through_map(gpu):
+    """return_map=True with a non-uniform upstream gradient."""
+    xa, ya = float_pair((1, 1, 72, 88), 0.05, seed=1)
+    rng = np.random.default_rng(7)
+    wmap = rng.random((1, 1, 62, 78))
+    x = torch.from_numpy(xa).to(gpu).requires_grad_(True)
+    y = torch.from_numpy(ya).to(gpu).requires_grad_(True)
+    m = fa.ssim(x, y, data_range=1.0, return_map=True)
+    (m * torch.from_numpy(wmap).to(gpu, torch.float32)).sum().backward()
+    rx, ry = ref.ssim_mean_grad(xa.astype(np.float64), ya.astype(np.float64), 1.0,
+                                upstream=wmap.astype(np.float32).astype(np.float64))
+    assert _normwise(x.grad.double().cpu().numpy(), rx) <= REL
+    assert _normwise(y.grad.double().cpu().numpy(), ry) <= REL
+
+
+def test_backward_matches_finite_differences(gpu):
+    """Independent of the adjoint: central differences of the float64 forward
+    (reference test_metrics.py:148-171)."""
+    rng = np.random.default_rng(1)
+    h = w = 40
+    xa = rng.random((h, w))
+    ya = np.clip(xa + 0.05 * rng.standard_normal((h, w)), 0, 1)
+    x = torch.as_tensor(xa, dtype=torch.float32, device=gpu)[None, None].requires_grad_(True)
+    y = torch.as_tensor(ya, dtype=torch.float32, device=gpu)[None, None]
+    fa.ssim(x, y, data_range=1.0).backward()
+    g = x.grad[0, 0].double().cpu().numpy()
+    x32 = x.detach()[0, 0].double().cpu().numpy()
+    y32 = y[0, 0].double().cpu().numpy()
+    h = 1e-4  # see tests/test_oracle.py: truncation vs float64 cancellation
+    scale = np.abs(g).max()
+    for (i, j) in [(5, 7), (20, 20), (12, 33), (25, 18), (0, 0), (39, 39)]:
+        xp = x32.copy(); xp[i, j] += h
+        xm = x32.copy(); xm[i, j] -= h
+        fd = (ref.ssim(xp[None, None], y32[None, None], 1.0)
+              - ref.ssim(xm[None, None], y32[None, None], 1.0)) / (2 * h)
+        assert abs(fd - g[i, j]) <= 2e-6 * scale, (i, j, fd, g[i, j])
+
+
+def test_backward_does_not_sync(gpu):
+    x = torch.rand(1, 1, 128, 128, device=gpu, requires_grad=True)
+    y = torch.rand(1, 1, 128, 128, device=gpu)
+    (1.0 - fa.ssim(x, y, data_range=1.0)).backward()
+    torch.cuda.synchronize()
+    x.grad = None
+    with torch.cuda.stream(torch.cuda.Stream()):
+        torch.cuda._sleep(50_000_000)
+        (1.0 - fa.ssim(x, y, data_range=1.0)).backward()
+        assert not torch.cuda.current_stream().query()
+    torch.cuda.synchronize()
+
+
+def test_double_backward_refuses(gpu):
+    x = torch.rand(1, 1, 64, 64, device=gpu, requires_grad=True)
+    y = (x.detach() + 0.05 * torch.randn_like(x)).clamp(0, 1)
+    with pytest.raises(RuntimeError, match="twice differentiable"):
+        g, = torch.autograd.grad(fa.ssim(x, y, data_range=1.0), x, create_graph=True)
+        torch.autograd.grad(g.sum(), x)
+    g, = torch.autograd.grad(fa.ssim(x, y, data_range=1.0, backend_hint="torch"), x,
+                             create_graph=True)
+    g2, = torch.autograd.grad(g.sum(), x)
+    assert torch.isfinite(g2).all() and float(g2.abs().max()) > 0
+
+
+def test_module_loss_gradients_flow(gpu):
+    x = torch.rand(1, 1, 64, 64, device=gpu, requires_grad=True)
+    y = torch.rand(1, 1, 64, 64, device=gpu)
+    fa.SSIM(data_range=1.0).loss(x, y).backward()
+    assert torch.isfinite(x.grad).all() and float(x.grad.abs().sum()) > 0

@@ -1,0 +1,169 @@
+"""GPU parity of the pixel reductions (MSE / PSNR / L1 / Charbonnier / Huber).
+
+Bar: uint8 MSE and L1 are bit-exact against integer sums (the oracle's int64
+SSE/SAD divided once by the count); PSNR matches 10 log10(L^2) - 10 log10(mse)
+to 1e-12 (device and host log10 may differ in the last ulp); float ops are
+within 1e-9 relative of float64 (Charbonnier on non-float64 input: 1e-6, its
+square root is float32 like the reference's).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import frame_analytics_amd as fa
+from oracle import reference as ref
+from tests.conftest import u8_pair
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 33, 41), (2, 3, 64, 64), (5, 1, 97, 131),
+                                   (3, 3, 127, 233), (1, 3, 512, 512), (4, 2, 1, 4099)])
+def test_mse_psnr_l1_u8_bit_exact(gpu, shape):
+    a, b = u8_pair(shape, 8.0, seed=sum(shape))
+    ta, tb = _t(a, gpu), _t(b, gpu)
+    for red in ("mean", "none"):
+        got = fa.mse(ta, tb, reduction=red).cpu().numpy()
+        want = ref.mse(a, b, red)
+        assert np.array_equal(got, np.asarray(want)), (red, got, want)
+        got_l1 = fa.l1(ta, tb, reduction=red).cpu().numpy()
+        assert np.array_equal(got_l1, np.asarray(ref.l1(a, b, red)))
+        p = fa.psnr(ta, tb, data_range=255.0, reduction=red).cpu().numpy()
+        assert np.allclose(p, ref.psnr(a, b, 255.0, red), rtol=1e-12, atol=0)
+
+
+def test_configs2_full_size_sse_exact(gpu):
+    """8x3x2160x3840 uint8, sigma 4; SSE exact, PSNR consistent."""
+    shape = (8, 3, 2160, 3840)
+    torch.manual_seed(0)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(2)
+    ta = torch.randint(0, 256, shape, dtype=torch.uint8, device=gpu, generator=g)
+    noise = torch.round(torch.randn(shape, device=gpu, generator=g) * 4.0)
+    tb = (ta.to(torch.int16) + noise.to(torch.int16)).clamp(0, 255).to(torch.uint8)
+    del noise
+    per = fa.mse(ta, tb, reduction="none").cpu().numpy()
+    a, b = ta.cpu().numpy(), tb.cpu().numpy()
+    sse = ref.sse_u8(a, b, per_image=True)
+    n = a[0].size
+    assert np.array_equal(per, sse.astype(np.float64) / float(n))
+    total = float(fa.mse(ta, tb))
+    assert total == float(int(sse.sum())) / float(n * 8)
+    p = float(fa.psnr(ta, tb, data_range=255.0))
+    assert abs(p - (10 * math.log10(255.0 ** 2) - 10 * math.log10(total))) < 1e-12
+    assert np.array_equal(fa.l1(ta, tb, reduction="none").cpu().numpy(),
+                          ref.sad_u8(a, b, per_image=True).astype(np.float64) / float(n))
+
+
+@pytest.mark.parametrize("off_a,off_b", [(0, 0), (1, 1), (3, 3), (0, 1), (1, 2), (2, 6),
+                                         (4, 8), (5, 13), (15, 0)])
+def test_unaligned_views(gpu, off_a, off_b):
+    """Contiguous uint8 slices at any byte offset, equal or different between
+    the two operands, give the same exact sums (reference
+    test_training_metrics.py:423-443)."""
+    n = 3 * 64 * 33 + 7
+    base_a, base_b = u8_pair((1, n + 32), 20.0, seed=off_a * 31 + off_b)
+    ta, tb = _t(base_a[0], gpu), _t(base_b[0], gpu)
+    x = ta[off_a:off_a + n]
+    y = tb[off_b:off_b + n]
+    assert x.is_contiguous() and x.data_ptr() % 16 == (ta.data_ptr() + off_a) % 16
+    xs = x.view(1, 1, 1, n)
+    ys = y.view(1, 1, 1, n)
+    a = base_a[0, off_a:off_a + n][None, None, None]
+    b = base_b[0, off_b:off_b + n][None, None, None]
+    assert float(fa.mse(xs, ys)) == ref.mse(a, b)
+    assert float(fa.l1(xs, ys)) == ref.l1(a, b)
+    assert abs(float(fa.huber(xs, ys, delta=3.0)) - ref.huber(a, b, 3.0)) <= 1e-9 * ref.huber(a, b, 3.0)
+    # and with several images of odd size, so every image peels its own head
+    m = (n - 7) // 3
+    x3, y3 = x[: 3 * m].view(3, 1, 1, m), y[: 3 * m].view(3, 1, 1, m)
+    a3, b3 = a.reshape(-1)[: 3 * m].reshape(3, 1, 1, m), b.reshape(-1)[: 3 * m].reshape(3, 1, 1, m)
+    assert np.array_equal(fa.mse(x3, y3, reduction="none").cpu().numpy(), ref.mse(a3, b3, "none"))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32, torch.float64])
+def test_float_dtypes(gpu, dt):
+    a, b = u8_pair((3, 2, 45, 77), 12.0, seed=7)
+    xa = torch.from_numpy(a.astype(np.float64) / 255.0).to(dt)
+    xb = torch.from_numpy(b.astype(np.float64) / 255.0).to(dt)
+    # the oracle sees exactly the values the kernel sees
+    a64, b64 = xa.double().numpy(), xb.double().numpy()
+    ta, tb = xa.to(gpu), xb.to(gpu)
+    for red in ("mean", "none"):
+        cases = [
+            (fa.mse(ta, tb, reduction=red), ref.mse(a64, b64, red), 1e-12),
+            (fa.l1(ta, tb, reduction=red), ref.l1(a64, b64, red), 1e-12),
+            (fa.huber(ta, tb, delta=0.02, reduction=red), ref.huber(a64, b64, 0.02, red), 1e-12),
+            (fa.charbonnier(ta, tb, eps=1e-3, reduction=red), ref.charbonnier(a64, b64, 1e-3, red),
+             1e-12 if dt == torch.float64 else 1e-6),
+        ]
+        for got, want, tol in cases:
+            got, want = got.cpu().numpy(), np.asarray(want)
+            assert np.allclose(got, want, rtol=tol, atol=0), (dt, red, got, want)
+
+
+def test_u8_float_terms(gpu):
+    a, b = u8_pair((2, 3, 200, 232), 9.0, seed=3)
+    ta, tb = _t(a, gpu), _t(b, gpu)
+    for eps in (1e-3, 3.0):
+        got = float(fa.charbonnier(ta, tb, eps=eps))
+        want = ref.charbonnier(a, b, eps)
+        assert abs(got - want) <= 1e-6 * want
+    for delta in (1.0, 4.0, 17.0):
+        got = float(fa.huber(ta, tb, delta=delta))
+        want = ref.huber(a, b, delta)
+        assert abs(got - want) <= 1e-6 * want
+
+
+def test_float64_not_narrowed(gpu):
+    """A 1e-6 residual on float64 input has no float32 answer
+    (reference test_training_metrics.py:446-463)."""
+    x = torch.full((1, 1, 64, 64), 100.0, dtype=torch.float64, device=gpu)
+    y = x + 1e-6
+    assert abs(float(fa.mse(x, y)) - 1e-12) <= 1e-3 * 1e-12
+    assert abs(float(fa.huber(x, y)) - 5e-13) <= 1e-3 * 5e-13
+    assert abs(float(fa.l1(x, y)) - 1e-6) <= 1e-3 * 1e-6
+    assert abs(float(fa.charbonnier(x, y, eps=0.0)) - 1e-6) <= 1e-3 * 1e-6
+
+
+def test_identities_and_reductions(gpu):
+    x = torch.randint(0, 256, (2, 3, 64, 64), dtype=torch.uint8, device=gpu)
+    y = torch.randint(0, 256, (2, 3, 64, 64), dtype=torch.uint8, device=gpu)
+    assert float(fa.mse(x, x)) == 0.0
+    assert float(fa.psnr(x, x, data_range=255.0)) == float("inf")
+    assert float(fa.l1(x, x)) == 0.0 and float(fa.huber(x, x)) == 0.0
+    assert abs(float(fa.charbonnier(x, x, eps=0.25)) - 0.25) < 1e-9
+    for fn in (fa.mse, fa.l1, fa.charbonnier, fa.huber):
+        per = fn(x, y, reduction="none")
+        assert per.shape == (2,)
+        assert abs(float(per.mean()) - float(fn(x, y))) < 1e-9 * max(1.0, float(fn(x, y)))
+    assert fa.psnr(x, y, reduction="none").shape == (2,)
+    m = float(fa.mse(x, y))
+    assert abs(float(fa.psnr(x, y, data_range=255.0)) - 10 * math.log10(255.0 ** 2 / m)) < 1e-9
+
+
+def test_luma_and_crop(gpu):
+    rng = np.random.default_rng(12)
+    a = rng.integers(0, 256, (3, 140, 176)).astype(np.float64)
+    b = np.clip(a + 9.0 * rng.standard_normal(a.shape), 0, 255).round()
+    ta = torch.from_numpy(a.astype(np.uint8))[None].to(gpu)
+    tb = torch.from_numpy(b.astype(np.uint8))[None].to(gpu)
+    for mode in ("bt601", "bt709", "matlab"):
+        for cb in (0, 4):
+            ya = ref.crop(ref.rgb_to_luma(a[None], mode), cb)
+            yb = ref.crop(ref.rgb_to_luma(b[None], mode), cb)
+            got = float(fa.psnr(ta, tb, data_range=255.0, luma=mode, crop_border=cb))
+            assert abs(got - float(ref.psnr(ya, yb, 255.0))) < 1e-5
+            assert abs(float(fa.mse(ta, tb, luma=mode, crop_border=cb)) - ref.mse(ya, yb)) < 1e-4
+    # an integer crop stays exact
+    got = float(fa.mse(ta, tb, crop_border=3))
+    assert got == ref.mse(ref.crop(a[None].astype(np.uint8), 3), ref.crop(b[None].astype(np.uint8), 3))

@@ -1,0 +1,164 @@
+"""GPU parity of the fused SSIM forward against the float64 oracle.
+
+Bar (north star): SSIM values within 1e-6 relative of float64.  The SSIM map
+is stored as float32; its elements are held to 2e-5 absolute (the reference's
+own gate is 5e-5, validate.py:25).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import frame_analytics_amd as fa
+from oracle import reference as ref
+from tests.conftest import natural_pair, u8_pair
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-6
+MAP_ABS = 2e-5
+
+# the reference's accuracy-gate corpus (validate.py:80-87)
+CASES = [(64, 64, "uniform", 20.0), (127, 233, "natural", 8.0), (256, 256, "natural", 3.0),
+         (512, 384, "natural", 25.0), (720, 1280, "natural", 12.0), (33, 41, "flat", 5.0)]
+
+
+def _rel(got, want):
+    return abs(got - want) / max(abs(want), 1e-12)
+
+
+@pytest.mark.parametrize("h,w,kind,noise", CASES)
+def test_ssim_matches_oracle(gpu, h, w, kind, noise):
+    a, b = natural_pair(h, w, noise, seed=h * w, kind=kind)
+    want = ref.ssim(a[None, None], b[None, None], 255.0)
+    want_map = ref.ssim(a[None, None], b[None, None], 255.0, return_map=True)
+    for dt in (torch.uint8, torch.float32):
+        x = torch.as_tensor(a, dtype=dt, device=gpu)
+        y = torch.as_tensor(b, dtype=dt, device=gpu)
+        got = float(fa.ssim(x, y, data_range=255.0))
+        assert _rel(got, want) <= REL, (dt, got, want)
+        m = fa.ssim(x, y, data_range=255.0, return_map=True)
+        assert m.shape == (1, 1, h - 10, w - 10) and m.dtype == torch.float32
+        err = float((m.double().cpu() - torch.from_numpy(want_map)).abs().max())
+        assert err <= MAP_ABS, (dt, err)
+
+
+@pytest.mark.parametrize("win", [3, 5, 7, 9, 11])
+def test_window_sizes(gpu, win):
+    a, b = natural_pair(97, 131, 7.0, seed=3)
+    want = ref.ssim(a[None, None], b[None, None], 255.0, win_size=win)
+    x = torch.as_tensor(a, dtype=torch.uint8, device=gpu)
+    y = torch.as_tensor(b, dtype=torch.uint8, device=gpu)
+    got = float(fa.ssim(x, y, data_range=255.0, win_size=win))
+    assert _rel(got, want) <= REL, (win, got, want)
+    got_map = fa.ssim(x, y, data_range=255.0, win_size=win, return_map=True).double().cpu()
+    want_map = ref.ssim(a[None, None], b[None, None], 255.0, win_size=win, return_map=True)
+    assert float((got_map - torch.from_numpy(want_map)).abs().max()) <= MAP_ABS
+
+
+def test_sigma_and_K(gpu):
+    a, b = natural_pair(90, 120, 10.0, seed=5)
+    want = ref.ssim(a[None, None], b[None, None], 255.0, win_size=7, sigma=2.0, K=(0.02, 0.05))
+    x = torch.as_tensor(a, dtype=torch.uint8, device=gpu)
+    y = torch.as_tensor(b, dtype=torch.uint8, device=gpu)
+    got = float(fa.ssim(x, y, data_range=255.0, win_size=7, sigma=2.0, K=(0.02, 0.05)))
+    assert _rel(got, want) <= REL
+
+
+@pytest.mark.parametrize("dt", [torch.uint8, torch.float16, torch.bfloat16, torch.float32,
+                                torch.float64])
+def test_dtypes(gpu, dt):
+    a, b = natural_pair(97, 131, 7.0, seed=4)
+    x = torch.as_tensor(a, dtype=dt, device=gpu)
+    y = torch.as_tensor(b, dtype=dt, device=gpu)
+    # the oracle sees the values the kernel sees (integers are exact in all five)
+    want = ref.ssim(x.double().cpu().numpy()[None, None], y.double().cpu().numpy()[None, None],
+                    255.0)
+    got = float(fa.ssim(x, y, data_range=255.0))
+    tol = 1e-12 if dt == torch.float64 else REL
+    assert _rel(got, want) <= tol, (dt, got, want)
+
+
+def test_batch_channels_reduction_none(gpu):
+    a, b = u8_pair((5, 3, 64, 80), 10.0, seed=9)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    per = fa.ssim(x, y, data_range=255.0, reduction="none").cpu().numpy()
+    want = ref.ssim(a, b, 255.0, reduction="none")
+    assert per.shape == (5,)
+    assert np.all(np.abs(per - want) <= REL * np.abs(want))
+    assert abs(float(per.mean()) - float(fa.ssim(x, y, data_range=255.0))) < 1e-12
+    m = fa.ssim(x, y, data_range=255.0, return_map=True)
+    assert abs(float(m.double().mean()) - float(fa.ssim(x, y, data_range=255.0))) < 1e-7
+
+
+def test_ranks_agree_bitwise(gpu):
+    a, b = natural_pair(97, 131, 7.0, seed=3)
+    x = torch.as_tensor(a, dtype=torch.uint8, device=gpu)
+    y = torch.as_tensor(b, dtype=torch.uint8, device=gpu)
+    v2 = float(fa.ssim(x, y, data_range=255.0))
+    v3 = float(fa.ssim(x[None], y[None], data_range=255.0))
+    v4 = float(fa.ssim(x[None, None], y[None, None], data_range=255.0))
+    assert v2 == v3 == v4
+
+
+def test_identity(gpu):
+    x = torch.randint(0, 256, (2, 3, 64, 64), dtype=torch.uint8, device=gpu)
+    assert abs(float(fa.ssim(x, x, data_range=255.0)) - 1.0) < 1e-6
+    xf = torch.rand(2, 3, 64, 64, device=gpu)
+    assert abs(float(fa.ssim(xf, xf, data_range=1.0)) - 1.0) < 1e-6
+
+
+def test_luma_and_crop(gpu):
+    rng = np.random.default_rng(12)
+    a = rng.integers(0, 256, (3, 140, 176)).astype(np.float64)
+    b = np.clip(a + 9.0 * rng.standard_normal(a.shape), 0, 255).round()
+    ta = torch.from_numpy(a.astype(np.uint8))[None].to(gpu)
+    tb = torch.from_numpy(b.astype(np.uint8))[None].to(gpu)
+    for mode in ("bt601", "bt709", "matlab"):
+        for cb in (0, 4):
+            ya = ref.crop(ref.rgb_to_luma(a[None], mode), cb)
+            yb = ref.crop(ref.rgb_to_luma(b[None], mode), cb)
+            want = ref.ssim(ya, yb, 255.0)
+            got = float(fa.ssim(ta, tb, data_range=255.0, luma=mode, crop_border=cb))
+            assert _rel(got, want) <= REL, (mode, cb)
+    for cb in (1, 3, 8):
+        manual = float(fa.ssim(ta[..., cb:-cb, cb:-cb].contiguous(),
+                               tb[..., cb:-cb, cb:-cb].contiguous(), data_range=255.0))
+        assert abs(float(fa.ssim(ta, tb, data_range=255.0, crop_border=cb)) - manual) < 1e-12
+
+
+def test_configs1_full_size(gpu):
+    """8x3x1080x1920 uint8 (sigma 8).  Image 0 against the oracle;
+    the batch through size-independent properties (per-image consistency,
+    map mean = per-image value, map shape)."""
+    a, b = u8_pair((8, 3, 1080, 1920), 8.0, seed=1)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    per = fa.ssim(x, y, data_range=255.0, reduction="none").cpu().numpy()
+    total = float(fa.ssim(x, y, data_range=255.0))
+    want0 = ref.ssim(a[:1], b[:1], 255.0)
+    assert _rel(float(per[0]), want0) <= REL, (per[0], want0)
+    single = float(fa.ssim(x[5:6], y[5:6], data_range=255.0))
+    assert abs(single - float(per[5])) < 1e-12
+    assert abs(total - float(per.mean())) < 1e-12
+    m = fa.ssim(x, y, data_range=255.0, return_map=True)
+    assert m.shape == (8, 3, 1070, 1910)
+    pm = m.double().mean(dim=(1, 2, 3)).cpu().numpy()
+    assert np.all(np.abs(pm - per) < 1e-7)
+
+
+def test_native_hint_and_errors(gpu):
+    x = torch.zeros(1, 1, 32, 32, device=gpu)
+    with pytest.raises(ValueError):
+        fa.ssim(x, torch.zeros(1, 1, 32, 33, device=gpu))
+    with pytest.raises(ValueError):
+        fa.ssim(torch.zeros(1, 1, 8, 8, device=gpu), torch.zeros(1, 1, 8, 8, device=gpu))
+    # a 13-wide window has no kernel: "native" must say so, "auto" must still answer
+    a, b = natural_pair(64, 64, 5.0, seed=1)
+    ta = torch.as_tensor(a, dtype=torch.float32, device=gpu)
+    tb = torch.as_tensor(b, dtype=torch.float32, device=gpu)
+    with pytest.raises(RuntimeError):
+        fa.ssim(ta, tb, data_range=255.0, win_size=13, backend_hint="native")
+    want = ref.ssim(a[None, None], b[None, None], 255.0, win_size=13)
+    assert _rel(float(fa.ssim(ta, tb, data_range=255.0, win_size=13)), want) < 1e-5
