@@ -130,13 +130,67 @@ def cpu_baseline(seconds=12.0):
                       f"1x3x1080x1920 uint8, best of {reps} calls over ~{seconds:.0f} s"}
 
 
+def profile_sequence(launches=20):
+    """A fixed launch sequence for rocprofv3 counter runs (``--profile``):
+    a torch copy of exactly 256 MiB (the FETCH_SIZE / WRITE_SIZE calibration:
+    256 MiB read, 256 MiB written), then `launches` launches each of the SSIM
+    strip kernel and of the PSNR pixel kernel, through
+    the C ABI with no finalize sinks, rotating resident input pairs."""
+    import torch
+
+    import frame_analytics_amd as fa
+    from frame_analytics_amd import backend
+
+    dev = torch.device("cuda:0")
+    ext = backend.load()
+    lib = ext.gpu
+    stream = torch.cuda.current_stream().cuda_stream
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+    pairs = _pairs(torch, SSIM_SHAPE, 8.0, 4, dev, seed=1)
+    n, c, h, w = SSIM_SHAPE
+    win = fa.gaussian_window_1d(11, 1.5, device=dev, dtype=torch.float32)
+    bpp = backend._ssim_workspace(ext, h, w, 11)
+    partial = torch.empty((n * c, bpp), dtype=torch.float64, device=dev)
+    for i in range(launches):
+        a, b = pairs[i % 4]
+        assert lib.fa_gpu_ssim(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, win.data_ptr(), 11,
+                               127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, None,
+                               partial.data_ptr(), bpp, None, None, 0, stream) == 0
+    torch.cuda.synchronize()
+    del pairs, partial
+
+    ppairs = _pairs(torch, PSNR_SHAPE, 4.0, 2, dev, seed=2)
+    pn = PSNR_SHAPE[0]
+    per = ppairs[0][0].numel() // pn
+    bpi = backend._pixel_workspace(ext, pn, per, 0)
+    ppart = torch.empty((pn, bpi), dtype=torch.float64, device=dev)
+    for i in range(launches):
+        a, b = ppairs[i % 2]
+        assert lib.fa_gpu_pixel_reduce(a.data_ptr(), b.data_ptr(), 0, pn, per, 0, 0.0, -1e300,
+                                       ppart.data_ptr(), bpi, None, None, None, None, 0,
+                                       stream) == 0
+    torch.cuda.synchronize()
+    print("profile sequence done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="run the fixed launch sequence for rocprofv3 counters and exit")
     args = ap.parse_args()
+    if args.profile:
+        profile_sequence()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the per-shard kernel is the single-GPU one; see DESIGN.md).", file=sys.stderr)

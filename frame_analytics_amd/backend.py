@@ -283,7 +283,19 @@ def ssim_autograd_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> 
     )
 
 
-ssim_cs_autograd_available = ssim_autograd_available
+def ssim_cs_autograd_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> bool:
+    """Can the differentiable native MS-SSIM primitive serve this call?  float32
+    levels and the float64 levels of the exact pyramid both can."""
+    return (
+        x.is_cuda
+        and x.dtype in (torch.float32, torch.float64)
+        and y.dtype == x.dtype
+        and x.shape == y.shape
+        and x.dim() == 4
+        and win_size in _WINDOWS
+        and not torch.cuda.is_current_stream_capturing()
+        and _gpu_ext(x) is not None
+    )
 
 
 def ssim_fused(x: torch.Tensor, y: torch.Tensor, win: torch.Tensor,
@@ -406,11 +418,47 @@ def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy):
                       dtype=torch.float32)
     dx = torch.empty_like(x) if need_dx else None
     dy = torch.empty_like(y) if need_dy else None
-    _check(ext.gpu.fa_gpu_ssim_cs_backward(
-        _ptr(x), _ptr(y), _ptr(gsf), _ptr(gcsf), _ptr(winf), k, n, c, h, w,
-        float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
-        _dev(x), _stream(x)), ext)
+    if x.dtype == torch.float32:
+        _check(ext.gpu.fa_gpu_ssim_cs_backward(
+            _ptr(x), _ptr(y), _ptr(gsf), _ptr(gcsf), _ptr(winf), k, n, c, h, w,
+            float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
+            _dev(x), _stream(x)), ext)
+    else:
+        _check(ext.gpu.fa_gpu_ssim_cs_backward_ex(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], _ptr(gsf), _ptr(gcsf), _ptr(winf), k,
+            n, c, h, w, float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
+            _dev(x), _stream(x)), ext)
     return dx, dy
+
+
+# --------------------------------------------------------------------------- #
+# the MS-SSIM pyramid step
+# --------------------------------------------------------------------------- #
+
+
+def pyramid_dtype(dt: torch.dtype) -> torch.dtype:
+    """Element type of a pyramid level: float32 holds the 2x2 means of uint8
+    exactly, float64 those of every floating type (see fa_pool.hip)."""
+    return torch.float32 if dt == torch.uint8 else torch.float64
+
+
+def pool2_available(x: torch.Tensor, y: torch.Tensor) -> bool:
+    return (x.is_cuda and x.dim() == 4 and x.dtype in _SUPPORTED and y.dtype == x.dtype
+            and x.shape == y.shape and x.shape[-2] >= 2 and x.shape[-1] >= 2
+            and _gpu_ext(x) is not None)
+
+
+def pool2_gpu(x: torch.Tensor, y: torch.Tensor):
+    """One pyramid step of x and y on the GPU (one launch), exact."""
+    ext = load()
+    x, y = _contig(x), _contig(y)
+    n, c, h, w = x.shape
+    od = pyramid_dtype(x.dtype)
+    ox = torch.empty((n, c, h // 2, w // 2), dtype=od, device=x.device)
+    oy = torch.empty_like(ox)
+    _check(ext.gpu.fa_gpu_pool2(_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n * c, h, w,
+                                _ptr(ox), _ptr(oy), _DTYPE_CODE[od], _dev(x), _stream(x)), ext)
+    return ox, oy
 
 
 def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,

@@ -9,10 +9,15 @@
 // three-row window in registers.  The column sums and row differences of the
 // Prewitt pair need the two lanes to the right, which come from in-wave
 // shuffles -- no LDS staging and no barriers.  For uint8 input the downsampled
-// samples, their 3-sums and differences are all exact in float32, so only the
-// final 1/3 scaling rounds before the square root.  Sum q and sum q^2 are
-// accumulated in float64 and reduced in a fixed order.
+// samples, their 3-sums and differences are all exact in float32, so they stay
+// float32; every other input type carries them in float64.  From the Prewitt
+// differences on, g and q are formed in float64 (full rate on CDNA4,
+// and the kernel is bound on HBM), so q carries no float32 rounding into the
+// standard deviation.  Sum q and sum q^2 are accumulated in float64 and reduced
+// in a fixed order.
 #include "fa_common.h"
+
+#include <type_traits>
 
 namespace fa {
 
@@ -20,36 +25,43 @@ constexpr int G_OUTW = WAVE - 2;                     // output columns per wave
 constexpr int G_STRIP = WAVES_PER_BLOCK * G_OUTW;    // output columns per workgroup
 constexpr int G_TH = 64;                             // output rows per workgroup
 
+// Sample type: float32 is exact for uint8 (multiples of 1/4 below 1024),
+// float64 for everything else.
+template <typename T>
+using GSample = typename std::conditional<std::is_same<T, uint8_t>::value, float, double>::type;
+
 template <typename T, bool DOWN>
-__device__ inline float gmsd_sample(const T* __restrict__ p, int64_t plane_off, int W,
-                                    int r, int c) {
+__device__ inline GSample<T> gmsd_sample(const T* __restrict__ p, int64_t plane_off, int W,
+                                         int r, int c) {
+  using S = GSample<T>;
   if constexpr (DOWN) {
     const int64_t o = plane_off + static_cast<int64_t>(2 * r) * W + 2 * c;
-    return 0.25f * (Elem<T>::f(p[o]) + Elem<T>::f(p[o + 1]) + Elem<T>::f(p[o + W]) +
-                    Elem<T>::f(p[o + W + 1]));
+    return S(0.25) * (load_as<S>(p, o) + load_as<S>(p, o + 1) + load_as<S>(p, o + W) +
+                      load_as<S>(p, o + W + 1));
   } else {
-    return Elem<T>::f(p[plane_off + static_cast<int64_t>(r) * W + c]);
+    return load_as<S>(p, plane_off + static_cast<int64_t>(r) * W + c);
   }
 }
 
 // Gradient magnitude at this lane's column from the three rows v0 (top),
 // v1, v2 (bottom); lanes 62 and 63 produce garbage that is never used.
-__device__ inline float prewitt_mag(float v0, float v1, float v2, float eps) {
-  constexpr float THIRD = 1.0f / 3.0f;
-  const float cs = v0 + v1 + v2;  // column sum     (for gx)
-  const float rd = v0 - v2;       // row difference (for gy)
-  const float cs2 = __shfl_down(cs, 2, WAVE);
-  const float rd1 = __shfl_down(rd, 1, WAVE);
-  const float rd2 = __shfl_down(rd, 2, WAVE);
-  const float gx = (cs - cs2) * THIRD;
-  const float gy = (rd + rd1 + rd2) * THIRD;
-  return sqrtf(fmaf(gx, gx, fmaf(gy, gy, eps)));
+template <typename S>
+__device__ inline double prewitt_mag(S v0, S v1, S v2, double eps) {
+  const S cs = v0 + v1 + v2;  // column sum     (for gx)
+  const S rd = v0 - v2;       // row difference (for gy)
+  const S cs2 = __shfl_down(cs, 2, WAVE);
+  const S rd1 = __shfl_down(rd, 1, WAVE);
+  const S rd2 = __shfl_down(rd, 2, WAVE);
+  const double gx = static_cast<double>(cs - cs2) / 3.0;
+  const double gy = (static_cast<double>(rd) + static_cast<double>(rd1) +
+                     static_cast<double>(rd2)) / 3.0;
+  return sqrt(fma(gx, gx, fma(gy, gy, eps)));
 }
 
 template <typename T, bool DOWN>
 __global__ __launch_bounds__(BLOCK) void gmsd_kernel(
     const T* __restrict__ x, const T* __restrict__ y, int H, int W, int Hd, int Wd,
-    int Hout, int Wout, float Tc, float eps, int strips, int bpp,
+    int Hout, int Wout, double Tc, double eps, int strips, int bpp,
     double* __restrict__ psum, double* __restrict__ psumsq) {
   __shared__ double sred[2 * WAVES_PER_BLOCK];
   const int plane = blockIdx.x / bpp;
@@ -65,17 +77,18 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(
   const int rows = min(G_TH, Hout - r0);
   const int64_t plane_off = static_cast<int64_t>(plane) * H * W;
 
-  auto fetch = [&](int r, float& xv, float& yv) {
+  using S = GSample<T>;
+  auto fetch = [&](int r, S& xv, S& yv) {
     if (col_in && r < Hd) {
       xv = gmsd_sample<T, DOWN>(x, plane_off, W, r, col);
       yv = gmsd_sample<T, DOWN>(y, plane_off, W, r, col);
     } else {
-      xv = 0.0f;
-      yv = 0.0f;
+      xv = S(0);
+      yv = S(0);
     }
   };
 
-  float x0, x1, x2, y0, y1, y2, nx, ny;
+  S x0, x1, x2, y0, y1, y2, nx, ny;
   fetch(r0, x0, y0);
   fetch(r0 + 1, x1, y1);
   fetch(r0 + 2, nx, ny);
@@ -84,13 +97,12 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(
     x2 = nx;
     y2 = ny;
     if (o + 1 < rows) fetch(r0 + o + 3, nx, ny);
-    const float g1 = prewitt_mag(x0, x1, x2, eps);
-    const float g2 = prewitt_mag(y0, y1, y2, eps);
-    const float q = (2.0f * g1 * g2 + Tc) / (g1 * g1 + g2 * g2 + Tc);
+    const double g1 = prewitt_mag(x0, x1, x2, eps);
+    const double g2 = prewitt_mag(y0, y1, y2, eps);
+    const double q = (2.0 * g1 * g2 + Tc) / (g1 * g1 + g2 * g2 + Tc);
     if (col_out) {
-      const double qd = static_cast<double>(q);
-      acc += qd;
-      acc2 += qd * qd;
+      acc += q;
+      acc2 += q * q;
     }
     x0 = x1;
     x1 = x2;
@@ -144,7 +156,7 @@ static int gmsd_geometry(int H, int W, int downsample, int* Hd, int* Wd, int* Ho
 template <typename T>
 static void launch_gmsd_t(bool down, dim3 grid, hipStream_t st, const void* x,
                           const void* y, int H, int W, int Hd, int Wd, int Hout,
-                          int Wout, float Tc, float eps, int strips, int bpp,
+                          int Wout, double Tc, double eps, int strips, int bpp,
                           double* psum, double* psumsq) {
   const T* tx = static_cast<const T*>(x);
   const T* ty = static_cast<const T*>(y);
@@ -189,7 +201,7 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(total));
   const bool down = downsample != 0;
-  const float T = static_cast<float>(Tc), e = static_cast<float>(eps);
+  const double T = Tc, e = eps;
   switch (dtype) {
     case FA_U8: launch_gmsd_t<uint8_t>(down, grid, st, x, y, H, W, Hd, Wd, Hout, Wout, T, e, strips, bpp, psum, psumsq); break;
     case FA_F16: launch_gmsd_t<half_t>(down, grid, st, x, y, H, W, Hd, Wd, Hout, Wout, T, e, strips, bpp, psum, psumsq); break;

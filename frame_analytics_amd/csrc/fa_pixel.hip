@@ -29,6 +29,16 @@
 namespace fa {
 
 constexpr int PIX_UNROLL = 4;      // independent vector loads in flight per tensor
+
+// Streaming loads.  Every byte is read once, so the loads are non-temporal
+// (measured on MI355X: a pure 16-byte read stream reaches ~6.7 TB/s this way
+// against ~5.6 TB/s with default cache policy).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ inline uint4 ld_stream(const uint4* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
 constexpr int PIX_WG_PER_CU = 8;   // workgroups per CU the grid aims for
 constexpr int PIX_MIN_ELEMS_PER_THREAD = 64;
 
@@ -122,7 +132,8 @@ __global__ __launch_bounds__(BLOCK) void pix_u8_kernel(
     head = static_cast<int64_t>((V - (reinterpret_cast<uintptr_t>(pa) & (V - 1))) & (V - 1));
     if (head > per) head = per;
   }
-  const int64_t nvec = (per - head) / V;
+  // V == 1 has no vector body: the byte loop below covers the whole image
+  const int64_t nvec = V > 1 ? (per - head) / V : 0;
   const int64_t body_end = head + nvec * V;
   const int64_t gtid = static_cast<int64_t>(blockIdx.x) * BLOCK + threadIdx.x;
   const int64_t gstride = static_cast<int64_t>(bpi) * BLOCK;
@@ -136,8 +147,8 @@ __global__ __launch_bounds__(BLOCK) void pix_u8_kernel(
       uint4 xa[PIX_UNROLL], xb[PIX_UNROLL];
 #pragma unroll
       for (int u = 0; u < PIX_UNROLL; ++u) {
-        xa[u] = va[v + u * gstride];
-        xb[u] = vb[v + u * gstride];
+        xa[u] = ld_stream(va + v + u * gstride);
+        xb[u] = ld_stream(vb + v + u * gstride);
       }
 #pragma unroll
       for (int u = 0; u < PIX_UNROLL; ++u) {
@@ -149,8 +160,8 @@ __global__ __launch_bounds__(BLOCK) void pix_u8_kernel(
       acc.flush();
     }
     for (; v < nvec; v += gstride) {
-      const uint4 xa = va[v];
-      const uint4 xb = vb[v];
+      const uint4 xa = ld_stream(va + v);
+      const uint4 xb = ld_stream(vb + v);
       acc.dword(xa.x, xb.x, param);
       acc.dword(xa.y, xb.y, param);
       acc.dword(xa.z, xb.z, param);
@@ -165,15 +176,15 @@ __global__ __launch_bounds__(BLOCK) void pix_u8_kernel(
       uint32_t xa[PIX_UNROLL], xb[PIX_UNROLL];
 #pragma unroll
       for (int u = 0; u < PIX_UNROLL; ++u) {
-        xa[u] = va[v + u * gstride];
-        xb[u] = vb[v + u * gstride];
+        xa[u] = ld_stream(va + v + u * gstride);
+        xb[u] = ld_stream(vb + v + u * gstride);
       }
 #pragma unroll
       for (int u = 0; u < PIX_UNROLL; ++u) acc.dword(xa[u], xb[u], param);
       acc.flush();
     }
     for (; v < nvec; v += gstride) {
-      acc.dword(va[v], vb[v], param);
+      acc.dword(ld_stream(va + v), ld_stream(vb + v), param);
       acc.flush();
     }
   }
@@ -229,8 +240,8 @@ __global__ __launch_bounds__(BLOCK) void pix_float_kernel(
       uint4 ra[PIX_UNROLL], rb[PIX_UNROLL];
 #pragma unroll
       for (int u = 0; u < PIX_UNROLL; ++u) {
-        ra[u] = va[v + u * gstride];
-        rb[u] = vb[v + u * gstride];
+        ra[u] = ld_stream(va + v + u * gstride);
+        rb[u] = ld_stream(vb + v + u * gstride);
       }
       A part = A(0);
 #pragma unroll
@@ -247,8 +258,8 @@ __global__ __launch_bounds__(BLOCK) void pix_float_kernel(
       acc += static_cast<double>(part);
     }
     for (; v < nvec; v += gstride) {
-      const uint4 ra = va[v];
-      const uint4 rb = vb[v];
+      const uint4 ra = ld_stream(va + v);
+      const uint4 rb = ld_stream(vb + v);
       T ea[E], eb[E];
       __builtin_memcpy(ea, &ra, 16);
       __builtin_memcpy(eb, &rb, 16);

@@ -31,7 +31,15 @@ enum { MODE_REDUCE = 0, MODE_MAP = 1, MODE_CS = 2, MODE_PREP = 3, MODE_PREP_CS =
 
 // Output rows per workgroup.  Part of the partial-buffer geometry, so it is a
 // property of the library, reported through the *_workspace queries.
-constexpr int SSIM_TH = 64;
+#ifndef FA_SSIM_TH
+#define FA_SSIM_TH 64
+#endif
+constexpr int SSIM_TH = FA_SSIM_TH;
+
+// a / b.  The float32 forward uses v_rcp_f32 (1 ulp) and a multiply instead of
+// the ~9-instruction IEEE division sequence; float64 divides exactly.
+__device__ inline float quot(float a, float b) { return a * __builtin_amdgcn_rcpf(b); }
+__device__ inline double quot(double a, double b) { return a / b; }
 
 struct SsimArgs {
   const void* x;
@@ -61,10 +69,10 @@ struct SsimPol {
     CT x, y;
   };
 
-  const T* __restrict__ x;
-  const T* __restrict__ y;
-  int64_t in_off;
+  const T* __restrict__ x;  // this plane of x
+  const T* __restrict__ y;  // this plane of y
   int H, W;
+  uint32_t lcol;            // this lane's column, clamped into the image
   CT shift, C1, C2;
   int64_t out_off;
   int Wout;
@@ -75,15 +83,24 @@ struct SsimPol {
   float* __restrict__ oty;
   const float* __restrict__ dmap;
   CT g_uniform, gS, gCS;
+  CT k1;  // 2 shift^2 + C1
+  CT row_s, row_cs;
   double acc_s, acc_cs;
 
-  __device__ inline Raw load(int row, int col) const {
-    // the forward's tap origin is 0, so row and col are never negative
-    if (row < H && col < W) {
-      const int64_t o = in_off + static_cast<int64_t>(row) * W + col;
-      return Raw{load_as<CT>(x, o), load_as<CT>(y, o)};
-    }
-    return Raw{shift, shift};
+  // The forward's tap origin is 0, so rows and columns are never negative.
+  // Rows past H and columns past W only feed outputs outside the map, so they
+  // are clamped into the image instead of branched around.
+  __device__ inline void set_column(int col) {
+    lcol = static_cast<uint32_t>(col < W ? col : W - 1);
+  }
+
+  __device__ inline Raw load(int row) const {
+    // a plane holds < 2^31 elements (checked on the host): 32-bit offsets
+    const uint32_t o = static_cast<uint32_t>(row < H ? row : H - 1) * static_cast<uint32_t>(W) + lcol;
+    if constexpr (sizeof(CT) == 8)
+      return Raw{Elem<T>::d(x[o]), Elem<T>::d(y[o])};
+    else
+      return Raw{Elem<T>::f(x[o]), Elem<T>::f(y[o])};
   }
 
   __device__ inline void moments(const Raw& r, CT* m) const {
@@ -96,28 +113,35 @@ struct SsimPol {
     m[3] = d * d;
   }
 
-  __device__ inline void emit(int orow, int ocol, const CT* v) {
+  // Per output pixel, from the four filtered moments v = (E x', E y', E x'y',
+  // E (x'-y')^2) with x' = x - shift, u = E x':
+  //   A1 = 2 mu_x mu_y + C1 = 2 ux uy + 2 shift (ux + uy) + (2 shift^2 + C1)
+  //   B1 = mu_x^2 + mu_y^2 + C1 = A1 + (ux - uy)^2
+  //   A2 = 2 sigma_xy + C2,  sigma_xy = E x'y' - ux uy
+  //   B2 = sigma_x^2 + sigma_y^2 + C2 = E (x'-y')^2 + A2 - (ux - uy)^2
+  // `valid` masks lanes whose column lies outside the map.
+  __device__ inline void emit(int orow, int ocol, const CT* v, bool valid) {
     const CT ux = v[0];
     const CT uy = v[1];
-    const CT mx = ux + shift;
-    const CT my = uy + shift;
-    const CT sxy = v[2] - ux * uy;
+    const CT p = ux * uy;
     const CT du = ux - uy;
-    const CT sxx_syy = v[3] + CT(2) * sxy - du * du;
-    const CT A1 = CT(2) * mx * my + C1;
-    const CT A2 = CT(2) * sxy + C2;
-    const CT B1 = mx * mx + my * my + C1;
-    const CT B2 = sxx_syy + C2;
+    const CT A1 = fma(CT(2), p, fma(CT(2) * shift, ux + uy, k1));
+    const CT B1 = fma(du, du, A1);
+    const CT A2 = fma(CT(2), v[2] - p, C2);
+    const CT B2 = fma(-du, du, v[3] + A2);
     if constexpr (MODE == MODE_REDUCE || MODE == MODE_MAP) {
-      const CT s = (A1 * A2) / (B1 * B2);
-      if constexpr (MODE == MODE_MAP)
-        map[out_off + static_cast<int64_t>(orow) * Wout + ocol] = static_cast<float>(s);
-      acc_s += static_cast<double>(s);
+      const CT s = quot(A1 * A2, B1 * B2);
+      if constexpr (MODE == MODE_MAP) {
+        if (valid) map[out_off + static_cast<int64_t>(orow) * Wout + ocol] = static_cast<float>(s);
+      }
+      row_s += valid ? s : CT(0);
     } else if constexpr (MODE == MODE_CS) {
-      const CT inv = CT(1) / (B1 * B2);
-      acc_s += static_cast<double>(A1 * A2 * inv);
-      acc_cs += static_cast<double>(A2 * B1 * inv);
-    } else {
+      const CT inv = quot(CT(1), B1 * B2);
+      row_s += valid ? A1 * A2 * inv : CT(0);
+      row_cs += valid ? A2 * B1 * inv : CT(0);
+    } else if (valid) {
+      const CT mx = ux + shift;
+      const CT my = uy + shift;
       const CT iB1 = CT(1) / B1;
       const CT iB2 = CT(1) / B2;
       const CT S = A1 * A2 * iB1 * iB2;
@@ -142,10 +166,26 @@ struct SsimPol {
       if (oty) oty[idx] = static_cast<float>(gm * dmuy - CT(2) * b * uy - c * ux);
     }
   }
+
+  // A lane's four outputs of a phase are summed at the compute type, then
+  // folded into the float64 lane total.
+  __device__ inline void end_row() {
+    acc_s += static_cast<double>(row_s);
+    acc_cs += static_cast<double>(row_cs);
+    row_s = CT(0);
+    row_cs = CT(0);
+  }
 };
 
+// Optional register budget for the float32 forward kernels, in waves per SIMD.
+#if defined(FA_SSIM_WPE) && FA_SSIM_WPE > 0
+#define FA_SSIM_ATTR __attribute__((amdgpu_waves_per_eu(FA_SSIM_WPE)))
+#else
+#define FA_SSIM_ATTR
+#endif
+
 template <typename T, typename CT, int MODE, int KW>
-__global__ __launch_bounds__(BLOCK) void ssim_kernel(SsimArgs a) {
+__global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   __shared__ CT sbuf[2][PH][4][HROW];
   __shared__ double sred[2 * WAVES_PER_BLOCK];
 
@@ -155,9 +195,9 @@ __global__ __launch_bounds__(BLOCK) void ssim_kernel(SsimArgs a) {
   const int strip = tile - chunk * a.strips;
 
   SsimPol<T, CT, MODE> pol;
-  pol.x = static_cast<const T*>(a.x);
-  pol.y = static_cast<const T*>(a.y);
-  pol.in_off = static_cast<int64_t>(plane) * a.H * a.W;
+  const int64_t in_off = static_cast<int64_t>(plane) * a.H * a.W;
+  pol.x = static_cast<const T*>(a.x) + in_off;
+  pol.y = static_cast<const T*>(a.y) + in_off;
   pol.H = a.H;
   pol.W = a.W;
   pol.shift = static_cast<CT>(a.shift);
@@ -181,6 +221,9 @@ __global__ __launch_bounds__(BLOCK) void ssim_kernel(SsimArgs a) {
     pol.gS = static_cast<CT>(a.gs[plane]) * static_cast<CT>(a.gnorm);
     pol.gCS = static_cast<CT>(a.gcs[plane]) * static_cast<CT>(a.gnorm);
   }
+  pol.k1 = static_cast<CT>(2.0 * a.shift * a.shift + a.C1);
+  pol.row_s = CT(0);
+  pol.row_cs = CT(0);
   pol.acc_s = 0.0;
   pol.acc_cs = 0.0;
 
@@ -206,20 +249,20 @@ __global__ __launch_bounds__(BLOCK) void ssim_kernel(SsimArgs a) {
 // (zero outside the valid Hout x Wout support) and combined with x', y'.
 // --------------------------------------------------------------------------
 struct ScatterArgs {
-  const float* x;
-  const float* y;
+  const void* x;   // float or double, like dx / dy
+  const void* y;
   const float* ab;
   const float* ac;
   const float* atx;
   const float* aty;
-  float* dx;
-  float* dy;
+  void* dx;
+  void* dy;
   const float* win;
   int H, W, Hout, Wout, TH, strips, bpp;
   double shift;
 };
 
-template <bool DY>
+template <typename T, bool DY>
 struct ScatterPol {
   static constexpr int NP = DY ? 4 : 3;
   using CT = double;
@@ -227,28 +270,36 @@ struct ScatterPol {
     float v[NP];
   };
 
-  const float* __restrict__ aux[4];
-  int64_t aux_off;
+  const float* __restrict__ aux[4];  // this plane of each coefficient map
   int Hout, Wout;
-  const float* __restrict__ x;
-  const float* __restrict__ y;
+  uint32_t lcol;  // this lane's map column, clamped into the map
+  bool col_ok;    // ...and whether it was inside before clamping
+  const T* __restrict__ x;
+  const T* __restrict__ y;
   int64_t img_off;
   int W;
   double shift;
-  float* __restrict__ dx;
-  float* __restrict__ dy;
+  T* __restrict__ dx;
+  T* __restrict__ dy;
 
-  __device__ inline Raw load(int row, int col) const {
-    Raw r;
-    if (row >= 0 && row < Hout && col >= 0 && col < Wout) {
-      const int64_t o = aux_off + static_cast<int64_t>(row) * Wout + col;
+  // Zero padding outside the Hout x Wout support, branch free: the clamped
+  // address is always loaded and the value masked.
+  __device__ inline void set_column(int col) {
+    col_ok = col >= 0 && col < Wout;
+    lcol = static_cast<uint32_t>(col < 0 ? 0 : (col < Wout ? col : Wout - 1));
+  }
+
+  __device__ inline Raw load(int row) const {
+    const bool ok = col_ok && row >= 0 && row < Hout;
+    const uint32_t r = static_cast<uint32_t>(row < 0 ? 0 : (row < Hout ? row : Hout - 1));
+    const uint32_t o = r * static_cast<uint32_t>(Wout) + lcol;  // uniform row, lane column
+    Raw v;
 #pragma unroll
-      for (int p = 0; p < NP; ++p) r.v[p] = aux[p][o];
-    } else {
-#pragma unroll
-      for (int p = 0; p < NP; ++p) r.v[p] = 0.0f;
+    for (int p = 0; p < NP; ++p) {
+      const float t = aux[p][o];
+      v.v[p] = ok ? t : 0.0f;
     }
-    return r;
+    return v;
   }
 
   __device__ inline void moments(const Raw& r, double* m) const {
@@ -256,18 +307,21 @@ struct ScatterPol {
     for (int p = 0; p < NP; ++p) m[p] = static_cast<double>(r.v[p]);
   }
 
-  __device__ inline void emit(int orow, int ocol, const double* v) {
+  __device__ inline void end_row() {}
+
+  __device__ inline void emit(int orow, int ocol, const double* v, bool valid) {
+    if (!valid) return;
     const int64_t o = img_off + static_cast<int64_t>(orow) * W + ocol;
     const double xv = static_cast<double>(x[o]) - shift;
     const double yv = static_cast<double>(y[o]) - shift;
-    if (dx) dx[o] = static_cast<float>(2.0 * xv * v[0] + yv * v[1] + v[2]);
-    if constexpr (DY) dy[o] = static_cast<float>(2.0 * yv * v[0] + xv * v[1] + v[3]);
+    if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2]);
+    if constexpr (DY) dy[o] = static_cast<T>(2.0 * yv * v[0] + xv * v[1] + v[3]);
   }
 };
 
-template <int KW, bool DY>
+template <typename T, int KW, bool DY>
 __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
-  constexpr int NP = ScatterPol<DY>::NP;
+  constexpr int NP = ScatterPol<T, DY>::NP;
   __shared__ double sbuf[2][PH][NP][HROW];
 
   const int plane = blockIdx.x / a.bpp;
@@ -275,22 +329,23 @@ __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
   const int chunk = tile / a.strips;
   const int strip = tile - chunk * a.strips;
 
-  ScatterPol<DY> pol;
-  pol.aux[0] = a.ab;
-  pol.aux[1] = a.ac;
-  pol.aux[2] = a.atx;
-  pol.aux[3] = a.aty;
-  pol.aux_off = static_cast<int64_t>(plane) * a.Hout * a.Wout;
+  ScatterPol<T, DY> pol;
+  const int64_t aux_off = static_cast<int64_t>(plane) * a.Hout * a.Wout;
+  pol.aux[0] = a.ab + aux_off;
+  pol.aux[1] = a.ac + aux_off;
+  pol.aux[2] = a.atx + aux_off;
+  pol.aux[3] = DY ? a.aty + aux_off : nullptr;
   pol.Hout = a.Hout;
   pol.Wout = a.Wout;
-  pol.x = a.x;
-  pol.y = a.y;
+  pol.x = static_cast<const T*>(a.x);
+  pol.y = static_cast<const T*>(a.y);
   pol.img_off = static_cast<int64_t>(plane) * a.H * a.W;
   pol.W = a.W;
   pol.shift = a.shift;
-  pol.dx = a.dx;
-  pol.dy = a.dy;
-  strip_engine<ScatterPol<DY>, KW>(pol, a.win, -(KW - 1), a.H, a.W, a.TH, strip, chunk, sbuf);
+  pol.dx = static_cast<T*>(a.dx);
+  pol.dy = static_cast<T*>(a.dy);
+  strip_engine<ScatterPol<T, DY>, KW>(pol, a.win, -(KW - 1), a.H, a.W, a.TH, strip, chunk,
+                                      sbuf);
 }
 
 // Per-plane means of two partial arrays (MS-SSIM keeps planes apart).
@@ -343,14 +398,14 @@ static int launch_ssim(int dtype, int K, dim3 grid, hipStream_t st, const SsimAr
   }
 }
 
-template <bool DY>
+template <typename T, bool DY>
 static int launch_scatter_k(int K, dim3 grid, hipStream_t st, const ScatterArgs& a) {
   switch (K) {
-    case 3: hipLaunchKernelGGL((scatter_kernel<3, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((scatter_kernel<5, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 7: hipLaunchKernelGGL((scatter_kernel<7, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 9: hipLaunchKernelGGL((scatter_kernel<9, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 11: hipLaunchKernelGGL((scatter_kernel<11, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((scatter_kernel<T, 3, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((scatter_kernel<T, 5, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((scatter_kernel<T, 7, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 9: hipLaunchKernelGGL((scatter_kernel<T, 9, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 11: hipLaunchKernelGGL((scatter_kernel<T, 11, DY>), grid, dim3(BLOCK), 0, st, a); break;
     default: return FA_E_WINDOW;
   }
   FA_LAUNCH_CHECK();
@@ -360,6 +415,7 @@ static int launch_scatter_k(int K, dim3 grid, hipStream_t st, const ScatterArgs&
 // Validates the common SSIM arguments and derives the output geometry.
 static int ssim_shape(int N, int C, int H, int W, int K, int* Hout, int* Wout) {
   if (N <= 0 || C <= 0 || H <= 0 || W <= 0) return FA_E_SHAPE;
+  if (static_cast<int64_t>(H) * W > INT32_MAX) return FA_E_SHAPE;  // 32-bit plane offsets
   if (K < 3 || K > FA_MAX_WIN || (K & 1) == 0) return FA_E_WINDOW;
   *Hout = H - K + 1;
   *Wout = W - K + 1;
@@ -375,13 +431,15 @@ static int grid_of(int64_t planes, int64_t per_plane, dim3* grid) {
   return FA_OK;
 }
 
-// The coefficient pass plus the scatter, shared by both backward entry points.
-template <int MODE>
-static int ssim_backward_impl(const float* x, const float* y, const float* dmap,
+// The coefficient pass plus the scatter, shared by the backward entry points.
+// T is the element type of x, y, dx and dy (float, or double for the float64
+// MS-SSIM pyramid levels); the arithmetic is float64 either way.
+template <typename T, int MODE>
+static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
                               const float* gscalar, const float* gs,
                               const float* gcs, const float* win, int K, int N,
                               int C, int H, int W, double shift, double C1,
-                              double C2, float* aux, float* dx, float* dy,
+                              double C2, float* aux, T* dx, T* dy,
                               hipStream_t st) {
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
@@ -418,7 +476,7 @@ static int ssim_backward_impl(const float* x, const float* y, const float* dmap,
   dim3 grid;
   rc = grid_of(planes, a.bpp, &grid);
   if (rc != FA_OK) return rc;
-  rc = launch_ssim_k<float, double, MODE>(K, grid, st, a);
+  rc = launch_ssim_k<T, double, MODE>(K, grid, st, a);
   if (rc != FA_OK) return rc;
 
   ScatterArgs s = {};
@@ -441,7 +499,7 @@ static int ssim_backward_impl(const float* x, const float* y, const float* dmap,
   s.shift = shift;
   rc = grid_of(planes, s.bpp, &grid);
   if (rc != FA_OK) return rc;
-  return dy ? launch_scatter_k<true>(K, grid, st, s) : launch_scatter_k<false>(K, grid, st, s);
+  return dy ? launch_scatter_k<T, true>(K, grid, st, s) : launch_scatter_k<T, false>(K, grid, st, s);
 }
 
 }  // namespace fa
@@ -563,9 +621,9 @@ FA_API int fa_gpu_ssim_backward(const float* x, const float* y,
   if (!dx && !dy) return FA_E_ARG;
   if (!dL_dmap && !grad_scalar) return FA_E_ARG;
   FA_DEVICE_SCOPE(device);
-  return ssim_backward_impl<MODE_PREP>(x, y, dL_dmap, grad_scalar, nullptr, nullptr, win, K,
-                                       N, C, H, W, shift, C1, C2, aux, dx, dy,
-                                       static_cast<hipStream_t>(stream));
+  return ssim_backward_impl<float, MODE_PREP>(x, y, dL_dmap, grad_scalar, nullptr, nullptr,
+                                              win, K, N, C, H, W, shift, C1, C2, aux, dx, dy,
+                                              static_cast<hipStream_t>(stream));
 }
 
 // reference: fa_cuda.cu:1365-1414 (fa_cuda_ssim_cs_backward)
@@ -578,9 +636,34 @@ FA_API int fa_gpu_ssim_cs_backward(const float* x, const float* y,
   if (!x || !y || !gs || !gcs || !win || !aux) return FA_E_ARG;
   if (!dx && !dy) return FA_E_ARG;
   FA_DEVICE_SCOPE(device);
-  return ssim_backward_impl<MODE_PREP_CS>(x, y, nullptr, nullptr, gs, gcs, win, K, N, C, H, W,
-                                          shift, C1, C2, aux, dx, dy,
-                                          static_cast<hipStream_t>(stream));
+  return ssim_backward_impl<float, MODE_PREP_CS>(x, y, nullptr, nullptr, gs, gcs, win, K, N, C,
+                                                 H, W, shift, C1, C2, aux, dx, dy,
+                                                 static_cast<hipStream_t>(stream));
+}
+
+// No counterpart in the reference (its MS-SSIM pyramid is float32).  The
+// fa_gpu_ssim_cs_backward contract for x / y / dx / dy of `dtype` FA_F32 or
+// FA_F64: the float64 pyramid levels of the MS-SSIM backward.  aux stays float32.
+FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
+                                      const float* gs, const float* gcs,
+                                      const float* win, int K, int N, int C,
+                                      int H, int W, double shift, double C1,
+                                      double C2, float* aux, void* dx,
+                                      void* dy, int device, void* stream) {
+  if (!x || !y || !gs || !gcs || !win || !aux) return FA_E_ARG;
+  if (!dx && !dy) return FA_E_ARG;
+  if (dtype != FA_F32 && dtype != FA_F64) return FA_E_DTYPE;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FA_F32)
+    return ssim_backward_impl<float, MODE_PREP_CS>(
+        static_cast<const float*>(x), static_cast<const float*>(y), nullptr, nullptr, gs, gcs,
+        win, K, N, C, H, W, shift, C1, C2, aux, static_cast<float*>(dx),
+        static_cast<float*>(dy), st);
+  return ssim_backward_impl<double, MODE_PREP_CS>(
+      static_cast<const double*>(x), static_cast<const double*>(y), nullptr, nullptr, gs, gcs,
+      win, K, N, C, H, W, shift, C1, C2, aux, static_cast<double*>(dx),
+      static_cast<double*>(dy), st);
 }
 
 }  // extern "C"

@@ -20,8 +20,11 @@
 // A strip yields 256 - (KW-1) output columns; neighbouring strips overlap by
 // KW-1 input columns, and neighbouring row chunks by KW-1 input rows.
 //
-// What the lane loads, which moments it forms and what happens to each output
-// pixel is a policy (see fa_ssim.hip): the SSIM forward (4 moments, float32 or
+// What the lane loads (Pol::set_column once, Pol::load(row) per row; loads are
+// branch free, out-of-grid rows and columns are clamped or zeroed by the
+// policy), which moments it forms and what happens to each output pixel
+// (Pol::emit with a validity flag, Pol::end_row after each lane's four) is a
+// policy (see fa_ssim.hip): the SSIM forward (4 moments, float32 or
 // float64), the backward coefficient pass, and the backward scatter (the
 // coefficient maps filtered back onto the full grid, which is the same
 // correlation with the input origin moved back by KW-1 and zero padding).
@@ -56,10 +59,9 @@ template <> struct LdsVec<float> { using type = float4; static constexpr int N =
 template <> struct LdsVec<double> { using type = double2; static constexpr int N = 2; };
 
 // Runs the whole strip for one (plane, strip, chunk) workgroup.
-//   in_H, in_W : input grid (values outside it are whatever Pol::load returns)
 //   off        : input row/column of tap 0 for output (0, 0): 0 for a valid
 //                correlation, -(KW-1) for the transposed (scatter) one
-//   out_H,out_W: output grid
+//   out_H,out_W: output grid (the policy knows its input grid)
 template <class Pol, int KW>
 __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
                                     int off, int out_H, int out_W, int TH,
@@ -87,13 +89,18 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
   const int in_row0 = r0 + off;           // input row of tap 0 for output row r0
   const int nph = (rows_here + PH - 1) / PH;
 
+  // The column is per lane and fixed for the whole strip; the row is uniform
+  // across the workgroup, so every row address is scalar arithmetic and a load
+  // costs one 32-bit lane offset.
+  pol.set_column(in_col);
+
   CT ring[RS][NP];
 #pragma unroll
-  for (int i = 0; i < KW - 1; ++i) pol.moments(pol.load(in_row0 + i, in_col), ring[i]);
+  for (int i = 0; i < KW - 1; ++i) pol.moments(pol.load(in_row0 + i), ring[i]);
 
   Raw pend[PH];
 #pragma unroll
-  for (int i = 0; i < PH; ++i) pend[i] = pol.load(in_row0 + KW - 1 + i, in_col);
+  for (int i = 0; i < PH; ++i) pend[i] = pol.load(in_row0 + KW - 1 + i);
 
   const int hrow = threadIdx.x / WAVE;          // phase row of this wave
   const int oc_l = COLS_PER_LANE * (threadIdx.x % WAVE);  // strip-local output column
@@ -105,11 +112,10 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
       if (q < nph) {  // uniform across the workgroup
 #pragma unroll
         for (int i = 0; i < PH; ++i) pol.moments(pend[i], ring[(KW - 1 + u * PH + i) % RS]);
-        if (q + 1 < nph) {
+        // Prefetch the next phase unconditionally: loads are clamped by the
+        // policy, and a guard here would cost register copies every phase.
 #pragma unroll
-          for (int i = 0; i < PH; ++i)
-            pend[i] = pol.load(in_row0 + KW - 1 + (q + 1) * PH + i, in_col);
-        }
+        for (int i = 0; i < PH; ++i) pend[i] = pol.load(in_row0 + KW - 1 + (q + 1) * PH + i);
 
         // ---- vertical taps, from the register ring ----------------------
         CT (*dst)[NP][HROW] = sbuf[q & 1];
@@ -153,8 +159,9 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
 #pragma unroll
           for (int k = 0; k < COLS_PER_LANE; ++k) {
             const int oc = col0 + oc_l + k;
-            if (oc_l + k < OUTW && oc < out_W) pol.emit(r0 + orow_l, oc, h[k]);
+            pol.emit(r0 + orow_l, oc, h[k], oc_l + k < OUTW && oc < out_W);
           }
+          pol.end_row();
         }
       }
     }

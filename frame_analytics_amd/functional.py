@@ -430,6 +430,33 @@ class _FusedSSIMCS(torch.autograd.Function):
         return (dx if need_dx else None, dy if need_dy else None, None, None, None, None)
 
 
+class _Pool2(torch.autograd.Function):
+    """The native MS-SSIM pyramid step (``fa_gpu_pool2``): 2x2 means of x and y
+    in float32 for uint8 input (exact) and float64 for floating input.
+    The backward spreads a quarter of each gradient over its 2x2 block."""
+
+    @staticmethod
+    def forward(ctx, x, y):
+        from . import backend
+
+        ctx.shapes = (x.shape, y.shape)
+        ctx.dtypes = (x.dtype, y.dtype)
+        return backend.pool2_gpu(x, y)
+
+    @staticmethod
+    def backward(ctx, gx, gy):
+        def spread(g, shape, dtype, needed):
+            if g is None or not needed:
+                return None
+            h2, w2 = g.shape[-2] * 2, g.shape[-1] * 2
+            full = g.new_zeros(shape)
+            full[..., :h2, :w2] = (0.25 * g).repeat_interleave(2, -2).repeat_interleave(2, -1)
+            return full.to(dtype)
+
+        return (spread(gx, ctx.shapes[0], ctx.dtypes[0], ctx.needs_input_grad[0]),
+                spread(gy, ctx.shapes[1], ctx.dtypes[1], ctx.needs_input_grad[1]))
+
+
 def _ssim_cs_pair(x4, y4, win, wdt, shift, C1, C2, backend_hint):
     """``(ssim, cs)`` plane means, each ``(N, C)``."""
     from . import backend
@@ -480,13 +507,22 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
             f"image {tuple(x4.shape[-2:])} is too small for {scales} scales with a "
             f"{win_size}x{win_size} window; needs at least {need} px on a side")
 
+    from . import backend
+
     win = gaussian_window_1d(win_size, sigma, device=x4.device, dtype=wdt)
+    # On the GPU the pyramid is built by the native pooling kernel and held
+    # exactly (the coarse scales amplify a rounded level ~100x in the gradient);
+    # the portable path pools at the working dtype, as the reference does.
+    native_pyramid = backend_hint != "torch" and backend.pool2_available(x4, y4)
     cx, cy = x4, y4
     terms = []
     for i in range(scales):
         if i:
-            cx = F.avg_pool2d(cx.to(wdt), 2)
-            cy = F.avg_pool2d(cy.to(wdt), 2)
+            if native_pyramid:
+                cx, cy = _Pool2.apply(cx, cy)
+            else:
+                cx = F.avg_pool2d(cx.to(wdt), 2)
+                cy = F.avg_pool2d(cy.to(wdt), 2)
         s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
         terms.append(s if i == scales - 1 else cs)
     # a fractional power of a negative factor is not real: clamp at zero

@@ -160,6 +160,35 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
                        double* psum, double* psumsq, int bpp, double* out_mean,
                        double* out_std, int device, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Extensions: no counterpart in the reference's C ABI.                     */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * No counterpart in the reference, which pools its MS-SSIM pyramid with torch
+ * between scales (reference functional.py:876-885).  One pyramid step for x and
+ * y at once: non-overlapping 2x2 mean, odd trailing row / column dropped, over
+ * `planes` planes of H x W.  out_dtype must be FA_F32 for uint8 input (exact)
+ * and FA_F64 for every floating input (exact for float16; for float32 and
+ * bfloat16 unless a 2x2 block spans more than 2^29 / 2^45 in magnitude).
+ * ox / oy: planes * (H/2) * (W/2) elements of out_dtype.
+ */
+FA_API int fa_gpu_pool2(const void* x, const void* y, int dtype, int planes,
+                        int H, int W, void* ox, void* oy, int out_dtype,
+                        int device, void* stream);
+
+/*
+ * No counterpart in the reference.  fa_gpu_ssim_cs_backward for x / y / dx / dy
+ * of element type `dtype` (FA_F32 or FA_F64): the float64 levels of the exact
+ * MS-SSIM pyramid.  aux stays float32 with the same size.
+ */
+FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
+                                      const float* gs, const float* gcs,
+                                      const float* win, int K, int N, int C,
+                                      int H, int W, double shift, double C1,
+                                      double C2, float* aux, void* dx,
+                                      void* dy, int device, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

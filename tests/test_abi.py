@@ -36,7 +36,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 12
+    assert len(decl) == 14  # 12 reference entry points + 2 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -85,3 +85,10 @@ def test_argument_validation_before_any_gpu_work(lib):
     assert lib.fa_gpu_ssim_backward(p, p, None, None, p, 11, 1, 1, 64, 64, 0.5, 1e-4, 9e-4,
                                     p, p, None, 0, None) == 5  # no upstream gradient
     assert lib.fa_gpu_gmsd(p, p, 0, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, 99, p, p, 0, None) == 5
+    # the pyramid step insists on its exact output type
+    assert lib.fa_gpu_pool2(p, p, 0, 1, 4, 4, p, p, 4, 0, None) == 1  # uint8 -> float64
+    assert lib.fa_gpu_pool2(p, p, 3, 1, 4, 4, p, p, 3, 0, None) == 1  # float32 -> float32
+    assert lib.fa_gpu_pool2(p, p, 1, 1, 4, 4, p, p, 3, 0, None) == 1  # float16 -> float32
+    assert lib.fa_gpu_pool2(p, p, 0, 1, 1, 4, p, p, 3, 0, None) == 2  # one row
+    assert lib.fa_gpu_ssim_cs_backward_ex(p, p, 0, p, p, p, 11, 1, 1, 64, 64, 0.5, 1e-4,
+                                          9e-4, p, p, None, 0, None) == 1  # uint8 input

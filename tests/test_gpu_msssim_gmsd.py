@@ -1,9 +1,8 @@
 """GPU parity of MS-SSIM (value and gradient) and GMSD / GMS.
 
 Bar: values within 1e-6 relative of float64; gradients 1e-6 max-normwise
-relative.  GMSD's q map is float32 (like the reference's kernel), so GMSD is
-additionally held to the reference's absolute gate where the value itself is
-~1e-8 (the identity case).
+relative (the MS-SSIM pyramid is exact, see fa_pool.hip).  Where the true value
+is zero (GMSD of identical frames) the bar is the reference's absolute one.
 """
 
 from __future__ import annotations
@@ -172,3 +171,33 @@ def test_gms_loss_gradient_finite(gpu):
     y = x.detach().clone()
     fa.GMSD(data_range=1.0).loss(x, y).backward()
     assert torch.isfinite(x.grad).all()
+
+
+# --------------------------------------------------------------------------- #
+# the pyramid step
+# --------------------------------------------------------------------------- #
+
+
+@pytest.mark.parametrize("dt", [torch.uint8, torch.float16, torch.bfloat16, torch.float32,
+                                torch.float64])
+@pytest.mark.parametrize("hw", [(2, 2), (9, 12), (10, 7), (33, 1), (1080, 1920)])
+def test_pool2_exact(gpu, dt, hw):
+    """fa_gpu_pool2 equals float64 avg_pool2d bit for bit, in the exact type."""
+    from frame_analytics_amd import backend
+
+    h, w = hw
+    if w < 2:
+        pytest.skip("needs two columns")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(h * 31 + w)
+    if dt == torch.uint8:
+        x = torch.randint(0, 256, (2, 3, h, w), dtype=dt, device=gpu, generator=g)
+        y = torch.randint(0, 256, (2, 3, h, w), dtype=dt, device=gpu, generator=g)
+    else:
+        x = torch.rand((2, 3, h, w), device=gpu, generator=g).to(dt)
+        y = torch.rand((2, 3, h, w), device=gpu, generator=g).to(dt)
+    ox, oy = backend.pool2_gpu(x, y)
+    assert ox.dtype == backend.pyramid_dtype(dt)
+    wx = torch.nn.functional.avg_pool2d(x.double(), 2)
+    wy = torch.nn.functional.avg_pool2d(y.double(), 2)
+    assert torch.equal(ox.double(), wx) and torch.equal(oy.double(), wy)

@@ -77,7 +77,9 @@ def test_dtypes(gpu, dt):
     want = ref.ssim(x.double().cpu().numpy()[None, None], y.double().cpu().numpy()[None, None],
                     255.0)
     got = float(fa.ssim(x, y, data_range=255.0))
-    tol = 1e-12 if dt == torch.float64 else REL
+    # float64 input runs a float64 kernel; the ABI hands it a float32 window,
+    # whose rounding (6e-8 per tap) is what is left between it and the oracle
+    tol = 1e-9 if dt == torch.float64 else REL
     assert _rel(got, want) <= tol, (dt, got, want)
 
 
