@@ -134,8 +134,8 @@ def profile_sequence(launches=20):
     """A fixed launch sequence for rocprofv3 counter runs (``--profile``):
     a torch copy of exactly 256 MiB (the FETCH_SIZE / WRITE_SIZE calibration:
     256 MiB read, 256 MiB written), then `launches` launches each of the SSIM
-    strip kernel and of the PSNR pixel kernel, through
-    the C ABI with no finalize sinks, rotating resident input pairs."""
+    strip kernel, the GMSD kernel and the PSNR pixel
+    kernel, through the C ABI, rotating resident input pairs."""
     import torch
 
     import frame_analytics_amd as fa
@@ -163,7 +163,19 @@ def profile_sequence(launches=20):
                                127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, None,
                                partial.data_ptr(), bpp, None, None, 0, stream) == 0
     torch.cuda.synchronize()
-    del pairs, partial
+    # GMSD (configs[4]: downsample, per-channel pooled) on the same pairs
+    gbpp = backend._gmsd_workspace(ext, h, w, True)
+    ps = torch.empty((n * c, gbpp), dtype=torch.float64, device=dev)
+    ps2 = torch.empty_like(ps)
+    gm = torch.empty(n, dtype=torch.float64, device=dev)
+    gs = torch.empty_like(gm)
+    for i in range(launches):
+        a, b = pairs[i % 4]
+        assert lib.fa_gpu_gmsd(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, 170.0, (255e-6) ** 2,
+                               1, ps.data_ptr(), ps2.data_ptr(), gbpp, gm.data_ptr(),
+                               gs.data_ptr(), 0, stream) == 0
+    torch.cuda.synchronize()
+    del pairs, partial, ps, ps2
 
     ppairs = _pairs(torch, PSNR_SHAPE, 4.0, 2, dev, seed=2)
     pn = PSNR_SHAPE[0]
@@ -182,8 +194,9 @@ def profile_sequence(launches=20):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=300)
+    # the part ramps its clock over the first ~100 launches of this kernel
+    ap.add_argument("--warmup", type=int, default=150)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile", action="store_true",
                     help="run the fixed launch sequence for rocprofv3 counters and exit")
@@ -237,8 +250,33 @@ def main():
     achieved = bytes_per_launch / (k_ms * 1e-3) / 1e9
     out_px = n * c * (h - 10) * (w - 10)
     tflops = out_px * SSIM_FLOP_PER_PIXEL / (k_ms * 1e-3) / 1e12
+
+    # ---------------- MS-SSIM and GMSD on the same pairs ---- #
+    reps = max(20, args.steps // 10)
+    c4 = {"workload": "8x3x1080x1920 uint8 (configs[4]), 4 resident pairs rotated"}
+    for key, fn in (
+            ("ms_ssim_ms", lambda i: fa.ms_ssim(*pairs[i % 4], data_range=255.0)),
+            ("gmsd_ms", lambda i: fa.gmsd(*pairs[i % 4], data_range=255.0)),
+            ("gmsd_luma_bt601_ms",
+             lambda i: fa.gmsd(*pairs[i % 4], data_range=255.0, luma="bt601"))):
+        c4[key] = round(_time_steps(torch, fn, reps, 5) / reps * 1e3, 4)
+    c4["gmsd_GBps"] = round(2.0 * samples / (c4["gmsd_ms"] * 1e-3) / 1e9, 1)
     del pairs, partial
     torch.cuda.empty_cache()
+
+    # ---------------- SSIM loss, forward + backward -------- #
+    g3 = torch.Generator(device=dev)
+    g3.manual_seed(3)
+    x3 = torch.rand((16, 3, 256, 256), device=dev, generator=g3)
+    y3 = (x3 + 0.05 * torch.randn(x3.shape, device=dev, generator=g3)).clamp(0, 1)
+    x3.requires_grad_(True)
+
+    def loss_step(i):
+        x3.grad = None
+        (1.0 - fa.ssim(x3, y3, data_range=1.0)).backward()
+
+    c3_ms = _time_steps(torch, loss_step, reps, 5) / reps * 1e3
+    del x3, y3
 
     # ---------------- PSNR, configs[2] ---------------------------------- #
     ppairs = _pairs(torch, PSNR_SHAPE, 4.0, 2, dev, seed=2)
@@ -301,6 +339,9 @@ def main():
             "GBps_kernel": round(pbytes / (pk_ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(pbytes / (pk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         },
+        "configs4": c4,
+        "configs3": {"workload": "1 - ssim(x, y) forward + backward, 16x3x256x256 float32",
+                     "ms_per_step": round(c3_ms, 4)},
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
     print(json.dumps(line), flush=True)

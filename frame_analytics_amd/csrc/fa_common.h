@@ -113,6 +113,23 @@ __device__ inline void block_sum2(V a, V b, V* smem, V* oa, V* ob) {
   }
 }
 
+// --------------------------------------------------------------------------
+// XCD-aware tile order
+//
+// MI355X dispatches consecutive workgroups round-robin over its 8 XCDs, each
+// with a private L2.  Tiles that share input rows / columns (neighbouring
+// strips and row chunks of one plane) should run on the same XCD, so tile t is
+// given to workgroup (t % 8)-major: XCD x takes tiles [x*q, (x+1)*q) in order.
+// The map is a bijection of [0, total) when total is a multiple of 8 and the
+// identity otherwise.
+// --------------------------------------------------------------------------
+constexpr unsigned NUM_XCD = 8;
+
+__device__ inline unsigned xcd_tile(unsigned wg, unsigned total) {
+  if (total % NUM_XCD != 0) return wg;
+  return (wg % NUM_XCD) * (total / NUM_XCD) + wg / NUM_XCD;
+}
+
 }  // namespace fa
 
 // --------------------------------------------------------------------------

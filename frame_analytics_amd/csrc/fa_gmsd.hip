@@ -64,8 +64,9 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(
     int Hout, int Wout, double Tc, double eps, int strips, int bpp,
     double* __restrict__ psum, double* __restrict__ psumsq) {
   __shared__ double sred[2 * WAVES_PER_BLOCK];
-  const int plane = blockIdx.x / bpp;
-  const int tile = blockIdx.x - plane * bpp;
+  const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
+  const int plane = t / bpp;
+  const int tile = t - plane * bpp;
   const int chunk = tile / strips;
   const int strip = tile - chunk * strips;
   const int wave = threadIdx.x / WAVE;

@@ -189,8 +189,9 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   __shared__ CT sbuf[2][PH][4][HROW];
   __shared__ double sred[2 * WAVES_PER_BLOCK];
 
-  const int plane = blockIdx.x / a.bpp;
-  const int tile = blockIdx.x - plane * a.bpp;
+  const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
+  const int plane = t / a.bpp;
+  const int tile = t - plane * a.bpp;
   const int chunk = tile / a.strips;
   const int strip = tile - chunk * a.strips;
 
@@ -324,8 +325,9 @@ __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
   constexpr int NP = ScatterPol<T, DY>::NP;
   __shared__ double sbuf[2][PH][NP][HROW];
 
-  const int plane = blockIdx.x / a.bpp;
-  const int tile = blockIdx.x - plane * a.bpp;
+  const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
+  const int plane = t / a.bpp;
+  const int tile = t - plane * a.bpp;
   const int chunk = tile / a.strips;
   const int strip = tile - chunk * a.strips;
 
