@@ -383,7 +383,17 @@ def try_ssim(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
 # --------------------------------------------------------------------------- #
 
 
-def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2):
+def pyramid_dtype(dt: torch.dtype) -> torch.dtype:
+    """Element type of the MS-SSIM pyramid levels below an input of type ``dt``:
+    float32 holds the 2x2 means of uint8 levels exactly at every depth (a level
+    k value is a multiple of 4^-k below 256), float64 those of every floating
+    type."""
+    return torch.float32 if dt == torch.uint8 else torch.float64
+
+
+def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2, pool_dtype=None):
+    """``(s, cs)`` plane means, plus the next pyramid level ``(px, py)`` of
+    ``pool_dtype`` when one is asked for (one fused pass)."""
     n, c, h, w = x.shape
     k = int(winf.numel())
     planes = n * c
@@ -392,20 +402,34 @@ def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2):
     partial_cs = _f64(x.device, planes, bpp)
     out_s = _f64(x.device, planes)
     out_cs = _f64(x.device, planes)
-    _check(ext.gpu.fa_gpu_ssim_cs(
+    if pool_dtype is None:
+        _check(ext.gpu.fa_gpu_ssim_cs(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
+            float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
+            bpp, _ptr(out_s), _ptr(out_cs), _dev(x), _stream(x)), ext)
+        return out_s, out_cs
+    px = torch.empty((n, c, h // 2, w // 2), dtype=pool_dtype, device=x.device)
+    py = torch.empty_like(px)
+    _check(ext.gpu.fa_gpu_ssim_cs_pool(
         _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
         float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
-        bpp, _ptr(out_s), _ptr(out_cs), _dev(x), _stream(x)), ext)
-    return out_s, out_cs
+        bpp, _ptr(out_s), _ptr(out_cs), _ptr(px), _ptr(py), _DTYPE_CODE[pool_dtype],
+        _dev(x), _stream(x)), ext)
+    return out_s, out_cs, px, py
 
 
-def ssim_cs_forward(x, y, win, shift, C1, C2):
-    """``(ssim, cs)`` plane means from the differentiable native path."""
+def ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype=None):
+    """``(ssim, cs)`` plane means from the differentiable native path, plus the
+    next pyramid level when ``pool_dtype`` is given."""
     ext = load()
-    return _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2)
+    return _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2,
+                        pool_dtype)
 
 
-def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy):
+def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy,
+                     gpx=None, gpy=None):
+    """Gradients of the plane means (and of the pyramid level the forward
+    pooled, ``gpx`` / ``gpy``) with respect to x and y."""
     ext = load()
     x, y = _contig(x), _contig(y)
     winf = _win_f32(win)
@@ -418,47 +442,39 @@ def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy):
                       dtype=torch.float32)
     dx = torch.empty_like(x) if need_dx else None
     dy = torch.empty_like(y) if need_dy else None
-    if x.dtype == torch.float32:
+    gpx = _contig(gpx) if (gpx is not None and need_dx) else None
+    gpy = _contig(gpy) if (gpy is not None and need_dy) else None
+    if x.dtype == torch.float32 and gpx is None and gpy is None:
         _check(ext.gpu.fa_gpu_ssim_cs_backward(
             _ptr(x), _ptr(y), _ptr(gsf), _ptr(gcsf), _ptr(winf), k, n, c, h, w,
             float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
             _dev(x), _stream(x)), ext)
     else:
+        gp = gpx if gpx is not None else gpy
+        gp_code = _DTYPE_CODE[gp.dtype] if gp is not None else _DTYPE_CODE[torch.float64]
+        if gpx is not None and gpy is not None and gpx.dtype != gpy.dtype:
+            gpy = gpy.to(gpx.dtype)
         _check(ext.gpu.fa_gpu_ssim_cs_backward_ex(
             _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], _ptr(gsf), _ptr(gcsf), _ptr(winf), k,
-            n, c, h, w, float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
-            _dev(x), _stream(x)), ext)
+            n, c, h, w, float(shift), float(C1), float(C2), _ptr(gpx), _ptr(gpy), gp_code,
+            _ptr(aux), _ptr(dx), _ptr(dy), _dev(x), _stream(x)), ext)
     return dx, dy
 
 
-# --------------------------------------------------------------------------- #
-# the MS-SSIM pyramid step
-# --------------------------------------------------------------------------- #
-
-
-def pyramid_dtype(dt: torch.dtype) -> torch.dtype:
-    """Element type of a pyramid level: float32 holds the 2x2 means of uint8
-    exactly, float64 those of every floating type (see fa_pool.hip)."""
-    return torch.float32 if dt == torch.uint8 else torch.float64
-
-
-def pool2_available(x: torch.Tensor, y: torch.Tensor) -> bool:
+def ssim_cs_pool_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> bool:
+    """Can the native MS-SSIM scale step (CS means + fused pyramid) serve x, y?"""
     return (x.is_cuda and x.dim() == 4 and x.dtype in _SUPPORTED and y.dtype == x.dtype
-            and x.shape == y.shape and x.shape[-2] >= 2 and x.shape[-1] >= 2
+            and x.shape == y.shape and win_size in _WINDOWS
+            and x.shape[-2] >= win_size and x.shape[-1] >= win_size
             and _gpu_ext(x) is not None)
 
 
-def pool2_gpu(x: torch.Tensor, y: torch.Tensor):
-    """One pyramid step of x and y on the GPU (one launch), exact."""
+def ssim_cs_pool(x, y, win, shift, C1, C2, pool_dtype):
+    """Inference form of one MS-SSIM scale: ``(s, cs, px, py)``, or ``(s, cs)``
+    when ``pool_dtype`` is None (the coarsest scale)."""
     ext = load()
-    x, y = _contig(x), _contig(y)
-    n, c, h, w = x.shape
-    od = pyramid_dtype(x.dtype)
-    ox = torch.empty((n, c, h // 2, w // 2), dtype=od, device=x.device)
-    oy = torch.empty_like(ox)
-    _check(ext.gpu.fa_gpu_pool2(_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n * c, h, w,
-                                _ptr(ox), _ptr(oy), _DTYPE_CODE[od], _dev(x), _stream(x)), ext)
-    return ox, oy
+    return _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2,
+                        pool_dtype)
 
 
 def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,

@@ -29,12 +29,47 @@ namespace fa {
 
 enum { MODE_REDUCE = 0, MODE_MAP = 1, MODE_CS = 2, MODE_PREP = 3, MODE_PREP_CS = 4 };
 
-// Output rows per workgroup.  Part of the partial-buffer geometry, so it is a
-// property of the library, reported through the *_workspace queries.
-#ifndef FA_SSIM_TH
-#define FA_SSIM_TH 64
+// Output rows per workgroup (TH).  A workgroup walks its rows in sequence, so
+// TH is the launch's critical path: a launch takes the largest TH of
+// 64, 32, 16, 8, 4 that still gives it SSIM_MIN_WGS workgroups (the halo of
+// K-1 rows re-read per chunk is what a smaller TH costs).  Large frames keep
+// TH = 64; the coarse MS-SSIM scales, small batches and small crops get the
+// parallelism back.  Every TH is a multiple of the phase height and even, so
+// pyramid row pairs never straddle two chunks.  The partial buffers are sized
+// for the smallest TH (the *_workspace queries) and a launch uses the first
+// strips * chunks slots of each plane.
+#ifndef FA_SSIM_TH_MAX
+#define FA_SSIM_TH_MAX 64
 #endif
-constexpr int SSIM_TH = FA_SSIM_TH;
+#ifndef FA_SSIM_MIN_WGS
+#define FA_SSIM_MIN_WGS 2048
+#endif
+constexpr int SSIM_TH_MAX = FA_SSIM_TH_MAX;
+constexpr int SSIM_TH_MIN = 4;
+constexpr int64_t SSIM_MIN_WGS = FA_SSIM_MIN_WGS;
+static_assert(SSIM_TH_MIN % PH == 0 && SSIM_TH_MAX % SSIM_TH_MIN == 0, "TH ladder");
+
+struct Tiling {
+  int TH, strips, tiles;  // tiles = strips * chunks, per plane
+};
+
+// The tiling of one launch over `planes` planes of an out_H x out_W grid.
+inline Tiling tiling_for(int64_t planes, int out_H, int out_W, int K) {
+  Tiling t = {SSIM_TH_MAX, 0, 0};
+  for (;; t.TH /= 2) {
+    int chunks = 0;
+    strip_grid(out_H, out_W, K, t.TH, &t.strips, &chunks);
+    t.tiles = t.strips * chunks;
+    if (t.TH <= SSIM_TH_MIN || planes * t.tiles >= SSIM_MIN_WGS) return t;
+  }
+}
+
+// Partial slots per plane the workspace query reports: enough for any TH.
+inline int ssim_slots(int out_H, int out_W, int K) {
+  int strips = 0, chunks = 0;
+  strip_grid(out_H, out_W, K, SSIM_TH_MIN, &strips, &chunks);
+  return strips * chunks;
+}
 
 // a / b.  The float32 forward uses v_rcp_f32 (1 ulp) and a multiply instead of
 // the ~9-instruction IEEE division sequence; float64 divides exactly.
@@ -59,6 +94,9 @@ struct SsimArgs {
   float* oc;
   float* otx;
   float* oty;
+  void* px;             // MODE_CS: optional pyramid step (2x2 means of x / y)
+  void* py;
+  int pool_f64;         // pyramid element type: float64 (1) or float32 (0)
 };
 
 template <typename T, typename CTy, int MODE>
@@ -86,6 +124,15 @@ struct SsimPol {
   CT k1;  // 2 shift^2 + C1
   CT row_s, row_cs;
   double acc_s, acc_cs;
+  // MODE_CS pyramid step: this workgroup owns input rows [prow0, prow1) and,
+  // on even lanes, the column pair starting at its column (pcol = col / 2)
+  void* px;
+  void* py;
+  bool pool_on, pool_f64, pcol_ok;
+  int prow0, prow1, Wd;
+  int64_t pool_off;
+  uint32_t pcol;
+  double hx, hy;  // the even row of the current row pair
 
   // The forward's tap origin is 0, so rows and columns are never negative.
   // Rows past H and columns past W only feed outputs outside the map, so they
@@ -101,6 +148,35 @@ struct SsimPol {
       return Raw{Elem<T>::d(x[o]), Elem<T>::d(y[o])};
     else
       return Raw{Elem<T>::f(x[o]), Elem<T>::f(y[o])};
+  }
+
+  // The 2x2 mean of rows (2i, 2i+1) and columns (2j, 2j+1), formed in float64
+  // (exact for the pyramid's element types) and written by the even lane.
+  __device__ inline void pool(int row, const Raw& r) {
+    if constexpr (MODE == MODE_CS) {
+      if (!pool_on || row < prow0 || row >= prow1) return;  // uniform
+      const double vx = static_cast<double>(r.x);
+      const double vy = static_cast<double>(r.y);
+      if ((row & 1) == 0) {
+        hx = vx;
+        hy = vy;
+        return;
+      }
+      double sx = hx + vx;
+      double sy = hy + vy;
+      sx += __shfl_xor(sx, 1, WAVE);
+      sy += __shfl_xor(sy, 1, WAVE);
+      if (pcol_ok) {
+        const int64_t o = pool_off + static_cast<int64_t>(row >> 1) * Wd + pcol;
+        if (pool_f64) {
+          static_cast<double*>(px)[o] = 0.25 * sx;
+          static_cast<double*>(py)[o] = 0.25 * sy;
+        } else {
+          static_cast<float*>(px)[o] = static_cast<float>(0.25 * sx);
+          static_cast<float*>(py)[o] = static_cast<float>(0.25 * sy);
+        }
+      }
+    }
   }
 
   __device__ inline void moments(const Raw& r, CT* m) const {
@@ -227,6 +303,34 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   pol.row_cs = CT(0);
   pol.acc_s = 0.0;
   pol.acc_cs = 0.0;
+  pol.px = a.px;
+  pol.py = a.py;
+  pol.pool_on = false;
+  if constexpr (MODE == MODE_CS) {
+    if (a.px) {
+      // rows and columns of the output map this workgroup owns, extended to
+      // the image edge (2 * floor(H/2), 2 * floor(W/2)) in the last chunk /
+      // strip; strip and chunk origins are even, so pairs never straddle
+      constexpr int OUTW = StripGeom<KW>::OUTW;
+      const int Hd = a.H / 2;
+      const int r0 = chunk * a.TH;
+      const bool last_chunk = r0 + a.TH >= a.Hout;
+      const int c0 = strip * OUTW;
+      const bool last_strip = c0 + OUTW >= a.Wout;
+      const int col = c0 + static_cast<int>(threadIdx.x);
+      const int cend = last_strip ? 2 * (a.W / 2) : c0 + OUTW;
+      pol.pool_on = true;
+      pol.pool_f64 = a.pool_f64 != 0;
+      pol.prow0 = r0;
+      pol.prow1 = last_chunk ? 2 * Hd : r0 + a.TH;
+      pol.Wd = a.W / 2;
+      pol.pool_off = static_cast<int64_t>(plane) * Hd * (a.W / 2);
+      pol.pcol_ok = (col & 1) == 0 && col < cend;
+      pol.pcol = static_cast<uint32_t>(col >> 1);
+      pol.hx = 0.0;
+      pol.hy = 0.0;
+    }
+  }
 
   strip_engine<SsimPol<T, CT, MODE>, KW>(pol, a.win, 0, a.Hout, a.Wout, a.TH, strip,
                                          chunk, sbuf);
@@ -261,6 +365,9 @@ struct ScatterArgs {
   const float* win;
   int H, W, Hout, Wout, TH, strips, bpp;
   double shift;
+  const void* gpx;  // optional gradient of the next pyramid level (2x2 means)
+  const void* gpy;
+  int gp_f64;       // its element type: float64 (1) or float32 (0)
 };
 
 template <typename T, bool DY>
@@ -282,6 +389,11 @@ struct ScatterPol {
   double shift;
   T* __restrict__ dx;
   T* __restrict__ dy;
+  const void* gpx;
+  const void* gpy;
+  bool gp_f64;
+  int Hp, Wp;        // pyramid level grid: floor(H/2) x floor(W/2)
+  int64_t gp_off;    // this plane of the pyramid gradient
 
   // Zero padding outside the Hout x Wout support, branch free: the clamped
   // address is always loaded and the value masked.
@@ -309,14 +421,26 @@ struct ScatterPol {
   }
 
   __device__ inline void end_row() {}
+  __device__ inline void pool(int, const Raw&) {}
+
+  // A quarter of the pyramid gradient of the 2x2 block this pixel belongs
+  // to (the odd trailing row / column belongs to none).
+  __device__ inline double pyr_grad(const void* g, int orow, int ocol) const {
+    const int pr = orow >> 1, pc = ocol >> 1;
+    if (!g || pr >= Hp || pc >= Wp) return 0.0;
+    const int64_t o = gp_off + static_cast<int64_t>(pr) * Wp + pc;
+    return 0.25 * (gp_f64 ? static_cast<const double*>(g)[o]
+                          : static_cast<double>(static_cast<const float*>(g)[o]));
+  }
 
   __device__ inline void emit(int orow, int ocol, const double* v, bool valid) {
     if (!valid) return;
     const int64_t o = img_off + static_cast<int64_t>(orow) * W + ocol;
     const double xv = static_cast<double>(x[o]) - shift;
     const double yv = static_cast<double>(y[o]) - shift;
-    if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2]);
-    if constexpr (DY) dy[o] = static_cast<T>(2.0 * yv * v[0] + xv * v[1] + v[3]);
+    if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + pyr_grad(gpx, orow, ocol));
+    if constexpr (DY)
+      dy[o] = static_cast<T>(2.0 * yv * v[0] + xv * v[1] + v[3] + pyr_grad(gpy, orow, ocol));
   }
 };
 
@@ -346,6 +470,12 @@ __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
   pol.shift = a.shift;
   pol.dx = static_cast<T*>(a.dx);
   pol.dy = static_cast<T*>(a.dy);
+  pol.gpx = a.gpx;
+  pol.gpy = a.gpy;
+  pol.gp_f64 = a.gp_f64 != 0;
+  pol.Hp = a.H / 2;
+  pol.Wp = a.W / 2;
+  pol.gp_off = static_cast<int64_t>(plane) * pol.Hp * pol.Wp;
   strip_engine<ScatterPol<T, DY>, KW>(pol, a.win, -(KW - 1), a.H, a.W, a.TH, strip, chunk,
                                       sbuf);
 }
@@ -442,6 +572,7 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
                               const float* gcs, const float* win, int K, int N,
                               int C, int H, int W, double shift, double C1,
                               double C2, float* aux, T* dx, T* dy,
+                              const void* gpx, const void* gpy, int gp_dtype,
                               hipStream_t st) {
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
@@ -457,10 +588,10 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
   a.W = W;
   a.Hout = Hout;
   a.Wout = Wout;
-  a.TH = SSIM_TH;
-  int chunks = 0;
-  strip_grid(Hout, Wout, K, SSIM_TH, &a.strips, &chunks);
-  a.bpp = a.strips * chunks;
+  const Tiling tp = tiling_for(planes, Hout, Wout, K);
+  a.TH = tp.TH;
+  a.strips = tp.strips;
+  a.bpp = tp.tiles;
   a.shift = shift;
   a.C1 = C1;
   a.C2 = C2;
@@ -495,13 +626,64 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
   s.W = W;
   s.Hout = Hout;
   s.Wout = Wout;
-  s.TH = SSIM_TH;
-  strip_grid(H, W, K, SSIM_TH, &s.strips, &chunks);
-  s.bpp = s.strips * chunks;
+  const Tiling ts = tiling_for(planes, H, W, K);
+  s.TH = ts.TH;
+  s.strips = ts.strips;
+  s.bpp = ts.tiles;
   s.shift = shift;
+  s.gpx = gpx;
+  s.gpy = gpy;
+  s.gp_f64 = gp_dtype == FA_F64 ? 1 : 0;
   rc = grid_of(planes, s.bpp, &grid);
   if (rc != FA_OK) return rc;
   return dy ? launch_scatter_k<T, true>(K, grid, st, s) : launch_scatter_k<T, false>(K, grid, st, s);
+}
+
+// fa_gpu_ssim_cs, optionally writing the next pyramid level (px / py non-null).
+static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, int H, int W,
+                        const float* win, int K, double shift, double C1, double C2,
+                        double* partial, double* partial_cs, int bpp, double* out_s,
+                        double* out_cs, void* px, void* py, int pool_dtype, int device,
+                        void* stream) {
+  if (!x || !y || !win || !partial || !partial_cs || !out_s || !out_cs) return FA_E_ARG;
+  int Hout = 0, Wout = 0;
+  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  const Tiling tl = tiling_for(planes, Hout, Wout, K);
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  SsimArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.H = H;
+  a.W = W;
+  a.Hout = Hout;
+  a.Wout = Wout;
+  a.TH = tl.TH;
+  a.strips = tl.strips;
+  a.bpp = tl.tiles;
+  a.shift = shift;
+  a.C1 = C1;
+  a.C2 = C2;
+  a.win = win;
+  a.partial = partial;
+  a.partial_cs = partial_cs;
+  a.px = px;
+  a.py = py;
+  a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
+  dim3 grid;
+  rc = grid_of(planes, tl.tiles, &grid);
+  if (rc != FA_OK) return rc;
+  rc = launch_ssim<MODE_CS>(dtype, K, grid, st, a);
+  if (rc != FA_OK) return rc;
+  hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
+                     partial, partial_cs, tl.tiles, static_cast<double>(Hout) * Wout, out_s,
+                     out_cs);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
 }
 
 }  // namespace fa
@@ -516,9 +698,7 @@ FA_API int fa_gpu_ssim_workspace(int H, int W, int K, int* out_bpp) {
   int Hout = 0, Wout = 0;
   const int rc = ssim_shape(1, 1, H, W, K, &Hout, &Wout);
   if (rc != FA_OK) return rc;
-  int strips = 0, chunks = 0;
-  strip_grid(Hout, Wout, K, SSIM_TH, &strips, &chunks);
-  *out_bpp = strips * chunks;
+  *out_bpp = ssim_slots(Hout, Wout, K);
   return FA_OK;
 }
 
@@ -532,9 +712,8 @@ FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
   if (rc != FA_OK) return rc;
-  int strips = 0, chunks = 0;
-  strip_grid(Hout, Wout, K, SSIM_TH, &strips, &chunks);
-  if (bpp != strips * chunks) return FA_E_ARG;
+  if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
+  const Tiling tl = tiling_for(static_cast<int64_t>(N) * C, Hout, Wout, K);
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
@@ -545,9 +724,9 @@ FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
   a.W = W;
   a.Hout = Hout;
   a.Wout = Wout;
-  a.TH = SSIM_TH;
-  a.strips = strips;
-  a.bpp = bpp;
+  a.TH = tl.TH;
+  a.strips = tl.strips;
+  a.bpp = tl.tiles;
   a.shift = shift;
   a.C1 = C1;
   a.C2 = C2;
@@ -555,15 +734,15 @@ FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
   a.map = map_out;
   a.partial = partial;
   dim3 grid;
-  rc = grid_of(static_cast<int64_t>(N) * C, bpp, &grid);
+  rc = grid_of(static_cast<int64_t>(N) * C, tl.tiles, &grid);
   if (rc != FA_OK) return rc;
   rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, grid, st, a)
                : launch_ssim<MODE_REDUCE>(dtype, K, grid, st, a);
   if (rc != FA_OK) return rc;
 
-  // each image owns C consecutive plane rows of `partial`
+  // each image owns C * tiles consecutive slots of `partial`
   const double npix = static_cast<double>(Hout) * Wout;
-  return launch_finalize(partial, false, N, C * bpp, npix * C,
+  return launch_finalize(partial, false, N, C * tl.tiles, npix * C,
                          npix * C * static_cast<double>(N), FA_PSNR_NONE,
                          out_per_image, out_total, nullptr, nullptr, st);
 }
@@ -574,42 +753,26 @@ FA_API int fa_gpu_ssim_cs(const void* x, const void* y, int dtype, int N,
                           double shift, double C1, double C2, double* partial,
                           double* partial_cs, int bpp, double* out_s,
                           double* out_cs, int device, void* stream) {
-  if (!x || !y || !win || !partial || !partial_cs || !out_s || !out_cs) return FA_E_ARG;
-  int Hout = 0, Wout = 0;
-  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
-  if (rc != FA_OK) return rc;
-  int strips = 0, chunks = 0;
-  strip_grid(Hout, Wout, K, SSIM_TH, &strips, &chunks);
-  if (bpp != strips * chunks) return FA_E_ARG;
-  FA_DEVICE_SCOPE(device);
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  return ssim_cs_impl(x, y, dtype, N, C, H, W, win, K, shift, C1, C2, partial, partial_cs,
+                      bpp, out_s, out_cs, nullptr, nullptr, FA_F64, device, stream);
+}
 
-  SsimArgs a = {};
-  a.x = x;
-  a.y = y;
-  a.H = H;
-  a.W = W;
-  a.Hout = Hout;
-  a.Wout = Wout;
-  a.TH = SSIM_TH;
-  a.strips = strips;
-  a.bpp = bpp;
-  a.shift = shift;
-  a.C1 = C1;
-  a.C2 = C2;
-  a.win = win;
-  a.partial = partial;
-  a.partial_cs = partial_cs;
-  const int64_t planes = static_cast<int64_t>(N) * C;
-  dim3 grid;
-  rc = grid_of(planes, bpp, &grid);
-  if (rc != FA_OK) return rc;
-  rc = launch_ssim<MODE_CS>(dtype, K, grid, st, a);
-  if (rc != FA_OK) return rc;
-  hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
-                     partial, partial_cs, bpp, static_cast<double>(Hout) * Wout, out_s, out_cs);
-  FA_LAUNCH_CHECK();
-  return FA_OK;
+// No counterpart in the reference (it pools between scales with torch,
+// functional.py:876-885).  fa_gpu_ssim_cs plus the next pyramid level, fused.
+FA_API int fa_gpu_ssim_cs_pool(const void* x, const void* y, int dtype, int N,
+                               int C, int H, int W, const float* win, int K,
+                               double shift, double C1, double C2, double* partial,
+                               double* partial_cs, int bpp, double* out_s,
+                               double* out_cs, void* px, void* py, int pool_dtype,
+                               int device, void* stream) {
+  if (!px || !py) return FA_E_ARG;
+  // float32 levels hold the pyramid of uint8 input exactly; every other
+  // input pools into float64
+  const bool ok = pool_dtype == FA_F64 ||
+                  (pool_dtype == FA_F32 && (dtype == FA_U8 || dtype == FA_F32));
+  if (!ok) return FA_E_DTYPE;
+  return ssim_cs_impl(x, y, dtype, N, C, H, W, win, K, shift, C1, C2, partial, partial_cs,
+                      bpp, out_s, out_cs, px, py, pool_dtype, device, stream);
 }
 
 // reference: fa_cuda.cu:1299-1353 (fa_cuda_ssim_backward)
@@ -625,6 +788,7 @@ FA_API int fa_gpu_ssim_backward(const float* x, const float* y,
   FA_DEVICE_SCOPE(device);
   return ssim_backward_impl<float, MODE_PREP>(x, y, dL_dmap, grad_scalar, nullptr, nullptr,
                                               win, K, N, C, H, W, shift, C1, C2, aux, dx, dy,
+                                              nullptr, nullptr, FA_F32,
                                               static_cast<hipStream_t>(stream));
 }
 
@@ -640,32 +804,38 @@ FA_API int fa_gpu_ssim_cs_backward(const float* x, const float* y,
   FA_DEVICE_SCOPE(device);
   return ssim_backward_impl<float, MODE_PREP_CS>(x, y, nullptr, nullptr, gs, gcs, win, K, N, C,
                                                  H, W, shift, C1, C2, aux, dx, dy,
+                                                 nullptr, nullptr, FA_F32,
                                                  static_cast<hipStream_t>(stream));
 }
 
-// No counterpart in the reference (its MS-SSIM pyramid is float32).  The
-// fa_gpu_ssim_cs_backward contract for x / y / dx / dy of `dtype` FA_F32 or
-// FA_F64: the float64 pyramid levels of the MS-SSIM backward.  aux stays float32.
+// No counterpart in the reference (its MS-SSIM pyramid is float32 and pooled
+// by torch).  The fa_gpu_ssim_cs_backward contract for x / y / dx / dy of
+// `dtype` FA_F32 or FA_F64 (the exact pyramid levels), plus the gradient of
+// the next level that fa_gpu_ssim_cs_pool wrote: gpx / gpy (either may be
+// null) of `gp_dtype` FA_F32 or FA_F64, floor(H/2) x floor(W/2) per plane,
+// spread as 1/4 over each 2x2 block into dx / dy.  aux stays float32.
 FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
                                       const float* gs, const float* gcs,
                                       const float* win, int K, int N, int C,
                                       int H, int W, double shift, double C1,
-                                      double C2, float* aux, void* dx,
+                                      double C2, const void* gpx, const void* gpy,
+                                      int gp_dtype, float* aux, void* dx,
                                       void* dy, int device, void* stream) {
   if (!x || !y || !gs || !gcs || !win || !aux) return FA_E_ARG;
   if (!dx && !dy) return FA_E_ARG;
   if (dtype != FA_F32 && dtype != FA_F64) return FA_E_DTYPE;
+  if ((gpx || gpy) && gp_dtype != FA_F32 && gp_dtype != FA_F64) return FA_E_DTYPE;
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == FA_F32)
     return ssim_backward_impl<float, MODE_PREP_CS>(
         static_cast<const float*>(x), static_cast<const float*>(y), nullptr, nullptr, gs, gcs,
         win, K, N, C, H, W, shift, C1, C2, aux, static_cast<float*>(dx),
-        static_cast<float*>(dy), st);
+        static_cast<float*>(dy), gpx, gpy, gp_dtype, st);
   return ssim_backward_impl<double, MODE_PREP_CS>(
       static_cast<const double*>(x), static_cast<const double*>(y), nullptr, nullptr, gs, gcs,
       win, K, N, C, H, W, shift, C1, C2, aux, static_cast<double*>(dx),
-      static_cast<double*>(dy), st);
+      static_cast<double*>(dy), gpx, gpy, gp_dtype, st);
 }
 
 }  // extern "C"

@@ -22,7 +22,8 @@
 //
 // What the lane loads (Pol::set_column once, Pol::load(row) per row; loads are
 // branch free, out-of-grid rows and columns are clamped or zeroed by the
-// policy), which moments it forms and what happens to each output pixel
+// policy), what it does with each raw row besides (Pol::pool: the MS-SSIM
+// pyramid step rides along), which moments it forms and what happens to each output pixel
 // (Pol::emit with a validity flag, Pol::end_row after each lane's four) is a
 // policy (see fa_ssim.hip): the SSIM forward (4 moments, float32 or
 // float64), the backward coefficient pass, and the backward scatter (the
@@ -96,7 +97,11 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
 
   CT ring[RS][NP];
 #pragma unroll
-  for (int i = 0; i < KW - 1; ++i) pol.moments(pol.load(in_row0 + i), ring[i]);
+  for (int i = 0; i < KW - 1; ++i) {
+    const Raw r = pol.load(in_row0 + i);
+    pol.pool(in_row0 + i, r);
+    pol.moments(r, ring[i]);
+  }
 
   Raw pend[PH];
 #pragma unroll
@@ -111,7 +116,10 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
       const int q = qc + u;
       if (q < nph) {  // uniform across the workgroup
 #pragma unroll
-        for (int i = 0; i < PH; ++i) pol.moments(pend[i], ring[(KW - 1 + u * PH + i) % RS]);
+        for (int i = 0; i < PH; ++i) {
+          pol.pool(in_row0 + KW - 1 + q * PH + i, pend[i]);
+          pol.moments(pend[i], ring[(KW - 1 + u * PH + i) % RS]);
+        }
         // Prefetch the next phase unconditionally: loads are clamped by the
         // policy, and a guard here would cost register copies every phase.
 #pragma unroll

@@ -430,31 +430,42 @@ class _FusedSSIMCS(torch.autograd.Function):
         return (dx if need_dx else None, dy if need_dy else None, None, None, None, None)
 
 
-class _Pool2(torch.autograd.Function):
-    """The native MS-SSIM pyramid step (``fa_gpu_pool2``): 2x2 means of x and y
-    in float32 for uint8 input (exact) and float64 for floating input.
-    The backward spreads a quarter of each gradient over its 2x2 block."""
+class _FusedSSIMCSPool(torch.autograd.Function):
+    """One differentiable native MS-SSIM scale: the ``(ssim, cs)`` plane means
+    and the next pyramid level ``(px, py)`` from one pass over x and y
+    (``fa_gpu_ssim_cs_pool``).  The backward spreads a quarter of the level's
+    gradient over each 2x2 block inside the scatter of the (ssim, cs) gradient
+    (``fa_gpu_ssim_cs_backward_ex``), so a scale costs one forward and two
+    backward launches whatever reaches it."""
 
     @staticmethod
-    def forward(ctx, x, y):
+    def forward(ctx, x, y, win, shift, C1, C2, pool_dtype):
         from . import backend
 
-        ctx.shapes = (x.shape, y.shape)
-        ctx.dtypes = (x.dtype, y.dtype)
-        return backend.pool2_gpu(x, y)
+        s, cs, px, py = backend.ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype)
+        ctx.save_for_backward(x, y, win)
+        ctx.consts = (shift, C1, C2)
+        ctx.set_materialize_grads(False)
+        return s, cs, px, py
 
     @staticmethod
-    def backward(ctx, gx, gy):
-        def spread(g, shape, dtype, needed):
-            if g is None or not needed:
-                return None
-            h2, w2 = g.shape[-2] * 2, g.shape[-1] * 2
-            full = g.new_zeros(shape)
-            full[..., :h2, :w2] = (0.25 * g).repeat_interleave(2, -2).repeat_interleave(2, -1)
-            return full.to(dtype)
+    def backward(ctx, g_s, g_cs, g_px, g_py):
+        from . import backend
 
-        return (spread(gx, ctx.shapes[0], ctx.dtypes[0], ctx.needs_input_grad[0]),
-                spread(gy, ctx.shapes[1], ctx.dtypes[1], ctx.needs_input_grad[1]))
+        _reject_double_backward()
+        x, y, win = ctx.saved_tensors
+        shift, C1, C2 = ctx.consts
+        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_dx or need_dy):
+            return (None,) * 7
+        planes = x.shape[0] * x.shape[1]
+        if g_s is None:
+            g_s = torch.zeros(planes, device=x.device)
+        if g_cs is None:
+            g_cs = torch.zeros(planes, device=x.device)
+        dx, dy = backend.ssim_cs_backward(x, y, g_s, g_cs, win, shift, C1, C2,
+                                          need_dx, need_dy, g_px, g_py)
+        return (dx if need_dx else None, dy if need_dy else None) + (None,) * 5
 
 
 def _ssim_cs_pair(x4, y4, win, wdt, shift, C1, C2, backend_hint):
@@ -510,21 +521,46 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
     from . import backend
 
     win = gaussian_window_1d(win_size, sigma, device=x4.device, dtype=wdt)
-    # On the GPU the pyramid is built by the native pooling kernel and held
-    # exactly (the coarse scales amplify a rounded level ~100x in the gradient);
-    # the portable path pools at the working dtype, as the reference does.
-    native_pyramid = backend_hint != "torch" and backend.pool2_available(x4, y4)
-    cx, cy = x4, y4
+    n, c = x4.shape[0], x4.shape[1]
     terms = []
-    for i in range(scales):
-        if i:
-            if native_pyramid:
-                cx, cy = _Pool2.apply(cx, cy)
+    grad = torch.is_grad_enabled() and (x4.requires_grad or y4.requires_grad)
+    native = (backend_hint != "torch"
+              and backend.ssim_cs_pool_available(x4, y4, win_size)
+              and not (grad and torch.cuda.is_current_stream_capturing()))
+    if native:
+        # On the GPU every scale is one fused pass that also writes the next
+        # pyramid level, held exactly (the coarse scales amplify a rounded
+        # level ~100x in the gradient): float32 below uint8, float64 below
+        # floating input.  float16 / bfloat16 widen exactly to float32 when a
+        # gradient is wanted, and a float64 working dtype widens the input.
+        if wdt == torch.float64 and x4.dtype != torch.float64:
+            x4, y4 = x4.double(), y4.double()
+        elif grad and x4.dtype in (torch.float16, torch.bfloat16):
+            x4, y4 = x4.float(), y4.float()
+        pdt = backend.pyramid_dtype(x4.dtype)
+        cx, cy = x4, y4
+        for i in range(scales):
+            last = i == scales - 1
+            if grad:
+                if last:
+                    s, cs = _FusedSSIMCS.apply(cx, cy, win, shift, C1, C2)
+                else:
+                    s, cs, cx, cy = _FusedSSIMCSPool.apply(cx, cy, win, shift, C1, C2, pdt)
             else:
+                out = backend.ssim_cs_pool(cx, cy, win, shift, C1, C2, None if last else pdt)
+                s, cs = out[0], out[1]
+                if not last:
+                    cx, cy = out[2], out[3]
+            terms.append((s if last else cs).view(n, c))
+    else:
+        # the portable path pools at the working dtype, as the reference does
+        cx, cy = x4, y4
+        for i in range(scales):
+            if i:
                 cx = F.avg_pool2d(cx.to(wdt), 2)
                 cy = F.avg_pool2d(cy.to(wdt), 2)
-        s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
-        terms.append(s if i == scales - 1 else cs)
+            s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
+            terms.append(s if i == scales - 1 else cs)
     # a fractional power of a negative factor is not real: clamp at zero
     per_plane = torch.stack(terms).clamp_min(0.0).pow(_ms_weights(w, x4.device)).prod(dim=0)
     per_image = per_plane.mean(dim=1)

@@ -166,28 +166,38 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
 
 /*
  * No counterpart in the reference, which pools its MS-SSIM pyramid with torch
- * between scales (reference functional.py:876-885).  One pyramid step for x and
- * y at once: non-overlapping 2x2 mean, odd trailing row / column dropped, over
- * `planes` planes of H x W.  out_dtype must be FA_F32 for uint8 input (exact)
- * and FA_F64 for every floating input (exact for float16; for float32 and
- * bfloat16 unless a 2x2 block spans more than 2^29 / 2^45 in magnitude).
- * ox / oy: planes * (H/2) * (W/2) elements of out_dtype.
+ * between scales (reference functional.py:876-885).  fa_gpu_ssim_cs plus the
+ * next pyramid level of x and y, written by the same pass: non-overlapping 2x2
+ * mean, odd trailing row / column dropped.  px / py: N*C*(H/2)*(W/2) elements
+ * of pool_dtype, which is FA_F64, or FA_F32 for uint8 and float32 input.  The
+ * means are formed in float64, so the levels of a uint8 pyramid are exact in
+ * float32 and those of float16 / bfloat16 / float32 exact in float64 (unless a
+ * 2x2 block spans more than 2^29 / 2^45 in magnitude; then correctly rounded).
  */
-FA_API int fa_gpu_pool2(const void* x, const void* y, int dtype, int planes,
-                        int H, int W, void* ox, void* oy, int out_dtype,
-                        int device, void* stream);
+FA_API int fa_gpu_ssim_cs_pool(const void* x, const void* y, int dtype, int N,
+                               int C, int H, int W, const float* win, int K,
+                               double shift, double C1, double C2,
+                               double* partial, double* partial_cs, int bpp,
+                               double* out_s, double* out_cs, void* px,
+                               void* py, int pool_dtype, int device,
+                               void* stream);
 
 /*
  * No counterpart in the reference.  fa_gpu_ssim_cs_backward for x / y / dx / dy
- * of element type `dtype` (FA_F32 or FA_F64): the float64 levels of the exact
- * MS-SSIM pyramid.  aux stays float32 with the same size.
+ * of element type `dtype` (FA_F32 or FA_F64, the exact pyramid levels), plus
+ * the gradient of the level fa_gpu_ssim_cs_pool derived from them: gpx / gpy
+ * (either may be null), (H/2) x (W/2) per plane of gp_dtype (FA_F32 or
+ * FA_F64), each value spread as 1/4 over its 2x2 block of dx / dy.  aux stays
+ * float32 with the same size as in fa_gpu_ssim_cs_backward.
  */
 FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
                                       const float* gs, const float* gcs,
                                       const float* win, int K, int N, int C,
                                       int H, int W, double shift, double C1,
-                                      double C2, float* aux, void* dx,
-                                      void* dy, int device, void* stream);
+                                      double C2, const void* gpx,
+                                      const void* gpy, int gp_dtype,
+                                      float* aux, void* dx, void* dy,
+                                      int device, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -57,8 +57,8 @@ def test_abi_version_and_status_strings(lib):
 def test_workspace_queries(lib):
     out = ctypes.c_int(0)
     assert lib.fa_gpu_ssim_workspace(1080, 1920, 11, ctypes.byref(out)) == 0
-    # 246 output columns per 256-lane strip, 64 output rows per workgroup
-    assert out.value == 8 * 17
+    # 246 output columns per 256-lane strip; slots for the smallest row tile (4)
+    assert out.value == 8 * 268
     assert lib.fa_gpu_ssim_workspace(8, 8, 11, ctypes.byref(out)) == 2  # FA_E_SHAPE
     assert lib.fa_gpu_ssim_workspace(64, 64, 4, ctypes.byref(out)) == 3  # even window
     assert lib.fa_gpu_ssim_workspace(64, 64, 13, ctypes.byref(out)) == 3
@@ -85,10 +85,17 @@ def test_argument_validation_before_any_gpu_work(lib):
     assert lib.fa_gpu_ssim_backward(p, p, None, None, p, 11, 1, 1, 64, 64, 0.5, 1e-4, 9e-4,
                                     p, p, None, 0, None) == 5  # no upstream gradient
     assert lib.fa_gpu_gmsd(p, p, 0, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, 99, p, p, 0, None) == 5
-    # the pyramid step insists on its exact output type
-    assert lib.fa_gpu_pool2(p, p, 0, 1, 4, 4, p, p, 4, 0, None) == 1  # uint8 -> float64
-    assert lib.fa_gpu_pool2(p, p, 3, 1, 4, 4, p, p, 3, 0, None) == 1  # float32 -> float32
-    assert lib.fa_gpu_pool2(p, p, 1, 1, 4, 4, p, p, 3, 0, None) == 1  # float16 -> float32
-    assert lib.fa_gpu_pool2(p, p, 0, 1, 1, 4, p, p, 3, 0, None) == 2  # one row
+    # the fused pyramid step insists on an exact level type
+    cs = (1, 1, 1, 64, 64, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)  # float16, bpp 99
+    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, p, p, 3, 0, None) == 1  # float16 -> float32
+    assert lib.fa_gpu_ssim_cs_pool(p, p, 2, *cs[1:], p, p, 3, 0, None) == 1  # bfloat16
+    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, p, p, 0, 0, None) == 1  # uint8 levels
+    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, None, p, 4, 0, None) == 5  # no level buffer
+    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, p, p, 4, 0, None) == 5  # bpp mismatch
+    assert lib.fa_gpu_ssim_cs_pool(p, p, 0, *cs[1:], p, p, 3, 0, None) == 5  # u8 -> f32 ok
     assert lib.fa_gpu_ssim_cs_backward_ex(p, p, 0, p, p, p, 11, 1, 1, 64, 64, 0.5, 1e-4,
-                                          9e-4, p, p, None, 0, None) == 1  # uint8 input
+                                          9e-4, None, None, 0, p, p, None, 0,
+                                          None) == 1  # uint8 input
+    assert lib.fa_gpu_ssim_cs_backward_ex(p, p, 3, p, p, p, 11, 1, 1, 64, 64, 0.5, 1e-4,
+                                          9e-4, p, None, 1, p, p, None, 0,
+                                          None) == 1  # float16 pyramid gradient

@@ -1,7 +1,8 @@
 """GPU parity of MS-SSIM (value and gradient) and GMSD / GMS.
 
 Bar: values within 1e-6 relative of float64; gradients 1e-6 max-normwise
-relative (the MS-SSIM pyramid is exact, see fa_pool.hip).  Where the true value
+relative (the MS-SSIM pyramid levels are exact: float32 below uint8 input,
+float64 below floating input).  Where the true value
 is zero (GMSD of identical frames) the bar is the reference's absolute one.
 """
 
@@ -178,26 +179,86 @@ def test_gms_loss_gradient_finite(gpu):
 # --------------------------------------------------------------------------- #
 
 
+def _rand_pair(dt, shape, seed, gpu):
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    if dt == torch.uint8:
+        x = torch.randint(0, 256, shape, dtype=dt, device=gpu, generator=g)
+        y = torch.randint(0, 256, shape, dtype=dt, device=gpu, generator=g)
+    else:
+        x = (255 * torch.rand(shape, device=gpu, generator=g, dtype=torch.float64)).to(dt)
+        y = (255 * torch.rand(shape, device=gpu, generator=g, dtype=torch.float64)).to(dt)
+    return x, y
+
+
+# (H, W, K): one strip / chunk, odd trailing row and column, several strips
+# (246 output columns each at K=11) and 64-row chunks, other windows
+_LEVEL_CASES = [(11, 11, 11), (12, 13, 11), (75, 300, 11), (141, 501, 11), (257, 511, 7),
+                (66, 258, 3), (1080, 1920, 11)]
+
+
 @pytest.mark.parametrize("dt", [torch.uint8, torch.float16, torch.bfloat16, torch.float32,
                                 torch.float64])
-@pytest.mark.parametrize("hw", [(2, 2), (9, 12), (10, 7), (33, 1), (1080, 1920)])
-def test_pool2_exact(gpu, dt, hw):
-    """fa_gpu_pool2 equals float64 avg_pool2d bit for bit, in the exact type."""
+@pytest.mark.parametrize("case", _LEVEL_CASES)
+def test_fused_pyramid_level_exact(gpu, dt, case):
+    """The level written by the CS pass equals float64 avg_pool2d bit for bit
+    (float64 input: to rounding), and the (ssim, cs) means equal those of the
+    plain CS pass bit for bit."""
     from frame_analytics_amd import backend
+    from frame_analytics_amd.functional import gaussian_window_1d
 
-    h, w = hw
-    if w < 2:
-        pytest.skip("needs two columns")
-    g = torch.Generator(device=gpu)
-    g.manual_seed(h * 31 + w)
-    if dt == torch.uint8:
-        x = torch.randint(0, 256, (2, 3, h, w), dtype=dt, device=gpu, generator=g)
-        y = torch.randint(0, 256, (2, 3, h, w), dtype=dt, device=gpu, generator=g)
-    else:
-        x = torch.rand((2, 3, h, w), device=gpu, generator=g).to(dt)
-        y = torch.rand((2, 3, h, w), device=gpu, generator=g).to(dt)
-    ox, oy = backend.pool2_gpu(x, y)
-    assert ox.dtype == backend.pyramid_dtype(dt)
+    h, w, k = case
+    x, y = _rand_pair(dt, (2, 3, h, w), h * 31 + w + k, gpu)
+    win = gaussian_window_1d(k, 1.5, device=gpu, dtype=torch.float32)
+    pdt = backend.pyramid_dtype(dt)
+    s, cs, px, py = backend.ssim_cs_pool(x, y, win, 127.5, 6.5025, 58.5225, pdt)
+    s0, cs0 = backend.ssim_cs_pool(x, y, win, 127.5, 6.5025, 58.5225, None)
+    torch.cuda.synchronize()
+    assert px.dtype == pdt and px.shape == (2, 3, h // 2, w // 2)
     wx = torch.nn.functional.avg_pool2d(x.double(), 2)
     wy = torch.nn.functional.avg_pool2d(y.double(), 2)
-    assert torch.equal(ox.double(), wx) and torch.equal(oy.double(), wy)
+    if dt == torch.float64:
+        # four doubles summed in another order: within two units in the last place
+        for got, want in ((px, wx), (py, wy)):
+            assert ((got - want).abs() <= 2.0 ** -51 * want.abs()).all()
+    else:
+        assert torch.equal(px.double(), wx) and torch.equal(py.double(), wy)
+    assert torch.equal(s, s0) and torch.equal(cs, cs0)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+def test_fused_pyramid_level_gradient(gpu, dt):
+    """d/dx of a loss on (s, cs, px, py) equals the CS gradient plus a quarter
+    of the level gradient spread over each 2x2 block (odd edge excluded)."""
+    from frame_analytics_amd import backend
+    from frame_analytics_amd.functional import _FusedSSIMCSPool, gaussian_window_1d
+
+    n, c, h, w = 1, 2, 75, 263
+    x0, y0 = _rand_pair(dt, (n, c, h, w), 5, gpu)
+    win = gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    pdt = torch.float64
+    x = x0.clone().requires_grad_(True)
+    y = y0.clone().requires_grad_(True)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(9)
+    rs = torch.rand(n * c, device=gpu, generator=g, dtype=torch.float64)
+    rcs = torch.rand(n * c, device=gpu, generator=g, dtype=torch.float64)
+    r1 = torch.rand((n, c, h // 2, w // 2), device=gpu, generator=g, dtype=pdt)
+    r2 = torch.rand((n, c, h // 2, w // 2), device=gpu, generator=g, dtype=pdt)
+    s, cs, px, py = _FusedSSIMCSPool.apply(x, y, win, 127.5, 6.5025, 58.5225, pdt)
+    ((s * rs).sum() + (cs * rcs).sum() + (px * r1).sum() + (py * r2).sum()).backward()
+
+    dx, dy = backend.ssim_cs_backward(x0, y0, rs, rcs, win, 127.5, 6.5025, 58.5225,
+                                      True, True)
+
+    def spread(r):
+        full = torch.zeros((n, c, h, w), dtype=torch.float64, device=gpu)
+        full[..., : 2 * (h // 2), : 2 * (w // 2)] = (
+            0.25 * r).repeat_interleave(2, -2).repeat_interleave(2, -1)
+        return full
+
+    tol = 1e-6 if dt == torch.float32 else 1e-12
+    for got, base, r in ((x.grad, dx, r1), (y.grad, dy, r2)):
+        want = base.double() + spread(r)
+        err = (got.double() - want).abs().max() / want.abs().max()
+        assert err <= tol, (dt, float(err))
