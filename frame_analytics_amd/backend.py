@@ -496,21 +496,49 @@ def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
 # --------------------------------------------------------------------------- #
 
 
-def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsample: bool):
-    """``(gms_mean, gmsd)`` per image, float64; ``None`` if unavailable."""
+def _view_strides(t: torch.Tensor):
+    """``(tensor, strides)``: a unit-column-stride view passes its (image,
+    channel, row) strides as an int64[3] host array; anything else is copied
+    contiguous and passes null."""
+    if t.is_contiguous():
+        return t, None
+    if t.stride(-1) != 1 or min(t.stride()) < 0:
+        return t.contiguous(), None
+    return t, (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+
+
+def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsample: bool,
+             luma: Optional[tuple] = None):
+    """``(gms_mean, gmsd)`` per image, float64; ``None`` if unavailable.
+
+    ``luma`` = (kr, kg, kb) makes the kernel read the three channels and form
+    the luma plane itself; cropped views are read in place through their
+    strides (``fa_gpu_gmsd_ex``).
+    """
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y):
         return None
     n, c = int(x.shape[0]), int(x.shape[1])
     h, w = int(x.shape[-2]), int(x.shape[-1])
-    x, y = _contig(x), _contig(y)
+    if luma is not None and c != 3:
+        return None
+    x, xs = _view_strides(x)
+    y, ys = _view_strides(y)
+    planes = n * (1 if luma is not None else c)
     bpp = _gmsd_workspace(ext, h, w, downsample)
-    psum = _f64(x.device, n * c, bpp)
-    psumsq = _f64(x.device, n * c, bpp)
+    psum = _f64(x.device, planes, bpp)
+    psumsq = _f64(x.device, planes, bpp)
     mean = _f64(x.device, n)
     dev = _f64(x.device, n)
-    _check(ext.gpu.fa_gpu_gmsd(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
-        int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
-        _dev(x), _stream(x)), ext)
+    if luma is None and xs is None and ys is None:
+        _check(ext.gpu.fa_gpu_gmsd(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
+            int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
+            _dev(x), _stream(x)), ext)
+    else:
+        lw = (ctypes.c_double * 3)(*luma) if luma is not None else None
+        _check(ext.gpu.fa_gpu_gmsd_ex(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, lw,
+            float(T), float(eps), int(downsample), _ptr(psum), _ptr(psumsq), bpp,
+            _ptr(mean), _ptr(dev), _dev(x), _stream(x)), ext)
     return mean, dev

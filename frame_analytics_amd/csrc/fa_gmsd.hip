@@ -4,123 +4,429 @@
 // and the per-image mean and population standard deviation of q
 // (reference: fa_cuda.cu:926-1026, 1416-1466; reference.py:288-335).
 //
-// Layout on CDNA4: every wave owns a strip of 64 downsampled columns (62
-// outputs, the last two lanes are the Prewitt halo) and walks down it with a
-// three-row window in registers.  The column sums and row differences of the
-// Prewitt pair need the two lanes to the right, which come from in-wave
-// shuffles -- no LDS staging and no barriers.  For uint8 input the downsampled
-// samples, their 3-sums and differences are all exact in float32, so they stay
-// float32; every other input type carries them in float64.  From the Prewitt
-// differences on, g and q are formed in float64 (full rate on CDNA4,
-// and the kernel is bound on HBM), so q carries no float32 rounding into the
-// standard deviation.  Sum q and sum q^2 are accumulated in float64 and reduced
-// in a fixed order.
+// Layout on CDNA4.  A wave walks a strip of 64 * NC sample columns (NC per
+// lane) top to bottom with a three-row window in registers and the next rows'
+// loads in flight; the Prewitt neighbours to the right come from in-wave
+// shuffles.  No LDS and no barriers, so every wave is independent.  The four
+// waves of a workgroup take four adjacent strips over the same rows (one
+// contiguous stretch of each input row), and the launch is exactly one round
+// of resident workgroups: each takes an equal share of its image's (channel,
+// strip group, row) space, a run of rows that may continue into the next
+// group or channel with a fresh two-row window.  Every workgroup does the
+// same work (to a row), so there is no tail, and the re-read halo is two rows
+// per run.  Loads beyond a run are clamped to its last row rather than
+// branched around, which keeps the double-buffered loads in flight.
+//
+// Arithmetic.  Samples are kept unnormalised: the sum of a 2x2 block (or the
+// sample itself), so for uint8 input they are integers and the Prewitt sums,
+// differences and M = (3 s gx)^2 + (3 s gy)^2 are exact int32 (s = 4 with
+// downsampling, else 1).  With G = M + 9 s^2 eps and T' = 9 s^2 T the kernel
+// accumulates not q but
+//     d = 1 - q = (g1 - g2)^2 / (G1 + G2 + T')
+//              = (M1 - M2)^2 / ((G1 + G2 + 2 sqrt(G1 G2)) (G1 + G2 + T'))
+// whose numerator is an exact integer for uint8.  Every rounding after it is
+// then *relative* to d, so it scales the variance instead of being amplified
+// by the difference E[q^2] - E[q]^2 of two numbers near 1 (an absolute error
+// of e in q moves the deviation by ~e / var(q), i.e. ~1e4 e).  Where the
+// sample magnitudes are bounded (uint8, float16) d is formed in float32 with
+// v_sqrt_f32 / v_rcp_f32 (a few ulp, relative); other inputs form it in
+// float64.  Sum d and sum d^2 are float64, reduced in a fixed order; the
+// finalize returns mean q = 1 - mean d and std q = std d.
+//
+// Luma (an extension): with per-channel weights the kernel reads the three
+// channels of each pixel and forms kr R + kg G + kb B itself, in float64,
+// instead of a float32 luma plane materialised beforehand.  A luma offset
+// cancels out of every gradient, so it is not an argument.
 #include "fa_common.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace fa {
 
-constexpr int G_OUTW = WAVE - 2;                     // output columns per wave
-constexpr int G_STRIP = WAVES_PER_BLOCK * G_OUTW;    // output columns per workgroup
-constexpr int G_TH = 64;                             // output rows per workgroup
+constexpr int G_PD = 4;        // rows of loads in flight ahead of the window
+constexpr int G_MIN_ROWS = 8;  // fewest rows a wave is given, where rows are scarce
+constexpr int G_SLOT_ROWS = 4; // workspace: one partial slot per 4 rows of a strip
+constexpr int G_OUTW_WIDE = 2 * WAVE - 2;  // output columns per wave, 2 columns per lane
+constexpr int G_OUTW_NARROW = WAVE - 2;    // ... 1 column per lane
 
-// Sample type: float32 is exact for uint8 (multiples of 1/4 below 1024),
-// float64 for everything else.
-template <typename T>
-using GSample = typename std::conditional<std::is_same<T, uint8_t>::value, float, double>::type;
+struct GView {
+  int64_t sn, sc, sh;  // element strides of image, channel, row (columns are unit stride)
+};
 
-template <typename T, bool DOWN>
-__device__ inline GSample<T> gmsd_sample(const T* __restrict__ p, int64_t plane_off, int W,
-                                         int r, int c) {
-  using S = GSample<T>;
-  if constexpr (DOWN) {
-    const int64_t o = plane_off + static_cast<int64_t>(2 * r) * W + 2 * c;
-    return S(0.25) * (load_as<S>(p, o) + load_as<S>(p, o + 1) + load_as<S>(p, o + W) +
-                      load_as<S>(p, o + W + 1));
+struct GmsdArgs {
+  const void* x;
+  const void* y;
+  GView vx, vy;
+  int Cout;                  // output planes per image (1 with luma)
+  int Hd, Wd, Hout, Wout;    // sample grid and 'valid' output grid
+  int strips;                // strips per plane
+  int groups;                // strip groups per plane: the 4 waves of a workgroup
+  int wpi;                   // workgroups per image
+  int tasks;                 // N * wpi
+  int64_t rows_img;          // Cout * groups * Hout: an image's row space
+  double kr, kg, kb;         // luma weights
+  double T2, eps2;           // T and eps scaled by 9 s^2
+  float T2f, eps2f;
+  int ext_x, ext_y;          // bytes from a plane's base to its last byte + 1 (dword path)
+  double* psum;
+  double* psumsq;
+};
+
+// d = 1 - q from the squared gradient magnitudes M1, M2 (without eps) and
+// their difference dm = M1 - M2 (exact for integer samples; zero for masked
+// columns, which then contribute d = 0).  float32 where FAST, else float64.
+template <bool FAST, typename S>
+__device__ inline typename std::conditional<FAST, float, double>::type one_minus_q(
+    S m1, S m2, S dm, float e_f, float t_f, double e_d, double t_d) {
+  if constexpr (FAST) {
+    const float G1 = static_cast<float>(m1) + e_f;
+    const float G2 = static_cast<float>(m2) + e_f;
+    const float Gs = G1 + G2;
+    const float A = fmaf(2.0f, __builtin_amdgcn_sqrtf(G1 * G2), Gs);  // (g1 + g2)^2
+    const float n = static_cast<float>(dm);
+    // the floor keeps 0 / 0 (flat, eps = 0) at 0; a non-zero dm implies A > 0
+    return (n * n) * __builtin_amdgcn_rcpf(fmaxf(A * (Gs + t_f), 1e-30f));
   } else {
-    return load_as<S>(p, plane_off + static_cast<int64_t>(r) * W + c);
+    const double G1 = static_cast<double>(m1) + e_d;
+    const double G2 = static_cast<double>(m2) + e_d;
+    const double Gs = G1 + G2;
+    const double A = fma(2.0, sqrt(G1 * G2), Gs);
+    const double n = static_cast<double>(dm);
+    return dm != S(0) ? (n * n) / (A * (Gs + t_d)) : 0.0;
   }
 }
 
-// Gradient magnitude at this lane's column from the three rows v0 (top),
-// v1, v2 (bottom); lanes 62 and 63 produce garbage that is never used.
-template <typename S>
-__device__ inline double prewitt_mag(S v0, S v1, S v2, double eps) {
-  const S cs = v0 + v1 + v2;  // column sum     (for gx)
-  const S rd = v0 - v2;       // row difference (for gy)
-  const S cs2 = __shfl_down(cs, 2, WAVE);
-  const S rd1 = __shfl_down(rd, 1, WAVE);
-  const S rd2 = __shfl_down(rd, 2, WAVE);
-  const double gx = static_cast<double>(cs - cs2) / 3.0;
-  const double gy = (static_cast<double>(rd) + static_cast<double>(rd1) +
-                     static_cast<double>(rd2)) / 3.0;
-  return sqrt(fma(gx, gx, fma(gy, gy, eps)));
-}
+// Buffer-resource word 3 for raw (untyped, unswizzled) dword access on CDNA.
+constexpr int G_RSRC_WORD3 = 0x00020000;
 
-template <typename T, bool DOWN>
-__global__ __launch_bounds__(BLOCK) void gmsd_kernel(
-    const T* __restrict__ x, const T* __restrict__ y, int H, int W, int Hd, int Wd,
-    int Hout, int Wout, double Tc, double eps, int strips, int bpp,
-    double* __restrict__ psum, double* __restrict__ psumsq) {
-  __shared__ double sred[2 * WAVES_PER_BLOCK];
-  const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
-  const int plane = t / bpp;
-  const int tile = t - plane * bpp;
-  const int chunk = tile / strips;
-  const int strip = tile - chunk * strips;
-  const int wave = threadIdx.x / WAVE;
-  const int lane = threadIdx.x % WAVE;
-  const int col = strip * G_STRIP + wave * G_OUTW + lane;  // downsampled column
-  const bool col_in = col < Wd;
-  const bool col_out = lane < G_OUTW && col < Wout;
-  const int r0 = chunk * G_TH;
-  const int rows = min(G_TH, Hout - r0);
-  const int64_t plane_off = static_cast<int64_t>(plane) * H * W;
+// --------------------------------------------------------------------------
+// sample sources: what one lane loads for one sample row, and the samples
+// --------------------------------------------------------------------------
 
-  using S = GSample<T>;
-  auto fetch = [&](int r, S& xv, S& yv) {
-    if (col_in && r < Hd) {
-      xv = gmsd_sample<T, DOWN>(x, plane_off, W, r, col);
-      yv = gmsd_sample<T, DOWN>(y, plane_off, W, r, col);
-    } else {
-      xv = S(0);
-      yv = S(0);
-    }
+// uint8, 2x2 downsampling, 4-byte aligned rows: each lane owns two sample
+// columns (four input bytes per input row) and loads them as one dword.
+// Channel sums are integers formed by v_dot4_u32_u8.
+template <bool LUMA>
+struct SrcU8Wide {
+  static constexpr int NC = 2;
+  static constexpr int OUTW = G_OUTW_WIDE;
+  static constexpr int CH = LUMA ? 3 : 1;
+  static constexpr bool FAST = true;
+  using S = typename std::conditional<LUMA, double, int>::type;
+  struct Raw {
+    uint32_t w[2][CH][2];  // tensor, channel, input row of the pair
   };
 
-  S x0, x1, x2, y0, y1, y2, nx, ny;
-  fetch(r0, x0, y0);
-  fetch(r0 + 1, x1, y1);
-  fetch(r0 + 2, nx, ny);
-  double acc = 0.0, acc2 = 0.0;
-  for (int o = 0; o < rows; ++o) {
-    x2 = nx;
-    y2 = ny;
-    if (o + 1 < rows) fetch(r0 + o + 3, nx, ny);
-    const double g1 = prewitt_mag(x0, x1, x2, eps);
-    const double g2 = prewitt_mag(y0, y1, y2, eps);
-    const double q = (2.0 * g1 * g2 + Tc) / (g1 * g1 + g2 * g2 + Tc);
-    if (col_out) {
-      acc += q;
-      acc2 += q * q;
+  // Buffer resources on the channel planes of x / y for this image (range:
+  // the plane's extent): a row is a scalar offset and the lane a 32-bit
+  // vector offset, so a load costs no VALU address arithmetic.  Rows and
+  // column pairs are clamped, so every access is inside the plane.
+  __amdgpu_buffer_rsrc_t rx[CH], ry[CH];
+  uint32_t shx, shy;
+  int rlim;       // last sample row a load may touch (clamp)
+  uint32_t boff;  // this lane's byte offset in a row
+  double kr, kg, kb;
+
+  __device__ inline void setup(const GmsdArgs& a, int n, int c, int strip, int lane) {
+    const uint8_t* bx = static_cast<const uint8_t*>(a.x) + n * a.vx.sn;
+    const uint8_t* by = static_cast<const uint8_t*>(a.y) + n * a.vy.sn;
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+      rx[ch] = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(bx + (LUMA ? ch : c) * a.vx.sc), 0, a.ext_x, G_RSRC_WORD3);
+      ry[ch] = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(by + (LUMA ? ch : c) * a.vy.sc), 0, a.ext_y, G_RSRC_WORD3);
     }
-    x0 = x1;
-    x1 = x2;
-    y0 = y1;
-    y1 = y2;
+    shx = static_cast<uint32_t>(a.vx.sh);
+    shy = static_cast<uint32_t>(a.vy.sh);
+    rlim = a.Hd - 1;
+    int pair = strip * (OUTW / 2) + lane;  // covers sample columns 2 pair, 2 pair + 1
+    const int last = a.Wd / 2 - 1;         // Wd is even on this path
+    boff = 4u * static_cast<uint32_t>(pair < last ? pair : last);
+    kr = a.kr;
+    kg = a.kg;
+    kb = a.kb;
   }
-  double s = 0.0, s2 = 0.0;
-  block_sum2(acc, acc2, sred, &s, &s2);
-  if (threadIdx.x == 0) {
-    const int64_t o = static_cast<int64_t>(plane) * bpp + tile;
-    psum[o] = s;
-    psumsq[o] = s2;
+
+  __device__ inline Raw load(int r) const {
+    const uint32_t ir = 2u * static_cast<uint32_t>(r < rlim ? r : rlim);
+    const int ox = static_cast<int>(ir * shx), oy = static_cast<int>(ir * shy);
+    Raw v;
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+      v.w[0][ch][0] = __builtin_amdgcn_raw_buffer_load_b32(rx[ch], boff, ox, 0);
+      v.w[0][ch][1] = __builtin_amdgcn_raw_buffer_load_b32(rx[ch], boff, ox + static_cast<int>(shx), 0);
+      v.w[1][ch][0] = __builtin_amdgcn_raw_buffer_load_b32(ry[ch], boff, oy, 0);
+      v.w[1][ch][1] = __builtin_amdgcn_raw_buffer_load_b32(ry[ch], boff, oy + static_cast<int>(shy), 0);
+    }
+    return v;
+  }
+
+  __device__ inline void samples(const Raw& v, S (&sx)[NC], S (&sy)[NC]) const {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      int s[CH][NC];
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        s[ch][0] = static_cast<int>(__builtin_amdgcn_udot4(
+            v.w[t][ch][1], 0x00000101u, __builtin_amdgcn_udot4(v.w[t][ch][0], 0x00000101u, 0u, false), false));
+        s[ch][1] = static_cast<int>(__builtin_amdgcn_udot4(
+            v.w[t][ch][1], 0x01010000u, __builtin_amdgcn_udot4(v.w[t][ch][0], 0x01010000u, 0u, false), false));
+      }
+      S* o = t ? sy : sx;
+#pragma unroll
+      for (int k = 0; k < NC; ++k) {
+        if constexpr (LUMA)
+          o[k] = fma(kb, static_cast<double>(s[2][k]),
+                     fma(kg, static_cast<double>(s[1][k]), kr * static_cast<double>(s[0][k])));
+        else
+          o[k] = s[0][k];
+      }
+    }
+  }
+};
+
+// Any element type, with or without downsampling, any strides: one sample
+// column per lane, float64 samples (exact sums for every 8/16/32-bit input).
+template <typename T, bool DOWN, bool LUMA>
+struct SrcGeneric {
+  static constexpr int NC = 1;
+  static constexpr int OUTW = G_OUTW_NARROW;
+  static constexpr int CH = LUMA ? 3 : 1;
+  static constexpr int NV = DOWN ? 4 : 1;
+  static constexpr bool FAST = std::is_same<T, uint8_t>::value || std::is_same<T, half_t>::value;
+  using S = double;
+  struct Raw {
+    T v[2][CH][NV];
+  };
+
+  const T* px[CH];
+  const T* py[CH];
+  int64_t shx, shy;
+  int rlim;      // last sample row a load may touch (clamp)
+  uint32_t col;  // first input column of this lane's sample
+  double kr, kg, kb;
+
+  __device__ inline void setup(const GmsdArgs& a, int n, int c, int strip, int lane) {
+    const T* bx = static_cast<const T*>(a.x) + n * a.vx.sn;
+    const T* by = static_cast<const T*>(a.y) + n * a.vy.sn;
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+      px[ch] = bx + (LUMA ? ch : c) * a.vx.sc;
+      py[ch] = by + (LUMA ? ch : c) * a.vy.sc;
+    }
+    shx = a.vx.sh;
+    shy = a.vy.sh;
+    rlim = a.Hd - 1;
+    const int sc = strip * OUTW + lane;
+    col = static_cast<uint32_t>(DOWN ? 2 * (sc < a.Wd ? sc : a.Wd - 1) : (sc < a.Wd ? sc : a.Wd - 1));
+    kr = a.kr;
+    kg = a.kg;
+    kb = a.kb;
+  }
+
+  __device__ inline Raw load(int r) const {
+    const int rr = r < rlim ? r : rlim;
+    const int64_t ir = DOWN ? 2 * static_cast<int64_t>(rr) : rr;
+    Raw v;
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+      const T* rx = px[ch] + ir * shx + col;
+      const T* ry = py[ch] + ir * shy + col;
+      v.v[0][ch][0] = rx[0];
+      v.v[1][ch][0] = ry[0];
+      if constexpr (DOWN) {
+        v.v[0][ch][1] = rx[1];
+        v.v[0][ch][2] = rx[shx];
+        v.v[0][ch][3] = rx[shx + 1];
+        v.v[1][ch][1] = ry[1];
+        v.v[1][ch][2] = ry[shy];
+        v.v[1][ch][3] = ry[shy + 1];
+      }
+    }
+    return v;
+  }
+
+  __device__ inline void samples(const Raw& v, S (&sx)[NC], S (&sy)[NC]) const {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      double s[CH];
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        s[ch] = Elem<T>::d(v.v[t][ch][0]);
+        if constexpr (DOWN)
+          s[ch] = (s[ch] + Elem<T>::d(v.v[t][ch][1])) +
+                  (Elem<T>::d(v.v[t][ch][2]) + Elem<T>::d(v.v[t][ch][3]));
+      }
+      S* o = t ? sy : sx;
+      if constexpr (LUMA)
+        o[0] = fma(kb, s[2], fma(kg, s[1], kr * s[0]));
+      else
+        o[0] = s[0];
+    }
+  }
+};
+
+// --------------------------------------------------------------------------
+// one wave: one (plane, chunk, strip) task
+// --------------------------------------------------------------------------
+
+// 3 s gx and 3 s gy at this lane's NC columns from the window rows a (top),
+// b, c (bottom).
+template <typename S, int NC>
+__device__ inline void prewitt(const S (&a)[NC], const S (&b)[NC], const S (&c)[NC],
+                               S (&gx)[NC], S (&gy)[NC]) {
+  S cs[NC + 2], rd[NC + 2];  // this lane's columns, then the next lane's first two
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    cs[k] = a[k] + b[k] + c[k];  // column sums, differenced across for gx
+    rd[k] = a[k] - c[k];         // row differences, summed across for gy
+  }
+  if constexpr (NC >= 2) {
+    cs[NC] = __shfl_down(cs[0], 1, WAVE);
+    cs[NC + 1] = __shfl_down(cs[1], 1, WAVE);
+    rd[NC] = __shfl_down(rd[0], 1, WAVE);
+    rd[NC + 1] = __shfl_down(rd[1], 1, WAVE);
+  } else {
+    cs[2] = __shfl_down(cs[0], 2, WAVE);
+    rd[1] = __shfl_down(rd[0], 1, WAVE);
+    rd[2] = __shfl_down(rd[0], 2, WAVE);
+  }
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    gx[k] = cs[k] - cs[k + 2];
+    gy[k] = rd[k] + rd[k + 1] + rd[k + 2];
+  }
+}
+
+// M1, M2 and M1 - M2.  Integer components are below 2^13 in magnitude, so the
+// 24-bit multiplier (full rate) is exact; float64 components use the
+// factored difference, which keeps dm accurate when M1 ~ M2.
+__device__ inline void mag2(int gx1, int gy1, int gx2, int gy2, int& m1, int& m2, int& dm) {
+  m1 = __mul24(gx1, gx1) + __mul24(gy1, gy1);
+  m2 = __mul24(gx2, gx2) + __mul24(gy2, gy2);
+  dm = m1 - m2;
+}
+__device__ inline void mag2(double gx1, double gy1, double gx2, double gy2, double& m1,
+                            double& m2, double& dm) {
+  m1 = fma(gx1, gx1, gy1 * gy1);
+  m2 = fma(gx2, gx2, gy2 * gy2);
+  dm = fma(gx1 - gx2, gx1 + gx2, (gy1 - gy2) * (gy1 + gy2));
+}
+
+// Rows [row0, row0 + rows) of one strip of one plane, added to acc / acc2.
+template <class Src>
+__device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int row0, int rows,
+                                double& acc, double& acc2) {
+  using S = typename Src::S;
+  using Raw = typename Src::Raw;
+  constexpr int NC = Src::NC;
+  const int lane = threadIdx.x % WAVE;
+
+  Src src;
+  src.setup(a, n, c, strip, lane);
+  // Loads past the run re-read its last row (cached) instead of being
+  // branched around: a conditional load group makes the compiler wait for
+  // every load in flight, which would serialise the double buffering.
+  src.rlim = row0 + rows + 1;
+  const int col = strip * Src::OUTW + NC * lane;  // first output column of the lane
+  bool ok[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) ok[k] = NC * lane + k < Src::OUTW && col + k < a.Wout;
+
+  // every load of the prologue is in flight before the first one is used
+  const Raw p0 = src.load(row0), p1 = src.load(row0 + 1);
+  // two named row buffers, so a group never copies the one in flight
+  Raw bufA[G_PD], bufB[G_PD];
+#pragma unroll
+  for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(row0 + 2 + i);
+  S xa[NC], xb[NC], ya[NC], yb[NC];
+  src.samples(p0, xa, ya);
+  src.samples(p1, xb, yb);
+
+  using Acc = typename std::conditional<Src::FAST, float, double>::type;
+  // G_PD rows from `cur`, starting at row g of the run; the group's sums are
+  // formed at the accumulation type, then added in float64
+  auto group = [&](const Raw (&cur)[G_PD], int g) {
+    Acc gs = Acc(0), gs2 = Acc(0);
+#pragma unroll
+    for (int i = 0; i < G_PD; ++i) {
+      if (g + i < rows) {  // uniform
+        S xc[NC], yc[NC];
+        src.samples(cur[i], xc, yc);
+        S gx1[NC], gy1[NC], gx2[NC], gy2[NC];
+        prewitt<S, NC>(xa, xb, xc, gx1, gy1);
+        prewitt<S, NC>(ya, yb, yc, gx2, gy2);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+          S m1, m2, dm;
+          mag2(gx1[k], gy1[k], gx2[k], gy2[k], m1, m2, dm);
+          dm = ok[k] ? dm : S(0);
+          const Acc d = one_minus_q<Src::FAST, S>(m1, m2, dm, a.eps2f, a.T2f, a.eps2, a.T2);
+          gs += d;
+          gs2 = fma(d, d, gs2);
+        }
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+          xa[k] = xb[k];
+          xb[k] = xc[k];
+          ya[k] = yb[k];
+          yb[k] = yc[k];
+        }
+      }
+    }
+    acc += static_cast<double>(gs);
+    acc2 += static_cast<double>(gs2);
+  };
+
+  for (int g = 0; g < rows; g += 2 * G_PD) {
+#pragma unroll
+    for (int i = 0; i < G_PD; ++i) bufB[i] = src.load(row0 + 2 + g + G_PD + i);
+    group(bufA, g);
+    if (g + G_PD >= rows) break;
+#pragma unroll
+    for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(row0 + 2 + g + 2 * G_PD + i);
+    group(bufB, g + G_PD);
+  }
+}
+
+template <class Src>
+__global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
+  // one task per workgroup: its four waves take four adjacent strips over the
+  // same rows, so each input row is fetched as one contiguous stretch
+  const int task = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
+  if (task >= a.tasks) return;  // whole workgroup; no barrier follows
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int lane = threadIdx.x % WAVE;
+  const int n = task / a.wpi;
+  const int k = task - n * a.wpi;
+  // this workgroup's share [s, e) of the image's (channel, group, row) space
+  int64_t s = a.rows_img * k / a.wpi;
+  const int64_t e = a.rows_img * (k + 1) / a.wpi;
+  const int64_t per_plane = static_cast<int64_t>(a.groups) * a.Hout;
+  double acc = 0.0, acc2 = 0.0;
+  while (s < e) {  // uniform; one run per strip group touched
+    const int c = static_cast<int>(s / per_plane);
+    const int64_t rem = s - c * per_plane;
+    const int grp = static_cast<int>(rem / a.Hout);
+    const int row = static_cast<int>(rem - static_cast<int64_t>(grp) * a.Hout);
+    const int len = static_cast<int>(min(e - s, static_cast<int64_t>(a.Hout - row)));
+    const int strip = grp * WAVES_PER_BLOCK + wave;
+    if (strip < a.strips) gmsd_run<Src>(a, n, c, strip, row, len, acc, acc2);
+    s += len;
+  }
+  acc = wave_sum(acc);
+  acc2 = wave_sum(acc2);
+  if (lane == 0) {
+    const int slot = task * WAVES_PER_BLOCK + wave;
+    a.psum[slot] = acc;
+    a.psumsq[slot] = acc2;
   }
 }
 
 // Block b reduces image b: mean and population standard deviation of its map
-// (reference fa_cuda.cu:1005-1026).
+// (reference fa_cuda.cu:1005-1026), from the sums of d = 1 - q.
 __global__ __launch_bounds__(BLOCK) void gmsd_finalize_kernel(
     const double* __restrict__ psum, const double* __restrict__ psumsq, int ncols,
     double npix, double* __restrict__ out_mean, double* __restrict__ out_std) {
@@ -134,39 +440,159 @@ __global__ __launch_bounds__(BLOCK) void gmsd_finalize_kernel(
   double sa = 0.0, sb = 0.0;
   block_sum2(a, b, smem, &sa, &sb);
   if (threadIdx.x == 0) {
-    const double m = sa / npix;
-    const double var = sb / npix - m * m;
-    out_mean[blockIdx.x] = m;
+    const double md = sa / npix;  // mean of d = 1 - q
+    const double var = sb / npix - md * md;
+    out_mean[blockIdx.x] = 1.0 - md;
     out_std[blockIdx.x] = sqrt(var > 0.0 ? var : 0.0);
   }
 }
 
-static int gmsd_geometry(int H, int W, int downsample, int* Hd, int* Wd, int* Hout,
-                         int* Wout, int* strips, int* chunks) {
+struct GGeom {
+  int Hd, Wd, Hout, Wout;
+};
+
+static int gmsd_geometry(int H, int W, int downsample, GGeom* g) {
   if (H <= 0 || W <= 0) return FA_E_SHAPE;
-  *Hd = downsample ? H / 2 : H;
-  *Wd = downsample ? W / 2 : W;
-  *Hout = *Hd - 2;
-  *Wout = *Wd - 2;
-  if (*Hout <= 0 || *Wout <= 0) return FA_E_SHAPE;
-  *strips = (*Wout + G_STRIP - 1) / G_STRIP;
-  *chunks = (*Hout + G_TH - 1) / G_TH;
+  g->Hd = downsample ? H / 2 : H;
+  g->Wd = downsample ? W / 2 : W;
+  g->Hout = g->Hd - 2;
+  g->Wout = g->Wd - 2;
+  if (g->Hout <= 0 || g->Wout <= 0) return FA_E_SHAPE;
   return FA_OK;
 }
 
-template <typename T>
-static void launch_gmsd_t(bool down, dim3 grid, hipStream_t st, const void* x,
-                          const void* y, int H, int W, int Hd, int Wd, int Hout,
-                          int Wout, double Tc, double eps, int strips, int bpp,
-                          double* psum, double* psumsq) {
-  const T* tx = static_cast<const T*>(x);
-  const T* ty = static_cast<const T*>(y);
-  if (down)
-    hipLaunchKernelGGL((gmsd_kernel<T, true>), grid, dim3(BLOCK), 0, st, tx, ty, H, W, Hd, Wd,
-                       Hout, Wout, Tc, eps, strips, bpp, psum, psumsq);
-  else
-    hipLaunchKernelGGL((gmsd_kernel<T, false>), grid, dim3(BLOCK), 0, st, tx, ty, H, W, Hd, Wd,
-                       Hout, Wout, Tc, eps, strips, bpp, psum, psumsq);
+// Partial slots per output plane (the workspace query): one per G_SLOT_ROWS
+// rows of the narrowest strips, and at least one workgroup's worth.  A launch
+// uses at most Cout * slots per image, one per wave.
+static int gmsd_slots(const GGeom& g) {
+  const int strips = (g.Wout + G_OUTW_NARROW - 1) / G_OUTW_NARROW;
+  const int chunks = (g.Hout + G_SLOT_ROWS - 1) / G_SLOT_ROWS;
+  return std::max(strips * chunks, WAVES_PER_BLOCK);
+}
+
+static bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+// Workgroups per image: one round of resident workgroups over the whole
+// launch, no more than the workspace holds (a slot per wave) or than leaves a
+// workgroup G_MIN_ROWS rows.
+template <class Src>
+static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipStream_t st,
+                       int* wpi_used) {
+  static int wgs_per_cu = 0;  // occupancy of this kernel, queried once
+  if (wgs_per_cu <= 0) {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &v, reinterpret_cast<const void*>(&gmsd_kernel<Src>), BLOCK, 0) != hipSuccess ||
+        v <= 0)
+      v = 1;
+    wgs_per_cu = v;
+  }
+  a.strips = (a.Wout + Src::OUTW - 1) / Src::OUTW;
+  a.groups = (a.strips + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+  a.rows_img = static_cast<int64_t>(a.Cout) * a.groups * a.Hout;
+  const int64_t resident = static_cast<int64_t>(cu_count(device)) * wgs_per_cu;
+  int64_t wpi = (resident + N - 1) / N;
+  wpi = std::min<int64_t>(wpi, (a.rows_img + G_MIN_ROWS - 1) / G_MIN_ROWS);
+  wpi = std::min<int64_t>(wpi, slots_per_image / WAVES_PER_BLOCK);
+  wpi = std::max<int64_t>(wpi, 1);
+  const int64_t tasks = static_cast<int64_t>(N) * wpi;
+  if (tasks > INT32_MAX / WAVES_PER_BLOCK) return FA_E_SHAPE;
+  a.wpi = static_cast<int>(wpi);
+  a.tasks = static_cast<int>(tasks);
+  hipLaunchKernelGGL((gmsd_kernel<Src>), dim3(static_cast<unsigned>(tasks)), dim3(BLOCK), 0, st, a);
+  FA_LAUNCH_CHECK();
+  *wpi_used = a.wpi * WAVES_PER_BLOCK;  // partial slots per image
+  return FA_OK;
+}
+
+struct GLaunch {
+  int N, slots, device;
+  hipStream_t st;
+};
+
+template <typename T, bool LUMA>
+static int dispatch_gmsd_t(const GmsdArgs& a, const GLaunch& l, bool down, int* wpi) {
+  if (down) return launch_gmsd<SrcGeneric<T, true, LUMA>>(a, l.N, l.slots, l.device, l.st, wpi);
+  return launch_gmsd<SrcGeneric<T, false, LUMA>>(a, l.N, l.slots, l.device, l.st, wpi);
+}
+
+template <bool LUMA>
+static int dispatch_gmsd(int dtype, const GmsdArgs& a, const GLaunch& l, bool down, bool wide,
+                         int* wpi) {
+  switch (dtype) {
+    case FA_U8:
+      if (wide) return launch_gmsd<SrcU8Wide<LUMA>>(a, l.N, l.slots, l.device, l.st, wpi);
+      return dispatch_gmsd_t<uint8_t, LUMA>(a, l, down, wpi);
+    case FA_F16: return dispatch_gmsd_t<half_t, LUMA>(a, l, down, wpi);
+    case FA_BF16: return dispatch_gmsd_t<bf16_t, LUMA>(a, l, down, wpi);
+    case FA_F32: return dispatch_gmsd_t<float, LUMA>(a, l, down, wpi);
+    case FA_F64: return dispatch_gmsd_t<double, LUMA>(a, l, down, wpi);
+    default: return FA_E_DTYPE;
+  }
+}
+
+static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int H, int W,
+                     const int64_t* xs, const int64_t* ys, const double* luma, double Tc,
+                     double eps, int downsample, double* psum, double* psumsq, int bpp,
+                     double* out_mean, double* out_std, int device, void* stream) {
+  if (!x || !y || !psum || !psumsq || !out_mean || !out_std) return FA_E_ARG;
+  if (N <= 0 || C <= 0) return FA_E_SHAPE;
+  if (dtype < FA_U8 || dtype > FA_F64) return FA_E_DTYPE;
+  if (luma && C != 3) return FA_E_SHAPE;
+  GGeom g;
+  const int rc = gmsd_geometry(H, W, downsample, &g);
+  if (rc != FA_OK) return rc;
+  if (bpp != gmsd_slots(g)) return FA_E_ARG;
+
+  GmsdArgs a = {};
+  a.x = x;
+  a.y = y;
+  const int64_t cs = static_cast<int64_t>(H) * W;
+  a.vx = xs ? GView{xs[0], xs[1], xs[2]} : GView{cs * C, cs, W};
+  a.vy = ys ? GView{ys[0], ys[1], ys[2]} : GView{cs * C, cs, W};
+  // rows may not overlap; planes and images run forward
+  if (a.vx.sh < W || a.vy.sh < W || a.vx.sc < 0 || a.vy.sc < 0 || a.vx.sn < 0 || a.vy.sn < 0)
+    return FA_E_SHAPE;
+  a.Cout = luma ? 1 : C;
+  a.Hd = g.Hd;
+  a.Wd = g.Wd;
+  a.Hout = g.Hout;
+  a.Wout = g.Wout;
+  if (luma) {
+    a.kr = luma[0];
+    a.kg = luma[1];
+    a.kb = luma[2];
+  }
+  const double sc2 = downsample ? 144.0 : 9.0;  // 9 s^2
+  a.T2 = Tc * sc2;
+  a.eps2 = eps * sc2;
+  a.T2f = static_cast<float>(a.T2);
+  a.eps2f = static_cast<float>(a.eps2);
+  a.psum = psum;
+  a.psumsq = psumsq;
+  const bool down = downsample != 0;
+  // the dword path: uint8, downsampled, every row of every plane 4-byte aligned
+  // (buffer addressing: a plane's rows must lie within 2^31 bytes of its base)
+  const int64_t ext_x = static_cast<int64_t>(2 * g.Hd - 1) * a.vx.sh + W;
+  const int64_t ext_y = static_cast<int64_t>(2 * g.Hd - 1) * a.vy.sh + W;
+  const int64_t strides = a.vx.sn | a.vx.sc | a.vx.sh | a.vy.sn | a.vy.sc | a.vy.sh;
+  const bool wide = dtype == FA_U8 && down && W % 4 == 0 && aligned4(x) && aligned4(y) &&
+                    (strides & 3) == 0 && ext_x <= INT32_MAX && ext_y <= INT32_MAX;
+  a.ext_x = wide ? static_cast<int>(ext_x) : 0;
+  a.ext_y = wide ? static_cast<int>(ext_y) : 0;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const GLaunch l = {N, a.Cout * bpp, device, st};  // psum is [N * Cout, bpp]
+  int wpi = 0;
+  const int r = luma ? dispatch_gmsd<true>(dtype, a, l, down, wide, &wpi)
+                     : dispatch_gmsd<false>(dtype, a, l, down, wide, &wpi);
+  if (r != FA_OK) return r;
+  // each image owns wpi consecutive slots, one per wave
+  hipLaunchKernelGGL(gmsd_finalize_kernel, dim3(static_cast<unsigned>(N)), dim3(BLOCK), 0, st,
+                     psum, psumsq, wpi,
+                     static_cast<double>(g.Hout) * g.Wout * a.Cout, out_mean, out_std);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
 }
 
 }  // namespace fa
@@ -178,10 +604,10 @@ extern "C" {
 // reference: fa_cuda.cu:1416-1424 (fa_cuda_gmsd_workspace)
 FA_API int fa_gpu_gmsd_workspace(int H, int W, int downsample, int* out_bpp) {
   if (!out_bpp) return FA_E_ARG;
-  int Hd, Wd, Hout, Wout, strips, chunks;
-  const int rc = gmsd_geometry(H, W, downsample, &Hd, &Wd, &Hout, &Wout, &strips, &chunks);
+  GGeom g;
+  const int rc = gmsd_geometry(H, W, downsample, &g);
   if (rc != FA_OK) return rc;
-  *out_bpp = strips * chunks;
+  *out_bpp = gmsd_slots(g);
   return FA_OK;
 }
 
@@ -190,33 +616,20 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
                        int H, int W, double Tc, double eps, int downsample,
                        double* psum, double* psumsq, int bpp, double* out_mean,
                        double* out_std, int device, void* stream) {
-  if (!x || !y || !psum || !psumsq || !out_mean || !out_std) return FA_E_ARG;
-  if (N <= 0 || C <= 0) return FA_E_SHAPE;
-  int Hd, Wd, Hout, Wout, strips, chunks;
-  const int rc = gmsd_geometry(H, W, downsample, &Hd, &Wd, &Hout, &Wout, &strips, &chunks);
-  if (rc != FA_OK) return rc;
-  if (bpp != strips * chunks) return FA_E_ARG;
-  const int64_t total = static_cast<int64_t>(N) * C * bpp;
-  if (total > static_cast<int64_t>(INT32_MAX) / BLOCK) return FA_E_SHAPE;
-  FA_DEVICE_SCOPE(device);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(total));
-  const bool down = downsample != 0;
-  const double T = Tc, e = eps;
-  switch (dtype) {
-    case FA_U8: launch_gmsd_t<uint8_t>(down, grid, st, x, y, H, W, Hd, Wd, Hout, Wout, T, e, strips, bpp, psum, psumsq); break;
-    case FA_F16: launch_gmsd_t<half_t>(down, grid, st, x, y, H, W, Hd, Wd, Hout, Wout, T, e, strips, bpp, psum, psumsq); break;
-    case FA_BF16: launch_gmsd_t<bf16_t>(down, grid, st, x, y, H, W, Hd, Wd, Hout, Wout, T, e, strips, bpp, psum, psumsq); break;
-    case FA_F32: launch_gmsd_t<float>(down, grid, st, x, y, H, W, Hd, Wd, Hout, Wout, T, e, strips, bpp, psum, psumsq); break;
-    case FA_F64: launch_gmsd_t<double>(down, grid, st, x, y, H, W, Hd, Wd, Hout, Wout, T, e, strips, bpp, psum, psumsq); break;
-    default: return FA_E_DTYPE;
-  }
-  FA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(gmsd_finalize_kernel, dim3(static_cast<unsigned>(N)), dim3(BLOCK), 0, st,
-                     psum, psumsq, C * bpp, static_cast<double>(Hout) * Wout * C, out_mean,
-                     out_std);
-  FA_LAUNCH_CHECK();
-  return FA_OK;
+  return gmsd_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, Tc, eps, downsample,
+                   psum, psumsq, bpp, out_mean, out_std, device, stream);
+}
+
+// No counterpart in the reference, which materialises a float32 luma plane
+// (functional.py:267-271) and copies crops contiguous (backend.py:346,482).
+FA_API int fa_gpu_gmsd_ex(const void* x, const void* y, int dtype, int N, int C,
+                          int H, int W, const int64_t* x_strides,
+                          const int64_t* y_strides, const double* luma, double Tc,
+                          double eps, int downsample, double* psum, double* psumsq,
+                          int bpp, double* out_mean, double* out_std, int device,
+                          void* stream) {
+  return gmsd_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, Tc, eps, downsample,
+                   psum, psumsq, bpp, out_mean, out_std, device, stream);
 }
 
 }  // extern "C"

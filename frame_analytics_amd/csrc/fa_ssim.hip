@@ -29,39 +29,45 @@ namespace fa {
 
 enum { MODE_REDUCE = 0, MODE_MAP = 1, MODE_CS = 2, MODE_PREP = 3, MODE_PREP_CS = 4 };
 
-// Output rows per workgroup (TH).  A workgroup walks its rows in sequence, so
-// TH is the launch's critical path: a launch takes the largest TH of
-// 64, 32, 16, 8, 4 that still gives it SSIM_MIN_WGS workgroups (the halo of
-// K-1 rows re-read per chunk is what a smaller TH costs).  Large frames keep
-// TH = 64; the coarse MS-SSIM scales, small batches and small crops get the
-// parallelism back.  Every TH is a multiple of the phase height and even, so
-// pyramid row pairs never straddle two chunks.  The partial buffers are sized
-// for the smallest TH (the *_workspace queries) and a launch uses the first
-// strips * chunks slots of each plane.
+// Output rows per workgroup (TH), one of 64, 32, 16, 8, 4.  A workgroup walks
+// its rows in sequence and re-reads K-1 halo rows, so a launch trades rounds
+// of resident workgroups against rows per workgroup (tiling_for): configs of
+// many large frames keep TH = 64, while single frames, the coarse MS-SSIM
+// scales and small crops get the parallelism back, and the float64 backward
+// kernels (one workgroup per CU) are cut only as fine as they can use.  Every
+// TH is a multiple of the phase height and even, so pyramid row pairs never
+// straddle two chunks.  The partial buffers are sized for the smallest TH
+// (the *_workspace queries) and a launch uses the first strips * chunks slots
+// of each plane.
 #ifndef FA_SSIM_TH_MAX
 #define FA_SSIM_TH_MAX 64
 #endif
-#ifndef FA_SSIM_MIN_WGS
-#define FA_SSIM_MIN_WGS 2048
-#endif
 constexpr int SSIM_TH_MAX = FA_SSIM_TH_MAX;
 constexpr int SSIM_TH_MIN = 4;
-constexpr int64_t SSIM_MIN_WGS = FA_SSIM_MIN_WGS;
 static_assert(SSIM_TH_MIN % PH == 0 && SSIM_TH_MAX % SSIM_TH_MIN == 0, "TH ladder");
 
 struct Tiling {
   int TH, strips, tiles;  // tiles = strips * chunks, per plane
 };
 
-// The tiling of one launch over `planes` planes of an out_H x out_W grid.
-inline Tiling tiling_for(int64_t planes, int out_H, int out_W, int K) {
-  Tiling t = {SSIM_TH_MAX, 0, 0};
-  for (;; t.TH /= 2) {
-    int chunks = 0;
-    strip_grid(out_H, out_W, K, t.TH, &t.strips, &chunks);
-    t.tiles = t.strips * chunks;
-    if (t.TH <= SSIM_TH_MIN || planes * t.tiles >= SSIM_MIN_WGS) return t;
+// The tiling of one launch over `planes` planes of an out_H x out_W grid
+// when the chip holds `resident` workgroups at once: the TH that minimises
+// rounds x rows walked per workgroup, ceil(wgs / resident) * (TH + K + 1)
+// (K - 1 halo rows plus about two rows of set-up); ties keep the larger TH.
+inline Tiling tiling_for(int64_t planes, int out_H, int out_W, int K, int64_t resident) {
+  Tiling best = {0, 0, 0};
+  int64_t best_cost = INT64_MAX;
+  for (int th = SSIM_TH_MAX; th >= SSIM_TH_MIN; th /= 2) {
+    int strips = 0, chunks = 0;
+    strip_grid(out_H, out_W, K, th, &strips, &chunks);
+    const int64_t wgs = planes * strips * chunks;
+    const int64_t cost = ((wgs + resident - 1) / resident) * (th + K + 1);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = Tiling{th, strips, strips * chunks};
+    }
   }
+  return best;
 }
 
 // Partial slots per plane the workspace query reports: enough for any TH.
@@ -504,44 +510,89 @@ __global__ __launch_bounds__(BLOCK) void planes2_kernel(const double* __restrict
 // --------------------------------------------------------------------------
 // host dispatch
 // --------------------------------------------------------------------------
-template <typename T, typename CT, int MODE>
-static int launch_ssim_k(int K, dim3 grid, hipStream_t st, const SsimArgs& a) {
-  switch (K) {
-    case 3: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 3>), grid, dim3(BLOCK), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 5>), grid, dim3(BLOCK), 0, st, a); break;
-    case 7: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 7>), grid, dim3(BLOCK), 0, st, a); break;
-    case 9: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 9>), grid, dim3(BLOCK), 0, st, a); break;
-    case 11: hipLaunchKernelGGL((ssim_kernel<T, CT, MODE, 11>), grid, dim3(BLOCK), 0, st, a); break;
-    default: return FA_E_WINDOW;
-  }
+// Workgroups of this kernel one CU holds at once.
+static int occupancy_wgs(const void* fn) {
+  int v = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, fn, BLOCK, 0) != hipSuccess || v <= 0)
+    v = 1;
+  return v;
+}
+
+// Workgroups of a strip-engine launch over `planes` planes; the grid is 1-D.
+static int grid_of(int64_t planes, int64_t per_plane, dim3* grid) {
+  const int64_t total = planes * per_plane;
+  if (total <= 0 || total > (static_cast<int64_t>(INT32_MAX) / BLOCK)) return FA_E_SHAPE;
+  *grid = dim3(static_cast<unsigned>(total));
+  return FA_OK;
+}
+
+// Tiles `kern` over `planes` planes of an out_H x out_W grid for its
+// occupancy `occ` and launches it; a.TH / a.strips / a.bpp report the tiling.
+template <typename Args>
+static int launch_strips(void (*kern)(Args), int occ, Args& a, int64_t planes, int out_H,
+                         int out_W, int K, int device, hipStream_t st) {
+  const Tiling t = tiling_for(planes, out_H, out_W, K, static_cast<int64_t>(cu_count(device)) * occ);
+  a.TH = t.TH;
+  a.strips = t.strips;
+  a.bpp = t.tiles;
+  dim3 grid;
+  const int rc = grid_of(planes, t.tiles, &grid);
+  if (rc != FA_OK) return rc;
+  hipLaunchKernelGGL(kern, grid, dim3(BLOCK), 0, st, a);
   FA_LAUNCH_CHECK();
   return FA_OK;
 }
 
+template <typename T, typename CT, int MODE, int KW>
+static int launch_ssim_kw(SsimArgs& a, int64_t planes, int device, hipStream_t st) {
+  static const int occ =
+      occupancy_wgs(reinterpret_cast<const void*>(&ssim_kernel<T, CT, MODE, KW>));
+  return launch_strips(ssim_kernel<T, CT, MODE, KW>, occ, a, planes, a.Hout, a.Wout, KW,
+                       device, st);
+}
+
+template <typename T, typename CT, int MODE>
+static int launch_ssim_k(int K, SsimArgs& a, int64_t planes, int device, hipStream_t st) {
+  switch (K) {
+    case 3: return launch_ssim_kw<T, CT, MODE, 3>(a, planes, device, st);
+    case 5: return launch_ssim_kw<T, CT, MODE, 5>(a, planes, device, st);
+    case 7: return launch_ssim_kw<T, CT, MODE, 7>(a, planes, device, st);
+    case 9: return launch_ssim_kw<T, CT, MODE, 9>(a, planes, device, st);
+    case 11: return launch_ssim_kw<T, CT, MODE, 11>(a, planes, device, st);
+    default: return FA_E_WINDOW;
+  }
+}
+
 template <int MODE>
-static int launch_ssim(int dtype, int K, dim3 grid, hipStream_t st, const SsimArgs& a) {
+static int launch_ssim(int dtype, int K, SsimArgs& a, int64_t planes, int device,
+                       hipStream_t st) {
   switch (dtype) {
-    case FA_U8: return launch_ssim_k<uint8_t, float, MODE>(K, grid, st, a);
-    case FA_F16: return launch_ssim_k<half_t, float, MODE>(K, grid, st, a);
-    case FA_BF16: return launch_ssim_k<bf16_t, float, MODE>(K, grid, st, a);
-    case FA_F32: return launch_ssim_k<float, float, MODE>(K, grid, st, a);
-    case FA_F64: return launch_ssim_k<double, double, MODE>(K, grid, st, a);
+    case FA_U8: return launch_ssim_k<uint8_t, float, MODE>(K, a, planes, device, st);
+    case FA_F16: return launch_ssim_k<half_t, float, MODE>(K, a, planes, device, st);
+    case FA_BF16: return launch_ssim_k<bf16_t, float, MODE>(K, a, planes, device, st);
+    case FA_F32: return launch_ssim_k<float, float, MODE>(K, a, planes, device, st);
+    case FA_F64: return launch_ssim_k<double, double, MODE>(K, a, planes, device, st);
     default: return FA_E_DTYPE;
   }
 }
 
+template <typename T, int KW, bool DY>
+static int launch_scatter_kw(ScatterArgs& a, int64_t planes, int device, hipStream_t st) {
+  static const int occ = occupancy_wgs(reinterpret_cast<const void*>(&scatter_kernel<T, KW, DY>));
+  return launch_strips(scatter_kernel<T, KW, DY>, occ, a, planes, a.H, a.W, KW, device, st);
+}
+
 template <typename T, bool DY>
-static int launch_scatter_k(int K, dim3 grid, hipStream_t st, const ScatterArgs& a) {
+static int launch_scatter_k(int K, ScatterArgs& a, int64_t planes, int device,
+                            hipStream_t st) {
   switch (K) {
-    case 3: hipLaunchKernelGGL((scatter_kernel<T, 3, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((scatter_kernel<T, 5, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 7: hipLaunchKernelGGL((scatter_kernel<T, 7, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 9: hipLaunchKernelGGL((scatter_kernel<T, 9, DY>), grid, dim3(BLOCK), 0, st, a); break;
-    case 11: hipLaunchKernelGGL((scatter_kernel<T, 11, DY>), grid, dim3(BLOCK), 0, st, a); break;
+    case 3: return launch_scatter_kw<T, 3, DY>(a, planes, device, st);
+    case 5: return launch_scatter_kw<T, 5, DY>(a, planes, device, st);
+    case 7: return launch_scatter_kw<T, 7, DY>(a, planes, device, st);
+    case 9: return launch_scatter_kw<T, 9, DY>(a, planes, device, st);
+    case 11: return launch_scatter_kw<T, 11, DY>(a, planes, device, st);
     default: return FA_E_WINDOW;
   }
-  FA_LAUNCH_CHECK();
-  return FA_OK;
 }
 
 // Validates the common SSIM arguments and derives the output geometry.
@@ -555,14 +606,6 @@ static int ssim_shape(int N, int C, int H, int W, int K, int* Hout, int* Wout) {
   return FA_OK;
 }
 
-// Workgroups of a strip-engine launch over `planes` planes; the grid is 1-D.
-static int grid_of(int64_t planes, int64_t per_plane, dim3* grid) {
-  const int64_t total = planes * per_plane;
-  if (total <= 0 || total > (static_cast<int64_t>(INT32_MAX) / BLOCK)) return FA_E_SHAPE;
-  *grid = dim3(static_cast<unsigned>(total));
-  return FA_OK;
-}
-
 // The coefficient pass plus the scatter, shared by the backward entry points.
 // T is the element type of x, y, dx and dy (float, or double for the float64
 // MS-SSIM pyramid levels); the arithmetic is float64 either way.
@@ -573,7 +616,7 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
                               int C, int H, int W, double shift, double C1,
                               double C2, float* aux, T* dx, T* dy,
                               const void* gpx, const void* gpy, int gp_dtype,
-                              hipStream_t st) {
+                              int device, hipStream_t st) {
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
   if (rc != FA_OK) return rc;
@@ -588,10 +631,6 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
   a.W = W;
   a.Hout = Hout;
   a.Wout = Wout;
-  const Tiling tp = tiling_for(planes, Hout, Wout, K);
-  a.TH = tp.TH;
-  a.strips = tp.strips;
-  a.bpp = tp.tiles;
   a.shift = shift;
   a.C1 = C1;
   a.C2 = C2;
@@ -606,10 +645,7 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
   a.oc = aux + aux_stride;
   a.otx = aux + 2 * aux_stride;
   a.oty = dy ? aux + 3 * aux_stride : nullptr;
-  dim3 grid;
-  rc = grid_of(planes, a.bpp, &grid);
-  if (rc != FA_OK) return rc;
-  rc = launch_ssim_k<T, double, MODE>(K, grid, st, a);
+  rc = launch_ssim_k<T, double, MODE>(K, a, planes, device, st);
   if (rc != FA_OK) return rc;
 
   ScatterArgs s = {};
@@ -626,17 +662,12 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
   s.W = W;
   s.Hout = Hout;
   s.Wout = Wout;
-  const Tiling ts = tiling_for(planes, H, W, K);
-  s.TH = ts.TH;
-  s.strips = ts.strips;
-  s.bpp = ts.tiles;
   s.shift = shift;
   s.gpx = gpx;
   s.gpy = gpy;
   s.gp_f64 = gp_dtype == FA_F64 ? 1 : 0;
-  rc = grid_of(planes, s.bpp, &grid);
-  if (rc != FA_OK) return rc;
-  return dy ? launch_scatter_k<T, true>(K, grid, st, s) : launch_scatter_k<T, false>(K, grid, st, s);
+  return dy ? launch_scatter_k<T, true>(K, s, planes, device, st)
+            : launch_scatter_k<T, false>(K, s, planes, device, st);
 }
 
 // fa_gpu_ssim_cs, optionally writing the next pyramid level (px / py non-null).
@@ -651,7 +682,6 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   if (rc != FA_OK) return rc;
   if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
   const int64_t planes = static_cast<int64_t>(N) * C;
-  const Tiling tl = tiling_for(planes, Hout, Wout, K);
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
@@ -662,9 +692,6 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   a.W = W;
   a.Hout = Hout;
   a.Wout = Wout;
-  a.TH = tl.TH;
-  a.strips = tl.strips;
-  a.bpp = tl.tiles;
   a.shift = shift;
   a.C1 = C1;
   a.C2 = C2;
@@ -674,13 +701,10 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   a.px = px;
   a.py = py;
   a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
-  dim3 grid;
-  rc = grid_of(planes, tl.tiles, &grid);
-  if (rc != FA_OK) return rc;
-  rc = launch_ssim<MODE_CS>(dtype, K, grid, st, a);
+  rc = launch_ssim<MODE_CS>(dtype, K, a, planes, device, st);
   if (rc != FA_OK) return rc;
   hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
-                     partial, partial_cs, tl.tiles, static_cast<double>(Hout) * Wout, out_s,
+                     partial, partial_cs, a.bpp, static_cast<double>(Hout) * Wout, out_s,
                      out_cs);
   FA_LAUNCH_CHECK();
   return FA_OK;
@@ -713,7 +737,6 @@ FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
   if (rc != FA_OK) return rc;
   if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
-  const Tiling tl = tiling_for(static_cast<int64_t>(N) * C, Hout, Wout, K);
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
@@ -724,25 +747,20 @@ FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
   a.W = W;
   a.Hout = Hout;
   a.Wout = Wout;
-  a.TH = tl.TH;
-  a.strips = tl.strips;
-  a.bpp = tl.tiles;
   a.shift = shift;
   a.C1 = C1;
   a.C2 = C2;
   a.win = win;
   a.map = map_out;
   a.partial = partial;
-  dim3 grid;
-  rc = grid_of(static_cast<int64_t>(N) * C, tl.tiles, &grid);
-  if (rc != FA_OK) return rc;
-  rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, grid, st, a)
-               : launch_ssim<MODE_REDUCE>(dtype, K, grid, st, a);
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, a, planes, device, st)
+               : launch_ssim<MODE_REDUCE>(dtype, K, a, planes, device, st);
   if (rc != FA_OK) return rc;
 
   // each image owns C * tiles consecutive slots of `partial`
   const double npix = static_cast<double>(Hout) * Wout;
-  return launch_finalize(partial, false, N, C * tl.tiles, npix * C,
+  return launch_finalize(partial, false, N, C * a.bpp, npix * C,
                          npix * C * static_cast<double>(N), FA_PSNR_NONE,
                          out_per_image, out_total, nullptr, nullptr, st);
 }
@@ -788,7 +806,7 @@ FA_API int fa_gpu_ssim_backward(const float* x, const float* y,
   FA_DEVICE_SCOPE(device);
   return ssim_backward_impl<float, MODE_PREP>(x, y, dL_dmap, grad_scalar, nullptr, nullptr,
                                               win, K, N, C, H, W, shift, C1, C2, aux, dx, dy,
-                                              nullptr, nullptr, FA_F32,
+                                              nullptr, nullptr, FA_F32, device,
                                               static_cast<hipStream_t>(stream));
 }
 
@@ -804,7 +822,7 @@ FA_API int fa_gpu_ssim_cs_backward(const float* x, const float* y,
   FA_DEVICE_SCOPE(device);
   return ssim_backward_impl<float, MODE_PREP_CS>(x, y, nullptr, nullptr, gs, gcs, win, K, N, C,
                                                  H, W, shift, C1, C2, aux, dx, dy,
-                                                 nullptr, nullptr, FA_F32,
+                                                 nullptr, nullptr, FA_F32, device,
                                                  static_cast<hipStream_t>(stream));
 }
 
@@ -831,11 +849,11 @@ FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
     return ssim_backward_impl<float, MODE_PREP_CS>(
         static_cast<const float*>(x), static_cast<const float*>(y), nullptr, nullptr, gs, gcs,
         win, K, N, C, H, W, shift, C1, C2, aux, static_cast<float*>(dx),
-        static_cast<float*>(dy), gpx, gpy, gp_dtype, st);
+        static_cast<float*>(dy), gpx, gpy, gp_dtype, device, st);
   return ssim_backward_impl<double, MODE_PREP_CS>(
       static_cast<const double*>(x), static_cast<const double*>(y), nullptr, nullptr, gs, gcs,
       win, K, N, C, H, W, shift, C1, C2, aux, static_cast<double*>(dx),
-      static_cast<double*>(dy), gpx, gpy, gp_dtype, st);
+      static_cast<double*>(dy), gpx, gpy, gp_dtype, device, st);
 }
 
 }  // extern "C"

@@ -607,21 +607,26 @@ def _gmsd_common(x, y, data_range, T, eps, downsample, dtype, luma, crop_border,
     _check_reduction(reduction)
     x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
     wdt = _work_dtype(x4, dtype)
-    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     Tv = float(T) if T is not None else 170.0 * (L / 255.0) ** 2
     ev = float(eps) if eps is not None else (1e-6 * L) ** 2
     if backend_hint != "torch":
         from . import backend
 
-        # the kernel never writes the map and computes in float32
-        native_ok = not return_map and wdt != torch.float64
-        fast = (backend.try_gmsd(x4, y4, T=Tv, eps=ev, downsample=downsample)
-                if native_ok else None)
+        # The kernel forms the luma plane itself (its offset cancels out of
+        # every gradient) and reads crops in place; it computes in float64,
+        # so a float64 working dtype needs no other path.  It writes no map.
+        fast = None
+        if not return_map:
+            if mode is not None and x4.shape[1] != 3:
+                raise ValueError(f"luma needs a 3-channel image, got {x4.shape[1]} channels")
+            lw = LUMA_COEFFS[mode][:3] if mode is not None else None
+            fast = backend.try_gmsd(x4, y4, T=Tv, eps=ev, downsample=downsample, luma=lw)
         if fast is not None:
             return None, fast
         if backend_hint == "native":
             raise RuntimeError("native GMSD backend unavailable for these inputs"
                                + (" (return_map=True has no native kernel)" if return_map else ""))
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     q = _gms_map(x4, y4, wdt, Tv, ev, downsample)
     if return_map:
         return q, None

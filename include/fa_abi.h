@@ -183,6 +183,24 @@ FA_API int fa_gpu_ssim_cs_pool(const void* x, const void* y, int dtype, int N,
                                void* stream);
 
 /*
+ * No counterpart in the reference, which materialises a float32 luma plane
+ * before GMSD (functional.py:267-271) and copies crops contiguous
+ * (backend.py:346,482).  fa_gpu_gmsd over strided views, optionally of luma:
+ *   x_strides / y_strides: {image, channel, row} strides in elements (columns
+ *     are contiguous), or null for a contiguous N x C x H x W tensor;
+ *   luma: {kr, kg, kb} or null.  With luma, C must be 3 and each image is one
+ *     plane kr R + kg G + kb B, formed in float64 (an offset would cancel).
+ * psum / psumsq: [N * (luma ? 1 : C), bpp] float64 with bpp from
+ * fa_gpu_gmsd_workspace; out_mean / out_std: N float64 each.
+ */
+FA_API int fa_gpu_gmsd_ex(const void* x, const void* y, int dtype, int N, int C,
+                          int H, int W, const int64_t* x_strides,
+                          const int64_t* y_strides, const double* luma,
+                          double Tc, double eps, int downsample, double* psum,
+                          double* psumsq, int bpp, double* out_mean,
+                          double* out_std, int device, void* stream);
+
+/*
  * No counterpart in the reference.  fa_gpu_ssim_cs_backward for x / y / dx / dy
  * of element type `dtype` (FA_F32 or FA_F64, the exact pyramid levels), plus
  * the gradient of the level fa_gpu_ssim_cs_pool derived from them: gpx / gpy

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 14  # 12 reference entry points + 2 extensions
+    assert len(decl) == 15  # 12 reference entry points + 3 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -64,7 +64,7 @@ def test_workspace_queries(lib):
     assert lib.fa_gpu_ssim_workspace(64, 64, 13, ctypes.byref(out)) == 3
     assert lib.fa_gpu_ssim_workspace(64, 64, 11, None) == 5  # FA_E_ARG
     assert lib.fa_gpu_gmsd_workspace(1080, 1920, 1, ctypes.byref(out)) == 0
-    assert out.value == 4 * 9  # 538x958 output: 248-column strips, 64-row chunks
+    assert out.value == 16 * 135  # 538x958 output: 62-column strips, 4-row tiles
     assert lib.fa_gpu_gmsd_workspace(5, 5, 1, ctypes.byref(out)) == 2
 
 
@@ -85,6 +85,14 @@ def test_argument_validation_before_any_gpu_work(lib):
     assert lib.fa_gpu_ssim_backward(p, p, None, None, p, 11, 1, 1, 64, 64, 0.5, 1e-4, 9e-4,
                                     p, p, None, 0, None) == 5  # no upstream gradient
     assert lib.fa_gpu_gmsd(p, p, 0, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, 99, p, p, 0, None) == 5
+    lw = (ctypes.c_double * 3)(0.299, 0.587, 0.114)
+    assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 1, 64, 64, None, None, lw, 170.0, 0.0, 1, p, p, 99,
+                              p, p, 0, None) == 2  # luma needs 3 channels
+    bad = (ctypes.c_int64 * 3)(3 * 64 * 64, 64 * 64, 32)  # rows overlap
+    ws = ctypes.c_int(0)
+    assert lib.fa_gpu_gmsd_workspace(64, 64, 1, ctypes.byref(ws)) == 0
+    assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 3, 64, 64, bad, None, None, 170.0, 0.0, 1, p, p,
+                              ws.value, p, p, 0, None) == 2
     # the fused pyramid step insists on an exact level type
     cs = (1, 1, 1, 64, 64, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)  # float16, bpp 99
     assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, p, p, 3, 0, None) == 1  # float16 -> float32

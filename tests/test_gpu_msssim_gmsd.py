@@ -148,6 +148,65 @@ def test_gmsd_batch_channels(gpu):
     assert np.all(np.abs(got1 - s1) <= REL * np.abs(s1))
 
 
+@pytest.mark.parametrize("down", [True, False])
+@pytest.mark.parametrize("dt", [torch.uint8, torch.float16, torch.float32, torch.float64])
+@pytest.mark.parametrize("mode", ["bt601", "bt709", "matlab"])
+def test_gmsd_luma_fused(gpu, mode, dt, down):
+    """Luma formed inside the kernel (float64) against the float64 oracle's
+    luma-then-GMSD; 216 columns take the dword path for uint8 + downsampling."""
+    a, b = u8_pair((2, 3, 134, 216), 12.0, seed=21)
+    la = ref.rgb_to_luma(a.astype(np.float64), mode)
+    lb = ref.rgb_to_luma(b.astype(np.float64), mode)
+    m, s = ref.gmsd_stats(la, lb, 255.0, downsample=down)
+    x, y = torch.from_numpy(a).to(gpu, dt), torch.from_numpy(b).to(gpu, dt)
+    kw = dict(data_range=255.0, luma=mode, downsample=down, reduction="none")
+    got_s = fa.gmsd(x, y, **kw).cpu().numpy()
+    got_m = fa.gms(x, y, **kw).cpu().numpy()
+    assert np.all(np.abs(got_s - s) <= REL * np.abs(s)), (got_s, s)
+    assert np.all(np.abs(got_m - m) <= REL * np.abs(m)), (got_m, m)
+
+
+@pytest.mark.parametrize("luma", [None, "bt601"])
+@pytest.mark.parametrize("border", [3, 4, 8])
+def test_gmsd_crop_read_in_place(gpu, border, luma):
+    """Cropped views go to the kernel through their strides: border 4 / 8
+    keeps every row 4-byte aligned (dword path), border 3 does not."""
+    a, b = u8_pair((2, 3, 140, 216), 10.0, seed=border)
+    ca = ref.crop(a.astype(np.float64), border)
+    cb = ref.crop(b.astype(np.float64), border)
+    if luma:
+        ca, cb = ref.rgb_to_luma(ca, luma), ref.rgb_to_luma(cb, luma)
+    m, s = ref.gmsd_stats(ca, cb, 255.0)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    kw = dict(data_range=255.0, luma=luma, crop_border=border, reduction="none")
+    got_s = fa.gmsd(x, y, **kw).cpu().numpy()
+    got_m = fa.gms(x, y, **kw).cpu().numpy()
+    assert np.all(np.abs(got_s - s) <= REL * np.abs(s)), (got_s, s)
+    assert np.all(np.abs(got_m - m) <= REL * np.abs(m)), (got_m, m)
+
+
+def test_gmsd_channel_view_strides(gpu):
+    """A channel slice (image stride 3 planes, channel stride 1 plane)."""
+    a, b = u8_pair((3, 3, 96, 128), 14.0, seed=2)
+    m, s = ref.gmsd_stats(a[:, 1:3], b[:, 1:3], 255.0)
+    x, y = torch.from_numpy(a).to(gpu)[:, 1:3], torch.from_numpy(b).to(gpu)[:, 1:3]
+    assert not x.is_contiguous()
+    got = fa.gmsd(x, y, data_range=255.0, reduction="none").cpu().numpy()
+    assert np.all(np.abs(got - s) <= REL * np.abs(s))
+
+
+@pytest.mark.parametrize("hw", [(8, 8), (10, 260), (9, 264), (300, 516), (40, 1016), (13, 520)])
+def test_gmsd_dword_path_edges(gpu, hw):
+    """The uint8 dword path at its edges: smallest grid, one to four wave
+    strips (126 outputs each, e.g. 126 + 2), odd row counts."""
+    a, b = natural_pair(*hw, noise=9.0, seed=hw[1])
+    m, s = ref.gmsd_stats(a[None, None], b[None, None], 255.0)
+    x = torch.as_tensor(a, dtype=torch.uint8, device=gpu)[None, None]
+    y = torch.as_tensor(b, dtype=torch.uint8, device=gpu)[None, None]
+    assert _rel(float(fa.gmsd(x, y, data_range=255.0)), float(s[0])) <= REL
+    assert _rel(float(fa.gms(x, y, data_range=255.0)), float(m[0])) <= REL
+
+
 def test_gmsd_identity(gpu):
     a, _ = _plane_pair()
     x = torch.as_tensor(a, dtype=torch.uint8, device=gpu)[None, None]
