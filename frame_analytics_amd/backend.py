@@ -130,6 +130,25 @@ def _contig(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+def _view_strides(t: torch.Tensor):
+    """``(tensor, strides)``: a unit-column-stride view passes its (image,
+    channel, row) strides as an int64[3] host array; anything else is copied
+    contiguous and passes null."""
+    if t.is_contiguous():
+        return t, None
+    if t.stride(-1) != 1 or min(t.stride()) < 0:
+        return t.contiguous(), None
+    return t, (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+
+
+def _luma_arg(luma: Optional[tuple]):
+    """{kr, kg, kb, offset} as a double[4] host array, or None."""
+    if luma is None:
+        return None
+    kr, kg, kb, off = (tuple(luma) + (0.0,))[:4]
+    return (ctypes.c_double * 4)(float(kr), float(kg), float(kb), float(off))
+
+
 def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
@@ -342,37 +361,50 @@ def ssim_backward(x, y, dL_dmap, grad_scalar, win, shift, C1, C2, need_dx, need_
 
 def try_ssim(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
              shift: float, C1: float, C2: float, reduction: str,
-             return_map: bool, dtype: torch.dtype) -> Optional[torch.Tensor]:
+             return_map: bool, dtype: torch.dtype,
+             luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
     """SSIM on the GPU; ``None`` when the native path does not apply.
 
     Float64 input runs a float64 kernel.  A float64 *map* still takes the
-    portable path, because the C ABI's map buffer is float32.
+    portable path, because the C ABI's map buffer is float32.  ``luma`` =
+    (kr, kg, kb, offset) has the kernel form the luma plane of three-channel
+    input itself; cropped views are read in place (``fa_gpu_ssim_ex``).
     """
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y) or win_size not in _WINDOWS:
         return None
     if dtype == torch.float64 and (x.dtype != torch.float64 or return_map):
         return None
+    n, c = int(x.shape[0]), int(x.shape[1])
+    if luma is not None and c != 3:
+        return None
     from .functional import gaussian_window_1d
 
     win = _win_f32(gaussian_window_1d(win_size, sigma, device=x.device, dtype=torch.float32))
-    n, c = int(x.shape[0]), int(x.shape[1])
     h, w = int(x.shape[-2]), int(x.shape[-1])
     hout, wout = h - win_size + 1, w - win_size + 1
-    x, y = _contig(x), _contig(y)
+    x, xs = _view_strides(x)
+    y, ys = _view_strides(y)
+    cout = 1 if luma is not None else c
     bpp = _ssim_workspace(ext, h, w, win_size)
-    partial = _f64(x.device, n * c, bpp)
+    partial = _f64(x.device, n * cout, bpp)
     smap = per_image = total = None
     if return_map:
-        smap = torch.empty((n, c, hout, wout), device=x.device, dtype=torch.float32)
+        smap = torch.empty((n, cout, hout, wout), device=x.device, dtype=torch.float32)
     elif reduction == "none":
         per_image = _f64(x.device, n)
     else:
         total = _f64(x.device)
-    _check(ext.gpu.fa_gpu_ssim(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), win_size,
-        float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
-        _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
+    if luma is None and xs is None and ys is None:
+        _check(ext.gpu.fa_gpu_ssim(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), win_size,
+            float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
+            _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
+    else:
+        _check(ext.gpu.fa_gpu_ssim_ex(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
+            _ptr(win), win_size, float(shift), float(C1), float(C2), _ptr(smap),
+            _ptr(partial), bpp, _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
     if return_map:
         return smap if dtype == torch.float32 else smap.to(dtype)
     return per_image if reduction == "none" else total
@@ -391,31 +423,37 @@ def pyramid_dtype(dt: torch.dtype) -> torch.dtype:
     return torch.float32 if dt == torch.uint8 else torch.float64
 
 
-def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2, pool_dtype=None):
+def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2, pool_dtype=None, luma=None):
     """``(s, cs)`` plane means, plus the next pyramid level ``(px, py)`` of
-    ``pool_dtype`` when one is asked for (one fused pass)."""
+    ``pool_dtype`` when one is asked for (one fused pass).  x / y may be
+    strided views; ``luma`` = (kr, kg, kb, offset) makes each image one plane."""
     n, c, h, w = x.shape
     k = int(winf.numel())
-    planes = n * c
+    cout = 1 if luma is not None else c
+    planes = n * cout
+    x, xs = _view_strides(x)
+    y, ys = _view_strides(y)
     bpp = _ssim_workspace(ext, h, w, k)
     partial = _f64(x.device, planes, bpp)
     partial_cs = _f64(x.device, planes, bpp)
     out_s = _f64(x.device, planes)
     out_cs = _f64(x.device, planes)
-    if pool_dtype is None:
+    if pool_dtype is None and luma is None and xs is None and ys is None:
         _check(ext.gpu.fa_gpu_ssim_cs(
             _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
             float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
             bpp, _ptr(out_s), _ptr(out_cs), _dev(x), _stream(x)), ext)
         return out_s, out_cs
-    px = torch.empty((n, c, h // 2, w // 2), dtype=pool_dtype, device=x.device)
-    py = torch.empty_like(px)
-    _check(ext.gpu.fa_gpu_ssim_cs_pool(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
-        float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
-        bpp, _ptr(out_s), _ptr(out_cs), _ptr(px), _ptr(py), _DTYPE_CODE[pool_dtype],
-        _dev(x), _stream(x)), ext)
-    return out_s, out_cs, px, py
+    px = py = None
+    if pool_dtype is not None:
+        px = torch.empty((n, cout, h // 2, w // 2), dtype=pool_dtype, device=x.device)
+        py = torch.empty_like(px)
+    pcode = _DTYPE_CODE[pool_dtype if pool_dtype is not None else torch.float64]
+    _check(ext.gpu.fa_gpu_ssim_cs_ex(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
+        _ptr(winf), k, float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
+        bpp, _ptr(out_s), _ptr(out_cs), _ptr(px), _ptr(py), pcode, _dev(x), _stream(x)), ext)
+    return (out_s, out_cs) if pool_dtype is None else (out_s, out_cs, px, py)
 
 
 def ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype=None):
@@ -466,15 +504,16 @@ def ssim_cs_pool_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> b
     return (x.is_cuda and x.dim() == 4 and x.dtype in _SUPPORTED and y.dtype == x.dtype
             and x.shape == y.shape and win_size in _WINDOWS
             and x.shape[-2] >= win_size and x.shape[-1] >= win_size
+            and x.stride(-1) == 1 and y.stride(-1) == 1
             and _gpu_ext(x) is not None)
 
 
-def ssim_cs_pool(x, y, win, shift, C1, C2, pool_dtype):
+def ssim_cs_pool(x, y, win, shift, C1, C2, pool_dtype, luma=None):
     """Inference form of one MS-SSIM scale: ``(s, cs, px, py)``, or ``(s, cs)``
-    when ``pool_dtype`` is None (the coarsest scale)."""
+    when ``pool_dtype`` is None (the coarsest scale).  Views are read in place;
+    ``luma`` forms the luma plane of three-channel input in the kernel."""
     ext = load()
-    return _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2,
-                        pool_dtype)
+    return _ssim_cs_gpu(ext, x, y, _win_f32(win), shift, C1, C2, pool_dtype, luma)
 
 
 def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
@@ -494,17 +533,6 @@ def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
 # --------------------------------------------------------------------------- #
 # GMSD
 # --------------------------------------------------------------------------- #
-
-
-def _view_strides(t: torch.Tensor):
-    """``(tensor, strides)``: a unit-column-stride view passes its (image,
-    channel, row) strides as an int64[3] host array; anything else is copied
-    contiguous and passes null."""
-    if t.is_contiguous():
-        return t, None
-    if t.stride(-1) != 1 or min(t.stride()) < 0:
-        return t.contiguous(), None
-    return t, (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
 
 
 def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsample: bool,
@@ -536,7 +564,7 @@ def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsamp
             int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
             _dev(x), _stream(x)), ext)
     else:
-        lw = (ctypes.c_double * 3)(*luma) if luma is not None else None
+        lw = _luma_arg(luma)
         _check(ext.gpu.fa_gpu_gmsd_ex(
             _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, lw,
             float(T), float(eps), int(downsample), _ptr(psum), _ptr(psumsq), bpp,

@@ -103,20 +103,32 @@ struct SsimArgs {
   void* px;             // MODE_CS: optional pyramid step (2x2 means of x / y)
   void* py;
   int pool_f64;         // pyramid element type: float64 (1) or float32 (0)
+  // input views (forward modes): element strides of image and channel, row
+  // stride; columns are contiguous.  Planes are (image, output channel).
+  int64_t xsn, xsc, ysn, ysc;
+  int xsh, ysh;
+  int Cout;             // output planes per image (1 with luma)
+  double kr, kg, kb;    // luma weights
+  double offset;        // luma offset: added to every sample the kernel forms
 };
 
-template <typename T, typename CTy, int MODE>
+template <typename T, typename CTy, int MODE, bool LUMA = false>
 struct SsimPol {
   static constexpr int NP = 4;
+  static constexpr int CH = LUMA ? 3 : 1;
   using CT = CTy;
   struct Raw {
     CT x, y;
   };
 
-  const T* __restrict__ x;  // this plane of x
-  const T* __restrict__ y;  // this plane of y
+  const T* __restrict__ x[CH];  // this plane of x (the R, G, B planes with luma)
+  const T* __restrict__ y[CH];
   int H, W;
+  uint32_t shx, shy;        // row strides
   uint32_t lcol;            // this lane's column, clamped into the image
+  CT kr, kg, kb;            // luma weights
+  CT cshift;                // shift - offset: centres the samples as loaded
+  double poff;              // offset, added to the pyramid means
   CT shift, C1, C2;
   int64_t out_off;
   int Wout;
@@ -147,13 +159,20 @@ struct SsimPol {
     lcol = static_cast<uint32_t>(col < W ? col : W - 1);
   }
 
+  __device__ inline CT elem(const T* p, uint32_t o) const {
+    if constexpr (sizeof(CT) == 8) return Elem<T>::d(p[o]);
+    else return Elem<T>::f(p[o]);
+  }
+
   __device__ inline Raw load(int row) const {
-    // a plane holds < 2^31 elements (checked on the host): 32-bit offsets
-    const uint32_t o = static_cast<uint32_t>(row < H ? row : H - 1) * static_cast<uint32_t>(W) + lcol;
-    if constexpr (sizeof(CT) == 8)
-      return Raw{Elem<T>::d(x[o]), Elem<T>::d(y[o])};
+    // a plane spans < 2^31 elements (checked on the host): 32-bit offsets
+    const uint32_t r = static_cast<uint32_t>(row < H ? row : H - 1);
+    const uint32_t ox = r * shx + lcol, oy = r * shy + lcol;
+    if constexpr (LUMA)
+      return Raw{fma(kb, elem(x[2], ox), fma(kg, elem(x[1], ox), kr * elem(x[0], ox))),
+                 fma(kb, elem(y[2], oy), fma(kg, elem(y[1], oy), kr * elem(y[0], oy)))};
     else
-      return Raw{Elem<T>::f(x[o]), Elem<T>::f(y[o])};
+      return Raw{elem(x[0], ox), elem(y[0], oy)};
   }
 
   // The 2x2 mean of rows (2i, 2i+1) and columns (2j, 2j+1), formed in float64
@@ -175,19 +194,19 @@ struct SsimPol {
       if (pcol_ok) {
         const int64_t o = pool_off + static_cast<int64_t>(row >> 1) * Wd + pcol;
         if (pool_f64) {
-          static_cast<double*>(px)[o] = 0.25 * sx;
-          static_cast<double*>(py)[o] = 0.25 * sy;
+          static_cast<double*>(px)[o] = fma(0.25, sx, poff);
+          static_cast<double*>(py)[o] = fma(0.25, sy, poff);
         } else {
-          static_cast<float*>(px)[o] = static_cast<float>(0.25 * sx);
-          static_cast<float*>(py)[o] = static_cast<float>(0.25 * sy);
+          static_cast<float*>(px)[o] = static_cast<float>(fma(0.25, sx, poff));
+          static_cast<float*>(py)[o] = static_cast<float>(fma(0.25, sy, poff));
         }
       }
     }
   }
 
   __device__ inline void moments(const Raw& r, CT* m) const {
-    const CT xs = r.x - shift;
-    const CT ys = r.y - shift;
+    const CT xs = r.x - cshift;
+    const CT ys = r.y - cshift;
     const CT d = xs - ys;
     m[0] = xs;
     m[1] = ys;
@@ -266,7 +285,7 @@ struct SsimPol {
 #define FA_SSIM_ATTR
 #endif
 
-template <typename T, typename CT, int MODE, int KW>
+template <typename T, typename CT, int MODE, int KW, bool LUMA = false>
 __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   __shared__ CT sbuf[2][PH][4][HROW];
   __shared__ double sred[2 * WAVES_PER_BLOCK];
@@ -277,13 +296,28 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   const int chunk = tile / a.strips;
   const int strip = tile - chunk * a.strips;
 
-  SsimPol<T, CT, MODE> pol;
-  const int64_t in_off = static_cast<int64_t>(plane) * a.H * a.W;
-  pol.x = static_cast<const T*>(a.x) + in_off;
-  pol.y = static_cast<const T*>(a.y) + in_off;
+  using Pol = SsimPol<T, CT, MODE, LUMA>;
+  Pol pol;
+  {
+    const int n = plane / a.Cout;
+    const int c = plane - n * a.Cout;
+#pragma unroll
+    for (int ch = 0; ch < Pol::CH; ++ch) {
+      const int cc = LUMA ? ch : c;
+      pol.x[ch] = static_cast<const T*>(a.x) + n * a.xsn + cc * a.xsc;
+      pol.y[ch] = static_cast<const T*>(a.y) + n * a.ysn + cc * a.ysc;
+    }
+  }
   pol.H = a.H;
   pol.W = a.W;
+  pol.shx = static_cast<uint32_t>(a.xsh);
+  pol.shy = static_cast<uint32_t>(a.ysh);
+  pol.kr = static_cast<CT>(a.kr);
+  pol.kg = static_cast<CT>(a.kg);
+  pol.kb = static_cast<CT>(a.kb);
   pol.shift = static_cast<CT>(a.shift);
+  pol.cshift = static_cast<CT>(a.shift - a.offset);
+  pol.poff = a.offset;
   pol.C1 = static_cast<CT>(a.C1);
   pol.C2 = static_cast<CT>(a.C2);
   pol.out_off = static_cast<int64_t>(plane) * a.Hout * a.Wout;
@@ -338,8 +372,7 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
     }
   }
 
-  strip_engine<SsimPol<T, CT, MODE>, KW>(pol, a.win, 0, a.Hout, a.Wout, a.TH, strip,
-                                         chunk, sbuf);
+  strip_engine<Pol, KW>(pol, a.win, 0, a.Hout, a.Wout, a.TH, strip, chunk, sbuf);
 
   const int64_t slot = static_cast<int64_t>(plane) * a.bpp + tile;
   if constexpr (MODE == MODE_REDUCE || MODE == MODE_MAP) {
@@ -543,37 +576,45 @@ static int launch_strips(void (*kern)(Args), int occ, Args& a, int64_t planes, i
   return FA_OK;
 }
 
-template <typename T, typename CT, int MODE, int KW>
+template <typename T, typename CT, int MODE, int KW, bool LUMA>
 static int launch_ssim_kw(SsimArgs& a, int64_t planes, int device, hipStream_t st) {
   static const int occ =
-      occupancy_wgs(reinterpret_cast<const void*>(&ssim_kernel<T, CT, MODE, KW>));
-  return launch_strips(ssim_kernel<T, CT, MODE, KW>, occ, a, planes, a.Hout, a.Wout, KW,
-                       device, st);
+      occupancy_wgs(reinterpret_cast<const void*>(&ssim_kernel<T, CT, MODE, KW, LUMA>));
+  return launch_strips(ssim_kernel<T, CT, MODE, KW, LUMA>, occ, a, planes, a.Hout, a.Wout,
+                       KW, device, st);
 }
 
-template <typename T, typename CT, int MODE>
+template <typename T, typename CT, int MODE, bool LUMA = false>
 static int launch_ssim_k(int K, SsimArgs& a, int64_t planes, int device, hipStream_t st) {
   switch (K) {
-    case 3: return launch_ssim_kw<T, CT, MODE, 3>(a, planes, device, st);
-    case 5: return launch_ssim_kw<T, CT, MODE, 5>(a, planes, device, st);
-    case 7: return launch_ssim_kw<T, CT, MODE, 7>(a, planes, device, st);
-    case 9: return launch_ssim_kw<T, CT, MODE, 9>(a, planes, device, st);
-    case 11: return launch_ssim_kw<T, CT, MODE, 11>(a, planes, device, st);
+    case 3: return launch_ssim_kw<T, CT, MODE, 3, LUMA>(a, planes, device, st);
+    case 5: return launch_ssim_kw<T, CT, MODE, 5, LUMA>(a, planes, device, st);
+    case 7: return launch_ssim_kw<T, CT, MODE, 7, LUMA>(a, planes, device, st);
+    case 9: return launch_ssim_kw<T, CT, MODE, 9, LUMA>(a, planes, device, st);
+    case 11: return launch_ssim_kw<T, CT, MODE, 11, LUMA>(a, planes, device, st);
     default: return FA_E_WINDOW;
   }
 }
 
-template <int MODE>
-static int launch_ssim(int dtype, int K, SsimArgs& a, int64_t planes, int device,
-                       hipStream_t st) {
+template <int MODE, bool LUMA>
+static int launch_ssim_t(int dtype, int K, SsimArgs& a, int64_t planes, int device,
+                         hipStream_t st) {
   switch (dtype) {
-    case FA_U8: return launch_ssim_k<uint8_t, float, MODE>(K, a, planes, device, st);
-    case FA_F16: return launch_ssim_k<half_t, float, MODE>(K, a, planes, device, st);
-    case FA_BF16: return launch_ssim_k<bf16_t, float, MODE>(K, a, planes, device, st);
-    case FA_F32: return launch_ssim_k<float, float, MODE>(K, a, planes, device, st);
-    case FA_F64: return launch_ssim_k<double, double, MODE>(K, a, planes, device, st);
+    case FA_U8: return launch_ssim_k<uint8_t, float, MODE, LUMA>(K, a, planes, device, st);
+    case FA_F16: return launch_ssim_k<half_t, float, MODE, LUMA>(K, a, planes, device, st);
+    case FA_BF16: return launch_ssim_k<bf16_t, float, MODE, LUMA>(K, a, planes, device, st);
+    case FA_F32: return launch_ssim_k<float, float, MODE, LUMA>(K, a, planes, device, st);
+    case FA_F64: return launch_ssim_k<double, double, MODE, LUMA>(K, a, planes, device, st);
     default: return FA_E_DTYPE;
   }
+}
+
+// Forward launches: with luma (a.Cout == 1 over three input channels) or not.
+template <int MODE>
+static int launch_ssim(int dtype, int K, bool luma, SsimArgs& a, int64_t planes, int device,
+                       hipStream_t st) {
+  return luma ? launch_ssim_t<MODE, true>(dtype, K, a, planes, device, st)
+              : launch_ssim_t<MODE, false>(dtype, K, a, planes, device, st);
 }
 
 template <typename T, int KW, bool DY>
@@ -606,6 +647,36 @@ static int ssim_shape(int N, int C, int H, int W, int K, int* Hout, int* Wout) {
   return FA_OK;
 }
 
+// Fills the input views of `a` (null strides: contiguous N x C x H x W) and
+// the luma transform {kr, kg, kb, offset} (null: none; otherwise C must be 3
+// and each image is one plane).  Row offsets within a plane stay 32-bit.
+static int set_views(SsimArgs& a, int C, int H, int W, const int64_t* xs, const int64_t* ys,
+                     const double* luma) {
+  const int64_t plane = static_cast<int64_t>(H) * W;
+  const int64_t vx[3] = {xs ? xs[0] : plane * C, xs ? xs[1] : plane, xs ? xs[2] : W};
+  const int64_t vy[3] = {ys ? ys[0] : plane * C, ys ? ys[1] : plane, ys ? ys[2] : W};
+  for (int i = 0; i < 3; ++i)
+    if (vx[i] < 0 || vy[i] < 0) return FA_E_SHAPE;
+  // rows may not overlap, and a plane's last element must be 32-bit addressable
+  if (vx[2] < W || vy[2] < W) return FA_E_SHAPE;
+  if ((H - 1) * vx[2] + W > INT32_MAX || (H - 1) * vy[2] + W > INT32_MAX) return FA_E_SHAPE;
+  if (luma && C != 3) return FA_E_SHAPE;
+  a.xsn = vx[0];
+  a.xsc = vx[1];
+  a.xsh = static_cast<int>(vx[2]);
+  a.ysn = vy[0];
+  a.ysc = vy[1];
+  a.ysh = static_cast<int>(vy[2]);
+  a.Cout = luma ? 1 : C;
+  if (luma) {
+    a.kr = luma[0];
+    a.kg = luma[1];
+    a.kb = luma[2];
+    a.offset = luma[3];
+  }
+  return FA_OK;
+}
+
 // The coefficient pass plus the scatter, shared by the backward entry points.
 // T is the element type of x, y, dx and dy (float, or double for the float64
 // MS-SSIM pyramid levels); the arithmetic is float64 either way.
@@ -631,6 +702,8 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
   a.W = W;
   a.Hout = Hout;
   a.Wout = Wout;
+  rc = set_views(a, C, H, W, nullptr, nullptr, nullptr);
+  if (rc != FA_OK) return rc;
   a.shift = shift;
   a.C1 = C1;
   a.C2 = C2;
@@ -670,22 +743,27 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
             : launch_scatter_k<T, false>(K, s, planes, device, st);
 }
 
-// fa_gpu_ssim_cs, optionally writing the next pyramid level (px / py non-null).
+// fa_gpu_ssim_cs over views, with optional luma and, when px / py are not
+// null, the next pyramid level.
 static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, int H, int W,
+                        const int64_t* xs, const int64_t* ys, const double* luma,
                         const float* win, int K, double shift, double C1, double C2,
                         double* partial, double* partial_cs, int bpp, double* out_s,
                         double* out_cs, void* px, void* py, int pool_dtype, int device,
                         void* stream) {
   if (!x || !y || !win || !partial || !partial_cs || !out_s || !out_cs) return FA_E_ARG;
+  if ((px == nullptr) != (py == nullptr)) return FA_E_ARG;
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
   if (rc != FA_OK) return rc;
   if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
-  const int64_t planes = static_cast<int64_t>(N) * C;
+  SsimArgs a = {};
+  rc = set_views(a, C, H, W, xs, ys, luma);
+  if (rc != FA_OK) return rc;
+  const int64_t planes = static_cast<int64_t>(N) * a.Cout;
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  SsimArgs a = {};
   a.x = x;
   a.y = y;
   a.H = H;
@@ -701,13 +779,56 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   a.px = px;
   a.py = py;
   a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
-  rc = launch_ssim<MODE_CS>(dtype, K, a, planes, device, st);
+  rc = launch_ssim<MODE_CS>(dtype, K, luma != nullptr, a, planes, device, st);
   if (rc != FA_OK) return rc;
   hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
                      partial, partial_cs, a.bpp, static_cast<double>(Hout) * Wout, out_s,
                      out_cs);
   FA_LAUNCH_CHECK();
   return FA_OK;
+}
+
+// fa_gpu_ssim over views, with optional luma.
+static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int H, int W,
+                     const int64_t* xs, const int64_t* ys, const double* luma,
+                     const float* win, int K, double shift, double C1, double C2,
+                     float* map_out, double* partial, int bpp, double* out_per_image,
+                     double* out_total, int device, void* stream) {
+  if (!x || !y || !win || !partial) return FA_E_ARG;
+  int Hout = 0, Wout = 0;
+  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
+  SsimArgs a = {};
+  rc = set_views(a, C, H, W, xs, ys, luma);
+  if (rc != FA_OK) return rc;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  a.x = x;
+  a.y = y;
+  a.H = H;
+  a.W = W;
+  a.Hout = Hout;
+  a.Wout = Wout;
+  a.shift = shift;
+  a.C1 = C1;
+  a.C2 = C2;
+  a.win = win;
+  a.map = map_out;
+  a.partial = partial;
+  const int Cout = a.Cout;
+  const int64_t planes = static_cast<int64_t>(N) * Cout;
+  const bool lm = luma != nullptr;
+  rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, lm, a, planes, device, st)
+               : launch_ssim<MODE_REDUCE>(dtype, K, lm, a, planes, device, st);
+  if (rc != FA_OK) return rc;
+
+  // each image owns Cout * tiles consecutive slots of `partial`
+  const double npix = static_cast<double>(Hout) * Wout;
+  return launch_finalize(partial, false, N, Cout * a.bpp, npix * Cout,
+                         npix * Cout * static_cast<double>(N), FA_PSNR_NONE,
+                         out_per_image, out_total, nullptr, nullptr, st);
 }
 
 }  // namespace fa
@@ -732,37 +853,20 @@ FA_API int fa_gpu_ssim(const void* x, const void* y, int dtype, int N, int C,
                        double C1, double C2, float* map_out, double* partial,
                        int bpp, double* out_per_image, double* out_total,
                        int device, void* stream) {
-  if (!x || !y || !win || !partial) return FA_E_ARG;
-  int Hout = 0, Wout = 0;
-  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
-  if (rc != FA_OK) return rc;
-  if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
-  FA_DEVICE_SCOPE(device);
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  return ssim_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, win, K, shift, C1, C2,
+                   map_out, partial, bpp, out_per_image, out_total, device, stream);
+}
 
-  SsimArgs a = {};
-  a.x = x;
-  a.y = y;
-  a.H = H;
-  a.W = W;
-  a.Hout = Hout;
-  a.Wout = Wout;
-  a.shift = shift;
-  a.C1 = C1;
-  a.C2 = C2;
-  a.win = win;
-  a.map = map_out;
-  a.partial = partial;
-  const int64_t planes = static_cast<int64_t>(N) * C;
-  rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, a, planes, device, st)
-               : launch_ssim<MODE_REDUCE>(dtype, K, a, planes, device, st);
-  if (rc != FA_OK) return rc;
-
-  // each image owns C * tiles consecutive slots of `partial`
-  const double npix = static_cast<double>(Hout) * Wout;
-  return launch_finalize(partial, false, N, C * a.bpp, npix * C,
-                         npix * C * static_cast<double>(N), FA_PSNR_NONE,
-                         out_per_image, out_total, nullptr, nullptr, st);
+// No counterpart in the reference, which materialises a float32 luma plane
+// (functional.py:267-271) and copies crops contiguous (backend.py:346,482).
+FA_API int fa_gpu_ssim_ex(const void* x, const void* y, int dtype, int N, int C, int H,
+                          int W, const int64_t* x_strides, const int64_t* y_strides,
+                          const double* luma, const float* win, int K, double shift,
+                          double C1, double C2, float* map_out, double* partial, int bpp,
+                          double* out_per_image, double* out_total, int device,
+                          void* stream) {
+  return ssim_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, win, K, shift, C1, C2,
+                   map_out, partial, bpp, out_per_image, out_total, device, stream);
 }
 
 // reference: fa_cuda.cu:1235-1283 (fa_cuda_ssim_cs)
@@ -771,26 +875,30 @@ FA_API int fa_gpu_ssim_cs(const void* x, const void* y, int dtype, int N,
                           double shift, double C1, double C2, double* partial,
                           double* partial_cs, int bpp, double* out_s,
                           double* out_cs, int device, void* stream) {
-  return ssim_cs_impl(x, y, dtype, N, C, H, W, win, K, shift, C1, C2, partial, partial_cs,
-                      bpp, out_s, out_cs, nullptr, nullptr, FA_F64, device, stream);
+  return ssim_cs_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, win, K, shift, C1,
+                      C2, partial, partial_cs, bpp, out_s, out_cs, nullptr, nullptr, FA_F64,
+                      device, stream);
 }
 
-// No counterpart in the reference (it pools between scales with torch,
-// functional.py:876-885).  fa_gpu_ssim_cs plus the next pyramid level, fused.
-FA_API int fa_gpu_ssim_cs_pool(const void* x, const void* y, int dtype, int N,
-                               int C, int H, int W, const float* win, int K,
-                               double shift, double C1, double C2, double* partial,
-                               double* partial_cs, int bpp, double* out_s,
-                               double* out_cs, void* px, void* py, int pool_dtype,
-                               int device, void* stream) {
-  if (!px || !py) return FA_E_ARG;
-  // float32 levels hold the pyramid of uint8 input exactly; every other
-  // input pools into float64
-  const bool ok = pool_dtype == FA_F64 ||
-                  (pool_dtype == FA_F32 && (dtype == FA_U8 || dtype == FA_F32));
-  if (!ok) return FA_E_DTYPE;
-  return ssim_cs_impl(x, y, dtype, N, C, H, W, win, K, shift, C1, C2, partial, partial_cs,
-                      bpp, out_s, out_cs, px, py, pool_dtype, device, stream);
+// No counterpart in the reference (it pools between MS-SSIM scales with torch,
+// functional.py:876-885, and materialises luma planes and crops).
+// fa_gpu_ssim_cs over views with optional luma, plus the next pyramid level.
+FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N, int C, int H,
+                             int W, const int64_t* x_strides, const int64_t* y_strides,
+                             const double* luma, const float* win, int K, double shift,
+                             double C1, double C2, double* partial, double* partial_cs,
+                             int bpp, double* out_s, double* out_cs, void* px, void* py,
+                             int pool_dtype, int device, void* stream) {
+  if (px) {
+    // float32 levels hold the pyramid of uint8 input exactly, float64 levels
+    // that of every floating input; a luma plane pools into float64
+    const bool ok = pool_dtype == FA_F64 ||
+                    (pool_dtype == FA_F32 && !luma && (dtype == FA_U8 || dtype == FA_F32));
+    if (!ok) return FA_E_DTYPE;
+  }
+  return ssim_cs_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, win, K, shift, C1,
+                      C2, partial, partial_cs, bpp, out_s, out_cs, px, py, pool_dtype, device,
+                      stream);
 }
 
 // reference: fa_cuda.cu:1299-1353 (fa_cuda_ssim_backward)
@@ -829,7 +937,7 @@ FA_API int fa_gpu_ssim_cs_backward(const float* x, const float* y,
 // No counterpart in the reference (its MS-SSIM pyramid is float32 and pooled
 // by torch).  The fa_gpu_ssim_cs_backward contract for x / y / dx / dy of
 // `dtype` FA_F32 or FA_F64 (the exact pyramid levels), plus the gradient of
-// the next level that fa_gpu_ssim_cs_pool wrote: gpx / gpy (either may be
+// the next level that fa_gpu_ssim_cs_ex wrote: gpx / gpy (either may be
 // null) of `gp_dtype` FA_F32 or FA_F64, floor(H/2) x floor(W/2) per plane,
 // spread as 1/4 over each 2x2 block into dx / dy.  aux stays float32.
 FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,

@@ -140,6 +140,12 @@ def _prep(x, y, luma, crop_border: int, data_range: Optional[float]):
     return _crop_border(x4, crop_border), _crop_border(y4, crop_border), L, mode
 
 
+def _luma_tuple(mode, L):
+    """(kr, kg, kb, offset in data units) of a luma convention, for the kernels."""
+    kr, kg, kb, off = LUMA_COEFFS[mode]
+    return (kr, kg, kb, off * L)
+
+
 def _apply_luma(x4, y4, mode, L, dtype):
     if mode is None:
         return x4, y4
@@ -341,9 +347,23 @@ def ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None
     _check_reduction(reduction)
     x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
     wdt = _work_dtype(x4, dtype)
-    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     C1 = (float(K[0]) * L) ** 2
     C2 = (float(K[1]) * L) ** 2
+    from . import backend
+
+    # Inference on the GPU: the kernel forms the luma plane and reads crops in
+    # place, so neither is materialised first.
+    grad = torch.is_grad_enabled() and (x4.requires_grad or y4.requires_grad)
+    if (backend_hint != "torch" and not grad and not downsample and mode is not None
+            and x4.shape[-2] >= win_size and x4.shape[-1] >= win_size):
+        if x4.shape[1] != 3:
+            raise ValueError(f"luma needs a 3-channel image, got {x4.shape[1]} channels")
+        fast = backend.try_ssim(x4, y4, win_size=win_size, sigma=sigma, shift=0.5 * L,
+                                C1=C1, C2=C2, reduction=reduction, return_map=return_map,
+                                dtype=wdt, luma=_luma_tuple(mode, L))
+        if fast is not None:
+            return fast
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     if downsample:
         f = max(1, int(round(min(x4.shape[-2], x4.shape[-1]) / 256.0)))
         if f > 1:
@@ -352,7 +372,6 @@ def ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None
     if x4.shape[-2] < win_size or x4.shape[-1] < win_size:
         raise ValueError(f"image {tuple(x4.shape[-2:])} smaller than window {win_size}x{win_size}")
     shift = 0.5 * L
-    from . import backend
 
     if (backend_hint != "torch" and (x4.requires_grad or y4.requires_grad)
             and torch.is_grad_enabled() and reduction == "mean" and not downsample
@@ -433,7 +452,7 @@ class _FusedSSIMCS(torch.autograd.Function):
 class _FusedSSIMCSPool(torch.autograd.Function):
     """One differentiable native MS-SSIM scale: the ``(ssim, cs)`` plane means
     and the next pyramid level ``(px, py)`` from one pass over x and y
-    (``fa_gpu_ssim_cs_pool``).  The backward spreads a quarter of the level's
+    (``fa_gpu_ssim_cs_ex``).  The backward spreads a quarter of the level's
     gradient over each 2x2 block inside the scatter of the (ssim, cs) gradient
     (``fa_gpu_ssim_cs_backward_ex``), so a scale costs one forward and two
     backward launches whatever reaches it."""
@@ -507,7 +526,6 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
         raise ValueError("weights must not be empty")
     x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
     wdt = _work_dtype(x4, dtype)
-    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     C1 = (float(K[0]) * L) ** 2
     C2 = (float(K[1]) * L) ** 2
     shift = 0.5 * L
@@ -521,12 +539,22 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
     from . import backend
 
     win = gaussian_window_1d(win_size, sigma, device=x4.device, dtype=wdt)
-    n, c = x4.shape[0], x4.shape[1]
     terms = []
     grad = torch.is_grad_enabled() and (x4.requires_grad or y4.requires_grad)
     native = (backend_hint != "torch"
               and backend.ssim_cs_pool_available(x4, y4, win_size)
               and not (grad and torch.cuda.is_current_stream_capturing()))
+    # without a gradient the first scale forms the luma plane itself (its
+    # pyramid is float64); with one, luma is an autograd op in front
+    lw = None
+    if mode is not None:
+        if x4.shape[1] != 3:
+            raise ValueError(f"luma needs a 3-channel image, got {x4.shape[1]} channels")
+        if native and not grad:
+            lw = _luma_tuple(mode, L)
+        else:
+            x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    n, c = x4.shape[0], (1 if lw is not None else x4.shape[1])
     if native:
         # On the GPU every scale is one fused pass that also writes the next
         # pyramid level, held exactly (the coarse scales amplify a rounded
@@ -537,7 +565,7 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
             x4, y4 = x4.double(), y4.double()
         elif grad and x4.dtype in (torch.float16, torch.bfloat16):
             x4, y4 = x4.float(), y4.float()
-        pdt = backend.pyramid_dtype(x4.dtype)
+        pdt = torch.float64 if lw is not None else backend.pyramid_dtype(x4.dtype)
         cx, cy = x4, y4
         for i in range(scales):
             last = i == scales - 1
@@ -547,7 +575,8 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
                 else:
                     s, cs, cx, cy = _FusedSSIMCSPool.apply(cx, cy, win, shift, C1, C2, pdt)
             else:
-                out = backend.ssim_cs_pool(cx, cy, win, shift, C1, C2, None if last else pdt)
+                out = backend.ssim_cs_pool(cx, cy, win, shift, C1, C2, None if last else pdt,
+                                           luma=lw if i == 0 else None)
                 s, cs = out[0], out[1]
                 if not last:
                     cx, cy = out[2], out[3]

@@ -165,22 +165,45 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
 /* ------------------------------------------------------------------------ */
 
 /*
- * No counterpart in the reference, which pools its MS-SSIM pyramid with torch
- * between scales (reference functional.py:876-885).  fa_gpu_ssim_cs plus the
- * next pyramid level of x and y, written by the same pass: non-overlapping 2x2
- * mean, odd trailing row / column dropped.  px / py: N*C*(H/2)*(W/2) elements
- * of pool_dtype, which is FA_F64, or FA_F32 for uint8 and float32 input.  The
- * means are formed in float64, so the levels of a uint8 pyramid are exact in
- * float32 and those of float16 / bfloat16 / float32 exact in float64 (unless a
- * 2x2 block spans more than 2^29 / 2^45 in magnitude; then correctly rounded).
+ * No counterpart in the reference, which materialises a float32 luma plane
+ * (functional.py:267-271) and copies crops contiguous (backend.py:346,482).
+ * fa_gpu_ssim over strided views, optionally of luma:
+ *   x_strides / y_strides: {image, channel, row} strides in elements (columns
+ *     are contiguous), or null for a contiguous N x C x H x W tensor; a plane
+ *     must span fewer than 2^31 elements;
+ *   luma: {kr, kg, kb, offset} or null.  With luma, C must be 3 and each
+ *     image is one plane kr R + kg G + kb B + offset (offset in data units).
+ * map_out / partial / outputs as fa_gpu_ssim with N * (luma ? 1 : C) planes.
  */
-FA_API int fa_gpu_ssim_cs_pool(const void* x, const void* y, int dtype, int N,
-                               int C, int H, int W, const float* win, int K,
-                               double shift, double C1, double C2,
-                               double* partial, double* partial_cs, int bpp,
-                               double* out_s, double* out_cs, void* px,
-                               void* py, int pool_dtype, int device,
-                               void* stream);
+FA_API int fa_gpu_ssim_ex(const void* x, const void* y, int dtype, int N, int C,
+                          int H, int W, const int64_t* x_strides,
+                          const int64_t* y_strides, const double* luma,
+                          const float* win, int K, double shift, double C1,
+                          double C2, float* map_out, double* partial, int bpp,
+                          double* out_per_image, double* out_total, int device,
+                          void* stream);
+
+/*
+ * No counterpart in the reference, which pools its MS-SSIM pyramid with torch
+ * between scales (reference functional.py:876-885).  fa_gpu_ssim_cs over
+ * views with optional luma (as fa_gpu_ssim_ex), plus, when px / py are not
+ * null, the next pyramid level of x and y written by the same pass:
+ * non-overlapping 2x2 mean (of the luma plane, offset included, with luma),
+ * odd trailing row / column dropped.  px / py:
+ * N * Cout * (H/2) * (W/2) elements of pool_dtype, which is FA_F64, or FA_F32
+ * for uint8 and float32 input without luma.  The means are formed in float64,
+ * so the levels of a uint8 pyramid are exact in float32 and those of float16 /
+ * bfloat16 / float32 exact in float64 (unless a 2x2 block spans more than
+ * 2^29 / 2^45 in magnitude; then correctly rounded).
+ */
+FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N,
+                             int C, int H, int W, const int64_t* x_strides,
+                             const int64_t* y_strides, const double* luma,
+                             const float* win, int K, double shift, double C1,
+                             double C2, double* partial, double* partial_cs,
+                             int bpp, double* out_s, double* out_cs, void* px,
+                             void* py, int pool_dtype, int device,
+                             void* stream);
 
 /*
  * No counterpart in the reference, which materialises a float32 luma plane
@@ -188,8 +211,9 @@ FA_API int fa_gpu_ssim_cs_pool(const void* x, const void* y, int dtype, int N,
  * (backend.py:346,482).  fa_gpu_gmsd over strided views, optionally of luma:
  *   x_strides / y_strides: {image, channel, row} strides in elements (columns
  *     are contiguous), or null for a contiguous N x C x H x W tensor;
- *   luma: {kr, kg, kb} or null.  With luma, C must be 3 and each image is one
- *     plane kr R + kg G + kb B, formed in float64 (an offset would cancel).
+ *   luma: {kr, kg, kb, offset} or null.  With luma, C must be 3 and each
+ *     image is one plane kr R + kg G + kb B, formed in float64 (the offset
+ *     cancels out of every gradient and is not read).
  * psum / psumsq: [N * (luma ? 1 : C), bpp] float64 with bpp from
  * fa_gpu_gmsd_workspace; out_mean / out_std: N float64 each.
  */
@@ -203,7 +227,7 @@ FA_API int fa_gpu_gmsd_ex(const void* x, const void* y, int dtype, int N, int C,
 /*
  * No counterpart in the reference.  fa_gpu_ssim_cs_backward for x / y / dx / dy
  * of element type `dtype` (FA_F32 or FA_F64, the exact pyramid levels), plus
- * the gradient of the level fa_gpu_ssim_cs_pool derived from them: gpx / gpy
+ * the gradient of the level fa_gpu_ssim_cs_ex derived from them: gpx / gpy
  * (either may be null), (H/2) x (W/2) per plane of gp_dtype (FA_F32 or
  * FA_F64), each value spread as 1/4 over its 2x2 block of dx / dy.  aux stays
  * float32 with the same size as in fa_gpu_ssim_cs_backward.

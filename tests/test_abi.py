@@ -36,7 +36,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 15  # 12 reference entry points + 3 extensions
+    assert len(decl) == 16  # 12 reference entry points + 4 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -94,13 +94,25 @@ def test_argument_validation_before_any_gpu_work(lib):
     assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 3, 64, 64, bad, None, None, 170.0, 0.0, 1, p, p,
                               ws.value, p, p, 0, None) == 2
     # the fused pyramid step insists on an exact level type
-    cs = (1, 1, 1, 64, 64, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)  # float16, bpp 99
-    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, p, p, 3, 0, None) == 1  # float16 -> float32
-    assert lib.fa_gpu_ssim_cs_pool(p, p, 2, *cs[1:], p, p, 3, 0, None) == 1  # bfloat16
-    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, p, p, 0, 0, None) == 1  # uint8 levels
-    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, None, p, 4, 0, None) == 5  # no level buffer
-    assert lib.fa_gpu_ssim_cs_pool(p, p, *cs, p, p, 4, 0, None) == 5  # bpp mismatch
-    assert lib.fa_gpu_ssim_cs_pool(p, p, 0, *cs[1:], p, p, 3, 0, None) == 5  # u8 -> f32 ok
+    cs = (1, 1, 1, 64, 64, None, None, None, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)  # f16
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, p, p, 3, 0, None) == 1  # float16 -> float32
+    assert lib.fa_gpu_ssim_cs_ex(p, p, 2, *cs[1:], p, p, 3, 0, None) == 1  # bfloat16
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, p, p, 0, 0, None) == 1  # uint8 levels
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, None, p, 4, 0, None) == 5  # one level buffer
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, p, p, 4, 0, None) == 5  # bpp mismatch
+    assert lib.fa_gpu_ssim_cs_ex(p, p, 0, *cs[1:], p, p, 3, 0, None) == 5  # u8 -> f32 ok
+    lw = (ctypes.c_double * 4)(0.299, 0.587, 0.114, 0.0)
+    u8l = (0, 1, 3, 64, 64, None, None, lw, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *u8l, p, p, 3, 0, None) == 1  # luma pools to f64
+    ws = ctypes.c_int(0)
+    assert lib.fa_gpu_ssim_workspace(64, 64, 11, ctypes.byref(ws)) == 0
+    one = u8l[:2] + (1,) + u8l[3:15] + (ws.value,) + u8l[16:]
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *one, None, None, 4, 0, None) == 2  # luma needs 3 channels
+    rows = (ctypes.c_int64 * 3)(3 * 64 * 64, 64 * 64, 60)  # rows overlap
+    assert lib.fa_gpu_ssim_ex(p, p, 0, 1, 3, 64, 64, rows, None, None, p, 11, 0.5, 1e-4, 9e-4,
+                              None, p, 99, None, None, 0, None) == 5  # bpp checked first
+    assert lib.fa_gpu_ssim_ex(p, p, 0, 1, 3, 64, 64, rows, None, None, p, 11, 0.5, 1e-4, 9e-4,
+                              None, p, ws.value, None, None, 0, None) == 2
     assert lib.fa_gpu_ssim_cs_backward_ex(p, p, 0, p, p, p, 11, 1, 1, 64, 64, 0.5, 1e-4,
                                           9e-4, None, None, 0, p, p, None, 0,
                                           None) == 1  # uint8 input

@@ -131,6 +131,44 @@ def test_luma_and_crop(gpu):
         assert abs(float(fa.ssim(ta, tb, data_range=255.0, crop_border=cb)) - manual) < 1e-12
 
 
+@pytest.mark.parametrize("dt", [torch.uint8, torch.float16, torch.float32, torch.float64])
+@pytest.mark.parametrize("mode", ["bt601", "bt709", "matlab"])
+def test_luma_formed_in_kernel(gpu, mode, dt):
+    """The kernel forms kr R + kg G + kb B + offset itself (fa_gpu_ssim_ex):
+    per-image values and the map against the float64 oracle on luma planes."""
+    rng = np.random.default_rng(5)
+    a = rng.integers(0, 256, (2, 3, 97, 131)).astype(np.float64)
+    b = np.clip(a + 11.0 * rng.standard_normal(a.shape), 0, 255).round()
+    la, lb = ref.rgb_to_luma(a, mode), ref.rgb_to_luma(b, mode)
+    x, y = torch.from_numpy(a).to(gpu, dt), torch.from_numpy(b).to(gpu, dt)
+    want = ref.ssim(la, lb, 255.0, reduction="none")
+    got = fa.ssim(x, y, data_range=255.0, luma=mode, reduction="none").cpu().numpy()
+    assert np.all(np.abs(got - want) <= REL * np.abs(want)), (got, want)
+    if dt != torch.float64:  # a float64 map takes the portable path
+        wmap = ref.ssim(la, lb, 255.0, return_map=True)
+        gmap = fa.ssim(x, y, data_range=255.0, luma=mode, return_map=True).cpu().double().numpy()
+        assert gmap.shape == wmap.shape and np.abs(gmap - wmap).max() <= MAP_ABS
+
+
+@pytest.mark.parametrize("cb", [3, 4, 7])
+def test_ms_ssim_luma_and_crop_in_place(gpu, cb):
+    """MS-SSIM's first scale reads the crop in place and forms luma itself;
+    the pyramid below it is float64."""
+    rng = np.random.default_rng(cb)
+    a = rng.integers(0, 256, (2, 3, 200, 240)).astype(np.float64)
+    b = np.clip(a + 9.0 * rng.standard_normal(a.shape), 0, 255).round()
+    x = torch.from_numpy(a.astype(np.uint8)).to(gpu)
+    y = torch.from_numpy(b.astype(np.uint8)).to(gpu)
+    for mode in (None, "bt601", "matlab"):
+        ca, cbb = ref.crop(a, cb), ref.crop(b, cb)
+        if mode:
+            ca, cbb = ref.rgb_to_luma(ca, mode), ref.rgb_to_luma(cbb, mode)
+        want = ref.ms_ssim(ca, cbb, 255.0, reduction="none")
+        got = fa.ms_ssim(x, y, data_range=255.0, luma=mode, crop_border=cb,
+                         reduction="none").cpu().numpy()
+        assert np.all(np.abs(got - want) <= REL * np.abs(want)), (mode, got, want)
+
+
 def test_configs1_full_size(gpu):
     """configs[1]: 8x3x1080x1920 uint8 (sigma 8).  Image 0 against the oracle;
     the batch through size-independent properties (per-image consistency,
