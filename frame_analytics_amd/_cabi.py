@@ -47,6 +47,8 @@ SIGNATURES = {
     "fa_gpu_gmsd":
         ([_P, _P, _I, _I, _I, _I, _I, _D, _D, _I, _P, _P, _I, _P, _P, _I, _P], _I),
     # extensions without a reference counterpart
+    "fa_gpu_pixel_reduce_ex":
+        ([_P, _P, _I, _L, _I, _I, _I, _P, _P, _P, _I, _D, _D, _P, _I, _P, _P, _P, _P, _I, _P], _I),
     "fa_gpu_ssim_ex":
         ([_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _D, _D, _D, _P, _P, _I, _P, _P,
           _I, _P], _I),

@@ -241,10 +241,15 @@ def _gmsd_workspace(ext: _Native, h: int, w: int, downsample: bool) -> int:
 
 
 def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
-              param: float, per_image: bool, psnr_bias: float) -> torch.Tensor:
-    """One fused reduction; exactly one output tensor is allocated."""
-    n = int(x.shape[0])
-    per = x.numel() // n
+              param: float, per_image: bool, psnr_bias: float,
+              luma: Optional[tuple] = None) -> torch.Tensor:
+    """One fused reduction; exactly one output tensor is allocated.  Strided
+    (cropped) views and ``luma`` = (kr, kg, kb, offset) go through
+    ``fa_gpu_pixel_reduce_ex``, which reads them in place."""
+    n, c, h, w = (int(v) for v in x.shape)
+    x, xs = _view_strides(x)
+    y, ys = _view_strides(y)
+    per = c * h * w
     dev = _dev(x)
     bpi = _pixel_workspace(ext, n, per, dev)
     partial = _f64(x.device, n, bpi)
@@ -252,34 +257,47 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
     out = _f64(x.device, n) if per_image else _f64(x.device)
     sinks: list = [None, None, None, None]
     sinks[(2 if want_psnr else 0) + (0 if per_image else 1)] = out
-    _check(ext.gpu.fa_gpu_pixel_reduce(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op, float(param),
-        float(psnr_bias), _ptr(partial), bpi,
-        _ptr(sinks[0]), _ptr(sinks[1]), _ptr(sinks[2]), _ptr(sinks[3]),
-        dev, _stream(x)), ext)
+    if luma is None and xs is None and ys is None:
+        _check(ext.gpu.fa_gpu_pixel_reduce(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op, float(param),
+            float(psnr_bias), _ptr(partial), bpi,
+            _ptr(sinks[0]), _ptr(sinks[1]), _ptr(sinks[2]), _ptr(sinks[3]),
+            dev, _stream(x)), ext)
+    else:
+        _check(ext.gpu.fa_gpu_pixel_reduce_ex(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
+            op, float(param), float(psnr_bias), _ptr(partial), bpi,
+            _ptr(sinks[0]), _ptr(sinks[1]), _ptr(sinks[2]), _ptr(sinks[3]),
+            dev, _stream(x)), ext)
     return out
 
 
 def try_mse(x: torch.Tensor, y: torch.Tensor, *, per_image: bool,
-            dtype: torch.dtype, psnr_bias: Optional[float] = None) -> Optional[torch.Tensor]:
+            dtype: torch.dtype, psnr_bias: Optional[float] = None,
+            luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
     """Squared-error reduction, or PSNR when ``psnr_bias`` (= 10 log10 L^2) is given."""
     ext = _gpu_ext(x)
-    if ext is None or not _usable(x, y):
+    if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
+        return None
+    if luma is not None and x.shape[1] != 3:
         return None
     bias = psnr_bias if psnr_bias is not None else _PSNR_NONE
-    out = pixel_gpu(ext, _contig(x), _contig(y), op=_OP_MSE, param=0.0,
-                    per_image=per_image, psnr_bias=bias)
+    out = pixel_gpu(ext, x, y, op=_OP_MSE, param=0.0, per_image=per_image, psnr_bias=bias,
+                    luma=luma)
     return out if dtype == torch.float64 else out.to(dtype)
 
 
 def try_pixel(x: torch.Tensor, y: torch.Tensor, *, op: int, param: float,
-              per_image: bool, dtype: torch.dtype) -> Optional[torch.Tensor]:
+              per_image: bool, dtype: torch.dtype,
+              luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
     """L1 / Charbonnier / Huber reduction; ``None`` if no kernel applies."""
     ext = _gpu_ext(x)
-    if ext is None or not _usable(x, y):
+    if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
         return None
-    out = pixel_gpu(ext, _contig(x), _contig(y), op=op, param=param,
-                    per_image=per_image, psnr_bias=_PSNR_NONE)
+    if luma is not None and x.shape[1] != 3:
+        return None
+    out = pixel_gpu(ext, x, y, op=op, param=param, per_image=per_image,
+                    psnr_bias=_PSNR_NONE, luma=luma)
     return out if dtype == torch.float64 else out.to(dtype)
 
 

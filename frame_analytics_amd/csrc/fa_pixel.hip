@@ -285,6 +285,126 @@ __global__ __launch_bounds__(BLOCK) void pix_float_kernel(
 }
 
 // --------------------------------------------------------------------------
+// strided views and luma (fa_gpu_pixel_reduce_ex): a workgroup reduces an
+// equal share of its image's (channel, row) space, lanes striding along a row
+// (dwords for 4-byte aligned uint8 rows).  With luma the difference of the
+// two luma samples, kr dR + kg dG + kb dB (the offset cancels), is formed in
+// float64 from the channel differences, and every term is float64.
+// --------------------------------------------------------------------------
+struct PixView {
+  const void* a;
+  const void* b;
+  int64_t asn, asc, ash;  // element strides of image, channel, row
+  int64_t bsn, bsc, bsh;
+  int Cout, H, W;
+  double kr, kg, kb;
+  int bpi;
+  double param;
+  void* partial;
+};
+
+template <typename T, int OP, bool LUMA, int V>
+__global__ __launch_bounds__(BLOCK) void pix_view_kernel(PixView v) {
+  constexpr bool U8 = std::is_same<T, uint8_t>::value;
+  constexpr bool EXACT = U8 && !LUMA && (OP == FA_OP_MSE || OP == FA_OP_L1);
+  constexpr bool WIDE = LUMA || (OP != FA_OP_CHARB) || sizeof(T) == 8;
+  using A = typename std::conditional<WIDE, double, float>::type;
+  __shared__ uint64_t s_u[WAVES_PER_BLOCK];
+  __shared__ double s_d[WAVES_PER_BLOCK];
+
+  const int img = blockIdx.y;
+  const int64_t R = static_cast<int64_t>(v.Cout) * v.H;
+  const int64_t r0 = R * blockIdx.x / v.bpi;
+  const int64_t r1 = R * (blockIdx.x + 1) / v.bpi;
+  const T* ia = static_cast<const T*>(v.a) + img * v.asn;
+  const T* ib = static_cast<const T*>(v.b) + img * v.bsn;
+  const A p = static_cast<A>(v.param);
+
+  U8Lane<OP> lane8;   // uint8 without luma
+  double acc = 0.0;   // everything else
+  for (int64_t rr = r0; rr < r1; ++rr) {  // uniform
+    const int c = static_cast<int>(rr / v.H);
+    const int row = static_cast<int>(rr - static_cast<int64_t>(c) * v.H);
+    if constexpr (LUMA) {
+      const T* pa = ia + row * v.ash;
+      const T* pb = ib + row * v.bsh;
+      double part = 0.0;
+      for (int j = threadIdx.x; j < v.W; j += BLOCK) {
+        const double dr = Elem<T>::d(pa[j]) - Elem<T>::d(pb[j]);
+        const double dg = Elem<T>::d(pa[v.asc + j]) - Elem<T>::d(pb[v.bsc + j]);
+        const double db = Elem<T>::d(pa[2 * v.asc + j]) - Elem<T>::d(pb[2 * v.bsc + j]);
+        part += pix_term<OP, double>(fma(v.kb, db, fma(v.kg, dg, v.kr * dr)), p);
+      }
+      acc += part;
+    } else {
+      const T* pa = ia + c * v.asc + row * v.ash;
+      const T* pb = ib + c * v.bsc + row * v.bsh;
+      if constexpr (U8 && V == 4) {
+        const uint32_t* wa = reinterpret_cast<const uint32_t*>(pa);
+        const uint32_t* wb = reinterpret_cast<const uint32_t*>(pb);
+        for (int j = threadIdx.x; j < v.W / 4; j += BLOCK) {
+          lane8.dword(wa[j], wb[j], static_cast<float>(v.param));
+          lane8.flush();
+        }
+      } else if constexpr (U8) {
+        for (int j = threadIdx.x; j < v.W; j += BLOCK) lane8.byte(pa[j], pb[j], static_cast<float>(v.param));
+      } else {
+        A part = A(0);
+        for (int j = threadIdx.x; j < v.W; j += BLOCK)
+          part += pix_term<OP, A>(load_as<A>(pa, j) - load_as<A>(pb, j), p);
+        acc += static_cast<double>(part);
+      }
+    }
+  }
+
+  const int64_t slot = static_cast<int64_t>(img) * v.bpi + blockIdx.x;
+  if constexpr (EXACT) {
+    const uint64_t t = block_sum(lane8.exact, s_u);
+    if (threadIdx.x == 0) reinterpret_cast<uint64_t*>(v.partial)[slot] = t;
+  } else {
+    if constexpr (U8 && !LUMA) {
+      lane8.flush();
+      acc += lane8.wide;
+    }
+    const double t = block_sum(acc, s_d);
+    if (threadIdx.x == 0) reinterpret_cast<double*>(v.partial)[slot] = t;
+  }
+}
+
+template <typename T, int OP, bool LUMA>
+static void launch_view(bool dw, dim3 grid, hipStream_t st, const PixView& v) {
+  if (dw)
+    hipLaunchKernelGGL((pix_view_kernel<T, OP, LUMA, 4>), grid, dim3(BLOCK), 0, st, v);
+  else
+    hipLaunchKernelGGL((pix_view_kernel<T, OP, LUMA, 1>), grid, dim3(BLOCK), 0, st, v);
+}
+
+template <typename T, bool LUMA>
+static void launch_view_op(int op, bool dw, dim3 grid, hipStream_t st, const PixView& v) {
+  switch (op) {
+    case FA_OP_MSE: launch_view<T, FA_OP_MSE, LUMA>(dw, grid, st, v); break;
+    case FA_OP_L1: launch_view<T, FA_OP_L1, LUMA>(dw, grid, st, v); break;
+    case FA_OP_CHARB: launch_view<T, FA_OP_CHARB, LUMA>(dw, grid, st, v); break;
+    default: launch_view<T, FA_OP_HUBER, LUMA>(dw, grid, st, v); break;
+  }
+}
+
+template <bool LUMA>
+static int launch_view_dtype(int dtype, int op, bool dw, dim3 grid, hipStream_t st,
+                             const PixView& v) {
+  switch (dtype) {
+    case FA_U8: launch_view_op<uint8_t, LUMA>(op, dw, grid, st, v); break;
+    case FA_F16: launch_view_op<half_t, LUMA>(op, false, grid, st, v); break;
+    case FA_BF16: launch_view_op<bf16_t, LUMA>(op, false, grid, st, v); break;
+    case FA_F32: launch_view_op<float, LUMA>(op, false, grid, st, v); break;
+    case FA_F64: launch_view_op<double, LUMA>(op, false, grid, st, v); break;
+    default: return FA_E_DTYPE;
+  }
+  FA_LAUNCH_CHECK();
+  return FA_OK;
+}
+
+// --------------------------------------------------------------------------
 // finalize: block r < nrows reduces row r, block nrows reduces everything.
 // Means are divisions by the count (reference fa_cuda.cu:177-181); a PSNR is
 // psnr_bias - 10*log10(mean), +inf for a zero mean (reference :203-208).
@@ -448,6 +568,68 @@ FA_API int fa_gpu_pixel_reduce(const void* a, const void* b, int dtype,
                          n_each * static_cast<double>(n_images), psnr_bias,
                          out_per_image, out_total, out_psnr_per_image,
                          out_psnr_total, st);
+}
+
+// No counterpart in the reference, which materialises a float32 luma plane
+// (functional.py:267-271) and copies crops contiguous (backend.py:346,482).
+FA_API int fa_gpu_pixel_reduce_ex(const void* a, const void* b, int dtype, int64_t n_images,
+                                  int C, int H, int W, const int64_t* a_strides,
+                                  const int64_t* b_strides, const double* luma, int op,
+                                  double param, double psnr_bias, double* partial, int bpi,
+                                  double* out_per_image, double* out_total,
+                                  double* out_psnr_per_image, double* out_psnr_total,
+                                  int device, void* stream) {
+  if (!a || !b || !partial) return FA_E_ARG;
+  if (op < 0 || op > 3) return FA_E_OP;
+  if (dtype < FA_U8 || dtype > FA_F64) return FA_E_DTYPE;
+  if (n_images <= 0 || n_images > 65535 || C <= 0 || H <= 0 || W <= 0 || bpi <= 0)
+    return FA_E_SHAPE;
+  if (luma && C != 3) return FA_E_SHAPE;
+  const int64_t plane = static_cast<int64_t>(H) * W;
+  const int64_t va[3] = {a_strides ? a_strides[0] : plane * C, a_strides ? a_strides[1] : plane,
+                         a_strides ? a_strides[2] : W};
+  const int64_t vb[3] = {b_strides ? b_strides[0] : plane * C, b_strides ? b_strides[1] : plane,
+                         b_strides ? b_strides[2] : W};
+  for (int i = 0; i < 3; ++i)
+    if (va[i] < 0 || vb[i] < 0) return FA_E_SHAPE;
+  if (va[2] < W || vb[2] < W) return FA_E_SHAPE;  // rows may not overlap
+
+  PixView v = {};
+  v.a = a;
+  v.b = b;
+  v.asn = va[0];
+  v.asc = va[1];
+  v.ash = va[2];
+  v.bsn = vb[0];
+  v.bsc = vb[1];
+  v.bsh = vb[2];
+  v.Cout = luma ? 1 : C;
+  v.H = H;
+  v.W = W;
+  if (luma) {
+    v.kr = luma[0];
+    v.kg = luma[1];
+    v.kb = luma[2];
+  }
+  v.bpi = bpi;
+  v.param = param;
+  v.partial = partial;
+  // uint8 rows whose every start is 4-byte aligned are read as dwords
+  const uintptr_t bases = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
+  const int64_t strides = va[0] | va[1] | va[2] | vb[0] | vb[1] | vb[2];
+  const bool dw = dtype == FA_U8 && !luma && W % 4 == 0 && (bases & 3) == 0 && (strides & 3) == 0;
+
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(bpi), static_cast<unsigned>(n_images));
+  const int rc = luma ? launch_view_dtype<true>(dtype, op, dw, grid, st, v)
+                      : launch_view_dtype<false>(dtype, op, dw, grid, st, v);
+  if (rc != FA_OK) return rc;
+  const bool exact = dtype == FA_U8 && !luma && (op == FA_OP_MSE || op == FA_OP_L1);
+  const double n_each = static_cast<double>(v.Cout) * plane;
+  return launch_finalize(partial, exact, static_cast<int>(n_images), bpi, n_each,
+                         n_each * static_cast<double>(n_images), psnr_bias, out_per_image,
+                         out_total, out_psnr_per_image, out_psnr_total, st);
 }
 
 }  // extern "C"

@@ -146,6 +146,15 @@ def _luma_tuple(mode, L):
     return (kr, kg, kb, off * L)
 
 
+def _luma_arg_checked(x4, mode, L):
+    """The kernels' luma tuple for a pixel reduction, after the channel check."""
+    if mode is None:
+        return None
+    if x4.shape[1] != 3:
+        raise ValueError(f"luma needs a 3-channel image, got {x4.shape[1]} channels")
+    return _luma_tuple(mode, L)
+
+
 def _apply_luma(x4, y4, mode, L, dtype):
     if mode is None:
         return x4, y4
@@ -184,14 +193,16 @@ def mse(x: torch.Tensor, y: torch.Tensor, *, reduction: str = "mean",
     """
     x4, y4, L, mode = _prep(x, y, luma, crop_border, None)
     wdt = _work_dtype(x4, dtype)
-    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     _check_reduction(reduction)
     per_image = reduction == "none"
     from . import backend
 
-    fast = backend.try_mse(x4, y4, per_image=per_image, dtype=out_dtype)
+    # luma is formed inside the kernel and crops are read in place
+    fast = backend.try_mse(x4, y4, per_image=per_image, dtype=out_dtype,
+                           luma=_luma_arg_checked(x4, mode, L))
     if fast is not None:
         return fast
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     return _sum_sq(x4, y4, wdt, per_image).to(out_dtype)
 
 
@@ -202,16 +213,17 @@ def psnr(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None
     """Peak signal-to-noise ratio in dB; identical inputs give ``+inf`` unless ``eps``."""
     _check_reduction(reduction)
     x4, y4, L, mode = _prep(x, y, luma, crop_border, data_range)
-    x4, y4 = _apply_luma(x4, y4, mode, L, _work_dtype(x4, dtype))
     bias = 10.0 * math.log10(L * L)
     from . import backend
 
     if not eps:
-        # the dB conversion happens inside the reduction's finalize kernel
+        # the dB conversion happens inside the reduction's finalize kernel, the
+        # luma plane inside the reduction, and crops are read in place
         fast = backend.try_mse(x4, y4, per_image=reduction == "none", dtype=out_dtype,
-                               psnr_bias=bias)
+                               psnr_bias=bias, luma=_luma_arg_checked(x4, mode, L))
         if fast is not None:
             return fast
+    x4, y4 = _apply_luma(x4, y4, mode, L, _work_dtype(x4, dtype))
     m = mse(x4, y4, reduction=reduction, dtype=dtype, out_dtype=out_dtype)
     if eps:
         m = m.clamp_min(eps)
@@ -718,17 +730,18 @@ def _pixel_loss(name, x, y, param, reduction, dtype, out_dtype, luma, crop_borde
     _check_reduction(reduction)
     x4, y4, L, mode = _prep(x, y, luma, crop_border, None)
     wdt = _work_dtype(x4, dtype)
-    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     per_image = reduction == "none"
     from . import backend
 
     if backend_hint != "torch":
         fast = backend.try_pixel(x4, y4, op=_PIXEL_OPS[name], param=param,
-                                 per_image=per_image, dtype=out_dtype)
+                                 per_image=per_image, dtype=out_dtype,
+                                 luma=_luma_arg_checked(x4, mode, L))
         if fast is not None:
             return fast
         if backend_hint == "native":
             raise RuntimeError(f"native {name} backend unavailable for these inputs")
+    x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     t = _pixel_terms(name, x4.to(wdt) - y4.to(wdt), param)
     if per_image:
         out = t.sum(dim=(1, 2, 3), dtype=torch.float64) / t[0].numel()

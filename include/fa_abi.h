@@ -167,6 +167,30 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
 /*
  * No counterpart in the reference, which materialises a float32 luma plane
  * (functional.py:267-271) and copies crops contiguous (backend.py:346,482).
+ * fa_gpu_pixel_reduce over strided N x C x H x W views, optionally of luma:
+ *   a_strides / b_strides: {image, channel, row} strides in elements (columns
+ *     are contiguous), or null for contiguous;
+ *   luma: {kr, kg, kb, offset} or null.  With luma, C must be 3 and each
+ *     image is one plane; the term is formed from the luma difference
+ *     kr dR + kg dG + kb dB in float64 (the offset cancels and is not read).
+ * The mean is over (luma ? 1 : C) * H * W elements per image.  partial:
+ * [n_images, bpi] with bpi from fa_gpu_pixel_workspace(n_images, C * H * W);
+ * it holds uint64 exact sums for uint8 MSE / L1 without luma.
+ */
+FA_API int fa_gpu_pixel_reduce_ex(const void* a, const void* b, int dtype,
+                                  int64_t n_images, int C, int H, int W,
+                                  const int64_t* a_strides,
+                                  const int64_t* b_strides, const double* luma,
+                                  int op, double param, double psnr_bias,
+                                  double* partial, int bpi,
+                                  double* out_per_image, double* out_total,
+                                  double* out_psnr_per_image,
+                                  double* out_psnr_total, int device,
+                                  void* stream);
+
+/*
+ * No counterpart in the reference, which materialises a float32 luma plane
+ * (functional.py:267-271) and copies crops contiguous (backend.py:346,482).
  * fa_gpu_ssim over strided views, optionally of luma:
  *   x_strides / y_strides: {image, channel, row} strides in elements (columns
  *     are contiguous), or null for a contiguous N x C x H x W tensor; a plane

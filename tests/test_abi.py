@@ -36,7 +36,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 16  # 12 reference entry points + 4 extensions
+    assert len(decl) == 17  # 12 reference entry points + 5 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name

@@ -162,8 +162,47 @@ def test_luma_and_crop(gpu):
             ya = ref.crop(ref.rgb_to_luma(a[None], mode), cb)
             yb = ref.crop(ref.rgb_to_luma(b[None], mode), cb)
             got = float(fa.psnr(ta, tb, data_range=255.0, luma=mode, crop_border=cb))
-            assert abs(got - float(ref.psnr(ya, yb, 255.0))) < 1e-5
-            assert abs(float(fa.mse(ta, tb, luma=mode, crop_border=cb)) - ref.mse(ya, yb)) < 1e-4
+            assert abs(got - float(ref.psnr(ya, yb, 255.0))) < 1e-10
+            want = ref.mse(ya, yb)
+            assert abs(float(fa.mse(ta, tb, luma=mode, crop_border=cb)) - want) <= 1e-12 * want
     # an integer crop stays exact
     got = float(fa.mse(ta, tb, crop_border=3))
     assert got == ref.mse(ref.crop(a[None].astype(np.uint8), 3), ref.crop(b[None].astype(np.uint8), 3))
+
+
+@pytest.mark.parametrize("dt", [torch.uint8, torch.float16, torch.float32, torch.float64])
+@pytest.mark.parametrize("cb", [0, 3, 4])
+def test_luma_formed_in_kernel(gpu, dt, cb):
+    """fa_gpu_pixel_reduce_ex: the luma difference kr dR + kg dG + kb dB in
+    float64, crops read in place, every op, against the float64 oracle."""
+    a, b = u8_pair((2, 3, 70, 100), 10.0, seed=cb + 7)
+    x, y = torch.from_numpy(a).to(gpu, dt), torch.from_numpy(b).to(gpu, dt)
+    for mode in ("bt601", "bt709", "matlab"):
+        la = ref.crop(ref.rgb_to_luma(a.astype(np.float64), mode), cb)
+        lb = ref.crop(ref.rgb_to_luma(b.astype(np.float64), mode), cb)
+        kw = dict(luma=mode, crop_border=cb, reduction="none")
+        for fn, want in ((fa.mse, ref.mse(la, lb, "none")), (fa.l1, ref.l1(la, lb, "none")),
+                         (fa.charbonnier, ref.charbonnier(la, lb, reduction="none")),
+                         (fa.huber, ref.huber(la, lb, reduction="none"))):
+            got = fn(x, y, **kw).cpu().numpy()
+            assert np.all(np.abs(got - want) <= 1e-12 * np.abs(want)), (fn.__name__, mode)
+        gp = fa.psnr(x, y, data_range=255.0, **kw).cpu().numpy()
+        assert np.all(np.abs(gp - ref.psnr(la, lb, 255.0, "none")) < 1e-10)
+
+
+@pytest.mark.parametrize("cb", [1, 2, 3, 4, 8])
+def test_crop_read_in_place_exact(gpu, cb):
+    """uint8 crops stay bit-exact: borders 4 and 8 keep rows 4-byte aligned
+    (dword path), 1 / 2 / 3 do not (byte path)."""
+    a, b = u8_pair((3, 3, 60, 100), 12.0, seed=cb)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    ca, cbb = ref.crop(a, cb), ref.crop(b, cb)
+    got = fa.mse(x, y, crop_border=cb, reduction="none").cpu().numpy()
+    assert np.array_equal(got, ref.mse(ca, cbb, "none"))
+    got = fa.l1(x, y, crop_border=cb, reduction="none").cpu().numpy()
+    assert np.array_equal(got, ref.l1(ca, cbb, "none"))
+    assert float(fa.mse(x, y, crop_border=cb)) == ref.mse(ca, cbb)
+    # float terms on the byte / dword paths
+    got = fa.huber(x, y, crop_border=cb, reduction="none").cpu().numpy()
+    want = ref.huber(ca.astype(np.float64), cbb.astype(np.float64), reduction="none")
+    assert np.all(np.abs(got - want) <= 1e-9 * np.abs(want))
