@@ -554,12 +554,13 @@ def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
 
 
 def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsample: bool,
-             luma: Optional[tuple] = None):
-    """``(gms_mean, gmsd)`` per image, float64; ``None`` if unavailable.
+             luma: Optional[tuple] = None, want_map: bool = False):
+    """``(gms_mean, gmsd)`` per image, float64 -- plus the float32 q map when
+    ``want_map`` -- or ``None`` if unavailable.
 
-    ``luma`` = (kr, kg, kb) makes the kernel read the three channels and form
-    the luma plane itself; cropped views are read in place through their
-    strides (``fa_gpu_gmsd_ex``).
+    ``luma`` = (kr, kg, kb[, offset]) makes the kernel read the three channels
+    and form the luma plane itself; cropped views are read in place through
+    their strides (``fa_gpu_gmsd_ex``).
     """
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y):
@@ -570,21 +571,67 @@ def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsamp
         return None
     x, xs = _view_strides(x)
     y, ys = _view_strides(y)
-    planes = n * (1 if luma is not None else c)
+    cout = 1 if luma is not None else c
+    planes = n * cout
     bpp = _gmsd_workspace(ext, h, w, downsample)
     psum = _f64(x.device, planes, bpp)
     psumsq = _f64(x.device, planes, bpp)
     mean = _f64(x.device, n)
     dev = _f64(x.device, n)
-    if luma is None and xs is None and ys is None:
+    qmap = None
+    if want_map:
+        hd, wd = (h // 2, w // 2) if downsample else (h, w)
+        qmap = torch.empty((n, cout, hd - 2, wd - 2), dtype=torch.float32, device=x.device)
+    if luma is None and xs is None and ys is None and qmap is None:
         _check(ext.gpu.fa_gpu_gmsd(
             _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
             int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
             _dev(x), _stream(x)), ext)
     else:
-        lw = _luma_arg(luma)
         _check(ext.gpu.fa_gpu_gmsd_ex(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, lw,
-            float(T), float(eps), int(downsample), _ptr(psum), _ptr(psumsq), bpp,
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
+            float(T), float(eps), int(downsample), _ptr(qmap), _ptr(psum), _ptr(psumsq), bpp,
             _ptr(mean), _ptr(dev), _dev(x), _stream(x)), ext)
+    return (mean, dev, qmap) if want_map else (mean, dev)
+
+
+def gmsd_autograd_available(x: torch.Tensor, y: torch.Tensor) -> bool:
+    """Can the differentiable native GMS / GMSD path serve this call?"""
+    return (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float64)
+            and y.dtype == x.dtype and x.shape == y.shape
+            and not torch.cuda.is_current_stream_capturing() and _gpu_ext(x) is not None)
+
+
+def gmsd_stats_fwd(x, y, T, eps, downsample):
+    """Forward half of the differentiable GMS / GMSD: ``(mean, std)`` per image."""
+    ext = load()
+    x, y = _contig(x), _contig(y)
+    n, c, h, w = x.shape
+    bpp = _gmsd_workspace(ext, h, w, downsample)
+    psum = _f64(x.device, n * c, bpp)
+    psumsq = _f64(x.device, n * c, bpp)
+    mean = _f64(x.device, n)
+    dev = _f64(x.device, n)
+    _check(ext.gpu.fa_gpu_gmsd(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
+        int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
+        _dev(x), _stream(x)), ext)
     return mean, dev
+
+
+def gmsd_stats_bwd(x, y, mean, std, g_mean, g_std, T, eps, downsample, need_dx, need_dy):
+    ext = load()
+    x, y = _contig(x), _contig(y)
+    n, c, h, w = x.shape
+    hd, wd = (h // 2, w // 2) if downsample else (h, w)
+    aux = torch.empty((4, n * c, hd - 2, wd - 2), dtype=torch.float64, device=x.device)
+    gm = g_mean.to(torch.float64).contiguous() if g_mean is not None else None
+    gs = g_std.to(torch.float64).contiguous() if g_std is not None else None
+    dx = torch.empty_like(x) if need_dx else None
+    dy = torch.empty_like(y) if need_dy else None
+    _check(ext.gpu.fa_gpu_gmsd_backward(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
+        int(downsample), _ptr(mean), _ptr(std), _ptr(gm), _ptr(gs), _ptr(aux), _ptr(dx),
+        _ptr(dy), _dev(x), _stream(x)), ext)
+    return dx, dy
+

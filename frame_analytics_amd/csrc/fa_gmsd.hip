@@ -71,6 +71,7 @@ struct GmsdArgs {
   int ext_x, ext_y;          // bytes from a plane's base to its last byte + 1 (dword path)
   double* psum;
   double* psumsq;
+  float* map;                // optional q map, [N * Cout, Hout, Wout]
 };
 
 // d = 1 - q from the squared gradient magnitudes M1, M2 (without eps) and
@@ -319,6 +320,8 @@ __device__ inline void mag2(double gx1, double gy1, double gx2, double gy2, doub
 template <class Src>
 __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int row0, int rows,
                                 double& acc, double& acc2) {
+  float* const map_plane =
+      a.map ? a.map + (static_cast<int64_t>(n) * a.Cout + c) * a.Hout * a.Wout : nullptr;
   using S = typename Src::S;
   using Raw = typename Src::Raw;
   constexpr int NC = Src::NC;
@@ -364,6 +367,9 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
           mag2(gx1[k], gy1[k], gx2[k], gy2[k], m1, m2, dm);
           dm = ok[k] ? dm : S(0);
           const Acc d = one_minus_q<Src::FAST, S>(m1, m2, dm, a.eps2f, a.T2f, a.eps2, a.T2);
+          if (map_plane && ok[k])  // uniform test of the pointer
+            map_plane[static_cast<int64_t>(row0 + g + i) * a.Wout + col + k] =
+                static_cast<float>(1.0 - static_cast<double>(d));
           gs += d;
           gs2 = fma(d, d, gs2);
         }
@@ -445,6 +451,178 @@ __global__ __launch_bounds__(BLOCK) void gmsd_finalize_kernel(
     out_mean[blockIdx.x] = 1.0 - md;
     out_std[blockIdx.x] = sqrt(var > 0.0 ? var : 0.0);
   }
+}
+
+// --------------------------------------------------------------------------
+// backward (an extension): gradients of per-image mean and standard
+// deviation of q, for x / y of float32 or float64, all in float64.
+//
+//   coefficient pass: per output pixel, with w = dL/dq = g_mean/n +
+//     g_std (q - m)/(n std), dq/dg1 = 2 (g2 - g1)(g2 (g1 + g2) + T)/D^2 (the
+//     factored form, exact in sign and accurate where g1 ~ g2) and
+//     dg/dgx = gx/g: the four maps dL/dgx1, dL/dgy1, dL/dgx2, dL/dgy2.
+//     A workgroup stages the (16 + 2) x (64 + 2) samples of its tile in LDS.
+//   scatter: per input pixel, the Prewitt adjoint of those maps at its
+//     sample (12 taps per tensor, zero outside the map), a quarter of it with
+//     downsampling, none for the dropped odd row / column.
+// --------------------------------------------------------------------------
+constexpr int GB_TR = 16;  // output rows per coefficient tile
+constexpr int GB_TC = 64;  // output columns per coefficient tile
+
+struct GmsdBwdArgs {
+  const void* x;
+  const void* y;
+  int C, H, W, Hd, Wd, Hout, Wout;
+  double T, eps;
+  const double* mean;
+  const double* std_;
+  const double* g_mean;  // may be null: zero
+  const double* g_std;   // may be null: zero
+  double* aux;           // 4 maps [planes, Hout, Wout]
+  int64_t map_stride;    // planes * Hout * Wout
+  void* dx;
+  void* dy;
+  int tiles_x, tiles_y;
+};
+
+template <typename T, bool DOWN>
+__device__ inline double gb_sample(const T* plane, int W, int r, int c) {
+  if constexpr (DOWN) {
+    const int64_t o = static_cast<int64_t>(2 * r) * W + 2 * c;
+    return 0.25 * ((Elem<T>::d(plane[o]) + Elem<T>::d(plane[o + 1])) +
+                   (Elem<T>::d(plane[o + W]) + Elem<T>::d(plane[o + W + 1])));
+  } else {
+    return Elem<T>::d(plane[static_cast<int64_t>(r) * W + c]);
+  }
+}
+
+template <typename T, bool DOWN>
+__global__ __launch_bounds__(BLOCK) void gmsd_coef_kernel(GmsdBwdArgs a) {
+  __shared__ double sx[GB_TR + 2][GB_TC + 2];
+  __shared__ double sy[GB_TR + 2][GB_TC + 2];
+  const int per_plane = a.tiles_x * a.tiles_y;
+  const int plane = blockIdx.x / per_plane;
+  const int t = blockIdx.x - plane * per_plane;
+  const int R0 = (t / a.tiles_x) * GB_TR;
+  const int C0 = (t % a.tiles_x) * GB_TC;
+  const int64_t poff = static_cast<int64_t>(plane) * a.H * a.W;
+  const T* px = static_cast<const T*>(a.x) + poff;
+  const T* py = static_cast<const T*>(a.y) + poff;
+  // stage the samples; rows / columns past the sample grid are clamped (they
+  // only feed outputs outside the map)
+  for (int e = threadIdx.x; e < (GB_TR + 2) * (GB_TC + 2); e += BLOCK) {
+    const int r = e / (GB_TC + 2), c = e - r * (GB_TC + 2);
+    const int gr = min(R0 + r, a.Hd - 1), gc = min(C0 + c, a.Wd - 1);
+    sx[r][c] = gb_sample<T, DOWN>(px, a.W, gr, gc);
+    sy[r][c] = gb_sample<T, DOWN>(py, a.W, gr, gc);
+  }
+  __syncthreads();
+
+  const int n = plane / a.C;
+  const double cnt = static_cast<double>(a.C) * a.Hout * a.Wout;
+  const double gm = a.g_mean ? a.g_mean[n] : 0.0;
+  const double gsd = a.g_std ? a.g_std[n] : 0.0;
+  const double sd = a.std_[n];
+  const double ks = sd > 0.0 ? gsd / (cnt * sd) : 0.0;
+  const double m = a.mean[n];
+  const double third = 1.0 / 3.0;
+  for (int e = threadIdx.x; e < GB_TR * GB_TC; e += BLOCK) {
+    const int i = e / GB_TC, j = e - i * GB_TC;
+    const int oi = R0 + i, oj = C0 + j;
+    if (oi >= a.Hout || oj >= a.Wout) continue;
+    double gx1 = 0.0, gy1 = 0.0, gx2 = 0.0, gy2 = 0.0;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      gx1 += sx[i + u][j] - sx[i + u][j + 2];
+      gy1 += sx[i][j + u] - sx[i + 2][j + u];
+      gx2 += sy[i + u][j] - sy[i + u][j + 2];
+      gy2 += sy[i][j + u] - sy[i + 2][j + u];
+    }
+    gx1 *= third;
+    gy1 *= third;
+    gx2 *= third;
+    gy2 *= third;
+    const double G1 = fma(gx1, gx1, fma(gy1, gy1, a.eps));
+    const double G2 = fma(gx2, gx2, fma(gy2, gy2, a.eps));
+    const double g1 = sqrt(G1), g2 = sqrt(G2);
+    const double D = G1 + G2 + a.T;
+    const double q = fma(2.0 * g1, g2, a.T) / D;
+    const double w = gm / cnt + ks * (q - m);
+    // g2 - g1 = (G2 - G1) / (g1 + g2), with G2 - G1 in factored form
+    const double dG = fma(gx2 - gx1, gx2 + gx1, (gy2 - gy1) * (gy2 + gy1));
+    const double dg = dG / (g1 + g2);
+    const double iD2 = 1.0 / (D * D);
+    const double d1 = w * 2.0 * dg * fma(g2, g1 + g2, a.T) * iD2;   // w dq/dg1
+    const double d2 = -w * 2.0 * dg * fma(g1, g1 + g2, a.T) * iD2;  // w dq/dg2
+    const int64_t o = static_cast<int64_t>(plane) * a.Hout * a.Wout +
+                      static_cast<int64_t>(oi) * a.Wout + oj;
+    a.aux[o] = d1 * gx1 / g1;
+    a.aux[a.map_stride + o] = d1 * gy1 / g1;
+    a.aux[2 * a.map_stride + o] = d2 * gx2 / g2;
+    a.aux[3 * a.map_stride + o] = d2 * gy2 / g2;
+  }
+}
+
+// (1/3) sum_u [Gx(a-u, b) - Gx(a-u, b-2)] + (1/3) sum_u [Gy(a, b-u) - Gy(a-2, b-u)]
+__device__ inline double prewitt_adjoint(const double* gx, const double* gy, int Hout, int Wout,
+                                         int r, int c) {
+  auto at = [&](const double* m, int i, int j) {
+    return (i >= 0 && i < Hout && j >= 0 && j < Wout) ? m[static_cast<int64_t>(i) * Wout + j]
+                                                      : 0.0;
+  };
+  double s = 0.0;
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    s += at(gx, r - u, c) - at(gx, r - u, c - 2);
+    s += at(gy, r, c - u) - at(gy, r - 2, c - u);
+  }
+  return s * (1.0 / 3.0);
+}
+
+template <typename T, bool DOWN>
+__global__ __launch_bounds__(BLOCK) void gmsd_scatter_kernel(GmsdBwdArgs a, int64_t total) {
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * BLOCK + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * BLOCK) {
+    const int64_t plane = e / (static_cast<int64_t>(a.H) * a.W);
+    const int64_t rem = e - plane * a.H * a.W;
+    const int h = static_cast<int>(rem / a.W), w = static_cast<int>(rem - (rem / a.W) * a.W);
+    const int r = DOWN ? h / 2 : h, c = DOWN ? w / 2 : w;
+    const bool in = r < a.Hd && c < a.Wd;  // the dropped odd row / column
+    const int64_t mo = plane * a.Hout * a.Wout;
+    const double scale = DOWN ? 0.25 : 1.0;
+    if (a.dx) {
+      const double v = in ? scale * prewitt_adjoint(a.aux + mo, a.aux + a.map_stride + mo,
+                                                    a.Hout, a.Wout, r, c)
+                          : 0.0;
+      static_cast<T*>(a.dx)[e] = static_cast<T>(v);
+    }
+    if (a.dy) {
+      const double v = in ? scale * prewitt_adjoint(a.aux + 2 * a.map_stride + mo,
+                                                    a.aux + 3 * a.map_stride + mo, a.Hout,
+                                                    a.Wout, r, c)
+                          : 0.0;
+      static_cast<T*>(a.dy)[e] = static_cast<T>(v);
+    }
+  }
+}
+
+template <typename T, bool DOWN>
+static int launch_gmsd_bwd(GmsdBwdArgs& a, int64_t planes, int device, hipStream_t st) {
+  a.tiles_x = (a.Wout + GB_TC - 1) / GB_TC;
+  a.tiles_y = (a.Hout + GB_TR - 1) / GB_TR;
+  const int64_t wgs = planes * a.tiles_x * a.tiles_y;
+  if (wgs > INT32_MAX) return FA_E_SHAPE;
+  hipLaunchKernelGGL((gmsd_coef_kernel<T, DOWN>), dim3(static_cast<unsigned>(wgs)), dim3(BLOCK),
+                     0, st, a);
+  FA_LAUNCH_CHECK();
+  const int64_t total = planes * a.H * a.W;
+  const int64_t want = (total + BLOCK - 1) / BLOCK;
+  const int64_t cap = static_cast<int64_t>(cu_count(device)) * 16;
+  hipLaunchKernelGGL((gmsd_scatter_kernel<T, DOWN>),
+                     dim3(static_cast<unsigned>(want < cap ? want : cap)), dim3(BLOCK), 0, st, a,
+                     total);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
 }
 
 struct GGeom {
@@ -533,8 +711,8 @@ static int dispatch_gmsd(int dtype, const GmsdArgs& a, const GLaunch& l, bool do
 
 static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int H, int W,
                      const int64_t* xs, const int64_t* ys, const double* luma, double Tc,
-                     double eps, int downsample, double* psum, double* psumsq, int bpp,
-                     double* out_mean, double* out_std, int device, void* stream) {
+                     double eps, int downsample, float* map_out, double* psum, double* psumsq,
+                     int bpp, double* out_mean, double* out_std, int device, void* stream) {
   if (!x || !y || !psum || !psumsq || !out_mean || !out_std) return FA_E_ARG;
   if (N <= 0 || C <= 0) return FA_E_SHAPE;
   if (dtype < FA_U8 || dtype > FA_F64) return FA_E_DTYPE;
@@ -570,6 +748,7 @@ static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int 
   a.eps2f = static_cast<float>(a.eps2);
   a.psum = psum;
   a.psumsq = psumsq;
+  a.map = map_out;
   const bool down = downsample != 0;
   // the dword path: uint8, downsampled, every row of every plane 4-byte aligned
   // (buffer addressing: a plane's rows must lie within 2^31 bytes of its base)
@@ -617,7 +796,7 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
                        double* psum, double* psumsq, int bpp, double* out_mean,
                        double* out_std, int device, void* stream) {
   return gmsd_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, Tc, eps, downsample,
-                   psum, psumsq, bpp, out_mean, out_std, device, stream);
+                   nullptr, psum, psumsq, bpp, out_mean, out_std, device, stream);
 }
 
 // No counterpart in the reference, which materialises a float32 luma plane
@@ -625,11 +804,61 @@ FA_API int fa_gpu_gmsd(const void* x, const void* y, int dtype, int N, int C,
 FA_API int fa_gpu_gmsd_ex(const void* x, const void* y, int dtype, int N, int C,
                           int H, int W, const int64_t* x_strides,
                           const int64_t* y_strides, const double* luma, double Tc,
-                          double eps, int downsample, double* psum, double* psumsq,
-                          int bpp, double* out_mean, double* out_std, int device,
-                          void* stream) {
+                          double eps, int downsample, float* map_out, double* psum,
+                          double* psumsq, int bpp, double* out_mean, double* out_std,
+                          int device, void* stream) {
   return gmsd_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, Tc, eps, downsample,
-                   psum, psumsq, bpp, out_mean, out_std, device, stream);
+                   map_out, psum, psumsq, bpp, out_mean, out_std, device, stream);
+}
+
+// No counterpart in the reference: its GMS / GMSD losses differentiate the
+// portable PyTorch path (modules.py:183-184).  Gradients of
+//   L = sum_n g_mean[n] mean_n(q) + g_std[n] std_n(q)
+// with respect to contiguous x and y (N x C x H x W, FA_F32 or FA_F64); mean /
+// std are fa_gpu_gmsd's outputs for the same inputs; g_mean / g_std are
+// device arrays of N (either may be null: zero); aux is 4 * N*C*Hout*Wout
+// float64 scratch; dx / dy (either may be null) are written in full.
+FA_API int fa_gpu_gmsd_backward(const void* x, const void* y, int dtype, int N, int C, int H,
+                                int W, double Tc, double eps, int downsample,
+                                const double* mean, const double* std_dev,
+                                const double* g_mean, const double* g_std, double* aux,
+                                void* dx, void* dy, int device, void* stream) {
+  if (!x || !y || !mean || !std_dev || !aux) return FA_E_ARG;
+  if (!dx && !dy) return FA_E_ARG;
+  if (dtype != FA_F32 && dtype != FA_F64) return FA_E_DTYPE;
+  if (N <= 0 || C <= 0) return FA_E_SHAPE;
+  GGeom g;
+  const int rc = gmsd_geometry(H, W, downsample, &g);
+  if (rc != FA_OK) return rc;
+  GmsdBwdArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.C = C;
+  a.H = H;
+  a.W = W;
+  a.Hd = g.Hd;
+  a.Wd = g.Wd;
+  a.Hout = g.Hout;
+  a.Wout = g.Wout;
+  a.T = Tc;
+  a.eps = eps;
+  a.mean = mean;
+  a.std_ = std_dev;
+  a.g_mean = g_mean;
+  a.g_std = g_std;
+  a.aux = aux;
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  a.map_stride = planes * g.Hout * g.Wout;
+  a.dx = dx;
+  a.dy = dy;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool down = downsample != 0;
+  if (dtype == FA_F32)
+    return down ? launch_gmsd_bwd<float, true>(a, planes, device, st)
+                : launch_gmsd_bwd<float, false>(a, planes, device, st);
+  return down ? launch_gmsd_bwd<double, true>(a, planes, device, st)
+              : launch_gmsd_bwd<double, false>(a, planes, device, st);
 }
 
 }  // extern "C"

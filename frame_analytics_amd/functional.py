@@ -642,6 +642,35 @@ def _gms_map(x4, y4, wdt, T, eps, downsample):
     return q.reshape(n, c, h - 2, w - 2)
 
 
+class _FusedGMSD(torch.autograd.Function):
+    """Differentiable native per-image ``(mean q, std q)`` of the GMS map
+    (``fa_gpu_gmsd`` forward, ``fa_gpu_gmsd_backward`` in float64)."""
+
+    @staticmethod
+    def forward(ctx, x, y, T, eps, downsample):
+        from . import backend
+
+        mean, std = backend.gmsd_stats_fwd(x, y, T, eps, downsample)
+        ctx.save_for_backward(x, y, mean, std)
+        ctx.consts = (T, eps, downsample)
+        ctx.set_materialize_grads(False)
+        return mean, std
+
+    @staticmethod
+    def backward(ctx, g_mean, g_std):
+        from . import backend
+
+        _reject_double_backward()
+        x, y, mean, std = ctx.saved_tensors
+        T, eps, downsample = ctx.consts
+        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_dx or need_dy) or (g_mean is None and g_std is None):
+            return (None,) * 5
+        dx, dy = backend.gmsd_stats_bwd(x, y, mean, std, g_mean, g_std, T, eps, downsample,
+                                        need_dx, need_dy)
+        return dx if need_dx else None, dy if need_dy else None, None, None, None
+
+
 def _gmsd_common(x, y, data_range, T, eps, downsample, dtype, luma, crop_border,
                  reduction, return_map, backend_hint):
     """``(map, None)`` or ``(None, (gms_mean, gmsd))`` per image."""
@@ -650,23 +679,37 @@ def _gmsd_common(x, y, data_range, T, eps, downsample, dtype, luma, crop_border,
     wdt = _work_dtype(x4, dtype)
     Tv = float(T) if T is not None else 170.0 * (L / 255.0) ** 2
     ev = float(eps) if eps is not None else (1e-6 * L) ** 2
+    grad = torch.is_grad_enabled() and (x4.requires_grad or y4.requires_grad)
+    if backend_hint != "torch" and grad and not return_map:
+        # training: luma (if any) is an autograd op in front, then the native
+        # statistics with a float64 backward
+        from . import backend
+
+        xl, yl = _apply_luma(x4, y4, mode, L, wdt)
+        if xl.dtype in (torch.float16, torch.bfloat16):
+            xl, yl = xl.float(), yl.float()
+        if backend.gmsd_autograd_available(xl, yl):
+            return None, _FusedGMSD.apply(xl, yl, Tv, ev, downsample)
     if backend_hint != "torch":
         from . import backend
 
         # The kernel forms the luma plane itself (its offset cancels out of
-        # every gradient) and reads crops in place; it computes in float64,
-        # so a float64 working dtype needs no other path.  It writes no map.
+        # every gradient) and reads crops in place; its statistics are
+        # float64-accurate, so a float64 working dtype needs no other path.
+        # Its map is float32, so a float64 map takes the portable path.
+        if mode is not None and x4.shape[1] != 3:
+            raise ValueError(f"luma needs a 3-channel image, got {x4.shape[1]} channels")
+        lw = LUMA_COEFFS[mode][:3] if mode is not None else None
         fast = None
-        if not return_map:
-            if mode is not None and x4.shape[1] != 3:
-                raise ValueError(f"luma needs a 3-channel image, got {x4.shape[1]} channels")
-            lw = LUMA_COEFFS[mode][:3] if mode is not None else None
-            fast = backend.try_gmsd(x4, y4, T=Tv, eps=ev, downsample=downsample, luma=lw)
+        if not (return_map and wdt == torch.float64):
+            fast = backend.try_gmsd(x4, y4, T=Tv, eps=ev, downsample=downsample, luma=lw,
+                                    want_map=return_map)
         if fast is not None:
+            if return_map:
+                return (fast[2] if wdt == torch.float32 else fast[2].to(wdt)), None
             return None, fast
         if backend_hint == "native":
-            raise RuntimeError("native GMSD backend unavailable for these inputs"
-                               + (" (return_map=True has no native kernel)" if return_map else ""))
+            raise RuntimeError("native GMSD backend unavailable for these inputs")
     x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
     q = _gms_map(x4, y4, wdt, Tv, ev, downsample)
     if return_map:

@@ -238,15 +238,18 @@ FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N,
  *   luma: {kr, kg, kb, offset} or null.  With luma, C must be 3 and each
  *     image is one plane kr R + kg G + kb B, formed in float64 (the offset
  *     cancels out of every gradient and is not read).
+ * map_out: null, or the similarity map q, float32 [N * (luma ? 1 : C), Hout,
+ * Wout] with Hout x Wout the 'valid' Prewitt grid of the (downsampled) image.
  * psum / psumsq: [N * (luma ? 1 : C), bpp] float64 with bpp from
  * fa_gpu_gmsd_workspace; out_mean / out_std: N float64 each.
  */
 FA_API int fa_gpu_gmsd_ex(const void* x, const void* y, int dtype, int N, int C,
                           int H, int W, const int64_t* x_strides,
                           const int64_t* y_strides, const double* luma,
-                          double Tc, double eps, int downsample, double* psum,
-                          double* psumsq, int bpp, double* out_mean,
-                          double* out_std, int device, void* stream);
+                          double Tc, double eps, int downsample, float* map_out,
+                          double* psum, double* psumsq, int bpp,
+                          double* out_mean, double* out_std, int device,
+                          void* stream);
 
 /*
  * No counterpart in the reference.  fa_gpu_ssim_cs_backward for x / y / dx / dy
@@ -264,6 +267,23 @@ FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
                                       const void* gpy, int gp_dtype,
                                       float* aux, void* dx, void* dy,
                                       int device, void* stream);
+
+/*
+ * No counterpart in the reference, whose GMS / GMSD losses differentiate the
+ * portable PyTorch path (modules.py:183-184).  Gradients of
+ *   L = sum_n g_mean[n] * mean_n(q) + g_std[n] * std_n(q)
+ * with respect to contiguous x and y (N x C x H x W of dtype FA_F32 or
+ * FA_F64), computed in float64.  mean / std_dev: fa_gpu_gmsd's outputs for
+ * the same inputs (device, N each); g_mean / g_std: device arrays of N (either
+ * may be null: zero); aux: 4 * N*C*Hout*Wout float64 scratch; dx / dy: either
+ * may be null, written in full (zero on the row / column a downsample drops).
+ */
+FA_API int fa_gpu_gmsd_backward(const void* x, const void* y, int dtype, int N,
+                                int C, int H, int W, double Tc, double eps,
+                                int downsample, const double* mean,
+                                const double* std_dev, const double* g_mean,
+                                const double* g_std, double* aux, void* dx,
+                                void* dy, int device, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -20,6 +20,7 @@ How each function is pinned (see tests/test_oracle.py):
     the reference CPU C++ per-scale primitive
   * gmsd: identity, the reference CPU C++ gmsd, torch conv2d Prewitt
   * ssim gradient: float64 central differences and float64 torch autograd
+  * gms / gmsd gradient: float64 central differences of gmsd_stats
 """
 
 from __future__ import annotations
@@ -374,3 +375,69 @@ def ssim_mean_grad(x, y, data_range=1.0, win_size=11, sigma=1.5, K=(0.01, 0.03),
     dx = 2 * x * Pb + y * Pc + full_correlate_transposed(tx, w, H, W)
     dy = 2 * y * Pb + x * Pc + full_correlate_transposed(ty, w, H, W)
     return dx, dy
+
+
+def valid_correlate_adjoint(m: np.ndarray, k: np.ndarray, H: int, W: int) -> np.ndarray:
+    """sum_p k(q - p) m(p): the adjoint of valid_correlate2d with the 2-D
+    kernel k, from its (H-kh+1) x (W-kw+1) grid back onto H x W."""
+    kh, kw = k.shape
+    oh, ow = m.shape[-2:]
+    out = np.zeros(m.shape[:-2] + (H, W), dtype=np.float64)
+    for i in range(kh):
+        for j in range(kw):
+            out[..., i:i + oh, j:j + ow] += k[i, j] * m
+    return out
+
+
+def gms_stats_grad(x, y, data_range=255.0, T=None, downsample=True, eps=None,
+                   g_mean=None, g_std=None) -> Tuple[np.ndarray, np.ndarray]:
+    """d L / d x and d L / d y in float64 for
+    L = sum_n g_mean[n] mean(q_n) + g_std[n] std(q_n), the per-image mean and
+    population standard deviation of the GMS map over its channels (the
+    statistics of gmsd_stats; reference functional.py:959-971).
+
+    By the chain rule: dmean/dq = 1/n, dstd/dq = (q - m)/(n std);
+    dq/dg1 = 2 (g2 D - g1 N)/D^2 with N = 2 g1 g2 + T, D = g1^2 + g2^2 + T;
+    dg/dgx = gx/g, dg/dgy = gy/g; the Prewitt correlations' adjoints; and the
+    2x2 mean's adjoint (a quarter to each pixel of the block, none to the
+    dropped odd row / column)."""
+    x = np.asarray(x, np.float64)
+    y = np.asarray(y, np.float64)
+    N, C, H, W = x.shape
+    L = float(data_range)
+    T = 170.0 * (L / 255.0) ** 2 if T is None else float(T)
+    eps = (1e-6 * L) ** 2 if eps is None else float(eps)
+    gm = np.zeros(N) if g_mean is None else np.asarray(g_mean, np.float64)
+    gs = np.zeros(N) if g_std is None else np.asarray(g_std, np.float64)
+    xs, ys = (avg_pool2(x), avg_pool2(y)) if downsample else (x, y)
+    Hd, Wd = xs.shape[-2:]
+    gx1, gy1 = valid_correlate2d(xs, PREWITT_X), valid_correlate2d(xs, PREWITT_Y)
+    gx2, gy2 = valid_correlate2d(ys, PREWITT_X), valid_correlate2d(ys, PREWITT_Y)
+    g1 = np.sqrt(gx1 ** 2 + gy1 ** 2 + eps)
+    g2 = np.sqrt(gx2 ** 2 + gy2 ** 2 + eps)
+    num = 2.0 * g1 * g2 + T
+    den = g1 * g1 + g2 * g2 + T
+    q = num / den
+    n = q[0].size
+    flat = q.reshape(N, -1)
+    m = flat.mean(axis=1)
+    sd = np.sqrt(((flat - m[:, None]) ** 2).mean(axis=1))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ks = np.where(sd > 0, gs / (n * sd), 0.0)
+    w = gm[:, None, None, None] / n + ks[:, None, None, None] * (q - m[:, None, None, None])
+    d1 = w * 2.0 * (g2 * den - g1 * num) / den ** 2
+    d2 = w * 2.0 * (g1 * den - g2 * num) / den ** 2
+    dxs = (valid_correlate_adjoint(d1 * gx1 / g1, PREWITT_X, Hd, Wd)
+           + valid_correlate_adjoint(d1 * gy1 / g1, PREWITT_Y, Hd, Wd))
+    dys = (valid_correlate_adjoint(d2 * gx2 / g2, PREWITT_X, Hd, Wd)
+           + valid_correlate_adjoint(d2 * gy2 / g2, PREWITT_Y, Hd, Wd))
+    if not downsample:
+        return dxs, dys
+
+    def spread(ds):
+        out = np.zeros((N, C, H, W))
+        out[..., :2 * Hd, :2 * Wd] = 0.25 * np.repeat(np.repeat(ds, 2, axis=-2), 2, axis=-1)
+        return out
+
+    return spread(dxs), spread(dys)
+

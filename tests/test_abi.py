@@ -36,7 +36,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 17  # 12 reference entry points + 5 extensions
+    assert len(decl) == 18  # 12 reference entry points + 6 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -86,13 +86,17 @@ def test_argument_validation_before_any_gpu_work(lib):
                                     p, p, None, 0, None) == 5  # no upstream gradient
     assert lib.fa_gpu_gmsd(p, p, 0, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, 99, p, p, 0, None) == 5
     lw = (ctypes.c_double * 3)(0.299, 0.587, 0.114)
-    assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 1, 64, 64, None, None, lw, 170.0, 0.0, 1, p, p, 99,
-                              p, p, 0, None) == 2  # luma needs 3 channels
+    assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 1, 64, 64, None, None, lw, 170.0, 0.0, 1, None, p, p,
+                              99, p, p, 0, None) == 2  # luma needs 3 channels
     bad = (ctypes.c_int64 * 3)(3 * 64 * 64, 64 * 64, 32)  # rows overlap
+    assert lib.fa_gpu_gmsd_backward(p, p, 0, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, None, None, p,
+                                    p, None, 0, None) == 1  # uint8 has no gradient
+    assert lib.fa_gpu_gmsd_backward(p, p, 3, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, None, None, p,
+                                    None, None, 0, None) == 5  # neither dx nor dy
     ws = ctypes.c_int(0)
     assert lib.fa_gpu_gmsd_workspace(64, 64, 1, ctypes.byref(ws)) == 0
-    assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 3, 64, 64, bad, None, None, 170.0, 0.0, 1, p, p,
-                              ws.value, p, p, 0, None) == 2
+    assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 3, 64, 64, bad, None, None, 170.0, 0.0, 1, None, p,
+                              p, ws.value, p, p, 0, None) == 2
     # the fused pyramid step insists on an exact level type
     cs = (1, 1, 1, 64, 64, None, None, None, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)  # f16
     assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, p, p, 3, 0, None) == 1  # float16 -> float32

@@ -214,16 +214,60 @@ def test_gmsd_identity(gpu):
     assert abs(float(fa.gms(x, x, data_range=255.0)) - 1.0) < 1e-7
 
 
-def test_gmsd_map_and_native_hint(gpu):
+@pytest.mark.parametrize("down", [True, False])
+def test_gmsd_map_native(gpu, down):
+    """The kernel writes the float32 q map (return_map=True)."""
     a, b = _plane_pair()
     x = torch.as_tensor(a, dtype=torch.uint8, device=gpu)[None, None]
     y = torch.as_tensor(b, dtype=torch.uint8, device=gpu)[None, None]
-    m = fa.gmsd(x, y, data_range=255.0, return_map=True)
-    assert m.shape == (1, 1, a.shape[0] // 2 - 2, a.shape[1] // 2 - 2)
-    assert abs(float(m.double().std(unbiased=False)) - float(fa.gmsd(x, y, data_range=255.0))) < 1e-6
+    want = ref.gms_map(a[None, None], b[None, None], 255.0, downsample=down)
     for fn in (fa.gms, fa.gmsd):
-        with pytest.raises(RuntimeError, match="native GMSD"):
-            fn(x, y, data_range=255.0, return_map=True, backend_hint="native")
+        m = fn(x, y, data_range=255.0, return_map=True, downsample=down, backend_hint="native")
+        assert m.dtype == torch.float32 and tuple(m.shape) == want.shape
+        assert np.abs(m.cpu().double().numpy() - want).max() <= 1e-6
+    xf, yf = x.float(), y.float()
+    m = fa.gmsd(xf, yf, data_range=255.0, return_map=True, downsample=down)
+    assert np.abs(m.cpu().double().numpy() - want).max() <= 1e-6
+
+
+def test_gmsd_map_luma_crop(gpu):
+    a, b = u8_pair((2, 3, 90, 120), 12.0, seed=31)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    la = ref.rgb_to_luma(ref.crop(a.astype(np.float64), 4), "bt709")
+    lb = ref.rgb_to_luma(ref.crop(b.astype(np.float64), 4), "bt709")
+    want = ref.gms_map(la, lb, 255.0)
+    m = fa.gms(x, y, data_range=255.0, return_map=True, luma="bt709", crop_border=4)
+    assert tuple(m.shape) == want.shape
+    assert np.abs(m.cpu().double().numpy() - want).max() <= 1e-6
+
+
+@pytest.mark.parametrize("down", [True, False])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+def test_gms_gmsd_gradient_matches_oracle(gpu, down, dt):
+    """The native float64 backward of per-image GMS and GMSD (both at once,
+    mixed upstream) against the float64 oracle gradient, 1e-6 normwise."""
+    rng = np.random.default_rng(17)
+    a = np.stack([_plane_pair(75, 93, seed=s)[0] for s in range(6)]).reshape(2, 3, 75, 93) / 255.0
+    b = np.clip(a + 0.05 * rng.standard_normal(a.shape), 0, 1)
+    gm = np.array([0.8, -1.1])
+    gs = np.array([1.7, 0.6])
+    x = torch.tensor(a, dtype=dt, device=gpu, requires_grad=True)
+    y = torch.tensor(b, dtype=dt, device=gpu, requires_grad=True)
+    # the oracle sees exactly the values the kernel sees (float32-rounded)
+    a, b = x.detach().cpu().double().numpy(), y.detach().cpu().double().numpy()
+    kw = dict(data_range=1.0, downsample=down, reduction="none")
+    m = fa.gms(x, y, **kw)
+    s = fa.gmsd(x, y, **kw)
+    mw, sw = ref.gmsd_stats(a, b, 1.0, downsample=down)
+    assert np.all(np.abs(m.detach().cpu().numpy() - mw) <= REL * np.abs(mw))
+    assert np.all(np.abs(s.detach().cpu().numpy() - sw) <= REL * np.abs(sw))
+    ((m * torch.tensor(gm, device=gpu)).sum() + (s * torch.tensor(gs, device=gpu)).sum()).backward()
+    wx, wy = ref.gms_stats_grad(a, b, 1.0, downsample=down, g_mean=gm, g_std=gs)
+    for got, want in ((x.grad, wx), (y.grad, wy)):
+        g = got.detach().cpu().double().numpy()
+        assert g.shape == want.shape
+        err = np.abs(g - want).max() / np.abs(want).max()
+        assert err <= 1e-6, err
 
 
 def test_gms_loss_gradient_finite(gpu):

@@ -322,3 +322,35 @@ def test_oracle_against_reference_cpu_live():
         for delta in (1.0, 4.0):
             assert abs(ref_cpu.pixel_reduce(a8, b8, "huber", delta)
                        - ref.huber(a8, b8, delta)) < 1e-6 * max(ref.huber(a8, b8, delta), 1e-12)
+
+
+@pytest.mark.parametrize("down", [True, False])
+def test_gms_stats_grad_central_differences(down):
+    """The analytic GMS / GMSD gradient against central differences of the
+    float64 forward, for a mixed upstream on both statistics (odd sizes, so
+    the dropped row / column is exercised)."""
+    rng = np.random.default_rng(3)
+    x = rng.uniform(0, 255, (2, 2, 13, 15))
+    y = np.clip(x + rng.normal(0, 20, x.shape), 0, 255)
+    gm, gs = np.array([0.7, -1.3]), np.array([2.1, 0.4])
+
+    def loss(a, b):
+        m, s = ref.gmsd_stats(a, b, 255.0, downsample=down)
+        return float((gm * m + gs * s).sum())
+
+    dx, dy = ref.gms_stats_grad(x, y, 255.0, downsample=down, g_mean=gm, g_std=gs)
+    h = 1e-3
+    for arr, grad, other_first in ((x, dx, True), (y, dy, False)):
+        num = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            p, mm = arr.copy(), arr.copy()
+            p[idx] += h
+            mm[idx] -= h
+            fp = loss(p, y) if other_first else loss(x, p)
+            fm = loss(mm, y) if other_first else loss(x, mm)
+            num[idx] = (fp - fm) / (2 * h)
+        err = np.abs(num - grad).max() / np.abs(num).max()
+        assert err < 1e-6, err
+    if down:  # the dropped odd row / column gets no gradient
+        assert np.all(dx[..., 12, :] == 0) and np.all(dx[..., :, 14] == 0)
+
