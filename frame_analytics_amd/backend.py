@@ -635,3 +635,18 @@ def gmsd_stats_bwd(x, y, mean, std, g_mean, g_std, T, eps, downsample, need_dx, 
         _ptr(dy), _dev(x), _stream(x)), ext)
     return dx, dy
 
+
+def ms_ssim_combine(terms, weights, per_image: bool):
+    """MS-SSIM's final product / channel mean / batch mean in one launch
+    (``fa_gpu_ms_ssim_combine``); ``terms`` are contiguous (N, C) float64."""
+    ext = load()
+    n, c = int(terms[0].shape[0]), int(terms[0].shape[1])
+    ts = [t.contiguous() for t in terms]
+    arr = (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+    w = (ctypes.c_double * len(ts))(*[float(v) for v in weights])
+    out = _f64(ts[0].device, n) if per_image else _f64(ts[0].device)
+    _check(ext.gpu.fa_gpu_ms_ssim_combine(
+        arr, w, len(ts), n, c, _ptr(out) if per_image else None,
+        None if per_image else _ptr(out), _dev(ts[0]), _stream(ts[0])), ext)
+    return out
+

@@ -24,6 +24,7 @@
 #include "fa_strip.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace fa {
 
@@ -54,6 +55,8 @@ struct Tiling {
 // when the chip holds `resident` workgroups at once: the TH that minimises
 // rounds x rows walked per workgroup, ceil(wgs / resident) * (TH + K + 1)
 // (K - 1 halo rows plus about two rows of set-up); ties keep the larger TH.
+// (Charging a partial round only its share was measured slower: MS-SSIM
+// 301 vs 291 us, the float64 backward 155 vs 133 us.)
 inline Tiling tiling_for(int64_t planes, int out_H, int out_W, int K, int64_t resident) {
   Tiling best = {0, 0, 0};
   int64_t best_cost = INT64_MAX;
@@ -150,7 +153,11 @@ struct SsimPol {
   int prow0, prow1, Wd;
   int64_t pool_off;
   uint32_t pcol;
-  double hx, hy;  // the even row of the current row pair
+  // pyramid sums: a 2x2 block of uint8 sums to at most 1020, exact in
+  // float32 (as is its quarter); every other input sums in float64
+  using PA = typename std::conditional<std::is_same<T, uint8_t>::value && !LUMA, float,
+                                       double>::type;
+  PA hx, hy;  // the even row of the current row pair
 
   // The forward's tap origin is 0, so rows and columns are never negative.
   // Rows past H and columns past W only feed outputs outside the map, so they
@@ -180,22 +187,25 @@ struct SsimPol {
   __device__ inline void pool(int row, const Raw& r) {
     if constexpr (MODE == MODE_CS) {
       if (!pool_on || row < prow0 || row >= prow1) return;  // uniform
-      const double vx = static_cast<double>(r.x);
-      const double vy = static_cast<double>(r.y);
+      const PA vx = static_cast<PA>(r.x);
+      const PA vy = static_cast<PA>(r.y);
       if ((row & 1) == 0) {
         hx = vx;
         hy = vy;
         return;
       }
-      double sx = hx + vx;
-      double sy = hy + vy;
+      PA sx = hx + vx;
+      PA sy = hy + vy;
       sx += __shfl_xor(sx, 1, WAVE);
       sy += __shfl_xor(sy, 1, WAVE);
       if (pcol_ok) {
         const int64_t o = pool_off + static_cast<int64_t>(row >> 1) * Wd + pcol;
         if (pool_f64) {
-          static_cast<double*>(px)[o] = fma(0.25, sx, poff);
-          static_cast<double*>(py)[o] = fma(0.25, sy, poff);
+          static_cast<double*>(px)[o] = fma(0.25, static_cast<double>(sx), poff);
+          static_cast<double*>(py)[o] = fma(0.25, static_cast<double>(sy), poff);
+        } else if constexpr (std::is_same<PA, float>::value) {
+          static_cast<float*>(px)[o] = PA(0.25) * sx;  // poff is 0 without luma
+          static_cast<float*>(py)[o] = PA(0.25) * sy;
         } else {
           static_cast<float*>(px)[o] = static_cast<float>(fma(0.25, sx, poff));
           static_cast<float*>(py)[o] = static_cast<float>(fma(0.25, sy, poff));
@@ -367,8 +377,8 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
       pol.pool_off = static_cast<int64_t>(plane) * Hd * (a.W / 2);
       pol.pcol_ok = (col & 1) == 0 && col < cend;
       pol.pcol = static_cast<uint32_t>(col >> 1);
-      pol.hx = 0.0;
-      pol.hy = 0.0;
+      pol.hx = 0;
+      pol.hy = 0;
     }
   }
 
@@ -538,6 +548,39 @@ __global__ __launch_bounds__(BLOCK) void planes2_kernel(const double* __restrict
     oa[blockIdx.x] = sa / npix;
     ob[blockIdx.x] = sb / npix;
   }
+}
+
+// MS-SSIM's last step in one launch (reference functional.py:897-901): per
+// plane prod_j max(t_j, 0)^w_j over the scales, its mean over the C channels
+// of each image, and the mean of those over the batch.
+constexpr int MS_MAX_SCALES = 8;
+struct MsTerms {
+  const double* t[MS_MAX_SCALES];  // per scale: N * C plane values
+  double w[MS_MAX_SCALES];
+};
+
+__global__ __launch_bounds__(BLOCK) void ms_combine_kernel(MsTerms terms, int M, int N, int C,
+                                                           double* __restrict__ out_per_image,
+                                                           double* __restrict__ out_total) {
+  __shared__ double smem[WAVES_PER_BLOCK];
+  double tot = 0.0;
+  for (int n = threadIdx.x; n < N; n += BLOCK) {
+    double img = 0.0;
+    for (int c = 0; c < C; ++c) {
+      const int64_t i = static_cast<int64_t>(n) * C + c;
+      double prod = 1.0;
+      for (int j = 0; j < M; ++j) {
+        const double v = terms.t[j][i];
+        prod *= pow(v > 0.0 ? v : 0.0, terms.w[j]);
+      }
+      img += prod;
+    }
+    img /= static_cast<double>(C);
+    if (out_per_image) out_per_image[n] = img;
+    tot += img;
+  }
+  tot = block_sum(tot, smem);
+  if (threadIdx.x == 0 && out_total) *out_total = tot / static_cast<double>(N);
 }
 
 // --------------------------------------------------------------------------
@@ -962,6 +1005,30 @@ FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
       static_cast<const double*>(x), static_cast<const double*>(y), nullptr, nullptr, gs, gcs,
       win, K, N, C, H, W, shift, C1, C2, aux, static_cast<double*>(dx),
       static_cast<double*>(dy), gpx, gpy, gp_dtype, device, st);
+}
+
+// No counterpart in the reference, which combines the MS-SSIM scales with
+// torch ops (functional.py:897-901).  terms: host array of M device pointers,
+// each to N * C float64 plane values (cs at the finer scales, SSIM at the
+// coarsest); weights: host array of M.  out_per_image (N) / out_total (1):
+// either may be null.
+FA_API int fa_gpu_ms_ssim_combine(const double* const* terms, const double* weights, int M,
+                                  int N, int C, double* out_per_image, double* out_total,
+                                  int device, void* stream) {
+  if (!terms || !weights) return FA_E_ARG;
+  if (M <= 0 || M > MS_MAX_SCALES || N <= 0 || C <= 0) return FA_E_SHAPE;
+  if (!out_per_image && !out_total) return FA_E_ARG;
+  MsTerms t = {};
+  for (int j = 0; j < M; ++j) {
+    if (!terms[j]) return FA_E_ARG;
+    t.t[j] = terms[j];
+    t.w[j] = weights[j];
+  }
+  FA_DEVICE_SCOPE(device);
+  hipLaunchKernelGGL(ms_combine_kernel, dim3(1), dim3(BLOCK), 0,
+                     static_cast<hipStream_t>(stream), t, M, N, C, out_per_image, out_total);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
 }
 
 }  // extern "C"

@@ -602,6 +602,9 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
                 cy = F.avg_pool2d(cy.to(wdt), 2)
             s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
             terms.append(s if i == scales - 1 else cs)
+    if native and not grad and len(w) <= 8:
+        # product, clamp, channel and batch means in one launch
+        return backend.ms_ssim_combine(terms, w, per_image=reduction == "none")
     # a fractional power of a negative factor is not real: clamp at zero
     per_plane = torch.stack(terms).clamp_min(0.0).pow(_ms_weights(w, x4.device)).prod(dim=0)
     per_image = per_plane.mean(dim=1)

@@ -285,6 +285,19 @@ FA_API int fa_gpu_gmsd_backward(const void* x, const void* y, int dtype, int N,
                                 const double* g_std, double* aux, void* dx,
                                 void* dy, int device, void* stream);
 
+/*
+ * No counterpart in the reference, which combines the MS-SSIM scales with
+ * torch ops (functional.py:897-901).  Per plane prod_j max(t_j, 0)^w_j, its
+ * mean over the C channels of each image, and the batch mean of those.
+ * terms: host array of M (<= 8) device pointers, each to N * C float64 plane
+ * values; weights: host array of M; out_per_image (N) / out_total (1) float64,
+ * either may be null but not both.
+ */
+FA_API int fa_gpu_ms_ssim_combine(const double* const* terms,
+                                  const double* weights, int M, int N, int C,
+                                  double* out_per_image, double* out_total,
+                                  int device, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 18  # 12 reference entry points + 6 extensions
+    assert len(decl) == 19  # 12 reference entry points + 7 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -93,6 +93,10 @@ def test_argument_validation_before_any_gpu_work(lib):
                                     p, None, 0, None) == 1  # uint8 has no gradient
     assert lib.fa_gpu_gmsd_backward(p, p, 3, 1, 1, 64, 64, 170.0, 0.0, 1, p, p, None, None, p,
                                     None, None, 0, None) == 5  # neither dx nor dy
+    ptrs = (ctypes.c_void_p * 5)(p, p, p, p, p)
+    wts = (ctypes.c_double * 5)(0.0448, 0.2856, 0.3001, 0.2363, 0.1333)
+    assert lib.fa_gpu_ms_ssim_combine(ptrs, wts, 9, 1, 1, p, None, 0, None) == 2  # > 8 scales
+    assert lib.fa_gpu_ms_ssim_combine(ptrs, wts, 5, 1, 1, None, None, 0, None) == 5  # no output
     ws = ctypes.c_int(0)
     assert lib.fa_gpu_gmsd_workspace(64, 64, 1, ctypes.byref(ws)) == 0
     assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 3, 64, 64, bad, None, None, 170.0, 0.0, 1, None, p,
