@@ -1,4 +1,6 @@
-"""Builds the gfx950 kernel library ``libfa_gpu.so`` in-tree with hipcc.
+"""Builds the gfx950 kernel library ``libfa_gpu.so`` in-tree with hipcc, and
+the host kernel library ``libfa_cpu.so`` (``csrc/fa_cpu.cpp``, C ABI in
+``include/fa_cpu_abi.h``) with the host C++ compiler.
 
 The library is plain HIP C++ behind the C ABI in ``include/fa_abi.h``; it
 links only the HIP runtime, whose soname (``libamdhip64.so.7``) is the one
@@ -24,10 +26,26 @@ CSRC = PKG / "csrc"
 INCLUDE = REPO / "include"
 LIBDIR = PKG / "_lib"
 LIBNAME = "libfa_gpu.so"
+CPU_LIBNAME = "libfa_cpu.so"
 
 
 def library_path() -> Path:
     return LIBDIR / LIBNAME
+
+
+def cpu_library_path() -> Path:
+    return LIBDIR / CPU_LIBNAME
+
+
+def cpu_sources() -> List[Path]:
+    return sorted(CSRC.glob("*.cpp"))
+
+
+def cxx() -> str:
+    for cand in (os.environ.get("CXX"), shutil.which("g++"), shutil.which("c++")):
+        if cand and Path(cand).exists():
+            return cand
+    raise FileNotFoundError("no host C++ compiler found (set CXX)")
 
 
 def hipcc() -> str:
@@ -70,8 +88,28 @@ def _run(cmd: Sequence[str], verbose: bool) -> None:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
 
 
+def build_cpu(verbose: bool = False) -> Path:
+    """Compile the host kernels into ``libfa_cpu.so``; returns its path.
+
+    The hot loops are built for AVX2 + FMA; ``fa_cpu_has_avx2`` (compiled into
+    the same library, safe on any x86-64) tells the loader whether it may call
+    them on the machine at hand.
+    """
+    LIBDIR.mkdir(exist_ok=True)
+    out = cpu_library_path()
+    tmp = out.with_name(f".{out.name}.{os.getpid()}.tmp")
+    cmd = [cxx(), "-O3", "-std=c++17", "-fPIC", "-shared", "-pthread", "-mavx2", "-mfma",
+           "-fvisibility=hidden", "-fno-math-errno", f"-I{INCLUDE}",
+           *map(str, cpu_sources()), "-o", str(tmp)]
+    _run(cmd, verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False, jobs: int = 0) -> Path:
-    """Compile every kernel source and link ``libfa_gpu.so``; returns its path."""
+    """Compile every kernel source and link ``libfa_gpu.so`` (and build
+    ``libfa_cpu.so``); returns the GPU library's path."""
+    build_cpu(verbose)
     cc = hipcc()
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
@@ -97,12 +135,14 @@ def build(verbose: bool = False, jobs: int = 0) -> Path:
 
 
 def is_stale() -> bool:
-    """True when the library is missing or older than any source or header."""
-    lib = library_path()
-    if not lib.exists():
-        return True
-    t = lib.stat().st_mtime
-    return any(p.stat().st_mtime > t for p in (*sources(), *headers()))
+    """True when a library is missing or older than any source or header."""
+    for lib, srcs in ((library_path(), sources()), (cpu_library_path(), cpu_sources())):
+        if not lib.exists():
+            return True
+        t = lib.stat().st_mtime
+        if any(p.stat().st_mtime > t for p in (*srcs, *headers())):
+            return True
+    return False
 
 
 if __name__ == "__main__":

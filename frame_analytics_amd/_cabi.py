@@ -1,13 +1,15 @@
-"""Loader and ctypes binder for the gfx950 kernel library.
+"""Loaders and ctypes binders for the kernel libraries.
 
 Counterpart of the reference's ``frame_analytics/_cabi.py`` (load_cuda at
-_cabi.py:515, _bind_cuda at :432-462, _check_abi at :465-471): find the
-library (building it in-tree with hipcc if it is missing), bind the
-prototypes of ``include/fa_abi.h`` and reject a library whose ABI version does
-not match this Python package.
+_cabi.py:515, load_cpu at :474-512, the binders at :414-462, _check_abi at
+:465-471): find a library (building it in-tree if it is missing), bind the
+prototypes of ``include/fa_abi.h`` / ``include/fa_cpu_abi.h`` and reject a
+library whose ABI version does not match this Python package.
 
-Unlike the reference there is no prebuilt/JIT cache directory and no CPU
-library: the only native code is ``libfa_gpu.so`` next to this file.
+Unlike the reference there is no prebuilt/JIT cache directory and no
+baseline/AVX2 pair of CPU builds: ``libfa_gpu.so`` (gfx950) and
+``libfa_cpu.so`` (x86-64 AVX2 + FMA, used only where the CPU has both) sit next
+to this file.
 """
 
 from __future__ import annotations
@@ -67,6 +69,19 @@ SIGNATURES = {
 }
 
 
+# one line per entry point of include/fa_cpu_abi.h (reference _cabi.py:416-423)
+CPU_SIGNATURES = {
+    "fa_cpu_abi_version": ([], _I),
+    "fa_cpu_has_avx2": ([], _I),
+    "fa_cpu_set_num_threads": ([_I], _I),
+    "fa_cpu_num_threads": ([], _I),
+    "fa_cpu_pixel_reduce": ([_P, _P, _I, _L, _L, _I, _D, _D, _I, _P], _I),
+    "fa_cpu_ssim": ([_P, _P, _I, _I, _I, _I, _I, _P, _I, _D, _D, _D, _P, _P], _I),
+    "fa_cpu_ssim_cs": ([_P, _P, _I, _I, _I, _I, _I, _P, _I, _D, _D, _D, _P, _P], _I),
+    "fa_cpu_gmsd": ([_P, _P, _I, _I, _I, _I, _I, _D, _D, _I, _P, _P], _I),
+}
+
+
 class KernelError(RuntimeError):
     """A native entry point returned a non-zero status."""
 
@@ -86,16 +101,16 @@ def _verbose() -> bool:
     return os.environ.get("FA_VERBOSE", "0") == "1"
 
 
-def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
-    for name, (args, res) in SIGNATURES.items():
+def bind(lib: ctypes.CDLL, signatures: Optional[dict] = None) -> ctypes.CDLL:
+    for name, (args, res) in (SIGNATURES if signatures is None else signatures).items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = res
     return lib
 
 
-def _check_abi(lib: ctypes.CDLL, origin: Path) -> None:
-    got = lib.fa_gpu_abi_version()
+def _check_abi(lib: ctypes.CDLL, origin: Path, cpu: bool = False) -> None:
+    got = lib.fa_cpu_abi_version() if cpu else lib.fa_gpu_abi_version()
     if got != FA_ABI_VERSION:
         raise RuntimeError(
             f"{origin} reports ABI version {got}, this package expects "
@@ -117,4 +132,21 @@ def load_gpu(path: Optional[Path] = None) -> Tuple[ctypes.CDLL, str]:
     # RTLD_GLOBAL is not needed: nothing links against this library.
     lib = bind(ctypes.CDLL(str(p)))
     _check_abi(lib, p)
+    return lib, origin
+
+
+def load_cpu(path: Optional[Path] = None) -> Tuple[Optional[ctypes.CDLL], str]:
+    """Return ``(lib, origin)`` for the host kernel library, or ``(None,
+    reason)`` when this CPU lacks AVX2 + FMA (the library's hot loops are
+    compiled for them; ``fa_cpu_has_avx2`` itself is safe to call anywhere).
+    Built in-tree with the host compiler when missing."""
+    p = Path(path) if path is not None else _build.cpu_library_path()
+    origin = "in-tree"
+    if not p.exists():
+        _build.build_cpu(verbose=_verbose())
+        origin = "built"
+    lib = bind(ctypes.CDLL(str(p)), CPU_SIGNATURES)
+    _check_abi(lib, p, cpu=True)
+    if not lib.fa_cpu_has_avx2():
+        return None, "host CPU lacks AVX2/FMA"
     return lib, origin

@@ -14,9 +14,15 @@ falls back to PyTorch, backend.py:215-224):
 * a kernel that returns a non-zero status raises :class:`KernelError`; there is
   no silent retry on another path.
 * ``try_*`` return ``None`` only when the native path does not apply to the
-  call by design (a CPU tensor, a gradient that the kernel cannot give, a
-  window width without a kernel); the caller then takes the portable path,
-  exactly where the reference would.
+  call by design (a gradient that the kernel cannot give, a window width
+  without a kernel, a CPU tensor on a host without the CPU library); the
+  caller then takes the portable path, exactly where the reference would.
+
+CPU tensors go to the host kernel library ``libfa_cpu.so``
+(``include/fa_cpu_abi.h``) for inference calls, as in the reference
+(backend.py:318-328, 505-515, 615-622, 656-662).  That library is optional:
+without it (or on a CPU without AVX2 + FMA) CPU tensors take the portable
+path, which is the reference's own behaviour on such hosts.
 """
 
 from __future__ import annotations
@@ -98,6 +104,47 @@ def load(force: bool = False) -> Optional[_Native]:
     return _ext
 
 
+_cpu: Any = None
+_cpu_state: Optional[str] = None  # None: not tried yet; "" loaded; else why not
+
+
+def load_cpu() -> Any:
+    """The host kernel library, or ``None`` (``FA_NATIVE=0``, a CPU without
+    AVX2 + FMA, or a library that cannot be built here).  Its pool is sized
+    to ``torch.get_num_threads()`` on first load (reference backend.py:94-97)."""
+    global _cpu, _cpu_state
+    if _cpu_state is not None:
+        return _cpu
+    if _disabled():
+        _cpu_state = "disabled via FA_NATIVE"
+        return None
+    from . import _cabi
+
+    try:
+        lib, why = _cabi.load_cpu()
+    except Exception as exc:  # no compiler / no library: the portable path serves
+        lib, why = None, f"{type(exc).__name__}: {exc}"
+    if lib is not None:
+        lib.fa_cpu_set_num_threads(int(torch.get_num_threads()))
+        why = ""
+    _cpu, _cpu_state = lib, why
+    return _cpu
+
+
+def _cpu_ready(x: torch.Tensor, y: torch.Tensor) -> Any:
+    """The host library when an inference call on CPU tensors can use it."""
+    if x.is_cuda or y.is_cuda or x.device.type != "cpu" or not _usable(x, y):
+        return None
+    if x.dim() != 4 or x.shape != y.shape or x.numel() == 0:
+        return None
+    return load_cpu()
+
+
+def _check_cpu(code: int) -> None:
+    if code != 0:
+        raise KernelError(f"host kernel returned status {code}")
+
+
 def status() -> dict:
     try:
         ext = load()
@@ -114,6 +161,8 @@ def status() -> dict:
         "error": _load_error,
         "gpu_source": None if ext is None else ext.gpu_origin,
         "gpu_library": path,
+        "cpu": load_cpu() is not None,
+        "cpu_error": _cpu_state or None,
     }
 
 
@@ -272,10 +321,29 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
     return out
 
 
+def pixel_cpu(lib: Any, x: torch.Tensor, y: torch.Tensor, *, op: int, param: float,
+              per_image: bool, psnr_bias: float) -> torch.Tensor:
+    """One host reduction (``fa_cpu_pixel_reduce``) over contiguous copies."""
+    x, y = _contig(x), _contig(y)
+    n = int(x.shape[0])
+    out = torch.empty((n,) if per_image else (), dtype=torch.float64)
+    _check_cpu(lib.fa_cpu_pixel_reduce(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, x.numel() // n, op, float(param),
+        float(psnr_bias), int(per_image), _ptr(out)))
+    return out
+
+
 def try_mse(x: torch.Tensor, y: torch.Tensor, *, per_image: bool,
             dtype: torch.dtype, psnr_bias: Optional[float] = None,
             luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
     """Squared-error reduction, or PSNR when ``psnr_bias`` (= 10 log10 L^2) is given."""
+    if not x.is_cuda:
+        lib = _cpu_ready(x, y) if luma is None else None
+        if lib is None:
+            return None
+        bias = psnr_bias if psnr_bias is not None else _PSNR_NONE
+        out = pixel_cpu(lib, x, y, op=_OP_MSE, param=0.0, per_image=per_image, psnr_bias=bias)
+        return out if dtype == torch.float64 else out.to(dtype)
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
         return None
@@ -291,6 +359,13 @@ def try_pixel(x: torch.Tensor, y: torch.Tensor, *, op: int, param: float,
               per_image: bool, dtype: torch.dtype,
               luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
     """L1 / Charbonnier / Huber reduction; ``None`` if no kernel applies."""
+    if not x.is_cuda:
+        lib = _cpu_ready(x, y) if luma is None else None
+        if lib is None:
+            return None
+        out = pixel_cpu(lib, x, y, op=op, param=param, per_image=per_image,
+                        psnr_bias=_PSNR_NONE)
+        return out if dtype == torch.float64 else out.to(dtype)
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
         return None
@@ -377,6 +452,24 @@ def ssim_backward(x, y, dL_dmap, grad_scalar, win, shift, C1, C2, need_dx, need_
     return dx, dy
 
 
+def _ssim_cpu(lib: Any, x, y, win_size, sigma, shift, C1, C2, reduction, return_map, dtype):
+    from .functional import gaussian_window_1d
+
+    x, y = _contig(x), _contig(y)
+    n, c, h, w = (int(v) for v in x.shape)
+    hout, wout = h - win_size + 1, w - win_size + 1
+    win = gaussian_window_1d(win_size, sigma, device=x.device, dtype=torch.float32).contiguous()
+    per_plane = torch.empty((n * c,), dtype=torch.float64)
+    smap = torch.empty((n, c, hout, wout), dtype=torch.float32) if return_map else None
+    _check_cpu(lib.fa_cpu_ssim(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), win_size,
+        float(shift), float(C1), float(C2), _ptr(smap), _ptr(per_plane)))
+    if return_map:
+        return smap if dtype == torch.float32 else smap.to(dtype)
+    per_image = per_plane.view(n, c).sum(dim=1) / float(hout * wout * c)
+    return per_image if reduction == "none" else per_image.mean()
+
+
 def try_ssim(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
              shift: float, C1: float, C2: float, reduction: str,
              return_map: bool, dtype: torch.dtype,
@@ -387,11 +480,19 @@ def try_ssim(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
     portable path, because the C ABI's map buffer is float32.  ``luma`` =
     (kr, kg, kb, offset) has the kernel form the luma plane of three-channel
     input itself; cropped views are read in place (``fa_gpu_ssim_ex``).
+    CPU tensors run ``fa_cpu_ssim`` (float32 arithmetic, float64 for float64
+    input), without luma or in-place crops.
     """
+    if dtype == torch.float64 and (x.dtype != torch.float64 or return_map):
+        return None
+    if not x.is_cuda:
+        lib = _cpu_ready(x, y) if luma is None and win_size in _WINDOWS else None
+        if lib is None or x.shape[-2] < win_size or x.shape[-1] < win_size:
+            return None
+        return _ssim_cpu(lib, x, y, win_size, sigma, shift, C1, C2, reduction, return_map,
+                         dtype)
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y) or win_size not in _WINDOWS:
-        return None
-    if dtype == torch.float64 and (x.dtype != torch.float64 or return_map):
         return None
     n, c = int(x.shape[0]), int(x.shape[1])
     if luma is not None and c != 3:
@@ -537,10 +638,23 @@ def ssim_cs_pool(x, y, win, shift, C1, C2, pool_dtype, luma=None):
 def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
                 shift: float, C1: float, C2: float):
     """``(ssim, cs)`` per plane, shaped ``(N, C)``; ``None`` if unavailable."""
+    k = int(win.numel())
+    if not x.is_cuda:
+        lib = _cpu_ready(x, y) if k in _WINDOWS else None
+        if lib is None or x.shape[-2] < k or x.shape[-1] < k:
+            return None
+        x, y = _contig(x), _contig(y)
+        n, c, h, w = (int(v) for v in x.shape)
+        winf = win.to(torch.float32).contiguous()
+        s = torch.empty((n * c,), dtype=torch.float64)
+        cs = torch.empty((n * c,), dtype=torch.float64)
+        _check_cpu(lib.fa_cpu_ssim_cs(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
+            float(shift), float(C1), float(C2), _ptr(s), _ptr(cs)))
+        return s.view(n, c), cs.view(n, c)
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y):
         return None
-    k = int(win.numel())
     if k not in _WINDOWS or x.shape[-2] < k or x.shape[-1] < k:
         return None
     n, c = int(x.shape[0]), int(x.shape[1])
@@ -560,8 +674,24 @@ def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsamp
 
     ``luma`` = (kr, kg, kb[, offset]) makes the kernel read the three channels
     and form the luma plane itself; cropped views are read in place through
-    their strides (``fa_gpu_gmsd_ex``).
+    their strides (``fa_gpu_gmsd_ex``).  CPU tensors run ``fa_cpu_gmsd``
+    (statistics only: no luma, no map).
     """
+    if not x.is_cuda:
+        lib = _cpu_ready(x, y) if luma is None and not want_map else None
+        if lib is None:
+            return None
+        x, y = _contig(x), _contig(y)
+        n, c, h, w = (int(v) for v in x.shape)
+        hd, wd = (h // 2, w // 2) if downsample else (h, w)
+        if hd < 3 or wd < 3:
+            return None
+        mean = torch.empty((n,), dtype=torch.float64)
+        dev = torch.empty((n,), dtype=torch.float64)
+        _check_cpu(lib.fa_cpu_gmsd(
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
+            int(downsample), _ptr(mean), _ptr(dev)))
+        return mean, dev
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y):
         return None

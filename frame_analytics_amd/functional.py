@@ -203,6 +203,10 @@ def mse(x: torch.Tensor, y: torch.Tensor, *, reduction: str = "mean",
     if fast is not None:
         return fast
     x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    if mode is not None:  # the host kernels take the luma plane formed here
+        fast = backend.try_mse(x4, y4, per_image=per_image, dtype=out_dtype)
+        if fast is not None:
+            return fast
     return _sum_sq(x4, y4, wdt, per_image).to(out_dtype)
 
 
@@ -714,6 +718,12 @@ def _gmsd_common(x, y, data_range, T, eps, downsample, dtype, luma, crop_border,
         if backend_hint == "native":
             raise RuntimeError("native GMSD backend unavailable for these inputs")
     x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    if mode is not None and backend_hint != "torch" and not return_map:
+        from . import backend  # host kernels: luma formed here
+
+        fast = backend.try_gmsd(x4, y4, T=Tv, eps=ev, downsample=downsample)
+        if fast is not None:
+            return None, fast
     q = _gms_map(x4, y4, wdt, Tv, ev, downsample)
     if return_map:
         return q, None
@@ -788,6 +798,11 @@ def _pixel_loss(name, x, y, param, reduction, dtype, out_dtype, luma, crop_borde
         if backend_hint == "native":
             raise RuntimeError(f"native {name} backend unavailable for these inputs")
     x4, y4 = _apply_luma(x4, y4, mode, L, wdt)
+    if mode is not None and backend_hint != "torch":  # host kernels: luma formed here
+        fast = backend.try_pixel(x4, y4, op=_PIXEL_OPS[name], param=param,
+                                 per_image=per_image, dtype=out_dtype)
+        if fast is not None:
+            return fast
     t = _pixel_terms(name, x4.to(wdt) - y4.to(wdt), param)
     if per_image:
         out = t.sum(dim=(1, 2, 3), dtype=torch.float64) / t[0].numel()

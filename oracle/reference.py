@@ -18,7 +18,8 @@ How each function is pinned (see tests/test_oracle.py):
     CPU C++ (oracle/_ref, built from the reference sources) at its 5e-6 gate
   * ms_ssim: single-scale special cases reduce to ssim / cs, avg-pool via torch,
     the reference CPU C++ per-scale primitive
-  * gmsd: identity, the reference CPU C++ gmsd, torch conv2d Prewitt
+  * gmsd: identity, the reference CPU C++ gmsd, torch conv2d Prewitt;
+    gmsd_stats_hp: gmsd_stats at ordinary noise, a 40-digit decimal brute force
   * ssim gradient: float64 central differences and float64 torch autograd
   * gms / gmsd gradient: float64 central differences of gmsd_stats
 """
@@ -319,6 +320,39 @@ def gmsd_stats(x, y, data_range=255.0, T=None, downsample=True, eps=None):
     f = q.reshape(q.shape[0], -1)
     m = f.mean(axis=1)
     return m, np.sqrt(((f - m[:, None]) ** 2).mean(axis=1))
+
+
+def gmsd_stats_hp(x, y, data_range=255.0, T=None, downsample=True, eps=None):
+    """The statistics of :func:`gmsd_stats`, evaluated through d = 1 - q in a
+    cancellation-free float64 form, for nearly identical images where q sits
+    within 1e-9 of 1 and ``gmsd_stats``' own rounding (~1e-16 on q) is no
+    longer small against the spread.
+
+    With s = x + y, e = x - y and P the Prewitt response (linear):
+    g1 = (Ps + Pe)/2, g2 = (Ps - Pe)/2, g1^2 - g2^2 = Pxs Pxe + Pys Pye, and
+    1 - q = (g1 - g2)^2 / (g1^2 + g2^2 + T) with
+    (g1 - g2)^2 = (G1 - G2)^2 / (sqrt G1 + sqrt G2)^2, G = g^2.  The 2x2 mean
+    is taken of e itself, not of two rounded means.  Same mathematics as the
+    reference's functional.py:959-971; pinned against ``gmsd_stats`` at
+    ordinary noise and against a 40-digit decimal brute force."""
+    x = np.asarray(x, np.float64)
+    y = np.asarray(y, np.float64)
+    L = float(data_range)
+    T = 170.0 * (L / 255.0) ** 2 if T is None else float(T)
+    eps = (1e-6 * L) ** 2 if eps is None else float(eps)
+    s, e = x + y, x - y
+    if downsample:
+        s, e = avg_pool2(s), avg_pool2(e)
+    pxs, pys = valid_correlate2d(s, PREWITT_X), valid_correlate2d(s, PREWITT_Y)
+    pxe, pye = valid_correlate2d(e, PREWITT_X), valid_correlate2d(e, PREWITT_Y)
+    G1 = 0.25 * ((pxs + pxe) ** 2 + (pys + pye) ** 2) + eps
+    G2 = 0.25 * ((pxs - pxe) ** 2 + (pys - pye) ** 2) + eps
+    dG = pxs * pxe + pys * pye
+    den = (G1 + G2 + 2.0 * np.sqrt(G1 * G2)) * (G1 + G2 + T)
+    d = np.divide(dG * dG, den, out=np.zeros_like(den), where=den > 0)
+    f = d.reshape(d.shape[0], -1)
+    m = f.mean(axis=1)
+    return 1.0 - m, np.sqrt(((f - m[:, None]) ** 2).mean(axis=1))
 
 
 # --------------------------------------------------------------------------- #

@@ -1,12 +1,14 @@
-"""The C-ABI library: builds, loads, exports exactly what include/fa_abi.h
-declares, with the ctypes prototypes the binder uses.  No compute calls (these
-run without a GPU); the status and workspace queries used here are pure host
-arithmetic."""
+"""The C-ABI libraries: build, load, export exactly what include/fa_abi.h
+(libfa_gpu.so) and include/fa_cpu_abi.h (libfa_cpu.so) declare, with the
+ctypes prototypes the binders use.  No GPU compute calls (these run without a
+GPU); the status and workspace queries used here are pure host arithmetic.
+The host library's compute is covered by tests/test_cpu_kernels.py."""
 
 from __future__ import annotations
 
 import ctypes
 import re
+import subprocess
 from pathlib import Path
 
 import pytest
@@ -14,11 +16,12 @@ import pytest
 from frame_analytics_amd import _build, _cabi
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "fa_abi.h"
+CPU_HEADER = HEADER.with_name("fa_cpu_abi.h")
 
 
-def _declared():
+def _declared(header: Path = HEADER):
     """name -> number of parameters, for every FA_API function in the header."""
-    txt = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    txt = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     out = {}
     for m in re.finditer(r"FA_API\s+[\w\s\*]+?\b(fa_\w+)\s*\(([^)]*)\)\s*;", txt, flags=re.S):
         params = m.group(2).strip()
@@ -45,6 +48,31 @@ def test_header_and_binder_agree():
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared():
         assert hasattr(lib, name), name
+
+
+def test_cpu_header_and_binder_agree():
+    decl = _declared(CPU_HEADER)
+    assert len(decl) == 8  # the reference's eight fa_cpu_* entry points
+    assert set(decl) == set(_cabi.CPU_SIGNATURES)
+    for name, n in decl.items():
+        assert len(_cabi.CPU_SIGNATURES[name][0]) == n, name
+
+
+def test_cpu_library_exports_every_declared_symbol():
+    path = _build.cpu_library_path()
+    if not path.exists():
+        _build.build_cpu()
+    lib = _cabi.bind(ctypes.CDLL(str(path)), _cabi.CPU_SIGNATURES)
+    for name in _declared(CPU_HEADER):
+        assert hasattr(lib, name), name
+    assert lib.fa_cpu_abi_version() == _cabi.FA_ABI_VERSION
+    # nothing but the declared entry points is exported
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True,
+                        text=True)
+    if nm.returncode == 0:
+        exported = {ln.split()[-1] for ln in nm.stdout.splitlines()
+                    if " T " in ln and ln.split()[-1].startswith("fa_")}
+        assert exported == set(_declared(CPU_HEADER))
 
 
 def test_abi_version_and_status_strings(lib):

@@ -192,6 +192,63 @@ def test_gmsd_against_torch_conv_and_identity():
     assert mi[0] == 1.0 and si[0] == 0.0
 
 
+def _gmsd_decimal(x, y, L, down, digits=40):
+    """Per-pixel GMS statistics of one plane in 40-digit decimal arithmetic."""
+    import decimal
+
+    ctx = decimal.Context(prec=digits)
+    D = lambda v: decimal.Decimal(float(v))  # noqa: E731  exact binary value
+    X = [[D(v) for v in row] for row in x]
+    Y = [[D(v) for v in row] for row in y]
+    if down:
+        q4 = decimal.Decimal(4)
+        pool = lambda A: [[ctx.divide(A[2 * i][2 * j] + A[2 * i][2 * j + 1] + A[2 * i + 1][2 * j]  # noqa: E731
+                                      + A[2 * i + 1][2 * j + 1], q4)
+                           for j in range(len(A[0]) // 2)] for i in range(len(A) // 2)]
+        X, Y = pool(X), pool(Y)
+    T = D(170.0 * (L / 255.0) ** 2)
+    eps = D((1e-6 * L) ** 2)
+    three = decimal.Decimal(3)
+
+    def grad(A, i, j):
+        gx = sum(A[i + r][j] - A[i + r][j + 2] for r in range(3))
+        gy = sum(A[i][j + c] - A[i + 2][j + c] for c in range(3))
+        gx, gy = ctx.divide(gx, three), ctx.divide(gy, three)
+        return ctx.sqrt(gx * gx + gy * gy + eps)
+
+    qs = []
+    for i in range(len(X) - 2):
+        for j in range(len(X[0]) - 2):
+            g1, g2 = grad(X, i, j), grad(Y, i, j)
+            qs.append(ctx.divide(2 * g1 * g2 + T, g1 * g1 + g2 * g2 + T))
+    n = decimal.Decimal(len(qs))
+    m = ctx.divide(sum(qs), n)
+    var = ctx.divide(sum((q - m) * (q - m) for q in qs), n)
+    return m, ctx.sqrt(var)
+
+
+def test_gmsd_stats_hp_pinned():
+    """gmsd_stats_hp equals gmsd_stats where both are accurate, and matches a
+    40-digit brute force on nearly identical images, where gmsd_stats' float64
+    q (rounded near 1) is not."""
+    for kind in ("natural", "uniform"):
+        a, b = natural_pair(29, 34, 9.0, seed=4, kind=kind)
+        for down in (True, False):
+            m0, s0 = ref.gmsd_stats(a[None, None], b[None, None], 255.0, downsample=down)
+            m1, s1 = ref.gmsd_stats_hp(a[None, None], b[None, None], 255.0, downsample=down)
+            assert abs(m0[0] - m1[0]) < 1e-14 and abs(s0[0] / s1[0] - 1) < 1e-12
+    rng = np.random.default_rng(11)
+    for down, shape in ((False, (8, 9)), (True, (12, 14))):
+        x = rng.random(shape)
+        y = x + 1e-7 * rng.standard_normal(shape)
+        dm, ds = _gmsd_decimal(x, y, 1.0, down)
+        m, sd = ref.gmsd_stats_hp(x[None, None], y[None, None], 1.0, downsample=down)
+        assert abs(m[0] - float(dm)) < 1e-15
+        assert abs(sd[0] / float(ds) - 1) < 1e-9
+    mi, si = ref.gmsd_stats_hp(x[None, None], x[None, None], 1.0)
+    assert mi[0] == 1.0 and si[0] == 0.0
+
+
 # --------------------------------------------------------------------------- #
 # SSIM gradient
 # --------------------------------------------------------------------------- #
