@@ -261,7 +261,26 @@ def main():
              lambda i: fa.gmsd(*pairs[i % 4], data_range=255.0, luma="bt601"))):
         c4[key] = round(_time_steps(torch, fn, reps, 5) / reps * 1e3, 4)
     c4["gmsd_GBps"] = round(2.0 * samples / (c4["gmsd_ms"] * 1e-3) / 1e9, 1)
-    del pairs, partial
+    c4["l1_ms"] = round(_time_steps(torch, lambda i: fa.l1(*pairs[i % 4]), reps, 5) / reps * 1e3, 4)
+    del partial
+    # MS-SSIM as a training loss (the reference's bench_training.py:172-200 step):
+    # x = frames / 255 in float32 with requires_grad, loss = 1 - ms_ssim, backward
+    xl = (pairs[0][0].float() / 255.0).requires_grad_(True)
+    yl = pairs[0][1].float() / 255.0
+    del pairs
+    torch.cuda.empty_cache()
+
+    def msssim_loss_step(i):
+        xl.grad = None
+        (1.0 - fa.ms_ssim(xl, yl, data_range=1.0)).backward()
+
+    lreps = max(5, reps // 4)
+    c4["ms_ssim_loss_fwd_bwd_fp32_ms"] = round(
+        _time_steps(torch, msssim_loss_step, lreps, 2) / lreps * 1e3, 3)
+    del xl, yl
+    # the reference's published RTX 3090 figures for the same calls
+    c4["reference_rtx3090_ms"] = {"ms_ssim": 3.088, "gmsd": 0.313, "l1": 0.115,
+                                  "ms_ssim_loss_fwd_bwd_fp32": 12.7}
     torch.cuda.empty_cache()
 
     # ---------------- SSIM loss, forward + backward -------- #

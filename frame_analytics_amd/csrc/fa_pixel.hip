@@ -28,7 +28,13 @@
 
 namespace fa {
 
-constexpr int PIX_UNROLL = 4;      // independent vector loads in flight per tensor
+#ifndef FA_PIX_UNROLL
+#define FA_PIX_UNROLL 4
+#endif
+#ifndef FA_PIX_WG_PER_CU
+#define FA_PIX_WG_PER_CU 8
+#endif
+constexpr int PIX_UNROLL = FA_PIX_UNROLL;  // independent vector loads in flight per tensor
 
 // Streaming loads.  Every byte is read once, so the loads are non-temporal
 // (measured on MI355X: a pure 16-byte read stream reaches ~6.7 TB/s this way
@@ -39,7 +45,7 @@ __device__ inline uint4 ld_stream(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ inline uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
-constexpr int PIX_WG_PER_CU = 8;   // workgroups per CU the grid aims for
+constexpr int PIX_WG_PER_CU = FA_PIX_WG_PER_CU;  // workgroups per CU the grid aims for
 constexpr int PIX_MIN_ELEMS_PER_THREAD = 64;
 
 // The four penalties (reference fa_cuda.cu:252-260).  Huber in the branchless
