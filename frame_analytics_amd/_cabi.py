@@ -56,13 +56,13 @@ SIGNATURES = {
           _I, _P], _I),
     "fa_gpu_ssim_cs_ex":
         ([_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _D, _D, _D, _P, _P, _I, _P, _P,
-          _P, _P, _I, _I, _P], _I),
+          _P, _P, _P, _I, _I, _P], _I),
     "fa_gpu_gmsd_ex":
         ([_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _D, _D, _I, _P, _P, _P, _I, _P, _P, _I, _P],
          _I),
     "fa_gpu_gmsd_backward":
         ([_P, _P, _I, _I, _I, _I, _I, _D, _D, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P], _I),
-    "fa_gpu_ms_ssim_combine": ([_P, _P, _I, _I, _I, _P, _P, _I, _P], _I),
+    "fa_gpu_ms_ssim_reduce": ([_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _P], _I),
     "fa_gpu_ssim_cs_backward_ex":
         ([_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _D, _D, _D, _P, _P, _I, _P, _P, _P,
           _I, _P], _I),

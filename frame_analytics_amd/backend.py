@@ -571,8 +571,40 @@ def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2, pool_dtype=None, luma=
     _check(ext.gpu.fa_gpu_ssim_cs_ex(
         _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
         _ptr(winf), k, float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
-        bpp, _ptr(out_s), _ptr(out_cs), _ptr(px), _ptr(py), pcode, _dev(x), _stream(x)), ext)
+        bpp, _ptr(out_s), _ptr(out_cs), None, _ptr(px), _ptr(py), pcode, _dev(x),
+        _stream(x)), ext)
     return (out_s, out_cs) if pool_dtype is None else (out_s, out_cs, px, py)
+
+
+def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None):
+    """One inference MS-SSIM scale left unreduced: ``(partial, partial_cs,
+    slots, npix, px, py)`` -- the per-plane partial sums of the SSIM and cs
+    maps (``slots`` per plane, packed), the plane's output pixel count, and the
+    next pyramid level (``None`` at the coarsest scale).  The partial sums go
+    to :func:`ms_ssim_reduce`; nothing is synchronised."""
+    ext = load()
+    winf = _win_f32(win)
+    n, c, h, w = x.shape
+    k = int(winf.numel())
+    cout = 1 if luma is not None else c
+    x, xs = _view_strides(x)
+    y, ys = _view_strides(y)
+    bpp = _ssim_workspace(ext, h, w, k)
+    partial = _f64(x.device, n * cout, bpp)
+    partial_cs = _f64(x.device, n * cout, bpp)
+    px = py = None
+    if pool_dtype is not None:
+        px = torch.empty((n, cout, h // 2, w // 2), dtype=pool_dtype, device=x.device)
+        py = torch.empty_like(px)
+    pcode = _DTYPE_CODE[pool_dtype if pool_dtype is not None else torch.float64]
+    slots = ctypes.c_int(0)
+    _check(ext.gpu.fa_gpu_ssim_cs_ex(
+        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
+        _ptr(winf), k, float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
+        bpp, None, None, ctypes.byref(slots), _ptr(px), _ptr(py), pcode, _dev(x),
+        _stream(x)), ext)
+    npix = float((h - k + 1) * (w - k + 1))
+    return partial, partial_cs, int(slots.value), npix, px, py
 
 
 def ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype=None):
@@ -766,17 +798,20 @@ def gmsd_stats_bwd(x, y, mean, std, g_mean, g_std, T, eps, downsample, need_dx, 
     return dx, dy
 
 
-def ms_ssim_combine(terms, weights, per_image: bool):
-    """MS-SSIM's final product / channel mean / batch mean in one launch
-    (``fa_gpu_ms_ssim_combine``); ``terms`` are contiguous (N, C) float64."""
+def ms_ssim_reduce(partials, slots, npix, weights, n: int, c: int, per_image: bool):
+    """MS-SSIM's per-scale plane reductions, clamp / power / product and the
+    channel and batch means in two launches (``fa_gpu_ms_ssim_reduce``) from
+    the partial sums of :func:`ssim_cs_partials`."""
     ext = load()
-    n, c = int(terms[0].shape[0]), int(terms[0].shape[1])
-    ts = [t.contiguous() for t in terms]
-    arr = (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
-    w = (ctypes.c_double * len(ts))(*[float(v) for v in weights])
-    out = _f64(ts[0].device, n) if per_image else _f64(ts[0].device)
-    _check(ext.gpu.fa_gpu_ms_ssim_combine(
-        arr, w, len(ts), n, c, _ptr(out) if per_image else None,
-        None if per_image else _ptr(out), _dev(ts[0]), _stream(ts[0])), ext)
+    dev = partials[0].device
+    m = len(partials)
+    arr = (ctypes.c_void_p * m)(*[t.data_ptr() for t in partials])
+    sl = (ctypes.c_int * m)(*[int(v) for v in slots])
+    npx = (ctypes.c_double * m)(*[float(v) for v in npix])
+    w = (ctypes.c_double * m)(*[float(v) for v in weights])
+    scratch = _f64(dev, m * n * c)
+    out = _f64(dev, n) if per_image else _f64(dev)
+    _check(ext.gpu.fa_gpu_ms_ssim_reduce(
+        arr, sl, npx, w, m, n, c, _ptr(scratch), _ptr(out) if per_image else None,
+        None if per_image else _ptr(out), _dev(partials[0]), _stream(partials[0])), ext)
     return out
-

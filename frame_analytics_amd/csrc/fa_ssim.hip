@@ -157,7 +157,6 @@ struct SsimPol {
   // float32 (as is its quarter); every other input sums in float64
   using PA = typename std::conditional<std::is_same<T, uint8_t>::value && !LUMA, float,
                                        double>::type;
-  PA hx, hy;  // the even row of the current row pair
 
   // The forward's tap origin is 0, so rows and columns are never negative.
   // Rows past H and columns past W only feed outputs outside the map, so they
@@ -182,20 +181,16 @@ struct SsimPol {
       return Raw{elem(x[0], ox), elem(y[0], oy)};
   }
 
-  // The 2x2 mean of rows (2i, 2i+1) and columns (2j, 2j+1), formed in float64
-  // (exact for the pyramid's element types) and written by the even lane.
-  __device__ inline void pool(int row, const Raw& r) {
+  // The 2x2 means of rows (row, row + 1), row even, and columns (2j, 2j+1),
+  // summed in PA (exact for the pyramid's element types) and written by the
+  // even lane.  The engine hands both rows of a pair at once, so there is no
+  // row-parity branch and no state between calls.
+  __device__ inline void pool2(int row, const Raw& a, const Raw& b) {
     if constexpr (MODE == MODE_CS) {
+      // prow1 is even, so row < prow1 covers row + 1 too
       if (!pool_on || row < prow0 || row >= prow1) return;  // uniform
-      const PA vx = static_cast<PA>(r.x);
-      const PA vy = static_cast<PA>(r.y);
-      if ((row & 1) == 0) {
-        hx = vx;
-        hy = vy;
-        return;
-      }
-      PA sx = hx + vx;
-      PA sy = hy + vy;
+      PA sx = static_cast<PA>(a.x) + static_cast<PA>(b.x);
+      PA sy = static_cast<PA>(a.y) + static_cast<PA>(b.y);
       sx += __shfl_xor(sx, 1, WAVE);
       sy += __shfl_xor(sy, 1, WAVE);
       if (pcol_ok) {
@@ -377,8 +372,6 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
       pol.pool_off = static_cast<int64_t>(plane) * Hd * (a.W / 2);
       pol.pcol_ok = (col & 1) == 0 && col < cend;
       pol.pcol = static_cast<uint32_t>(col >> 1);
-      pol.hx = 0;
-      pol.hy = 0;
     }
   }
 
@@ -470,7 +463,7 @@ struct ScatterPol {
   }
 
   __device__ inline void end_row() {}
-  __device__ inline void pool(int, const Raw&) {}
+  __device__ inline void pool2(int, const Raw&, const Raw&) {}
 
   // A quarter of the pyramid gradient of the 2x2 block this pixel belongs
   // to (the odd trailing row / column belongs to none).
@@ -550,31 +543,56 @@ __global__ __launch_bounds__(BLOCK) void planes2_kernel(const double* __restrict
   }
 }
 
-// MS-SSIM's last step in one launch (reference functional.py:897-901): per
-// plane prod_j max(t_j, 0)^w_j over the scales, its mean over the C channels
-// of each image, and the mean of those over the batch.
+// MS-SSIM's last steps (reference functional.py:897-901) straight from the
+// per-scale partial sums the CS passes left.  One workgroup per (plane,
+// scale) reduces that scale's slots in the order planes2_kernel uses (so the
+// plane terms are the same bits); one more workgroup clamps, raises to the
+// weights, multiplies over the scales, and takes the channel mean of each
+// image and the mean over the batch.
 constexpr int MS_MAX_SCALES = 8;
-struct MsTerms {
-  const double* t[MS_MAX_SCALES];  // per scale: N * C plane values
+struct MsParts {
+  const double* p[MS_MAX_SCALES];  // per scale: planes * slots[m] partial sums
+  int slots[MS_MAX_SCALES];
+  double npix[MS_MAX_SCALES];      // output pixels of one plane at that scale
   double w[MS_MAX_SCALES];
 };
 
-__global__ __launch_bounds__(BLOCK) void ms_combine_kernel(MsTerms terms, int M, int N, int C,
-                                                           double* __restrict__ out_per_image,
-                                                           double* __restrict__ out_total) {
+// grid (planes, M): terms[m * planes + plane] = plane mean at scale m
+__global__ __launch_bounds__(BLOCK) void ms_term_kernel(MsParts parts,
+                                                        double* __restrict__ terms) {
   __shared__ double smem[WAVES_PER_BLOCK];
+  const int plane = blockIdx.x;
+  const int m = blockIdx.y;
+  const int n = parts.slots[m];
+  const double* src = parts.p[m] + static_cast<int64_t>(plane) * n;
+  double a = 0.0;
+  for (int i = threadIdx.x; i < n; i += BLOCK) a += src[i];
+  const double sum = block_sum(a, smem);
+  if (threadIdx.x == 0)
+    terms[static_cast<int64_t>(m) * gridDim.x + plane] = sum / parts.npix[m];
+}
+
+__global__ __launch_bounds__(BLOCK) void ms_finish_kernel(MsParts parts, int M, int N, int C,
+                                                          double* __restrict__ terms,
+                                                          double* __restrict__ out_per_image,
+                                                          double* __restrict__ out_total) {
+  __shared__ double smem[WAVES_PER_BLOCK];
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  // each thread turns its planes' terms into the product over the scales,
+  // kept in the scale-0 row of `terms`
+  for (int64_t p = threadIdx.x; p < planes; p += BLOCK) {
+    double prod = 1.0;
+    for (int m = 0; m < M; ++m) {
+      const double v = terms[m * planes + p];
+      prod *= pow(v > 0.0 ? v : 0.0, parts.w[m]);
+    }
+    terms[p] = prod;
+  }
+  __syncthreads();  // global writes of this workgroup are visible to it after the barrier
   double tot = 0.0;
   for (int n = threadIdx.x; n < N; n += BLOCK) {
     double img = 0.0;
-    for (int c = 0; c < C; ++c) {
-      const int64_t i = static_cast<int64_t>(n) * C + c;
-      double prod = 1.0;
-      for (int j = 0; j < M; ++j) {
-        const double v = terms.t[j][i];
-        prod *= pow(v > 0.0 ? v : 0.0, terms.w[j]);
-      }
-      img += prod;
-    }
+    for (int c = 0; c < C; ++c) img += terms[static_cast<int64_t>(n) * C + c];
     img /= static_cast<double>(C);
     if (out_per_image) out_per_image[n] = img;
     tot += img;
@@ -792,9 +810,12 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
                         const int64_t* xs, const int64_t* ys, const double* luma,
                         const float* win, int K, double shift, double C1, double C2,
                         double* partial, double* partial_cs, int bpp, double* out_s,
-                        double* out_cs, void* px, void* py, int pool_dtype, int device,
-                        void* stream) {
-  if (!x || !y || !win || !partial || !partial_cs || !out_s || !out_cs) return FA_E_ARG;
+                        double* out_cs, int* out_slots, void* px, void* py, int pool_dtype,
+                        int device, void* stream) {
+  if (!x || !y || !win || !partial || !partial_cs) return FA_E_ARG;
+  // plane means, or (both null) the partial sums left for fa_gpu_ms_ssim_reduce
+  if ((out_s == nullptr) != (out_cs == nullptr)) return FA_E_ARG;
+  if (!out_s && !out_slots) return FA_E_ARG;
   if ((px == nullptr) != (py == nullptr)) return FA_E_ARG;
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
@@ -824,6 +845,8 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
   rc = launch_ssim<MODE_CS>(dtype, K, luma != nullptr, a, planes, device, st);
   if (rc != FA_OK) return rc;
+  if (out_slots) *out_slots = a.bpp;  // the launch packed each plane's partials this densely
+  if (!out_s) return FA_OK;
   hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
                      partial, partial_cs, a.bpp, static_cast<double>(Hout) * Wout, out_s,
                      out_cs);
@@ -918,9 +941,10 @@ FA_API int fa_gpu_ssim_cs(const void* x, const void* y, int dtype, int N,
                           double shift, double C1, double C2, double* partial,
                           double* partial_cs, int bpp, double* out_s,
                           double* out_cs, int device, void* stream) {
+  if (!out_s || !out_cs) return FA_E_ARG;
   return ssim_cs_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, win, K, shift, C1,
-                      C2, partial, partial_cs, bpp, out_s, out_cs, nullptr, nullptr, FA_F64,
-                      device, stream);
+                      C2, partial, partial_cs, bpp, out_s, out_cs, nullptr, nullptr, nullptr,
+                      FA_F64, device, stream);
 }
 
 // No counterpart in the reference (it pools between MS-SSIM scales with torch,
@@ -930,8 +954,8 @@ FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N, int
                              int W, const int64_t* x_strides, const int64_t* y_strides,
                              const double* luma, const float* win, int K, double shift,
                              double C1, double C2, double* partial, double* partial_cs,
-                             int bpp, double* out_s, double* out_cs, void* px, void* py,
-                             int pool_dtype, int device, void* stream) {
+                             int bpp, double* out_s, double* out_cs, int* out_slots,
+                             void* px, void* py, int pool_dtype, int device, void* stream) {
   if (px) {
     // float32 levels hold the pyramid of uint8 input exactly, float64 levels
     // that of every floating input; a luma plane pools into float64
@@ -940,8 +964,8 @@ FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N, int
     if (!ok) return FA_E_DTYPE;
   }
   return ssim_cs_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, win, K, shift, C1,
-                      C2, partial, partial_cs, bpp, out_s, out_cs, px, py, pool_dtype, device,
-                      stream);
+                      C2, partial, partial_cs, bpp, out_s, out_cs, out_slots, px, py, pool_dtype,
+                      device, stream);
 }
 
 // reference: fa_cuda.cu:1299-1353 (fa_cuda_ssim_backward)
@@ -1007,26 +1031,33 @@ FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
       static_cast<double*>(dy), gpx, gpy, gp_dtype, device, st);
 }
 
-// No counterpart in the reference, which combines the MS-SSIM scales with
-// torch ops (functional.py:897-901).  terms: host array of M device pointers,
-// each to N * C float64 plane values (cs at the finer scales, SSIM at the
-// coarsest); weights: host array of M.  out_per_image (N) / out_total (1):
-// either may be null.
-FA_API int fa_gpu_ms_ssim_combine(const double* const* terms, const double* weights, int M,
-                                  int N, int C, double* out_per_image, double* out_total,
-                                  int device, void* stream) {
-  if (!terms || !weights) return FA_E_ARG;
+// No counterpart in the reference, which reduces each MS-SSIM scale in its own
+// finalize launch and combines the scales with torch ops (functional.py:897-901).
+FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials, const int* slots,
+                                 const double* npix, const double* weights, int M, int N,
+                                 int C, double* plane_scratch, double* out_per_image,
+                                 double* out_total, int device, void* stream) {
+  if (!partials || !slots || !npix || !weights || !plane_scratch) return FA_E_ARG;
   if (M <= 0 || M > MS_MAX_SCALES || N <= 0 || C <= 0) return FA_E_SHAPE;
   if (!out_per_image && !out_total) return FA_E_ARG;
-  MsTerms t = {};
-  for (int j = 0; j < M; ++j) {
-    if (!terms[j]) return FA_E_ARG;
-    t.t[j] = terms[j];
-    t.w[j] = weights[j];
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  if (planes > INT32_MAX) return FA_E_SHAPE;
+  MsParts parts = {};
+  for (int m = 0; m < M; ++m) {
+    if (!partials[m]) return FA_E_ARG;
+    if (slots[m] <= 0 || !(npix[m] > 0.0)) return FA_E_SHAPE;
+    parts.p[m] = partials[m];
+    parts.slots[m] = slots[m];
+    parts.npix[m] = npix[m];
+    parts.w[m] = weights[m];
   }
   FA_DEVICE_SCOPE(device);
-  hipLaunchKernelGGL(ms_combine_kernel, dim3(1), dim3(BLOCK), 0,
-                     static_cast<hipStream_t>(stream), t, M, N, C, out_per_image, out_total);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(ms_term_kernel, dim3(static_cast<unsigned>(planes), M), dim3(BLOCK), 0, st,
+                     parts, plane_scratch);
+  FA_LAUNCH_CHECK();
+  hipLaunchKernelGGL(ms_finish_kernel, dim3(1), dim3(BLOCK), 0, st, parts, M, N, C,
+                     plane_scratch, out_per_image, out_total);
   FA_LAUNCH_CHECK();
   return FA_OK;
 }

@@ -23,7 +23,7 @@
 // What the lane loads (Pol::set_column once, Pol::load(row) per row; loads are
 // branch free, out-of-grid rows and columns are clamped or zeroed by the
 // policy), what it does with each raw row besides (Pol::pool: the MS-SSIM
-// pyramid step rides along), which moments it forms and what happens to each output pixel
+// pyramid step rides along, one (even, odd) row pair at a time), which moments it forms and what happens to each output pixel
 // (Pol::emit with a validity flag, Pol::end_row after each lane's four) is a
 // policy (see fa_ssim.hip): the SSIM forward (4 moments, float32 or
 // float64), the backward coefficient pass, and the backward scatter (the
@@ -95,12 +95,17 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
   // costs one 32-bit lane offset.
   pol.set_column(in_col);
 
+  // Rows come in (even, odd) pairs for Pol::pool2: KW - 1 and PH are even,
+  // and the forward's in_row0 (a chunk origin) is even.
+  static_assert(KW % 2 == 1 && PH % 2 == 0, "row pairs must not straddle a phase");
   CT ring[RS][NP];
 #pragma unroll
-  for (int i = 0; i < KW - 1; ++i) {
-    const Raw r = pol.load(in_row0 + i);
-    pol.pool(in_row0 + i, r);
-    pol.moments(r, ring[i]);
+  for (int i = 0; i < KW - 1; i += 2) {
+    const Raw ra = pol.load(in_row0 + i);
+    const Raw rb = pol.load(in_row0 + i + 1);
+    pol.pool2(in_row0 + i, ra, rb);
+    pol.moments(ra, ring[i]);
+    pol.moments(rb, ring[i + 1]);
   }
 
   Raw pend[PH];
@@ -116,10 +121,9 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
       const int q = qc + u;
       if (q < nph) {  // uniform across the workgroup
 #pragma unroll
-        for (int i = 0; i < PH; ++i) {
-          pol.pool(in_row0 + KW - 1 + q * PH + i, pend[i]);
-          pol.moments(pend[i], ring[(KW - 1 + u * PH + i) % RS]);
-        }
+        for (int i = 0; i < PH; i += 2) pol.pool2(in_row0 + KW - 1 + q * PH + i, pend[i], pend[i + 1]);
+#pragma unroll
+        for (int i = 0; i < PH; ++i) pol.moments(pend[i], ring[(KW - 1 + u * PH + i) % RS]);
         // Prefetch the next phase unconditionally: loads are clamped by the
         // policy, and a guard here would cost register copies every phase.
 #pragma unroll

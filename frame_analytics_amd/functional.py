@@ -583,6 +583,20 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
             x4, y4 = x4.float(), y4.float()
         pdt = torch.float64 if lw is not None else backend.pyramid_dtype(x4.dtype)
         cx, cy = x4, y4
+        if not grad and len(w) <= 8:
+            # inference: every scale leaves its partial sums, and one reduction
+            # finishes all scales (plane terms, product, channel and batch means)
+            parts, slots, npix = [], [], []
+            for i in range(scales):
+                last = i == scales - 1
+                ps, pcs, sl, npx, cx, cy = backend.ssim_cs_partials(
+                    cx, cy, win, shift, C1, C2, None if last else pdt,
+                    luma=lw if i == 0 else None)
+                parts.append(ps if last else pcs)
+                slots.append(sl)
+                npix.append(npx)
+            return backend.ms_ssim_reduce(parts, slots, npix, w, n, c,
+                                          per_image=reduction == "none")
         for i in range(scales):
             last = i == scales - 1
             if grad:
@@ -606,9 +620,6 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
                 cy = F.avg_pool2d(cy.to(wdt), 2)
             s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
             terms.append(s if i == scales - 1 else cs)
-    if native and not grad and len(w) <= 8:
-        # product, clamp, channel and batch means in one launch
-        return backend.ms_ssim_combine(terms, w, per_image=reduction == "none")
     # a fractional power of a negative factor is not real: clamp at zero
     per_plane = torch.stack(terms).clamp_min(0.0).pow(_ms_weights(w, x4.device)).prod(dim=0)
     per_image = per_plane.mean(dim=1)

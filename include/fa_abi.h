@@ -219,15 +219,21 @@ FA_API int fa_gpu_ssim_ex(const void* x, const void* y, int dtype, int N, int C,
  * so the levels of a uint8 pyramid are exact in float32 and those of float16 /
  * bfloat16 / float32 exact in float64 (unless a 2x2 block spans more than
  * 2^29 / 2^45 in magnitude; then correctly rounded).
+ * out_s / out_cs: N * Cout plane means as in fa_gpu_ssim_cs, or both null:
+ * then no finalize runs and the partial sums stay in partial / partial_cs for
+ * fa_gpu_ms_ssim_reduce.  out_slots: host int, may be null unless both means
+ * are null; receives the number of slots per plane the launch used (each
+ * plane's partial sums are packed at that stride from the start of the
+ * buffer).
  */
 FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N,
                              int C, int H, int W, const int64_t* x_strides,
                              const int64_t* y_strides, const double* luma,
                              const float* win, int K, double shift, double C1,
                              double C2, double* partial, double* partial_cs,
-                             int bpp, double* out_s, double* out_cs, void* px,
-                             void* py, int pool_dtype, int device,
-                             void* stream);
+                             int bpp, double* out_s, double* out_cs,
+                             int* out_slots, void* px, void* py,
+                             int pool_dtype, int device, void* stream);
 
 /*
  * No counterpart in the reference, which materialises a float32 luma plane
@@ -286,17 +292,25 @@ FA_API int fa_gpu_gmsd_backward(const void* x, const void* y, int dtype, int N,
                                 void* dy, int device, void* stream);
 
 /*
- * No counterpart in the reference, which combines the MS-SSIM scales with
- * torch ops (functional.py:897-901).  Per plane prod_j max(t_j, 0)^w_j, its
- * mean over the C channels of each image, and the batch mean of those.
- * terms: host array of M (<= 8) device pointers, each to N * C float64 plane
- * values; weights: host array of M; out_per_image (N) / out_total (1) float64,
- * either may be null but not both.
+ * No counterpart in the reference, which reduces every MS-SSIM scale in a
+ * finalize launch of its own and combines the scales with torch ops
+ * (functional.py:897-901).  From the partial sums fa_gpu_ssim_cs_ex left
+ * (out_s = out_cs = null): per plane t_j = (sum of its slots) / npix[j],
+ * prod_j max(t_j, 0)^w_j, the mean over the C channels of each image and the
+ * batch mean of those, in two launches.
+ *   partials: host array of M (<= 8) device pointers, scale j's partial_cs
+ *     (partial, the SSIM sums, for the coarsest scale), N * C * slots[j]
+ *     float64 each;
+ *   slots / npix / weights: host arrays of M: slots per plane (out_slots of
+ *     that scale's call), output pixels of one plane, and the weights;
+ *   plane_scratch: M * N * C float64 device scratch;
+ *   out_per_image (N) / out_total (1) float64: either may be null, not both.
  */
-FA_API int fa_gpu_ms_ssim_combine(const double* const* terms,
-                                  const double* weights, int M, int N, int C,
-                                  double* out_per_image, double* out_total,
-                                  int device, void* stream);
+FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials,
+                                 const int* slots, const double* npix,
+                                 const double* weights, int M, int N, int C,
+                                 double* plane_scratch, double* out_per_image,
+                                 double* out_total, int device, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -123,27 +123,37 @@ def test_argument_validation_before_any_gpu_work(lib):
                                     None, None, 0, None) == 5  # neither dx nor dy
     ptrs = (ctypes.c_void_p * 5)(p, p, p, p, p)
     wts = (ctypes.c_double * 5)(0.0448, 0.2856, 0.3001, 0.2363, 0.1333)
-    assert lib.fa_gpu_ms_ssim_combine(ptrs, wts, 9, 1, 1, p, None, 0, None) == 2  # > 8 scales
-    assert lib.fa_gpu_ms_ssim_combine(ptrs, wts, 5, 1, 1, None, None, 0, None) == 5  # no output
+    slots = (ctypes.c_int * 5)(4, 4, 4, 4, 4)
+    npix = (ctypes.c_double * 5)(100.0, 50.0, 20.0, 8.0, 2.0)
+    red = lib.fa_gpu_ms_ssim_reduce
+    assert red(ptrs, slots, npix, wts, 9, 1, 1, p, p, None, 0, None) == 2  # > 8 scales
+    assert red(ptrs, slots, npix, wts, 5, 1, 1, p, None, None, 0, None) == 5  # no output
+    assert red(ptrs, slots, npix, wts, 5, 1, 1, None, p, None, 0, None) == 5  # no scratch
+    zero = (ctypes.c_int * 5)(4, 0, 4, 4, 4)
+    assert red(ptrs, zero, npix, wts, 5, 1, 1, p, p, None, 0, None) == 2  # empty scale
+    # partial sums left unreduced need the slot count back, and both means go together
+    cs2 = (3, 1, 1, 64, 64, None, None, None, p, 11, 0.5, 1e-4, 9e-4, p, p, 99)
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs2, None, None, None, None, None, 4, 0, None) == 5
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs2, p, None, None, None, None, 4, 0, None) == 5
     ws = ctypes.c_int(0)
     assert lib.fa_gpu_gmsd_workspace(64, 64, 1, ctypes.byref(ws)) == 0
     assert lib.fa_gpu_gmsd_ex(p, p, 0, 1, 3, 64, 64, bad, None, None, 170.0, 0.0, 1, None, p,
                               p, ws.value, p, p, 0, None) == 2
     # the fused pyramid step insists on an exact level type
     cs = (1, 1, 1, 64, 64, None, None, None, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)  # f16
-    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, p, p, 3, 0, None) == 1  # float16 -> float32
-    assert lib.fa_gpu_ssim_cs_ex(p, p, 2, *cs[1:], p, p, 3, 0, None) == 1  # bfloat16
-    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, p, p, 0, 0, None) == 1  # uint8 levels
-    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, None, p, 4, 0, None) == 5  # one level buffer
-    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, p, p, 4, 0, None) == 5  # bpp mismatch
-    assert lib.fa_gpu_ssim_cs_ex(p, p, 0, *cs[1:], p, p, 3, 0, None) == 5  # u8 -> f32 ok
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, None, p, p, 3, 0, None) == 1  # float16 -> float32
+    assert lib.fa_gpu_ssim_cs_ex(p, p, 2, *cs[1:], None, p, p, 3, 0, None) == 1  # bfloat16
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, None, p, p, 0, 0, None) == 1  # uint8 levels
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, None, None, p, 4, 0, None) == 5  # one level buffer
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *cs, None, p, p, 4, 0, None) == 5  # bpp mismatch
+    assert lib.fa_gpu_ssim_cs_ex(p, p, 0, *cs[1:], None, p, p, 3, 0, None) == 5  # u8 -> f32 ok
     lw = (ctypes.c_double * 4)(0.299, 0.587, 0.114, 0.0)
     u8l = (0, 1, 3, 64, 64, None, None, lw, p, 11, 0.5, 1e-4, 9e-4, p, p, 99, p, p)
-    assert lib.fa_gpu_ssim_cs_ex(p, p, *u8l, p, p, 3, 0, None) == 1  # luma pools to f64
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *u8l, None, p, p, 3, 0, None) == 1  # luma pools to f64
     ws = ctypes.c_int(0)
     assert lib.fa_gpu_ssim_workspace(64, 64, 11, ctypes.byref(ws)) == 0
     one = u8l[:2] + (1,) + u8l[3:15] + (ws.value,) + u8l[16:]
-    assert lib.fa_gpu_ssim_cs_ex(p, p, *one, None, None, 4, 0, None) == 2  # luma needs 3 channels
+    assert lib.fa_gpu_ssim_cs_ex(p, p, *one, None, None, None, 4, 0, None) == 2  # luma needs 3 channels
     rows = (ctypes.c_int64 * 3)(3 * 64 * 64, 64 * 64, 60)  # rows overlap
     assert lib.fa_gpu_ssim_ex(p, p, 0, 1, 3, 64, 64, rows, None, None, p, 11, 0.5, 1e-4, 9e-4,
                               None, p, 99, None, None, 0, None) == 5  # bpp checked first

@@ -76,6 +76,43 @@ def test_ms_ssim_configs4_full_size(gpu):
     assert abs(float(fa.ms_ssim(x, y, data_range=255.0)) - float(per.mean())) < 1e-12
 
 
+@pytest.mark.parametrize("weights", [None, (0.2, 0.3, 0.5)])
+@pytest.mark.parametrize("luma", [None, "bt601"])
+def test_ms_ssim_one_reduction_matches_per_scale_means(gpu, weights, luma):
+    """The inference path leaves each scale's partial sums unreduced and
+    finishes every scale in one reduction (fa_gpu_ms_ssim_reduce).  Its result
+    equals the per-scale plane means (one finalize per scale, as the training
+    path uses them) combined on the host, for both reductions, with luma and a
+    cropped view."""
+    from frame_analytics_amd import backend
+    from frame_analytics_amd.functional import MS_SSIM_WEIGHTS, _luma_tuple, gaussian_window_1d
+
+    a, b = u8_pair((3, 3, 200, 216), 9.0, seed=21)
+    x = torch.from_numpy(a).to(gpu)[..., 2:-2, 3:-1]
+    y = torch.from_numpy(b).to(gpu)[..., 2:-2, 3:-1]
+    w = MS_SSIM_WEIGHTS if weights is None else weights
+    kw = {} if weights is None else {"weights": weights}
+    per = fa.ms_ssim(x, y, data_range=255.0, reduction="none", luma=luma, **kw)
+    tot = fa.ms_ssim(x, y, data_range=255.0, luma=luma, **kw)
+    win = gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    lw = None if luma is None else _luma_tuple(luma, 255.0)
+    pdt = torch.float64 if lw is not None else torch.float32
+    cx, cy, terms = x, y, []
+    for i in range(len(w)):
+        last = i == len(w) - 1
+        out = backend.ssim_cs_pool(cx, cy, win, 127.5, 6.5025, 58.5225, None if last else pdt,
+                                   luma=lw if i == 0 else None)
+        terms.append((out[0] if last else out[1]).double().cpu().numpy().reshape(3, -1))
+        if not last:
+            cx, cy = out[2], out[3]
+    plane = np.ones_like(terms[0])
+    for t, wi in zip(terms, w):
+        plane = plane * np.maximum(t, 0.0) ** wi
+    want = plane.mean(axis=1)
+    assert np.abs(per.cpu().numpy() - want).max() < 1e-14
+    assert abs(float(tot) - want.mean()) < 1e-14
+
+
 def test_ms_ssim_too_small(gpu):
     x = torch.zeros(1, 1, 175, 300, device=gpu)
     with pytest.raises(ValueError, match="too small"):
