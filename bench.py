@@ -22,7 +22,9 @@ committed rocprofv3 PMC summary when present.
 
 ``cpu_baseline`` times the reference's own CPU kernels (oracle/_ref, compiled
 from the reference sources) on a bounded sample of the same workload, on all
-host cores.
+host cores.  ``cpu_configs0`` runs configs[0] (1x3x512x512 uint8) through the
+``fa.*`` API on CPU tensors -- this build's host library, libfa_cpu.so -- with
+the reference CPU build's time for the same kernel beside it.
 """
 
 from __future__ import annotations
@@ -128,6 +130,69 @@ def cpu_baseline(seconds=12.0):
             "kind": "reference",
             "sample": f"reference fa_cpu_ssim (oracle/_ref, -O3 -mavx2 -mfma -ffast-math) on "
                       f"1x3x1080x1920 uint8, best of {reps} calls over ~{seconds:.0f} s"}
+
+
+def _best_of(fn, seconds):
+    fn()
+    best, reps = float("inf"), 0
+    t_end = time.perf_counter() + seconds
+    while reps < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+        reps += 1
+    return best
+
+
+def _host_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_configs0(seconds=0.6):
+    """configs[0] (1x3x512x512 uint8, sigma 8) through fa.* on CPU tensors
+    (libfa_cpu.so), each call timed best-of over ~`seconds`, and the reference
+    CPU build's kernel for the same call where it has one."""
+    import numpy as np
+    import torch
+
+    import frame_analytics_amd as fa
+    from frame_analytics_amd import backend
+    from oracle import ref_cpu
+
+    if backend.load_cpu() is None:
+        return None
+    rng = np.random.default_rng(0)
+    shape = (1, 3, 512, 512)
+    a = rng.integers(0, 256, shape, dtype=np.uint8)
+    b = np.clip(a.astype(np.int16) + np.round(rng.normal(0, 8, shape)).astype(np.int16),
+                0, 255).astype(np.uint8)
+    ta, tb = torch.from_numpy(a), torch.from_numpy(b)
+    calls = {
+        "ssim": (lambda: fa.ssim(ta, tb, data_range=255.0), lambda: ref_cpu.ssim_per_image(a, b)),
+        "psnr": (lambda: fa.psnr(ta, tb),
+                 lambda: ref_cpu.pixel_reduce(a, b, "mse", psnr_bias=20 * np.log10(255.0))),
+        "mse": (lambda: fa.mse(ta, tb), lambda: ref_cpu.pixel_reduce(a, b, "mse")),
+        "gmsd": (lambda: fa.gmsd(ta, tb, data_range=255.0), lambda: ref_cpu.gmsd(a, b)),
+        "ms_ssim": (lambda: fa.ms_ssim(ta, tb, data_range=255.0), None),
+    }
+    have_ref = ref_cpu.available()
+    if have_ref:
+        ref_cpu.load(threads=torch.get_num_threads())
+    out = {"workload": "1x3x512x512 uint8 (configs[0]), fa.* on CPU tensors",
+           "host": f"{_host_model()}, {os.cpu_count()} logical CPUs, "
+                   f"{torch.get_num_threads()} threads"}
+    for name, (mine, theirs) in calls.items():
+        row = {"ms": round(_best_of(mine, seconds) * 1e3, 4)}
+        if theirs is not None and have_ref:
+            row["reference_kernel_ms"] = round(_best_of(theirs, seconds) * 1e3, 4)
+        out[name] = row
+    return out
 
 
 def profile_sequence(launches=20):
@@ -348,6 +413,8 @@ def main():
             "kernel_ms": round(k_ms, 4),
             "valu_tflops": round(tflops, 2),
             "valu_frac_of_fp32_peak": round(tflops / FP32_PEAK_TFLOPS, 4),
+            # packed FP32 is kept off in this build: the issue ceiling is half
+            "valu_frac_of_unpacked_fp32": round(tflops / (FP32_PEAK_TFLOPS / 2), 4),
         },
         "psnr": {
             "workload": "psnr 8x3x2160x3840 uint8 (configs[2]), 2 resident pairs rotated",
@@ -362,6 +429,7 @@ def main():
         "configs3": {"workload": "1 - ssim(x, y) forward + backward, 16x3x256x256 float32",
                      "ms_per_step": round(c3_ms, 4)},
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
+        "cpu_configs0": None if args.no_cpu_baseline else cpu_configs0(),
     }
     print(json.dumps(line), flush=True)
 

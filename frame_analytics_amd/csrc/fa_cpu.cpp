@@ -58,33 +58,37 @@ class Pool {
     return size_locked();
   }
 
-  // fn(t) for every t in [0, n), on the workers and the calling thread.
+  // fn(t) for every t in [0, n), on the calling thread and whichever workers
+  // join in.  Jobs run one at a time (run_mu_).  A job is one 64-bit ticket,
+  // (job id << 32) | next task: a worker claims a task with a compare-and-swap
+  // that only succeeds while its job is still the current one, and run()
+  // returns once all n tasks have completed -- workers still asleep need not
+  // wake for it, and a late one cannot take a task of the next job.
   void run(int64_t n, const std::function<void(int64_t)>& fn) {
     if (n <= 0) return;
     std::lock_guard<std::mutex> g(run_mu_);
     start_locked();
-    const int nw = static_cast<int>(workers_.size());
-    if (nw == 0 || n == 1) {
+    if (workers_.empty() || n == 1 || n >= (int64_t(1) << 31)) {
       for (int64_t t = 0; t < n; ++t) fn(t);
       return;
     }
+    uint32_t id;
     {
       std::lock_guard<std::mutex> lk(mu_);
       fn_ = &fn;
-      n_ = n;
-      next_.store(0, std::memory_order_relaxed);
-      finished_.store(0, std::memory_order_relaxed);
-      gen_.fetch_add(1, std::memory_order_release);
+      n_.store(n, std::memory_order_relaxed);
+      done_.store(0, std::memory_order_relaxed);
+      id = ++job_;
+      ticket_.store(static_cast<uint64_t>(id) << 32, std::memory_order_release);
     }
     cv_.notify_all();
-    drain();
-    // the last workers finish their final task within microseconds: spin
-    // briefly before sleeping on the condition variable
-    if (!spin_until([&] { return finished_.load(std::memory_order_acquire) == nw; })) {
+    work(id);
+    // the last tasks finish within microseconds: spin briefly, then sleep
+    auto finished = [&] { return done_.load(std::memory_order_acquire) == n; };
+    if (!spin_until(finished)) {
       std::unique_lock<std::mutex> lk(mu_);
-      done_cv_.wait(lk, [&] { return finished_.load(std::memory_order_acquire) == nw; });
+      done_cv_.wait(lk, finished);
     }
-    fn_ = nullptr;
   }
 
   ~Pool() {
@@ -129,37 +133,42 @@ class Pool {
     for (int i = 0; i < n; ++i) workers_.emplace_back([this] { worker(); });
   }
 
-  void drain() {
+  // Claims and runs tasks of job `id` until none is left.  fn_ and n_ are
+  // read only after a successful claim: the job cannot complete (so no later
+  // job can overwrite them) while a claimed task is outstanding.
+  void work(uint32_t id) {
+    uint64_t t = ticket_.load(std::memory_order_acquire);
     for (;;) {
-      const int64_t t = next_.fetch_add(1, std::memory_order_relaxed);
-      if (t >= n_) break;
-      (*fn_)(t);
+      if (static_cast<uint32_t>(t >> 32) != id) return;
+      const int64_t idx = static_cast<int64_t>(t & 0xffffffffu);
+      const int64_t n = n_.load(std::memory_order_relaxed);
+      if (idx >= n) return;
+      if (!ticket_.compare_exchange_weak(t, t + 1, std::memory_order_acq_rel,
+                                         std::memory_order_acquire))
+        continue;  // t now holds the current ticket
+      (*fn_)(idx);
+      if (done_.fetch_add(1, std::memory_order_acq_rel) + 1 == n) {
+        std::lock_guard<std::mutex> lk(mu_);  // pairs with the waiter's predicate check
+        done_cv_.notify_all();
+      }
+      t = ticket_.load(std::memory_order_acquire);
     }
   }
 
-  // Every worker takes part in (and acknowledges) every job: run() returns
-  // only after all of them have, so the job's state is never reused early.
   void worker() {
-    uint64_t seen = 0;
+    uint32_t seen = 0;
+    auto fresh = [&] {
+      return stop_.load(std::memory_order_relaxed) ||
+             static_cast<uint32_t>(ticket_.load(std::memory_order_acquire) >> 32) != seen;
+    };
     for (;;) {
-      const bool hot = spin_until([&] {
-        return gen_.load(std::memory_order_acquire) != seen || stop_.load(std::memory_order_relaxed);
-      });
-      if (!hot) {
+      if (!spin_until(fresh)) {
         std::unique_lock<std::mutex> lk(mu_);
-        cv_.wait(lk, [&] {
-          return stop_.load(std::memory_order_relaxed) ||
-                 gen_.load(std::memory_order_relaxed) != seen;
-        });
+        cv_.wait(lk, fresh);
       }
       if (stop_.load(std::memory_order_relaxed)) return;
-      seen = gen_.load(std::memory_order_acquire);
-      drain();
-      {
-        std::lock_guard<std::mutex> lk(mu_);
-        finished_.fetch_add(1, std::memory_order_release);
-      }
-      done_cv_.notify_one();
+      seen = static_cast<uint32_t>(ticket_.load(std::memory_order_acquire) >> 32);
+      work(seen);
     }
   }
 
@@ -167,11 +176,11 @@ class Pool {
   std::mutex mu_;      // pairs with the condition variables
   std::condition_variable cv_, done_cv_;
   std::vector<std::thread> workers_;
-  const std::function<void(int64_t)>* fn_ = nullptr;  // published before gen_
-  int64_t n_ = 0;
-  std::atomic<int64_t> next_{0};
-  std::atomic<uint64_t> gen_{0};
-  std::atomic<int> finished_{0};
+  const std::function<void(int64_t)>* fn_ = nullptr;  // published before the ticket
+  std::atomic<int64_t> n_{0};  // a stale read is harmless: the claim's CAS decides
+  uint32_t job_ = 0;
+  std::atomic<uint64_t> ticket_{0};
+  std::atomic<int64_t> done_{0};
   std::atomic<bool> stop_{false};
   bool started_ = false;
   int want_ = 0;
@@ -464,6 +473,54 @@ struct SsimPlane {
   float* map;   // this plane's map or null
 };
 
+// The four moments x', y', x'y', (x'-y')^2 of one input row (x' = x - shift).
+// Out of line so that the loop keeps its no-alias facts and vectorises
+// (inlined, float32 input ran the scalar copy at twice the whole call's time).
+template <typename T, typename CT>
+__attribute__((noinline)) void ssim_moments(const T* __restrict__ xr, const T* __restrict__ yr,
+                                            int W, CT shift, CT* __restrict__ m0,
+                                            CT* __restrict__ m1, CT* __restrict__ m2,
+                                            CT* __restrict__ m3) {
+  for (int c = 0; c < W; ++c) {
+    const CT xs = to_c<CT>(xr[c]) - shift;
+    const CT ys = to_c<CT>(yr[c]) - shift;
+    const CT d = xs - ys;
+    m0[c] = xs;
+    m1[c] = ys;
+    m2[c] = xs * ys;
+    m3[c] = d * d;
+  }
+}
+
+// dst[c] = sum_j w[j] src[c + j] and dst[c] = sum_j w[j] rows[j][c], c < n:
+// each column's K taps accumulate in a register.  Out of line (and ivdep for
+// the K row pointers, which GCC would otherwise check pairwise at run time and
+// give up on past ten) so that both loops vectorise.
+template <int K, typename CT>
+__attribute__((noinline)) void filter_h(const CT* __restrict__ src, const CT* __restrict__ w,
+                                        int n, CT* __restrict__ dst) {
+  for (int c = 0; c < n; ++c) {
+    CT acc = w[0] * src[c];
+#pragma GCC unroll 11
+    for (int j = 1; j < K; ++j) acc = std::fma(w[j], src[c + j], acc);
+    dst[c] = acc;
+  }
+}
+
+template <int K, typename CT>
+__attribute__((noinline)) void filter_v(const CT* const* rows, const CT* __restrict__ w, int n,
+                                        CT* __restrict__ dst) {
+  const CT* r[K];
+  for (int j = 0; j < K; ++j) r[j] = rows[j];
+#pragma GCC ivdep
+  for (int c = 0; c < n; ++c) {
+    CT acc = w[0] * r[0][c];
+#pragma GCC unroll 11
+    for (int j = 1; j < K; ++j) acc = std::fma(w[j], r[j][c], acc);
+    dst[c] = acc;
+  }
+}
+
 // Output rows [r0, r1) of one plane; returns the sums of SSIM and cs.  K is a
 // compile-time width so that each output column's K taps accumulate in a
 // register (one load per tap, one store per column) and the column loops
@@ -486,42 +543,19 @@ void ssim_band(const SsimPlane<T, CT>& P, int r0, int r1, double* out_s, double*
   const CT k1 = CT(2) * shift * shift + P.C1;
 
   for (int i = r0; i < r1 + K - 1; ++i) {
-    const T* xr = P.x + static_cast<int64_t>(i) * W;
-    const T* yr = P.y + static_cast<int64_t>(i) * W;
-    for (int c = 0; c < W; ++c) {
-      const CT xs = to_c<CT>(xr[c]) - shift;
-      const CT ys = to_c<CT>(yr[c]) - shift;
-      const CT d = xs - ys;
-      m0[c] = xs;
-      m1[c] = ys;
-      m2[c] = xs * ys;
-      m3[c] = d * d;
-    }
+    ssim_moments<T, CT>(P.x + static_cast<int64_t>(i) * W, P.y + static_cast<int64_t>(i) * W, W,
+                        shift, m0, m1, m2, m3);
     CT* h = ring.data() + static_cast<size_t>((i - r0) % K) * 4 * Wout;
-    for (int q = 0; q < 4; ++q) {
-      const CT* __restrict__ src = m0 + static_cast<size_t>(q) * W;
-      CT* __restrict__ dst = h + static_cast<size_t>(q) * Wout;
-      for (int c = 0; c < Wout; ++c) {
-        CT acc = w[0] * src[c];
-#pragma GCC unroll 11
-        for (int j = 1; j < K; ++j) acc = std::fma(w[j], src[c + j], acc);
-        dst[c] = acc;
-      }
-    }
+    for (int q = 0; q < 4; ++q)
+      filter_h<K, CT>(m0 + static_cast<size_t>(q) * W, w, Wout, h + static_cast<size_t>(q) * Wout);
     const int o = i - (K - 1);  // the output row this input row completes
     if (o < r0) continue;
-    const CT* rows[K];
-    for (int j = 0; j < K; ++j)
-      rows[j] = ring.data() + static_cast<size_t>((o + j - r0) % K) * 4 * Wout;
     for (int q = 0; q < 4; ++q) {
-      CT* __restrict__ dst = v.data() + static_cast<size_t>(q) * Wout;
-      const size_t off = static_cast<size_t>(q) * Wout;
-      for (int c = 0; c < Wout; ++c) {
-        CT acc = w[0] * rows[0][off + c];
-#pragma GCC unroll 11
-        for (int j = 1; j < K; ++j) acc = std::fma(w[j], rows[j][off + c], acc);
-        dst[c] = acc;
-      }
+      const CT* rows[K];
+      for (int j = 0; j < K; ++j)
+        rows[j] = ring.data() + static_cast<size_t>((o + j - r0) % K) * 4 * Wout +
+                  static_cast<size_t>(q) * Wout;
+      filter_v<K, CT>(rows, w, Wout, v.data() + static_cast<size_t>(q) * Wout);
     }
     const CT* __restrict__ vx = v.data();
     const CT* __restrict__ vy = vx + Wout;

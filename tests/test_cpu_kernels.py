@@ -352,6 +352,37 @@ def test_concurrent_calls_are_serialised_and_deterministic(lib):
     assert lib.fa_cpu_num_threads() >= 1
 
 
+def test_many_small_jobs_from_several_threads(lib):
+    """Tiny jobs finish without waiting for sleeping workers, and a worker that
+    wakes late cannot take a task of the next job: 4 threads x 150 mixed calls
+    on small planes, every result equal to the single-threaded one."""
+    a, b = u8_pair((2, 3, 24, 40), 12.0, seed=8)
+    x, y = _t(a), _t(b)
+    want = (_ssim(lib, x, y, 255.0)[0], _pixel(lib, x, y, "l1"), _gmsd(lib, x, y, 255.0, False))
+    errors = []
+
+    def work(k):
+        try:
+            for i in range(150):
+                j = (i + k) % 3
+                if j == 0:
+                    assert np.array_equal(_ssim(lib, x, y, 255.0)[0], want[0])
+                elif j == 1:
+                    assert _pixel(lib, x, y, "l1") == want[1]
+                else:
+                    m, sd = _gmsd(lib, x, y, 255.0, False)
+                    assert np.array_equal(m, want[2][0]) and np.array_equal(sd, want[2][1])
+        except Exception as exc:  # surfaced below
+            errors.append(exc)
+
+    threads = [threading.Thread(target=work, args=(k,)) for k in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
 def test_python_api_routes_cpu_tensors_to_the_library(lib, monkeypatch):
     """Inference calls on CPU tensors go through fa_cpu_*; a gradient request
     and luma (formed first, then the kernel) still give the oracle's values."""
