@@ -123,6 +123,11 @@ struct SsimPol {
   struct Raw {
     CT x, y;
   };
+  // Ring rows: the four moments at float32; at float64 only x', y', whose
+  // products vtap forms per tap (exact in float64, so the sums are the same
+  // bits) -- half the ring's registers.
+  using RT = CT;
+  static constexpr int NR = sizeof(CT) == 8 ? 2 : 4;
 
   const T* __restrict__ x[CH];  // this plane of x (the R, G, B planes with luma)
   const T* __restrict__ y[CH];
@@ -209,14 +214,30 @@ struct SsimPol {
     }
   }
 
-  __device__ inline void moments(const Raw& r, CT* m) const {
+  __device__ inline void moments(const Raw& r, RT* m) const {
     const CT xs = r.x - cshift;
     const CT ys = r.y - cshift;
-    const CT d = xs - ys;
     m[0] = xs;
     m[1] = ys;
-    m[2] = xs * ys;
-    m[3] = d * d;
+    if constexpr (NR == 4) {
+      const CT d = xs - ys;
+      m[2] = xs * ys;
+      m[3] = d * d;
+    }
+  }
+
+  // v += w * (x', y', x'y', (x'-y')^2) of one ring row
+  __device__ inline void vtap(CT w, const RT* m, CT* v) const {
+    v[0] = fma(w, m[0], v[0]);
+    v[1] = fma(w, m[1], v[1]);
+    if constexpr (NR == 4) {
+      v[2] = fma(w, m[2], v[2]);
+      v[3] = fma(w, m[3], v[3]);
+    } else {
+      const CT d = m[0] - m[1];
+      v[2] = fma(w, m[0] * m[1], v[2]);
+      v[3] = fma(w, d * d, v[3]);
+    }
   }
 
   // Per output pixel, from the four filtered moments v = (E x', E y', E x'y',
@@ -419,6 +440,10 @@ struct ScatterPol {
   struct Raw {
     float v[NP];
   };
+  // the coefficient maps are float32: the ring keeps them so (half the
+  // registers) and each tap widens exactly
+  using RT = float;
+  static constexpr int NR = NP;
 
   const float* __restrict__ aux[4];  // this plane of each coefficient map
   int Hout, Wout;
@@ -457,9 +482,14 @@ struct ScatterPol {
     return v;
   }
 
-  __device__ inline void moments(const Raw& r, double* m) const {
+  __device__ inline void moments(const Raw& r, float* m) const {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) m[p] = static_cast<double>(r.v[p]);
+    for (int p = 0; p < NP; ++p) m[p] = r.v[p];
+  }
+
+  __device__ inline void vtap(double w, const float* m, double* v) const {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) v[p] = fma(w, static_cast<double>(m[p]), v[p]);
   }
 
   __device__ inline void end_row() {}
@@ -546,9 +576,9 @@ __global__ __launch_bounds__(BLOCK) void planes2_kernel(const double* __restrict
 // MS-SSIM's last steps (reference functional.py:897-901) straight from the
 // per-scale partial sums the CS passes left.  One workgroup per (plane,
 // scale) reduces that scale's slots in the order planes2_kernel uses (so the
-// plane terms are the same bits); one more workgroup clamps, raises to the
-// weights, multiplies over the scales, and takes the channel mean of each
-// image and the mean over the batch.
+// plane terms are the same bits), clamps at zero and raises to the scale's
+// weight; one more workgroup multiplies over the scales and takes the channel
+// mean of each image and the mean over the batch.
 constexpr int MS_MAX_SCALES = 8;
 struct MsParts {
   const double* p[MS_MAX_SCALES];  // per scale: planes * slots[m] partial sums
@@ -557,7 +587,7 @@ struct MsParts {
   double w[MS_MAX_SCALES];
 };
 
-// grid (planes, M): terms[m * planes + plane] = plane mean at scale m
+// grid (planes, M): terms[m * planes + plane] = max(plane mean, 0)^w[m] at scale m
 __global__ __launch_bounds__(BLOCK) void ms_term_kernel(MsParts parts,
                                                         double* __restrict__ terms) {
   __shared__ double smem[WAVES_PER_BLOCK];
@@ -568,11 +598,13 @@ __global__ __launch_bounds__(BLOCK) void ms_term_kernel(MsParts parts,
   double a = 0.0;
   for (int i = threadIdx.x; i < n; i += BLOCK) a += src[i];
   const double sum = block_sum(a, smem);
-  if (threadIdx.x == 0)
-    terms[static_cast<int64_t>(m) * gridDim.x + plane] = sum / parts.npix[m];
+  if (threadIdx.x == 0) {
+    const double v = sum / parts.npix[m];
+    terms[static_cast<int64_t>(m) * gridDim.x + plane] = pow(v > 0.0 ? v : 0.0, parts.w[m]);
+  }
 }
 
-__global__ __launch_bounds__(BLOCK) void ms_finish_kernel(MsParts parts, int M, int N, int C,
+__global__ __launch_bounds__(BLOCK) void ms_finish_kernel(int M, int N, int C,
                                                           double* __restrict__ terms,
                                                           double* __restrict__ out_per_image,
                                                           double* __restrict__ out_total) {
@@ -582,10 +614,7 @@ __global__ __launch_bounds__(BLOCK) void ms_finish_kernel(MsParts parts, int M, 
   // kept in the scale-0 row of `terms`
   for (int64_t p = threadIdx.x; p < planes; p += BLOCK) {
     double prod = 1.0;
-    for (int m = 0; m < M; ++m) {
-      const double v = terms[m * planes + p];
-      prod *= pow(v > 0.0 ? v : 0.0, parts.w[m]);
-    }
+    for (int m = 0; m < M; ++m) prod *= terms[m * planes + p];
     terms[p] = prod;
   }
   __syncthreads();  // global writes of this workgroup are visible to it after the barrier
@@ -1056,8 +1085,8 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials, const int* slots
   hipLaunchKernelGGL(ms_term_kernel, dim3(static_cast<unsigned>(planes), M), dim3(BLOCK), 0, st,
                      parts, plane_scratch);
   FA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(ms_finish_kernel, dim3(1), dim3(BLOCK), 0, st, parts, M, N, C,
-                     plane_scratch, out_per_image, out_total);
+  hipLaunchKernelGGL(ms_finish_kernel, dim3(1), dim3(BLOCK), 0, st, M, N, C, plane_scratch,
+                     out_per_image, out_total);
   FA_LAUNCH_CHECK();
   return FA_OK;
 }

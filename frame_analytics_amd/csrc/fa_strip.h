@@ -98,7 +98,13 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
   // Rows come in (even, odd) pairs for Pol::pool2: KW - 1 and PH are even,
   // and the forward's in_row0 (a chunk origin) is even.
   static_assert(KW % 2 == 1 && PH % 2 == 0, "row pairs must not straddle a phase");
-  CT ring[RS][NP];
+  // The ring holds what the policy keeps per input row (Pol::NR values of
+  // Pol::RT; Pol::moments fills a row, Pol::vtap adds one tap's weighted
+  // moments): the NP moments themselves, or fewer, narrower values the tap
+  // expands exactly, which frees registers for the float64 kernels.
+  using RT = typename Pol::RT;
+  constexpr int NR = Pol::NR;
+  RT ring[RS][NR];
 #pragma unroll
   for (int i = 0; i < KW - 1; i += 2) {
     const Raw ra = pol.load(in_row0 + i);
@@ -137,11 +143,7 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
 #pragma unroll
           for (int p = 0; p < NP; ++p) v[p] = CT(0);
 #pragma unroll
-          for (int j = 0; j < KW; ++j) {
-#pragma unroll
-            for (int p = 0; p < NP; ++p)
-              v[p] = fma(w[j], ring[(u * PH + i + j) % RS][p], v[p]);
-          }
+          for (int j = 0; j < KW; ++j) pol.vtap(w[j], ring[(u * PH + i + j) % RS], v);
 #pragma unroll
           for (int p = 0; p < NP; ++p) dst[i][p][lane] = v[p];
         }
