@@ -12,7 +12,7 @@ SSIM / MS-SSIM 1e-6 (float64 input 1e-9); GMSD / GMS 1e-6 relative on
 with the oracle on their rounded values.  On the CPU a luma plane is formed
 in the working type first (float32 below float64 input, as the reference's
 portable path does), so pixel losses and PSNR with luma are held to 1e-6
-there.
+there, and GMSD / GMS to 1e-5.
 """
 
 from __future__ import annotations
@@ -131,7 +131,8 @@ def test_sweep_case(where, i, request):
     if fn in ("gmsd", "gms"):
         # relative on the spread (gmsd) and on 1 - q (gms)
         scale = np.abs(want) if fn == "gmsd" else np.abs(1.0 - want)
-        assert np.all(np.abs(got - want) <= 1e-6 * scale + 1e-15), (cfg, got, want)
+        tol = 1e-5 if host_luma else 1e-6  # a float32 luma plane shifts the gradients
+        assert np.all(np.abs(got - want) <= tol * scale + 1e-15), (cfg, got, want)
         return
     if fn in ("ssim", "ms_ssim"):
         tol = 1e-9 if dt == torch.float64 else 1e-6
