@@ -481,6 +481,12 @@ class _FusedSSIMCSPool(torch.autograd.Function):
         ctx.save_for_backward(x, y, win)
         ctx.consts = (shift, C1, C2)
         ctx.set_materialize_grads(False)
+        # a level of an input that needs no gradient needs none either: without
+        # this the next scale would compute (and this one spread) its gradient
+        if not ctx.needs_input_grad[0]:
+            ctx.mark_non_differentiable(px)
+        if not ctx.needs_input_grad[1]:
+            ctx.mark_non_differentiable(py)
         return s, cs, px, py
 
     @staticmethod
