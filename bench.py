@@ -271,7 +271,8 @@ def main():
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the per-shard kernel is the single-GPU one; see DESIGN.md).", file=sys.stderr)
+              "(the per-shard kernel is the single-GPU one; each GPU would run it on its own "
+              "images and exchange per-image sums once).", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -343,7 +344,7 @@ def main():
     c4["ms_ssim_loss_fwd_bwd_fp32_ms"] = round(
         _time_steps(torch, msssim_loss_step, lreps, 2) / lreps * 1e3, 3)
     del xl, yl
-    # the reference's published RTX 3090 figures for the same calls
+    # the reference's published RTX 3090 figures for the same calls (its README)
     c4["reference_rtx3090_ms"] = {"ms_ssim": 3.088, "gmsd": 0.313, "l1": 0.115,
                                   "ms_ssim_loss_fwd_bwd_fp32": 12.7}
     torch.cuda.empty_cache()
