@@ -421,7 +421,7 @@ def main():
             "workload": "psnr 8x3x2160x3840 uint8 (configs[2]), 2 resident pairs rotated",
             "ms_per_step": round(p_ms, 4),
             "GBps_end_to_end": round(pbytes / (p_ms * 1e-3) / 1e9, 1),
-            "kernel": "pix_u8_kernel<MSE,16>",
+            "kernel": "pix_sweep_kernel<uint8,MSE>",
             "kernel_ms": round(pk_ms, 4),
             "GBps_kernel": round(pbytes / (pk_ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(pbytes / (pk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -74,8 +74,8 @@ __device__ inline V wave_sum(V v) {
   return v;
 }
 
-template <typename V>
-__device__ inline V block_sum(V v, V* smem /* >= WAVES_PER_BLOCK */) {
+template <typename V, int NT = BLOCK>
+__device__ inline V block_sum(V v, V* smem /* >= NT / WAVE */) {
   v = wave_sum(v);
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
@@ -84,7 +84,7 @@ __device__ inline V block_sum(V v, V* smem /* >= WAVES_PER_BLOCK */) {
   V out = V(0);
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int i = 0; i < WAVES_PER_BLOCK; ++i) out += smem[i];
+    for (int i = 0; i < NT / WAVE; ++i) out += smem[i];
   }
   return out;
 }

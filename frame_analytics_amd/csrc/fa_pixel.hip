@@ -7,9 +7,12 @@
 // count, optionally turned into dB as psnr_bias - 10*log10(mse).
 //
 // The design is CDNA4's own:
-//   * uint8 is streamed with 16-byte global loads (global_load_dwordx4), four
-//     vectors in flight per lane per tensor, so a 256-CU part keeps enough
-//     bytes outstanding to sit on the HBM roofline.
+//   * large contiguous batches (>= 4 Mi elements per image) take the sweep:
+//     one workgroup per CU walks the whole batch as one flat run of 16-byte
+//     vectors (global_load_dwordx4), so the grid reads a compact window of
+//     each tensor at any moment, and each wave follows the image edges
+//     itself (pix_sweep_kernel).  Smaller or misaligned batches take a
+//     (bpi, N) grid with four vectors in flight per lane per tensor.
 //   * the exact uint8 sums never leave the integer pipe: squared error is
 //     sum(a^2) + sum(b^2) - 2*sum(ab), three v_dot4_u32_u8 per dword pair, and
 //     absolute error is one v_sad_u8 per dword pair.  Lane sums are flushed to
@@ -47,6 +50,11 @@ __device__ inline uint4 ld_stream(const uint4* p) {
 __device__ inline uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
 constexpr int PIX_WG_PER_CU = FA_PIX_WG_PER_CU;  // workgroups per CU the grid aims for
 constexpr int PIX_MIN_ELEMS_PER_THREAD = 64;
+// Images of at least this many elements get the sweep's workspace (bpi = one
+// partial per wave of one workgroup per CU).  At 4 Mi elements one round of
+// the sweep (2 strides of 256 x 512 vectors on a 256-CU part) spans no more
+// than one image for every element size, which the sweep requires.
+constexpr int64_t PIX_SWEEP_MIN_ELEMS = int64_t(1) << 22;
 
 // The four penalties (reference fa_cuda.cu:252-260).  Huber in the branchless
 // form 0.5*min(a,d)^2 + d*(a - min(a,d)), equal to torch's HuberLoss term.
@@ -291,6 +299,231 @@ __global__ __launch_bounds__(BLOCK) void pix_float_kernel(
 }
 
 // --------------------------------------------------------------------------
+// Large contiguous images: the sweep.
+//
+// One workgroup per CU, and the whole grid walks the batch as one flat run
+// of 16-byte vectors: round r reads U gridwide strides of G*BLOCK
+// consecutive vectors from each tensor, so at any moment the workgroups read
+// a compact window of a few MB.  HBM3E serves that with better row locality
+// than a (bpi, N) grid whose workgroups stream every image at once (measured
+// on MI355X: configs[2] 55.4 us against 58.8 us per launch, 89.8% against
+// 84.6% of 8 TB/s; 8 x 3 x 1080 x 1920 uint8 15.7 against 16.1 us).
+//
+// Images are contiguous, so a wave's vectors move from image to image as the
+// run goes on.  Each wave tracks the image it is in (uniform) and the vector
+// where the next one starts.  A round that lies wholly inside the image is a
+// plain unpredicated burst of loads; only the about one round per image that
+// reaches the edge (a round spans at most U*G*BLOCK <= nv vectors, checked by
+// the host, so it touches at most two images) sorts its lanes into two
+// accumulators.  Once every lane has passed the edge the wave writes its
+// partial of that image, partial[img * bpi + wave], bpi = G * WAVES_PER_BLOCK.
+// No barrier and no LDS: a workgroup partial behind a barrier measured 3 us
+// slower per launch, and a form that predicated every load ran at 74 us (at
+// one wave per SIMD each extra instruction in a round is time with no load
+// in flight).
+// --------------------------------------------------------------------------
+// Launch shape, from a sweep on MI355X (uint8 MSE kernel time; one workgroup
+// per CU unless noted):
+//   U x threads      4Kx8   1080p RGB x8   1080p RGB x32
+//   4 x 256           55.7-56.1 us        16.8-17.2 us   58.3-58.6 us
+//   2 x 512           55.7                15.9-16.2      56.5-58.8
+//   2 x 256, 2/CU     56.6-56.7           16.0-16.4      56.4
+//   1 x 1024          57.6                15.8-15.9      58.6
+//   3 x 256           59.5-59.7           18.6-18.7      65.4-65.6
+// Two waves per SIMD with two strides in flight each keep the same bytes in
+// flight as one wave with four, but one wave's loads are issued while the
+// other sums.
+#ifndef FA_SWEEP_UNROLL
+#define FA_SWEEP_UNROLL 2
+#endif
+#ifndef FA_SWEEP_BLOCK
+#define FA_SWEEP_BLOCK 512
+#endif
+constexpr int SWEEP_UNROLL = FA_SWEEP_UNROLL;  // gridwide strides per round
+constexpr int SWEEP_BLOCK = FA_SWEEP_BLOCK;    // threads per workgroup (one per CU)
+
+template <typename T, int OP>
+struct VecAcc {
+  static constexpr bool U8 = std::is_same<T, uint8_t>::value;
+  static constexpr bool EXACT = U8 && (OP == FA_OP_MSE || OP == FA_OP_L1);
+  static constexpr bool WIDE = (OP != FA_OP_CHARB) || sizeof(T) == 8;
+  static constexpr int E = 16 / static_cast<int>(sizeof(T));
+  using A = typename std::conditional<WIDE, double, float>::type;
+
+  U8Lane<OP> u8;        // uint8
+  A part = A(0);        // float types: this round
+  double acc = 0.0;     // float types: flushed rounds
+
+  __device__ inline void add(const uint4& ra, const uint4& rb, float p8, A p) {
+    if constexpr (U8) {
+      u8.dword(ra.x, rb.x, p8);
+      u8.dword(ra.y, rb.y, p8);
+      u8.dword(ra.z, rb.z, p8);
+      u8.dword(ra.w, rb.w, p8);
+    } else {
+      T ea[E], eb[E];
+      __builtin_memcpy(ea, &ra, 16);
+      __builtin_memcpy(eb, &rb, 16);
+#pragma unroll
+      for (int k = 0; k < E; ++k) part += pix_term<OP, A>(load_as<A>(ea, k) - load_as<A>(eb, k), p);
+    }
+  }
+  // The vector's terms go to this accumulator, or to `other` where `hi` is
+  // set: lane-wise selects, no divergent branch.
+  __device__ inline void add_split(const uint4& ra, const uint4& rb, float p8, A p, bool hi,
+                                   VecAcc& other) {
+    VecAcc t;
+    t.add(ra, rb, p8, p);
+    if constexpr (U8) {
+      u8.s += hi ? 0u : t.u8.s;
+      other.u8.s += hi ? t.u8.s : 0u;
+      if constexpr (OP == FA_OP_MSE) {
+        u8.t += hi ? 0u : t.u8.t;
+        other.u8.t += hi ? t.u8.t : 0u;
+      }
+      if constexpr (!EXACT) {
+        u8.f += hi ? 0.0f : t.u8.f;
+        other.u8.f += hi ? t.u8.f : 0.0f;
+      }
+    } else {
+      part += hi ? A(0) : t.part;
+      other.part += hi ? t.part : A(0);
+    }
+  }
+  __device__ inline void flush() {
+    if constexpr (U8) {
+      u8.flush();
+    } else {
+      acc += static_cast<double>(part);
+      part = A(0);
+    }
+  }
+  __device__ inline void emit(void* partial, int64_t slot) const {
+    const bool lead = (threadIdx.x & (WAVE - 1)) == 0;
+    if constexpr (EXACT) {
+      const uint64_t s = wave_sum(u8.exact);
+      if (lead) reinterpret_cast<uint64_t*>(partial)[slot] = s;
+    } else {
+      const double s = wave_sum(U8 ? u8.wide : acc);
+      if (lead) reinterpret_cast<double*>(partial)[slot] = s;
+    }
+  }
+};
+
+template <typename T, int OP, int U = SWEEP_UNROLL, int NT = SWEEP_BLOCK>
+__global__ __launch_bounds__(NT) void pix_sweep_kernel(
+    const uint4* __restrict__ a, const uint4* __restrict__ b, int64_t nv, int n_images,
+    double param, void* __restrict__ partial) {
+  using Acc = VecAcc<T, OP>;
+  constexpr int WPB = NT / WAVE;
+  const int64_t gs = static_cast<int64_t>(gridDim.x) * NT;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+  const int64_t w0 = t0 - (threadIdx.x & (WAVE - 1));  // lane 0 of this wave
+  const int64_t total = nv * n_images;
+  const int64_t bpi = static_cast<int64_t>(gridDim.x) * WPB;
+  const int64_t wslot = static_cast<int64_t>(blockIdx.x) * WPB + threadIdx.x / WAVE;
+  const float p8 = static_cast<float>(param);
+  const typename Acc::A p = static_cast<typename Acc::A>(param);
+
+  Acc cur, nxt;        // this wave's image `img`, and the one after it
+  int img = 0;         // wave-uniform
+  int64_t edge = nv;   // first vector of image img + 1 (<= total while img < n_images)
+  // A wave stops once it has written its last image: the batch's final round
+  // can be short, and a wave past it would otherwise test its loads against
+  // an edge beyond the end of the batch.  There is no barrier, so waves may
+  // leave at different rounds.
+  for (int64_t base = 0; img < n_images; base += U * gs) {  // wave-uniform
+    uint4 xa[U], xb[U];
+    if (base + (U - 1) * gs + w0 + (WAVE - 1) < edge) {
+      // the wave's whole round lies in image img: no predication
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        xa[u] = ld_stream(a + base + u * gs + t0);
+        xb[u] = ld_stream(b + base + u * gs + t0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) cur.add(xa[u], xb[u], p8, p);
+      cur.flush();
+    } else if (base + (U - 1) * gs + w0 + (WAVE - 1) < total) {
+      // the round reaches the next image: lanes past the edge feed `nxt`
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        xa[u] = ld_stream(a + base + u * gs + t0);
+        xb[u] = ld_stream(b + base + u * gs + t0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) cur.add_split(xa[u], xb[u], p8, p, base + u * gs + t0 >= edge, nxt);
+      cur.flush();
+      nxt.flush();
+    } else {
+      // the end of the batch: loads past it are skipped
+      bool in[U], hi[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t v = base + u * gs + t0;
+        in[u] = v < total;
+        hi[u] = v >= edge;
+        xa[u] = in[u] ? ld_stream(a + v) : make_uint4(0u, 0u, 0u, 0u);
+        xb[u] = in[u] ? ld_stream(b + v) : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        // zero vectors add nothing, except Charbonnier's sqrt(0 + eps^2)
+        if (OP != FA_OP_CHARB || in[u]) {
+          if (hi[u]) nxt.add(xa[u], xb[u], p8, p);
+          else cur.add(xa[u], xb[u], p8, p);
+        }
+      }
+      cur.flush();
+      nxt.flush();
+    }
+    // emit every image all of whose vectors this wave has passed
+    const int64_t next = base + U * gs + w0;
+    while (img < n_images && next >= edge) {
+      cur.emit(partial, img * bpi + wslot);
+      cur = nxt;
+      nxt = Acc();
+      ++img;
+      edge += nv;
+    }
+  }
+}
+
+// Launch of the sweep (one wave per partial column) when it applies: 16-byte
+// aligned bases, whole vectors per image, bpi a multiple of the waves per
+// workgroup and at least U gridwide strides per image.  Returns false
+// (nothing launched) otherwise.
+template <typename T, int OP>
+static bool launch_sweep(hipStream_t st, const void* a, const void* b, int64_t n_images,
+                         int64_t per, int bpi, double param, void* partial) {
+  constexpr int64_t E = 16 / static_cast<int64_t>(sizeof(T));
+  const uintptr_t bases = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
+  constexpr int WPB = SWEEP_BLOCK / WAVE;
+  if ((bases & 15) != 0 || per % E != 0 || bpi % WPB != 0) return false;
+  const int64_t nv = per / E;
+  const int64_t G = bpi / WPB;
+  // the kernel needs a round to span no more than one image (so it touches
+  // at most two); smaller images take the per-image grid
+  if (nv < SWEEP_UNROLL * G * SWEEP_BLOCK) return false;
+  hipLaunchKernelGGL((pix_sweep_kernel<T, OP>), dim3(static_cast<unsigned>(G)), dim3(SWEEP_BLOCK), 0,
+                     st, static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
+                     static_cast<int>(n_images), param, partial);
+  return true;
+}
+
+template <typename T>
+static bool launch_sweep_op(int op, hipStream_t st, const void* a, const void* b,
+                            int64_t n_images, int64_t per, int bpi, double param,
+                            void* partial) {
+  switch (op) {
+    case FA_OP_MSE: return launch_sweep<T, FA_OP_MSE>(st, a, b, n_images, per, bpi, param, partial);
+    case FA_OP_L1: return launch_sweep<T, FA_OP_L1>(st, a, b, n_images, per, bpi, param, partial);
+    case FA_OP_CHARB: return launch_sweep<T, FA_OP_CHARB>(st, a, b, n_images, per, bpi, param, partial);
+    default: return launch_sweep<T, FA_OP_HUBER>(st, a, b, n_images, per, bpi, param, partial);
+  }
+}
+
+// --------------------------------------------------------------------------
 // strided views and luma (fa_gpu_pixel_reduce_ex): a workgroup reduces an
 // equal share of its image's (channel, row) space, lanes striding along a row
 // (dwords for 4-byte aligned uint8 rows).  With luma the difference of the
@@ -415,13 +648,44 @@ static int launch_view_dtype(int dtype, int op, bool dw, dim3 grid, hipStream_t 
 // Means are divisions by the count (reference fa_cuda.cu:177-181); a PSNR is
 // psnr_bias - 10*log10(mean), +inf for a zero mean (reference :203-208).
 // --------------------------------------------------------------------------
-__global__ __launch_bounds__(BLOCK) void finalize_kernel(
+// The finalize's workgroup size: the partials come from other XCDs' L2s, so
+// every round of dependent loads waits the full memory latency; with 1024
+// lanes and 8 loads in flight per lane the total of a configs[2] PSNR
+// (8 x 2048 partials) is two rounds (256 lanes took 5.5 us for it).
+constexpr int FIN_BLOCK = 1024;
+
+// Sum of p[begin, end) over the workgroup's lanes (this lane's share), the
+// loads of 8 strides issued together.
+template <typename V>
+__device__ inline V strided_sum(const V* __restrict__ p, int64_t begin, int64_t end) {
+  constexpr int FU = 8;
+  V acc[FU];
+#pragma unroll
+  for (int u = 0; u < FU; ++u) acc[u] = V(0);
+  int64_t i = begin + threadIdx.x;
+  for (; i + (FU - 1) * FIN_BLOCK < end; i += FU * FIN_BLOCK) {
+    V x[FU];
+#pragma unroll
+    for (int u = 0; u < FU; ++u) x[u] = p[i + u * FIN_BLOCK];
+#pragma unroll
+    for (int u = 0; u < FU; ++u) acc[u] += x[u];
+  }
+#pragma unroll
+  for (int u = 0; u < FU; ++u)
+    if (i + u * FIN_BLOCK < end) acc[u] += p[i + u * FIN_BLOCK];
+  V t = acc[0];
+#pragma unroll
+  for (int u = 1; u < FU; ++u) t += acc[u];
+  return t;
+}
+
+__global__ __launch_bounds__(FIN_BLOCK) void finalize_kernel(
     const void* __restrict__ partial, int exact, int nrows, int ncols,
     double n_per_row, double n_total, double psnr_bias,
     double* __restrict__ out_per_row, double* __restrict__ out_total,
     double* __restrict__ out_psnr_per_row, double* __restrict__ out_psnr_total) {
-  __shared__ uint64_t s_u[WAVES_PER_BLOCK];
-  __shared__ double s_d[WAVES_PER_BLOCK];
+  __shared__ uint64_t s_u[FIN_BLOCK / WAVE];
+  __shared__ double s_d[FIN_BLOCK / WAVE];
   const int row = blockIdx.x;
   const bool is_total = (row == nrows);
   const int64_t begin = is_total ? 0 : static_cast<int64_t>(row) * ncols;
@@ -429,15 +693,11 @@ __global__ __launch_bounds__(BLOCK) void finalize_kernel(
 
   double s;
   if (exact) {
-    const uint64_t* p = reinterpret_cast<const uint64_t*>(partial);
-    uint64_t acc = 0;
-    for (int64_t i = begin + threadIdx.x; i < end; i += BLOCK) acc += p[i];
-    s = static_cast<double>(block_sum(acc, s_u));
+    const uint64_t t = strided_sum(reinterpret_cast<const uint64_t*>(partial), begin, end);
+    s = static_cast<double>(block_sum<uint64_t, FIN_BLOCK>(t, s_u));
   } else {
-    const double* p = reinterpret_cast<const double*>(partial);
-    double acc = 0.0;
-    for (int64_t i = begin + threadIdx.x; i < end; i += BLOCK) acc += p[i];
-    s = block_sum(acc, s_d);
+    s = block_sum<double, FIN_BLOCK>(
+        strided_sum(reinterpret_cast<const double*>(partial), begin, end), s_d);
   }
   if (threadIdx.x == 0) {
     const double v = s / (is_total ? n_total : n_per_row);
@@ -464,7 +724,7 @@ int launch_finalize(const void* partial, bool exact, int nrows, int ncols,
                     hipStream_t st) {
   if (!out_per_row && !out_total && !out_psnr_per_row && !out_psnr_total)
     return FA_OK;
-  hipLaunchKernelGGL(finalize_kernel, dim3(nrows + 1), dim3(BLOCK), 0, st,
+  hipLaunchKernelGGL(finalize_kernel, dim3(nrows + 1), dim3(FIN_BLOCK), 0, st,
                      partial, exact ? 1 : 0, nrows, ncols, n_per_row, n_total,
                      psnr_bias, out_per_row, out_total, out_psnr_per_row,
                      out_psnr_total);
@@ -521,8 +781,13 @@ FA_API int fa_gpu_pixel_workspace(int64_t n_images, int64_t n_per_image,
                                   int device, int* out_bpi) {
   if (!out_bpi) return FA_E_ARG;
   if (n_images <= 0 || n_per_image <= 0 || n_images > 65535) return FA_E_SHAPE;
-  const int64_t by_device =
-      std::max<int64_t>(1, static_cast<int64_t>(cu_count(device)) * PIX_WG_PER_CU / n_images);
+  const int64_t cus = cu_count(device);
+  if (n_per_image >= PIX_SWEEP_MIN_ELEMS) {
+    // the sweep: one workgroup per CU, one partial per wave
+    *out_bpi = static_cast<int>(cus * (SWEEP_BLOCK / WAVE));
+    return FA_OK;
+  }
+  const int64_t by_device = std::max<int64_t>(1, cus * PIX_WG_PER_CU / n_images);
   const int64_t per_wg = static_cast<int64_t>(BLOCK) * PIX_MIN_ELEMS_PER_THREAD;
   const int64_t by_size = std::max<int64_t>(1, (n_per_image + per_wg - 1) / per_wg);
   *out_bpi = static_cast<int>(std::min(by_device, by_size));
@@ -547,7 +812,18 @@ FA_API int fa_gpu_pixel_reduce(const void* a, const void* b, int dtype,
   const uintptr_t rel = reinterpret_cast<uintptr_t>(a) - reinterpret_cast<uintptr_t>(b);
 
   bool exact = false;
-  if (dtype == FA_U8) {
+  bool swept = false;
+  switch (dtype) {
+    case FA_U8: swept = launch_sweep_op<uint8_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
+    case FA_F16: swept = launch_sweep_op<half_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
+    case FA_BF16: swept = launch_sweep_op<bf16_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
+    case FA_F32: swept = launch_sweep_op<float>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
+    case FA_F64: swept = launch_sweep_op<double>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
+    default: return FA_E_DTYPE;
+  }
+  if (swept) {
+    exact = dtype == FA_U8 && (op == FA_OP_MSE || op == FA_OP_L1);
+  } else if (dtype == FA_U8) {
     const int vec = (rel & 15) == 0 ? 16 : ((rel & 3) == 0 ? 4 : 1);
     const float p = static_cast<float>(param);
     exact = (op == FA_OP_MSE || op == FA_OP_L1);

@@ -64,6 +64,63 @@ def test_configs2_full_size_sse_exact(gpu):
                           ref.sad_u8(a, b, per_image=True).astype(np.float64) / float(n))
 
 
+@pytest.mark.parametrize("shape", [(2, 1, 2048, 2048),   # 2^22 per image: S == U strides
+                                   (3, 3, 1100, 1300),   # S = 5: a round straddles two images
+                                   (5, 3, 1080, 1920)])  # 1080p RGB frames
+def test_sweep_u8_exact(gpu, shape):
+    """Images of >= 2^22 elements take the one-workgroup-per-CU sweep; its
+    per-wave partials and image edges keep the integer sums exact."""
+    a, b = u8_pair(shape, 6.0, seed=shape[2])
+    ta, tb = _t(a, gpu), _t(b, gpu)
+    assert np.array_equal(fa.mse(ta, tb, reduction="none").cpu().numpy(), ref.mse(a, b, "none"))
+    assert float(fa.mse(ta, tb)) == ref.mse(a, b)
+    assert np.array_equal(fa.l1(ta, tb, reduction="none").cpu().numpy(), ref.l1(a, b, "none"))
+    p = fa.psnr(ta, tb, data_range=255.0, reduction="none").cpu().numpy()
+    assert np.allclose(p, ref.psnr(a, b, 255.0, "none"), rtol=1e-12, atol=0)
+    for got, want in ((fa.charbonnier(ta, tb, eps=1e-3, reduction="none"),
+                       ref.charbonnier(a, b, 1e-3, "none")),
+                      (fa.huber(ta, tb, delta=4.0, reduction="none"), ref.huber(a, b, 4.0, "none"))):
+        assert np.allclose(got.cpu().numpy(), want, rtol=1e-6, atol=0)
+
+
+def test_sweep_fallbacks_exact(gpu):
+    """Large images the sweep does not take -- a base off 16-byte alignment,
+    or an element count that is not whole 16-byte vectors -- run the per-image
+    grid with the sweep's workspace and stay exact."""
+    a, b = u8_pair((2, 1, 2049, 2051), 7.0, seed=11)   # 4202499 per image: not whole vectors
+    ta, tb = _t(a, gpu), _t(b, gpu)
+    assert np.array_equal(fa.mse(ta, tb, reduction="none").cpu().numpy(), ref.mse(a, b, "none"))
+    assert np.array_equal(fa.l1(ta, tb, reduction="none").cpu().numpy(), ref.l1(a, b, "none"))
+    n = 2 * 2048 * 2048
+    base_a, base_b = u8_pair((1, n + 16), 7.0, seed=12)
+    for off in (1, 4, 8):
+        x = _t(base_a[0], gpu)[off:off + n].view(2, 1, 2048, 2048)
+        y = _t(base_b[0], gpu)[off:off + n].view(2, 1, 2048, 2048)
+        xa = base_a[0, off:off + n].reshape(2, 1, 2048, 2048)
+        yb = base_b[0, off:off + n].reshape(2, 1, 2048, 2048)
+        assert np.array_equal(fa.mse(x, y, reduction="none").cpu().numpy(), ref.mse(xa, yb, "none"))
+        assert float(fa.l1(x, y)) == ref.l1(xa, yb)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32, torch.float64])
+def test_sweep_float_dtypes(gpu, dt):
+    a, b = u8_pair((2, 1, 2048, 2560), 12.0, seed=5)
+    xa = torch.from_numpy(a.astype(np.float64) / 255.0).to(dt)
+    xb = torch.from_numpy(b.astype(np.float64) / 255.0).to(dt)
+    a64, b64 = xa.double().numpy(), xb.double().numpy()
+    ta, tb = xa.to(gpu), xb.to(gpu)
+    cases = [
+        (fa.mse(ta, tb, reduction="none"), ref.mse(a64, b64, "none"), 1e-12),
+        (fa.l1(ta, tb, reduction="none"), ref.l1(a64, b64, "none"), 1e-12),
+        (fa.huber(ta, tb, delta=0.02, reduction="none"), ref.huber(a64, b64, 0.02, "none"), 1e-12),
+        (fa.charbonnier(ta, tb, eps=1e-3, reduction="none"), ref.charbonnier(a64, b64, 1e-3, "none"),
+         1e-12 if dt == torch.float64 else 1e-6),
+    ]
+    for got, want, tol in cases:
+        got = got.cpu().numpy()
+        assert np.allclose(got, want, rtol=tol, atol=0), (dt, got, want)
+
+
 @pytest.mark.parametrize("off_a,off_b", [(0, 0), (1, 1), (3, 3), (0, 1), (1, 2), (2, 6),
                                          (4, 8), (5, 13), (15, 0)])
 def test_unaligned_views(gpu, off_a, off_b):
