@@ -125,7 +125,7 @@ struct SrcU8Wide {
   // column pairs are clamped, so every access is inside the plane.
   __amdgpu_buffer_rsrc_t rx[CH], ry[CH];
   uint32_t shx, shy;
-  int rlim;       // last sample row a load may touch (clamp)
+  int rlo, rlim;  // first and last sample row a load may touch (clamp)
   uint32_t boff;  // this lane's byte offset in a row
   double kr, kg, kb;
 
@@ -141,6 +141,7 @@ struct SrcU8Wide {
     }
     shx = static_cast<uint32_t>(a.vx.sh);
     shy = static_cast<uint32_t>(a.vy.sh);
+    rlo = 0;
     rlim = a.Hd - 1;
     int pair = strip * (OUTW / 2) + lane;  // covers sample columns 2 pair, 2 pair + 1
     const int last = a.Wd / 2 - 1;         // Wd is even on this path
@@ -151,7 +152,8 @@ struct SrcU8Wide {
   }
 
   __device__ inline Raw load(int r) const {
-    const uint32_t ir = 2u * static_cast<uint32_t>(r < rlim ? r : rlim);
+    const int rc = r < rlo ? rlo : (r < rlim ? r : rlim);
+    const uint32_t ir = 2u * static_cast<uint32_t>(rc);
     const int ox = static_cast<int>(ir * shx), oy = static_cast<int>(ir * shy);
     Raw v;
 #pragma unroll
@@ -205,7 +207,7 @@ struct SrcGeneric {
   const T* px[CH];
   const T* py[CH];
   int64_t shx, shy;
-  int rlim;      // last sample row a load may touch (clamp)
+  int rlo, rlim;  // first and last sample row a load may touch (clamp)
   uint32_t col;  // first input column of this lane's sample
   double kr, kg, kb;
 
@@ -219,6 +221,7 @@ struct SrcGeneric {
     }
     shx = a.vx.sh;
     shy = a.vy.sh;
+    rlo = 0;
     rlim = a.Hd - 1;
     const int sc = strip * OUTW + lane;
     col = static_cast<uint32_t>(DOWN ? 2 * (sc < a.Wd ? sc : a.Wd - 1) : (sc < a.Wd ? sc : a.Wd - 1));
@@ -228,7 +231,7 @@ struct SrcGeneric {
   }
 
   __device__ inline Raw load(int r) const {
-    const int rr = r < rlim ? r : rlim;
+    const int rr = r < rlo ? rlo : (r < rlim ? r : rlim);
     const int64_t ir = DOWN ? 2 * static_cast<int64_t>(rr) : rr;
     Raw v;
 #pragma unroll
@@ -316,10 +319,13 @@ __device__ inline void mag2(double gx1, double gy1, double gx2, double gy2, doub
   dm = fma(gx1 - gx2, gx1 + gx2, (gy1 - gy2) * (gy1 + gy2));
 }
 
-// Rows [row0, row0 + rows) of one strip of one plane, added to acc / acc2.
+// Rows [row0, row0 + rows) of one strip of one plane, added to acc / acc2,
+// walked top-down, or bottom-up when `up` (uniform).  Walking up swaps the
+// window's top and bottom rows, which only flips the sign of gy: the
+// magnitudes, and so every term, are the same.
 template <class Src>
 __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int row0, int rows,
-                                double& acc, double& acc2) {
+                                bool up, double& acc, double& acc2) {
   float* const map_plane =
       a.map ? a.map + (static_cast<int64_t>(n) * a.Cout + c) * a.Hout * a.Wout : nullptr;
   using S = typename Src::S;
@@ -332,18 +338,21 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
   // Loads past the run re-read its last row (cached) instead of being
   // branched around: a conditional load group makes the compiler wait for
   // every load in flight, which would serialise the double buffering.
+  src.rlo = row0;
   src.rlim = row0 + rows + 1;
+  // sample row of step j of the walk (the window's newest row)
+  auto srow = [&](int j) { return up ? row0 + rows + 1 - j : row0 + j; };
   const int col = strip * Src::OUTW + NC * lane;  // first output column of the lane
   bool ok[NC];
 #pragma unroll
   for (int k = 0; k < NC; ++k) ok[k] = NC * lane + k < Src::OUTW && col + k < a.Wout;
 
   // every load of the prologue is in flight before the first one is used
-  const Raw p0 = src.load(row0), p1 = src.load(row0 + 1);
+  const Raw p0 = src.load(srow(0)), p1 = src.load(srow(1));
   // two named row buffers, so a group never copies the one in flight
   Raw bufA[G_PD], bufB[G_PD];
 #pragma unroll
-  for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(row0 + 2 + i);
+  for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(srow(2 + i));
   S xa[NC], xb[NC], ya[NC], yb[NC];
   src.samples(p0, xa, ya);
   src.samples(p1, xb, yb);
@@ -368,7 +377,8 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
           dm = ok[k] ? dm : S(0);
           const Acc d = one_minus_q<Src::FAST, S>(m1, m2, dm, a.eps2f, a.T2f, a.eps2, a.T2);
           if (map_plane && ok[k])  // uniform test of the pointer
-            map_plane[static_cast<int64_t>(row0 + g + i) * a.Wout + col + k] =
+            map_plane[static_cast<int64_t>(up ? row0 + rows - 1 - g - i : row0 + g + i) * a.Wout +
+                      col + k] =
                 static_cast<float>(1.0 - static_cast<double>(d));
           gs += d;
           gs2 = fma(d, d, gs2);
@@ -388,11 +398,11 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
 
   for (int g = 0; g < rows; g += 2 * G_PD) {
 #pragma unroll
-    for (int i = 0; i < G_PD; ++i) bufB[i] = src.load(row0 + 2 + g + G_PD + i);
+    for (int i = 0; i < G_PD; ++i) bufB[i] = src.load(srow(2 + g + G_PD + i));
     group(bufA, g);
     if (g + G_PD >= rows) break;
 #pragma unroll
-    for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(row0 + 2 + g + 2 * G_PD + i);
+    for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(srow(2 + g + 2 * G_PD + i));
     group(bufB, g + G_PD);
   }
 }
@@ -412,15 +422,34 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
   const int64_t e = a.rows_img * (k + 1) / a.wpi;
   const int64_t per_plane = static_cast<int64_t>(a.groups) * a.Hout;
   double acc = 0.0, acc2 = 0.0;
-  while (s < e) {  // uniform; one run per strip group touched
-    const int c = static_cast<int>(s / per_plane);
-    const int64_t rem = s - c * per_plane;
-    const int grp = static_cast<int>(rem / a.Hout);
-    const int row = static_cast<int>(rem - static_cast<int64_t>(grp) * a.Hout);
-    const int len = static_cast<int>(min(e - s, static_cast<int64_t>(a.Hout - row)));
-    const int strip = grp * WAVES_PER_BLOCK + wave;
-    if (strip < a.strips) gmsd_run<Src>(a, n, c, strip, row, len, acc, acc2);
-    s += len;
+  // Odd shares walk bottom-up, from their end: two neighbouring shares then
+  // read the sample rows around their common boundary at the same time (both
+  // at the start, or both at the end), on the same XCD (consecutive tasks
+  // share one), so the second read of those halo rows is an L2 hit.
+  if ((k & 1) == 0) {
+    while (s < e) {  // uniform; one run per strip group touched
+      const int c = static_cast<int>(s / per_plane);
+      const int64_t rem = s - c * per_plane;
+      const int grp = static_cast<int>(rem / a.Hout);
+      const int row = static_cast<int>(rem - static_cast<int64_t>(grp) * a.Hout);
+      const int len = static_cast<int>(min(e - s, static_cast<int64_t>(a.Hout - row)));
+      const int strip = grp * WAVES_PER_BLOCK + wave;
+      if (strip < a.strips) gmsd_run<Src>(a, n, c, strip, row, len, false, acc, acc2);
+      s += len;
+    }
+  } else {
+    int64_t t = e;
+    while (t > s) {  // uniform; the runs in reverse order
+      const int64_t q = t - 1;  // last row of the run
+      const int c = static_cast<int>(q / per_plane);
+      const int64_t rem = q - c * per_plane;
+      const int grp = static_cast<int>(rem / a.Hout);
+      const int rq = static_cast<int>(rem - static_cast<int64_t>(grp) * a.Hout);
+      const int len = static_cast<int>(min(t - s, static_cast<int64_t>(rq + 1)));
+      const int strip = grp * WAVES_PER_BLOCK + wave;
+      if (strip < a.strips) gmsd_run<Src>(a, n, c, strip, rq - len + 1, len, true, acc, acc2);
+      t -= len;
+    }
   }
   acc = wave_sum(acc);
   acc2 = wave_sum(acc2);
