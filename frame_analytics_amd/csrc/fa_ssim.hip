@@ -30,22 +30,25 @@ namespace fa {
 
 enum { MODE_REDUCE = 0, MODE_MAP = 1, MODE_CS = 2, MODE_PREP = 3, MODE_PREP_CS = 4 };
 
-// Output rows per workgroup (TH), one of 64, 32, 16, 8, 4.  A workgroup walks
-// its rows in sequence and re-reads K-1 halo rows, so a launch trades rounds
-// of resident workgroups against rows per workgroup (tiling_for): configs of
-// many large frames keep TH = 64, while single frames, the coarse MS-SSIM
-// scales and small crops get the parallelism back, and the float64 backward
-// kernels (one workgroup per CU) are cut only as fine as they can use.  Every
-// TH is a multiple of the phase height and even, so pyramid row pairs never
-// straddle two chunks.  The partial buffers are sized for the smallest TH
-// (the *_workspace queries) and a launch uses the first strips * chunks slots
-// of each plane.
+// Output rows per workgroup (TH), a multiple of 4 up to 128.  A workgroup
+// walks its rows in sequence and re-reads K-1 halo rows, so a launch trades
+// rounds of resident workgroups against rows per workgroup (tiling_for):
+// configs of many large frames take long chunks (configs[1]: TH = 68, 3072
+// workgroups = 3 rounds of 1024), while single frames,
+// the coarse MS-SSIM scales and small crops get the parallelism back, and the
+// float64 backward kernels (one workgroup per CU) are cut only as fine as
+// they can use.  Every TH is a multiple of the phase height and even, so
+// pyramid row pairs never straddle two chunks.  The partial buffers are
+// sized for the smallest TH (the *_workspace queries) and a launch uses the
+// first strips * chunks slots of each plane.
 #ifndef FA_SSIM_TH_MAX
-#define FA_SSIM_TH_MAX 64
+#define FA_SSIM_TH_MAX 128
 #endif
 constexpr int SSIM_TH_MAX = FA_SSIM_TH_MAX;
 constexpr int SSIM_TH_MIN = 4;
-static_assert(SSIM_TH_MIN % PH == 0 && SSIM_TH_MAX % SSIM_TH_MIN == 0, "TH ladder");
+constexpr int SSIM_TH_STEP = 4;
+static_assert(SSIM_TH_MIN % PH == 0 && SSIM_TH_STEP % PH == 0 && SSIM_TH_MAX % SSIM_TH_STEP == 0,
+              "TH ladder");
 
 struct Tiling {
   int TH, strips, tiles;  // tiles = strips * chunks, per plane
@@ -53,18 +56,25 @@ struct Tiling {
 
 // The tiling of one launch over `planes` planes of an out_H x out_W grid
 // when the chip holds `resident` workgroups at once: the TH that minimises
-// rounds x rows walked per workgroup, ceil(wgs / resident) * (TH + K + 1)
-// (K - 1 halo rows plus about two rows of set-up); ties keep the larger TH.
+// rounds x work per workgroup, ceil(wgs / resident) * (TH + (K + 1) / 2),
+// in output rows; ties keep the larger TH.  A halo row only forms its
+// moments, so the K - 1 halo rows and the set-up weigh about half as much as
+// the output rows.  Measured on MI355X (TH any multiple of 4 up to 128):
+//                           charged TH+K+1   TH+(K+1)/2   (64/32/16/8/4, TH+K+1)
+//   configs[1] kernel         156.7 us        147.4         147.6
+//   1x3x1080x1920 call         27.6            27.6          30.4
+//   MS-SSIM configs[4] call   274.4           264.4         264.5
+//   MS-SSIM loss step        1887            1848          1920
 // (Charging a partial round only its share was measured slower: MS-SSIM
 // 301 vs 291 us, the float64 backward 155 vs 133 us.)
 inline Tiling tiling_for(int64_t planes, int out_H, int out_W, int K, int64_t resident) {
   Tiling best = {0, 0, 0};
   int64_t best_cost = INT64_MAX;
-  for (int th = SSIM_TH_MAX; th >= SSIM_TH_MIN; th /= 2) {
+  for (int th = SSIM_TH_MAX; th >= SSIM_TH_MIN; th -= SSIM_TH_STEP) {
     int strips = 0, chunks = 0;
     strip_grid(out_H, out_W, K, th, &strips, &chunks);
     const int64_t wgs = planes * strips * chunks;
-    const int64_t cost = ((wgs + resident - 1) / resident) * (th + K + 1);
+    const int64_t cost = ((wgs + resident - 1) / resident) * (th + (K + 1) / 2);
     if (cost < best_cost) {
       best_cost = cost;
       best = Tiling{th, strips, strips * chunks};
