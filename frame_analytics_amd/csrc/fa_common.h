@@ -67,6 +67,38 @@ __device__ inline CT load_as(const T* p, int64_t i) {
 // valid in thread 0 only.  The order of additions is fixed, so every sum in
 // this library is deterministic run to run.
 // --------------------------------------------------------------------------
+// Lane i receives lane i+1's value; lane 63 receives 0.  One DPP move across
+// the whole wave (wave_shl:1, a VALU op) instead of the LDS round trip of
+// ds_bpermute that __shfl_down takes.
+__device__ inline int wave_next(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x130, 0xf, 0xf, true);
+}
+__device__ inline float wave_next(float v) {
+  return __int_as_float(wave_next(__float_as_int(v)));
+}
+__device__ inline double wave_next(double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = wave_next(static_cast<int>(b & 0xffffffff));
+  const int hi = wave_next(static_cast<int>(b >> 32));
+  return __longlong_as_double((static_cast<int64_t>(hi) << 32) |
+                              static_cast<int64_t>(static_cast<uint32_t>(lo)));
+}
+
+// Lane i receives lane i ^ 1's value: DPP quad_perm:[1,0,3,2], a VALU op.
+__device__ inline int lane_xor1(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);
+}
+__device__ inline float lane_xor1(float v) {
+  return __int_as_float(lane_xor1(__float_as_int(v)));
+}
+__device__ inline double lane_xor1(double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = lane_xor1(static_cast<int>(b & 0xffffffff));
+  const int hi = lane_xor1(static_cast<int>(b >> 32));
+  return __longlong_as_double((static_cast<int64_t>(hi) << 32) |
+                              static_cast<int64_t>(static_cast<uint32_t>(lo)));
+}
+
 template <typename V>
 __device__ inline V wave_sum(V v) {
 #pragma unroll

@@ -287,15 +287,17 @@ __device__ inline void prewitt(const S (&a)[NC], const S (&b)[NC], const S (&c)[
     cs[k] = a[k] + b[k] + c[k];  // column sums, differenced across for gx
     rd[k] = a[k] - c[k];         // row differences, summed across for gy
   }
+  // neighbours by DPP; the last lanes' are zero, and those lanes' columns lie
+  // past the strip's output (masked by the caller)
   if constexpr (NC >= 2) {
-    cs[NC] = __shfl_down(cs[0], 1, WAVE);
-    cs[NC + 1] = __shfl_down(cs[1], 1, WAVE);
-    rd[NC] = __shfl_down(rd[0], 1, WAVE);
-    rd[NC + 1] = __shfl_down(rd[1], 1, WAVE);
+    cs[NC] = wave_next(cs[0]);
+    cs[NC + 1] = wave_next(cs[1]);
+    rd[NC] = wave_next(rd[0]);
+    rd[NC + 1] = wave_next(rd[1]);
   } else {
-    cs[2] = __shfl_down(cs[0], 2, WAVE);
-    rd[1] = __shfl_down(rd[0], 1, WAVE);
-    rd[2] = __shfl_down(rd[0], 2, WAVE);
+    cs[2] = wave_next(wave_next(cs[0]));
+    rd[1] = wave_next(rd[0]);
+    rd[2] = wave_next(rd[1]);
   }
 #pragma unroll
   for (int k = 0; k < NC; ++k) {

@@ -206,8 +206,8 @@ struct SsimPol {
       if (!pool_on || row < prow0 || row >= prow1) return;  // uniform
       PA sx = static_cast<PA>(a.x) + static_cast<PA>(b.x);
       PA sy = static_cast<PA>(a.y) + static_cast<PA>(b.y);
-      sx += __shfl_xor(sx, 1, WAVE);
-      sy += __shfl_xor(sy, 1, WAVE);
+      sx += lane_xor1(sx);
+      sy += lane_xor1(sy);
       if (pcol_ok) {
         const int64_t o = pool_off + static_cast<int64_t>(row >> 1) * Wd + pcol;
         if (pool_f64) {
