@@ -893,7 +893,14 @@ FA_API int fa_gpu_pixel_reduce_ex(const void* a, const void* b, int dtype, int64
     v.kg = luma[1];
     v.kb = luma[2];
   }
-  v.bpi = bpi;
+  // The view kernel wants the (bpi, N) grid's own size, not the sweep's
+  // larger workspace: it uses the first `cols` partial slots of each image,
+  // packed (measured at 8x3x2160x3840: crop 4, 85 against 91 us; luma, 106
+  // against 126 us with all 2048 columns).
+  const int64_t cus = cu_count(device);
+  const int cols = static_cast<int>(std::max<int64_t>(
+      1, std::min<int64_t>(bpi, std::max<int64_t>(1, cus * PIX_WG_PER_CU / n_images))));
+  v.bpi = cols;
   v.param = param;
   v.partial = partial;
   // uint8 rows whose every start is 4-byte aligned are read as dwords
@@ -903,13 +910,13 @@ FA_API int fa_gpu_pixel_reduce_ex(const void* a, const void* b, int dtype, int64
 
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(bpi), static_cast<unsigned>(n_images));
+  const dim3 grid(static_cast<unsigned>(cols), static_cast<unsigned>(n_images));
   const int rc = luma ? launch_view_dtype<true>(dtype, op, dw, grid, st, v)
                       : launch_view_dtype<false>(dtype, op, dw, grid, st, v);
   if (rc != FA_OK) return rc;
   const bool exact = dtype == FA_U8 && !luma && (op == FA_OP_MSE || op == FA_OP_L1);
   const double n_each = static_cast<double>(v.Cout) * plane;
-  return launch_finalize(partial, exact, static_cast<int>(n_images), bpi, n_each,
+  return launch_finalize(partial, exact, static_cast<int>(n_images), cols, n_each,
                          n_each * static_cast<double>(n_images), psnr_bias, out_per_image,
                          out_total, out_psnr_per_image, out_psnr_total, st);
 }
