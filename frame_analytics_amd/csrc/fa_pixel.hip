@@ -526,9 +526,10 @@ static bool launch_sweep_op(int op, hipStream_t st, const void* a, const void* b
 // --------------------------------------------------------------------------
 // strided views and luma (fa_gpu_pixel_reduce_ex): a workgroup reduces an
 // equal share of its image's (channel, row) space, lanes striding along a row
-// (dwords for 4-byte aligned uint8 rows).  With luma the difference of the
-// two luma samples, kr dR + kg dG + kb dB (the offset cancels), is formed in
-// float64 from the channel differences, and every term is float64.
+// (dwords for uint8 rows, realigned where a row starts off a 4-byte
+// boundary).  With luma the difference of the two luma samples,
+// kr dR + kg dG + kb dB (the offset cancels), is formed in float64 from the
+// channel differences, and every term is float64.
 // --------------------------------------------------------------------------
 struct PixView {
   const void* a;
@@ -542,13 +543,11 @@ struct PixView {
   void* partial;
 };
 
-template <typename T, int OP, bool LUMA, int V>
+// Float views (float16 ... float64), one element per lane per row position.
+template <typename T, int OP, bool LUMA>
 __global__ __launch_bounds__(BLOCK) void pix_view_kernel(PixView v) {
-  constexpr bool U8 = std::is_same<T, uint8_t>::value;
-  constexpr bool EXACT = U8 && !LUMA && (OP == FA_OP_MSE || OP == FA_OP_L1);
   constexpr bool WIDE = LUMA || (OP != FA_OP_CHARB) || sizeof(T) == 8;
   using A = typename std::conditional<WIDE, double, float>::type;
-  __shared__ uint64_t s_u[WAVES_PER_BLOCK];
   __shared__ double s_d[WAVES_PER_BLOCK];
 
   const int img = blockIdx.y;
@@ -559,8 +558,7 @@ __global__ __launch_bounds__(BLOCK) void pix_view_kernel(PixView v) {
   const T* ib = static_cast<const T*>(v.b) + img * v.bsn;
   const A p = static_cast<A>(v.param);
 
-  U8Lane<OP> lane8;   // uint8 without luma
-  double acc = 0.0;   // everything else
+  double acc = 0.0;
   for (int64_t rr = r0; rr < r1; ++rr) {  // uniform
     const int c = static_cast<int>(rr / v.H);
     const int row = static_cast<int>(rr - static_cast<int64_t>(c) * v.H);
@@ -578,20 +576,168 @@ __global__ __launch_bounds__(BLOCK) void pix_view_kernel(PixView v) {
     } else {
       const T* pa = ia + c * v.asc + row * v.ash;
       const T* pb = ib + c * v.bsc + row * v.bsh;
-      if constexpr (U8 && V == 4) {
-        const uint32_t* wa = reinterpret_cast<const uint32_t*>(pa);
-        const uint32_t* wb = reinterpret_cast<const uint32_t*>(pb);
-        for (int j = threadIdx.x; j < v.W / 4; j += BLOCK) {
-          lane8.dword(wa[j], wb[j], static_cast<float>(v.param));
-          lane8.flush();
+      A part = A(0);
+      for (int j = threadIdx.x; j < v.W; j += BLOCK)
+        part += pix_term<OP, A>(load_as<A>(pa, j) - load_as<A>(pb, j), p);
+      acc += static_cast<double>(part);
+    }
+  }
+  const double t = block_sum(acc, s_d);
+  if (threadIdx.x == 0) reinterpret_cast<double*>(v.partial)[static_cast<int64_t>(img) * v.bpi + blockIdx.x] = t;
+}
+
+// uint8 views: crops at any byte offset, with or without luma.  A row is read
+// as dwords -- realigned with v_alignbyte when it does not start on a 4-byte
+// boundary, since the aligned dword holding any byte of the row is mapped --
+// and a lane issues the loads of VR rows x VQ dwords (rows up to 4 KiB in one
+// step) before it sums any, so enough bytes are in flight: one dword load per
+// row at a time left this kernel latency bound (a 4-byte aligned crop of
+// configs[2] took 85 us, a byte-offset one 204 us).  With luma the three
+// channels' dwords are read and kr dR + kg dG + kb dB is formed per pixel in
+// float64 (the luma offset cancels).
+constexpr int PIX_VQ = 4;  // dwords per lane per row and step
+constexpr int PIX_VIEW_WG_PER_CU = 4;
+
+// A row at address `row` = m (mod 4) is read as the aligned dwords
+// al[j] = (row - m)[4j, 4j + 4): the bytes [4j, 4j + 4) of the row are
+// alignbyte(al[j + 1], al[j], m).  Lanes of a wave hold consecutive j, so
+// al[j + 1] is the next lane's dword (a DPP move), and only lane 63 loads it
+// itself.  The aligned dwords up to index nq = W / 4 each hold a byte of the
+// row, so they are mapped.  All loads of a step are issued before the first
+// DPP move: a move per load, between the loads, made the compiler wait for
+// each load in turn (crop at a byte offset: 355 us against 232).
+template <int OP, bool LUMA>
+__global__ __launch_bounds__(BLOCK) void pix_view_u8_kernel(PixView v) {
+  constexpr bool EXACT = !LUMA && (OP == FA_OP_MSE || OP == FA_OP_L1);
+  constexpr int CH = LUMA ? 3 : 1;
+  constexpr int VR = LUMA ? 1 : 2;  // rows per step
+  __shared__ uint64_t s_u[WAVES_PER_BLOCK];
+  __shared__ double s_d[WAVES_PER_BLOCK];
+
+  const int img = blockIdx.y;
+  const int64_t R = static_cast<int64_t>(v.Cout) * v.H;
+  const int64_t r0 = R * blockIdx.x / v.bpi;
+  const int64_t r1 = R * (blockIdx.x + 1) / v.bpi;
+  const uint8_t* ia = static_cast<const uint8_t*>(v.a) + img * v.asn;
+  const uint8_t* ib = static_cast<const uint8_t*>(v.b) + img * v.bsn;
+  const float p8 = static_cast<float>(v.param);
+  const double pd = v.param;
+  const int nq = v.W / 4;          // whole dwords per row
+  const int tail = v.W - 4 * nq;   // trailing bytes per row
+
+  U8Lane<OP> lane8;   // without luma
+  double acc = 0.0;   // with luma
+  // the luma term of byte k of the dwords xa / xb of the three channels
+  auto luma_px = [&](const uint32_t (&xa)[3], const uint32_t (&xb)[3], int k) {
+    double d[3];
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch)
+      d[ch] = static_cast<double>(static_cast<int>((xa[ch] >> (8 * k)) & 0xffu) -
+                                  static_cast<int>((xb[ch] >> (8 * k)) & 0xffu));
+    return pix_term<OP, double>(fma(v.kb, d[2], fma(v.kg, d[1], v.kr * d[0])), pd);
+  };
+
+  for (int64_t rr = r0; rr < r1; rr += VR) {  // uniform
+    const uint8_t* pa[VR][CH];
+    const uint8_t* pb[VR][CH];
+    uint32_t ma[VR][CH], mb[VR][CH];
+    bool rv[VR];
+#pragma unroll
+    for (int q = 0; q < VR; ++q) {
+      rv[q] = rr + q < r1;
+      const int64_t rq = rv[q] ? rr + q : rr;
+      const int c = static_cast<int>(rq / v.H);
+      const int row = static_cast<int>(rq - static_cast<int64_t>(c) * v.H);
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        const int cc = LUMA ? ch : c;
+        pa[q][ch] = ia + cc * v.asc + row * v.ash;
+        pb[q][ch] = ib + cc * v.bsc + row * v.bsh;
+        ma[q][ch] = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(pa[q][ch]) & 3);
+        mb[q][ch] = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(pb[q][ch]) & 3);
+      }
+    }
+    for (int j0 = 0; j0 < nq; j0 += PIX_VQ * BLOCK) {  // uniform; one step for rows <= 4 KiB
+      uint32_t xa[VR][PIX_VQ][CH], xb[VR][PIX_VQ][CH];
+      uint32_t ha[VR][PIX_VQ][CH], hb[VR][PIX_VQ][CH];  // lane 63's al[j + 1]
+      bool ok[VR][PIX_VQ];
+      const bool last_lane = (threadIdx.x & (WAVE - 1)) == WAVE - 1;
+      // every load of the step first ...
+#pragma unroll
+      for (int q = 0; q < VR; ++q) {
+#pragma unroll
+        for (int u = 0; u < PIX_VQ; ++u) {
+          const int j = j0 + u * BLOCK + static_cast<int>(threadIdx.x);
+          ok[q][u] = rv[q] && j < nq;
+          const bool feed = rv[q] && j == nq;  // loads only for its neighbour
+#pragma unroll
+          for (int ch = 0; ch < CH; ++ch) {
+            const uint32_t* wa = reinterpret_cast<const uint32_t*>(pa[q][ch] - ma[q][ch]);
+            const uint32_t* wb = reinterpret_cast<const uint32_t*>(pb[q][ch] - mb[q][ch]);
+            xa[q][u][ch] = (ok[q][u] || (feed && ma[q][ch])) ? wa[j] : 0u;
+            xb[q][u][ch] = (ok[q][u] || (feed && mb[q][ch])) ? wb[j] : 0u;
+            ha[q][u][ch] = (last_lane && ok[q][u] && ma[q][ch]) ? wa[j + 1] : 0u;
+            hb[q][u][ch] = (last_lane && ok[q][u] && mb[q][ch]) ? wb[j + 1] : 0u;
+          }
         }
-      } else if constexpr (U8) {
-        for (int j = threadIdx.x; j < v.W; j += BLOCK) lane8.byte(pa[j], pb[j], static_cast<float>(v.param));
+      }
+      // ... then the realignment of rows off a 4-byte boundary (m uniform)
+#pragma unroll
+      for (int q = 0; q < VR; ++q) {
+#pragma unroll
+        for (int u = 0; u < PIX_VQ; ++u) {
+#pragma unroll
+          for (int ch = 0; ch < CH; ++ch) {
+            if (ma[q][ch]) {
+              const uint32_t nx = static_cast<uint32_t>(wave_next(static_cast<int>(xa[q][u][ch])));
+              const uint32_t hi = last_lane ? ha[q][u][ch] : nx;
+              xa[q][u][ch] = ok[q][u] ? __builtin_amdgcn_alignbyte(hi, xa[q][u][ch], ma[q][ch]) : 0u;
+            }
+            if (mb[q][ch]) {
+              const uint32_t nx = static_cast<uint32_t>(wave_next(static_cast<int>(xb[q][u][ch])));
+              const uint32_t hi = last_lane ? hb[q][u][ch] : nx;
+              xb[q][u][ch] = ok[q][u] ? __builtin_amdgcn_alignbyte(hi, xb[q][u][ch], mb[q][ch]) : 0u;
+            }
+          }
+        }
+      }
+      if constexpr (LUMA) {
+        double part = 0.0;
+#pragma unroll
+        for (int u = 0; u < PIX_VQ; ++u) {
+          if (ok[0][u]) {
+            const uint32_t a3[3] = {xa[0][u][0], xa[0][u][1], xa[0][u][2]};
+            const uint32_t b3[3] = {xb[0][u][0], xb[0][u][1], xb[0][u][2]};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) part += luma_px(a3, b3, k);
+          }
+        }
+        acc += part;
       } else {
-        A part = A(0);
-        for (int j = threadIdx.x; j < v.W; j += BLOCK)
-          part += pix_term<OP, A>(load_as<A>(pa, j) - load_as<A>(pb, j), p);
-        acc += static_cast<double>(part);
+#pragma unroll
+        for (int q = 0; q < VR; ++q) {
+#pragma unroll
+          for (int u = 0; u < PIX_VQ; ++u) {
+            // zeros add nothing, except Charbonnier's sqrt(0 + eps^2)
+            if (EXACT || ok[q][u]) lane8.dword(xa[q][u][0], xb[q][u][0], p8);
+          }
+        }
+        lane8.flush();  // at most VR * PIX_VQ = 8 dwords since the last flush
+      }
+    }
+    if (static_cast<int>(threadIdx.x) < tail) {  // the row's last W % 4 bytes
+      const int j = 4 * nq + static_cast<int>(threadIdx.x);
+#pragma unroll
+      for (int q = 0; q < VR; ++q) {
+        if (rv[q]) {
+          if constexpr (LUMA) {
+            const uint32_t a3[3] = {pa[q][0][j], pa[q][1][j], pa[q][2][j]};
+            const uint32_t b3[3] = {pb[q][0][j], pb[q][1][j], pb[q][2][j]};
+            acc += luma_px(a3, b3, 0);
+          } else {
+            lane8.byte(pa[q][0][j], pb[q][0][j], p8);
+          }
+        }
       }
     }
   }
@@ -601,7 +747,7 @@ __global__ __launch_bounds__(BLOCK) void pix_view_kernel(PixView v) {
     const uint64_t t = block_sum(lane8.exact, s_u);
     if (threadIdx.x == 0) reinterpret_cast<uint64_t*>(v.partial)[slot] = t;
   } else {
-    if constexpr (U8 && !LUMA) {
+    if constexpr (!LUMA) {
       lane8.flush();
       acc += lane8.wide;
     }
@@ -611,32 +757,31 @@ __global__ __launch_bounds__(BLOCK) void pix_view_kernel(PixView v) {
 }
 
 template <typename T, int OP, bool LUMA>
-static void launch_view(bool dw, dim3 grid, hipStream_t st, const PixView& v) {
-  if (dw)
-    hipLaunchKernelGGL((pix_view_kernel<T, OP, LUMA, 4>), grid, dim3(BLOCK), 0, st, v);
+static void launch_view(dim3 grid, hipStream_t st, const PixView& v) {
+  if constexpr (std::is_same<T, uint8_t>::value)
+    hipLaunchKernelGGL((pix_view_u8_kernel<OP, LUMA>), grid, dim3(BLOCK), 0, st, v);
   else
-    hipLaunchKernelGGL((pix_view_kernel<T, OP, LUMA, 1>), grid, dim3(BLOCK), 0, st, v);
+    hipLaunchKernelGGL((pix_view_kernel<T, OP, LUMA>), grid, dim3(BLOCK), 0, st, v);
 }
 
 template <typename T, bool LUMA>
-static void launch_view_op(int op, bool dw, dim3 grid, hipStream_t st, const PixView& v) {
+static void launch_view_op(int op, dim3 grid, hipStream_t st, const PixView& v) {
   switch (op) {
-    case FA_OP_MSE: launch_view<T, FA_OP_MSE, LUMA>(dw, grid, st, v); break;
-    case FA_OP_L1: launch_view<T, FA_OP_L1, LUMA>(dw, grid, st, v); break;
-    case FA_OP_CHARB: launch_view<T, FA_OP_CHARB, LUMA>(dw, grid, st, v); break;
-    default: launch_view<T, FA_OP_HUBER, LUMA>(dw, grid, st, v); break;
+    case FA_OP_MSE: launch_view<T, FA_OP_MSE, LUMA>(grid, st, v); break;
+    case FA_OP_L1: launch_view<T, FA_OP_L1, LUMA>(grid, st, v); break;
+    case FA_OP_CHARB: launch_view<T, FA_OP_CHARB, LUMA>(grid, st, v); break;
+    default: launch_view<T, FA_OP_HUBER, LUMA>(grid, st, v); break;
   }
 }
 
 template <bool LUMA>
-static int launch_view_dtype(int dtype, int op, bool dw, dim3 grid, hipStream_t st,
-                             const PixView& v) {
+static int launch_view_dtype(int dtype, int op, dim3 grid, hipStream_t st, const PixView& v) {
   switch (dtype) {
-    case FA_U8: launch_view_op<uint8_t, LUMA>(op, dw, grid, st, v); break;
-    case FA_F16: launch_view_op<half_t, LUMA>(op, false, grid, st, v); break;
-    case FA_BF16: launch_view_op<bf16_t, LUMA>(op, false, grid, st, v); break;
-    case FA_F32: launch_view_op<float, LUMA>(op, false, grid, st, v); break;
-    case FA_F64: launch_view_op<double, LUMA>(op, false, grid, st, v); break;
+    case FA_U8: launch_view_op<uint8_t, LUMA>(op, grid, st, v); break;
+    case FA_F16: launch_view_op<half_t, LUMA>(op, grid, st, v); break;
+    case FA_BF16: launch_view_op<bf16_t, LUMA>(op, grid, st, v); break;
+    case FA_F32: launch_view_op<float, LUMA>(op, grid, st, v); break;
+    case FA_F64: launch_view_op<double, LUMA>(op, grid, st, v); break;
     default: return FA_E_DTYPE;
   }
   FA_LAUNCH_CHECK();
@@ -893,26 +1038,23 @@ FA_API int fa_gpu_pixel_reduce_ex(const void* a, const void* b, int dtype, int64
     v.kg = luma[1];
     v.kb = luma[2];
   }
-  // The view kernel wants the (bpi, N) grid's own size, not the sweep's
-  // larger workspace: it uses the first `cols` partial slots of each image,
-  // packed (measured at 8x3x2160x3840: crop 4, 85 against 91 us; luma, 106
-  // against 126 us with all 2048 columns).
+  // The view kernels take about 4 workgroups per CU, whatever the workspace
+  // allows: each uses the first `cols` partial slots of its image, packed.
+  // Measured at 8x3x2160x3840 uint8 (1 / 2 / 4 / 8 workgroups per CU): crop
+  // border 4, 156 / 95 / 77 / 83 us; luma, 148 / 92 / 77 / 79 us; and 91 us
+  // and 126 us with all 2048 columns of the sweep's workspace.
   const int64_t cus = cu_count(device);
   const int cols = static_cast<int>(std::max<int64_t>(
-      1, std::min<int64_t>(bpi, std::max<int64_t>(1, cus * PIX_WG_PER_CU / n_images))));
+      1, std::min<int64_t>(bpi, std::max<int64_t>(1, cus * PIX_VIEW_WG_PER_CU / n_images))));
   v.bpi = cols;
   v.param = param;
   v.partial = partial;
-  // uint8 rows whose every start is 4-byte aligned are read as dwords
-  const uintptr_t bases = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
-  const int64_t strides = va[0] | va[1] | va[2] | vb[0] | vb[1] | vb[2];
-  const bool dw = dtype == FA_U8 && !luma && W % 4 == 0 && (bases & 3) == 0 && (strides & 3) == 0;
 
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(cols), static_cast<unsigned>(n_images));
-  const int rc = luma ? launch_view_dtype<true>(dtype, op, dw, grid, st, v)
-                      : launch_view_dtype<false>(dtype, op, dw, grid, st, v);
+  const int rc = luma ? launch_view_dtype<true>(dtype, op, grid, st, v)
+                      : launch_view_dtype<false>(dtype, op, grid, st, v);
   if (rc != FA_OK) return rc;
   const bool exact = dtype == FA_U8 && !luma && (op == FA_OP_MSE || op == FA_OP_L1);
   const double n_each = static_cast<double>(v.Cout) * plane;

@@ -263,3 +263,27 @@ def test_crop_read_in_place_exact(gpu, cb):
     got = fa.huber(x, y, crop_border=cb, reduction="none").cpu().numpy()
     want = ref.huber(ca.astype(np.float64), cbb.astype(np.float64), reduction="none")
     assert np.all(np.abs(got - want) <= 1e-9 * np.abs(want))
+    got = fa.charbonnier(x, y, eps=0.5, crop_border=cb, reduction="none").cpu().numpy()
+    want = ref.charbonnier(ca.astype(np.float64), cbb.astype(np.float64), 0.5, reduction="none")
+    assert np.all(np.abs(got - want) <= 1e-6 * np.abs(want))
+
+
+@pytest.mark.parametrize("cb", [0, 1, 2, 4])
+def test_crop_wide_rows(gpu, cb):
+    """Rows wider than one step of the uint8 view kernel (4 KiB), with and
+    without luma, an odd row count per image and every byte offset."""
+    a, b = u8_pair((2, 3, 13, 4210), 9.0, seed=40 + cb)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    # crop_border=0 on a strided view: a column slice keeps the rows strided
+    xs, ys = (x, y) if cb else (x[..., 1:4201], y[..., 1:4201])
+    ca = ref.crop(a, cb) if cb else a[..., 1:4201]
+    cbb = ref.crop(b, cb) if cb else b[..., 1:4201]
+    got = fa.mse(xs, ys, crop_border=cb, reduction="none").cpu().numpy()
+    assert np.array_equal(got, ref.mse(ca, cbb, "none"))
+    assert np.array_equal(fa.l1(xs, ys, crop_border=cb, reduction="none").cpu().numpy(),
+                          ref.l1(ca, cbb, "none"))
+    la = ref.rgb_to_luma(ca.astype(np.float64), "bt601")
+    lb = ref.rgb_to_luma(cbb.astype(np.float64), "bt601")
+    got = fa.mse(xs, ys, luma="bt601", crop_border=cb, reduction="none").cpu().numpy()
+    want = ref.mse(la, lb, "none")
+    assert np.all(np.abs(got - want) <= 1e-12 * np.abs(want))
