@@ -72,8 +72,10 @@ FA_API int fa_gpu_device_count(int* out_count);
 
 /*
  * Replaces fa_cuda_pixel_workspace (reference fa_abi.h:135-136).
- * out_bpi: workgroups per image of fa_gpu_pixel_reduce; `partial` must hold
- * n_images * bpi 8-byte slots.
+ * out_bpi: partial slots per image of fa_gpu_pixel_reduce; `partial` must hold
+ * n_images * bpi 8-byte slots.  Images of at least 4 Mi elements get one slot
+ * per wave of a one-workgroup-per-CU sweep (8 x CUs); smaller ones one per
+ * workgroup of a per-image grid.  Any bpi >= 1 is accepted by the reductions.
  */
 FA_API int fa_gpu_pixel_workspace(int64_t n_images, int64_t n_per_image,
                                   int device, int* out_bpi);
