@@ -315,12 +315,16 @@ __global__ __launch_bounds__(BLOCK) void pix_float_kernel(
 // plain unpredicated burst of loads; only the about one round per image that
 // reaches the edge (a round spans at most U*G*BLOCK <= nv vectors, checked by
 // the host, so it touches at most two images) sorts its lanes into two
-// accumulators.  Once every lane has passed the edge the wave writes its
-// partial of that image, partial[img * bpi + wave], bpi = G * WAVES_PER_BLOCK.
-// No barrier and no LDS: a workgroup partial behind a barrier measured 3 us
-// slower per launch, and a form that predicated every load ran at 74 us (at
-// one wave per SIMD each extra instruction in a round is time with no load
-// in flight).
+// accumulators.  Once every lane has passed the edge the wave sets its sum
+// for that image aside in LDS, and after the walk each workgroup writes one
+// partial per image (batches of more than SWEEP_LDS_IMAGES images write one
+// per wave instead).  No barrier inside the walk: a workgroup partial formed
+// behind a barrier at every image edge measured 3 us slower per launch, and a
+// form that predicated every load ran at 74 us (at one or two waves per SIMD
+// each extra instruction in a round is time with no load in flight).
+// A single-launch form whose last workgroup also finalized (a counter that
+// the caller zeroes once) measured no faster as a whole call: the finalize
+// launch already overlaps the tail of the sweep.
 // --------------------------------------------------------------------------
 // Launch shape, from a sweep on MI355X (uint8 MSE kernel time; one workgroup
 // per CU unless noted):
@@ -341,6 +345,7 @@ __global__ __launch_bounds__(BLOCK) void pix_float_kernel(
 #endif
 constexpr int SWEEP_UNROLL = FA_SWEEP_UNROLL;  // gridwide strides per round
 constexpr int SWEEP_BLOCK = FA_SWEEP_BLOCK;    // threads per workgroup (one per CU)
+constexpr int SWEEP_LDS_IMAGES = 32;           // batches up to this size sum waves in LDS
 
 template <typename T, int OP>
 struct VecAcc {
@@ -398,30 +403,38 @@ struct VecAcc {
       part = A(0);
     }
   }
-  __device__ inline void emit(void* partial, int64_t slot) const {
-    const bool lead = (threadIdx.x & (WAVE - 1)) == 0;
-    if constexpr (EXACT) {
-      const uint64_t s = wave_sum(u8.exact);
-      if (lead) reinterpret_cast<uint64_t*>(partial)[slot] = s;
-    } else {
-      const double s = wave_sum(U8 ? u8.wide : acc);
-      if (lead) reinterpret_cast<double*>(partial)[slot] = s;
-    }
+  // The wave's sum as 8 bytes (uint64, or the bits of a float64), valid in
+  // every lane.
+  __device__ inline uint64_t wave_bits() const {
+    if constexpr (EXACT) return wave_sum(u8.exact);
+    else return static_cast<uint64_t>(__double_as_longlong(wave_sum(U8 ? u8.wide : acc)));
+  }
+  // Adds two partials given as 8-byte patterns.
+  __device__ static inline uint64_t add_bits(uint64_t x, uint64_t y) {
+    if constexpr (EXACT) return x + y;
+    else return static_cast<uint64_t>(__double_as_longlong(__longlong_as_double(x) + __longlong_as_double(y)));
   }
 };
 
-template <typename T, int OP, int U = SWEEP_UNROLL, int NT = SWEEP_BLOCK>
+template <typename T, int OP, bool LDSP, int U = SWEEP_UNROLL, int NT = SWEEP_BLOCK>
 __global__ __launch_bounds__(NT) void pix_sweep_kernel(
     const uint4* __restrict__ a, const uint4* __restrict__ b, int64_t nv, int n_images,
     double param, void* __restrict__ partial) {
   using Acc = VecAcc<T, OP>;
   constexpr int WPB = NT / WAVE;
+  // LDSP: the waves' image sums wait in LDS and each workgroup writes one
+  // partial per image at the end, partial[img * G + workgroup] (the finalize
+  // then reads G instead of G * WPB per image); otherwise every wave writes
+  // its own, partial[img * G * WPB + wave].
+  __shared__ uint64_t s_p[LDSP ? SWEEP_LDS_IMAGES * WPB : 1];
   const int64_t gs = static_cast<int64_t>(gridDim.x) * NT;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
   const int64_t w0 = t0 - (threadIdx.x & (WAVE - 1));  // lane 0 of this wave
   const int64_t total = nv * n_images;
   const int64_t bpi = static_cast<int64_t>(gridDim.x) * WPB;
-  const int64_t wslot = static_cast<int64_t>(blockIdx.x) * WPB + threadIdx.x / WAVE;
+  const int wave = static_cast<int>(threadIdx.x) / WAVE;
+  const int64_t wslot = static_cast<int64_t>(blockIdx.x) * WPB + wave;
+  const bool lead = (threadIdx.x & (WAVE - 1)) == 0;
   const float p8 = static_cast<float>(param);
   const typename Acc::A p = static_cast<typename Acc::A>(param);
 
@@ -480,41 +493,62 @@ __global__ __launch_bounds__(NT) void pix_sweep_kernel(
     // emit every image all of whose vectors this wave has passed
     const int64_t next = base + U * gs + w0;
     while (img < n_images && next >= edge) {
-      cur.emit(partial, img * bpi + wslot);
+      const uint64_t bits = cur.wave_bits();
+      if (lead) {
+        if constexpr (LDSP) s_p[img * WPB + wave] = bits;
+        else reinterpret_cast<uint64_t*>(partial)[img * bpi + wslot] = bits;
+      }
       cur = nxt;
       nxt = Acc();
       ++img;
       edge += nv;
     }
   }
+  if constexpr (LDSP) {
+    __syncthreads();  // every wave has left the walk
+    for (int i = static_cast<int>(threadIdx.x); i < n_images; i += NT) {
+      uint64_t t = s_p[i * WPB];
+#pragma unroll
+      for (int w = 1; w < WPB; ++w) t = Acc::add_bits(t, s_p[i * WPB + w]);
+      reinterpret_cast<uint64_t*>(partial)[static_cast<int64_t>(i) * gridDim.x + blockIdx.x] = t;
+    }
+  }
 }
 
-// Launch of the sweep (one wave per partial column) when it applies: 16-byte
-// aligned bases, whole vectors per image, bpi a multiple of the waves per
-// workgroup and at least U gridwide strides per image.  Returns false
-// (nothing launched) otherwise.
+// Launch of the sweep when it applies: 16-byte aligned bases, whole vectors
+// per image, bpi a multiple of the waves per workgroup (one workgroup per WPB
+// slots) and at least U gridwide strides per image.  Returns the partial
+// columns per image it writes (G for up to SWEEP_LDS_IMAGES images, bpi
+// beyond), or 0 when it does not apply and nothing was launched.
 template <typename T, int OP>
-static bool launch_sweep(hipStream_t st, const void* a, const void* b, int64_t n_images,
-                         int64_t per, int bpi, double param, void* partial) {
+static int launch_sweep(hipStream_t st, const void* a, const void* b, int64_t n_images,
+                        int64_t per, int bpi, double param, void* partial) {
   constexpr int64_t E = 16 / static_cast<int64_t>(sizeof(T));
   const uintptr_t bases = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
   constexpr int WPB = SWEEP_BLOCK / WAVE;
-  if ((bases & 15) != 0 || per % E != 0 || bpi % WPB != 0) return false;
+  if ((bases & 15) != 0 || per % E != 0 || bpi % WPB != 0) return 0;
   const int64_t nv = per / E;
   const int64_t G = bpi / WPB;
   // the kernel needs a round to span no more than one image (so it touches
   // at most two); smaller images take the per-image grid
-  if (nv < SWEEP_UNROLL * G * SWEEP_BLOCK) return false;
-  hipLaunchKernelGGL((pix_sweep_kernel<T, OP>), dim3(static_cast<unsigned>(G)), dim3(SWEEP_BLOCK), 0,
-                     st, static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
+  if (nv < SWEEP_UNROLL * G * SWEEP_BLOCK) return 0;
+  const dim3 grid(static_cast<unsigned>(G));
+  if (n_images <= SWEEP_LDS_IMAGES) {
+    hipLaunchKernelGGL((pix_sweep_kernel<T, OP, true>), grid, dim3(SWEEP_BLOCK), 0, st,
+                       static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
+                       static_cast<int>(n_images), param, partial);
+    return static_cast<int>(G);
+  }
+  hipLaunchKernelGGL((pix_sweep_kernel<T, OP, false>), grid, dim3(SWEEP_BLOCK), 0, st,
+                     static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
                      static_cast<int>(n_images), param, partial);
-  return true;
+  return bpi;
 }
 
 template <typename T>
-static bool launch_sweep_op(int op, hipStream_t st, const void* a, const void* b,
-                            int64_t n_images, int64_t per, int bpi, double param,
-                            void* partial) {
+static int launch_sweep_op(int op, hipStream_t st, const void* a, const void* b,
+                           int64_t n_images, int64_t per, int bpi, double param,
+                           void* partial) {
   switch (op) {
     case FA_OP_MSE: return launch_sweep<T, FA_OP_MSE>(st, a, b, n_images, per, bpi, param, partial);
     case FA_OP_L1: return launch_sweep<T, FA_OP_L1>(st, a, b, n_images, per, bpi, param, partial);
@@ -957,7 +991,7 @@ FA_API int fa_gpu_pixel_reduce(const void* a, const void* b, int dtype,
   const uintptr_t rel = reinterpret_cast<uintptr_t>(a) - reinterpret_cast<uintptr_t>(b);
 
   bool exact = false;
-  bool swept = false;
+  int swept = 0;  // partial columns per image the sweep wrote, 0 if it did not run
   switch (dtype) {
     case FA_U8: swept = launch_sweep_op<uint8_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
     case FA_F16: swept = launch_sweep_op<half_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
@@ -991,10 +1025,9 @@ FA_API int fa_gpu_pixel_reduce(const void* a, const void* b, int dtype,
   FA_LAUNCH_CHECK();
 
   const double n_each = static_cast<double>(n_per_image);
-  return launch_finalize(partial, exact, static_cast<int>(n_images), bpi, n_each,
-                         n_each * static_cast<double>(n_images), psnr_bias,
-                         out_per_image, out_total, out_psnr_per_image,
-                         out_psnr_total, st);
+  return launch_finalize(partial, exact, static_cast<int>(n_images), swept ? swept : bpi,
+                         n_each, n_each * static_cast<double>(n_images), psnr_bias,
+                         out_per_image, out_total, out_psnr_per_image, out_psnr_total, st);
 }
 
 // No counterpart in the reference, which materialises a float32 luma plane
