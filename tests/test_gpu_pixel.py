@@ -287,3 +287,27 @@ def test_crop_wide_rows(gpu, cb):
     got = fa.mse(xs, ys, luma="bt601", crop_border=cb, reduction="none").cpu().numpy()
     want = ref.mse(la, lb, "none")
     assert np.all(np.abs(got - want) <= 1e-12 * np.abs(want))
+
+
+@pytest.mark.parametrize("n", [3, 40])
+def test_any_workspace_size_exact(gpu, n):
+    """fa_gpu_pixel_reduce gives the same exact uint8 sums for any bpi a caller
+    passes: the sweep's own (one workgroup per 8 slots, per-workgroup partials
+    up to 32 images, per-wave beyond), multiples of 8 that make a smaller or
+    larger sweep, and sizes that take the per-image grid."""
+    from frame_analytics_amd import backend
+
+    ext = backend.load()
+    a, b = u8_pair((n, 1, 2048, 2048), 5.0, seed=n)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    per = a[0].size
+    want = ref.mse(a, b, "none")
+    stream = torch.cuda.current_stream().cuda_stream
+    for bpi in (backend._pixel_workspace(ext, n, per, 0), 8, 64, 4096, 1, 7, 255, 1000):
+        part = torch.empty((n, bpi), dtype=torch.float64, device=gpu)
+        out = torch.empty(n, dtype=torch.float64, device=gpu)
+        rc = ext.gpu.fa_gpu_pixel_reduce(x.data_ptr(), y.data_ptr(), 0, n, per, 0, 0.0, -1e300,
+                                         part.data_ptr(), bpi, out.data_ptr(), None, None, None,
+                                         0, stream)
+        assert rc == 0, (bpi, rc)
+        assert np.array_equal(out.cpu().numpy(), want), bpi
