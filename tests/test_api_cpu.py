@@ -131,3 +131,17 @@ def test_status_without_gpu():
     st = fa.backend_status()
     if not torch.cuda.is_available():
         assert st["available"] is False and st["error"]
+
+
+def test_no_grad_still_reaches_the_native_kernel():
+    """requires_grad on a tensor nobody differentiates does not decline the
+    inference kernels (reference test_training_metrics.py:466-478)."""
+    from frame_analytics_amd import backend
+
+    x = torch.rand(1, 1, 64, 64, requires_grad=True)
+    y = torch.rand(1, 1, 64, 64)
+    assert not backend._usable(x, y)
+    with torch.no_grad():
+        assert backend._usable(x, y)
+    with torch.inference_mode():
+        assert backend._usable(x, y)

@@ -202,3 +202,22 @@ def test_native_hint_and_errors(gpu):
         fa.ssim(ta, tb, data_range=255.0, win_size=13, backend_hint="native")
     want = ref.ssim(a[None, None], b[None, None], 255.0, win_size=13)
     assert _rel(float(fa.ssim(ta, tb, data_range=255.0, win_size=13)), want) < 1e-5
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("fn", ["ssim", "ms_ssim", "gmsd", "gms"])
+def test_autocast_does_not_move_the_metric(gpu, dt, fn):
+    """A measurement does not change with the surrounding autocast context,
+    with or without a gradient (reference test_training_metrics.py:506-518)."""
+    torch.manual_seed(0)
+    x = torch.rand(1, 3, 192, 192, device=gpu, requires_grad=True)
+    y = (x.detach() + 0.05 * torch.randn_like(x)).clamp(0, 1)
+    call = getattr(fa, fn)
+    plain = float(call(x, y, data_range=1.0).detach())
+    with torch.autocast("cuda", dtype=dt):
+        cast = call(x, y, data_range=1.0)
+    assert abs(float(cast.detach()) - plain) <= 1e-6 * max(abs(plain), 1e-3)
+    cast.backward()  # the differentiable kernels run under autocast too
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    with torch.no_grad(), torch.autocast("cuda", dtype=dt):
+        assert abs(float(call(x, y, data_range=1.0)) - plain) <= 1e-6 * max(abs(plain), 1e-3)
