@@ -13,12 +13,15 @@ inputs.
 Also reported: PSNR on configs[2] (8x3x2160x3840 uint8), as achieved GB/s at 2
 bytes per sample and its fraction of the 8 TB/s HBM peak.
 
-``roofline`` is measured live for the dominant kernel (the SSIM strip kernel):
-its launches are bracketed with HIP events on the stream they run on, through
-the C ABI with no finalize sinks, so the average is that kernel alone.  The
-algorithmic bytes are 2 B per input sample; the kernel is VALU-bound, so its
-FP32 work is reported beside the HBM figure.  ``traffic`` is filled from the
-committed rocprofv3 PMC summary when present.
+``roofline`` is measured live for the dominant kernel (the matrix-core SSIM
+kernel, ssim_u8_mfma_kernel): its launches are bracketed with HIP events on the
+stream they run on, through the C ABI with no finalize sinks, so the average is
+that kernel alone.  The algorithmic bytes are 2 B per input sample; the kernel
+is bound by instruction issue (vector ALU and matrix cores together), so its
+arithmetic -- the two 11-tap passes over four moments and the SSIM formula,
+counted as float32 operations per output pixel -- is reported beside the HBM
+figure.  ``traffic`` is filled from the committed rocprofv3 PMC summary when
+present.
 
 ``cpu_baseline`` times the reference's own CPU kernels (oracle/_ref, compiled
 from the reference sources) on a bounded sample of the same workload, on all
@@ -410,12 +413,12 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _pmc_traffic(),
-            "kernel": "ssim_kernel<uint8,float,REDUCE,11>",
+            "kernel": "ssim_u8_mfma_kernel<REDUCE> (v_mfma_f32_16x16x32_f16 passes)",
             "kernel_ms": round(k_ms, 4),
-            "valu_tflops": round(tflops, 2),
-            "valu_frac_of_fp32_peak": round(tflops / FP32_PEAK_TFLOPS, 4),
-            # packed FP32 is kept off in this build: the issue ceiling is half
-            "valu_frac_of_unpacked_fp32": round(tflops / (FP32_PEAK_TFLOPS / 2), 4),
+            # the filter and formula work as float32 operations per output
+            # pixel, over the kernel time: what a vector-ALU kernel would issue
+            "arith_tflops": round(tflops, 2),
+            "arith_frac_of_fp32_vector_peak": round(tflops / FP32_PEAK_TFLOPS, 4),
         },
         "psnr": {
             "workload": "psnr 8x3x2160x3840 uint8 (configs[2]), 2 resident pairs rotated",

@@ -71,7 +71,9 @@ def headers() -> List[Path]:
 def compile_flags() -> List[str]:
     flags = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", f"-I{INCLUDE}",
              # CDNA4 packed-FP32 forms stay off: plain float code only.
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             # MFMA accumulators in VGPRs: no v_accvgpr_read copies before the VALU uses them
+             "-mllvm", "-amdgpu-mfma-vgpr-form"]
     for a in archs():
         flags.append(f"--offload-arch={a}")
     return flags

@@ -22,6 +22,7 @@
 //   * float64 inputs get a float64 forward instead of a refusal.
 //   * the block partial sums are float64 and reduced in a fixed order.
 #include "fa_strip.h"
+#include "fa_ssim_mfma.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -925,13 +926,26 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
   const int Cout = a.Cout;
   const int64_t planes = static_cast<int64_t>(N) * Cout;
   const bool lm = luma != nullptr;
-  rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, lm, a, planes, device, st)
-               : launch_ssim<MODE_REDUCE>(dtype, K, lm, a, planes, device, st);
-  if (rc != FA_OK) return rc;
+  int tiles = 0;
+  if (dtype == FA_U8 && !lm) {
+    // uint8 planes: both Gaussian passes on the matrix cores when the layout
+    // allows (fa_ssim_mfma.hip); otherwise the strip kernel below
+    const SsimMfmaCall mc = {static_cast<const uint8_t*>(x), static_cast<const uint8_t*>(y),
+                             a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh, N, C, H, W, Hout, Wout,
+                             K, win, C1, C2, map_out, partial, bpp};
+    rc = ssim_u8_mfma(mc, device, st, &tiles);
+    if (rc != FA_OK) return rc;
+  }
+  if (tiles == 0) {
+    rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, lm, a, planes, device, st)
+                 : launch_ssim<MODE_REDUCE>(dtype, K, lm, a, planes, device, st);
+    if (rc != FA_OK) return rc;
+    tiles = a.bpp;
+  }
 
   // each image owns Cout * tiles consecutive slots of `partial`
   const double npix = static_cast<double>(Hout) * Wout;
-  return launch_finalize(partial, false, N, Cout * a.bpp, npix * Cout,
+  return launch_finalize(partial, false, N, Cout * tiles, npix * Cout,
                          npix * Cout * static_cast<double>(N), FA_PSNR_NONE,
                          out_per_image, out_total, nullptr, nullptr, st);
 }

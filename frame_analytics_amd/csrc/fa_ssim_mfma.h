@@ -1,0 +1,29 @@
+// SSIM forward over uint8 planes on the matrix cores (fa_ssim_mfma.hip).
+#pragma once
+
+#include "fa_common.h"
+
+namespace fa {
+
+// One fa_gpu_ssim / fa_gpu_ssim_ex call over uint8 planes without luma.
+struct SsimMfmaCall {
+  const uint8_t* x;
+  const uint8_t* y;
+  int64_t xsn, xsc, ysn, ysc;  // image and channel strides (elements)
+  int xsh, ysh;                // row strides
+  int N, C, H, W, Hout, Wout, K;
+  const float* win;            // the 1-D window, K floats on the device
+  double C1, C2;
+  float* map;                  // optional float32 SSIM map (N, C, Hout, Wout)
+  double* partial;             // per-plane partial sums, bpp slots per plane
+  int bpp;
+};
+
+// Launches the matrix-core SSIM forward when the call fits it (uint8, 8-byte
+// aligned rows and planes, K <= 16, enough partial slots).  Returns FA_OK and
+// sets *tiles (partial slots used per plane) when it launched; returns FA_OK
+// with *tiles = 0 when the call does not fit, so the caller runs the
+// vector-ALU strip kernel instead.
+int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles);
+
+}  // namespace fa

@@ -1,0 +1,472 @@
+// SSIM forward over uint8 planes with both Gaussian passes on the matrix cores
+// (v_mfma_f32_16x16x32_f16).  The same statistics as the strip engine's
+// forward (fa_strip.h + SsimPol in fa_ssim.hip; reference: the fused SSIM
+// kernel, fa_cuda.cu:389-637): the separable window over x', y', x'y' and
+// (x' - y')^2 with x' = x - 128, then the SSIM formula per output pixel.
+//
+// Work split.  A wave owns a column strip of 16 output columns and walks down
+// a chunk of output rows, 16 rows per step; a workgroup is four neighbouring
+// strips.  There is no LDS traffic and no barrier until the final reduction.
+//
+// Operand layout of v_mfma_f32_16x16x32_f16 (lane l, g = l / 16, n = l % 16):
+//   A[m = n][k = 8g + i], B[k = 8g + i][n], D[m = 4g + i][n].
+//
+// Horizontal pass, one 16 x 16 block H_j per step:  H[r][c] = sum_k P[r][k] w(k - c)
+//   A = the raw planes: lane l holds row n of the 16-row block, input columns
+//       8g .. 8g+7 of the strip's 32-column window (one 8-byte load of x, one
+//       of y), turned into exact fp16 operands:
+//         x' and y' (integers in [-128, 127]),
+//         x'y' = 128 q3 + l3 with q3 in [-127, 128], l3 in [0, 127],
+//         (x-y)^2 = 128 q4 + l4 with q4 in [0, 508], l4 in [0, 127],
+//       built with packed 16-bit integer arithmetic and fp16 bit patterns
+//       (1024 + v for 0 <= v < 1024 is 0x6400 | v).
+//   B = the window, scaled by 2^10 and split into fp16 hi + lo pieces (the
+//       scale keeps the low piece of the smallest weight normal); the q
+//       planes use the same weights times 128.
+//   Products of fp16 integers and fp16 weights are exact and accumulate in
+//   float32, so each H value carries the window to 22 bits and float32
+//   accumulation, as the vector-ALU kernel does.
+//
+// Vertical pass, 16 output rows from H_j and H_{j+1}:  O[r][c] = sum_k w(k - r) H[k][c]
+//   B = the H values split into fp16 hi + lo (after undoing the 2^10); the D
+//       fragment of the horizontal pass already holds rows 4g .. 4g+3 of its
+//       block in column n, which is the B fragment's column n, so the rows of
+//       H_j and H_{j+1} sit in k = 8g + i as (block j, rows 4g+i) for i < 4
+//       and (block j+1, rows 4g+i-4) for i >= 4.  The sum over k does not
+//       care about order, so the A fragment (the window, hi + lo) is laid out
+//       to match; even and odd steps swap which half holds the newer block
+//       (two A layouts), so no register ever moves.
+//   D = rows 4g .. 4g+3 of the output block in column n: every lane finishes
+//       four output pixels with all four moments in its own registers.
+#include "fa_ssim_mfma.h"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace fa {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef short ss2 __attribute__((ext_vector_type(2)));
+
+template <class To, class From>
+__device__ inline To bc(From v) {
+  return __builtin_bit_cast(To, v);
+}
+
+constexpr int MT = 16;                 // rows / columns of an MFMA block
+constexpr float WSCALE = 512.0f;       // window scale of both passes (data: 2^-9)
+constexpr int MF_MAX_K = 16;           // 16 output rows + K - 1 <= 32 input rows
+
+struct MfArgs {
+  const uint8_t* x;
+  const uint8_t* y;
+  int64_t xsn, xsc, ysn, ysc;
+  uint32_t xsh, ysh;
+  int C, H, W, Hout, Wout, K;
+  int TH, strips, tiles;
+  const float* win;
+  float C1, C2;
+  float one;  // 1.0f (see split_pair)
+  float* map;
+  double* partial;
+};
+
+__device__ inline f4 mfma(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// The six fp16 A fragments of one lane's 8 pixels of x and y: the planes
+// x', y', l3, l4 scaled by 2^-9 and q3, q4 by 256 * 2^-9 (exact: small
+// integers times powers of two), so one set of weights serves all six.
+struct Frag {
+  h8 x, y, q3, l3, q4, l4;
+};
+
+__device__ inline uint32_t pkfma(uint32_t bits, h2 m, h2 c) {
+  return bc<uint32_t>(__builtin_elementwise_fma(bc<h2>(bits), m, c));
+}
+
+__device__ inline Frag prep(uint2 xa, uint2 ya) {
+  u4 ox, oy, o3h, o3l, o4h, o4l;
+  // t = 1024 + v (fp16 bit pattern 0x64vv, 0 <= v < 256):
+  //   t * 2^-9 - 2.25 = (v - 128) 2^-9,  t * 2^-9 - 2 = v 2^-9,
+  //   t / 2 - 576 = (v - 128) / 2,       t / 2 - 512 = v / 2
+  const h2 m = {static_cast<_Float16>(0x1p-9f), static_cast<_Float16>(0x1p-9f)};
+  const h2 c128 = {static_cast<_Float16>(-2.25f), static_cast<_Float16>(-2.25f)};
+  const h2 c0 = {static_cast<_Float16>(-2.0f), static_cast<_Float16>(-2.0f)};
+  const h2 mq = {static_cast<_Float16>(0.5f), static_cast<_Float16>(0.5f)};
+  const h2 cq128 = {static_cast<_Float16>(-576.0f), static_cast<_Float16>(-576.0f)};
+  const h2 cq0 = {static_cast<_Float16>(-512.0f), static_cast<_Float16>(-512.0f)};
+  const us2 k6480 = {0x6480, 0x6480};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t xw = j < 2 ? xa.x : xa.y;
+    const uint32_t yw = j < 2 ? ya.x : ya.y;
+    // v_perm_b32 picks bytes of {S0 : S1}: 0-3 from S1, 4-7 from S0
+    const uint32_t sf = (j & 1) ? 0x04030402u : 0x04010400u;  // two bytes under 0x64
+    const uint32_t xt = __builtin_amdgcn_perm(0x64646464u, xw, sf);
+    const uint32_t yt = __builtin_amdgcn_perm(0x64646464u, yw, sf);
+    ox[j] = pkfma(xt, m, c128);
+    oy[j] = pkfma(yt, m, c128);
+    // 16-bit integers: x - 128, y - 128 and x - y from the same patterns
+    const us2 xi = bc<us2>(xt) - k6480;
+    const us2 yi = bc<us2>(yt) - k6480;
+    const us2 d = bc<us2>(xt) - bc<us2>(yt);
+    // (x-128)(y-128) in [-16256, 16384] = 256 q + l, l = low byte, q = high
+    // byte as signed (q + 128 = high byte ^ 0x80); (x-y)^2 <= 65025 likewise
+    // with q the plain high byte
+    const uint32_t p3 = bc<uint32_t>(xi * yi);
+    const uint32_t p4 = bc<uint32_t>(d * d);
+    const uint32_t p3s = p3 ^ 0x80008000u;
+    o3l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3, 0x04020400u), m, c0);
+    o3h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3s, 0x04030401u), mq, cq128);
+    o4l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04020400u), m, c0);
+    o4h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04030401u), mq, cq0);
+  }
+  return Frag{bc<h8>(ox), bc<h8>(oy), bc<h8>(o3h), bc<h8>(o3l), bc<h8>(o4h), bc<h8>(o4l)};
+}
+
+// fp16 hi + lo of v (|v| < 65504): hi rounds to nearest, lo rounds the exact
+// remainder, so hi + lo carries v to 2^-22.
+__device__ inline void split2(float v, _Float16& hi, _Float16& lo) {
+  hi = static_cast<_Float16>(v);
+  lo = static_cast<_Float16>(v - static_cast<float>(hi));
+}
+
+// split2 of two values into packed pairs.  `one` is 1.0f from the kernel
+// arguments: the remainder is written as fma(v, one, -hi), which the compiler
+// cannot fold back to a subtraction, so it becomes one v_fma_mix per value
+// (reading hi straight from the packed pair) instead of convert, subtract,
+// convert.
+__device__ inline void split_pair(float v0, float v1, float one, uint32_t& hi, uint32_t& lo) {
+  const h2 h = {static_cast<_Float16>(v0), static_cast<_Float16>(v1)};
+  const h2 l = {static_cast<_Float16>(__builtin_fmaf(v0, one, -static_cast<float>(h.x))),
+                static_cast<_Float16>(__builtin_fmaf(v1, one, -static_cast<float>(h.y)))};
+  hi = bc<uint32_t>(h);
+  lo = bc<uint32_t>(l);
+}
+
+// The four H values of a D fragment into half HALF (u4 elements 2 HALF,
+// 2 HALF + 1) of the vertical pass's B fragments.
+template <int HALF>
+__device__ inline void stash(f4 h, float one, u4& bhi, u4& blo) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    uint32_t hi, lo;
+    split_pair(h[2 * p], h[2 * p + 1], one, hi, lo);
+    bhi[2 * HALF + p] = hi;
+    blo[2 * HALF + p] = lo;
+  }
+}
+
+struct Weights {
+  h8 bh, bl;      // horizontal B: w(8g + i - n) * 2^9, hi and lo
+  h8 eh, el;      // vertical A, even steps: block j in k = 8g + 0..3
+  h8 oh, ol;      // vertical A, odd steps: block j in k = 8g + 4..7
+};
+
+__device__ inline float tap(const float* win, int K, int d) {
+  return (d >= 0 && d < K) ? win[d] : 0.0f;
+}
+
+__device__ inline Weights load_weights(const float* win, int K, int g, int n) {
+  Weights w;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    _Float16 hi, lo;
+    const float wh = tap(win, K, 8 * g + i - n) * WSCALE;
+    split2(wh, hi, lo);
+    w.bh[i] = hi;
+    w.bl[i] = lo;
+    // input row (relative to the older block) that k = 8g + i stands for
+    const int re = i < 4 ? 4 * g + i : MT + 4 * g + (i - 4);
+    const int ro = i < 4 ? MT + 4 * g + i : 4 * g + (i - 4);
+    split2(tap(win, K, re - n) * WSCALE, hi, lo);
+    w.eh[i] = hi;
+    w.el[i] = lo;
+    split2(tap(win, K, ro - n) * WSCALE, hi, lo);
+    w.oh[i] = hi;
+    w.ol[i] = lo;
+  }
+  return w;
+}
+
+// The vertical pass's B fragments, per moment plane.
+struct VState {
+  u4 hi[4], lo[4];
+};
+
+// Horizontal sums of one 16-row block: E x', E y', E x'y', E (x'-y')^2
+// along the row (the data's 2^-9 and the window's 2^9 cancel).
+struct HAcc {
+  f4 x, y, p3, p4;
+};
+
+__device__ inline HAcc hmfma(const Frag& f, const Weights& w) {
+  const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  HAcc h;
+  h.x = mfma(f.x, w.bh, z);
+  h.y = mfma(f.y, w.bh, z);
+  h.p3 = mfma(f.q3, w.bh, z);
+  h.p4 = mfma(f.q4, w.bh, z);
+  h.x = mfma(f.x, w.bl, h.x);
+  h.y = mfma(f.y, w.bl, h.y);
+  h.p3 = mfma(f.q3, w.bl, h.p3);
+  h.p4 = mfma(f.q4, w.bl, h.p4);
+  h.p3 = mfma(f.l3, w.bh, h.p3);
+  h.p4 = mfma(f.l4, w.bh, h.p4);
+  h.p3 = mfma(f.l3, w.bl, h.p3);
+  h.p4 = mfma(f.l4, w.bl, h.p4);
+  return h;
+}
+
+template <int HALF>
+__device__ inline void stash_all(const HAcc& h, float one, VState& v) {
+  stash<HALF>(h.x, one, v.hi[0], v.lo[0]);
+  stash<HALF>(h.y, one, v.hi[1], v.lo[1]);
+  stash<HALF>(h.p3, one, v.hi[2], v.lo[2]);
+  stash<HALF>(h.p4, one, v.hi[3], v.lo[3]);
+}
+
+// Per-pixel SSIM from the four filtered moments, all scaled by 2^9:
+//   U = 2^9 E x', V = 2^9 E y', X = 2^9 E x'y', Q = 2^9 E (x'-y')^2,
+// with x' = x - 128 (any centre gives the same statistics):
+//   A1 = 2 ux uy + 256 (ux + uy) + 2 * 128^2 + C1,  B1 = A1 + (ux - uy)^2
+//   A2 = 2 (E x'y' - ux uy) + C2,  B2 = E (x'-y')^2 + A2 - (ux - uy)^2
+struct Epi {
+  float k1, C2;
+};
+
+__device__ inline float ssim_px(const Epi& e, float U, float V, float X, float Q) {
+  const float p = U * V;
+  const float t = U + V;
+  const float du = U - V;
+  const float dd = du * 0x1p-18f;
+  const float A1 = fmaf(0x1p-17f, p, fmaf(0.5f, t, e.k1));
+  const float B1 = fmaf(dd, du, A1);
+  const float A2 = fmaf(0x1p-8f, X, fmaf(-0x1p-17f, p, e.C2));
+  const float B2 = fmaf(-dd, du, fmaf(0x1p-9f, Q, A2));
+  return (A1 * A2) * __builtin_amdgcn_rcpf(B1 * B2);
+}
+
+// Sum of this lane's four outputs (rows row0 .. row0 + 3 of its column);
+// `full` (uniform) says the whole 16 x 16 block lies inside the map.
+template <bool MAP>
+__device__ inline float finish(const Epi& e, const f4* o, int row0, int row_end, bool col_ok,
+                               bool full, float* map_px, int Wout) {
+  float rs = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float s = ssim_px(e, o[0][i], o[1][i], o[2][i], o[3][i]);
+    const bool ok = full || (col_ok && row0 + i < row_end);
+    if constexpr (MAP) {
+      if (ok) map_px[static_cast<int64_t>(i) * Wout] = s;
+    }
+    rs += ok ? s : 0.0f;
+  }
+  return rs;
+}
+
+template <int PAR>
+__device__ inline void vblock(const Weights& w, const VState& v, f4* o) {
+  const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  const h8 ah = PAR == 0 ? w.eh : w.oh;
+  const h8 al = PAR == 0 ? w.el : w.ol;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.hi[q]), z);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = mfma(al, bc<h8>(v.hi[q]), o[q]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.lo[q]), o[q]);
+}
+
+// Optional register budget in waves per SIMD (a build-time tuning knob).
+#if defined(FA_SSIM_MFMA_WPE) && FA_SSIM_MFMA_WPE > 0
+#define FA_MFMA_ATTR __attribute__((amdgpu_waves_per_eu(FA_SSIM_MFMA_WPE)))
+#else
+#define FA_MFMA_ATTR
+#endif
+
+template <bool MAP>
+__global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs a) {
+  __shared__ double sred[WAVES_PER_BLOCK];
+  const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
+  const int plane = t / a.tiles;
+  const int tile = t - plane * a.tiles;
+  const int chunk = tile / a.strips;
+  const int strip = tile - chunk * a.strips;
+  const int wave = static_cast<int>(threadIdx.x) / WAVE;
+  const int lane = static_cast<int>(threadIdx.x) % WAVE;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int c0 = (strip * WAVES_PER_BLOCK + wave) * MT;  // first output column of the wave
+  const int r0 = chunk * a.TH;
+  const int r_end = min(r0 + a.TH, a.Hout);
+
+  double acc = 0.0;
+  if (c0 < a.Wout) {  // uniform per wave
+    const int img = plane / a.C;
+    const int ch = plane - img * a.C;
+    const uint8_t* __restrict__ xp = a.x + img * a.xsn + ch * a.xsc;
+    const uint8_t* __restrict__ yp = a.y + img * a.ysn + ch * a.ysc;
+    // this lane's 8 input columns; a chunk past the image only feeds output
+    // columns past Wout, so it is clamped (W % 8 == 0: chunks never straddle)
+    const uint32_t cc = static_cast<uint32_t>(min(c0 + 8 * g, a.W - 8));
+    const Weights w = load_weights(a.win, a.K, g, n);
+    const Epi e = {2.0f * 128.0f * 128.0f + a.C1, a.C2};
+    const bool col_ok = c0 + n < a.Wout;
+    float* map_col = nullptr;
+    if constexpr (MAP) map_col = a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout + c0 + n;
+
+    // rows past the image only feed output rows past Hout: clamped
+    auto load = [&](int j, uint2& xa, uint2& ya) {
+      const uint32_t r = static_cast<uint32_t>(min(r0 + MT * j + n, a.H - 1));
+      xa = *reinterpret_cast<const uint2*>(xp + r * a.xsh + cc);
+      ya = *reinterpret_cast<const uint2*>(yp + r * a.ysh + cc);
+    };
+
+    // Software pipeline: the horizontal MFMAs of block j + 2 are issued
+    // between the vertical MFMAs of step j and its epilogue, so the matrix
+    // cores and the vector ALU overlap within the wave too.
+    const int nb = (r_end - r0 + MT - 1) / MT;  // output blocks; H blocks 0 .. nb
+    VState v;
+    uint2 xa, ya;
+    load(0, xa, ya);
+    stash_all<0>(hmfma(prep(xa, ya), w), a.one, v);
+    load(1, xa, ya);
+    HAcc hn = hmfma(prep(xa, ya), w);  // H_1
+    load(2, xa, ya);
+    for (int b = 0; b < nb; b += 2) {
+      {
+        stash_all<1>(hn, a.one, v);  // H_{b+1} next to H_b
+        f4 o[4];
+        vblock<0>(w, v, o);
+        if (b + 2 <= nb) {  // uniform
+          hn = hmfma(prep(xa, ya), w);  // H_{b+2}
+          load(b + 3, xa, ya);
+        }
+        const int row0 = r0 + MT * b + 4 * g;
+        const bool full = r0 + MT * (b + 1) <= r_end && c0 + MT <= a.Wout;
+        acc += static_cast<double>(finish<MAP>(
+            e, o, row0, r_end, col_ok, full,
+            MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr, a.Wout));
+      }
+      if (b + 1 < nb) {
+        stash_all<0>(hn, a.one, v);  // H_{b+2} over H_b
+        f4 o[4];
+        vblock<1>(w, v, o);
+        if (b + 3 <= nb) {
+          hn = hmfma(prep(xa, ya), w);  // H_{b+3}
+          load(b + 4, xa, ya);
+        }
+        const int row0 = r0 + MT * (b + 1) + 4 * g;
+        const bool full = r0 + MT * (b + 2) <= r_end && c0 + MT <= a.Wout;
+        acc += static_cast<double>(finish<MAP>(
+            e, o, row0, r_end, col_ok, full,
+            MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr, a.Wout));
+      }
+    }
+  }
+  const double s = block_sum(acc, sred);
+  // packed: each image owns C * tiles consecutive slots, as the finalize reads them
+  if (threadIdx.x == 0) a.partial[static_cast<int64_t>(plane) * a.tiles + tile] = s;
+}
+
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
+
+// FA_SSIM_MFMA=0 in the environment selects the vector-ALU kernel instead.
+bool mfma_enabled() {
+  const char* e = std::getenv("FA_SSIM_MFMA");
+  return !(e && e[0] == '0');
+}
+
+template <bool MAP>
+int occupancy() {
+  static int occ = 0;
+  if (occ <= 0) {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &v, reinterpret_cast<const void*>(&ssim_u8_mfma_kernel<MAP>), BLOCK, 0) != hipSuccess ||
+        v <= 0)
+      v = 1;
+    occ = v;
+  }
+  return occ;
+}
+
+}  // namespace
+
+int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
+  *tiles = 0;
+  if (!mfma_enabled() || c.K > MF_MAX_K || c.W % 8 != 0 || c.W < 8) return FA_OK;
+  if (!aligned8(c.x) || !aligned8(c.y)) return FA_OK;
+  const int64_t s[6] = {c.xsn, c.xsc, c.ysn, c.ysc, c.xsh, c.ysh};
+  for (int64_t v : s)
+    if (v % 8 != 0) return FA_OK;
+
+  MfArgs a = {};
+  a.x = c.x;
+  a.y = c.y;
+  a.xsn = c.xsn;
+  a.xsc = c.xsc;
+  a.ysn = c.ysn;
+  a.ysc = c.ysc;
+  a.xsh = static_cast<uint32_t>(c.xsh);
+  a.ysh = static_cast<uint32_t>(c.ysh);
+  a.C = c.C;
+  a.H = c.H;
+  a.W = c.W;
+  a.Hout = c.Hout;
+  a.Wout = c.Wout;
+  a.K = c.K;
+  a.win = c.win;
+  a.C1 = static_cast<float>(c.C1);
+  a.C2 = static_cast<float>(c.C2);
+  a.one = 1.0f;
+  a.map = c.map;
+  a.partial = c.partial;
+
+  // Rows per chunk (a multiple of 16): the fewest rounds of resident
+  // workgroups times the work of one, charging the extra 16-row block of
+  // horizontal work each chunk starts with at 10 rows.
+  const int occ = c.map ? occupancy<true>() : occupancy<false>();
+  const int64_t resident = static_cast<int64_t>(cu_count(device)) * occ;
+  const int64_t planes = static_cast<int64_t>(c.N) * c.C;
+  const int strips = (c.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
+  const int blocks = (c.Hout + MT - 1) / MT;
+  int best_th = 0, best_chunks = 0;
+  int64_t best_cost = INT64_MAX;
+  for (int m = blocks; m >= 1; --m) {
+    const int chunks = (blocks + m - 1) / m;
+    if (static_cast<int64_t>(strips) * chunks > c.bpp) break;  // fewer rows: more slots
+    const int64_t wgs = planes * strips * chunks;
+    const int64_t cost = ((wgs + resident - 1) / resident) * (MT * m + 10);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best_th = MT * m;
+      best_chunks = chunks;
+    }
+  }
+  if (best_th == 0) return FA_OK;
+  a.TH = best_th;
+  a.strips = strips;
+  a.tiles = strips * best_chunks;
+  const int64_t wgs = planes * a.tiles;
+  if (wgs > INT32_MAX) return FA_OK;
+  if (c.map)
+    hipLaunchKernelGGL(ssim_u8_mfma_kernel<true>, dim3(static_cast<unsigned>(wgs)), dim3(BLOCK), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL(ssim_u8_mfma_kernel<false>, dim3(static_cast<unsigned>(wgs)), dim3(BLOCK), 0,
+                       st, a);
+  FA_LAUNCH_CHECK();
+  *tiles = a.tiles;
+  return FA_OK;
+}
+
+}  // namespace fa

@@ -1,0 +1,136 @@
+"""GPU parity of the matrix-core SSIM forward (uint8 planes, fa_ssim_mfma.hip).
+
+uint8 inputs whose rows and planes are 8-byte aligned (W % 8 == 0) take the
+MFMA kernel; everything else takes the vector-ALU strip kernel.  Both are held
+to the float64 oracle at the north star's bar (SSIM values within 1e-6
+relative; float32 map elements within 2e-5 absolute), and to each other:
+``FA_SSIM_MFMA=0`` in the environment selects the strip kernel for a call.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import frame_analytics_amd as fa
+from oracle import reference as ref
+from tests.conftest import natural_pair, u8_pair
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-6
+MAP_ABS = 2e-5
+
+
+def _rel(got, want):
+    return abs(got - want) / max(abs(want), 1e-12)
+
+
+class _VectorAlu:
+    """Runs the body with the matrix-core kernel switched off."""
+
+    def __enter__(self):
+        os.environ["FA_SSIM_MFMA"] = "0"
+
+    def __exit__(self, *exc):
+        os.environ.pop("FA_SSIM_MFMA", None)
+
+
+def _check(a, b, gpu, win=11, sigma=1.5, L=255.0, K=(0.01, 0.03)):
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    kw = dict(data_range=L, win_size=win, sigma=sigma, K=K)
+    want = ref.ssim(a, b, L, win_size=win, sigma=sigma, K=K, reduction="none")
+    want_map = ref.ssim(a, b, L, win_size=win, sigma=sigma, K=K, return_map=True)
+    got = fa.ssim(x, y, reduction="none", **kw).cpu().numpy()
+    for g, w in zip(got, want):
+        assert _rel(float(g), float(w)) <= REL, (a.shape, win, sigma, g, w)
+    m = fa.ssim(x, y, return_map=True, **kw).double().cpu().numpy()
+    assert m.shape == want_map.shape
+    assert float(np.abs(m - want_map).max()) <= MAP_ABS
+    with _VectorAlu():
+        alu = fa.ssim(x, y, reduction="none", **kw).cpu().numpy()
+    for g, w in zip(got, alu):
+        assert _rel(float(g), float(w)) <= REL, ("vs strip kernel", g, w)
+    return got
+
+
+# heights around the 16-row blocks, widths around the 64-column workgroup strips
+@pytest.mark.parametrize("h,w", [(16, 16), (26, 24), (27, 32), (42, 72), (43, 80), (58, 136),
+                                 (75, 200), (121, 264), (160, 320), (301, 1024)])
+def test_shapes(gpu, h, w):
+    a, b = natural_pair(h, w, 9.0, seed=h * 1000 + w)
+    _check(a[None, None], b[None, None], gpu)
+
+
+@pytest.mark.parametrize("win", [3, 5, 7, 9, 11])
+@pytest.mark.parametrize("sigma", [0.5, 1.5, 4.0])
+def test_windows(gpu, win, sigma):
+    a, b = natural_pair(67, 96, 6.0, seed=win * 10 + int(sigma * 2))
+    _check(a[None, None], b[None, None], gpu, win=win, sigma=sigma)
+
+
+def test_batch_and_channels(gpu):
+    a, b = u8_pair((3, 3, 90, 136), 10.0, seed=7)
+    _check(a, b, gpu)
+
+
+def test_baseline_generator_1080p(gpu):
+    a, b = u8_pair((1, 3, 1080, 1920), 8.0, seed=11)
+    _check(a, b, gpu)
+
+
+@pytest.mark.parametrize("kind", ["flat", "uniform"])
+def test_extremes(gpu, kind):
+    h, w = 48, 64
+    if kind == "flat":  # far apart means, no variance: the tiny-SSIM corner
+        a = np.full((1, 1, h, w), 255, np.uint8)
+        b = np.zeros((1, 1, h, w), np.uint8)
+    else:
+        rng = np.random.default_rng(5)
+        a = rng.integers(0, 256, (1, 1, h, w), dtype=np.uint8)
+        b = rng.integers(0, 256, (1, 1, h, w), dtype=np.uint8)
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    want_map = ref.ssim(a, b, 255.0, return_map=True)
+    m = fa.ssim(x, y, data_range=255.0, return_map=True).double().cpu().numpy()
+    assert float(np.abs(m - want_map).max()) <= MAP_ABS
+    # SSIM ~ 1e-4 for the flat pair: float32 moments cancel to ~1e-7 absolute
+    # there (sigma^2 = E (x'-y')^2 - (ux - uy)^2 with both terms near 65025),
+    # in this kernel and in the strip kernel alike
+    want = ref.ssim(a, b, 255.0)
+    bar = REL * abs(want) if abs(want) > 0.1 else 1e-7
+    got = float(fa.ssim(x, y, data_range=255.0))
+    assert abs(got - want) <= bar, (got, want)
+    with _VectorAlu():
+        alu = float(fa.ssim(x, y, data_range=255.0))
+    assert abs(alu - want) <= bar, (alu, want)
+
+
+def test_identity_is_one(gpu):
+    a, _ = natural_pair(80, 128, 5.0, seed=2)
+    x = torch.as_tensor(a[None, None], device=gpu)
+    got = fa.ssim(x, x.clone(), data_range=255.0, return_map=True)
+    assert float((got.double() - 1.0).abs().max()) <= 1e-6
+
+
+@pytest.mark.parametrize("L", [1.0, 100.0, 255.0])
+def test_data_range(gpu, L):
+    a, b = natural_pair(50, 88, 12.0, seed=int(L))
+    _check(a[None, None], b[None, None], gpu, L=L)
+
+
+def test_views_aligned_and_not(gpu):
+    # crops read in place: an 8-aligned crop stays on the matrix cores,
+    # a 4-pixel one moves to the strip kernel; both match the oracle
+    a, b = u8_pair((2, 3, 96, 160), 9.0, seed=13)
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    for c in (8, 4):
+        want = ref.ssim(a[..., c:-c, c:-c], b[..., c:-c, c:-c], 255.0, reduction="none")
+        got = fa.ssim(x, y, data_range=255.0, crop_border=c, reduction="none").cpu().numpy()
+        for g, w in zip(got, want):
+            assert _rel(float(g), float(w)) <= REL, (c, g, w)
