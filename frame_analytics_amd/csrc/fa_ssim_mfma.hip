@@ -138,13 +138,14 @@ __device__ inline void split2(float v, _Float16& hi, _Float16& lo) {
   lo = static_cast<_Float16>(v - static_cast<float>(hi));
 }
 
-// split2 of two values into packed pairs.  `one` is 1.0f from the kernel
+// fp16 hi + lo of two values as packed pairs: hi is packed with one
+// v_cvt_pkrtz (rounding toward zero), lo rounds the exact remainder, so
+// hi + lo carries each value to 2^-21.  `one` is 1.0f from the kernel
 // arguments: the remainder is written as fma(v, one, -hi), which the compiler
-// cannot fold back to a subtraction, so it becomes one v_fma_mix per value
-// (reading hi straight from the packed pair) instead of convert, subtract,
-// convert.
+// cannot fold back to a subtraction, so it maps onto v_fma_mix (reading hi
+// from the packed pair) instead of convert, subtract, convert.
 __device__ inline void split_pair(float v0, float v1, float one, uint32_t& hi, uint32_t& lo) {
-  const h2 h = {static_cast<_Float16>(v0), static_cast<_Float16>(v1)};
+  const h2 h = bc<h2>(__builtin_amdgcn_cvt_pkrtz(v0, v1));
   const h2 l = {static_cast<_Float16>(__builtin_fmaf(v0, one, -static_cast<float>(h.x))),
                 static_cast<_Float16>(__builtin_fmaf(v1, one, -static_cast<float>(h.y)))};
   hi = bc<uint32_t>(h);
