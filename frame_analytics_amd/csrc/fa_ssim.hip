@@ -883,12 +883,26 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   a.px = px;
   a.py = py;
   a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
-  rc = launch_ssim<MODE_CS>(dtype, K, luma != nullptr, a, planes, device, st);
-  if (rc != FA_OK) return rc;
-  if (out_slots) *out_slots = a.bpp;  // the launch packed each plane's partials this densely
+  int tiles = 0;
+  if (dtype == FA_U8 && !luma && (!px || pool_dtype == FA_F32)) {
+    // uint8 planes: the matrix-core kernel when the layout allows
+    // (fa_ssim_mfma.hip), pyramid level included
+    const SsimMfmaCall mc = {static_cast<const uint8_t*>(x), static_cast<const uint8_t*>(y),
+                             a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh, N, C, H, W, Hout, Wout,
+                             K, win, C1, C2, nullptr, partial, bpp, partial_cs,
+                             static_cast<float*>(px), static_cast<float*>(py)};
+    rc = ssim_u8_mfma(mc, device, st, &tiles);
+    if (rc != FA_OK) return rc;
+  }
+  if (tiles == 0) {
+    rc = launch_ssim<MODE_CS>(dtype, K, luma != nullptr, a, planes, device, st);
+    if (rc != FA_OK) return rc;
+    tiles = a.bpp;
+  }
+  if (out_slots) *out_slots = tiles;  // the launch packed each plane's partials this densely
   if (!out_s) return FA_OK;
   hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
-                     partial, partial_cs, a.bpp, static_cast<double>(Hout) * Wout, out_s,
+                     partial, partial_cs, tiles, static_cast<double>(Hout) * Wout, out_s,
                      out_cs);
   FA_LAUNCH_CHECK();
   return FA_OK;
@@ -932,7 +946,7 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
     // allows (fa_ssim_mfma.hip); otherwise the strip kernel below
     const SsimMfmaCall mc = {static_cast<const uint8_t*>(x), static_cast<const uint8_t*>(y),
                              a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh, N, C, H, W, Hout, Wout,
-                             K, win, C1, C2, map_out, partial, bpp};
+                             K, win, C1, C2, map_out, partial, bpp, nullptr, nullptr, nullptr};
     rc = ssim_u8_mfma(mc, device, st, &tiles);
     if (rc != FA_OK) return rc;
   }

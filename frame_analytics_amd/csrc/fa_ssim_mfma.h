@@ -17,10 +17,17 @@ struct SsimMfmaCall {
   float* map;                  // optional float32 SSIM map (N, C, Hout, Wout)
   double* partial;             // per-plane partial sums, bpp slots per plane
   int bpp;
+  // MS-SSIM's CS pass (partial_cs non-null): per-plane sums of SSIM and of
+  // cs = A2 / B2, and optionally the next pyramid level, the 2 x 2 means of x
+  // and y (float32, floor(H/2) x floor(W/2) per plane) into px / py
+  double* partial_cs;
+  float* px;
+  float* py;
 };
 
-// Launches the matrix-core SSIM forward when the call fits it (uint8, 8-byte
-// aligned rows and planes, K <= 16, enough partial slots).  Returns FA_OK and
+// Launches the matrix-core SSIM forward (or CS pass) when the call fits it
+// (uint8, 8-byte aligned rows and planes, K <= 16, enough partial slots,
+// 16-byte aligned pyramid planes).  Returns FA_OK and
 // sets *tiles (partial slots used per plane) when it launched; returns FA_OK
 // with *tiles = 0 when the call does not fit, so the caller runs the
 // vector-ALU strip kernel instead.

@@ -62,6 +62,8 @@ constexpr int MT = 16;                 // rows / columns of an MFMA block
 constexpr float WSCALE = 512.0f;       // window scale of both passes (data: 2^-9)
 constexpr int MF_MAX_K = 16;           // 16 output rows + K - 1 <= 32 input rows
 
+enum { MF_REDUCE = 0, MF_MAP = 1, MF_CS = 2 };
+
 struct MfArgs {
   const uint8_t* x;
   const uint8_t* y;
@@ -74,6 +76,9 @@ struct MfArgs {
   float one;  // 1.0f (see split_pair)
   float* map;
   double* partial;
+  double* partial_cs;   // MF_CS
+  float* px;            // MF_CS: optional pyramid level (2 x 2 means), float32
+  float* py;
 };
 
 __device__ inline f4 mfma(h8 a, h8 b, f4 c) {
@@ -255,22 +260,83 @@ __device__ inline float ssim_px(const Epi& e, float U, float V, float X, float Q
   return (A1 * A2) * __builtin_amdgcn_rcpf(B1 * B2);
 }
 
-// Sum of this lane's four outputs (rows row0 .. row0 + 3 of its column);
-// `full` (uniform) says the whole 16 x 16 block lies inside the map.
-template <bool MAP>
-__device__ inline float finish(const Epi& e, const f4* o, int row0, int row_end, bool col_ok,
-                               bool full, float* map_px, int Wout) {
-  float rs = 0.0f;
+// cs = A2 / B2 beside the SSIM value (MS-SSIM's CS pass).
+__device__ inline void ssim_cs_px(const Epi& e, float U, float V, float X, float Q, float& s,
+                                  float& cs) {
+  const float p = U * V;
+  const float t = U + V;
+  const float du = U - V;
+  const float dd = du * 0x1p-18f;
+  const float A1 = fmaf(0x1p-17f, p, fmaf(0.5f, t, e.k1));
+  const float B1 = fmaf(dd, du, A1);
+  const float A2 = fmaf(0x1p-8f, X, fmaf(-0x1p-17f, p, e.C2));
+  const float B2 = fmaf(-dd, du, fmaf(0x1p-9f, Q, A2));
+  const float inv = __builtin_amdgcn_rcpf(B1 * B2);
+  s = (A1 * A2) * inv;
+  cs = (A2 * B1) * inv;
+}
+
+// Adds this lane's four outputs (rows row0 .. row0 + 3 of its column) to the
+// lane's float64 sums; `full` (uniform) says the whole 16 x 16 block lies
+// inside the map.
+template <int MODE>
+__device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, bool col_ok,
+                              bool full, float* map_px, int Wout, double& acc,
+                              double& acc_cs) {
+  float rs = 0.0f, rcs = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float s = ssim_px(e, o[0][i], o[1][i], o[2][i], o[3][i]);
     const bool ok = full || (col_ok && row0 + i < row_end);
-    if constexpr (MAP) {
-      if (ok) map_px[static_cast<int64_t>(i) * Wout] = s;
+    if constexpr (MODE == MF_CS) {
+      float s, cs;
+      ssim_cs_px(e, o[0][i], o[1][i], o[2][i], o[3][i], s, cs);
+      rs += ok ? s : 0.0f;
+      rcs += ok ? cs : 0.0f;
+    } else {
+      const float s = ssim_px(e, o[0][i], o[1][i], o[2][i], o[3][i]);
+      if constexpr (MODE == MF_MAP) {
+        if (ok) map_px[static_cast<int64_t>(i) * Wout] = s;
+      }
+      rs += ok ? s : 0.0f;
     }
-    rs += ok ? s : 0.0f;
   }
-  return rs;
+  acc += static_cast<double>(rs);
+  if constexpr (MODE == MF_CS) acc_cs += static_cast<double>(rcs);
+}
+
+// MS-SSIM's next pyramid level from the raw bytes of one 16-row block: the
+// even lane of each row pair writes the 2 x 2 means of its 8 columns (four
+// float32 values, one 16-byte store); the odd lane's bytes come over by DPP.
+// uint8 sums of four are at most 1020, so the means are exact in float32.
+struct Pool {
+  float* px;
+  float* py;
+  int64_t off;  // this plane's first element
+  int Wd;       // level width, floor(W / 2)
+  int row_end;  // first input row this chunk does not pool
+  bool lane_on; // this lane's 8 columns belong to the wave and lie in the image
+};
+
+__device__ inline float4 pool4(uint2 a, uint2 b) {
+  const uint32_t m0 = 0x00000101u, m1 = 0x01010000u;  // bytes (0, 1) and (2, 3)
+  return make_float4(0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.x, m0, __builtin_amdgcn_udot4(b.x, m0, 0u, false), false)),
+                     0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.x, m1, __builtin_amdgcn_udot4(b.x, m1, 0u, false), false)),
+                     0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.y, m0, __builtin_amdgcn_udot4(b.y, m0, 0u, false), false)),
+                     0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.y, m1, __builtin_amdgcn_udot4(b.y, m1, 0u, false), false)));
+}
+
+__device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, uint2 xa, uint2 ya) {
+  // every lane takes part in the DPP moves; only even lanes store
+  const uint2 xb = {static_cast<uint32_t>(lane_xor1(static_cast<int>(xa.x))),
+                    static_cast<uint32_t>(lane_xor1(static_cast<int>(xa.y)))};
+  const uint2 yb = {static_cast<uint32_t>(lane_xor1(static_cast<int>(ya.x))),
+                    static_cast<uint32_t>(lane_xor1(static_cast<int>(ya.y)))};
+  // row is even on even lanes and row_end is even, so row + 1 < row_end too
+  if (pl.lane_on && (row & 1) == 0 && row < pl.row_end) {
+    const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
+    *reinterpret_cast<float4*>(pl.px + o) = pool4(xa, xb);
+    *reinterpret_cast<float4*>(pl.py + o) = pool4(ya, yb);
+  }
 }
 
 template <int PAR>
@@ -293,9 +359,9 @@ __device__ inline void vblock(const Weights& w, const VState& v, f4* o) {
 #define FA_MFMA_ATTR
 #endif
 
-template <bool MAP>
+template <int MODE>
 __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs a) {
-  __shared__ double sred[WAVES_PER_BLOCK];
+  __shared__ double sred[2 * WAVES_PER_BLOCK];
   const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
   const int plane = t / a.tiles;
   const int tile = t - plane * a.tiles;
@@ -309,7 +375,7 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
   const int r0 = chunk * a.TH;
   const int r_end = min(r0 + a.TH, a.Hout);
 
-  double acc = 0.0;
+  double acc = 0.0, acc_cs = 0.0;
   if (c0 < a.Wout) {  // uniform per wave
     const int img = plane / a.C;
     const int ch = plane - img * a.C;
@@ -322,13 +388,46 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
     const Epi e = {2.0f * 128.0f * 128.0f + a.C1, a.C2};
     const bool col_ok = c0 + n < a.Wout;
     float* map_col = nullptr;
-    if constexpr (MAP) map_col = a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout + c0 + n;
+    if constexpr (MODE == MF_MAP)
+      map_col = a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout + c0 + n;
+
+    // The pyramid level: a wave pools the input columns of its own 16 output
+    // columns (window columns 0..15); the last active wave of a row also
+    // pools the rest of its window up to the image edge, which covers the
+    // columns of the waves past Wout (W <= c0 + 16 + K - 1 there).  Rows:
+    // this chunk's TH input rows, and in the last chunk everything up to
+    // 2 floor(H / 2).  Every row the chunk pools lies in one of its H blocks.
+    Pool pl = {};
+    if constexpr (MODE == MF_CS) {
+      pl.px = a.px;
+      pl.py = a.py;
+      pl.Wd = a.W / 2;
+      pl.off = static_cast<int64_t>(plane) * (a.H / 2) * pl.Wd;
+      pl.row_end = r0 + a.TH >= a.Hout ? 2 * (a.H / 2) : r0 + a.TH;
+      const bool last_wave = c0 + MT >= a.Wout;
+      pl.lane_on = a.px != nullptr && (g < 2 || last_wave) && c0 + 8 * g < a.W;
+    }
+    const uint32_t pcol = static_cast<uint32_t>(c0 + 8 * g) >> 1;
 
     // rows past the image only feed output rows past Hout: clamped
     auto load = [&](int j, uint2& xa, uint2& ya) {
       const uint32_t r = static_cast<uint32_t>(min(r0 + MT * j + n, a.H - 1));
       xa = *reinterpret_cast<const uint2*>(xp + r * a.xsh + cc);
       ya = *reinterpret_cast<const uint2*>(yp + r * a.ysh + cc);
+    };
+    // horizontal pass of block j (and its share of the pyramid)
+    auto hpass = [&](int j, uint2 xa, uint2 ya) {
+      if constexpr (MODE == MF_CS) {
+        if (a.px) pool_block(pl, r0 + MT * j + n, pcol, xa, ya);  // uniform branch
+      }
+      return hmfma(prep(xa, ya), w);
+    };
+    auto epilogue = [&](int b, const f4* o) {
+      const int row0 = r0 + MT * b + 4 * g;
+      const bool full = r0 + MT * (b + 1) <= r_end && c0 + MT <= a.Wout;
+      finish<MODE>(e, o, row0, r_end, col_ok, full,
+                   MODE == MF_MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr,
+                   a.Wout, acc, acc_cs);
     };
 
     // Software pipeline: the horizontal MFMAs of block j + 2 are issued
@@ -338,9 +437,9 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
     VState v;
     uint2 xa, ya;
     load(0, xa, ya);
-    stash_all<0>(hmfma(prep(xa, ya), w), a.one, v);
+    stash_all<0>(hpass(0, xa, ya), a.one, v);
     load(1, xa, ya);
-    HAcc hn = hmfma(prep(xa, ya), w);  // H_1
+    HAcc hn = hpass(1, xa, ya);
     load(2, xa, ya);
     for (int b = 0; b < nb; b += 2) {
       {
@@ -348,34 +447,36 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
         f4 o[4];
         vblock<0>(w, v, o);
         if (b + 2 <= nb) {  // uniform
-          hn = hmfma(prep(xa, ya), w);  // H_{b+2}
+          hn = hpass(b + 2, xa, ya);
           load(b + 3, xa, ya);
         }
-        const int row0 = r0 + MT * b + 4 * g;
-        const bool full = r0 + MT * (b + 1) <= r_end && c0 + MT <= a.Wout;
-        acc += static_cast<double>(finish<MAP>(
-            e, o, row0, r_end, col_ok, full,
-            MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr, a.Wout));
+        epilogue(b, o);
       }
       if (b + 1 < nb) {
         stash_all<0>(hn, a.one, v);  // H_{b+2} over H_b
         f4 o[4];
         vblock<1>(w, v, o);
         if (b + 3 <= nb) {
-          hn = hmfma(prep(xa, ya), w);  // H_{b+3}
+          hn = hpass(b + 3, xa, ya);
           load(b + 4, xa, ya);
         }
-        const int row0 = r0 + MT * (b + 1) + 4 * g;
-        const bool full = r0 + MT * (b + 2) <= r_end && c0 + MT <= a.Wout;
-        acc += static_cast<double>(finish<MAP>(
-            e, o, row0, r_end, col_ok, full,
-            MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr, a.Wout));
+        epilogue(b + 1, o);
       }
     }
   }
-  const double s = block_sum(acc, sred);
   // packed: each image owns C * tiles consecutive slots, as the finalize reads them
-  if (threadIdx.x == 0) a.partial[static_cast<int64_t>(plane) * a.tiles + tile] = s;
+  const int64_t slot = static_cast<int64_t>(plane) * a.tiles + tile;
+  if constexpr (MODE == MF_CS) {
+    double s = 0.0, scs = 0.0;
+    block_sum2(acc, acc_cs, sred, &s, &scs);
+    if (threadIdx.x == 0) {
+      a.partial[slot] = s;
+      a.partial_cs[slot] = scs;
+    }
+  } else {
+    const double s = block_sum(acc, sred);
+    if (threadIdx.x == 0) a.partial[slot] = s;
+  }
 }
 
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
@@ -386,13 +487,13 @@ bool mfma_enabled() {
   return !(e && e[0] == '0');
 }
 
-template <bool MAP>
+template <int MODE>
 int occupancy() {
   static int occ = 0;
   if (occ <= 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, reinterpret_cast<const void*>(&ssim_u8_mfma_kernel<MAP>), BLOCK, 0) != hipSuccess ||
+            &v, reinterpret_cast<const void*>(&ssim_u8_mfma_kernel<MODE>), BLOCK, 0) != hipSuccess ||
         v <= 0)
       v = 1;
     occ = v;
@@ -406,6 +507,10 @@ int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) 
   *tiles = 0;
   if (!mfma_enabled() || c.K > MF_MAX_K || c.W % 8 != 0 || c.W < 8) return FA_OK;
   if (!aligned8(c.x) || !aligned8(c.y)) return FA_OK;
+  // float4 stores into the pyramid level (W % 8 == 0 makes every row of it
+  // a multiple of 16 bytes)
+  if (c.px && ((reinterpret_cast<uintptr_t>(c.px) | reinterpret_cast<uintptr_t>(c.py)) & 15))
+    return FA_OK;
   const int64_t s[6] = {c.xsn, c.xsc, c.ysn, c.ysc, c.xsh, c.ysh};
   for (int64_t v : s)
     if (v % 8 != 0) return FA_OK;
@@ -431,11 +536,17 @@ int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) 
   a.one = 1.0f;
   a.map = c.map;
   a.partial = c.partial;
+  a.partial_cs = c.partial_cs;
+  a.px = c.px;
+  a.py = c.py;
+  const int mode = c.partial_cs ? MF_CS : c.map ? MF_MAP : MF_REDUCE;
 
   // Rows per chunk (a multiple of 16): the fewest rounds of resident
   // workgroups times the work of one, charging the extra 16-row block of
   // horizontal work each chunk starts with at 10 rows.
-  const int occ = c.map ? occupancy<true>() : occupancy<false>();
+  const int occ = mode == MF_CS    ? occupancy<MF_CS>()
+                  : mode == MF_MAP ? occupancy<MF_MAP>()
+                                   : occupancy<MF_REDUCE>();
   const int64_t resident = static_cast<int64_t>(cu_count(device)) * occ;
   const int64_t planes = static_cast<int64_t>(c.N) * c.C;
   const int strips = (c.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
@@ -459,12 +570,13 @@ int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) 
   a.tiles = strips * best_chunks;
   const int64_t wgs = planes * a.tiles;
   if (wgs > INT32_MAX) return FA_OK;
-  if (c.map)
-    hipLaunchKernelGGL(ssim_u8_mfma_kernel<true>, dim3(static_cast<unsigned>(wgs)), dim3(BLOCK), 0,
-                       st, a);
+  const dim3 grid(static_cast<unsigned>(wgs));
+  if (mode == MF_CS)
+    hipLaunchKernelGGL(ssim_u8_mfma_kernel<MF_CS>, grid, dim3(BLOCK), 0, st, a);
+  else if (mode == MF_MAP)
+    hipLaunchKernelGGL(ssim_u8_mfma_kernel<MF_MAP>, grid, dim3(BLOCK), 0, st, a);
   else
-    hipLaunchKernelGGL(ssim_u8_mfma_kernel<false>, dim3(static_cast<unsigned>(wgs)), dim3(BLOCK), 0,
-                       st, a);
+    hipLaunchKernelGGL(ssim_u8_mfma_kernel<MF_REDUCE>, grid, dim3(BLOCK), 0, st, a);
   FA_LAUNCH_CHECK();
   *tiles = a.tiles;
   return FA_OK;

@@ -134,3 +134,58 @@ def test_views_aligned_and_not(gpu):
         got = fa.ssim(x, y, data_range=255.0, crop_border=c, reduction="none").cpu().numpy()
         for g, w in zip(got, want):
             assert _rel(float(g), float(w)) <= REL, (c, g, w)
+
+
+# MS-SSIM over uint8: scale 0 (SSIM and cs sums plus the first pyramid level,
+# 2 x 2 means written by the same kernel) runs on the matrix cores
+@pytest.mark.parametrize("shape", [(1, 1, 176, 176), (2, 3, 200, 264), (1, 3, 361, 648),
+                                   (3, 1, 190, 184)])
+def test_ms_ssim(gpu, shape):
+    a, b = u8_pair(shape, 9.0, seed=sum(shape))
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    want = ref.ms_ssim(a, b, 255.0, reduction="none")
+    got = fa.ms_ssim(x, y, data_range=255.0, reduction="none").cpu().numpy()
+    for g, w in zip(got, want):
+        assert _rel(float(g), float(w)) <= REL, (shape, g, w)
+    with _VectorAlu():
+        alu = fa.ms_ssim(x, y, data_range=255.0, reduction="none").cpu().numpy()
+    for g, w in zip(got, alu):
+        assert _rel(float(g), float(w)) <= REL, ("vs strip kernel", g, w)
+
+
+def test_ms_ssim_pyramid_level_exact(gpu):
+    # the level the CS pass writes is the exact 2 x 2 mean of the uint8 input
+    from frame_analytics_amd import backend
+
+    ext = backend.load()
+    a, b = u8_pair((2, 3, 90, 136), 7.0, seed=4)
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    n, c, h, w = a.shape
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    bpp = backend._ssim_workspace(ext, h, w, 11)
+    part = torch.empty((n * c, bpp), dtype=torch.float64, device=gpu)
+    part_cs = torch.empty_like(part)
+    out_s = torch.empty(n * c, dtype=torch.float64, device=gpu)
+    out_cs = torch.empty_like(out_s)
+    px = torch.full((n, c, h // 2, w // 2), -1.0, device=gpu)
+    py = torch.full_like(px, -1.0)
+    import ctypes
+    slots = ctypes.c_int(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = ext.gpu.fa_gpu_ssim_cs_ex(x.data_ptr(), y.data_ptr(), 0, n, c, h, w, None, None, None,
+                                   win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
+                                   (0.03 * 255) ** 2, part.data_ptr(), part_cs.data_ptr(), bpp,
+                                   out_s.data_ptr(), out_cs.data_ptr(), ctypes.addressof(slots),
+                                   px.data_ptr(), py.data_ptr(), 3, 0, stream)
+    assert rc == 0
+    want_x = ref.avg_pool2(a.astype(np.float64))
+    want_y = ref.avg_pool2(b.astype(np.float64))
+    assert np.array_equal(px.cpu().numpy().astype(np.float64), want_x)
+    assert np.array_equal(py.cpu().numpy().astype(np.float64), want_y)
+    s_ref, cs_ref = ref.ssim_maps(a.astype(float), b.astype(float))
+    got_s = out_s.cpu().numpy().reshape(n, c)
+    got_cs = out_cs.cpu().numpy().reshape(n, c)
+    assert np.allclose(got_s, s_ref.mean(axis=(-2, -1)), rtol=1e-6, atol=0)
+    assert np.allclose(got_cs, cs_ref.mean(axis=(-2, -1)), rtol=1e-6, atol=0)
