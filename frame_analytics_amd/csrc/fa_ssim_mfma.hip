@@ -172,8 +172,8 @@ __device__ inline void stash(f4 h, float one, u4& bhi, u4& blo) {
 
 struct Weights {
   h8 bh, bl;      // horizontal B: w(8g + i - n) * 2^9, hi and lo
-  h8 eh, el;      // vertical A, even steps: block j in k = 8g + 0..3
-  h8 oh, ol;      // vertical A, odd steps: block j in k = 8g + 4..7
+  h8 eh, el;      // vertical A, even steps: block j in k = 8g + 0..3 (odd
+                  // steps: halves swapped, block j in k = 8g + 4..7)
 };
 
 __device__ inline float tap(const float* win, int K, int d) {
@@ -191,13 +191,9 @@ __device__ inline Weights load_weights(const float* win, int K, int g, int n) {
     w.bl[i] = lo;
     // input row (relative to the older block) that k = 8g + i stands for
     const int re = i < 4 ? 4 * g + i : MT + 4 * g + (i - 4);
-    const int ro = i < 4 ? MT + 4 * g + i : 4 * g + (i - 4);
     split2(tap(win, K, re - n) * WSCALE, hi, lo);
     w.eh[i] = hi;
     w.el[i] = lo;
-    split2(tap(win, K, ro - n) * WSCALE, hi, lo);
-    w.oh[i] = hi;
-    w.ol[i] = lo;
   }
   return w;
 }
@@ -342,8 +338,16 @@ __device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, uint2 
 template <int PAR>
 __device__ inline void vblock(const Weights& w, const VState& v, f4* o) {
   const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-  const h8 ah = PAR == 0 ? w.eh : w.oh;
-  const h8 al = PAR == 0 ? w.el : w.ol;
+  h8 ah = w.eh, al = w.el;
+  if constexpr (PAR == 1) {
+    // the odd layout is the even one with its halves swapped, built here in
+    // each odd step (4 moves) so that it holds no registers between steps:
+    // that keeps the REDUCE and MAP kernels within 128 VGPRs (4 waves/SIMD)
+    u4 h = bc<u4>(w.eh), l = bc<u4>(w.el);
+    asm volatile("" : "+v"(h), "+v"(l));  // keeps the copy inside the loop
+    ah = bc<h8>(u4{h[2], h[3], h[0], h[1]});
+    al = bc<h8>(u4{l[2], l[3], l[0], l[1]});
+  }
 #pragma unroll
   for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.hi[q]), z);
 #pragma unroll
