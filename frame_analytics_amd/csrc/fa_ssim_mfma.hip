@@ -123,12 +123,13 @@ __device__ inline Frag prep(uint2 xa, uint2 ya) {
     const us2 yi = bc<us2>(yt) - k6480;
     const us2 d = bc<us2>(xt) - bc<us2>(yt);
     // (x-128)(y-128) in [-16256, 16384] = 256 q + l, l = low byte, q = high
-    // byte as signed (q + 128 = high byte ^ 0x80); (x-y)^2 <= 65025 likewise
-    // with q the plain high byte
-    const uint32_t p3 = bc<uint32_t>(xi * yi);
+    // byte as signed: adding 0x8000 (one v_pk_mad_u16 with the product) makes
+    // the high byte q + 128 and leaves the low byte; (x-y)^2 <= 65025 splits
+    // the same way with q the plain high byte
+    const us2 k8000 = {0x8000, 0x8000};
+    const uint32_t p3s = bc<uint32_t>(xi * yi + k8000);
     const uint32_t p4 = bc<uint32_t>(d * d);
-    const uint32_t p3s = p3 ^ 0x80008000u;
-    o3l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3, 0x04020400u), m, c0);
+    o3l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3s, 0x04020400u), m, c0);
     o3h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3s, 0x04030401u), mq, cq128);
     o4l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04020400u), m, c0);
     o4h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04030401u), mq, cq0);
@@ -275,14 +276,13 @@ __device__ inline void ssim_cs_px(const Epi& e, float U, float V, float X, float
 // Adds this lane's four outputs (rows row0 .. row0 + 3 of its column) to the
 // lane's float64 sums; `full` (uniform) says the whole 16 x 16 block lies
 // inside the map.
-template <int MODE>
+template <int MODE, bool FULL>
 __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, bool col_ok,
-                              bool full, float* map_px, int Wout, double& acc,
-                              double& acc_cs) {
+                              float* map_px, int Wout, double& acc, double& acc_cs) {
   float rs = 0.0f, rcs = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const bool ok = full || (col_ok && row0 + i < row_end);
+    const bool ok = FULL || (col_ok && row0 + i < row_end);
     if constexpr (MODE == MF_CS) {
       float s, cs;
       ssim_cs_px(e, o[0][i], o[1][i], o[2][i], o[3][i], s, cs);
@@ -413,11 +413,19 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
     }
     const uint32_t pcol = static_cast<uint32_t>(c0 + 8 * g) >> 1;
 
-    // rows past the image only feed output rows past Hout: clamped
-    auto load = [&](int j, uint2& xa, uint2& ya) {
-      const uint32_t r = static_cast<uint32_t>(min(r0 + MT * j + n, a.H - 1));
-      xa = *reinterpret_cast<const uint2*>(xp + r * a.xsh + cc);
-      ya = *reinterpret_cast<const uint2*>(yp + r * a.ysh + cc);
+    // rows past the image only feed output rows past Hout: clamped.  load(j)
+    // is called for j = 0, 1, 2, ... in order, so the row offsets advance by
+    // 16 rows per call and are clamped to the last row's.
+    const uint32_t rl = static_cast<uint32_t>(min(r0 + n, a.H - 1));
+    const uint32_t xmax = static_cast<uint32_t>(a.H - 1) * a.xsh + cc;
+    const uint32_t ymax = static_cast<uint32_t>(a.H - 1) * a.ysh + cc;
+    const uint32_t xstep = MT * a.xsh, ystep = MT * a.ysh;
+    uint32_t xo = rl * a.xsh + cc, yo = rl * a.ysh + cc;  // block 0
+    auto load = [&](int, uint2& xa, uint2& ya) {
+      xa = *reinterpret_cast<const uint2*>(xp + xo);
+      ya = *reinterpret_cast<const uint2*>(yp + yo);
+      xo = min(xo + xstep, xmax);
+      yo = min(yo + ystep, ymax);
     };
     // horizontal pass of block j (and its share of the pyramid)
     auto hpass = [&](int j, uint2 xa, uint2 ya) {
@@ -428,10 +436,11 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
     };
     auto epilogue = [&](int b, const f4* o) {
       const int row0 = r0 + MT * b + 4 * g;
-      const bool full = r0 + MT * (b + 1) <= r_end && c0 + MT <= a.Wout;
-      finish<MODE>(e, o, row0, r_end, col_ok, full,
-                   MODE == MF_MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr,
-                   a.Wout, acc, acc_cs);
+      float* mp = MODE == MF_MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr;
+      if (r0 + MT * (b + 1) <= r_end && c0 + MT <= a.Wout)  // uniform: the whole block
+        finish<MODE, true>(e, o, row0, r_end, col_ok, mp, a.Wout, acc, acc_cs);
+      else
+        finish<MODE, false>(e, o, row0, r_end, col_ok, mp, a.Wout, acc, acc_cs);
     };
 
     // Software pipeline: the horizontal MFMAs of block j + 2 are issued
