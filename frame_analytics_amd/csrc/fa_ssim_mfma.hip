@@ -13,31 +13,33 @@
 //
 // Horizontal pass, one 16 x 16 block H_j per step:  H[r][c] = sum_k P[r][k] w(k - c)
 //   A = the raw planes: lane l holds row n of the 16-row block, input columns
-//       8g .. 8g+7 of the strip's 32-column window (one 8-byte load of x, one
+//       8g .. 8g+7 of the wave's 32-column window (one 8-byte load of x, one
 //       of y), turned into exact fp16 operands:
 //         x' and y' (integers in [-128, 127]),
-//         x'y' = 128 q3 + l3 with q3 in [-127, 128], l3 in [0, 127],
-//         (x-y)^2 = 128 q4 + l4 with q4 in [0, 508], l4 in [0, 127],
-//       built with packed 16-bit integer arithmetic and fp16 bit patterns
-//       (1024 + v for 0 <= v < 1024 is 0x6400 | v).
-//   B = the window, scaled by 2^10 and split into fp16 hi + lo pieces (the
-//       scale keeps the low piece of the smallest weight normal); the q
-//       planes use the same weights times 128.
-//   Products of fp16 integers and fp16 weights are exact and accumulate in
-//   float32, so each H value carries the window to 22 bits and float32
-//   accumulation, as the vector-ALU kernel does.
+//         x'y' = 256 q3 + l3 with q3 in [-64, 64], l3 in [0, 255],
+//         (x-y)^2 = 256 q4 + l4 with q4 in [0, 254], l4 in [0, 255],
+//       built with v_perm_b32, packed 16-bit integer arithmetic and fp16 bit
+//       patterns (0x64vv is 1024 + v), x', y', l scaled by 2^-9 and q by
+//       256 * 2^-9, all exactly.
+//   B = the window scaled by 2^9 and split into fp16 hi + lo pieces (the scale
+//       keeps the low piece of the smallest Gaussian weight normal).  The
+//       scales cancel, products of fp16 operands are exact and accumulate in
+//       float32: each H value carries the window to 22 bits, with float32
+//       accumulation as in the vector-ALU kernel.  12 MFMAs per block.
 //
 // Vertical pass, 16 output rows from H_j and H_{j+1}:  O[r][c] = sum_k w(k - r) H[k][c]
-//   B = the H values split into fp16 hi + lo (after undoing the 2^10); the D
-//       fragment of the horizontal pass already holds rows 4g .. 4g+3 of its
-//       block in column n, which is the B fragment's column n, so the rows of
-//       H_j and H_{j+1} sit in k = 8g + i as (block j, rows 4g+i) for i < 4
-//       and (block j+1, rows 4g+i-4) for i >= 4.  The sum over k does not
-//       care about order, so the A fragment (the window, hi + lo) is laid out
-//       to match; even and odd steps swap which half holds the newer block
-//       (two A layouts), so no register ever moves.
-//   D = rows 4g .. 4g+3 of the output block in column n: every lane finishes
-//       four output pixels with all four moments in its own registers.
+//   B = the H values split into fp16 hi + lo; the D fragment of the
+//       horizontal pass already holds rows 4g .. 4g+3 of its block in column
+//       n, which is the B fragment's column n, so the rows of H_j and H_{j+1}
+//       sit in k = 8g + i as (block j, rows 4g+i) for i < 4 and (block j+1,
+//       rows 4g+i-4) for i >= 4.  The sum over k does not care about order,
+//       so the A fragment (the window scaled by 2^9, hi + lo) is laid out to
+//       match; even and odd steps swap which half of the B fragment holds the
+//       newer block, and the A fragment's halves swap with it, so the H values
+//       never move.  12 MFMAs per block (hi.hi, lo.hi, hi.lo per moment).
+//   D = rows 4g .. 4g+3 of the output block in column n, scaled by 2^9: every
+//       lane finishes four output pixels with all four moments in its own
+//       registers.
 #include "fa_ssim_mfma.h"
 
 #include <algorithm>
