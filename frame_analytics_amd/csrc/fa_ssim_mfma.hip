@@ -179,22 +179,34 @@ struct Weights {
                   // steps: halves swapped, block j in k = 8g + 4..7)
 };
 
-__device__ inline float tap(const float* win, int K, int d) {
-  return (d >= 0 && d < K) ? win[d] : 0.0f;
+// The window, zero padded, in LDS: swin[16 + d] = w(d) for -16 <= d < 32
+// (every tap offset a fragment uses).  Each wave fills its own copy, one
+// load per lane, and reads it back in the same wave (LDS operations of a wave
+// complete in order), so no barrier is needed and the 16 tap reads per lane
+// are unconditional.
+constexpr int WIN_PAD = 16, WIN_LEN = 48;
+
+__device__ inline void stage_window(const float* win, int K, float* sw, int lane) {
+  if (lane < WIN_LEN) {
+    const int d = lane - WIN_PAD;
+    sw[lane] = (d >= 0 && d < K) ? win[d] : 0.0f;
+  }
 }
 
-__device__ inline Weights load_weights(const float* win, int K, int g, int n) {
+__device__ inline float tap(const float* sw, int d) { return sw[WIN_PAD + d]; }
+
+__device__ inline Weights load_weights(const float* sw, int g, int n) {
   Weights w;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     _Float16 hi, lo;
-    const float wh = tap(win, K, 8 * g + i - n) * WSCALE;
+    const float wh = tap(sw, 8 * g + i - n) * WSCALE;
     split2(wh, hi, lo);
     w.bh[i] = hi;
     w.bl[i] = lo;
     // input row (relative to the older block) that k = 8g + i stands for
     const int re = i < 4 ? 4 * g + i : MT + 4 * g + (i - 4);
-    split2(tap(win, K, re - n) * WSCALE, hi, lo);
+    split2(tap(sw, re - n) * WSCALE, hi, lo);
     w.eh[i] = hi;
     w.el[i] = lo;
   }
@@ -368,6 +380,7 @@ __device__ inline void vblock(const Weights& w, const VState& v, f4* o) {
 template <int MODE>
 __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs a) {
   __shared__ double sred[2 * WAVES_PER_BLOCK];
+  __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
   const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
   const int plane = t / a.tiles;
   const int tile = t - plane * a.tiles;
@@ -390,7 +403,8 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
     // this lane's 8 input columns; a chunk past the image only feeds output
     // columns past Wout, so it is clamped (W % 8 == 0: chunks never straddle)
     const uint32_t cc = static_cast<uint32_t>(min(c0 + 8 * g, a.W - 8));
-    const Weights w = load_weights(a.win, a.K, g, n);
+    stage_window(a.win, a.K, swin[wave], lane);
+    const Weights w = load_weights(swin[wave], g, n);
     const Epi e = {2.0f * 128.0f * 128.0f + a.C1, a.C2};
     const bool col_ok = c0 + n < a.Wout;
     float* map_col = nullptr;
