@@ -159,8 +159,9 @@ def _host_model():
 
 def cpu_configs0(seconds=0.6):
     """configs[0] (1x3x512x512 uint8, sigma 8) through fa.* on CPU tensors
-    (libfa_cpu.so), each call timed best-of over ~`seconds`, and the reference
-    CPU build's kernel for the same call where it has one."""
+    (libfa_cpu.so), each call timed best-of over ~`seconds`; beside it this
+    build's host kernel alone (``kernel_ms``) and the reference CPU build's
+    kernel for the same call (``reference_kernel_ms``), both through the C ABI."""
     import numpy as np
     import torch
 
@@ -176,13 +177,40 @@ def cpu_configs0(seconds=0.6):
     b = np.clip(a.astype(np.int16) + np.round(rng.normal(0, 8, shape)).astype(np.int16),
                 0, 255).astype(np.uint8)
     ta, tb = torch.from_numpy(a), torch.from_numpy(b)
+    # this build's host kernels through the same C ABI and arguments as the
+    # reference's (oracle/ref_cpu.py), so the two kernel columns compare alike
+    mine = backend.load_cpu()
+    pa, pb = a.ctypes.data, b.ctypes.data
+    n, c, h, w = shape
+    win = ref_cpu._window(11, 1.5)
+
+    def my_pixel(bias):
+        out = np.zeros(1, np.float64)
+        assert mine.fa_cpu_pixel_reduce(pa, pb, 0, n, a.size // n, 0, 0.0, bias, 0,
+                                        out.ctypes.data) == 0
+
+    def my_ssim():
+        per_plane = np.zeros(n * c, np.float64)
+        assert mine.fa_cpu_ssim(pa, pb, 0, n, c, h, w, win.ctypes.data, 11, 127.5,
+                                (0.01 * 255) ** 2, (0.03 * 255) ** 2, None,
+                                per_plane.ctypes.data) == 0
+
+    def my_gmsd():
+        mean, std = np.zeros(n, np.float64), np.zeros(n, np.float64)
+        assert mine.fa_cpu_gmsd(pa, pb, 0, n, c, h, w, 170.0, (1e-6 * 255) ** 2, 1,
+                                mean.ctypes.data, std.ctypes.data) == 0
+
+    bias = 20 * np.log10(255.0)
     calls = {
-        "ssim": (lambda: fa.ssim(ta, tb, data_range=255.0), lambda: ref_cpu.ssim_per_image(a, b)),
-        "psnr": (lambda: fa.psnr(ta, tb),
-                 lambda: ref_cpu.pixel_reduce(a, b, "mse", psnr_bias=20 * np.log10(255.0))),
-        "mse": (lambda: fa.mse(ta, tb), lambda: ref_cpu.pixel_reduce(a, b, "mse")),
-        "gmsd": (lambda: fa.gmsd(ta, tb, data_range=255.0), lambda: ref_cpu.gmsd(a, b)),
-        "ms_ssim": (lambda: fa.ms_ssim(ta, tb, data_range=255.0), None),
+        "ssim": (lambda: fa.ssim(ta, tb, data_range=255.0), my_ssim,
+                 lambda: ref_cpu.ssim_per_image(a, b)),
+        "psnr": (lambda: fa.psnr(ta, tb), lambda: my_pixel(bias),
+                 lambda: ref_cpu.pixel_reduce(a, b, "mse", psnr_bias=bias)),
+        "mse": (lambda: fa.mse(ta, tb), lambda: my_pixel(-1e300),
+                lambda: ref_cpu.pixel_reduce(a, b, "mse")),
+        "gmsd": (lambda: fa.gmsd(ta, tb, data_range=255.0), my_gmsd,
+                 lambda: ref_cpu.gmsd(a, b)),
+        "ms_ssim": (lambda: fa.ms_ssim(ta, tb, data_range=255.0), None, None),
     }
     have_ref = ref_cpu.available()
     if have_ref:
@@ -190,8 +218,10 @@ def cpu_configs0(seconds=0.6):
     out = {"workload": "1x3x512x512 uint8 (configs[0]), fa.* on CPU tensors",
            "host": f"{_host_model()}, {os.cpu_count()} logical CPUs, "
                    f"{torch.get_num_threads()} threads"}
-    for name, (mine, theirs) in calls.items():
-        row = {"ms": round(_best_of(mine, seconds) * 1e3, 4)}
+    for name, (call, kern, theirs) in calls.items():
+        row = {"ms": round(_best_of(call, seconds) * 1e3, 4)}
+        if kern is not None:
+            row["kernel_ms"] = round(_best_of(kern, seconds) * 1e3, 4)
         if theirs is not None and have_ref:
             row["reference_kernel_ms"] = round(_best_of(theirs, seconds) * 1e3, 4)
         out[name] = row

@@ -329,7 +329,7 @@ inline double lane_sum(const double* a, int n) {
 // --------------------------------------------------------------------------
 // pixel reductions
 // --------------------------------------------------------------------------
-constexpr int64_t PIX_CHUNK = int64_t(1) << 18;  // elements per task
+constexpr int64_t PIX_CHUNK = int64_t(1) << 15;  // elements per task: 24 tasks at 1x3x512x512
 
 // Exact sum of (a-b)^2 of n uint8 pairs: |a-b| from two saturating
 // subtractions, widened to 16 bits in-lane and squared + pair-summed by madd.
