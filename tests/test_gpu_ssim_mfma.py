@@ -39,7 +39,15 @@ class _VectorAlu:
         os.environ.pop("FA_SSIM_MFMA", None)
 
 
+def _u8(a):
+    """The planes as uint8 (natural_pair returns integer-valued float64)."""
+    a = np.asarray(a)
+    return a if a.dtype == np.uint8 else np.clip(np.rint(a), 0, 255).astype(np.uint8)
+
+
 def _check(a, b, gpu, win=11, sigma=1.5, L=255.0, K=(0.01, 0.03)):
+    a, b = _u8(a), _u8(b)
+    assert a.dtype == np.uint8 and a.shape[-1] % 8 == 0  # the matrix-core kernel's inputs
     x = torch.as_tensor(a, device=gpu)
     y = torch.as_tensor(b, device=gpu)
     kw = dict(data_range=L, win_size=win, sigma=sigma, K=K)
@@ -64,6 +72,14 @@ def _check(a, b, gpu, win=11, sigma=1.5, L=255.0, K=(0.01, 0.03)):
 def test_shapes(gpu, h, w):
     a, b = natural_pair(h, w, 9.0, seed=h * 1000 + w)
     _check(a[None, None], b[None, None], gpu)
+
+
+# the narrowest rows the kernel takes (W = 8: one 8-byte chunk, clamped for
+# every lane past it) and the shortest maps (Hout = 1)
+@pytest.mark.parametrize("h,w,win", [(8, 8, 3), (9, 16, 5), (20, 8, 7), (11, 24, 11), (3, 40, 3)])
+def test_narrow_and_short(gpu, h, w, win):
+    a, b = natural_pair(h, w, 11.0, seed=h * 100 + w + win)
+    _check(a[None, None], b[None, None], gpu, win=win)
 
 
 @pytest.mark.parametrize("win", [3, 5, 7, 9, 11])
@@ -112,7 +128,7 @@ def test_extremes(gpu, kind):
 
 def test_identity_is_one(gpu):
     a, _ = natural_pair(80, 128, 5.0, seed=2)
-    x = torch.as_tensor(a[None, None], device=gpu)
+    x = torch.as_tensor(_u8(a)[None, None], device=gpu)
     got = fa.ssim(x, x.clone(), data_range=255.0, return_map=True)
     assert float((got.double() - 1.0).abs().max()) <= 1e-6
 
