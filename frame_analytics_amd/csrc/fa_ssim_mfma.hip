@@ -53,7 +53,6 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-typedef short ss2 __attribute__((ext_vector_type(2)));
 
 template <class To, class From>
 __device__ inline To bc(From v) {
