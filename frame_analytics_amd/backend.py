@@ -45,6 +45,8 @@ _DTYPE_CODE = {
     torch.float32: 3,
     torch.float64: 4,
 }
+# include/fa_abi.h: OR-ed into FA_F32 for the float32 levels of a uint8 pyramid
+FA_DTYPE_U8_PYRAMID = 0x100
 
 _PSNR_NONE = -1.0e300
 _OP_MSE = 0
@@ -576,12 +578,13 @@ def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2, pool_dtype=None, luma=
     return (out_s, out_cs) if pool_dtype is None else (out_s, out_cs, px, py)
 
 
-def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None):
+def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None, u8_pyramid=False):
     """One inference MS-SSIM scale left unreduced: ``(partial, partial_cs,
     slots, npix, px, py)`` -- the per-plane partial sums of the SSIM and cs
     maps (``slots`` per plane, packed), the plane's output pixel count, and the
     next pyramid level (``None`` at the coarsest scale).  The partial sums go
-    to :func:`ms_ssim_reduce`; nothing is synchronised."""
+    to :func:`ms_ssim_reduce`; nothing is synchronised.  ``u8_pyramid``: x and
+    y are float32 levels of a uint8 pyramid (FA_DTYPE_U8_PYRAMID)."""
     ext = load()
     winf = _win_f32(win)
     n, c, h, w = x.shape
@@ -598,8 +601,13 @@ def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None):
         py = torch.empty_like(px)
     pcode = _DTYPE_CODE[pool_dtype if pool_dtype is not None else torch.float64]
     slots = ctypes.c_int(0)
+    code = _DTYPE_CODE[x.dtype]
+    if u8_pyramid:
+        if x.dtype != torch.float32 or luma is not None:
+            raise ValueError("u8_pyramid needs float32 levels without luma")
+        code |= FA_DTYPE_U8_PYRAMID
     _check(ext.gpu.fa_gpu_ssim_cs_ex(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
+        _ptr(x), _ptr(y), code, n, c, h, w, xs, ys, _luma_arg(luma),
         _ptr(winf), k, float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
         bpp, None, None, ctypes.byref(slots), _ptr(px), _ptr(py), pcode, _dev(x),
         _stream(x)), ext)

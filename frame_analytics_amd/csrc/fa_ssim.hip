@@ -853,6 +853,11 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
                         double* out_cs, int* out_slots, void* px, void* py, int pool_dtype,
                         int device, void* stream) {
   if (!x || !y || !win || !partial || !partial_cs) return FA_E_ARG;
+  // FA_DTYPE_U8_PYRAMID: float32 samples of a uint8 pyramid level (a hint
+  // that admits the matrix-core kernel; the strip kernel reads plain float32)
+  const bool u8_pyramid = (dtype & FA_DTYPE_U8_PYRAMID) != 0;
+  dtype &= ~FA_DTYPE_U8_PYRAMID;
+  if (u8_pyramid && dtype != FA_F32) return FA_E_DTYPE;
   // plane means, or (both null) the partial sums left for fa_gpu_ms_ssim_reduce
   if ((out_s == nullptr) != (out_cs == nullptr)) return FA_E_ARG;
   if (!out_s && !out_slots) return FA_E_ARG;
@@ -884,14 +889,13 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   a.py = py;
   a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
   int tiles = 0;
-  if (dtype == FA_U8 && !luma && (!px || pool_dtype == FA_F32)) {
-    // uint8 planes: the matrix-core kernel when the layout allows
-    // (fa_ssim_mfma.hip), pyramid level included
-    const SsimMfmaCall mc = {static_cast<const uint8_t*>(x), static_cast<const uint8_t*>(y),
-                             a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh, N, C, H, W, Hout, Wout,
-                             K, win, C1, C2, nullptr, partial, bpp, partial_cs,
-                             static_cast<float*>(px), static_cast<float*>(py)};
-    rc = ssim_u8_mfma(mc, device, st, &tiles);
+  if ((dtype == FA_U8 || u8_pyramid) && !luma && (!px || pool_dtype == FA_F32)) {
+    // uint8 planes and the float32 levels of their pyramid: the matrix-core
+    // kernel when the layout allows (fa_ssim_mfma.hip), next level included
+    const SsimMfmaCall mc = {x, y, u8_pyramid, a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh,
+                             N, C, H, W, Hout, Wout, K, win, C1, C2, nullptr, partial, bpp,
+                             partial_cs, static_cast<float*>(px), static_cast<float*>(py)};
+    rc = ssim_mfma(mc, device, st, &tiles);
     if (rc != FA_OK) return rc;
   }
   if (tiles == 0) {
@@ -944,10 +948,10 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
   if (dtype == FA_U8 && !lm) {
     // uint8 planes: both Gaussian passes on the matrix cores when the layout
     // allows (fa_ssim_mfma.hip); otherwise the strip kernel below
-    const SsimMfmaCall mc = {static_cast<const uint8_t*>(x), static_cast<const uint8_t*>(y),
-                             a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh, N, C, H, W, Hout, Wout,
-                             K, win, C1, C2, map_out, partial, bpp, nullptr, nullptr, nullptr};
-    rc = ssim_u8_mfma(mc, device, st, &tiles);
+    const SsimMfmaCall mc = {x, y, false, a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh,
+                             N, C, H, W, Hout, Wout, K, win, C1, C2, map_out, partial, bpp,
+                             nullptr, nullptr, nullptr};
+    rc = ssim_mfma(mc, device, st, &tiles);
     if (rc != FA_OK) return rc;
   }
   if (tiles == 0) {
@@ -1009,6 +1013,7 @@ FA_API int fa_gpu_ssim_cs(const void* x, const void* y, int dtype, int N,
                           double* partial_cs, int bpp, double* out_s,
                           double* out_cs, int device, void* stream) {
   if (!out_s || !out_cs) return FA_E_ARG;
+  if (dtype & FA_DTYPE_U8_PYRAMID) return FA_E_DTYPE;  // a hint of the _ex entry only
   return ssim_cs_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, win, K, shift, C1,
                       C2, partial, partial_cs, bpp, out_s, out_cs, nullptr, nullptr, nullptr,
                       FA_F64, device, stream);
@@ -1026,8 +1031,9 @@ FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N, int
   if (px) {
     // float32 levels hold the pyramid of uint8 input exactly, float64 levels
     // that of every floating input; a luma plane pools into float64
+    const int base = dtype & ~FA_DTYPE_U8_PYRAMID;
     const bool ok = pool_dtype == FA_F64 ||
-                    (pool_dtype == FA_F32 && !luma && (dtype == FA_U8 || dtype == FA_F32));
+                    (pool_dtype == FA_F32 && !luma && (base == FA_U8 || base == FA_F32));
     if (!ok) return FA_E_DTYPE;
   }
   return ssim_cs_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, win, K, shift, C1,

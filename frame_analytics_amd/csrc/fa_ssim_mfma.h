@@ -5,10 +5,12 @@
 
 namespace fa {
 
-// One fa_gpu_ssim / fa_gpu_ssim_ex call over uint8 planes without luma.
+// One fa_gpu_ssim(_ex) / fa_gpu_ssim_cs(_ex) call over uint8 planes without
+// luma, or (pyr) over float32 planes of a uint8 input's 2 x 2 pyramid.
 struct SsimMfmaCall {
-  const uint8_t* x;
-  const uint8_t* y;
+  const void* x;
+  const void* y;
+  bool pyr;                    // float32 samples, multiples of 4^-s in [0, 255], s <= 4
   int64_t xsn, xsc, ysn, ysc;  // image and channel strides (elements)
   int xsh, ysh;                // row strides
   int N, C, H, W, Hout, Wout, K;
@@ -26,11 +28,12 @@ struct SsimMfmaCall {
 };
 
 // Launches the matrix-core SSIM forward (or CS pass) when the call fits it
-// (uint8, 8-byte aligned rows and planes, K <= 16, enough partial slots,
-// 16-byte aligned pyramid planes).  Returns FA_OK and
+// (rows and planes aligned to 8 samples, 8-byte (uint8) or 16-byte (float)
+// aligned bases, K <= 16, enough partial slots, 16-byte aligned pyramid
+// output planes).  Returns FA_OK and
 // sets *tiles (partial slots used per plane) when it launched; returns FA_OK
 // with *tiles = 0 when the call does not fit, so the caller runs the
 // vector-ALU strip kernel instead.
-int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles);
+int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles);
 
 }  // namespace fa

@@ -44,6 +44,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace fa {
 namespace {
@@ -66,8 +67,8 @@ constexpr int MF_MAX_K = 16;           // 16 output rows + K - 1 <= 32 input row
 enum { MF_REDUCE = 0, MF_MAP = 1, MF_CS = 2 };
 
 struct MfArgs {
-  const uint8_t* x;
-  const uint8_t* y;
+  const void* x;  // uint8 samples, or float samples of a uint8 pyramid level
+  const void* y;
   int64_t xsn, xsc, ysn, ysc;
   uint32_t xsh, ysh;
   int C, H, W, Hout, Wout, K;
@@ -91,6 +92,7 @@ __device__ inline f4 mfma(h8 a, h8 b, f4 c) {
 // integers times powers of two), so one set of weights serves all six.
 struct Frag {
   h8 x, y, q3, l3, q4, l4;
+  h8 xl, yl;  // pyramid levels only: the low fp16 pieces of x', y'
 };
 
 __device__ inline uint32_t pkfma(uint32_t bits, h2 m, h2 c) {
@@ -135,7 +137,14 @@ __device__ inline Frag prep(uint2 xa, uint2 ya) {
     o4l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04020400u), m, c0);
     o4h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04030401u), mq, cq0);
   }
-  return Frag{bc<h8>(ox), bc<h8>(oy), bc<h8>(o3h), bc<h8>(o3l), bc<h8>(o4h), bc<h8>(o4l)};
+  Frag f;
+  f.x = bc<h8>(ox);
+  f.y = bc<h8>(oy);
+  f.q3 = bc<h8>(o3h);
+  f.l3 = bc<h8>(o3l);
+  f.q4 = bc<h8>(o4h);
+  f.l4 = bc<h8>(o4l);
+  return f;
 }
 
 // fp16 hi + lo of v (|v| < 65504): hi rounds to nearest, lo rounds the exact
@@ -161,12 +170,14 @@ __device__ inline void split_pair(float v0, float v1, float one, uint32_t& hi, u
 
 // The four H values of a D fragment into half HALF (u4 elements 2 HALF,
 // 2 HALF + 1) of the vertical pass's B fragments.
-template <int HALF>
+template <int HALF, bool PYR>
 __device__ inline void stash(f4 h, float one, u4& bhi, u4& blo) {
+  // pyramid levels are not pre-scaled, so their sums carry the window's 2^9
+  constexpr float sc = PYR ? 1.0f / WSCALE : 1.0f;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     uint32_t hi, lo;
-    split_pair(h[2 * p], h[2 * p + 1], one, hi, lo);
+    split_pair(h[2 * p] * sc, h[2 * p + 1] * sc, one, hi, lo);
     bhi[2 * HALF + p] = hi;
     blo[2 * HALF + p] = lo;
   }
@@ -223,6 +234,11 @@ struct HAcc {
   f4 x, y, p3, p4;
 };
 
+// 12 MFMAs either way.  uint8: x', y' are exact single pieces (2 each), the
+// byte pieces of x'y' and (x-y)^2 take both window pieces (4 each).  Pyramid
+// levels: every plane is hi + lo and the lo.lo product (2^-22 of the sum) is
+// left out (3 each).
+template <bool PYR>
 __device__ inline HAcc hmfma(const Frag& f, const Weights& w) {
   const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
   HAcc h;
@@ -236,17 +252,77 @@ __device__ inline HAcc hmfma(const Frag& f, const Weights& w) {
   h.p4 = mfma(f.q4, w.bl, h.p4);
   h.p3 = mfma(f.l3, w.bh, h.p3);
   h.p4 = mfma(f.l4, w.bh, h.p4);
-  h.p3 = mfma(f.l3, w.bl, h.p3);
-  h.p4 = mfma(f.l4, w.bl, h.p4);
+  if constexpr (PYR) {
+    h.x = mfma(f.xl, w.bh, h.x);
+    h.y = mfma(f.yl, w.bh, h.y);
+  } else {
+    h.p3 = mfma(f.l3, w.bl, h.p3);
+    h.p4 = mfma(f.l4, w.bl, h.p4);
+  }
   return h;
 }
 
-template <int HALF>
+template <int HALF, bool PYR>
 __device__ inline void stash_all(const HAcc& h, float one, VState& v) {
-  stash<HALF>(h.x, one, v.hi[0], v.lo[0]);
-  stash<HALF>(h.y, one, v.hi[1], v.lo[1]);
-  stash<HALF>(h.p3, one, v.hi[2], v.lo[2]);
-  stash<HALF>(h.p4, one, v.hi[3], v.lo[3]);
+  stash<HALF, PYR>(h.x, one, v.hi[0], v.lo[0]);
+  stash<HALF, PYR>(h.y, one, v.hi[1], v.lo[1]);
+  stash<HALF, PYR>(h.p3, one, v.hi[2], v.lo[2]);
+  stash<HALF, PYR>(h.p4, one, v.hi[3], v.lo[3]);
+}
+
+// One lane's 8 samples of one 16-row block: 8 bytes of x and of y (uint8), or
+// 8 floats of each (pyramid levels).
+template <bool PYR>
+struct Raw;
+template <>
+struct Raw<false> {
+  uint2 x, y;
+};
+template <>
+struct Raw<true> {
+  float4 x0, x1, y0, y1;
+};
+
+__device__ inline Frag prep(const Raw<false>& r, float) { return prep(r.x, r.y); }
+
+// Pyramid levels of uint8 input: every sample is a multiple of 4^-s in
+// [0, 255] (s <= 4), so x' = x - 128 is exact in float32 and splits exactly
+// into fp16 hi + lo (at most 16 significant bits); x'y' and (x'-y')^2 are
+// formed in float32, as the strip kernel forms them, and split hi + lo (22
+// bits).  No scaling: the window's 2^9 is taken out of the sums (stash).
+__device__ inline Frag prep(const Raw<true>& r, float one) {
+  const float xs[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
+  const float ys[8] = {r.y0.x, r.y0.y, r.y0.z, r.y0.w, r.y1.x, r.y1.y, r.y1.z, r.y1.w};
+  u4 ox, oxl, oy, oyl, o3h, o3l, o4h, o4l;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a0 = xs[2 * j] - 128.0f, a1 = xs[2 * j + 1] - 128.0f;
+    const float b0 = ys[2 * j] - 128.0f, b1 = ys[2 * j + 1] - 128.0f;
+    const float d0 = a0 - b0, d1 = a1 - b1;
+    uint32_t h, l;
+    split_pair(a0, a1, one, h, l);
+    ox[j] = h;
+    oxl[j] = l;
+    split_pair(b0, b1, one, h, l);
+    oy[j] = h;
+    oyl[j] = l;
+    split_pair(a0 * b0, a1 * b1, one, h, l);
+    o3h[j] = h;
+    o3l[j] = l;
+    split_pair(d0 * d0, d1 * d1, one, h, l);
+    o4h[j] = h;
+    o4l[j] = l;
+  }
+  Frag f;
+  f.x = bc<h8>(ox);
+  f.xl = bc<h8>(oxl);
+  f.y = bc<h8>(oy);
+  f.yl = bc<h8>(oyl);
+  f.q3 = bc<h8>(o3h);
+  f.l3 = bc<h8>(o3l);
+  f.q4 = bc<h8>(o4h);
+  f.l4 = bc<h8>(o4l);
+  return f;
 }
 
 // Per-pixel SSIM from the four filtered moments, all scaled by 2^9:
@@ -334,7 +410,8 @@ __device__ inline float4 pool4(uint2 a, uint2 b) {
                      0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.y, m1, __builtin_amdgcn_udot4(b.y, m1, 0u, false), false)));
 }
 
-__device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, uint2 xa, uint2 ya) {
+__device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, const Raw<false>& r) {
+  const uint2 xa = r.x, ya = r.y;
   // every lane takes part in the DPP moves; only even lanes store
   const uint2 xb = {static_cast<uint32_t>(lane_xor1(static_cast<int>(xa.x))),
                     static_cast<uint32_t>(lane_xor1(static_cast<int>(xa.y)))};
@@ -345,6 +422,23 @@ __device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, uint2 
     const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
     *reinterpret_cast<float4*>(pl.px + o) = pool4(xa, xb);
     *reinterpret_cast<float4*>(pl.py + o) = pool4(ya, yb);
+  }
+}
+
+// Pyramid levels: the same 2 x 2 means from float samples (sums of four
+// multiples of 4^-s below 1020: exact in float32).  Column pairs are summed
+// in the lane first, so four values per tensor cross by DPP.
+__device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, const Raw<true>& r) {
+  const float4 sx = make_float4(r.x0.x + r.x0.y, r.x0.z + r.x0.w, r.x1.x + r.x1.y, r.x1.z + r.x1.w);
+  const float4 sy = make_float4(r.y0.x + r.y0.y, r.y0.z + r.y0.w, r.y1.x + r.y1.y, r.y1.z + r.y1.w);
+  const float4 tx = make_float4(lane_xor1(sx.x), lane_xor1(sx.y), lane_xor1(sx.z), lane_xor1(sx.w));
+  const float4 ty = make_float4(lane_xor1(sy.x), lane_xor1(sy.y), lane_xor1(sy.z), lane_xor1(sy.w));
+  if (pl.lane_on && (row & 1) == 0 && row < pl.row_end) {
+    const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
+    *reinterpret_cast<float4*>(pl.px + o) = make_float4(0.25f * (sx.x + tx.x), 0.25f * (sx.y + tx.y),
+                                                        0.25f * (sx.z + tx.z), 0.25f * (sx.w + tx.w));
+    *reinterpret_cast<float4*>(pl.py + o) = make_float4(0.25f * (sy.x + ty.x), 0.25f * (sy.y + ty.y),
+                                                        0.25f * (sy.z + ty.z), 0.25f * (sy.w + ty.w));
   }
 }
 
@@ -369,15 +463,10 @@ __device__ inline void vblock(const Weights& w, const VState& v, f4* o) {
   for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.lo[q]), o[q]);
 }
 
-// Optional register budget in waves per SIMD (a build-time tuning knob).
-#if defined(FA_SSIM_MFMA_WPE) && FA_SSIM_MFMA_WPE > 0
-#define FA_MFMA_ATTR __attribute__((amdgpu_waves_per_eu(FA_SSIM_MFMA_WPE)))
-#else
-#define FA_MFMA_ATTR
-#endif
-
-template <int MODE>
-__global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs a) {
+// uint8: 4 waves per SIMD (128 VGPRs) fit without spills and beat 3.
+template <bool PYR, int MODE>
+__global__ __launch_bounds__(BLOCK)
+__attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a) {
   __shared__ double sred[2 * WAVES_PER_BLOCK];
   __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
   const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
@@ -397,8 +486,10 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
   if (c0 < a.Wout) {  // uniform per wave
     const int img = plane / a.C;
     const int ch = plane - img * a.C;
-    const uint8_t* __restrict__ xp = a.x + img * a.xsn + ch * a.xsc;
-    const uint8_t* __restrict__ yp = a.y + img * a.ysn + ch * a.ysc;
+    // element pointers of this plane (uint8 samples, or float pyramid samples)
+    using E = typename std::conditional<PYR, float, uint8_t>::type;
+    const E* __restrict__ xp = reinterpret_cast<const E*>(a.x) + img * a.xsn + ch * a.xsc;
+    const E* __restrict__ yp = reinterpret_cast<const E*>(a.y) + img * a.ysn + ch * a.ysc;
     // this lane's 8 input columns; a chunk past the image only feeds output
     // columns past Wout, so it is clamped (W % 8 == 0: chunks never straddle)
     const uint32_t cc = static_cast<uint32_t>(min(c0 + 8 * g, a.W - 8));
@@ -436,18 +527,25 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
     const uint32_t ymax = static_cast<uint32_t>(a.H - 1) * a.ysh + cc;
     const uint32_t xstep = MT * a.xsh, ystep = MT * a.ysh;
     uint32_t xo = rl * a.xsh + cc, yo = rl * a.ysh + cc;  // block 0
-    auto load = [&](int, uint2& xa, uint2& ya) {
-      xa = *reinterpret_cast<const uint2*>(xp + xo);
-      ya = *reinterpret_cast<const uint2*>(yp + yo);
+    auto load = [&](int, Raw<PYR>& r) {
+      if constexpr (PYR) {
+        r.x0 = *reinterpret_cast<const float4*>(xp + xo);
+        r.x1 = *reinterpret_cast<const float4*>(xp + xo + 4);
+        r.y0 = *reinterpret_cast<const float4*>(yp + yo);
+        r.y1 = *reinterpret_cast<const float4*>(yp + yo + 4);
+      } else {
+        r.x = *reinterpret_cast<const uint2*>(xp + xo);
+        r.y = *reinterpret_cast<const uint2*>(yp + yo);
+      }
       xo = min(xo + xstep, xmax);
       yo = min(yo + ystep, ymax);
     };
     // horizontal pass of block j (and its share of the pyramid)
-    auto hpass = [&](int j, uint2 xa, uint2 ya) {
+    auto hpass = [&](int j, const Raw<PYR>& r) {
       if constexpr (MODE == MF_CS) {
-        if (a.px) pool_block(pl, r0 + MT * j + n, pcol, xa, ya);  // uniform branch
+        if (a.px) pool_block(pl, r0 + MT * j + n, pcol, r);  // uniform branch
       }
-      return hmfma(prep(xa, ya), w);
+      return hmfma<PYR>(prep(r, a.one), w);
     };
     auto epilogue = [&](int b, const f4* o) {
       const int row0 = r0 + MT * b + 4 * g;
@@ -463,30 +561,30 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
     // cores and the vector ALU overlap within the wave too.
     const int nb = (r_end - r0 + MT - 1) / MT;  // output blocks; H blocks 0 .. nb
     VState v;
-    uint2 xa, ya;
-    load(0, xa, ya);
-    stash_all<0>(hpass(0, xa, ya), a.one, v);
-    load(1, xa, ya);
-    HAcc hn = hpass(1, xa, ya);
-    load(2, xa, ya);
+    Raw<PYR> raw;
+    load(0, raw);
+    stash_all<0, PYR>(hpass(0, raw), a.one, v);
+    load(1, raw);
+    HAcc hn = hpass(1, raw);
+    load(2, raw);
     for (int b = 0; b < nb; b += 2) {
       {
-        stash_all<1>(hn, a.one, v);  // H_{b+1} next to H_b
+        stash_all<1, PYR>(hn, a.one, v);  // H_{b+1} next to H_b
         f4 o[4];
         vblock<0>(w, v, o);
         if (b + 2 <= nb) {  // uniform
-          hn = hpass(b + 2, xa, ya);
-          load(b + 3, xa, ya);
+          hn = hpass(b + 2, raw);
+          load(b + 3, raw);
         }
         epilogue(b, o);
       }
       if (b + 1 < nb) {
-        stash_all<0>(hn, a.one, v);  // H_{b+2} over H_b
+        stash_all<0, PYR>(hn, a.one, v);  // H_{b+2} over H_b
         f4 o[4];
         vblock<1>(w, v, o);
         if (b + 3 <= nb) {
-          hn = hpass(b + 3, xa, ya);
-          load(b + 4, xa, ya);
+          hn = hpass(b + 3, raw);
+          load(b + 4, raw);
         }
         epilogue(b + 1, o);
       }
@@ -507,21 +605,19 @@ __global__ __launch_bounds__(BLOCK) FA_MFMA_ATTR void ssim_u8_mfma_kernel(MfArgs
   }
 }
 
-bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
-
 // FA_SSIM_MFMA=0 in the environment selects the vector-ALU kernel instead.
 bool mfma_enabled() {
   const char* e = std::getenv("FA_SSIM_MFMA");
   return !(e && e[0] == '0');
 }
 
-template <int MODE>
+template <bool PYR, int MODE>
 int occupancy() {
   static int occ = 0;
   if (occ <= 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, reinterpret_cast<const void*>(&ssim_u8_mfma_kernel<MODE>), BLOCK, 0) != hipSuccess ||
+            &v, reinterpret_cast<const void*>(&ssim_mfma_kernel<PYR, MODE>), BLOCK, 0) != hipSuccess ||
         v <= 0)
       v = 1;
     occ = v;
@@ -531,10 +627,12 @@ int occupancy() {
 
 }  // namespace
 
-int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
+int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   *tiles = 0;
   if (!mfma_enabled() || c.K > MF_MAX_K || c.W % 8 != 0 || c.W < 8) return FA_OK;
-  if (!aligned8(c.x) || !aligned8(c.y)) return FA_OK;
+  const uintptr_t base_align = c.pyr ? 15 : 7;  // float4 or 8-byte loads
+  if ((reinterpret_cast<uintptr_t>(c.x) | reinterpret_cast<uintptr_t>(c.y)) & base_align)
+    return FA_OK;
   // float4 stores into the pyramid level (W % 8 == 0 makes every row of it
   // a multiple of 16 bytes)
   if (c.px && ((reinterpret_cast<uintptr_t>(c.px) | reinterpret_cast<uintptr_t>(c.py)) & 15))
@@ -572,9 +670,13 @@ int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) 
   // Rows per chunk (a multiple of 16): the fewest rounds of resident
   // workgroups times the work of one, charging the extra 16-row block of
   // horizontal work each chunk starts with at 10 rows.
-  const int occ = mode == MF_CS    ? occupancy<MF_CS>()
-                  : mode == MF_MAP ? occupancy<MF_MAP>()
-                                   : occupancy<MF_REDUCE>();
+  int occ;
+  if (c.pyr)
+    occ = mode == MF_CS ? occupancy<true, MF_CS>()
+          : mode == MF_MAP ? occupancy<true, MF_MAP>() : occupancy<true, MF_REDUCE>();
+  else
+    occ = mode == MF_CS ? occupancy<false, MF_CS>()
+          : mode == MF_MAP ? occupancy<false, MF_MAP>() : occupancy<false, MF_REDUCE>();
   const int64_t resident = static_cast<int64_t>(cu_count(device)) * occ;
   const int64_t planes = static_cast<int64_t>(c.N) * c.C;
   const int strips = (c.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
@@ -599,12 +701,21 @@ int ssim_u8_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) 
   const int64_t wgs = planes * a.tiles;
   if (wgs > INT32_MAX) return FA_OK;
   const dim3 grid(static_cast<unsigned>(wgs));
-  if (mode == MF_CS)
-    hipLaunchKernelGGL(ssim_u8_mfma_kernel<MF_CS>, grid, dim3(BLOCK), 0, st, a);
-  else if (mode == MF_MAP)
-    hipLaunchKernelGGL(ssim_u8_mfma_kernel<MF_MAP>, grid, dim3(BLOCK), 0, st, a);
-  else
-    hipLaunchKernelGGL(ssim_u8_mfma_kernel<MF_REDUCE>, grid, dim3(BLOCK), 0, st, a);
+  if (c.pyr) {
+    if (mode == MF_CS)
+      hipLaunchKernelGGL((ssim_mfma_kernel<true, MF_CS>), grid, dim3(BLOCK), 0, st, a);
+    else if (mode == MF_MAP)
+      hipLaunchKernelGGL((ssim_mfma_kernel<true, MF_MAP>), grid, dim3(BLOCK), 0, st, a);
+    else
+      hipLaunchKernelGGL((ssim_mfma_kernel<true, MF_REDUCE>), grid, dim3(BLOCK), 0, st, a);
+  } else {
+    if (mode == MF_CS)
+      hipLaunchKernelGGL((ssim_mfma_kernel<false, MF_CS>), grid, dim3(BLOCK), 0, st, a);
+    else if (mode == MF_MAP)
+      hipLaunchKernelGGL((ssim_mfma_kernel<false, MF_MAP>), grid, dim3(BLOCK), 0, st, a);
+    else
+      hipLaunchKernelGGL((ssim_mfma_kernel<false, MF_REDUCE>), grid, dim3(BLOCK), 0, st, a);
+  }
   FA_LAUNCH_CHECK();
   *tiles = a.tiles;
   return FA_OK;

@@ -38,6 +38,12 @@ extern "C" {
 #define FA_BF16 2
 #define FA_F32 3
 #define FA_F64 4
+/* No counterpart in the reference: a flag fa_gpu_ssim_cs_ex accepts OR-ed
+ * into FA_F32.  It promises that every sample is a level of the 2x2-mean
+ * pyramid of uint8 data (a multiple of 4^-s in [0, 255], s <= 4), which lets
+ * the call run on the matrix cores; without it float32 runs the vector-ALU
+ * kernel.  Results agree either way to the same 1e-6 bar. */
+#define FA_DTYPE_U8_PYRAMID 0x100
 
 /* pixel-loss selector (reference fa_abi.h:51-54) */
 #define FA_OP_MSE 0
@@ -226,7 +232,8 @@ FA_API int fa_gpu_ssim_ex(const void* x, const void* y, int dtype, int N, int C,
  * fa_gpu_ms_ssim_reduce.  out_slots: host int, may be null unless both means
  * are null; receives the number of slots per plane the launch used (each
  * plane's partial sums are packed at that stride from the start of the
- * buffer).
+ * buffer).  dtype: FA_F32 | FA_DTYPE_U8_PYRAMID marks a uint8 pyramid level
+ * (see FA_DTYPE_U8_PYRAMID).
  */
 FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N,
                              int C, int H, int W, const int64_t* x_strides,

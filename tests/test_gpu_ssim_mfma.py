@@ -205,3 +205,60 @@ def test_ms_ssim_pyramid_level_exact(gpu):
     got_cs = out_cs.cpu().numpy().reshape(n, c)
     assert np.allclose(got_s, s_ref.mean(axis=(-2, -1)), rtol=1e-6, atol=0)
     assert np.allclose(got_cs, cs_ref.mean(axis=(-2, -1)), rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("s", [1, 2, 4])
+def test_pyramid_level_flag(gpu, s):
+    # float32 samples that are multiples of 4^-s in [0, 255] (a uint8 pyramid
+    # level) run on the matrix cores with FA_DTYPE_U8_PYRAMID; the statistics
+    # and the next level match the strip kernel and the oracle
+    from frame_analytics_amd import backend
+
+    rng = np.random.default_rng(s)
+    q = 4 ** s
+    n, c, h, w = 2, 3, 70, 120
+    ka = rng.integers(0, 255 * q + 1, (n, c, h, w))
+    kb = np.clip(ka + rng.integers(-9 * q, 9 * q + 1, ka.shape), 0, 255 * q)
+    a, b = (ka / q).astype(np.float32), (kb / q).astype(np.float32)
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    C1, C2 = (0.01 * 255) ** 2, (0.03 * 255) ** 2
+    outs = {}
+    for flag in (True, False):
+        ps, pcs, sl, npix, px, py = backend.ssim_cs_partials(
+            x, y, win, 127.5, C1, C2, torch.float32, u8_pyramid=flag)
+        # each plane's partials are packed at the used stride `sl`
+        s_mean = ps.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+        cs_mean = pcs.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+        outs[flag] = (s_mean, cs_mean, px.cpu().numpy(), py.cpu().numpy())
+    s_ref, cs_ref = ref.ssim_maps(a.astype(np.float64), b.astype(np.float64))
+    want_s = s_ref.mean(axis=(-2, -1)).reshape(-1)
+    want_cs = cs_ref.mean(axis=(-2, -1)).reshape(-1)
+    for flag in (True, False):
+        got_s, got_cs, px, py = outs[flag]
+        assert np.allclose(got_s, want_s, rtol=REL, atol=0), (flag, got_s, want_s)
+        assert np.allclose(got_cs, want_cs, rtol=REL, atol=0), (flag, got_cs, want_cs)
+        assert np.array_equal(px.astype(np.float64), ref.avg_pool2(a.astype(np.float64)))
+        assert np.array_equal(py.astype(np.float64), ref.avg_pool2(b.astype(np.float64)))
+
+
+def test_pyramid_flag_is_an_ex_hint_only(gpu):
+    from frame_analytics_amd import backend
+
+    ext = backend.load()
+    x = torch.zeros((1, 1, 32, 32), device=gpu)
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    bpp = backend._ssim_workspace(ext, 32, 32, 11)
+    part = torch.empty((1, bpp), dtype=torch.float64, device=gpu)
+    o = torch.empty(1, dtype=torch.float64, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+    # the reference-shaped entry point refuses the flag
+    rc = ext.gpu.fa_gpu_ssim_cs(x.data_ptr(), x.data_ptr(), 3 | backend.FA_DTYPE_U8_PYRAMID,
+                                1, 1, 32, 32, win.data_ptr(), 11, 0.5, 1e-4, 9e-4,
+                                part.data_ptr(), part.data_ptr(), bpp, o.data_ptr(),
+                                o.data_ptr(), 0, stream)
+    assert rc == 1  # FA_E_DTYPE
+    with pytest.raises(ValueError):
+        backend.ssim_cs_partials(x.double(), x.double(), win, 0.5, 1e-4, 9e-4, None,
+                                 u8_pyramid=True)
