@@ -389,56 +389,44 @@ __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, 
   if constexpr (MODE == MF_CS) acc_cs += static_cast<double>(rcs);
 }
 
-// MS-SSIM's next pyramid level from the raw bytes of one 16-row block: the
-// even lane of each row pair writes the 2 x 2 means of its 8 columns (four
-// float32 values, one 16-byte store); the odd lane's bytes come over by DPP.
-// uint8 sums of four are at most 1020, so the means are exact in float32.
+// MS-SSIM's next pyramid level, as a matrix product of the A fragments the
+// horizontal pass already holds: the 0/1 matrix P[k][c] = (k / 2 == c) sums
+// column pairs of the 32-column window (B fragment: lane (g, n) holds
+// P[8g + i][n]), and the D fragment holds, in lane (g, n), rows 4g .. 4g+3 of
+// pooled column n, so each lane adds its two row pairs.  The sums are exact:
+// four samples of x' 2^-9 (uint8) or of x' = hi + lo (pyramid levels).
 struct Pool {
   float* px;
   float* py;
-  int64_t off;  // this plane's first element
-  int Wd;       // level width, floor(W / 2)
-  int row_end;  // first input row this chunk does not pool
-  bool lane_on; // this lane's 8 columns belong to the wave and lie in the image
+  int64_t off;   // this plane's first element
+  int Wd;        // level width, floor(W / 2)
+  int row_end;   // first input row this chunk does not pool
+  bool lane_on;  // pooled column c0/2 + n is this wave's and lies in the level
+  h8 pm;         // the column-pair matrix fragment
 };
 
-__device__ inline float4 pool4(uint2 a, uint2 b) {
-  const uint32_t m0 = 0x00000101u, m1 = 0x01010000u;  // bytes (0, 1) and (2, 3)
-  return make_float4(0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.x, m0, __builtin_amdgcn_udot4(b.x, m0, 0u, false), false)),
-                     0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.x, m1, __builtin_amdgcn_udot4(b.x, m1, 0u, false), false)),
-                     0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.y, m0, __builtin_amdgcn_udot4(b.y, m0, 0u, false), false)),
-                     0.25f * static_cast<float>(__builtin_amdgcn_udot4(a.y, m1, __builtin_amdgcn_udot4(b.y, m1, 0u, false), false)));
-}
-
-__device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, const Raw<false>& r) {
-  const uint2 xa = r.x, ya = r.y;
-  // every lane takes part in the DPP moves; only even lanes store
-  const uint2 xb = {static_cast<uint32_t>(lane_xor1(static_cast<int>(xa.x))),
-                    static_cast<uint32_t>(lane_xor1(static_cast<int>(xa.y)))};
-  const uint2 yb = {static_cast<uint32_t>(lane_xor1(static_cast<int>(ya.x))),
-                    static_cast<uint32_t>(lane_xor1(static_cast<int>(ya.y)))};
-  // row is even on even lanes and row_end is even, so row + 1 < row_end too
-  if (pl.lane_on && (row & 1) == 0 && row < pl.row_end) {
-    const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
-    *reinterpret_cast<float4*>(pl.px + o) = pool4(xa, xb);
-    *reinterpret_cast<float4*>(pl.py + o) = pool4(ya, yb);
+template <bool PYR>
+__device__ inline void pool_frag(const Pool& pl, int row0, uint32_t pcol, const Frag& f) {
+  const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 sx = mfma(f.x, pl.pm, z);
+  f4 sy = mfma(f.y, pl.pm, z);
+  if constexpr (PYR) {
+    sx = mfma(f.xl, pl.pm, sx);
+    sy = mfma(f.yl, pl.pm, sy);
   }
-}
-
-// Pyramid levels: the same 2 x 2 means from float samples (sums of four
-// multiples of 4^-s below 1020: exact in float32).  Column pairs are summed
-// in the lane first, so four values per tensor cross by DPP.
-__device__ inline void pool_block(const Pool& pl, int row, uint32_t pcol, const Raw<true>& r) {
-  const float4 sx = make_float4(r.x0.x + r.x0.y, r.x0.z + r.x0.w, r.x1.x + r.x1.y, r.x1.z + r.x1.w);
-  const float4 sy = make_float4(r.y0.x + r.y0.y, r.y0.z + r.y0.w, r.y1.x + r.y1.y, r.y1.z + r.y1.w);
-  const float4 tx = make_float4(lane_xor1(sx.x), lane_xor1(sx.y), lane_xor1(sx.z), lane_xor1(sx.w));
-  const float4 ty = make_float4(lane_xor1(sy.x), lane_xor1(sy.y), lane_xor1(sy.z), lane_xor1(sy.w));
-  if (pl.lane_on && (row & 1) == 0 && row < pl.row_end) {
-    const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
-    *reinterpret_cast<float4*>(pl.px + o) = make_float4(0.25f * (sx.x + tx.x), 0.25f * (sx.y + tx.y),
-                                                        0.25f * (sx.z + tx.z), 0.25f * (sx.w + tx.w));
-    *reinterpret_cast<float4*>(pl.py + o) = make_float4(0.25f * (sy.x + ty.x), 0.25f * (sy.y + ty.y),
-                                                        0.25f * (sy.z + ty.z), 0.25f * (sy.w + ty.w));
+  // a sum of four is (S - 512) 2^-9 (uint8) or S - 512: the mean S / 4 is
+  // sum * k + 128
+  constexpr float k = PYR ? 0.25f : 128.0f;
+  if (pl.lane_on) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int row = row0 + 2 * q;  // even; row_end is even, so row + 1 pools too
+      if (row < pl.row_end) {
+        const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
+        pl.px[o] = fmaf(sx[2 * q] + sx[2 * q + 1], k, 128.0f);
+        pl.py[o] = fmaf(sy[2 * q] + sy[2 * q + 1], k, 128.0f);
+      }
+    }
   }
 }
 
@@ -502,9 +490,9 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
       map_col = a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout + c0 + n;
 
     // The pyramid level: a wave pools the input columns of its own 16 output
-    // columns (window columns 0..15); the last active wave of a row also
-    // pools the rest of its window up to the image edge, which covers the
-    // columns of the waves past Wout (W <= c0 + 16 + K - 1 there).  Rows:
+    // columns (pooled columns c0/2 .. c0/2 + 7); the last active wave of a row
+    // also pools the rest of its window up to the image edge, which covers
+    // the columns of the waves past Wout (W <= c0 + 16 + K - 1 there).  Rows:
     // this chunk's TH input rows, and in the last chunk everything up to
     // 2 floor(H / 2).  Every row the chunk pools lies in one of its H blocks.
     Pool pl = {};
@@ -515,9 +503,12 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
       pl.off = static_cast<int64_t>(plane) * (a.H / 2) * pl.Wd;
       pl.row_end = r0 + a.TH >= a.Hout ? 2 * (a.H / 2) : r0 + a.TH;
       const bool last_wave = c0 + MT >= a.Wout;
-      pl.lane_on = a.px != nullptr && (g < 2 || last_wave) && c0 + 8 * g < a.W;
+      pl.lane_on = a.px != nullptr && (n < 8 || last_wave) && c0 / 2 + n < pl.Wd;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        pl.pm[i] = static_cast<_Float16>(((8 * g + i) >> 1) == n ? 1.0f : 0.0f);
     }
-    const uint32_t pcol = static_cast<uint32_t>(c0 + 8 * g) >> 1;
+    const uint32_t pcol = static_cast<uint32_t>(c0 / 2 + n);
 
     // rows past the image only feed output rows past Hout: clamped.  load(j)
     // is called for j = 0, 1, 2, ... in order, so the row offsets advance by
@@ -542,10 +533,11 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
     };
     // horizontal pass of block j (and its share of the pyramid)
     auto hpass = [&](int j, const Raw<PYR>& r) {
+      const Frag f = prep(r, a.one);
       if constexpr (MODE == MF_CS) {
-        if (a.px) pool_block(pl, r0 + MT * j + n, pcol, r);  // uniform branch
+        if (a.px) pool_frag<PYR>(pl, r0 + MT * j + 4 * g, pcol, f);  // uniform branch
       }
-      return hmfma<PYR>(prep(r, a.one), w);
+      return hmfma<PYR>(f, w);
     };
     auto epilogue = [&](int b, const f4* o) {
       const int row0 = r0 + MT * b + 4 * g;
