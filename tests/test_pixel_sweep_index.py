@@ -78,8 +78,9 @@ def simulate_sweep(nv: int, n_images: int, G: int, NT: int, U: int):
 
 CASES = [
     # (nv, n_images, G, NT, U)
-    (1_555_200, 8, 256, 256, 4),   # configs[2] on a 256-CU part, the shipped shape
-    (1_555_200, 8, 256, 512, 2),   # a short last round: waves finish a round early
+    (1_555_200, 8, 256, 512, 2),   # configs[2] on a 256-CU part, the shipped shape
+    (1_555_200, 8, 256, 256, 4),   # the 4 x 256 launch shape
+    (1_555_200, 8, 256, 512, 4),   # 4 x 512: a short last round, waves finish a round early
     (268_125, 3, 256, 256, 4),     # 3x3x1100x1300 uint8
     (388_800, 8, 256, 256, 4),     # 8x3x1080x1920 uint8
     (262_144, 2, 256, 256, 4),     # exactly one round per image
