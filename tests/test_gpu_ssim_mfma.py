@@ -155,7 +155,7 @@ def test_views_aligned_and_not(gpu):
 # MS-SSIM over uint8: scale 0 (SSIM and cs sums plus the first pyramid level,
 # 2 x 2 means written by the same kernel) runs on the matrix cores
 @pytest.mark.parametrize("shape", [(1, 1, 176, 176), (2, 3, 200, 264), (1, 3, 361, 648),
-                                   (3, 1, 190, 184)])
+                                   (3, 1, 190, 184), (22, 3, 176, 176)])  # 66 planes: two-launch reduction
 def test_ms_ssim(gpu, shape):
     a, b = u8_pair(shape, 9.0, seed=sum(shape))
     x = torch.as_tensor(a, device=gpu)
