@@ -1,7 +1,9 @@
-"""GPU parity of the matrix-core SSIM forward (uint8 planes, fa_ssim_mfma.hip).
+"""GPU parity of the matrix-core SSIM forward (fa_ssim_mfma.hip).
 
 uint8 inputs whose rows and planes are 8-byte aligned (W % 8 == 0) take the
-MFMA kernel; everything else takes the vector-ALU strip kernel.  Both are held
+MFMA kernel, and so do the float32 levels of a uint8 MS-SSIM pyramid when the
+caller flags them (FA_DTYPE_U8_PYRAMID); everything else takes the vector-ALU
+strip kernel.  Both are held
 to the float64 oracle at the north star's bar (SSIM values within 1e-6
 relative; float32 map elements within 2e-5 absolute), and to each other:
 ``FA_SSIM_MFMA=0`` in the environment selects the strip kernel for a call.
