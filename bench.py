@@ -253,7 +253,7 @@ def profile_sequence(launches=20):
     pairs = _pairs(torch, SSIM_SHAPE, 8.0, 4, dev, seed=1)
     n, c, h, w = SSIM_SHAPE
     win = fa.gaussian_window_1d(11, 1.5, device=dev, dtype=torch.float32)
-    bpp = backend._ssim_workspace(ext, h, w, 11)
+    bpp = backend.workspace_slots("ssim", h, w, 11)
     partial = torch.empty((n * c, bpp), dtype=torch.float64, device=dev)
     for i in range(launches):
         a, b = pairs[i % 4]
@@ -262,7 +262,7 @@ def profile_sequence(launches=20):
                                partial.data_ptr(), bpp, None, None, 0, stream) == 0
     torch.cuda.synchronize()
     # GMSD (configs[4]: downsample, per-channel pooled) on the same pairs
-    gbpp = backend._gmsd_workspace(ext, h, w, True)
+    gbpp = backend.workspace_slots("gmsd", h, w, 1)
     ps = torch.empty((n * c, gbpp), dtype=torch.float64, device=dev)
     ps2 = torch.empty_like(ps)
     gm = torch.empty(n, dtype=torch.float64, device=dev)
@@ -278,7 +278,7 @@ def profile_sequence(launches=20):
     ppairs = _pairs(torch, PSNR_SHAPE, 4.0, 2, dev, seed=2)
     pn = PSNR_SHAPE[0]
     per = ppairs[0][0].numel() // pn
-    bpi = backend._pixel_workspace(ext, pn, per, 0)
+    bpi = backend.workspace_slots("pixel", pn, per, 0)
     ppart = torch.empty((pn, bpi), dtype=torch.float64, device=dev)
     for i in range(launches):
         a, b = ppairs[i % 2]
@@ -333,7 +333,7 @@ def main():
 
     # dominant kernel alone: the C ABI with no finalize sinks launches only it
     win = fa.gaussian_window_1d(11, 1.5, device=dev, dtype=torch.float32)
-    bpp = backend._ssim_workspace(ext, h, w, 11)
+    bpp = backend.workspace_slots("ssim", h, w, 11)
     partial = torch.empty((n * c, bpp), dtype=torch.float64, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
 
@@ -408,7 +408,7 @@ def main():
     p_el = _time_steps(torch, psnr_step, args.steps, args.warmup)
     p_ms = p_el / args.steps * 1e3
     pbytes = 2.0 * ppairs[0][0].numel()
-    bpi = backend._pixel_workspace(ext, pn, per, 0)
+    bpi = backend.workspace_slots("pixel", pn, per, 0)
     ppart = torch.empty((pn, bpi), dtype=torch.float64, device=dev)
 
     def psnr_kernel(i):

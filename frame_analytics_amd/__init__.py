@@ -5,10 +5,13 @@ the same ``fa.ssim / fa.ms_ssim / fa.psnr / fa.mse / fa.l1 / fa.gmsd`` API,
 served on the GPU by hand-written gfx950 HIP kernels behind a C ABI
 (``include/fa_abi.h``, ``libfa_gpu.so``).
 
->>> import torch, frame_analytics_amd as fa
->>> a = torch.randint(0, 256, (8, 3, 1080, 1920), dtype=torch.uint8, device="cuda")
->>> b = (a.float() + 4 * torch.randn_like(a, dtype=torch.float32)).clamp(0, 255).byte()
->>> fa.psnr(a, b), fa.ssim(a, b)
+Usage, scoring a batch of decoded frames against their sources::
+
+    import frame_analytics_amd as fa
+    # src, out: (N, 3, H, W) uint8 tensors on the GPU
+    db = fa.psnr(src, out)                    # exact integer SSE, dB in-kernel
+    s = fa.ssim(src, out, reduction="none")   # one value per frame
+    loss = 1 - fa.ms_ssim(pred, target, data_range=1.0)  # float32, differentiable
 """
 
 from .functional import (  # noqa: F401

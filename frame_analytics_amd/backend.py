@@ -28,7 +28,9 @@ path, which is the reference's own behaviour on such hosts.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
+from collections import Counter
 from typing import Any, Optional
 
 import torch
@@ -204,34 +206,56 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
 
-def _dev(t: torch.Tensor) -> int:
-    i = t.device.index
-    return torch.cuda.current_device() if i is None else int(i)
+# --------------------------------------------------------------------------- #
+# calling into libfa_gpu.so
+# --------------------------------------------------------------------------- #
+
+#: entry point name -> calls made through :func:`call_gpu` in this process.
+#: Tests read it to show that a GPU call was served by the gfx950 kernels.
+native_calls: Counter = Counter()
+#: functional helper -> evaluations of the portable PyTorch path on GPU tensors
+portable_calls: Counter = Counter()
 
 
-def _stream(t: torch.Tensor):
-    return torch.cuda.current_stream(t.device).cuda_stream
+def note_portable(what: str, t: torch.Tensor) -> None:
+    """Record that the portable path computed ``what`` on a GPU tensor."""
+    if t.is_cuda:
+        portable_calls[what] += 1
 
 
-def _check(code: int, ext: _Native) -> None:
-    if code != 0:
-        raise KernelError(status_text(code, ext.gpu))
+def call_gpu(name: str, *args) -> int:
+    """Call one entry point of ``include/fa_abi.h`` and return its status.
+
+    Every GPU launch of this package goes through here, so
+    :data:`native_calls` counts them."""
+    ext = load()
+    if ext is None or not ext.has_gpu:
+        raise RuntimeError(f"{name}: the gfx950 kernel library is not loaded")
+    code = getattr(ext.gpu, name)(*args)
+    native_calls[name] += 1
+    return int(code)
 
 
-_win_cache: dict = {}
+def _run(name: str, *args) -> None:
+    """:func:`call_gpu`, raising :class:`KernelError` on a non-zero status."""
+    code = call_gpu(name, *args)
+    if code:
+        raise KernelError(f"{name}: " + status_text(code, _ext.gpu if _ext else None))
 
 
-def _win_f32(win: torch.Tensor) -> torch.Tensor:
-    """The window as contiguous float32, cast once per cached window."""
-    if win.dtype == torch.float32:
-        return _contig(win)
-    key = (id(win), str(win.device))
-    hit = _win_cache.get(key)
-    if hit is not None and hit[0] is win:
-        return hit[1]
-    w = win.to(torch.float32).contiguous()
-    _win_cache[key] = (win, w)
-    return w
+def _site(t: torch.Tensor):
+    """``(device ordinal, hipStream_t)`` of the caller's current stream on the
+    device of ``t``: kernels are enqueued where torch would enqueue its own."""
+    s = torch.cuda.current_stream(t.device)
+    return s.device_index, s.cuda_stream
+
+
+def _win32(win: torch.Tensor) -> torch.Tensor:
+    """The window as the ABI takes it: contiguous float32.  The functional
+    layer hands over its cached float32 windows, so this is a no-op there."""
+    if win.dtype != torch.float32:
+        win = win.to(torch.float32)
+    return _contig(win)
 
 
 def _usable(x: torch.Tensor, y: torch.Tensor) -> bool:
@@ -251,39 +275,23 @@ def _gpu_ext(x: torch.Tensor) -> Optional[_Native]:
     return ext
 
 
-# Workspace sizes depend on the shape only; caching them keeps the runtime
-# query out of graph capture (reference backend.py:247-286).
-_ws_cache: dict = {}
+_WORKSPACE_QUERY = {
+    "pixel": "fa_gpu_pixel_workspace",  # (n_images, n_per_image, device)
+    "ssim": "fa_gpu_ssim_workspace",    # (H, W, K)
+    "gmsd": "fa_gpu_gmsd_workspace",    # (H, W, downsample)
+}
 
 
-def _pixel_workspace(ext: _Native, n_images: int, n_per_image: int, dev: int) -> int:
-    key = ("pix", n_images, n_per_image, dev)
-    hit = _ws_cache.get(key)
-    if hit is None:
-        out = ctypes.c_int(0)
-        _check(ext.gpu.fa_gpu_pixel_workspace(n_images, n_per_image, dev, ctypes.byref(out)), ext)
-        hit = _ws_cache[key] = int(out.value)
-    return hit
-
-
-def _ssim_workspace(ext: _Native, h: int, w: int, k: int) -> int:
-    key = ("ssim", h, w, k)
-    hit = _ws_cache.get(key)
-    if hit is None:
-        out = ctypes.c_int(0)
-        _check(ext.gpu.fa_gpu_ssim_workspace(h, w, k, ctypes.byref(out)), ext)
-        hit = _ws_cache[key] = int(out.value)
-    return hit
-
-
-def _gmsd_workspace(ext: _Native, h: int, w: int, downsample: bool) -> int:
-    key = ("gmsd", h, w, bool(downsample))
-    hit = _ws_cache.get(key)
-    if hit is None:
-        out = ctypes.c_int(0)
-        _check(ext.gpu.fa_gpu_gmsd_workspace(h, w, int(downsample), ctypes.byref(out)), ext)
-        hit = _ws_cache[key] = int(out.value)
-    return hit
+@functools.lru_cache(maxsize=None)
+def workspace_slots(kind: str, a: int, b: int, c: int) -> int:
+    """Partial-sum slots per image (``"pixel"``) or per plane (``"ssim"``,
+    ``"gmsd"``) a launch of this shape needs; the arguments follow the
+    entry point's.  The answer depends on the shape only, so each shape is
+    asked once and a graph capture never issues the query (reference
+    backend.py:247-286 keeps the same property)."""
+    out = ctypes.c_int(0)
+    _run(_WORKSPACE_QUERY[kind], int(a), int(b), int(c), ctypes.byref(out))
+    return int(out.value)
 
 
 # --------------------------------------------------------------------------- #
@@ -297,29 +305,26 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
     """One fused reduction; exactly one output tensor is allocated.  Strided
     (cropped) views and ``luma`` = (kr, kg, kb, offset) go through
     ``fa_gpu_pixel_reduce_ex``, which reads them in place."""
+    del ext  # the library is reached through call_gpu
     n, c, h, w = (int(v) for v in x.shape)
     x, xs = _view_strides(x)
     y, ys = _view_strides(y)
     per = c * h * w
-    dev = _dev(x)
-    bpi = _pixel_workspace(ext, n, per, dev)
+    dev, stream = _site(x)
+    bpi = workspace_slots("pixel", n, per, dev)
     partial = _f64(x.device, n, bpi)
-    want_psnr = psnr_bias != _PSNR_NONE
     out = _f64(x.device, n) if per_image else _f64(x.device)
-    sinks: list = [None, None, None, None]
-    sinks[(2 if want_psnr else 0) + (0 if per_image else 1)] = out
+    # the four ABI sinks, in order: mean per image, mean total, dB per image,
+    # dB total; exactly one is written
+    slot = (2 if psnr_bias != _PSNR_NONE else 0) + (0 if per_image else 1)
+    sinks = [_ptr(out) if i == slot else None for i in range(4)]
     if luma is None and xs is None and ys is None:
-        _check(ext.gpu.fa_gpu_pixel_reduce(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op, float(param),
-            float(psnr_bias), _ptr(partial), bpi,
-            _ptr(sinks[0]), _ptr(sinks[1]), _ptr(sinks[2]), _ptr(sinks[3]),
-            dev, _stream(x)), ext)
+        _run("fa_gpu_pixel_reduce", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op,
+             float(param), float(psnr_bias), _ptr(partial), bpi, *sinks, dev, stream)
     else:
-        _check(ext.gpu.fa_gpu_pixel_reduce_ex(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
-            op, float(param), float(psnr_bias), _ptr(partial), bpi,
-            _ptr(sinks[0]), _ptr(sinks[1]), _ptr(sinks[2]), _ptr(sinks[3]),
-            dev, _stream(x)), ext)
+        _run("fa_gpu_pixel_reduce_ex", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w,
+             xs, ys, _luma_arg(luma), op, float(param), float(psnr_bias), _ptr(partial), bpi,
+             *sinks, dev, stream)
     return out
 
 
@@ -339,42 +344,30 @@ def try_mse(x: torch.Tensor, y: torch.Tensor, *, per_image: bool,
             dtype: torch.dtype, psnr_bias: Optional[float] = None,
             luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
     """Squared-error reduction, or PSNR when ``psnr_bias`` (= 10 log10 L^2) is given."""
-    if not x.is_cuda:
-        lib = _cpu_ready(x, y) if luma is None else None
-        if lib is None:
-            return None
-        bias = psnr_bias if psnr_bias is not None else _PSNR_NONE
-        out = pixel_cpu(lib, x, y, op=_OP_MSE, param=0.0, per_image=per_image, psnr_bias=bias)
-        return out if dtype == torch.float64 else out.to(dtype)
-    ext = _gpu_ext(x)
-    if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
-        return None
-    if luma is not None and x.shape[1] != 3:
-        return None
-    bias = psnr_bias if psnr_bias is not None else _PSNR_NONE
-    out = pixel_gpu(ext, x, y, op=_OP_MSE, param=0.0, per_image=per_image, psnr_bias=bias,
-                    luma=luma)
-    return out if dtype == torch.float64 else out.to(dtype)
+    return try_pixel(x, y, op=_OP_MSE, param=0.0, per_image=per_image, dtype=dtype,
+                     luma=luma, psnr_bias=psnr_bias)
 
 
 def try_pixel(x: torch.Tensor, y: torch.Tensor, *, op: int, param: float,
               per_image: bool, dtype: torch.dtype,
-              luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
-    """L1 / Charbonnier / Huber reduction; ``None`` if no kernel applies."""
+              luma: Optional[tuple] = None,
+              psnr_bias: Optional[float] = None) -> Optional[torch.Tensor]:
+    """MSE / L1 / Charbonnier / Huber reduction (PSNR with ``psnr_bias``);
+    ``None`` if no kernel applies."""
+    bias = _PSNR_NONE if psnr_bias is None else float(psnr_bias)
     if not x.is_cuda:
         lib = _cpu_ready(x, y) if luma is None else None
         if lib is None:
             return None
-        out = pixel_cpu(lib, x, y, op=op, param=param, per_image=per_image,
-                        psnr_bias=_PSNR_NONE)
-        return out if dtype == torch.float64 else out.to(dtype)
-    ext = _gpu_ext(x)
-    if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
-        return None
-    if luma is not None and x.shape[1] != 3:
-        return None
-    out = pixel_gpu(ext, x, y, op=op, param=param, per_image=per_image,
-                    psnr_bias=_PSNR_NONE, luma=luma)
+        out = pixel_cpu(lib, x, y, op=op, param=param, per_image=per_image, psnr_bias=bias)
+    else:
+        ext = _gpu_ext(x)
+        if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
+            return None
+        if luma is not None and x.shape[1] != 3:
+            return None
+        out = pixel_gpu(ext, x, y, op=op, param=param, per_image=per_image, psnr_bias=bias,
+                        luma=luma)
     return out if dtype == torch.float64 else out.to(dtype)
 
 
@@ -383,74 +376,66 @@ def try_pixel(x: torch.Tensor, y: torch.Tensor, *, op: int, param: float,
 # --------------------------------------------------------------------------- #
 
 
+def _autograd_ok(x: torch.Tensor, y: torch.Tensor, dtypes) -> bool:
+    return (x.is_cuda and x.dim() == 4 and x.dtype in dtypes and y.dtype == x.dtype
+            and x.shape == y.shape and not torch.cuda.is_current_stream_capturing()
+            and _gpu_ext(x) is not None)
+
+
 def ssim_autograd_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> bool:
     """Can the differentiable native SSIM path serve this call?"""
-    return (
-        x.is_cuda
-        and x.dtype == torch.float32
-        and y.dtype == torch.float32
-        and x.shape == y.shape
-        and x.dim() == 4
-        and win_size in _WINDOWS
-        and not torch.cuda.is_current_stream_capturing()
-        and _gpu_ext(x) is not None
-    )
+    return win_size in _WINDOWS and _autograd_ok(x, y, (torch.float32,))
 
 
 def ssim_cs_autograd_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> bool:
     """Can the differentiable native MS-SSIM primitive serve this call?  float32
     levels and the float64 levels of the exact pyramid both can."""
-    return (
-        x.is_cuda
-        and x.dtype in (torch.float32, torch.float64)
-        and y.dtype == x.dtype
-        and x.shape == y.shape
-        and x.dim() == 4
-        and win_size in _WINDOWS
-        and not torch.cuda.is_current_stream_capturing()
-        and _gpu_ext(x) is not None
-    )
+    return win_size in _WINDOWS and _autograd_ok(x, y, (torch.float32, torch.float64))
 
 
 def ssim_fused(x: torch.Tensor, y: torch.Tensor, win: torch.Tensor,
                shift: float, C1: float, C2: float, want_map: bool):
     """Forward half of the differentiable SSIM: ``[per_image, total(, map)]``."""
-    ext = load()
-    x, y = _contig(x), _contig(y)
-    winf = _win_f32(win)
-    n, c, h, w = x.shape
-    k = int(winf.numel())
-    bpp = _ssim_workspace(ext, h, w, k)
+    x, y, win = _contig(x), _contig(y), _win32(win)
+    n, c, h, w = (int(v) for v in x.shape)
+    k = int(win.numel())
+    bpp = workspace_slots("ssim", h, w, k)
+    dev, stream = _site(x)
     partial = _f64(x.device, n * c, bpp)
-    per_image = _f64(x.device, n)
-    total = _f64(x.device)
+    per_image, total = _f64(x.device, n), _f64(x.device)
     smap = (torch.empty((n, c, h - k + 1, w - k + 1), device=x.device, dtype=torch.float32)
             if want_map else None)
-    _check(ext.gpu.fa_gpu_ssim(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
-        float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
-        _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
+    _run("fa_gpu_ssim", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), k,
+         float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
+         _ptr(per_image), _ptr(total), dev, stream)
     return [per_image, total, smap] if want_map else [per_image, total]
 
 
-def ssim_backward(x, y, dL_dmap, grad_scalar, win, shift, C1, C2, need_dx, need_dy):
-    ext = load()
-    x, y = _contig(x), _contig(y)
-    winf = _win_f32(win)
-    n, c, h, w = x.shape
-    k = int(winf.numel())
-    hout, wout = h - k + 1, w - k + 1
-    has_map = dL_dmap is not None and dL_dmap.numel() > 0
-    dmap = dL_dmap.to(torch.float32).contiguous() if has_map else None
-    gscalar = None if has_map else grad_scalar.to(torch.float32).contiguous().reshape(1)
-    aux = torch.empty((4 if need_dy else 3, n * c, hout, wout), device=x.device,
+def _grad_buffers(x, y, k, need_dx, need_dy):
+    """The backward's float32 coefficient maps (3, or 4 with dy, per output
+    pixel: the ABI's ``aux``) and its outputs."""
+    n, c, h, w = (int(v) for v in x.shape)
+    aux = torch.empty((4 if need_dy else 3, n * c, h - k + 1, w - k + 1), device=x.device,
                       dtype=torch.float32)
-    dx = torch.empty_like(x) if need_dx else None
-    dy = torch.empty_like(y) if need_dy else None
-    _check(ext.gpu.fa_gpu_ssim_backward(
-        _ptr(x), _ptr(y), _ptr(dmap), _ptr(gscalar), _ptr(winf), k, n, c, h, w,
-        float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
-        _dev(x), _stream(x)), ext)
+    return (aux, torch.empty_like(x) if need_dx else None,
+            torch.empty_like(y) if need_dy else None)
+
+
+def ssim_backward(x, y, dL_dmap, grad_scalar, win, shift, C1, C2, need_dx, need_dy):
+    """dL/dx, dL/dy of the SSIM map (``dL_dmap``) or of the batch mean
+    (``grad_scalar``, a 1-element device tensor read by the kernel)."""
+    x, y, win = _contig(x), _contig(y), _win32(win)
+    n, c, h, w = (int(v) for v in x.shape)
+    k = int(win.numel())
+    if dL_dmap is not None and dL_dmap.numel() > 0:
+        dmap, gscalar = dL_dmap.to(torch.float32).contiguous(), None
+    else:
+        dmap, gscalar = None, grad_scalar.to(torch.float32).contiguous().reshape(1)
+    aux, dx, dy = _grad_buffers(x, y, k, need_dx, need_dy)
+    dev, stream = _site(x)
+    _run("fa_gpu_ssim_backward", _ptr(x), _ptr(y), _ptr(dmap), _ptr(gscalar), _ptr(win), k,
+         n, c, h, w, float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
+         dev, stream)
     return dx, dy
 
 
@@ -496,36 +481,34 @@ def try_ssim(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
     ext = _gpu_ext(x)
     if ext is None or not _usable(x, y) or win_size not in _WINDOWS:
         return None
-    n, c = int(x.shape[0]), int(x.shape[1])
+    n, c, h, w = (int(v) for v in x.shape)
     if luma is not None and c != 3:
         return None
     from .functional import gaussian_window_1d
 
-    win = _win_f32(gaussian_window_1d(win_size, sigma, device=x.device, dtype=torch.float32))
-    h, w = int(x.shape[-2]), int(x.shape[-1])
-    hout, wout = h - win_size + 1, w - win_size + 1
+    win = gaussian_window_1d(win_size, sigma, device=x.device, dtype=torch.float32)
     x, xs = _view_strides(x)
     y, ys = _view_strides(y)
-    cout = 1 if luma is not None else c
-    bpp = _ssim_workspace(ext, h, w, win_size)
-    partial = _f64(x.device, n * cout, bpp)
+    planes = n * (1 if luma is not None else c)
+    bpp = workspace_slots("ssim", h, w, win_size)
+    dev, stream = _site(x)
+    partial = _f64(x.device, planes, bpp)
+    # one sink: the float32 map, the per-image means or the batch mean
     smap = per_image = total = None
     if return_map:
-        smap = torch.empty((n, cout, hout, wout), device=x.device, dtype=torch.float32)
+        smap = torch.empty((n, planes // n, h - win_size + 1, w - win_size + 1),
+                           device=x.device, dtype=torch.float32)
     elif reduction == "none":
         per_image = _f64(x.device, n)
     else:
         total = _f64(x.device)
+    head = (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w)
+    tail = (_ptr(win), win_size, float(shift), float(C1), float(C2), _ptr(smap),
+            _ptr(partial), bpp, _ptr(per_image), _ptr(total), dev, stream)
     if luma is None and xs is None and ys is None:
-        _check(ext.gpu.fa_gpu_ssim(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), win_size,
-            float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
-            _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
+        _run("fa_gpu_ssim", *head, *tail)
     else:
-        _check(ext.gpu.fa_gpu_ssim_ex(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
-            _ptr(win), win_size, float(shift), float(C1), float(C2), _ptr(smap),
-            _ptr(partial), bpp, _ptr(per_image), _ptr(total), _dev(x), _stream(x)), ext)
+        _run("fa_gpu_ssim_ex", *head, xs, ys, _luma_arg(luma), *tail)
     if return_map:
         return smap if dtype == torch.float32 else smap.to(dtype)
     return per_image if reduction == "none" else total
@@ -544,38 +527,48 @@ def pyramid_dtype(dt: torch.dtype) -> torch.dtype:
     return torch.float32 if dt == torch.uint8 else torch.float64
 
 
-def _ssim_cs_gpu(ext: _Native, x, y, winf, shift, C1, C2, pool_dtype=None, luma=None):
-    """``(s, cs)`` plane means, plus the next pyramid level ``(px, py)`` of
-    ``pool_dtype`` when one is asked for (one fused pass).  x / y may be
-    strided views; ``luma`` = (kr, kg, kb, offset) makes each image one plane."""
-    n, c, h, w = x.shape
-    k = int(winf.numel())
-    cout = 1 if luma is not None else c
-    planes = n * cout
+def _cs_launch(x, y, win, shift, C1, C2, *, pool_dtype=None, luma=None, reduce=True,
+               u8_pyramid=False):
+    """One CS pass (``fa_gpu_ssim_cs_ex``, or ``fa_gpu_ssim_cs`` for a plain
+    contiguous call): the (ssim, cs) partial sums per plane, their plane means
+    when ``reduce``, and the next pyramid level of ``pool_dtype`` if given.
+
+    Returns ``(s, cs, partial, partial_cs, slots, px, py)``; ``s``/``cs`` are
+    ``None`` without ``reduce`` and ``slots`` is what the launch reports
+    (``-1`` when it was not asked)."""
+    win = _win32(win)
+    n, c, h, w = (int(v) for v in x.shape)
+    k = int(win.numel())
+    planes = n * (1 if luma is not None else c)
     x, xs = _view_strides(x)
     y, ys = _view_strides(y)
-    bpp = _ssim_workspace(ext, h, w, k)
+    bpp = workspace_slots("ssim", h, w, k)
+    dev, stream = _site(x)
     partial = _f64(x.device, planes, bpp)
     partial_cs = _f64(x.device, planes, bpp)
-    out_s = _f64(x.device, planes)
-    out_cs = _f64(x.device, planes)
-    if pool_dtype is None and luma is None and xs is None and ys is None:
-        _check(ext.gpu.fa_gpu_ssim_cs(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
-            float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
-            bpp, _ptr(out_s), _ptr(out_cs), _dev(x), _stream(x)), ext)
-        return out_s, out_cs
-    px = py = None
+    s = cs = px = py = None
+    if reduce:
+        s, cs = _f64(x.device, planes), _f64(x.device, planes)
     if pool_dtype is not None:
-        px = torch.empty((n, cout, h // 2, w // 2), dtype=pool_dtype, device=x.device)
+        px = torch.empty((n, planes // n, h // 2, w // 2), dtype=pool_dtype, device=x.device)
         py = torch.empty_like(px)
+    code = _DTYPE_CODE[x.dtype]
+    if u8_pyramid:
+        if x.dtype != torch.float32 or luma is not None:
+            raise ValueError("u8_pyramid needs float32 levels without luma")
+        code |= FA_DTYPE_U8_PYRAMID
+    head = (_ptr(x), _ptr(y), code, n, c, h, w)
+    consts = (_ptr(win), k, float(shift), float(C1), float(C2), _ptr(partial),
+              _ptr(partial_cs), bpp, _ptr(s), _ptr(cs))
+    if (reduce and pool_dtype is None and luma is None and xs is None and ys is None
+            and not u8_pyramid):
+        _run("fa_gpu_ssim_cs", *head, *consts, dev, stream)
+        return s, cs, partial, partial_cs, -1, None, None
+    slots = ctypes.c_int(-1)
     pcode = _DTYPE_CODE[pool_dtype if pool_dtype is not None else torch.float64]
-    _check(ext.gpu.fa_gpu_ssim_cs_ex(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
-        _ptr(winf), k, float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
-        bpp, _ptr(out_s), _ptr(out_cs), None, _ptr(px), _ptr(py), pcode, _dev(x),
-        _stream(x)), ext)
-    return (out_s, out_cs) if pool_dtype is None else (out_s, out_cs, px, py)
+    _run("fa_gpu_ssim_cs_ex", *head, xs, ys, _luma_arg(luma), *consts,
+         None if reduce else ctypes.byref(slots), _ptr(px), _ptr(py), pcode, dev, stream)
+    return s, cs, partial, partial_cs, int(slots.value), px, py
 
 
 def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None, u8_pyramid=False):
@@ -585,76 +578,46 @@ def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None, u8_pyramid
     next pyramid level (``None`` at the coarsest scale).  The partial sums go
     to :func:`ms_ssim_reduce`; nothing is synchronised.  ``u8_pyramid``: x and
     y are float32 levels of a uint8 pyramid (FA_DTYPE_U8_PYRAMID)."""
-    ext = load()
-    winf = _win_f32(win)
-    n, c, h, w = x.shape
-    k = int(winf.numel())
-    cout = 1 if luma is not None else c
-    x, xs = _view_strides(x)
-    y, ys = _view_strides(y)
-    bpp = _ssim_workspace(ext, h, w, k)
-    partial = _f64(x.device, n * cout, bpp)
-    partial_cs = _f64(x.device, n * cout, bpp)
-    px = py = None
-    if pool_dtype is not None:
-        px = torch.empty((n, cout, h // 2, w // 2), dtype=pool_dtype, device=x.device)
-        py = torch.empty_like(px)
-    pcode = _DTYPE_CODE[pool_dtype if pool_dtype is not None else torch.float64]
-    slots = ctypes.c_int(0)
-    code = _DTYPE_CODE[x.dtype]
-    if u8_pyramid:
-        if x.dtype != torch.float32 or luma is not None:
-            raise ValueError("u8_pyramid needs float32 levels without luma")
-        code |= FA_DTYPE_U8_PYRAMID
-    _check(ext.gpu.fa_gpu_ssim_cs_ex(
-        _ptr(x), _ptr(y), code, n, c, h, w, xs, ys, _luma_arg(luma),
-        _ptr(winf), k, float(shift), float(C1), float(C2), _ptr(partial), _ptr(partial_cs),
-        bpp, None, None, ctypes.byref(slots), _ptr(px), _ptr(py), pcode, _dev(x),
-        _stream(x)), ext)
-    npix = float((h - k + 1) * (w - k + 1))
-    return partial, partial_cs, int(slots.value), npix, px, py
+    _, _, ps, pcs, slots, px, py = _cs_launch(x, y, win, shift, C1, C2, pool_dtype=pool_dtype,
+                                              luma=luma, reduce=False, u8_pyramid=u8_pyramid)
+    k = int(win.numel())
+    npix = float((x.shape[-2] - k + 1) * (x.shape[-1] - k + 1))
+    return ps, pcs, slots, npix, px, py
 
 
 def ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype=None):
     """``(ssim, cs)`` plane means from the differentiable native path, plus the
     next pyramid level when ``pool_dtype`` is given."""
-    ext = load()
-    return _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2,
-                        pool_dtype)
+    s, cs, _, _, _, px, py = _cs_launch(_contig(x), _contig(y), win, shift, C1, C2,
+                                        pool_dtype=pool_dtype)
+    return (s, cs) if pool_dtype is None else (s, cs, px, py)
 
 
 def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy,
                      gpx=None, gpy=None):
     """Gradients of the plane means (and of the pyramid level the forward
     pooled, ``gpx`` / ``gpy``) with respect to x and y."""
-    ext = load()
-    x, y = _contig(x), _contig(y)
-    winf = _win_f32(win)
-    n, c, h, w = x.shape
-    k = int(winf.numel())
-    hout, wout = h - k + 1, w - k + 1
+    x, y, win = _contig(x), _contig(y), _win32(win)
+    n, c, h, w = (int(v) for v in x.shape)
+    k = int(win.numel())
     gsf = gs.to(torch.float32).contiguous().reshape(-1)
     gcsf = gcs.to(torch.float32).contiguous().reshape(-1)
-    aux = torch.empty((4 if need_dy else 3, n * c, hout, wout), device=x.device,
-                      dtype=torch.float32)
-    dx = torch.empty_like(x) if need_dx else None
-    dy = torch.empty_like(y) if need_dy else None
+    aux, dx, dy = _grad_buffers(x, y, k, need_dx, need_dy)
     gpx = _contig(gpx) if (gpx is not None and need_dx) else None
     gpy = _contig(gpy) if (gpy is not None and need_dy) else None
+    dev, stream = _site(x)
+    consts = (_ptr(win), k, n, c, h, w, float(shift), float(C1), float(C2))
     if x.dtype == torch.float32 and gpx is None and gpy is None:
-        _check(ext.gpu.fa_gpu_ssim_cs_backward(
-            _ptr(x), _ptr(y), _ptr(gsf), _ptr(gcsf), _ptr(winf), k, n, c, h, w,
-            float(shift), float(C1), float(C2), _ptr(aux), _ptr(dx), _ptr(dy),
-            _dev(x), _stream(x)), ext)
-    else:
-        gp = gpx if gpx is not None else gpy
-        gp_code = _DTYPE_CODE[gp.dtype] if gp is not None else _DTYPE_CODE[torch.float64]
-        if gpx is not None and gpy is not None and gpx.dtype != gpy.dtype:
-            gpy = gpy.to(gpx.dtype)
-        _check(ext.gpu.fa_gpu_ssim_cs_backward_ex(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], _ptr(gsf), _ptr(gcsf), _ptr(winf), k,
-            n, c, h, w, float(shift), float(C1), float(C2), _ptr(gpx), _ptr(gpy), gp_code,
-            _ptr(aux), _ptr(dx), _ptr(dy), _dev(x), _stream(x)), ext)
+        _run("fa_gpu_ssim_cs_backward", _ptr(x), _ptr(y), _ptr(gsf), _ptr(gcsf), *consts,
+             _ptr(aux), _ptr(dx), _ptr(dy), dev, stream)
+        return dx, dy
+    if gpx is not None and gpy is not None and gpx.dtype != gpy.dtype:
+        gpy = gpy.to(gpx.dtype)
+    gp = gpx if gpx is not None else gpy
+    gp_code = _DTYPE_CODE[gp.dtype if gp is not None else torch.float64]
+    _run("fa_gpu_ssim_cs_backward_ex", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], _ptr(gsf),
+         _ptr(gcsf), *consts, _ptr(gpx), _ptr(gpy), gp_code, _ptr(aux), _ptr(dx), _ptr(dy),
+         dev, stream)
     return dx, dy
 
 
@@ -671,34 +634,32 @@ def ssim_cs_pool(x, y, win, shift, C1, C2, pool_dtype, luma=None):
     """Inference form of one MS-SSIM scale: ``(s, cs, px, py)``, or ``(s, cs)``
     when ``pool_dtype`` is None (the coarsest scale).  Views are read in place;
     ``luma`` forms the luma plane of three-channel input in the kernel."""
-    ext = load()
-    return _ssim_cs_gpu(ext, x, y, _win_f32(win), shift, C1, C2, pool_dtype, luma)
+    s, cs, _, _, _, px, py = _cs_launch(x, y, win, shift, C1, C2, pool_dtype=pool_dtype,
+                                        luma=luma)
+    return (s, cs) if pool_dtype is None else (s, cs, px, py)
 
 
 def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
                 shift: float, C1: float, C2: float):
     """``(ssim, cs)`` per plane, shaped ``(N, C)``; ``None`` if unavailable."""
     k = int(win.numel())
+    if x.shape[-2] < k or x.shape[-1] < k or k not in _WINDOWS:
+        return None
+    n, c, h, w = (int(v) for v in x.shape)
     if not x.is_cuda:
-        lib = _cpu_ready(x, y) if k in _WINDOWS else None
-        if lib is None or x.shape[-2] < k or x.shape[-1] < k:
+        lib = _cpu_ready(x, y)
+        if lib is None:
             return None
-        x, y = _contig(x), _contig(y)
-        n, c, h, w = (int(v) for v in x.shape)
-        winf = win.to(torch.float32).contiguous()
+        x, y, win = _contig(x), _contig(y), _win32(win)
         s = torch.empty((n * c,), dtype=torch.float64)
         cs = torch.empty((n * c,), dtype=torch.float64)
         _check_cpu(lib.fa_cpu_ssim_cs(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(winf), k,
+            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), k,
             float(shift), float(C1), float(C2), _ptr(s), _ptr(cs)))
         return s.view(n, c), cs.view(n, c)
-    ext = _gpu_ext(x)
-    if ext is None or not _usable(x, y):
+    if _gpu_ext(x) is None or not _usable(x, y):
         return None
-    if k not in _WINDOWS or x.shape[-2] < k or x.shape[-1] < k:
-        return None
-    n, c = int(x.shape[0]), int(x.shape[1])
-    s, cs = _ssim_cs_gpu(ext, _contig(x), _contig(y), _win_f32(win), shift, C1, C2)
+    s, cs, *_ = _cs_launch(_contig(x), _contig(y), win, shift, C1, C2)
     return s.view(n, c), cs.view(n, c)
 
 
@@ -717,92 +678,78 @@ def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsamp
     their strides (``fa_gpu_gmsd_ex``).  CPU tensors run ``fa_cpu_gmsd``
     (statistics only: no luma, no map).
     """
+    n, c, h, w = (int(v) for v in x.shape)
+    hd, wd = (h // 2, w // 2) if downsample else (h, w)
     if not x.is_cuda:
         lib = _cpu_ready(x, y) if luma is None and not want_map else None
-        if lib is None:
+        if lib is None or hd < 3 or wd < 3:
             return None
         x, y = _contig(x), _contig(y)
-        n, c, h, w = (int(v) for v in x.shape)
-        hd, wd = (h // 2, w // 2) if downsample else (h, w)
-        if hd < 3 or wd < 3:
-            return None
         mean = torch.empty((n,), dtype=torch.float64)
         dev = torch.empty((n,), dtype=torch.float64)
         _check_cpu(lib.fa_cpu_gmsd(
             _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
             int(downsample), _ptr(mean), _ptr(dev)))
         return mean, dev
-    ext = _gpu_ext(x)
-    if ext is None or not _usable(x, y):
+    if _gpu_ext(x) is None or not _usable(x, y):
         return None
-    n, c = int(x.shape[0]), int(x.shape[1])
-    h, w = int(x.shape[-2]), int(x.shape[-1])
     if luma is not None and c != 3:
         return None
     x, xs = _view_strides(x)
     y, ys = _view_strides(y)
-    cout = 1 if luma is not None else c
-    planes = n * cout
-    bpp = _gmsd_workspace(ext, h, w, downsample)
-    psum = _f64(x.device, planes, bpp)
-    psumsq = _f64(x.device, planes, bpp)
-    mean = _f64(x.device, n)
-    dev = _f64(x.device, n)
-    qmap = None
-    if want_map:
-        hd, wd = (h // 2, w // 2) if downsample else (h, w)
-        qmap = torch.empty((n, cout, hd - 2, wd - 2), dtype=torch.float32, device=x.device)
+    planes = n * (1 if luma is not None else c)
+    mean, std, qmap = _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes,
+                                   want_map, hd, wd)
+    return (mean, std, qmap) if want_map else (mean, std)
+
+
+def _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, wd):
+    n, c, h, w = (int(v) for v in x.shape)
+    bpp = workspace_slots("gmsd", h, w, int(bool(downsample)))
+    dev, stream = _site(x)
+    psum, psumsq = _f64(x.device, planes, bpp), _f64(x.device, planes, bpp)
+    mean, std = _f64(x.device, n), _f64(x.device, n)
+    qmap = (torch.empty((n, planes // n, hd - 2, wd - 2), dtype=torch.float32,
+                        device=x.device) if want_map else None)
+    head = (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w)
+    consts = (float(T), float(eps), int(bool(downsample)))
+    sums = (_ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(std), dev, stream)
     if luma is None and xs is None and ys is None and qmap is None:
-        _check(ext.gpu.fa_gpu_gmsd(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
-            int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
-            _dev(x), _stream(x)), ext)
+        _run("fa_gpu_gmsd", *head, *consts, *sums)
     else:
-        _check(ext.gpu.fa_gpu_gmsd_ex(
-            _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, xs, ys, _luma_arg(luma),
-            float(T), float(eps), int(downsample), _ptr(qmap), _ptr(psum), _ptr(psumsq), bpp,
-            _ptr(mean), _ptr(dev), _dev(x), _stream(x)), ext)
-    return (mean, dev, qmap) if want_map else (mean, dev)
+        _run("fa_gpu_gmsd_ex", *head, xs, ys, _luma_arg(luma), *consts, _ptr(qmap), *sums)
+    return mean, std, qmap
 
 
 def gmsd_autograd_available(x: torch.Tensor, y: torch.Tensor) -> bool:
     """Can the differentiable native GMS / GMSD path serve this call?"""
-    return (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float64)
-            and y.dtype == x.dtype and x.shape == y.shape
-            and not torch.cuda.is_current_stream_capturing() and _gpu_ext(x) is not None)
+    return _autograd_ok(x, y, (torch.float32, torch.float64))
 
 
 def gmsd_stats_fwd(x, y, T, eps, downsample):
     """Forward half of the differentiable GMS / GMSD: ``(mean, std)`` per image."""
-    ext = load()
     x, y = _contig(x), _contig(y)
-    n, c, h, w = x.shape
-    bpp = _gmsd_workspace(ext, h, w, downsample)
-    psum = _f64(x.device, n * c, bpp)
-    psumsq = _f64(x.device, n * c, bpp)
-    mean = _f64(x.device, n)
-    dev = _f64(x.device, n)
-    _check(ext.gpu.fa_gpu_gmsd(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
-        int(downsample), _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(dev),
-        _dev(x), _stream(x)), ext)
-    return mean, dev
+    n, c, h, w = (int(v) for v in x.shape)
+    hd, wd = (h // 2, w // 2) if downsample else (h, w)
+    mean, std, _ = _gmsd_launch(x, y, None, None, None, T, eps, downsample, n * c, False,
+                                hd, wd)
+    return mean, std
 
 
 def gmsd_stats_bwd(x, y, mean, std, g_mean, g_std, T, eps, downsample, need_dx, need_dy):
-    ext = load()
+    """dL/dx, dL/dy of L = g_mean . mean + g_std . std (float64 arithmetic)."""
     x, y = _contig(x), _contig(y)
-    n, c, h, w = x.shape
+    n, c, h, w = (int(v) for v in x.shape)
     hd, wd = (h // 2, w // 2) if downsample else (h, w)
     aux = torch.empty((4, n * c, hd - 2, wd - 2), dtype=torch.float64, device=x.device)
-    gm = g_mean.to(torch.float64).contiguous() if g_mean is not None else None
-    gs = g_std.to(torch.float64).contiguous() if g_std is not None else None
+    gm = None if g_mean is None else g_mean.to(torch.float64).contiguous()
+    gs = None if g_std is None else g_std.to(torch.float64).contiguous()
     dx = torch.empty_like(x) if need_dx else None
     dy = torch.empty_like(y) if need_dy else None
-    _check(ext.gpu.fa_gpu_gmsd_backward(
-        _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, float(T), float(eps),
-        int(downsample), _ptr(mean), _ptr(std), _ptr(gm), _ptr(gs), _ptr(aux), _ptr(dx),
-        _ptr(dy), _dev(x), _stream(x)), ext)
+    dev, stream = _site(x)
+    _run("fa_gpu_gmsd_backward", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w,
+         float(T), float(eps), int(bool(downsample)), _ptr(mean), _ptr(std), _ptr(gm),
+         _ptr(gs), _ptr(aux), _ptr(dx), _ptr(dy), dev, stream)
     return dx, dy
 
 
@@ -810,16 +757,15 @@ def ms_ssim_reduce(partials, slots, npix, weights, n: int, c: int, per_image: bo
     """MS-SSIM's per-scale plane reductions, clamp / power / product and the
     channel and batch means in two launches (``fa_gpu_ms_ssim_reduce``) from
     the partial sums of :func:`ssim_cs_partials`."""
-    ext = load()
-    dev = partials[0].device
     m = len(partials)
+    ref = partials[0]
     arr = (ctypes.c_void_p * m)(*[t.data_ptr() for t in partials])
     sl = (ctypes.c_int * m)(*[int(v) for v in slots])
     npx = (ctypes.c_double * m)(*[float(v) for v in npix])
-    w = (ctypes.c_double * m)(*[float(v) for v in weights])
-    scratch = _f64(dev, m * n * c)
-    out = _f64(dev, n) if per_image else _f64(dev)
-    _check(ext.gpu.fa_gpu_ms_ssim_reduce(
-        arr, sl, npx, w, m, n, c, _ptr(scratch), _ptr(out) if per_image else None,
-        None if per_image else _ptr(out), _dev(partials[0]), _stream(partials[0])), ext)
+    wts = (ctypes.c_double * m)(*[float(v) for v in weights])
+    terms = _f64(ref.device, m * n * c)
+    out = _f64(ref.device, n) if per_image else _f64(ref.device)
+    dev, stream = _site(ref)
+    _run("fa_gpu_ms_ssim_reduce", arr, sl, npx, wts, m, n, c, _ptr(terms),
+         _ptr(out) if per_image else None, None if per_image else _ptr(out), dev, stream)
     return out

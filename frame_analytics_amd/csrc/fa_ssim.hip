@@ -611,7 +611,10 @@ __global__ __launch_bounds__(BLOCK) void ms_term_kernel(MsParts parts,
   const double sum = block_sum(a, smem);
   if (threadIdx.x == 0) {
     const double v = sum / parts.npix[m];
-    terms[static_cast<int64_t>(m) * gridDim.x + plane] = pow(v > 0.0 ? v : 0.0, parts.w[m]);
+    // clamp at zero like torch's clamp_min: a NaN term stays NaN (so does the
+    // product), it is not clamped to a finite 0
+    const double c = (v != v) ? v : (v > 0.0 ? v : 0.0);
+    terms[static_cast<int64_t>(m) * gridDim.x + plane] = pow(c, parts.w[m]);
   }
 }
 

@@ -15,6 +15,7 @@ Triton).  ``backend_hint="native"`` raises instead of taking it.
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import Optional, Sequence, Tuple
 
@@ -178,6 +179,9 @@ def _check_reduction(reduction: str) -> None:
 
 
 def _sum_sq(x, y, dtype, per_image):
+    from . import backend
+
+    backend.note_portable("mse", x)
     d = x.to(dtype) - y.to(dtype)
     if per_image:
         return (d * d).sum(dim=(1, 2, 3), dtype=torch.float64) / d[0].numel()
@@ -261,11 +265,22 @@ def gaussian_window_1d(win_size: int = 11, sigma: float = 1.5, *, device=None,
     return w
 
 
+def _f32_window(win: torch.Tensor) -> torch.Tensor:
+    """The float32 window the kernels take, for a window of any dtype: the
+    cached float32 copy when ``win`` came from :func:`gaussian_window_1d`."""
+    if win.dtype == torch.float32:
+        return win
+    return win.to(torch.float32).contiguous()
+
+
 def _moments_filtered(x4, y4, win, wdt, shift):
     """Separable 'valid' Gaussian of [x', y', x'^2, y'^2, x'y'], x' = x - shift.
 
     Returns a tuple of five (N, C, H-K+1, W-K+1) tensors.
     """
+    from . import backend
+
+    backend.note_portable("ssim_moments", x4)
     xs = x4.to(wdt) - shift
     ys = y4.to(wdt) - shift
     planes = torch.stack([xs, ys, xs * xs, ys * ys, xs * ys])  # (5, N, C, H, W)
@@ -303,40 +318,72 @@ def _reject_double_backward() -> None:
             "    ...(x, y, backend_hint='torch')")
 
 
-class _FusedSSIM(torch.autograd.Function):
-    """Differentiable native SSIM: only x, y and the window are saved; the
-    backward recomputes the moments (reference functional.py:521-572)."""
+class _NativeSSIM(torch.autograd.Function):
+    """Differentiable SSIM statistics from the gfx950 kernels, one class for
+    every form the public functions need (``form``):
+
+    * ``"mean"``: the batch-mean SSIM (``fa_gpu_ssim``).  The backward hands
+      the upstream gradient to the kernel as a 1-element device tensor, so it
+      never synchronises.
+    * ``"map"``: the float32 SSIM map; the backward takes the map's gradient.
+    * ``"cs"``: MS-SSIM's per-plane means ``(ssim, cs)`` (``fa_gpu_ssim_cs``).
+    * ``"cs+pool"``: the same plus the next pyramid level ``(px, py)`` from
+      the same pass (``fa_gpu_ssim_cs_ex``); the backward spreads a quarter of
+      the level's gradient over each 2x2 block inside the scatter of the
+      (ssim, cs) gradient (``fa_gpu_ssim_cs_backward_ex``), so a scale costs
+      one forward and two backward launches whatever reaches it.
+
+    Only x, y and the window are kept; the backward recomputes the moments
+    from them (the reference keeps the same memory profile,
+    functional.py:521-572 and :749-783).  ``consts`` is (shift, C1, C2).
+    """
 
     @staticmethod
-    def forward(ctx, x, y, win, shift, C1, C2, want_map):
+    def forward(ctx, x, y, win, consts, form, pool_dtype):
         from . import backend
 
-        res = backend.ssim_fused(x, y, win, shift, C1, C2, want_map)
+        shift, C1, C2 = consts
+        ctx.set_materialize_grads(False)
         ctx.save_for_backward(x, y, win)
-        ctx.consts = (shift, C1, C2)
-        ctx.want_map = want_map
-        return res[2] if want_map else res[1]
+        ctx.consts, ctx.form = consts, form
+        if form in ("mean", "map"):
+            res = backend.ssim_fused(x, y, win, shift, C1, C2, form == "map")
+            return res[2] if form == "map" else res[1]
+        if form == "cs":
+            return backend.ssim_cs_forward(x, y, win, shift, C1, C2)
+        s, cs, px, py = backend.ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype)
+        # a level of an input that needs no gradient needs none either: without
+        # this the next scale would compute (and this one spread) its gradient
+        for level, wanted in ((px, ctx.needs_input_grad[0]), (py, ctx.needs_input_grad[1])):
+            if not wanted:
+                ctx.mark_non_differentiable(level)
+        return s, cs, px, py
 
     @staticmethod
-    def backward(ctx, grad_out):
+    def backward(ctx, *grads):
         from . import backend
 
         _reject_double_backward()
+        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        nothing = (None,) * 6
+        if not (need_dx or need_dy) or all(g is None for g in grads):
+            return nothing
         x, y, win = ctx.saved_tensors
         shift, C1, C2 = ctx.consts
-        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not (need_dx or need_dy):
-            return (None,) * 7
-        empty = torch.empty(0, device=x.device, dtype=torch.float32)
-        if ctx.want_map:
-            dmap, gscalar = grad_out.contiguous(), empty
+        if ctx.form in ("mean", "map"):
+            g = grads[0]
+            dmap = g if ctx.form == "map" else None
+            gscalar = None if ctx.form == "map" else g.reshape(1)
+            dx, dy = backend.ssim_backward(x, y, dmap, gscalar, win, shift, C1, C2,
+                                           need_dx, need_dy)
         else:
-            # a 1-element device tensor: reading it on the host would sync
-            dmap, gscalar = empty, grad_out.reshape(1)
-        dx, dy = backend.ssim_backward(x, y, dmap, gscalar, win, shift, C1, C2,
-                                       need_dx, need_dy)
-        return (dx if need_dx else None, dy if need_dy else None,
-                None, None, None, None, None)
+            planes = x.shape[0] * x.shape[1]
+            g_s, g_cs = (g if g is not None else x.new_zeros(planes, dtype=torch.float32)
+                         for g in grads[:2])
+            g_px, g_py = grads[2:4] if ctx.form == "cs+pool" else (None, None)
+            dx, dy = backend.ssim_cs_backward(x, y, g_s, g_cs, win, shift, C1, C2,
+                                              need_dx, need_dy, g_px, g_py)
+        return (dx if need_dx else None, dy if need_dy else None) + nothing[2:]
 
 
 def _matlab_downsample(x: torch.Tensor, f: int) -> torch.Tensor:
@@ -393,7 +440,8 @@ def ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None
             and torch.is_grad_enabled() and reduction == "mean" and not downsample
             and backend.ssim_autograd_available(x4, y4, win_size)):
         win = gaussian_window_1d(win_size, sigma, device=x4.device, dtype=torch.float32)
-        return _FusedSSIM.apply(x4, y4, win, shift, C1, C2, return_map)
+        return _NativeSSIM.apply(x4, y4, win, (shift, C1, C2),
+                                 "map" if return_map else "mean", None)
 
     if backend_hint != "torch":
         fast = backend.try_ssim(x4, y4, win_size=win_size, sigma=sigma, shift=shift,
@@ -420,93 +468,19 @@ def ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None
 # Wang et al. 2003, table 1
 MS_SSIM_WEIGHTS = (0.0448, 0.2856, 0.3001, 0.2363, 0.1333)
 
-_ms_weight_cache: dict = {}
+@functools.lru_cache(maxsize=64)
+def _scale_exponents(weights: Tuple[float, ...], device: str) -> torch.Tensor:
+    """MS-SSIM's scale weights as an ``(M, 1, 1)`` float64 tensor on ``device``,
+    built once per (weights, device): a fresh tensor per call would be a
+    host-to-device copy, which a graph capture cannot hold."""
+    return torch.tensor(weights, dtype=torch.float64).view(-1, 1, 1).to(torch.device(device))
 
 
-def _ms_weights(w, device) -> torch.Tensor:
-    """Scale weights as a cached ``(M, 1, 1)`` float64 device tensor."""
-    key = (w, str(device))
-    t = _ms_weight_cache.get(key)
-    if t is None:
-        t = torch.tensor(w, dtype=torch.float64, device=device).view(-1, 1, 1)
-        _ms_weight_cache[key] = t
-    return t
-
-
-class _FusedSSIMCS(torch.autograd.Function):
-    """Differentiable native ``(ssim, cs)`` plane means, MS-SSIM's per-scale
-    primitive (reference functional.py:749-783)."""
-
-    @staticmethod
-    def forward(ctx, x, y, win, shift, C1, C2):
-        from . import backend
-
-        s, cs = backend.ssim_cs_forward(x, y, win, shift, C1, C2)
-        ctx.save_for_backward(x, y, win)
-        ctx.consts = (shift, C1, C2)
-        return s, cs
-
-    @staticmethod
-    def backward(ctx, g_s, g_cs):
-        from . import backend
-
-        _reject_double_backward()
-        x, y, win = ctx.saved_tensors
-        shift, C1, C2 = ctx.consts
-        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not (need_dx or need_dy):
-            return (None,) * 6
-        if g_s is None:
-            g_s = torch.zeros(x.shape[0] * x.shape[1], device=x.device)
-        if g_cs is None:
-            g_cs = torch.zeros(x.shape[0] * x.shape[1], device=x.device)
-        dx, dy = backend.ssim_cs_backward(x, y, g_s, g_cs, win, shift, C1, C2,
-                                          need_dx, need_dy)
-        return (dx if need_dx else None, dy if need_dy else None, None, None, None, None)
-
-
-class _FusedSSIMCSPool(torch.autograd.Function):
-    """One differentiable native MS-SSIM scale: the ``(ssim, cs)`` plane means
-    and the next pyramid level ``(px, py)`` from one pass over x and y
-    (``fa_gpu_ssim_cs_ex``).  The backward spreads a quarter of the level's
-    gradient over each 2x2 block inside the scatter of the (ssim, cs) gradient
-    (``fa_gpu_ssim_cs_backward_ex``), so a scale costs one forward and two
-    backward launches whatever reaches it."""
-
-    @staticmethod
-    def forward(ctx, x, y, win, shift, C1, C2, pool_dtype):
-        from . import backend
-
-        s, cs, px, py = backend.ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype)
-        ctx.save_for_backward(x, y, win)
-        ctx.consts = (shift, C1, C2)
-        ctx.set_materialize_grads(False)
-        # a level of an input that needs no gradient needs none either: without
-        # this the next scale would compute (and this one spread) its gradient
-        if not ctx.needs_input_grad[0]:
-            ctx.mark_non_differentiable(px)
-        if not ctx.needs_input_grad[1]:
-            ctx.mark_non_differentiable(py)
-        return s, cs, px, py
-
-    @staticmethod
-    def backward(ctx, g_s, g_cs, g_px, g_py):
-        from . import backend
-
-        _reject_double_backward()
-        x, y, win = ctx.saved_tensors
-        shift, C1, C2 = ctx.consts
-        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not (need_dx or need_dy):
-            return (None,) * 7
-        planes = x.shape[0] * x.shape[1]
-        if g_s is None:
-            g_s = torch.zeros(planes, device=x.device)
-        if g_cs is None:
-            g_cs = torch.zeros(planes, device=x.device)
-        dx, dy = backend.ssim_cs_backward(x, y, g_s, g_cs, win, shift, C1, C2,
-                                          need_dx, need_dy, g_px, g_py)
-        return (dx if need_dx else None, dy if need_dy else None) + (None,) * 5
+def _combine_scales(terms, weights, device) -> torch.Tensor:
+    """Per plane: prod_j max(t_j, 0)^w_j over the stacked ``(N, C)`` terms (a
+    fractional power of a negative factor is not real, hence the clamp)."""
+    stacked = torch.stack(terms).clamp_min(0.0)
+    return stacked.pow(_scale_exponents(tuple(weights), str(device))).prod(dim=0)
 
 
 def _ssim_cs_pair(x4, y4, win, wdt, shift, C1, C2, backend_hint):
@@ -517,7 +491,7 @@ def _ssim_cs_pair(x4, y4, win, wdt, shift, C1, C2, backend_hint):
     if (backend_hint != "torch" and (x4.requires_grad or y4.requires_grad)
             and torch.is_grad_enabled()
             and backend.ssim_cs_autograd_available(x4, y4, win.numel())):
-        s, cs = _FusedSSIMCS.apply(x4, y4, win, shift, C1, C2)
+        s, cs = _NativeSSIM.apply(x4, y4, _f32_window(win), (shift, C1, C2), "cs", None)
         return s.view(n, c), cs.view(n, c)
     if backend_hint != "torch":
         fast = backend.try_ssim_cs(x4, y4, win=win, shift=shift, C1=C1, C2=C2)
@@ -588,6 +562,8 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
         elif grad and x4.dtype in (torch.float16, torch.bfloat16):
             x4, y4 = x4.float(), y4.float()
         pdt = torch.float64 if lw is not None else backend.pyramid_dtype(x4.dtype)
+        win32 = _f32_window(win)
+        consts = (shift, C1, C2)
         cx, cy = x4, y4
         if not grad and len(w) <= 8:
             # inference: every scale leaves its partial sums, and one reduction
@@ -599,7 +575,7 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
             for i in range(scales):
                 last = i == scales - 1
                 ps, pcs, sl, npx, cx, cy = backend.ssim_cs_partials(
-                    cx, cy, win, shift, C1, C2, None if last else pdt,
+                    cx, cy, win32, shift, C1, C2, None if last else pdt,
                     luma=lw if i == 0 else None, u8_pyramid=u8 and i > 0)
                 parts.append(ps if last else pcs)
                 slots.append(sl)
@@ -610,18 +586,19 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
             last = i == scales - 1
             if grad:
                 if last:
-                    s, cs = _FusedSSIMCS.apply(cx, cy, win, shift, C1, C2)
+                    s, cs = _NativeSSIM.apply(cx, cy, win32, consts, "cs", None)
                 else:
-                    s, cs, cx, cy = _FusedSSIMCSPool.apply(cx, cy, win, shift, C1, C2, pdt)
+                    s, cs, cx, cy = _NativeSSIM.apply(cx, cy, win32, consts, "cs+pool", pdt)
             else:
-                out = backend.ssim_cs_pool(cx, cy, win, shift, C1, C2, None if last else pdt,
-                                           luma=lw if i == 0 else None)
+                out = backend.ssim_cs_pool(cx, cy, win32, shift, C1, C2,
+                                           None if last else pdt, luma=lw if i == 0 else None)
                 s, cs = out[0], out[1]
                 if not last:
                     cx, cy = out[2], out[3]
             terms.append((s if last else cs).view(n, c))
     else:
         # the portable path pools at the working dtype, as the reference does
+        backend.note_portable("ms_ssim_pyramid", x4)
         cx, cy = x4, y4
         for i in range(scales):
             if i:
@@ -629,9 +606,7 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
                 cy = F.avg_pool2d(cy.to(wdt), 2)
             s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
             terms.append(s if i == scales - 1 else cs)
-    # a fractional power of a negative factor is not real: clamp at zero
-    per_plane = torch.stack(terms).clamp_min(0.0).pow(_ms_weights(w, x4.device)).prod(dim=0)
-    per_image = per_plane.mean(dim=1)
+    per_image = _combine_scales(terms, w, x4.device).mean(dim=1)  # channels after the product
     return per_image if reduction == "none" else per_image.mean()
 
 
@@ -639,21 +614,20 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
 # GMSD / GMS
 # --------------------------------------------------------------------------- #
 
-_prewitt_cache: dict = {}
-
-
-def _prewitt_pair(device, dtype) -> torch.Tensor:
-    """``(2, 1, 3, 3)``: horizontal and vertical Prewitt taps, scaled by 1/3."""
-    key = (str(device), dtype)
-    k = _prewitt_cache.get(key)
-    if k is None:
-        gx = torch.tensor([[1.0, 0.0, -1.0]] * 3, dtype=torch.float64) / 3.0
-        k = torch.stack([gx, gx.t().contiguous()]).unsqueeze(1).to(device=device, dtype=dtype)
-        _prewitt_cache[key] = k
-    return k
+@functools.lru_cache(maxsize=16)
+def _prewitt_bank(device: str, dtype: torch.dtype) -> torch.Tensor:
+    """``(2, 1, 3, 3)``: the x and y Prewitt kernels with taps +-1/3, as one
+    convolution bank, built once per (device, dtype)."""
+    ramp = torch.tensor([1.0, 0.0, -1.0], dtype=torch.float64) / 3.0
+    flat = torch.ones(3, dtype=torch.float64)
+    bank = torch.stack([torch.outer(flat, ramp), torch.outer(ramp, flat)])
+    return bank.unsqueeze(1).to(device=torch.device(device), dtype=dtype)
 
 
 def _gms_map(x4, y4, wdt, T, eps, downsample):
+    from . import backend
+
+    backend.note_portable("gms_map", x4)
     xf, yf = x4.to(wdt), y4.to(wdt)
     if downsample:
         xf, yf = F.avg_pool2d(xf, 2), F.avg_pool2d(yf, 2)
@@ -662,7 +636,7 @@ def _gms_map(x4, y4, wdt, T, eps, downsample):
         raise ValueError(f"image {h}x{w} is smaller than the 3x3 Prewitt window")
     both = torch.cat([xf, yf], dim=0).reshape(2 * n * c, 1, h, w)
     with _no_autocast(both):
-        g = F.conv2d(both, _prewitt_pair(xf.device, wdt))  # (2NC, 2, H-2, W-2)
+        g = F.conv2d(both, _prewitt_bank(str(xf.device), wdt))  # (2NC, 2, H-2, W-2)
     g1 = torch.sqrt((g[: n * c] ** 2).sum(dim=1) + eps)
     g2 = torch.sqrt((g[n * c:] ** 2).sum(dim=1) + eps)
     q = (2.0 * g1 * g2 + T) / (g1 * g1 + g2 * g2 + T)
@@ -823,6 +797,7 @@ def _pixel_loss(name, x, y, param, reduction, dtype, out_dtype, luma, crop_borde
                                  per_image=per_image, dtype=out_dtype)
         if fast is not None:
             return fast
+    backend.note_portable(name, x4)
     t = _pixel_terms(name, x4.to(wdt) - y4.to(wdt), param)
     if per_image:
         out = t.sum(dim=(1, 2, 3), dtype=torch.float64) / t[0].numel()

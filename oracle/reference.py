@@ -17,7 +17,12 @@ How each function is pinned (see tests/test_oracle.py):
   * ssim / cs: identity ssim(x,x)=1, scipy cross-check, the reference's own
     CPU C++ (oracle/_ref, built from the reference sources) at its 5e-6 gate
   * ms_ssim: single-scale special cases reduce to ssim / cs, avg-pool via torch,
-    the reference CPU C++ per-scale primitive
+    the reference CPU C++ per-scale primitive, the reference's own
+    "channels averaged after the product" case (two 1-channel values against
+    one 2-channel call, with the channel-mean-first variant as a negative
+    control), weights (0,0,0,0,1) against ssim of the pair pooled four times
+    by torch, and the clamp on an anti-correlated pair (exactly 0)
+  * ms_ssim gradient: float64 central differences of ms_ssim
   * gmsd: identity, the reference CPU C++ gmsd, torch conv2d Prewitt;
     gmsd_stats_hp: gmsd_stats at ordinary noise, a 40-digit decimal brute force
   * ssim gradient: float64 central differences and float64 torch autograd
@@ -409,6 +414,107 @@ def ssim_mean_grad(x, y, data_range=1.0, win_size=11, sigma=1.5, K=(0.01, 0.03),
     dx = 2 * x * Pb + y * Pc + full_correlate_transposed(tx, w, H, W)
     dy = 2 * y * Pb + x * Pc + full_correlate_transposed(ty, w, H, W)
     return dx, dy
+
+
+def ssim_cs_map_grad(x, y, g_s, g_cs, data_range=1.0, win_size=11, sigma=1.5,
+                     K=(0.01, 0.03)) -> Tuple[np.ndarray, np.ndarray]:
+    """d L / d x and d L / d y in float64 for L = sum(g_s * ssim_map + g_cs * cs_map)
+    over the last two axes; g_s, g_cs broadcast against the (H-K+1, W-K+1) maps.
+
+    cs = A2/B2 depends on the means only through the variances:
+    dcs/dsxy = 2/B2, dcs/dsxx = dcs/dsyy = -cs/B2, no direct mu term.  The
+    SSIM part is that of :func:`ssim_mean_grad`; the two share the chain rule
+    through mu = w*x, sxx = w*x^2 - mu^2, sxy = w*xy - mu_x mu_y."""
+    x = np.asarray(x, np.float64)
+    y = np.asarray(y, np.float64)
+    w = gaussian_window_1d(win_size, sigma)
+    C1 = (K[0] * data_range) ** 2
+    C2 = (K[1] * data_range) ** 2
+    mx = separable_valid(x, w)
+    my = separable_valid(y, w)
+    sxx = separable_valid(x * x, w) - mx * mx
+    syy = separable_valid(y * y, w) - my * my
+    sxy = separable_valid(x * y, w) - mx * my
+    A1 = 2 * mx * my + C1
+    A2 = 2 * sxy + C2
+    B1 = mx * mx + my * my + C1
+    B2 = sxx + syy + C2
+    S = A1 * A2 / (B1 * B2)
+    cs = A2 / B2
+    gs = np.broadcast_to(np.asarray(g_s, np.float64), S.shape)
+    gc = np.broadcast_to(np.asarray(g_cs, np.float64), S.shape)
+    b = gs * (-S / B2) + gc * (-cs / B2)
+    c = gs * (2 * A1 / (B1 * B2)) + gc * (2.0 / B2)
+    tx = gs * (2 * A2 / (B1 * B2) * (my - mx * A1 / B1)) - 2 * b * mx - c * my
+    ty = gs * (2 * A2 / (B1 * B2) * (mx - my * A1 / B1)) - 2 * b * my - c * mx
+    H, W = x.shape[-2:]
+    Pb = full_correlate_transposed(b, w, H, W)
+    Pc = full_correlate_transposed(c, w, H, W)
+    dx = 2 * x * Pb + y * Pc + full_correlate_transposed(tx, w, H, W)
+    dy = 2 * y * Pb + x * Pc + full_correlate_transposed(ty, w, H, W)
+    return dx, dy
+
+
+def avg_pool2_adjoint(g: np.ndarray, H: int, W: int) -> np.ndarray:
+    """Adjoint of :func:`avg_pool2` onto an H x W plane: a quarter of each
+    pooled gradient to every pixel of its 2x2 block, nothing to a dropped odd
+    trailing row or column."""
+    h, w = g.shape[-2:]
+    out = np.zeros(g.shape[:-2] + (H, W), dtype=np.float64)
+    out[..., :2 * h, :2 * w] = 0.25 * np.repeat(np.repeat(g, 2, axis=-2), 2, axis=-1)
+    return out
+
+
+def ms_ssim_grad(x, y, data_range=1.0, win_size=11, sigma=1.5, K=(0.01, 0.03),
+                 weights: Sequence[float] = MS_SSIM_WEIGHTS,
+                 upstream=None) -> Tuple[np.ndarray, np.ndarray]:
+    """d L / d x and d L / d y in float64 of L = sum_n u[n] * ms_ssim_n(x, y),
+    the per-image MS-SSIM of :func:`ms_ssim` (``upstream`` u; default 1/N,
+    the gradient of the batch mean).
+
+    Through the composition of functional.py:887-901: per plane
+    P = prod_j max(t_j, 0)^w_j, so dP/dt_j = w_j t_j^(w_j - 1) prod_{k != j}
+    max(t_k, 0)^w_k for t_j > 0 and 0 where the clamp holds; the channel
+    mean gives each plane u[n]/C; t_j is the plane mean of the cs map (the
+    SSIM map at the coarsest scale), so its map-level upstream is
+    dP/dt_j / (map size); each level's gradient reaches the level above
+    through the 2x2 mean's adjoint."""
+    cx = np.asarray(x, np.float64)
+    cy = np.asarray(y, np.float64)
+    N, C = cx.shape[:2]
+    wts = [float(v) for v in weights]
+    M = len(wts)
+    levels = [(cx, cy)]
+    for _ in range(M - 1):
+        levels.append((avg_pool2(levels[-1][0]), avg_pool2(levels[-1][1])))
+    terms = []
+    for j, (lx, ly) in enumerate(levels):
+        s, cs = ssim_maps(lx, ly, data_range, win_size, sigma, K[0], K[1])
+        terms.append((s if j == M - 1 else cs).mean(axis=(-2, -1)))
+    t = np.stack(terms)                       # (M, N, C)
+    tc = np.maximum(t, 0.0)
+    u = np.full(N, 1.0 / N) if upstream is None else np.asarray(upstream, np.float64)
+    gP = np.broadcast_to((u / C)[:, None], (N, C))
+    gx = gy = None
+    for j in range(M - 1, -1, -1):
+        others = np.ones((N, C))
+        for k in range(M):
+            if k != j:
+                others = others * tc[k] ** wts[k]
+        with np.errstate(divide="ignore", invalid="ignore"):
+            dt = np.where(t[j] > 0, wts[j] * tc[j] ** (wts[j] - 1.0), 0.0) * others * gP
+        lx, ly = levels[j]
+        npix = (lx.shape[-2] - win_size + 1) * (lx.shape[-1] - win_size + 1)
+        g = (dt / npix)[..., None, None]
+        zero = np.zeros_like(g)
+        dlx, dly = ssim_cs_map_grad(lx, ly, g if j == M - 1 else zero,
+                                    zero if j == M - 1 else g,
+                                    data_range, win_size, sigma, K)
+        if gx is not None:  # the coarser level's gradient, spread back
+            dlx = dlx + avg_pool2_adjoint(gx, *lx.shape[-2:])
+            dly = dly + avg_pool2_adjoint(gy, *ly.shape[-2:])
+        gx, gy = dlx, dly
+    return gx, gy
 
 
 def valid_correlate_adjoint(m: np.ndarray, k: np.ndarray, H: int, W: int) -> np.ndarray:

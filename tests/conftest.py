@@ -15,6 +15,42 @@ if str(REPO) not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")
+    config.addinivalue_line(
+        "markers", "portable_ok: a gpu test that runs the portable PyTorch path on GPU "
+        "tensors on purpose (exempt from the native-dispatch check)")
+
+
+@pytest.hookimpl(hookwrapper=True)
+def pytest_runtest_makereport(item, call):
+    outcome = yield
+    rep = outcome.get_result()
+    setattr(item, "rep_" + rep.when, rep)
+
+
+@pytest.fixture(autouse=True)
+def _served_by_gfx950_kernels(request):
+    """A passing ``gpu`` test must have been served by the HIP kernels: at
+    least one entry point of libfa_gpu.so ran during it (counted by
+    ``backend.call_gpu``), and the portable PyTorch path computed nothing on a
+    GPU tensor (``backend.portable_calls``).  So a ``try_*`` that quietly
+    returned None -- which would let eager PyTorch meet the same numerical
+    bars -- fails the suite."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    from frame_analytics_amd import backend
+
+    ran0 = sum(backend.native_calls.values())
+    portable0 = dict(backend.portable_calls)
+    yield
+    rep = getattr(request.node, "rep_call", None)
+    if rep is None or not rep.passed or request.node.get_closest_marker("portable_ok"):
+        return
+    ran = sum(backend.native_calls.values()) - ran0
+    portable = {k: v - portable0.get(k, 0) for k, v in backend.portable_calls.items()
+                if v != portable0.get(k, 0)}
+    assert ran > 0, "no gfx950 entry point ran in this GPU test"
+    assert not portable, f"the portable PyTorch path ran on GPU tensors: {portable}"
 
 
 def u8_pair(shape, sigma, seed):

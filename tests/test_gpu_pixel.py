@@ -297,17 +297,16 @@ def test_any_workspace_size_exact(gpu, n):
     larger sweep, and sizes that take the per-image grid."""
     from frame_analytics_amd import backend
 
-    ext = backend.load()
     a, b = u8_pair((n, 1, 2048, 2048), 5.0, seed=n)
     x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
     per = a[0].size
     want = ref.mse(a, b, "none")
     stream = torch.cuda.current_stream().cuda_stream
-    for bpi in (backend._pixel_workspace(ext, n, per, 0), 8, 64, 4096, 1, 7, 255, 1000):
+    for bpi in (backend.workspace_slots("pixel", n, per, 0), 8, 64, 4096, 1, 7, 255, 1000):
         part = torch.empty((n, bpi), dtype=torch.float64, device=gpu)
         out = torch.empty(n, dtype=torch.float64, device=gpu)
-        rc = ext.gpu.fa_gpu_pixel_reduce(x.data_ptr(), y.data_ptr(), 0, n, per, 0, 0.0, -1e300,
-                                         part.data_ptr(), bpi, out.data_ptr(), None, None, None,
-                                         0, stream)
+        rc = backend.call_gpu("fa_gpu_pixel_reduce", x.data_ptr(), y.data_ptr(), 0, n, per, 0,
+                              0.0, -1e300, part.data_ptr(), bpi, out.data_ptr(), None, None,
+                              None, 0, stream)
         assert rc == 0, (bpi, rc)
         assert np.array_equal(out.cpu().numpy(), want), bpi

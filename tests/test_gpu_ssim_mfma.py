@@ -176,13 +176,12 @@ def test_ms_ssim_pyramid_level_exact(gpu):
     # the level the CS pass writes is the exact 2 x 2 mean of the uint8 input
     from frame_analytics_amd import backend
 
-    ext = backend.load()
     a, b = u8_pair((2, 3, 90, 136), 7.0, seed=4)
     x = torch.as_tensor(a, device=gpu)
     y = torch.as_tensor(b, device=gpu)
     n, c, h, w = a.shape
     win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
-    bpp = backend._ssim_workspace(ext, h, w, 11)
+    bpp = backend.workspace_slots("ssim", h, w, 11)
     part = torch.empty((n * c, bpp), dtype=torch.float64, device=gpu)
     part_cs = torch.empty_like(part)
     out_s = torch.empty(n * c, dtype=torch.float64, device=gpu)
@@ -192,11 +191,11 @@ def test_ms_ssim_pyramid_level_exact(gpu):
     import ctypes
     slots = ctypes.c_int(0)
     stream = torch.cuda.current_stream().cuda_stream
-    rc = ext.gpu.fa_gpu_ssim_cs_ex(x.data_ptr(), y.data_ptr(), 0, n, c, h, w, None, None, None,
-                                   win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
-                                   (0.03 * 255) ** 2, part.data_ptr(), part_cs.data_ptr(), bpp,
-                                   out_s.data_ptr(), out_cs.data_ptr(), ctypes.addressof(slots),
-                                   px.data_ptr(), py.data_ptr(), 3, 0, stream)
+    rc = backend.call_gpu("fa_gpu_ssim_cs_ex", x.data_ptr(), y.data_ptr(), 0, n, c, h, w,
+                          None, None, None, win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
+                          (0.03 * 255) ** 2, part.data_ptr(), part_cs.data_ptr(), bpp,
+                          out_s.data_ptr(), out_cs.data_ptr(), ctypes.addressof(slots),
+                          px.data_ptr(), py.data_ptr(), 3, 0, stream)
     assert rc == 0
     want_x = ref.avg_pool2(a.astype(np.float64))
     want_y = ref.avg_pool2(b.astype(np.float64))
@@ -248,18 +247,17 @@ def test_pyramid_level_flag(gpu, s):
 def test_pyramid_flag_is_an_ex_hint_only(gpu):
     from frame_analytics_amd import backend
 
-    ext = backend.load()
     x = torch.zeros((1, 1, 32, 32), device=gpu)
     win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
-    bpp = backend._ssim_workspace(ext, 32, 32, 11)
+    bpp = backend.workspace_slots("ssim", 32, 32, 11)
     part = torch.empty((1, bpp), dtype=torch.float64, device=gpu)
     o = torch.empty(1, dtype=torch.float64, device=gpu)
     stream = torch.cuda.current_stream().cuda_stream
     # the reference-shaped entry point refuses the flag
-    rc = ext.gpu.fa_gpu_ssim_cs(x.data_ptr(), x.data_ptr(), 3 | backend.FA_DTYPE_U8_PYRAMID,
-                                1, 1, 32, 32, win.data_ptr(), 11, 0.5, 1e-4, 9e-4,
-                                part.data_ptr(), part.data_ptr(), bpp, o.data_ptr(),
-                                o.data_ptr(), 0, stream)
+    rc = backend.call_gpu("fa_gpu_ssim_cs", x.data_ptr(), x.data_ptr(),
+                          3 | backend.FA_DTYPE_U8_PYRAMID, 1, 1, 32, 32, win.data_ptr(), 11,
+                          0.5, 1e-4, 9e-4, part.data_ptr(), part.data_ptr(), bpp, o.data_ptr(),
+                          o.data_ptr(), 0, stream)
     assert rc == 1  # FA_E_DTYPE
     with pytest.raises(ValueError):
         backend.ssim_cs_partials(x.double(), x.double(), win, 0.5, 1e-4, 9e-4, None,

@@ -174,6 +174,130 @@ def test_ms_ssim_special_cases():
     assert abs(ref.ms_ssim(a, a, 255.0, weights=(0.5, 0.5)) - 1.0) < 1e-14
 
 
+def _photo_pair(h, w, seed, noise):
+    """Smooth texture plus noise, the style of the reference's MS-SSIM tests
+    (test_training_metrics.py:30-36)."""
+    rng = np.random.default_rng(seed)
+    yy, xx = np.mgrid[0:h, 0:w].astype(np.float64)
+    a = np.clip(120 + 50 * np.sin(xx / 11.0) * np.cos(yy / 13.0)
+                + 12 * rng.standard_normal((h, w)), 0, 255).round()
+    b = np.clip(a + noise * rng.standard_normal((h, w)), 0, 255).round()
+    return a, b
+
+
+def test_ms_ssim_channels_averaged_after_the_product():
+    """The reference's own case (test_training_metrics.py:97-110): a 2-channel
+    MS-SSIM equals the mean of the two 1-channel values.  Averaging the
+    per-scale terms over channels before the product gives a different
+    number, so the check can tell the two conventions apart."""
+    a1, b1 = _photo_pair(184, 200, seed=21, noise=8.0)
+    a2, b2 = _photo_pair(184, 200, seed=22, noise=30.0)
+    r1 = ref.ms_ssim(a1[None, None], b1[None, None], 255.0)
+    r2 = ref.ms_ssim(a2[None, None], b2[None, None], 255.0)
+    x = np.stack([a1, a2])[None]
+    y = np.stack([b1, b2])[None]
+    got = ref.ms_ssim(x, y, 255.0)
+    assert abs(got - 0.5 * (r1 + r2)) < 1e-15
+    # negative control: the channel mean taken first, per scale
+    terms = ref.ms_ssim_terms(x, y, 255.0)
+    w = ref.MS_SSIM_WEIGHTS
+    first = 1.0
+    for i, wi in enumerate(w):
+        v = terms[i][0] if i == len(w) - 1 else terms[i][1]
+        first *= max(float(v.mean()), 0.0) ** wi
+    assert abs(first - got) > 1e-4, (first, got)
+
+
+def test_ms_ssim_coarsest_scale_alone_is_ssim_of_the_fourth_pool():
+    """weights (0, 0, 0, 0, 1) leave only the full SSIM at scale 4: the SSIM of
+    the pair pooled four times by torch's avg_pool2d (which drops an odd
+    trailing row / column).  A pyramid one level too shallow or too deep, or
+    cs in place of SSIM at the last scale, fails this."""
+    a, b = u8_pair((2, 2, 181, 199), 10.0, seed=31)
+    b = np.clip(b.astype(np.int32) + 40, 0, 255).astype(np.uint8)  # a luminance gap
+    tx = torch.from_numpy(a.astype(np.float64))
+    ty = torch.from_numpy(b.astype(np.float64))
+    pooled = []
+    for _ in range(4):
+        tx, ty = F.avg_pool2d(tx, 2), F.avg_pool2d(ty, 2)
+        pooled.append((tx.numpy(), ty.numpy()))
+    assert tuple(tx.shape[-2:]) == (11, 12)
+    want = ref.ssim(tx.numpy(), ty.numpy(), 255.0, reduction="none")
+    got = ref.ms_ssim(a, b, 255.0, weights=(0, 0, 0, 0, 1), reduction="none")
+    assert np.abs(got - want).max() < 1e-14
+    # negative controls: cs in place of SSIM at the coarsest scale, and a
+    # pyramid one level shallower, are measurably different
+    _, cs4 = ref.ssim_maps(tx.numpy(), ty.numpy(), 255.0)
+    assert np.abs(cs4.mean(axis=(-2, -1)).mean(axis=1) - got).max() > 1e-3
+    s3 = ref.ssim(*pooled[2], 255.0, reduction="none")
+    assert np.abs(s3 - got).max() > 1e-3
+
+
+def test_ms_ssim_clamps_anti_correlated_content_to_zero():
+    """y = 255 - x makes cs at scale 0 negative (sigma_xy = -sigma_x^2); the
+    clamp at zero (reference functional.py:893-896) makes the product exactly
+    0, where the unclamped fractional power is not real."""
+    a, _ = u8_pair((1, 1, 176, 180), 8.0, seed=41)
+    b = 255 - a
+    terms = ref.ms_ssim_terms(a, b, 255.0)
+    assert float(terms[0][1].min()) < -0.5
+    assert ref.ms_ssim(a, b, 255.0) == 0.0
+    with np.errstate(invalid="ignore"):
+        assert np.isnan(np.power(terms[0][1][0, 0], ref.MS_SSIM_WEIGHTS[0]))
+
+
+def _ms_fd(x, y, i, j, n=0, c=0, h=1e-4, **kw):
+    xp, xm = x.copy(), x.copy()
+    xp[n, c, i, j] += h
+    xm[n, c, i, j] -= h
+    return (ref.ms_ssim(xp, y, **kw) - ref.ms_ssim(xm, y, **kw)) / (2 * h)
+
+
+@pytest.mark.parametrize("shape,kw", [
+    ((2, 2, 180, 192), {}),
+    ((1, 3, 64, 70), {"win_size": 7, "weights": (0.3, 0.7)}),
+])
+def test_ms_ssim_grad_central_differences(shape, kw):
+    """The closed-form MS-SSIM adjoint (clamp, product, channel and batch
+    means, pyramid) against central differences of the float64 forward, at
+    pixels in different images and channels, inside the valid grid of every
+    scale and in a dropped odd trailing row / column."""
+    rng = np.random.default_rng(7)
+    x = rng.random(shape)
+    y = np.clip(x + 0.05 * rng.standard_normal(shape), 0, 1)
+    opts = dict(data_range=1.0, **kw)
+    gx, gy = ref.ms_ssim_grad(x, y, **opts)
+    H, W = shape[-2:]
+    pts = [(0, 0, 40, 60), (shape[0] - 1, shape[1] - 1, H // 2, W // 3),
+           (0, shape[1] - 1, 3, W - 5), (shape[0] - 1, 0, H - 1, 7)]
+    scale = np.abs(gx).max()
+    for n, c, i, j in pts:
+        fd = _ms_fd(x, y, i, j, n, c, **opts)
+        assert abs(fd - gx[n, c, i, j]) <= 2e-7 * scale, (n, c, i, j, fd, gx[n, c, i, j])
+    # d/dy by symmetry of the formula in (x, y): the swapped call's dx
+    gy2, _ = ref.ms_ssim_grad(y, x, **opts)
+    assert np.abs(gy - gy2).max() <= 1e-12 * scale
+    n, c, i, j = pts[1]
+    yp, ym = y.copy(), y.copy()
+    yp[n, c, i, j] += 1e-4
+    ym[n, c, i, j] -= 1e-4
+    fd = (ref.ms_ssim(x, yp, **opts) - ref.ms_ssim(x, ym, **opts)) / 2e-4
+    assert abs(fd - gy[n, c, i, j]) <= 2e-7 * scale
+
+
+def test_ms_ssim_grad_upstream_and_clamped_planes():
+    """A per-image upstream vector scales each image's gradient, and a plane
+    whose scale-0 cs is clamped contributes no gradient at all."""
+    rng = np.random.default_rng(8)
+    x = rng.random((2, 1, 176, 176))
+    y = np.clip(x + 0.05 * rng.standard_normal(x.shape), 0, 1)
+    y[1] = 1.0 - x[1]  # anti-correlated: clamped to 0
+    gx, _ = ref.ms_ssim_grad(x, y, data_range=1.0, upstream=np.array([3.0, 5.0]))
+    g0, _ = ref.ms_ssim_grad(x[:1], y[:1], data_range=1.0, upstream=np.array([1.0]))
+    assert np.abs(gx[0] - 3.0 * g0[0]).max() <= 1e-12 * np.abs(g0).max()
+    assert np.abs(gx[1]).max() == 0.0
+
+
 def test_gmsd_against_torch_conv_and_identity():
     a, b = natural_pair(40, 46, 9.0, seed=9)
     x4, y4 = a[None, None], b[None, None]
