@@ -36,6 +36,8 @@ FA_API const char* fa_gpu_error_string(int code) {
     case FA_E_OP: return "unknown pixel op";
     case FA_E_ARG: return "invalid argument";
     case FA_E_NOGPU: return "no GPU device";
+    case FA_E_SCRATCH:
+      return "the call needs more partial-sum slots than the no-allocation scratch holds";
     default: return "internal error";
   }
 }

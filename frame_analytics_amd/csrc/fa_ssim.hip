@@ -25,6 +25,7 @@
 #include "fa_ssim_mfma.h"
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace fa {
@@ -971,11 +972,71 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
                          out_per_image, out_total, nullptr, nullptr, st);
 }
 
+// ---------------------------------------------------------------------------
+// Fixed scratch for fa_gpu_ssim_noalloc: the float64 partial sums of one
+// call (N * C * slots per plane), in a file-scope device array.  Every GPU the
+// library runs on holds its own copy (8 MiB) until the process ends; calls on
+// one GPU share it, so calls that overlap on one GPU race.  No slot needs
+// clearing: every slot a launch's finalize reads was written by that launch.
+constexpr int64_t NOALLOC_SLOTS = FA_NOALLOC_SLOTS;
+__device__ __align__(256) double scratch[NOALLOC_SLOTS];
+
+namespace {
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::atomic<double*> g_scratch[NOALLOC_MAX_DEVICES];
+
+// The device address of the current device's `scratch`, asked once per device
+// (hipGetSymbolAddress with that device current) and kept.  The array's name
+// is a host-side stand-in in host code and is never passed to a kernel.
+int scratch_on_current_device(double** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return FA_E_ARG;
+  double* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    void* q = nullptr;
+    e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return -static_cast<int>(e);
+    if (q == nullptr) return FA_E_INTERNAL;
+    p = static_cast<double*>(q);
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return FA_OK;
+}
+
+}  // namespace
+
 }  // namespace fa
 
 using namespace fa;
 
 extern "C" {
+
+// No counterpart in the reference: fa_gpu_ssim without the `partial`
+// workspace, for callers that cannot allocate (see include/fa_abi.h).
+FA_API int fa_gpu_ssim_noalloc(const void* x, const void* y, int dtype, int N, int C, int H,
+                               int W, const float* win, int K, double shift, double C1,
+                               double C2, float* map_out, double* out_per_image,
+                               double* out_total, int device, void* stream) {
+  int Hout = 0, Wout = 0;
+  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  const int bpp = ssim_slots(Hout, Wout, K);
+  // host-side bound, before any HIP call: the launch below writes
+  // N * C * bpp slots of the scratch array
+  if (static_cast<int64_t>(N) * C * bpp > NOALLOC_SLOTS) return FA_E_SCRATCH;
+  double* partial = nullptr;
+  {
+    FA_DEVICE_SCOPE(device);
+    rc = scratch_on_current_device(&partial);
+    if (rc != FA_OK) return rc;
+  }
+  return ssim_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, win, K, shift, C1, C2,
+                   map_out, partial, bpp, out_per_image, out_total, device, stream);
+}
 
 // reference: fa_cuda.cu:1158-1165 (fa_cuda_ssim_workspace)
 FA_API int fa_gpu_ssim_workspace(int H, int W, int K, int* out_bpp) {

@@ -60,6 +60,9 @@ extern "C" {
 #define FA_E_ARG 5
 #define FA_E_INTERNAL 6
 #define FA_E_NOGPU 7
+/* No counterpart in the reference: fa_gpu_ssim_noalloc's fixed scratch is too
+ * small for the call (N * C * slots per plane > FA_NOALLOC_SLOTS). */
+#define FA_E_SCRATCH 8
 
 /* "not an MSE reduction, skip the dB conversion" (reference fa_abi.h:67) */
 #define FA_PSNR_NONE (-1.0e300)
@@ -320,6 +323,26 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials,
                                  const double* weights, int M, int N, int C,
                                  double* plane_scratch, double* out_per_image,
                                  double* out_total, int device, void* stream);
+
+/*
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc: fa_gpu_ssim (same arguments, same results, the same
+ * kernels) without the `partial` / `bpp` workspace.  The partial sums go to
+ * a fixed scratch array in the library, FA_NOALLOC_SLOTS float64 (8 MiB) per
+ * GPU, held by each GPU the library runs on until the process ends; the call
+ * itself allocates nothing.  A call needing more than N * C * (slots per
+ * plane, fa_gpu_ssim_workspace) > FA_NOALLOC_SLOTS returns FA_E_SCRATCH
+ * before touching the GPU (e.g. up to ~480 1080p planes at K = 11).
+ * Calls on one GPU share its scratch: calls that overlap on one GPU (two
+ * streams, two threads) race and must be serialised by the caller.
+ */
+#define FA_NOALLOC_SLOTS (1 << 20)
+FA_API int fa_gpu_ssim_noalloc(const void* x, const void* y, int dtype, int N,
+                               int C, int H, int W, const float* win, int K,
+                               double shift, double C1, double C2,
+                               float* map_out, double* out_per_image,
+                               double* out_total, int device, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

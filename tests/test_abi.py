@@ -39,7 +39,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 19  # 12 reference entry points + 7 extensions
+    assert len(decl) == 20  # 12 reference entry points + 8 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -165,3 +165,22 @@ def test_argument_validation_before_any_gpu_work(lib):
     assert lib.fa_gpu_ssim_cs_backward_ex(p, p, 3, p, p, p, 11, 1, 1, 64, 64, 0.5, 1e-4,
                                           9e-4, p, None, 1, p, p, None, 0,
                                           None) == 1  # float16 pyramid gradient
+
+
+def test_noalloc_bounds_its_scratch_on_the_host(lib):
+    """fa_gpu_ssim_noalloc rejects a call whose partial sums would not fit its
+    fixed scratch (FA_NOALLOC_SLOTS float64) before any HIP call: the checks
+    here run without a GPU, with null data pointers."""
+    slots = ctypes.c_int(0)
+    assert lib.fa_gpu_ssim_workspace(1080, 1920, 11, ctypes.byref(slots)) == 0
+    cap = 1 << 20
+    planes_max = cap // slots.value
+    args = (None, None, 0)
+    tail = (None, 11, 127.5, 6.5025, 58.5225, None, None, None, 0, None)
+    # one plane more than fits
+    assert lib.fa_gpu_ssim_noalloc(*args, planes_max + 1, 1, 1080, 1920, *tail) == 8
+    assert lib.fa_gpu_ssim_noalloc(*args, 1, planes_max + 1, 1080, 1920, *tail) == 8
+    assert b"scratch" in lib.fa_gpu_error_string(8)
+    # shape errors come first, as in fa_gpu_ssim
+    assert lib.fa_gpu_ssim_noalloc(*args, 1, 1, 8, 8, *tail) == 2
+    assert lib.fa_gpu_ssim_noalloc(*args, 1, 1, 64, 64, None, 12, *tail[2:]) == 3
