@@ -27,6 +27,8 @@ INCLUDE = REPO / "include"
 LIBDIR = PKG / "_lib"
 LIBNAME = "libfa_gpu.so"
 CPU_LIBNAME = "libfa_cpu.so"
+# measurement only: the read-bandwidth ceiling kernel bench.py reports
+READBW_LIBNAME = "libfa_readbw.so"
 
 
 def library_path() -> Path:
@@ -35,6 +37,10 @@ def library_path() -> Path:
 
 def cpu_library_path() -> Path:
     return LIBDIR / CPU_LIBNAME
+
+
+def readbw_library_path() -> Path:
+    return LIBDIR / READBW_LIBNAME
 
 
 def cpu_sources() -> List[Path]:
@@ -123,6 +129,11 @@ def build(verbose: bool = False, jobs: int = 0) -> Path:
         obj = objdir / (src.stem + ".o")
         objs.append(obj)
         cmds.append([cc, *flags, "-c", str(src), "-o", str(obj)])
+    # bench.py's read-bandwidth ceiling kernel, a library of its own
+    rb = readbw_library_path()
+    rb_tmp = rb.with_name(f".{rb.name}.{os.getpid()}.tmp")
+    cmds.append([cc, *flags, "-shared", *map(str, sorted((CSRC / "bench").glob("*.hip"))),
+                 "-o", str(rb_tmp)])
     n = jobs or min(len(cmds), max(1, os.cpu_count() or 1))
     with _cf.ThreadPoolExecutor(max_workers=n) as pool:
         for f in [pool.submit(_run, c, verbose) for c in cmds]:
@@ -133,6 +144,7 @@ def build(verbose: bool = False, jobs: int = 0) -> Path:
             *map(str, objs), "-o", str(tmp)]
     _run(link, verbose)
     os.replace(tmp, out)  # atomic: a concurrent loader never sees half a file
+    os.replace(rb_tmp, rb)
     return out
 
 

@@ -256,6 +256,28 @@ def test_gmsd_dword_path_edges(gpu, hw):
     assert _rel(float(fa.gms(x, y, data_range=255.0)), float(m[0])) <= REL
 
 
+def test_gmsd_configs4_full_batch(gpu):
+    """configs[4] GMSD at its real batch, 8x3x1080x1920 uint8, per channel and
+    grayscale through luma="bt601": image 0 against the oracle, every image by
+    per-image consistency with a one-image call."""
+    a, b = u8_pair((8, 3, 1080, 1920), 8.0, seed=1)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    for luma in (None, "bt601"):
+        kw = dict(data_range=255.0, luma=luma)
+        per = fa.gmsd(x, y, reduction="none", **kw).cpu().numpy()
+        a0, b0 = a[:1].astype(np.float64), b[:1].astype(np.float64)
+        if luma:
+            a0, b0 = ref.rgb_to_luma(a0, luma), ref.rgb_to_luma(b0, luma)
+        _, s0 = ref.gmsd_stats(a0, b0, 255.0)
+        assert _rel(float(per[0]), float(s0[0])) <= REL, (luma, per[0], s0)
+        # a one-image call splits the work differently, so its float32 group
+        # sums differ in the last bits: 1e-9 relative, well inside the bar
+        for i in (3, 7):
+            one = float(fa.gmsd(x[i:i + 1], y[i:i + 1], **kw))
+            assert abs(one - float(per[i])) <= 1e-9 * abs(one), (luma, i)
+        assert abs(float(fa.gmsd(x, y, **kw)) - float(per.mean())) <= 1e-12 * float(per.mean())
+
+
 def test_gmsd_identity(gpu):
     a, _ = _plane_pair()
     x = torch.as_tensor(a, dtype=torch.uint8, device=gpu)[None, None]
