@@ -6,14 +6,18 @@ kernels write -- scratch included -- is allocated here through torch's caching
 allocator, so no call ever allocates inside the library and every call stays
 legal inside a HIP graph capture (reference backend.py:145-153).
 
-Failure policy (deliberately stricter than the reference, which warns once and
-falls back to PyTorch, backend.py:215-224):
+Failure policy:
 
 * on a machine with a GPU the kernel library must load; if it cannot, the
-  first call raises.  ``FA_NATIVE=0`` is the explicit opt-out.
-* a kernel that returns a non-zero status raises :class:`KernelError`; there is
-  no silent retry on another path.
-* ``try_*`` return ``None`` only when the native path does not apply to the
+  first call raises (the reference would quietly run PyTorch instead).
+  ``FA_NATIVE=0`` is the explicit opt-out.
+* a kernel that declines an inference call (a non-zero status, raised as
+  :class:`KernelError`) makes its ``try_*`` warn once per distinct message
+  and return ``None``, so the call takes the portable path -- the reference's
+  behaviour (backend.py:213-224).  The differentiable entry points
+  (``ssim_fused``, ``ssim_cs_forward``, the backward passes) raise instead,
+  as the reference's do.
+* ``try_*`` also return ``None`` where the native path does not apply to the
   call by design (a gradient that the kernel cannot give, a window width
   without a kernel, a CPU tensor on a host without the CPU library); the
   caller then takes the portable path, exactly where the reference would.
@@ -30,6 +34,7 @@ from __future__ import annotations
 import ctypes
 import functools
 import os
+import warnings
 from collections import Counter
 from typing import Any, Optional
 
@@ -243,6 +248,20 @@ def _run(name: str, *args) -> None:
         raise KernelError(f"{name}: " + status_text(code, _ext.gpu if _ext else None))
 
 
+_declined_seen: set = set()
+
+
+def _declined(exc: KernelError) -> None:
+    """Warn (once per distinct message) that a kernel refused a call, which
+    then takes the portable path."""
+    key = str(exc)
+    if key in _declined_seen:
+        return
+    _declined_seen.add(key)
+    warnings.warn(f"frame_analytics_amd: a native kernel declined this call ({key}); "
+                  "computing it with the portable PyTorch path", RuntimeWarning, stacklevel=3)
+
+
 def _site(t: torch.Tensor):
     """``(device ordinal, hipStream_t)`` of the caller's current stream on the
     device of ``t``: kernels are enqueued where torch would enqueue its own."""
@@ -355,19 +374,23 @@ def try_pixel(x: torch.Tensor, y: torch.Tensor, *, op: int, param: float,
     """MSE / L1 / Charbonnier / Huber reduction (PSNR with ``psnr_bias``);
     ``None`` if no kernel applies."""
     bias = _PSNR_NONE if psnr_bias is None else float(psnr_bias)
-    if not x.is_cuda:
-        lib = _cpu_ready(x, y) if luma is None else None
-        if lib is None:
-            return None
-        out = pixel_cpu(lib, x, y, op=op, param=param, per_image=per_image, psnr_bias=bias)
-    else:
-        ext = _gpu_ext(x)
-        if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
-            return None
-        if luma is not None and x.shape[1] != 3:
-            return None
-        out = pixel_gpu(ext, x, y, op=op, param=param, per_image=per_image, psnr_bias=bias,
-                        luma=luma)
+    try:
+        if not x.is_cuda:
+            lib = _cpu_ready(x, y) if luma is None else None
+            if lib is None:
+                return None
+            out = pixel_cpu(lib, x, y, op=op, param=param, per_image=per_image, psnr_bias=bias)
+        else:
+            ext = _gpu_ext(x)
+            if ext is None or not _usable(x, y) or x.dim() != 4 or x.shape != y.shape:
+                return None
+            if luma is not None and x.shape[1] != 3:
+                return None
+            out = pixel_gpu(ext, x, y, op=op, param=param, per_image=per_image,
+                            psnr_bias=bias, luma=luma)
+    except KernelError as exc:
+        _declined(exc)
+        return None
     return out if dtype == torch.float64 else out.to(dtype)
 
 
@@ -461,6 +484,20 @@ def try_ssim(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
              shift: float, C1: float, C2: float, reduction: str,
              return_map: bool, dtype: torch.dtype,
              luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
+    """SSIM on the GPU (or the host library); ``None`` when the native path does
+    not apply or a kernel declined the call (warned once)."""
+    try:
+        return _ssim_native(x, y, win_size=win_size, sigma=sigma, shift=shift, C1=C1, C2=C2,
+                            reduction=reduction, return_map=return_map, dtype=dtype, luma=luma)
+    except KernelError as exc:
+        _declined(exc)
+        return None
+
+
+def _ssim_native(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: float,
+                 shift: float, C1: float, C2: float, reduction: str,
+                 return_map: bool, dtype: torch.dtype,
+                 luma: Optional[tuple] = None) -> Optional[torch.Tensor]:
     """SSIM on the GPU; ``None`` when the native path does not apply.
 
     Float64 input runs a float64 kernel.  A float64 *map* still takes the
@@ -641,7 +678,17 @@ def ssim_cs_pool(x, y, win, shift, C1, C2, pool_dtype, luma=None):
 
 def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
                 shift: float, C1: float, C2: float):
-    """``(ssim, cs)`` per plane, shaped ``(N, C)``; ``None`` if unavailable."""
+    """``(ssim, cs)`` per plane, shaped ``(N, C)``; ``None`` if unavailable or
+    a kernel declined the call (warned once)."""
+    try:
+        return _ssim_cs_native(x, y, win=win, shift=shift, C1=C1, C2=C2)
+    except KernelError as exc:
+        _declined(exc)
+        return None
+
+
+def _ssim_cs_native(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
+                    shift: float, C1: float, C2: float):
     k = int(win.numel())
     if x.shape[-2] < k or x.shape[-1] < k or k not in _WINDOWS:
         return None
@@ -670,6 +717,18 @@ def try_ssim_cs(x: torch.Tensor, y: torch.Tensor, *, win: torch.Tensor,
 
 def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsample: bool,
              luma: Optional[tuple] = None, want_map: bool = False):
+    """:func:`_gmsd_native`, or ``None`` when a kernel declined the call
+    (warned once)."""
+    try:
+        return _gmsd_native(x, y, T=T, eps=eps, downsample=downsample, luma=luma,
+                            want_map=want_map)
+    except KernelError as exc:
+        _declined(exc)
+        return None
+
+
+def _gmsd_native(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float,
+                 downsample: bool, luma: Optional[tuple] = None, want_map: bool = False):
     """``(gms_mean, gmsd)`` per image, float64 -- plus the float32 q map when
     ``want_map`` -- or ``None`` if unavailable.
 

@@ -145,3 +145,27 @@ def test_no_grad_still_reaches_the_native_kernel():
         assert backend._usable(x, y)
     with torch.inference_mode():
         assert backend._usable(x, y)
+
+
+def test_declined_kernel_warns_once_and_falls_back(monkeypatch):
+    """A kernel that returns a non-zero status makes the call warn once and
+    take the portable path, as the reference's backend does (backend.py:213-224)."""
+    import warnings
+
+    from frame_analytics_amd import backend
+
+    lib = backend.load_cpu()
+    if lib is None:
+        pytest.skip("host kernel library unavailable")
+    monkeypatch.setattr(lib, "fa_cpu_pixel_reduce", lambda *args: 5)
+    monkeypatch.setattr(backend, "_declined_seen", set())
+    g = torch.Generator().manual_seed(3)
+    x = torch.randint(0, 256, (2, 3, 20, 24), generator=g, dtype=torch.uint8)
+    y = torch.randint(0, 256, (2, 3, 20, 24), generator=g, dtype=torch.uint8)
+    want = ((x.double() - y.double()) ** 2).mean()
+    with pytest.warns(RuntimeWarning, match="declined"):
+        got = fa.mse(x, y)
+    assert abs(float(got) - float(want)) < 1e-9
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert abs(float(fa.mse(x, y)) - float(want)) < 1e-9  # warned once only

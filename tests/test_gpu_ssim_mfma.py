@@ -5,7 +5,8 @@ MFMA kernel, and so do the float32 levels of a uint8 MS-SSIM pyramid when the
 caller flags them (FA_DTYPE_U8_PYRAMID); everything else takes the vector-ALU
 strip kernel.  Both are held
 to the float64 oracle at the north star's bar (SSIM values within 1e-6
-relative; float32 map elements within 2e-5 absolute), and to each other:
+relative; float32 map elements within 2e-5 absolute, and the matrix-core
+kernel's own map within 1e-6 absolute), and to each other:
 ``FA_SSIM_MFMA=0`` in the environment selects the strip kernel for a call.
 """
 
@@ -24,7 +25,8 @@ from tests.conftest import natural_pair, u8_pair
 pytestmark = pytest.mark.gpu
 
 REL = 1e-6
-MAP_ABS = 2e-5
+MAP_ABS = 2e-5   # the reference-style gate for any float32 map
+MAP_TIGHT = 1e-6  # this kernel's own gate: window to 22 bits, H to 21, float32 epilogue
 
 
 def _rel(got, want):
@@ -60,7 +62,11 @@ def _check(a, b, gpu, win=11, sigma=1.5, L=255.0, K=(0.01, 0.03)):
         assert _rel(float(g), float(w)) <= REL, (a.shape, win, sigma, g, w)
     m = fa.ssim(x, y, return_map=True, **kw).double().cpu().numpy()
     assert m.shape == want_map.shape
-    assert float(np.abs(m - want_map).max()) <= MAP_ABS
+    err = float(np.abs(m - want_map).max())
+    assert err <= MAP_ABS
+    # per element, the matrix-core kernel stays within 1e-6 of float64: a lost
+    # low fp16 piece of the window or of H would show here, not at 2e-5
+    assert err <= MAP_TIGHT, (a.shape, win, sigma, err)
     with _VectorAlu():
         alu = fa.ssim(x, y, reduction="none", **kw).cpu().numpy()
     for g, w in zip(got, alu):
