@@ -348,6 +348,39 @@ def profile_sequence(launches=20):
     print("profile sequence done", flush=True)
 
 
+def trace_leg(name, steps, warmup):
+    """One training leg alone, for a kernel trace of its forward and backward
+    kernels (``--trace-leg``): ``configs3`` is 1 - ssim(x, y) on
+    16x3x256x256 float32, ``msssim_loss`` 1 - ms_ssim(x, y) on the configs[4]
+    frames as float32 in [0, 1].  Prints the step time."""
+    import torch
+
+    import frame_analytics_amd as fa
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    if name == "configs3":
+        x = torch.rand((16, 3, 256, 256), device=dev, generator=g)
+        y = (x + 0.05 * torch.randn(x.shape, device=dev, generator=g)).clamp(0, 1)
+        fn = fa.ssim
+    elif name == "msssim_loss":
+        a, b = _pairs(torch, SSIM_SHAPE, 8.0, 1, dev, seed=1)[0]
+        x, y = a.float() / 255.0, b.float() / 255.0
+        fn = fa.ms_ssim
+    else:
+        raise SystemExit(f"unknown leg {name!r}")
+    x.requires_grad_(True)
+
+    def step(i):
+        x.grad = None
+        (1.0 - fn(x, y, data_range=1.0)).backward()
+
+    _clock_warmup(torch, step, 0.3)
+    ms = _time_steps(torch, step, steps, warmup) / steps * 1e3
+    print(json.dumps({"leg": name, "steps": steps, "ms_per_step": round(ms, 4)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -359,9 +392,14 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile", action="store_true",
                     help="run the fixed launch sequence for rocprofv3 counters and exit")
+    ap.add_argument("--trace-leg", choices=("configs3", "msssim_loss"),
+                    help="run one training leg alone (for a kernel trace) and exit")
     args = ap.parse_args()
     if args.profile:
         profile_sequence()
+        return
+    if args.trace_leg:
+        trace_leg(args.trace_leg, args.steps, args.warmup)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
