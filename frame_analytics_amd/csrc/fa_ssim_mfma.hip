@@ -66,6 +66,9 @@ constexpr int MF_MAX_K = 16;           // 16 output rows + K - 1 <= 32 input row
 
 enum { MF_REDUCE = 0, MF_MAP = 1, MF_CS = 2 };
 
+// Buffer-resource word 3 for raw (untyped, unswizzled) access.
+constexpr int MF_RSRC_WORD3 = 0x00020000;
+
 struct MfArgs {
   const void* x;  // uint8 samples, or float samples of a uint8 pyramid level
   const void* y;
@@ -75,7 +78,8 @@ struct MfArgs {
   int TH, strips, tiles;
   const float* win;
   float C1, C2;
-  float one;  // 1.0f (see split_pair)
+  float one;      // 1.0f (see split_pair)
+  uint32_t pbias;  // 0x80008000 (see prep)
   float* map;
   double* partial;
   double* partial_cs;   // MF_CS
@@ -99,7 +103,7 @@ __device__ inline uint32_t pkfma(uint32_t bits, h2 m, h2 c) {
   return bc<uint32_t>(__builtin_elementwise_fma(bc<h2>(bits), m, c));
 }
 
-__device__ inline Frag prep(uint2 xa, uint2 ya) {
+__device__ inline Frag prep(uint2 xa, uint2 ya, uint32_t pbias) {
   u4 ox, oy, o3h, o3l, o4h, o4l;
   // t = 1024 + v (fp16 bit pattern 0x64vv, 0 <= v < 256):
   //   t * 2^-9 - 2.25 = (v - 128) 2^-9,  t * 2^-9 - 2 = v 2^-9,
@@ -128,9 +132,10 @@ __device__ inline Frag prep(uint2 xa, uint2 ya) {
     // (x-128)(y-128) in [-16256, 16384] = 256 q + l, l = low byte, q = high
     // byte as signed: adding 0x8000 (one v_pk_mad_u16 with the product) makes
     // the high byte q + 128 and leaves the low byte; (x-y)^2 <= 65025 splits
-    // the same way with q the plain high byte
-    const us2 k8000 = {0x8000, 0x8000};
-    const uint32_t p3s = bc<uint32_t>(xi * yi + k8000);
+    // the same way with q the plain high byte.  The 0x8000 pair comes in as a
+    // kernel argument: a literal would be folded into an exclusive or after
+    // the multiply, two instructions instead of one.
+    const uint32_t p3s = bc<uint32_t>(xi * yi + bc<us2>(pbias));
     const uint32_t p4 = bc<uint32_t>(d * d);
     o3l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3s, 0x04020400u), m, c0);
     o3h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3s, 0x04030401u), mq, cq128);
@@ -283,14 +288,16 @@ struct Raw<true> {
   float4 x0, x1, y0, y1;
 };
 
-__device__ inline Frag prep(const Raw<false>& r, float) { return prep(r.x, r.y); }
+__device__ inline Frag prep(const Raw<false>& r, float, uint32_t pbias) {
+  return prep(r.x, r.y, pbias);
+}
 
 // Pyramid levels of uint8 input: every sample is a multiple of 4^-s in
 // [0, 255] (s <= 4), so x' = x - 128 is exact in float32 and splits exactly
 // into fp16 hi + lo (at most 16 significant bits); x'y' and (x'-y')^2 are
 // formed in float32, as the strip kernel forms them, and split hi + lo (22
 // bits).  No scaling: the window's 2^9 is taken out of the sums (stash).
-__device__ inline Frag prep(const Raw<true>& r, float one) {
+__device__ inline Frag prep(const Raw<true>& r, float one, uint32_t) {
   const float xs[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
   const float ys[8] = {r.y0.x, r.y0.y, r.y0.z, r.y0.w, r.y1.x, r.y1.y, r.y1.z, r.y1.w};
   u4 ox, oxl, oy, oyl, o3h, o3l, o4h, o4l;
@@ -332,6 +339,7 @@ __device__ inline Frag prep(const Raw<true>& r, float one) {
 //   A2 = 2 (E x'y' - ux uy) + C2,  B2 = E (x'-y')^2 + A2 - (ux - uy)^2
 struct Epi {
   float k1, C2;
+  float k1s, c2s;  // 2^8 k1, 2^8 C2 (ssim_px_folded)
 };
 
 __device__ inline float ssim_px(const Epi& e, float U, float V, float X, float Q) {
@@ -343,6 +351,26 @@ __device__ inline float ssim_px(const Epi& e, float U, float V, float X, float Q
   const float B1 = fmaf(dd, du, A1);
   const float A2 = fmaf(0x1p-8f, X, fmaf(-0x1p-17f, p, e.C2));
   const float B2 = fmaf(-dd, du, fmaf(0x1p-9f, Q, A2));
+  return (A1 * A2) * __builtin_amdgcn_rcpf(B1 * B2);
+}
+
+// The same value with C2 folded into the vertical pass (the reduce kernel):
+// the x'y' sums start at 2^8 C2, the first MFMA's accumulator input, so
+// Xc = X + 2^8 C2, and A1, B1, A2, B2 are all taken times 2^8, which leaves
+// the ratio unchanged:
+//   A1' = 2^-9 U V + 2^7 (U + V) + 2^8 k1,  B1' = A1' + 2^-10 (U - V)^2
+//   A2' = Xc - 2^-9 U V,                     B2' = A2' + Q / 2 - 2^-10 (U - V)^2
+// One instruction fewer per pixel.  The map and CS kernels keep ssim_px:
+// they have no registers to spare for the four-wide accumulator input.
+__device__ inline float ssim_px_folded(const Epi& e, float U, float V, float Xc, float Q) {
+  const float p = U * V;
+  const float t = U + V;
+  const float du = U - V;
+  const float dd = du * 0x1p-10f;
+  const float A1 = fmaf(0x1p-9f, p, fmaf(128.0f, t, e.k1s));
+  const float B1 = fmaf(dd, du, A1);
+  const float A2 = fmaf(-0x1p-9f, p, Xc);
+  const float B2 = fmaf(-dd, du, fmaf(0.5f, Q, A2));
   return (A1 * A2) * __builtin_amdgcn_rcpf(B1 * B2);
 }
 
@@ -377,11 +405,12 @@ __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, 
       ssim_cs_px(e, o[0][i], o[1][i], o[2][i], o[3][i], s, cs);
       rs += ok ? s : 0.0f;
       rcs += ok ? cs : 0.0f;
-    } else {
+    } else if constexpr (MODE == MF_MAP) {
       const float s = ssim_px(e, o[0][i], o[1][i], o[2][i], o[3][i]);
-      if constexpr (MODE == MF_MAP) {
-        if (ok) map_px[static_cast<int64_t>(i) * Wout] = s;
-      }
+      if (ok) map_px[static_cast<int64_t>(i) * Wout] = s;
+      rs += ok ? s : 0.0f;
+    } else {
+      const float s = ssim_px_folded(e, o[0][i], o[1][i], o[2][i], o[3][i]);
       rs += ok ? s : 0.0f;
     }
   }
@@ -430,9 +459,11 @@ __device__ inline void pool_frag(const Pool& pl, int row0, uint32_t pcol, const 
   }
 }
 
-template <int PAR>
-__device__ inline void vblock(const Weights& w, const VState& v, f4* o) {
+// FOLD: the x'y' sums start at c2s (ssim_px_folded).
+template <int PAR, bool FOLD>
+__device__ inline void vblock(const Weights& w, const VState& v, f4* o, float c2s) {
   const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  const f4 zc = {c2s, c2s, c2s, c2s};
   h8 ah = w.eh, al = w.el;
   if constexpr (PAR == 1) {
     // the odd layout is the even one with its halves swapped, built here in
@@ -444,7 +475,7 @@ __device__ inline void vblock(const Weights& w, const VState& v, f4* o) {
     al = bc<h8>(u4{l[2], l[3], l[0], l[1]});
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.hi[q]), z);
+  for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.hi[q]), FOLD && q == 2 ? zc : z);
 #pragma unroll
   for (int q = 0; q < 4; ++q) o[q] = mfma(al, bc<h8>(v.hi[q]), o[q]);
 #pragma unroll
@@ -483,7 +514,8 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
     const uint32_t cc = static_cast<uint32_t>(min(c0 + 8 * g, a.W - 8));
     stage_window(a.win, a.K, swin[wave], lane);
     const Weights w = load_weights(swin[wave], g, n);
-    const Epi e = {2.0f * 128.0f * 128.0f + a.C1, a.C2};
+    const float k1 = 2.0f * 128.0f * 128.0f + a.C1;
+    const Epi e = {k1, a.C2, 256.0f * k1, 256.0f * a.C2};
     const bool col_ok = c0 + n < a.Wout;
     float* map_col = nullptr;
     if constexpr (MODE == MF_MAP)
@@ -510,30 +542,50 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
     }
     const uint32_t pcol = static_cast<uint32_t>(c0 / 2 + n);
 
-    // rows past the image only feed output rows past Hout: clamped.  load(j)
-    // is called for j = 0, 1, 2, ... in order, so the row offsets advance by
-    // 16 rows per call and are clamped to the last row's.
+    // Rows past the image only feed output rows past Hout.  load(j) is called
+    // for j = 0, 1, 2, ... in order, so the row offsets advance by 16 rows per
+    // call.  uint8 blocks are read through a buffer resource that starts at
+    // the block's first row and ends at the plane's end: its base and range
+    // are scalar values, the lane's offset within the block is fixed, so a
+    // load costs no vector instruction, and the range check turns rows past
+    // the image into zeros without touching memory.  Pyramid levels clamp
+    // their offsets to the last row.
+    const uint32_t xstep = MT * a.xsh, ystep = MT * a.ysh;
     const uint32_t rl = static_cast<uint32_t>(min(r0 + n, a.H - 1));
     const uint32_t xmax = static_cast<uint32_t>(a.H - 1) * a.xsh + cc;
     const uint32_t ymax = static_cast<uint32_t>(a.H - 1) * a.ysh + cc;
-    const uint32_t xstep = MT * a.xsh, ystep = MT * a.ysh;
     uint32_t xo = rl * a.xsh + cc, yo = rl * a.ysh + cc;  // block 0
+    const uint32_t vx = static_cast<uint32_t>(n) * a.xsh + cc;  // within the block
+    const uint32_t vy = static_cast<uint32_t>(n) * a.ysh + cc;
+    // plane bytes and the block's first byte; the host keeps (H + 48) rows of
+    // either plane below 2^31 bytes
+    const int ext_x = (a.H - 1) * static_cast<int>(a.xsh) + a.W;
+    const int ext_y = (a.H - 1) * static_cast<int>(a.ysh) + a.W;
+    int bx = r0 * static_cast<int>(a.xsh), by = r0 * static_cast<int>(a.ysh);
     auto load = [&](int, Raw<PYR>& r) {
       if constexpr (PYR) {
         r.x0 = *reinterpret_cast<const float4*>(xp + xo);
         r.x1 = *reinterpret_cast<const float4*>(xp + xo + 4);
         r.y0 = *reinterpret_cast<const float4*>(yp + yo);
         r.y1 = *reinterpret_cast<const float4*>(yp + yo + 4);
+        xo = min(xo + xstep, xmax);
+        yo = min(yo + ystep, ymax);
       } else {
-        r.x = *reinterpret_cast<const uint2*>(xp + xo);
-        r.y = *reinterpret_cast<const uint2*>(yp + yo);
+        const auto rx = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<E*>(xp + bx), 0, max(ext_x - bx, 0), MF_RSRC_WORD3);
+        const auto ry = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<E*>(yp + by), 0, max(ext_y - by, 0), MF_RSRC_WORD3);
+        const auto lx = __builtin_amdgcn_raw_buffer_load_b64(rx, vx, 0, 0);
+        const auto ly = __builtin_amdgcn_raw_buffer_load_b64(ry, vy, 0, 0);
+        r.x = uint2{lx[0], lx[1]};
+        r.y = uint2{ly[0], ly[1]};
+        bx += static_cast<int>(xstep);
+        by += static_cast<int>(ystep);
       }
-      xo = min(xo + xstep, xmax);
-      yo = min(yo + ystep, ymax);
     };
     // horizontal pass of block j (and its share of the pyramid)
     auto hpass = [&](int j, const Raw<PYR>& r) {
-      const Frag f = prep(r, a.one);
+      const Frag f = prep(r, a.one, a.pbias);
       if constexpr (MODE == MF_CS) {
         if (a.px) pool_frag<PYR>(pl, r0 + MT * j + 4 * g, pcol, f);  // uniform branch
       }
@@ -563,7 +615,7 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
       {
         stash_all<1, PYR>(hn, a.one, v);  // H_{b+1} next to H_b
         f4 o[4];
-        vblock<0>(w, v, o);
+        vblock<0, MODE == MF_REDUCE>(w, v, o, e.c2s);
         if (b + 2 <= nb) {  // uniform
           hn = hpass(b + 2, raw);
           load(b + 3, raw);
@@ -573,7 +625,7 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
       if (b + 1 < nb) {
         stash_all<0, PYR>(hn, a.one, v);  // H_{b+2} over H_b
         f4 o[4];
-        vblock<1>(w, v, o);
+        vblock<1, MODE == MF_REDUCE>(w, v, o, e.c2s);
         if (b + 3 <= nb) {
           hn = hpass(b + 3, raw);
           load(b + 4, raw);
@@ -632,6 +684,9 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   const int64_t s[6] = {c.xsn, c.xsc, c.ysn, c.ysc, c.xsh, c.ysh};
   for (int64_t v : s)
     if (v % 8 != 0) return FA_OK;
+  // 32-bit offsets within a plane: the uint8 loads run up to 47 rows past
+  // the last output row (their range check stops them at the plane's end)
+  if ((static_cast<int64_t>(c.H) + 48) * std::max(c.xsh, c.ysh) > INT32_MAX) return FA_OK;
 
   MfArgs a = {};
   a.x = c.x;
@@ -652,6 +707,7 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   a.C1 = static_cast<float>(c.C1);
   a.C2 = static_cast<float>(c.C2);
   a.one = 1.0f;
+  a.pbias = 0x80008000u;
   a.map = c.map;
   a.partial = c.partial;
   a.partial_cs = c.partial_cs;
