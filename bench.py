@@ -80,6 +80,9 @@ def _time_steps(torch, fn, steps, warmup):
     return time.perf_counter() - t0
 
 
+LEG_WARMUP_S = 0.2  # untimed calls before each secondary leg
+
+
 def _clock_warmup(torch, fn, seconds):
     """Run ``fn`` back to back for ``seconds`` of wall time (untimed).  The
     MI355X raises its clock over ~40 ms (~400 launches of the SSIM kernel) of
@@ -461,9 +464,13 @@ def main():
             ("gmsd_ms", lambda i: fa.gmsd(*pairs[i % 4], data_range=255.0)),
             ("gmsd_luma_bt601_ms",
              lambda i: fa.gmsd(*pairs[i % 4], data_range=255.0, luma="bt601"))):
+        # each leg raises the clock itself: between the legs it may drop
+        _clock_warmup(torch, fn, LEG_WARMUP_S)
         c4[key] = round(_time_steps(torch, fn, reps, 5) / reps * 1e3, 4)
     c4["gmsd_GBps"] = round(2.0 * samples / (c4["gmsd_ms"] * 1e-3) / 1e9, 1)
-    c4["l1_ms"] = round(_time_steps(torch, lambda i: fa.l1(*pairs[i % 4]), reps, 5) / reps * 1e3, 4)
+    l1_fn = lambda i: fa.l1(*pairs[i % 4])  # noqa: E731
+    _clock_warmup(torch, l1_fn, LEG_WARMUP_S)
+    c4["l1_ms"] = round(_time_steps(torch, l1_fn, reps, 5) / reps * 1e3, 4)
     del partial
     # MS-SSIM as a training loss (the reference's bench_training.py:172-200 step):
     # x = frames / 255 in float32 with requires_grad, loss = 1 - ms_ssim, backward
@@ -477,6 +484,7 @@ def main():
         (1.0 - fa.ms_ssim(xl, yl, data_range=1.0)).backward()
 
     lreps = max(5, reps // 4)
+    _clock_warmup(torch, msssim_loss_step, LEG_WARMUP_S)
     c4["ms_ssim_loss_fwd_bwd_fp32_ms"] = round(
         _time_steps(torch, msssim_loss_step, lreps, 2) / lreps * 1e3, 3)
     del xl, yl
@@ -496,6 +504,7 @@ def main():
         x3.grad = None
         (1.0 - fa.ssim(x3, y3, data_range=1.0)).backward()
 
+    _clock_warmup(torch, loss_step, LEG_WARMUP_S)
     c3_ms = _time_steps(torch, loss_step, reps, 5) / reps * 1e3
     del x3, y3
 
@@ -508,6 +517,7 @@ def main():
         a, b = ppairs[i % len(ppairs)]
         return fa.psnr(a, b, data_range=255.0)
 
+    _clock_warmup(torch, psnr_step, LEG_WARMUP_S)
     p_el = _time_steps(torch, psnr_step, args.steps, args.warmup)
     p_ms = p_el / args.steps * 1e3
     pbytes = 2.0 * ppairs[0][0].numel()
@@ -539,7 +549,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic uint8 (BASELINE.json generator, 4 resident pairs rotated); "
                 f"{args.clock_warmup:g} s clock warm-up ({warm_calls} untimed steps) before "
-                "the warm-up steps",
+                f"the warm-up steps; {LEG_WARMUP_S:g} s of untimed calls before each "
+                "secondary leg",
         "config": {"workload": "ssim_fwd 8x3x1080x1920 uint8, reduction=mean, 11x11 gaussian",
                    "batch": n, "channels": c, "height": h, "width": w},
         "roofline": {
