@@ -385,9 +385,10 @@ __device__ inline void ssim_cs_px(const Epi& e, float U, float V, float X, float
   const float B1 = fmaf(dd, du, A1);
   const float A2 = fmaf(0x1p-8f, X, fmaf(-0x1p-17f, p, e.C2));
   const float B2 = fmaf(-dd, du, fmaf(0x1p-9f, Q, A2));
-  const float inv = __builtin_amdgcn_rcpf(B1 * B2);
-  s = (A1 * A2) * inv;
-  cs = (A2 * B1) * inv;
+  // u = A2 / (B1 B2): ssim = A1 u, cs = B1 u
+  const float u = A2 * __builtin_amdgcn_rcpf(B1 * B2);
+  s = A1 * u;
+  cs = B1 * u;
 }
 
 // Adds this lane's four outputs (rows row0 .. row0 + 3 of its column) to the
