@@ -431,7 +431,7 @@ struct Pool {
   int64_t off;   // this plane's first element
   int Wd;        // level width, floor(W / 2)
   int row_end;   // first input row this chunk does not pool
-  bool lane_on;  // pooled column c0/2 + n is this wave's and lies in the level
+  bool lane_on;  // this lane stores pooled column c0/2 + n (inside the level)
   h8 pm;         // the column-pair matrix fragment
 };
 
@@ -522,12 +522,14 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
     if constexpr (MODE == MF_MAP)
       map_col = a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout + c0 + n;
 
-    // The pyramid level: a wave pools the input columns of its own 16 output
-    // columns (pooled columns c0/2 .. c0/2 + 7); the last active wave of a row
-    // also pools the rest of its window up to the image edge, which covers
-    // the columns of the waves past Wout (W <= c0 + 16 + K - 1 there).  Rows:
-    // this chunk's TH input rows, and in the last chunk everything up to
-    // 2 floor(H / 2).  Every row the chunk pools lies in one of its H blocks.
+    // The pyramid level: a wave's 32-column window pools to 16 columns, its
+    // own 8 (c0/2 .. c0/2 + 7) and its right neighbour's 8.  Even waves store
+    // all 16 (64 contiguous bytes per level row), odd waves none; the last
+    // active wave of a row, even or odd, stores its 16 up to the image edge,
+    // which covers the columns of the waves past Wout (W <= c0 + 16 + K - 1
+    // there).  Rows: this chunk's TH input rows, and in the last chunk
+    // everything up to 2 floor(H / 2).  Every row the chunk pools lies in one
+    // of its H blocks.
     Pool pl = {};
     if constexpr (MODE == MF_CS) {
       pl.px = a.px;
@@ -536,7 +538,7 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
       pl.off = static_cast<int64_t>(plane) * (a.H / 2) * pl.Wd;
       pl.row_end = r0 + a.TH >= a.Hout ? 2 * (a.H / 2) : r0 + a.TH;
       const bool last_wave = c0 + MT >= a.Wout;
-      pl.lane_on = a.px != nullptr && (n < 8 || last_wave) && c0 / 2 + n < pl.Wd;
+      pl.lane_on = a.px != nullptr && ((wave & 1) == 0 || last_wave) && c0 / 2 + n < pl.Wd;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         pl.pm[i] = static_cast<_Float16>(((8 * g + i) >> 1) == n ? 1.0f : 0.0f);
