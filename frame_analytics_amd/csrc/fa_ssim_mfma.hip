@@ -16,11 +16,12 @@
 //       8g .. 8g+7 of the wave's 32-column window (one 8-byte load of x, one
 //       of y), turned into exact fp16 operands:
 //         x' and y' (integers in [-128, 127]),
-//         x'y' = 256 q3 + l3 with q3 in [-64, 64], l3 in [0, 255],
-//         (x-y)^2 = 256 q4 + l4 with q4 in [0, 254], l4 in [0, 255],
-//       built with v_perm_b32, packed 16-bit integer arithmetic and fp16 bit
-//       patterns (0x64vv is 1024 + v), x', y', l scaled by 2^-9 and q by
-//       256 * 2^-9, all exactly.
+//         x'y' = p3h + p3l and (x-y)^2 = p4h + p4l: the fp16 rounding of the
+//         product (v_pk_mul_f16) and its remainder (v_pk_fma_f16 of the same
+//         operands minus the rounded product, exact: an integer of at most
+//         4 or 16 units),
+//       built with v_perm_b32 and packed fp16 arithmetic on the bit patterns
+//       0x64vv = 1024 + v, every plane scaled by 2^-9, all exactly.
 //   B = the window scaled by 2^9 and split into fp16 hi + lo pieces (the scale
 //       keeps the low piece of the smallest Gaussian weight normal).  The
 //       scales cancel, products of fp16 operands are exact and accumulate in
@@ -53,7 +54,6 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 template <class To, class From>
 __device__ inline To bc(From v) {
@@ -79,7 +79,6 @@ struct MfArgs {
   const float* win;
   float C1, C2;
   float one;      // 1.0f (see split_pair)
-  uint32_t pbias;  // 0x80008000 (see prep)
   float* map;
   double* partial;
   double* partial_cs;   // MF_CS
@@ -92,63 +91,55 @@ __device__ inline f4 mfma(h8 a, h8 b, f4 c) {
 }
 
 // The six fp16 A fragments of one lane's 8 pixels of x and y: the planes
-// x', y', l3, l4 scaled by 2^-9 and q3, q4 by 256 * 2^-9 (exact: small
-// integers times powers of two), so one set of weights serves all six.
+// x', y', and the hi + lo pieces of x'y' and (x' - y')^2, all scaled by 2^-9
+// (exact: small integers times powers of two, and remainders that are
+// multiples of 2^-9), so one set of weights serves all six.
 struct Frag {
-  h8 x, y, q3, l3, q4, l4;
+  h8 x, y, p3h, p3l, p4h, p4l;
   h8 xl, yl;  // pyramid levels only: the low fp16 pieces of x', y'
 };
 
-__device__ inline uint32_t pkfma(uint32_t bits, h2 m, h2 c) {
-  return bc<uint32_t>(__builtin_elementwise_fma(bc<h2>(bits), m, c));
-}
-
-__device__ inline Frag prep(uint2 xa, uint2 ya, uint32_t pbias) {
+__device__ inline Frag prep(uint2 xa, uint2 ya) {
   u4 ox, oy, o3h, o3l, o4h, o4l;
   // t = 1024 + v (fp16 bit pattern 0x64vv, 0 <= v < 256):
-  //   t * 2^-9 - 2.25 = (v - 128) 2^-9,  t * 2^-9 - 2 = v 2^-9,
-  //   t / 2 - 576 = (v - 128) / 2,       t / 2 - 512 = v / 2
+  //   t * 2^-9 - 2.25 = (v - 128) 2^-9,  t - 1152 = v - 128
   const h2 m = {static_cast<_Float16>(0x1p-9f), static_cast<_Float16>(0x1p-9f)};
   const h2 c128 = {static_cast<_Float16>(-2.25f), static_cast<_Float16>(-2.25f)};
-  const h2 c0 = {static_cast<_Float16>(-2.0f), static_cast<_Float16>(-2.0f)};
-  const h2 mq = {static_cast<_Float16>(0.5f), static_cast<_Float16>(0.5f)};
-  const h2 cq128 = {static_cast<_Float16>(-576.0f), static_cast<_Float16>(-576.0f)};
-  const h2 cq0 = {static_cast<_Float16>(-512.0f), static_cast<_Float16>(-512.0f)};
-  const us2 k6480 = {0x6480, 0x6480};
+  const h2 k1152 = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t xw = j < 2 ? xa.x : xa.y;
     const uint32_t yw = j < 2 ? ya.x : ya.y;
     // v_perm_b32 picks bytes of {S0 : S1}: 0-3 from S1, 4-7 from S0
     const uint32_t sf = (j & 1) ? 0x04030402u : 0x04010400u;  // two bytes under 0x64
-    const uint32_t xt = __builtin_amdgcn_perm(0x64646464u, xw, sf);
-    const uint32_t yt = __builtin_amdgcn_perm(0x64646464u, yw, sf);
-    ox[j] = pkfma(xt, m, c128);
-    oy[j] = pkfma(yt, m, c128);
-    // 16-bit integers: x - 128, y - 128 and x - y from the same patterns
-    const us2 xi = bc<us2>(xt) - k6480;
-    const us2 yi = bc<us2>(yt) - k6480;
-    const us2 d = bc<us2>(xt) - bc<us2>(yt);
-    // (x-128)(y-128) in [-16256, 16384] = 256 q + l, l = low byte, q = high
-    // byte as signed: adding 0x8000 (one v_pk_mad_u16 with the product) makes
-    // the high byte q + 128 and leaves the low byte; (x-y)^2 <= 65025 splits
-    // the same way with q the plain high byte.  The 0x8000 pair comes in as a
-    // kernel argument: a literal would be folded into an exclusive or after
-    // the multiply, two instructions instead of one.
-    const uint32_t p3s = bc<uint32_t>(xi * yi + bc<us2>(pbias));
-    const uint32_t p4 = bc<uint32_t>(d * d);
-    o3l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3s, 0x04020400u), m, c0);
-    o3h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p3s, 0x04030401u), mq, cq128);
-    o4l[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04020400u), m, c0);
-    o4h[j] = pkfma(__builtin_amdgcn_perm(0x64646464u, p4, 0x04030401u), mq, cq0);
+    const h2 xt = bc<h2>(__builtin_amdgcn_perm(0x64646464u, xw, sf));
+    const h2 yt = bc<h2>(__builtin_amdgcn_perm(0x64646464u, yw, sf));
+    const h2 xs = __builtin_elementwise_fma(xt, m, c128);  // x' 2^-9
+    const h2 ys = __builtin_elementwise_fma(yt, m, c128);  // y' 2^-9
+    const h2 xu = xt + k1152;                              // x'
+    const h2 du = xt - yt;                                 // x' - y'
+    const h2 ds = xs - ys;                                 // (x' - y') 2^-9
+    // x'y' 2^-9 in [-31.75, 32] and (x'-y')^2 2^-9 in [0, 127]: the product
+    // rounded to fp16, then the exact remainder from a fused multiply-add of
+    // the same operands (an integer of at most 4, resp. 16, units of 2^-9)
+    const h2 p3h = xu * ys;
+    const h2 p3l = __builtin_elementwise_fma(xu, ys, -p3h);
+    const h2 p4h = du * ds;
+    const h2 p4l = __builtin_elementwise_fma(du, ds, -p4h);
+    ox[j] = bc<uint32_t>(xs);
+    oy[j] = bc<uint32_t>(ys);
+    o3h[j] = bc<uint32_t>(p3h);
+    o3l[j] = bc<uint32_t>(p3l);
+    o4h[j] = bc<uint32_t>(p4h);
+    o4l[j] = bc<uint32_t>(p4l);
   }
   Frag f;
   f.x = bc<h8>(ox);
   f.y = bc<h8>(oy);
-  f.q3 = bc<h8>(o3h);
-  f.l3 = bc<h8>(o3l);
-  f.q4 = bc<h8>(o4h);
-  f.l4 = bc<h8>(o4l);
+  f.p3h = bc<h8>(o3h);
+  f.p3l = bc<h8>(o3l);
+  f.p4h = bc<h8>(o4h);
+  f.p4l = bc<h8>(o4l);
   return f;
 }
 
@@ -249,20 +240,20 @@ __device__ inline HAcc hmfma(const Frag& f, const Weights& w) {
   HAcc h;
   h.x = mfma(f.x, w.bh, z);
   h.y = mfma(f.y, w.bh, z);
-  h.p3 = mfma(f.q3, w.bh, z);
-  h.p4 = mfma(f.q4, w.bh, z);
+  h.p3 = mfma(f.p3h, w.bh, z);
+  h.p4 = mfma(f.p4h, w.bh, z);
   h.x = mfma(f.x, w.bl, h.x);
   h.y = mfma(f.y, w.bl, h.y);
-  h.p3 = mfma(f.q3, w.bl, h.p3);
-  h.p4 = mfma(f.q4, w.bl, h.p4);
-  h.p3 = mfma(f.l3, w.bh, h.p3);
-  h.p4 = mfma(f.l4, w.bh, h.p4);
+  h.p3 = mfma(f.p3h, w.bl, h.p3);
+  h.p4 = mfma(f.p4h, w.bl, h.p4);
+  h.p3 = mfma(f.p3l, w.bh, h.p3);
+  h.p4 = mfma(f.p4l, w.bh, h.p4);
   if constexpr (PYR) {
     h.x = mfma(f.xl, w.bh, h.x);
     h.y = mfma(f.yl, w.bh, h.y);
   } else {
-    h.p3 = mfma(f.l3, w.bl, h.p3);
-    h.p4 = mfma(f.l4, w.bl, h.p4);
+    h.p3 = mfma(f.p3l, w.bl, h.p3);
+    h.p4 = mfma(f.p4l, w.bl, h.p4);
   }
   return h;
 }
@@ -288,8 +279,8 @@ struct Raw<true> {
   float4 x0, x1, y0, y1;
 };
 
-__device__ inline Frag prep(const Raw<false>& r, float, uint32_t pbias) {
-  return prep(r.x, r.y, pbias);
+__device__ inline Frag prep(const Raw<false>& r, float) {
+  return prep(r.x, r.y);
 }
 
 // Pyramid levels of uint8 input: every sample is a multiple of 4^-s in
@@ -297,7 +288,7 @@ __device__ inline Frag prep(const Raw<false>& r, float, uint32_t pbias) {
 // into fp16 hi + lo (at most 16 significant bits); x'y' and (x'-y')^2 are
 // formed in float32, as the strip kernel forms them, and split hi + lo (22
 // bits).  No scaling: the window's 2^9 is taken out of the sums (stash).
-__device__ inline Frag prep(const Raw<true>& r, float one, uint32_t) {
+__device__ inline Frag prep(const Raw<true>& r, float one) {
   const float xs[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
   const float ys[8] = {r.y0.x, r.y0.y, r.y0.z, r.y0.w, r.y1.x, r.y1.y, r.y1.z, r.y1.w};
   u4 ox, oxl, oy, oyl, o3h, o3l, o4h, o4l;
@@ -325,10 +316,10 @@ __device__ inline Frag prep(const Raw<true>& r, float one, uint32_t) {
   f.xl = bc<h8>(oxl);
   f.y = bc<h8>(oy);
   f.yl = bc<h8>(oyl);
-  f.q3 = bc<h8>(o3h);
-  f.l3 = bc<h8>(o3l);
-  f.q4 = bc<h8>(o4h);
-  f.l4 = bc<h8>(o4l);
+  f.p3h = bc<h8>(o3h);
+  f.p3l = bc<h8>(o3l);
+  f.p4h = bc<h8>(o4h);
+  f.p4l = bc<h8>(o4l);
   return f;
 }
 
@@ -588,7 +579,7 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
     };
     // horizontal pass of block j (and its share of the pyramid)
     auto hpass = [&](int j, const Raw<PYR>& r) {
-      const Frag f = prep(r, a.one, a.pbias);
+      const Frag f = prep(r, a.one);
       if constexpr (MODE == MF_CS) {
         if (a.px) pool_frag<PYR>(pl, r0 + MT * j + 4 * g, pcol, f);  // uniform branch
       }
@@ -710,7 +701,6 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   a.C1 = static_cast<float>(c.C1);
   a.C2 = static_cast<float>(c.C2);
   a.one = 1.0f;
-  a.pbias = 0x80008000u;
   a.map = c.map;
   a.partial = c.partial;
   a.partial_cs = c.partial_cs;
