@@ -591,8 +591,9 @@ def _cs_launch(x, y, win, shift, C1, C2, *, pool_dtype=None, luma=None, reduce=T
         py = torch.empty_like(px)
     code = _DTYPE_CODE[x.dtype]
     if u8_pyramid:
-        if x.dtype != torch.float32 or luma is not None:
-            raise ValueError("u8_pyramid needs float32 levels without luma")
+        if x.dtype not in (torch.float32, torch.float16) or luma is not None:
+            raise ValueError("u8_pyramid needs float32 (or first-level float16) levels "
+                             "without luma")
         code |= FA_DTYPE_U8_PYRAMID
     head = (_ptr(x), _ptr(y), code, n, c, h, w)
     consts = (_ptr(win), k, float(shift), float(C1), float(C2), _ptr(partial),
@@ -614,7 +615,8 @@ def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None, u8_pyramid
     maps (``slots`` per plane, packed), the plane's output pixel count, and the
     next pyramid level (``None`` at the coarsest scale).  The partial sums go
     to :func:`ms_ssim_reduce`; nothing is synchronised.  ``u8_pyramid``: x and
-    y are float32 levels of a uint8 pyramid (FA_DTYPE_U8_PYRAMID)."""
+    y are levels of a uint8 pyramid (FA_DTYPE_U8_PYRAMID): float32, or the
+    first level in float16, where its quarter samples are exact."""
     _, _, ps, pcs, slots, px, py = _cs_launch(x, y, win, shift, C1, C2, pool_dtype=pool_dtype,
                                               luma=luma, reduce=False, u8_pyramid=u8_pyramid)
     k = int(win.numel())

@@ -117,7 +117,8 @@ struct SsimArgs {
   float* oty;
   void* px;             // MODE_CS: optional pyramid step (2x2 means of x / y)
   void* py;
-  int pool_f64;         // pyramid element type: float64 (1) or float32 (0)
+  int pool_f64;         // pyramid element type: float64 (1) or float32 (0),
+  int pool_f16;         //   or float16 (uint8 input without luma only)
   // input views (forward modes): element strides of image and channel, row
   // stride; columns are contiguous.  Planes are (image, output channel).
   int64_t xsn, xsc, ysn, ysc;
@@ -166,7 +167,7 @@ struct SsimPol {
   // on even lanes, the column pair starting at its column (pcol = col / 2)
   void* px;
   void* py;
-  bool pool_on, pool_f64, pcol_ok;
+  bool pool_on, pool_f64, pool_f16, pcol_ok;
   int prow0, prow1, Wd;
   int64_t pool_off;
   uint32_t pcol;
@@ -216,8 +217,14 @@ struct SsimPol {
           static_cast<double*>(px)[o] = fma(0.25, static_cast<double>(sx), poff);
           static_cast<double*>(py)[o] = fma(0.25, static_cast<double>(sy), poff);
         } else if constexpr (std::is_same<PA, float>::value) {
-          static_cast<float*>(px)[o] = PA(0.25) * sx;  // poff is 0 without luma
-          static_cast<float*>(py)[o] = PA(0.25) * sy;
+          // poff is 0 without luma; a quarter of a byte sum is exact in float16
+          if (pool_f16) {
+            static_cast<_Float16*>(px)[o] = static_cast<_Float16>(PA(0.25) * sx);
+            static_cast<_Float16*>(py)[o] = static_cast<_Float16>(PA(0.25) * sy);
+          } else {
+            static_cast<float*>(px)[o] = PA(0.25) * sx;
+            static_cast<float*>(py)[o] = PA(0.25) * sy;
+          }
         } else {
           static_cast<float*>(px)[o] = static_cast<float>(fma(0.25, sx, poff));
           static_cast<float*>(py)[o] = static_cast<float>(fma(0.25, sy, poff));
@@ -399,6 +406,7 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
       const int cend = last_strip ? 2 * (a.W / 2) : c0 + OUTW;
       pol.pool_on = true;
       pol.pool_f64 = a.pool_f64 != 0;
+      pol.pool_f16 = a.pool_f16 != 0;
       pol.prow0 = r0;
       pol.prow1 = last_chunk ? 2 * Hd : r0 + a.TH;
       pol.Wd = a.W / 2;
@@ -857,11 +865,12 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
                         double* out_cs, int* out_slots, void* px, void* py, int pool_dtype,
                         int device, void* stream) {
   if (!x || !y || !win || !partial || !partial_cs) return FA_E_ARG;
-  // FA_DTYPE_U8_PYRAMID: float32 samples of a uint8 pyramid level (a hint
-  // that admits the matrix-core kernel; the strip kernel reads plain float32)
+  // FA_DTYPE_U8_PYRAMID: float32 samples of a uint8 pyramid level, or
+  // float16 samples of its first level (a hint that admits the matrix-core
+  // kernel; the strip kernel reads plain float32 / float16)
   const bool u8_pyramid = (dtype & FA_DTYPE_U8_PYRAMID) != 0;
   dtype &= ~FA_DTYPE_U8_PYRAMID;
-  if (u8_pyramid && dtype != FA_F32) return FA_E_DTYPE;
+  if (u8_pyramid && dtype != FA_F32 && dtype != FA_F16) return FA_E_DTYPE;
   // plane means, or (both null) the partial sums left for fa_gpu_ms_ssim_reduce
   if ((out_s == nullptr) != (out_cs == nullptr)) return FA_E_ARG;
   if (!out_s && !out_slots) return FA_E_ARG;
@@ -892,13 +901,18 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
   a.px = px;
   a.py = py;
   a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
+  a.pool_f16 = pool_dtype == FA_F16 ? 1 : 0;
   int tiles = 0;
-  if ((dtype == FA_U8 || u8_pyramid) && !luma && (!px || pool_dtype == FA_F32)) {
-    // uint8 planes and the float32 levels of their pyramid: the matrix-core
-    // kernel when the layout allows (fa_ssim_mfma.hip), next level included
-    const SsimMfmaCall mc = {x, y, u8_pyramid, a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh,
+  if ((dtype == FA_U8 || u8_pyramid) && !luma &&
+      (!px || pool_dtype == FA_F32 || pool_dtype == FA_F16)) {
+    // uint8 planes and the levels of their pyramid: the matrix-core kernel
+    // when the layout allows (fa_ssim_mfma.hip), next level included
+    const int src = !u8_pyramid        ? SsimMfmaCall::U8
+                    : dtype == FA_F16 ? SsimMfmaCall::F16_LEVEL
+                                      : SsimMfmaCall::F32_LEVEL;
+    const SsimMfmaCall mc = {x, y, src, a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh,
                              N, C, H, W, Hout, Wout, K, win, C1, C2, nullptr, partial, bpp,
-                             partial_cs, static_cast<float*>(px), static_cast<float*>(py)};
+                             partial_cs, px, py, px != nullptr && pool_dtype == FA_F16};
     rc = ssim_mfma(mc, device, st, &tiles);
     if (rc != FA_OK) return rc;
   }
@@ -952,9 +966,9 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
   if (dtype == FA_U8 && !lm) {
     // uint8 planes: both Gaussian passes on the matrix cores when the layout
     // allows (fa_ssim_mfma.hip); otherwise the strip kernel below
-    const SsimMfmaCall mc = {x, y, false, a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh,
+    const SsimMfmaCall mc = {x, y, SsimMfmaCall::U8, a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh,
                              N, C, H, W, Hout, Wout, K, win, C1, C2, map_out, partial, bpp,
-                             nullptr, nullptr, nullptr};
+                             nullptr, nullptr, nullptr, false};
     rc = ssim_mfma(mc, device, st, &tiles);
     if (rc != FA_OK) return rc;
   }
@@ -1093,11 +1107,15 @@ FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N, int
                              int bpp, double* out_s, double* out_cs, int* out_slots,
                              void* px, void* py, int pool_dtype, int device, void* stream) {
   if (px) {
-    // float32 levels hold the pyramid of uint8 input exactly, float64 levels
-    // that of every floating input; a luma plane pools into float64
+    // float32 levels hold the pyramid of uint8 input exactly (and so do
+    // float16 levels its first level, multiples of 1/4 in [0, 255]); float64
+    // levels that of every floating input; a luma plane pools into float64
     const int base = dtype & ~FA_DTYPE_U8_PYRAMID;
+    const bool u8p = (dtype & FA_DTYPE_U8_PYRAMID) != 0;
     const bool ok = pool_dtype == FA_F64 ||
-                    (pool_dtype == FA_F32 && !luma && (base == FA_U8 || base == FA_F32));
+                    (pool_dtype == FA_F32 && !luma &&
+                     (base == FA_U8 || base == FA_F32 || (u8p && base == FA_F16))) ||
+                    (pool_dtype == FA_F16 && !luma && base == FA_U8);
     if (!ok) return FA_E_DTYPE;
   }
   return ssim_cs_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, win, K, shift, C1,

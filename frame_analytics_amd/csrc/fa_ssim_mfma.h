@@ -6,11 +6,16 @@
 namespace fa {
 
 // One fa_gpu_ssim(_ex) / fa_gpu_ssim_cs(_ex) call over uint8 planes without
-// luma, or (pyr) over float32 planes of a uint8 input's 2 x 2 pyramid.
+// luma, or (CS pass only) over the planes of a uint8 input's 2 x 2 pyramid.
 struct SsimMfmaCall {
+  enum Src {
+    U8 = 0,         // uint8 samples
+    F32_LEVEL = 1,  // float32 samples, multiples of 4^-s in [0, 255], s <= 4
+    F16_LEVEL = 2,  // float16 samples, multiples of 1/4 in [0, 255] (level 1)
+  };
   const void* x;
   const void* y;
-  bool pyr;                    // float32 samples, multiples of 4^-s in [0, 255], s <= 4
+  int src;                     // Src
   int64_t xsn, xsc, ysn, ysc;  // image and channel strides (elements)
   int xsh, ysh;                // row strides
   int N, C, H, W, Hout, Wout, K;
@@ -21,14 +26,16 @@ struct SsimMfmaCall {
   int bpp;
   // MS-SSIM's CS pass (partial_cs non-null): per-plane sums of SSIM and of
   // cs = A2 / B2, and optionally the next pyramid level, the 2 x 2 means of x
-  // and y (float32, floor(H/2) x floor(W/2) per plane) into px / py
+  // and y (floor(H/2) x floor(W/2) per plane) into px / py: float32, or
+  // float16 when level_f16 (uint8 input only: quarter samples are exact)
   double* partial_cs;
-  float* px;
-  float* py;
+  void* px;
+  void* py;
+  bool level_f16;
 };
 
 // Launches the matrix-core SSIM forward (or CS pass) when the call fits it
-// (rows and planes aligned to 8 samples, 8-byte (uint8) or 16-byte (float)
+// (rows and planes aligned to 8 samples, 8-byte (uint8) or 16-byte (levels)
 // aligned bases, K <= 16, enough partial slots, 16-byte aligned pyramid
 // output planes).  Returns FA_OK and
 // sets *tiles (partial slots used per plane) when it launched; returns FA_OK

@@ -66,11 +66,16 @@ constexpr int MF_MAX_K = 16;           // 16 output rows + K - 1 <= 32 input row
 
 enum { MF_REDUCE = 0, MF_MAP = 1, MF_CS = 2 };
 
+// What the planes hold: uint8 samples, the float32 levels of a uint8 image's
+// 2 x 2-mean pyramid (multiples of 4^-s in [0, 255], s <= 4), or its first
+// level stored as float16 (multiples of 1/4 in [0, 255], exact in fp16).
+enum { SRC_U8 = 0, SRC_F32 = 1, SRC_F16 = 2 };
+
 // Buffer-resource word 3 for raw (untyped, unswizzled) access.
 constexpr int MF_RSRC_WORD3 = 0x00020000;
 
 struct MfArgs {
-  const void* x;  // uint8 samples, or float samples of a uint8 pyramid level
+  const void* x;  // uint8 samples, or samples of a uint8 pyramid level (SRC_F32 / F16)
   const void* y;
   int64_t xsn, xsc, ysn, ysc;
   uint32_t xsh, ysh;
@@ -82,8 +87,9 @@ struct MfArgs {
   float* map;
   double* partial;
   double* partial_cs;   // MF_CS
-  float* px;            // MF_CS: optional pyramid level (2 x 2 means), float32
-  float* py;
+  void* px;             // MF_CS: optional pyramid level (2 x 2 means),
+  void* py;             //   float32, or float16 (level_f16, uint8 input)
+  int level_f16;
 };
 
 __device__ inline f4 mfma(h8 a, h8 b, f4 c) {
@@ -99,29 +105,27 @@ struct Frag {
   h8 xl, yl;  // pyramid levels only: the low fp16 pieces of x', y'
 };
 
-__device__ inline Frag prep(uint2 xa, uint2 ya) {
+// The six fragments from eight samples of x and of y held as four fp16 pairs
+// t = v + b, where the bias b is 1024 (uint8 bytes under the pattern 0x64vv)
+// or 0 (float16 pyramid level, v a multiple of 1/4); cs = -(128 + b) 2^-9 and
+// cu = -(128 + b) recentre them:
+//   t 2^-9 + cs = (v - 128) 2^-9 = x' 2^-9,   t + cu = x'.
+// Every value below is exact in fp16 for both sources (checked exhaustively
+// over all pairs of sample values).
+__device__ inline Frag prep_pairs(const h2 (&xt)[4], const h2 (&yt)[4], h2 cs, h2 cu) {
   u4 ox, oy, o3h, o3l, o4h, o4l;
-  // t = 1024 + v (fp16 bit pattern 0x64vv, 0 <= v < 256):
-  //   t * 2^-9 - 2.25 = (v - 128) 2^-9,  t - 1152 = v - 128
   const h2 m = {static_cast<_Float16>(0x1p-9f), static_cast<_Float16>(0x1p-9f)};
-  const h2 c128 = {static_cast<_Float16>(-2.25f), static_cast<_Float16>(-2.25f)};
-  const h2 k1152 = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t xw = j < 2 ? xa.x : xa.y;
-    const uint32_t yw = j < 2 ? ya.x : ya.y;
-    // v_perm_b32 picks bytes of {S0 : S1}: 0-3 from S1, 4-7 from S0
-    const uint32_t sf = (j & 1) ? 0x04030402u : 0x04010400u;  // two bytes under 0x64
-    const h2 xt = bc<h2>(__builtin_amdgcn_perm(0x64646464u, xw, sf));
-    const h2 yt = bc<h2>(__builtin_amdgcn_perm(0x64646464u, yw, sf));
-    const h2 xs = __builtin_elementwise_fma(xt, m, c128);  // x' 2^-9
-    const h2 ys = __builtin_elementwise_fma(yt, m, c128);  // y' 2^-9
-    const h2 xu = xt + k1152;                              // x'
-    const h2 du = xt - yt;                                 // x' - y'
-    const h2 ds = xs - ys;                                 // (x' - y') 2^-9
+    const h2 xs = __builtin_elementwise_fma(xt[j], m, cs);  // x' 2^-9
+    const h2 ys = __builtin_elementwise_fma(yt[j], m, cs);  // y' 2^-9
+    const h2 xu = xt[j] + cu;                               // x'
+    const h2 du = xt[j] - yt[j];                            // x' - y'
+    const h2 ds = xs - ys;                                  // (x' - y') 2^-9
     // x'y' 2^-9 in [-31.75, 32] and (x'-y')^2 2^-9 in [0, 127]: the product
     // rounded to fp16, then the exact remainder from a fused multiply-add of
-    // the same operands (an integer of at most 4, resp. 16, units of 2^-9)
+    // the same operands (at most 4, resp. 16, units of 2^-9 for bytes; a
+    // multiple of 2^-13 of at most 2^-7, resp. 2^-5, for quarter samples)
     const h2 p3h = xu * ys;
     const h2 p3l = __builtin_elementwise_fma(xu, ys, -p3h);
     const h2 p4h = du * ds;
@@ -141,6 +145,23 @@ __device__ inline Frag prep(uint2 xa, uint2 ya) {
   f.p4h = bc<h8>(o4h);
   f.p4l = bc<h8>(o4l);
   return f;
+}
+
+// uint8: v_perm_b32 places each byte under 0x64, the fp16 pattern of 1024 + v.
+__device__ inline Frag prep(uint2 xa, uint2 ya) {
+  h2 xt[4], yt[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t xw = j < 2 ? xa.x : xa.y;
+    const uint32_t yw = j < 2 ? ya.x : ya.y;
+    // v_perm_b32 picks bytes of {S0 : S1}: 0-3 from S1, 4-7 from S0
+    const uint32_t sf = (j & 1) ? 0x04030402u : 0x04010400u;  // two bytes under 0x64
+    xt[j] = bc<h2>(__builtin_amdgcn_perm(0x64646464u, xw, sf));
+    yt[j] = bc<h2>(__builtin_amdgcn_perm(0x64646464u, yw, sf));
+  }
+  const h2 cs = {static_cast<_Float16>(-2.25f), static_cast<_Float16>(-2.25f)};
+  const h2 cu = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+  return prep_pairs(xt, yt, cs, cu);
 }
 
 // fp16 hi + lo of v (|v| < 65504): hi rounds to nearest, lo rounds the exact
@@ -266,21 +287,39 @@ __device__ inline void stash_all(const HAcc& h, float one, VState& v) {
   stash<HALF, PYR>(h.p4, one, v.hi[3], v.lo[3]);
 }
 
-// One lane's 8 samples of one 16-row block: 8 bytes of x and of y (uint8), or
-// 8 floats of each (pyramid levels).
-template <bool PYR>
+// One lane's 8 samples of one 16-row block: 8 bytes of x and of y (uint8), 8
+// floats of each (float32 pyramid levels) or 8 halves (float16 level).
+template <int SRC>
 struct Raw;
 template <>
-struct Raw<false> {
+struct Raw<SRC_U8> {
   uint2 x, y;
 };
 template <>
-struct Raw<true> {
+struct Raw<SRC_F32> {
   float4 x0, x1, y0, y1;
 };
+template <>
+struct Raw<SRC_F16> {
+  u4 x, y;
+};
 
-__device__ inline Frag prep(const Raw<false>& r, float) {
+__device__ inline Frag prep(const Raw<SRC_U8>& r, float) {
   return prep(r.x, r.y);
+}
+
+// The first level of a uint8 pyramid in float16: the samples are the fp16
+// pairs themselves (bias 0).
+__device__ inline Frag prep(const Raw<SRC_F16>& r, float) {
+  h2 xt[4], yt[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    xt[j] = bc<h2>(r.x[j]);
+    yt[j] = bc<h2>(r.y[j]);
+  }
+  const h2 cs = {static_cast<_Float16>(-0.25f), static_cast<_Float16>(-0.25f)};
+  const h2 cu = {static_cast<_Float16>(-128.0f), static_cast<_Float16>(-128.0f)};
+  return prep_pairs(xt, yt, cs, cu);
 }
 
 // Pyramid levels of uint8 input: every sample is a multiple of 4^-s in
@@ -288,7 +327,7 @@ __device__ inline Frag prep(const Raw<false>& r, float) {
 // into fp16 hi + lo (at most 16 significant bits); x'y' and (x'-y')^2 are
 // formed in float32, as the strip kernel forms them, and split hi + lo (22
 // bits).  No scaling: the window's 2^9 is taken out of the sums (stash).
-__device__ inline Frag prep(const Raw<true>& r, float one) {
+__device__ inline Frag prep(const Raw<SRC_F32>& r, float one) {
   const float xs[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
   const float ys[8] = {r.y0.x, r.y0.y, r.y0.z, r.y0.w, r.y1.x, r.y1.y, r.y1.z, r.y1.w};
   u4 ox, oxl, oy, oyl, o3h, o3l, o4h, o4l;
@@ -415,10 +454,12 @@ __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, 
 // column pairs of the 32-column window (B fragment: lane (g, n) holds
 // P[8g + i][n]), and the D fragment holds, in lane (g, n), rows 4g .. 4g+3 of
 // pooled column n, so each lane adds its two row pairs.  The sums are exact:
-// four samples of x' 2^-9 (uint8) or of x' = hi + lo (pyramid levels).
+// four samples of x' 2^-9 (uint8, float16 level) or of x' = hi + lo (float32
+// levels); the mean of four bytes, a multiple of 1/4, is exact in float16 too.
 struct Pool {
-  float* px;
-  float* py;
+  void* px;
+  void* py;
+  bool half;     // float16 level (uint8 input), else float32
   int64_t off;   // this plane's first element
   int Wd;        // level width, floor(W / 2)
   int row_end;   // first input row this chunk does not pool
@@ -444,8 +485,15 @@ __device__ inline void pool_frag(const Pool& pl, int row0, uint32_t pcol, const 
       const int row = row0 + 2 * q;  // even; row_end is even, so row + 1 pools too
       if (row < pl.row_end) {
         const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
-        pl.px[o] = fmaf(sx[2 * q] + sx[2 * q + 1], k, 128.0f);
-        pl.py[o] = fmaf(sy[2 * q] + sy[2 * q + 1], k, 128.0f);
+        const float mx = fmaf(sx[2 * q] + sx[2 * q + 1], k, 128.0f);
+        const float my = fmaf(sy[2 * q] + sy[2 * q + 1], k, 128.0f);
+        if (pl.half) {  // uniform
+          static_cast<_Float16*>(pl.px)[o] = static_cast<_Float16>(mx);
+          static_cast<_Float16*>(pl.py)[o] = static_cast<_Float16>(my);
+        } else {
+          static_cast<float*>(pl.px)[o] = mx;
+          static_cast<float*>(pl.py)[o] = my;
+        }
       }
     }
   }
@@ -474,10 +522,12 @@ __device__ inline void vblock(const Weights& w, const VState& v, f4* o, float c2
   for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.lo[q]), o[q]);
 }
 
-// uint8: 4 waves per SIMD (128 VGPRs) fit without spills and beat 3.
-template <bool PYR, int MODE>
+// uint8 and float16 levels: 4 waves per SIMD (128 VGPRs) fit without spills
+// and beat 3.
+template <int SRC, int MODE>
 __global__ __launch_bounds__(BLOCK)
-__attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a) {
+__attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kernel(MfArgs a) {
+  constexpr bool PYR = SRC == SRC_F32;  // float32 samples: hi + lo operands
   __shared__ double sred[2 * WAVES_PER_BLOCK];
   __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
   const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
@@ -497,8 +547,10 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
   if (c0 < a.Wout) {  // uniform per wave
     const int img = plane / a.C;
     const int ch = plane - img * a.C;
-    // element pointers of this plane (uint8 samples, or float pyramid samples)
-    using E = typename std::conditional<PYR, float, uint8_t>::type;
+    // element pointers of this plane (uint8 samples, or pyramid samples)
+    using E = typename std::conditional<
+        PYR, float, typename std::conditional<SRC == SRC_F16, _Float16, uint8_t>::type>::type;
+    constexpr int EB = static_cast<int>(sizeof(E));  // bytes per sample
     const E* __restrict__ xp = reinterpret_cast<const E*>(a.x) + img * a.xsn + ch * a.xsc;
     const E* __restrict__ yp = reinterpret_cast<const E*>(a.y) + img * a.ysn + ch * a.ysc;
     // this lane's 8 input columns; a chunk past the image only feeds output
@@ -525,6 +577,7 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
     if constexpr (MODE == MF_CS) {
       pl.px = a.px;
       pl.py = a.py;
+      pl.half = a.level_f16 != 0;
       pl.Wd = a.W / 2;
       pl.off = static_cast<int64_t>(plane) * (a.H / 2) * pl.Wd;
       pl.row_end = r0 + a.TH >= a.Hout ? 2 * (a.H / 2) : r0 + a.TH;
@@ -538,25 +591,26 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
 
     // Rows past the image only feed output rows past Hout.  load(j) is called
     // for j = 0, 1, 2, ... in order, so the row offsets advance by 16 rows per
-    // call.  uint8 blocks are read through a buffer resource that starts at
-    // the block's first row and ends at the plane's end: its base and range
-    // are scalar values, the lane's offset within the block is fixed, so a
-    // load costs no vector instruction, and the range check turns rows past
-    // the image into zeros without touching memory.  Pyramid levels clamp
-    // their offsets to the last row.
+    // call.  uint8 blocks (and float16 levels) are read through a buffer
+    // resource that starts at the block's first row and ends at the plane's
+    // end: its base and range are scalar values, the lane's offset within the
+    // block is fixed, so a load costs no vector instruction, and the range
+    // check turns rows past the image into zeros without touching memory.
+    // float32 levels clamp their offsets to the last row.
     const uint32_t xstep = MT * a.xsh, ystep = MT * a.ysh;
     const uint32_t rl = static_cast<uint32_t>(min(r0 + n, a.H - 1));
     const uint32_t xmax = static_cast<uint32_t>(a.H - 1) * a.xsh + cc;
     const uint32_t ymax = static_cast<uint32_t>(a.H - 1) * a.ysh + cc;
     uint32_t xo = rl * a.xsh + cc, yo = rl * a.ysh + cc;  // block 0
-    const uint32_t vx = static_cast<uint32_t>(n) * a.xsh + cc;  // within the block
-    const uint32_t vy = static_cast<uint32_t>(n) * a.ysh + cc;
-    // plane bytes and the block's first byte; the host keeps (H + 48) rows of
-    // either plane below 2^31 bytes
+    // byte offsets within the block
+    const uint32_t vx = (static_cast<uint32_t>(n) * a.xsh + cc) * EB;
+    const uint32_t vy = (static_cast<uint32_t>(n) * a.ysh + cc) * EB;
+    // plane samples and the block's first sample; the host keeps (H + 48) rows
+    // of either plane below 2^31 bytes
     const int ext_x = (a.H - 1) * static_cast<int>(a.xsh) + a.W;
     const int ext_y = (a.H - 1) * static_cast<int>(a.ysh) + a.W;
     int bx = r0 * static_cast<int>(a.xsh), by = r0 * static_cast<int>(a.ysh);
-    auto load = [&](int, Raw<PYR>& r) {
+    auto load = [&](int, Raw<SRC>& r) {
       if constexpr (PYR) {
         r.x0 = *reinterpret_cast<const float4*>(xp + xo);
         r.x1 = *reinterpret_cast<const float4*>(xp + xo + 4);
@@ -566,19 +620,24 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
         yo = min(yo + ystep, ymax);
       } else {
         const auto rx = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<E*>(xp + bx), 0, max(ext_x - bx, 0), MF_RSRC_WORD3);
+            const_cast<E*>(xp + bx), 0, max(ext_x - bx, 0) * EB, MF_RSRC_WORD3);
         const auto ry = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<E*>(yp + by), 0, max(ext_y - by, 0), MF_RSRC_WORD3);
-        const auto lx = __builtin_amdgcn_raw_buffer_load_b64(rx, vx, 0, 0);
-        const auto ly = __builtin_amdgcn_raw_buffer_load_b64(ry, vy, 0, 0);
-        r.x = uint2{lx[0], lx[1]};
-        r.y = uint2{ly[0], ly[1]};
+            const_cast<E*>(yp + by), 0, max(ext_y - by, 0) * EB, MF_RSRC_WORD3);
+        if constexpr (SRC == SRC_F16) {
+          r.x = bc<u4>(__builtin_amdgcn_raw_buffer_load_b128(rx, vx, 0, 0));
+          r.y = bc<u4>(__builtin_amdgcn_raw_buffer_load_b128(ry, vy, 0, 0));
+        } else {
+          const auto lx = __builtin_amdgcn_raw_buffer_load_b64(rx, vx, 0, 0);
+          const auto ly = __builtin_amdgcn_raw_buffer_load_b64(ry, vy, 0, 0);
+          r.x = uint2{lx[0], lx[1]};
+          r.y = uint2{ly[0], ly[1]};
+        }
         bx += static_cast<int>(xstep);
         by += static_cast<int>(ystep);
       }
     };
     // horizontal pass of block j (and its share of the pyramid)
-    auto hpass = [&](int j, const Raw<PYR>& r) {
+    auto hpass = [&](int j, const Raw<SRC>& r) {
       const Frag f = prep(r, a.one);
       if constexpr (MODE == MF_CS) {
         if (a.px) pool_frag<PYR>(pl, r0 + MT * j + 4 * g, pcol, f);  // uniform branch
@@ -599,7 +658,7 @@ __attribute__((amdgpu_waves_per_eu(PYR ? 1 : 4))) void ssim_mfma_kernel(MfArgs a
     // cores and the vector ALU overlap within the wave too.
     const int nb = (r_end - r0 + MT - 1) / MT;  // output blocks; H blocks 0 .. nb
     VState v;
-    Raw<PYR> raw;
+    Raw<SRC> raw;
     load(0, raw);
     stash_all<0, PYR>(hpass(0, raw), a.one, v);
     load(1, raw);
@@ -649,13 +708,13 @@ bool mfma_enabled() {
   return !(e && e[0] == '0');
 }
 
-template <bool PYR, int MODE>
+template <int SRC, int MODE>
 int occupancy() {
   static int occ = 0;
   if (occ <= 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, reinterpret_cast<const void*>(&ssim_mfma_kernel<PYR, MODE>), BLOCK, 0) != hipSuccess ||
+            &v, reinterpret_cast<const void*>(&ssim_mfma_kernel<SRC, MODE>), BLOCK, 0) != hipSuccess ||
         v <= 0)
       v = 1;
     occ = v;
@@ -663,12 +722,44 @@ int occupancy() {
   return occ;
 }
 
+// The kernel of (source, mode): its occupancy (launch == false) or its launch.
+// float16 levels come only through the CS pass (fa_gpu_ssim_cs_ex).
+template <int SRC>
+int dispatch(int mode, bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
+  if (mode == MF_CS) {
+    if (!launch) return occupancy<SRC, MF_CS>();
+    hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_CS>), grid, dim3(BLOCK), 0, st, a);
+  } else if constexpr (SRC != SRC_F16) {
+    if (mode == MF_MAP) {
+      if (!launch) return occupancy<SRC, MF_MAP>();
+      hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_MAP>), grid, dim3(BLOCK), 0, st, a);
+    } else {
+      if (!launch) return occupancy<SRC, MF_REDUCE>();
+      hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_REDUCE>), grid, dim3(BLOCK), 0, st, a);
+    }
+  }
+  return 0;
+}
+
+int dispatch(int src, int mode, bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
+  return src == SRC_F32   ? dispatch<SRC_F32>(mode, launch, grid, st, a)
+         : src == SRC_F16 ? dispatch<SRC_F16>(mode, launch, grid, st, a)
+                          : dispatch<SRC_U8>(mode, launch, grid, st, a);
+}
+
 }  // namespace
 
 int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   *tiles = 0;
   if (!mfma_enabled() || c.K > MF_MAX_K || c.W % 8 != 0 || c.W < 8) return FA_OK;
-  const uintptr_t base_align = c.pyr ? 15 : 7;  // float4 or 8-byte loads
+  const int src = c.src == SsimMfmaCall::F32_LEVEL   ? SRC_F32
+                  : c.src == SsimMfmaCall::F16_LEVEL ? SRC_F16
+                                                     : SRC_U8;
+  const int mode = c.partial_cs ? MF_CS : c.map ? MF_MAP : MF_REDUCE;
+  if (src == SRC_F16 && mode != MF_CS) return FA_OK;
+  if (c.level_f16 && (src != SRC_U8 || mode != MF_CS)) return FA_OK;
+  // 16-byte loads (float32 and float16 levels) or 8-byte loads (uint8)
+  const uintptr_t base_align = src == SRC_U8 ? 7 : 15;
   if ((reinterpret_cast<uintptr_t>(c.x) | reinterpret_cast<uintptr_t>(c.y)) & base_align)
     return FA_OK;
   // float4 stores into the pyramid level (W % 8 == 0 makes every row of it
@@ -678,9 +769,10 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   const int64_t s[6] = {c.xsn, c.xsc, c.ysn, c.ysc, c.xsh, c.ysh};
   for (int64_t v : s)
     if (v % 8 != 0) return FA_OK;
-  // 32-bit offsets within a plane: the uint8 loads run up to 47 rows past
+  // 32-bit offsets within a plane: the buffer loads run up to 47 rows past
   // the last output row (their range check stops them at the plane's end)
-  if ((static_cast<int64_t>(c.H) + 48) * std::max(c.xsh, c.ysh) > INT32_MAX) return FA_OK;
+  const int64_t eb = src == SRC_F32 ? 4 : src == SRC_F16 ? 2 : 1;
+  if ((static_cast<int64_t>(c.H) + 48) * std::max(c.xsh, c.ysh) * eb > INT32_MAX) return FA_OK;
 
   MfArgs a = {};
   a.x = c.x;
@@ -706,18 +798,12 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   a.partial_cs = c.partial_cs;
   a.px = c.px;
   a.py = c.py;
-  const int mode = c.partial_cs ? MF_CS : c.map ? MF_MAP : MF_REDUCE;
+  a.level_f16 = c.level_f16 ? 1 : 0;
 
   // Rows per chunk (a multiple of 16): the fewest rounds of resident
   // workgroups times the work of one, charging the extra 16-row block of
   // horizontal work each chunk starts with at 10 rows.
-  int occ;
-  if (c.pyr)
-    occ = mode == MF_CS ? occupancy<true, MF_CS>()
-          : mode == MF_MAP ? occupancy<true, MF_MAP>() : occupancy<true, MF_REDUCE>();
-  else
-    occ = mode == MF_CS ? occupancy<false, MF_CS>()
-          : mode == MF_MAP ? occupancy<false, MF_MAP>() : occupancy<false, MF_REDUCE>();
+  const int occ = dispatch(src, mode, false, dim3(1), st, a);
   const int64_t resident = static_cast<int64_t>(cu_count(device)) * occ;
   const int64_t planes = static_cast<int64_t>(c.N) * c.C;
   const int strips = (c.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
@@ -741,22 +827,7 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   a.tiles = strips * best_chunks;
   const int64_t wgs = planes * a.tiles;
   if (wgs > INT32_MAX) return FA_OK;
-  const dim3 grid(static_cast<unsigned>(wgs));
-  if (c.pyr) {
-    if (mode == MF_CS)
-      hipLaunchKernelGGL((ssim_mfma_kernel<true, MF_CS>), grid, dim3(BLOCK), 0, st, a);
-    else if (mode == MF_MAP)
-      hipLaunchKernelGGL((ssim_mfma_kernel<true, MF_MAP>), grid, dim3(BLOCK), 0, st, a);
-    else
-      hipLaunchKernelGGL((ssim_mfma_kernel<true, MF_REDUCE>), grid, dim3(BLOCK), 0, st, a);
-  } else {
-    if (mode == MF_CS)
-      hipLaunchKernelGGL((ssim_mfma_kernel<false, MF_CS>), grid, dim3(BLOCK), 0, st, a);
-    else if (mode == MF_MAP)
-      hipLaunchKernelGGL((ssim_mfma_kernel<false, MF_MAP>), grid, dim3(BLOCK), 0, st, a);
-    else
-      hipLaunchKernelGGL((ssim_mfma_kernel<false, MF_REDUCE>), grid, dim3(BLOCK), 0, st, a);
-  }
+  dispatch(src, mode, true, dim3(static_cast<unsigned>(wgs)), st, a);
   FA_LAUNCH_CHECK();
   *tiles = a.tiles;
   return FA_OK;

@@ -568,14 +568,17 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
         if not grad and len(w) <= 8:
             # inference: every scale leaves its partial sums, and one reduction
             # finishes all scales (plane terms, product, channel and batch means)
-            # The float32 levels below uint8 input are exact 2x2 means of bytes,
-            # which the native side may treat as such (matrix-core kernel).
+            # The levels below uint8 input are exact 2x2 means of bytes, which
+            # the native side may treat as such (matrix-core kernel); the first
+            # (multiples of 1/4 in [0, 255]) is exact in float16, half the bytes
+            # to write and read, the deeper ones in float32.
             u8 = x4.dtype == torch.uint8 and lw is None
             parts, slots, npix = [], [], []
             for i in range(scales):
                 last = i == scales - 1
+                ldt = torch.float16 if u8 and i == 0 else pdt
                 ps, pcs, sl, npx, cx, cy = backend.ssim_cs_partials(
-                    cx, cy, win32, shift, C1, C2, None if last else pdt,
+                    cx, cy, win32, shift, C1, C2, None if last else ldt,
                     luma=lw if i == 0 else None, u8_pyramid=u8 and i > 0)
                 parts.append(ps if last else pcs)
                 slots.append(sl)

@@ -39,10 +39,11 @@ extern "C" {
 #define FA_F32 3
 #define FA_F64 4
 /* No counterpart in the reference: a flag fa_gpu_ssim_cs_ex accepts OR-ed
- * into FA_F32.  It promises that every sample is a level of the 2x2-mean
- * pyramid of uint8 data (a multiple of 4^-s in [0, 255], s <= 4), which lets
- * the call run on the matrix cores; without it float32 runs the vector-ALU
- * kernel.  Results agree either way to the same 1e-6 bar. */
+ * into FA_F32 or FA_F16.  It promises that every sample is a level of the
+ * 2x2-mean pyramid of uint8 data: with FA_F32 a multiple of 4^-s in [0, 255],
+ * s <= 4; with FA_F16 the first level (s = 1, multiples of 1/4, exact in
+ * float16).  That lets the call run on the matrix cores; without it the input
+ * runs the vector-ALU kernel.  Results agree either way to the same 1e-6 bar. */
 #define FA_DTYPE_U8_PYRAMID 0x100
 
 /* pixel-loss selector (reference fa_abi.h:51-54) */
@@ -226,17 +227,21 @@ FA_API int fa_gpu_ssim_ex(const void* x, const void* y, int dtype, int N, int C,
  * non-overlapping 2x2 mean (of the luma plane, offset included, with luma),
  * odd trailing row / column dropped.  px / py:
  * N * Cout * (H/2) * (W/2) elements of pool_dtype, which is FA_F64, or FA_F32
- * for uint8 and float32 input without luma.  The means are formed in float64,
- * so the levels of a uint8 pyramid are exact in float32 and those of float16 /
- * bfloat16 / float32 exact in float64 (unless a 2x2 block spans more than
- * 2^29 / 2^45 in magnitude; then correctly rounded).
+ * for uint8 and float32 input (and for a float16 first level flagged
+ * FA_DTYPE_U8_PYRAMID) without luma, or FA_F16 for uint8 input without luma
+ * (the first level of a uint8 image, multiples of 1/4 in [0, 255], is exact
+ * in float16).  The means are formed in float64, so the levels of a uint8
+ * pyramid are exact in float32 and those of float16 / bfloat16 / float32 exact
+ * in float64 (unless a 2x2 block spans more than 2^29 / 2^45 in magnitude;
+ * then correctly rounded).
  * out_s / out_cs: N * Cout plane means as in fa_gpu_ssim_cs, or both null:
  * then no finalize runs and the partial sums stay in partial / partial_cs for
  * fa_gpu_ms_ssim_reduce.  out_slots: host int, may be null unless both means
  * are null; receives the number of slots per plane the launch used (each
  * plane's partial sums are packed at that stride from the start of the
- * buffer).  dtype: FA_F32 | FA_DTYPE_U8_PYRAMID marks a uint8 pyramid level
- * (see FA_DTYPE_U8_PYRAMID).
+ * buffer).  dtype: FA_F32 | FA_DTYPE_U8_PYRAMID marks a uint8 pyramid level,
+ * FA_F16 | FA_DTYPE_U8_PYRAMID its first level in float16 (see
+ * FA_DTYPE_U8_PYRAMID).
  */
 FA_API int fa_gpu_ssim_cs_ex(const void* x, const void* y, int dtype, int N,
                              int C, int H, int W, const int64_t* x_strides,

@@ -184,11 +184,18 @@ def test_ms_ssim(gpu, shape):
         assert _rel(float(g), float(w)) <= REL, ("vs strip kernel", g, w)
 
 
-def test_ms_ssim_pyramid_level_exact(gpu):
-    # the level the CS pass writes is the exact 2 x 2 mean of the uint8 input
+@pytest.mark.parametrize("w", [136, 134])  # 134: rows of 134 bytes take the strip kernel
+@pytest.mark.parametrize("pool", ["float32", "float16"])
+@pytest.mark.parametrize("kernel", ["auto", "strip"])
+def test_ms_ssim_pyramid_level_exact(gpu, w, pool, kernel):
+    # the level the CS pass writes is the exact 2 x 2 mean of the uint8 input,
+    # in float32 or in float16 (a multiple of 1/4 in [0, 255] is exact there)
+    import contextlib
+    import ctypes
+
     from frame_analytics_amd import backend
 
-    a, b = u8_pair((2, 3, 90, 136), 7.0, seed=4)
+    a, b = u8_pair((2, 3, 90, w), 7.0, seed=4)
     x = torch.as_tensor(a, device=gpu)
     y = torch.as_tensor(b, device=gpu)
     n, c, h, w = a.shape
@@ -198,16 +205,18 @@ def test_ms_ssim_pyramid_level_exact(gpu):
     part_cs = torch.empty_like(part)
     out_s = torch.empty(n * c, dtype=torch.float64, device=gpu)
     out_cs = torch.empty_like(out_s)
-    px = torch.full((n, c, h // 2, w // 2), -1.0, device=gpu)
+    pdt = getattr(torch, pool)
+    px = torch.full((n, c, h // 2, w // 2), -1.0, device=gpu, dtype=pdt)
     py = torch.full_like(px, -1.0)
-    import ctypes
     slots = ctypes.c_int(0)
     stream = torch.cuda.current_stream().cuda_stream
-    rc = backend.call_gpu("fa_gpu_ssim_cs_ex", x.data_ptr(), y.data_ptr(), 0, n, c, h, w,
-                          None, None, None, win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
-                          (0.03 * 255) ** 2, part.data_ptr(), part_cs.data_ptr(), bpp,
-                          out_s.data_ptr(), out_cs.data_ptr(), ctypes.addressof(slots),
-                          px.data_ptr(), py.data_ptr(), 3, 0, stream)
+    with _VectorAlu() if kernel == "strip" else contextlib.nullcontext():
+        rc = backend.call_gpu("fa_gpu_ssim_cs_ex", x.data_ptr(), y.data_ptr(), 0, n, c, h, w,
+                              None, None, None, win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
+                              (0.03 * 255) ** 2, part.data_ptr(), part_cs.data_ptr(), bpp,
+                              out_s.data_ptr(), out_cs.data_ptr(), ctypes.addressof(slots),
+                              px.data_ptr(), py.data_ptr(), 3 if pool == "float32" else 1, 0,
+                              stream)
     assert rc == 0
     want_x = ref.avg_pool2(a.astype(np.float64))
     want_y = ref.avg_pool2(b.astype(np.float64))
@@ -218,6 +227,65 @@ def test_ms_ssim_pyramid_level_exact(gpu):
     got_cs = out_cs.cpu().numpy().reshape(n, c)
     assert np.allclose(got_s, s_ref.mean(axis=(-2, -1)), rtol=1e-6, atol=0)
     assert np.allclose(got_cs, cs_ref.mean(axis=(-2, -1)), rtol=1e-6, atol=0)
+
+
+def test_float16_level_only_below_uint8(gpu):
+    # a float16 level is exact only for the 2 x 2 means of bytes: any other
+    # input, or luma, is refused
+    import ctypes
+
+    from frame_analytics_amd import backend
+
+    n, c, h, w = 1, 3, 32, 32
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    bpp = backend.workspace_slots("ssim", h, w, 11)
+    part = torch.empty((3, bpp), dtype=torch.float64, device=gpu)
+    px = torch.empty((n, c, h // 2, w // 2), dtype=torch.float16, device=gpu)
+    slots = ctypes.c_int(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    lw = (ctypes.c_double * 4)(0.299, 0.587, 0.114, 0.0)
+    for dt, luma in ((torch.float32, None), (torch.float16, None), (torch.uint8, lw)):
+        x = torch.zeros((n, c, h, w), dtype=dt, device=gpu)
+        code = backend._DTYPE_CODE[dt]
+        rc = backend.call_gpu("fa_gpu_ssim_cs_ex", x.data_ptr(), x.data_ptr(), code, n, c, h, w,
+                              None, None, luma, win.data_ptr(), 11, 127.5, 1.0, 1.0,
+                              part.data_ptr(), part.data_ptr(), bpp, None, None,
+                              ctypes.addressof(slots), px.data_ptr(), px.data_ptr(), 1, 0,
+                              stream)
+        assert rc == 1, (dt, luma is not None)  # FA_E_DTYPE
+
+
+@pytest.mark.parametrize("kernel", ["auto", "strip"])
+@pytest.mark.parametrize("w", [120, 124])  # 124: the strip kernel reads the float16 level
+def test_pyramid_level_flag_float16(gpu, kernel, w):
+    # the first level of a uint8 pyramid in float16 (multiples of 1/4 in
+    # [0, 255]) with FA_DTYPE_U8_PYRAMID: the statistics match the oracle and
+    # the next level (float32) is exact
+    import contextlib
+
+    from frame_analytics_amd import backend
+
+    rng = np.random.default_rng(w)
+    n, c, h = 2, 3, 70
+    ka = rng.integers(0, 1021, (n, c, h, w))
+    kb = np.clip(ka + rng.integers(-36, 37, ka.shape), 0, 1020)
+    a, b = ka / 4.0, kb / 4.0
+    x = torch.as_tensor(a.astype(np.float16), device=gpu)
+    y = torch.as_tensor(b.astype(np.float16), device=gpu)
+    assert np.array_equal(x.cpu().numpy().astype(np.float64), a)
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    C1, C2 = (0.01 * 255) ** 2, (0.03 * 255) ** 2
+    with _VectorAlu() if kernel == "strip" else contextlib.nullcontext():
+        ps, pcs, sl, npix, px, py = backend.ssim_cs_partials(
+            x, y, win, 127.5, C1, C2, torch.float32, u8_pyramid=True)
+    s_mean = ps.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+    cs_mean = pcs.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+    s_ref, cs_ref = ref.ssim_maps(a, b)
+    assert np.allclose(s_mean, s_ref.mean(axis=(-2, -1)).reshape(-1), rtol=REL, atol=0)
+    assert np.allclose(cs_mean, cs_ref.mean(axis=(-2, -1)).reshape(-1), rtol=REL, atol=0)
+    assert px.dtype == torch.float32
+    assert np.array_equal(px.cpu().numpy().astype(np.float64), ref.avg_pool2(a))
+    assert np.array_equal(py.cpu().numpy().astype(np.float64), ref.avg_pool2(b))
 
 
 @pytest.mark.parametrize("s", [1, 2, 4])
