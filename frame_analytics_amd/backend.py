@@ -565,14 +565,15 @@ def pyramid_dtype(dt: torch.dtype) -> torch.dtype:
 
 
 def _cs_launch(x, y, win, shift, C1, C2, *, pool_dtype=None, luma=None, reduce=True,
-               u8_pyramid=False):
+               u8_pyramid=False, ssim_sums=True):
     """One CS pass (``fa_gpu_ssim_cs_ex``, or ``fa_gpu_ssim_cs`` for a plain
     contiguous call): the (ssim, cs) partial sums per plane, their plane means
     when ``reduce``, and the next pyramid level of ``pool_dtype`` if given.
+    Without ``reduce`` and ``ssim_sums`` the pass forms the cs sums alone.
 
     Returns ``(s, cs, partial, partial_cs, slots, px, py)``; ``s``/``cs`` are
-    ``None`` without ``reduce`` and ``slots`` is what the launch reports
-    (``-1`` when it was not asked)."""
+    ``None`` without ``reduce``, ``partial`` without the SSIM sums, and
+    ``slots`` is what the launch reports (``-1`` when it was not asked)."""
     win = _win32(win)
     n, c, h, w = (int(v) for v in x.shape)
     k = int(win.numel())
@@ -581,7 +582,7 @@ def _cs_launch(x, y, win, shift, C1, C2, *, pool_dtype=None, luma=None, reduce=T
     y, ys = _view_strides(y)
     bpp = workspace_slots("ssim", h, w, k)
     dev, stream = _site(x)
-    partial = _f64(x.device, planes, bpp)
+    partial = _f64(x.device, planes, bpp) if reduce or ssim_sums else None
     partial_cs = _f64(x.device, planes, bpp)
     s = cs = px = py = None
     if reduce:
@@ -609,16 +610,19 @@ def _cs_launch(x, y, win, shift, C1, C2, *, pool_dtype=None, luma=None, reduce=T
     return s, cs, partial, partial_cs, int(slots.value), px, py
 
 
-def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None, u8_pyramid=False):
+def ssim_cs_partials(x, y, win, shift, C1, C2, pool_dtype, luma=None, u8_pyramid=False,
+                     ssim_sums=True):
     """One inference MS-SSIM scale left unreduced: ``(partial, partial_cs,
-    slots, npix, px, py)`` -- the per-plane partial sums of the SSIM and cs
-    maps (``slots`` per plane, packed), the plane's output pixel count, and the
-    next pyramid level (``None`` at the coarsest scale).  The partial sums go
+    slots, npix, px, py)`` -- the per-plane partial sums of the SSIM map
+    (``None`` unless ``ssim_sums``: MS-SSIM reads them only at its coarsest
+    scale) and of the cs map (``slots`` per plane, packed), the plane's output
+    pixel count, and the next pyramid level (``None`` at the coarsest scale).  The partial sums go
     to :func:`ms_ssim_reduce`; nothing is synchronised.  ``u8_pyramid``: x and
     y are levels of a uint8 pyramid (FA_DTYPE_U8_PYRAMID): float32, or the
     first level in float16, where its quarter samples are exact."""
     _, _, ps, pcs, slots, px, py = _cs_launch(x, y, win, shift, C1, C2, pool_dtype=pool_dtype,
-                                              luma=luma, reduce=False, u8_pyramid=u8_pyramid)
+                                              luma=luma, reduce=False, u8_pyramid=u8_pyramid,
+                                              ssim_sums=ssim_sums)
     k = int(win.numel())
     npix = float((x.shape[-2] - k + 1) * (x.shape[-1] - k + 1))
     return ps, pcs, slots, npix, px, py

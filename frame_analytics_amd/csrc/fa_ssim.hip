@@ -426,7 +426,7 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
     double s = 0.0, scs = 0.0;
     block_sum2(pol.acc_s, pol.acc_cs, sred, &s, &scs);
     if (threadIdx.x == 0) {
-      a.partial[slot] = s;
+      if (a.partial) a.partial[slot] = s;  // null: the cs sums alone were asked for
       a.partial_cs[slot] = scs;
     }
   }
@@ -864,7 +864,10 @@ static int ssim_cs_impl(const void* x, const void* y, int dtype, int N, int C, i
                         double* partial, double* partial_cs, int bpp, double* out_s,
                         double* out_cs, int* out_slots, void* px, void* py, int pool_dtype,
                         int device, void* stream) {
-  if (!x || !y || !win || !partial || !partial_cs) return FA_E_ARG;
+  if (!x || !y || !win || !partial_cs) return FA_E_ARG;
+  // partial may be null only when nothing is finalized: then the pass forms
+  // the cs sums alone (all MS-SSIM reads below its coarsest scale)
+  if (!partial && (out_s || out_cs)) return FA_E_ARG;
   // FA_DTYPE_U8_PYRAMID: float32 samples of a uint8 pyramid level, or
   // float16 samples of its first level (a hint that admits the matrix-core
   // kernel; the strip kernel reads plain float32 / float16)

@@ -24,8 +24,9 @@ struct SsimMfmaCall {
   float* map;                  // optional float32 SSIM map (N, C, Hout, Wout)
   double* partial;             // per-plane partial sums, bpp slots per plane
   int bpp;
-  // MS-SSIM's CS pass (partial_cs non-null): per-plane sums of SSIM and of
-  // cs = A2 / B2, and optionally the next pyramid level, the 2 x 2 means of x
+  // MS-SSIM's CS pass (partial_cs non-null): per-plane sums of SSIM (unless
+  // partial is null) and of cs = A2 / B2, and optionally the next pyramid
+  // level, the 2 x 2 means of x
   // and y (floor(H/2) x floor(W/2) per plane) into px / py: float32, or
   // float16 when level_f16 (uint8 input only: quarter samples are exact)
   double* partial_cs;

@@ -64,7 +64,9 @@ constexpr int MT = 16;                 // rows / columns of an MFMA block
 constexpr float WSCALE = 512.0f;       // window scale of both passes (data: 2^-9)
 constexpr int MF_MAX_K = 16;           // 16 output rows + K - 1 <= 32 input rows
 
-enum { MF_REDUCE = 0, MF_MAP = 1, MF_CS = 2 };
+// MF_CSO: the CS pass without the SSIM sums (the cs sums alone, which is all
+// MS-SSIM reads below its coarsest scale).
+enum { MF_REDUCE = 0, MF_MAP = 1, MF_CS = 2, MF_CSO = 3 };
 
 // What the planes hold: uint8 samples, the float32 levels of a uint8 image's
 // 2 x 2-mean pyramid (multiples of 4^-s in [0, 255], s <= 4), or its first
@@ -86,8 +88,8 @@ struct MfArgs {
   float one;      // 1.0f (see split_pair)
   float* map;
   double* partial;
-  double* partial_cs;   // MF_CS
-  void* px;             // MF_CS: optional pyramid level (2 x 2 means),
+  double* partial_cs;   // MF_CS, MF_CSO
+  void* px;             // MF_CS, MF_CSO: optional pyramid level (2 x 2 means),
   void* py;             //   float32, or float16 (level_f16, uint8 input)
   int level_f16;
 };
@@ -404,6 +406,19 @@ __device__ inline float ssim_px_folded(const Epi& e, float U, float V, float Xc,
   return (A1 * A2) * __builtin_amdgcn_rcpf(B1 * B2);
 }
 
+// cs = A2 / B2 alone, with C2 folded into the vertical pass as in
+// ssim_px_folded (A2' = Xc - 2^-9 U V, B2' = A2' + Q / 2 - 2^-10 (U - V)^2,
+// both 2^8 times A2, B2): 8 instructions per pixel against 16 for the SSIM
+// value and cs together.
+__device__ inline float cs_px_folded(float U, float V, float Xc, float Q) {
+  const float p = U * V;
+  const float du = U - V;
+  const float dd = du * 0x1p-10f;
+  const float A2 = fmaf(-0x1p-9f, p, Xc);
+  const float B2 = fmaf(-dd, du, fmaf(0.5f, Q, A2));
+  return A2 * __builtin_amdgcn_rcpf(B2);
+}
+
 // cs = A2 / B2 beside the SSIM value (MS-SSIM's CS pass).
 __device__ inline void ssim_cs_px(const Epi& e, float U, float V, float X, float Q, float& s,
                                   float& cs) {
@@ -422,8 +437,8 @@ __device__ inline void ssim_cs_px(const Epi& e, float U, float V, float X, float
 }
 
 // Adds this lane's four outputs (rows row0 .. row0 + 3 of its column) to the
-// lane's float64 sums; `full` (uniform) says the whole 16 x 16 block lies
-// inside the map.
+// lane's float64 sums (MF_CSO: the cs values into acc); `full` (uniform) says
+// the whole 16 x 16 block lies inside the map.
 template <int MODE, bool FULL>
 __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, bool col_ok,
                               float* map_px, int Wout, double& acc, double& acc_cs) {
@@ -436,6 +451,9 @@ __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, 
       ssim_cs_px(e, o[0][i], o[1][i], o[2][i], o[3][i], s, cs);
       rs += ok ? s : 0.0f;
       rcs += ok ? cs : 0.0f;
+    } else if constexpr (MODE == MF_CSO) {
+      const float cs = cs_px_folded(o[0][i], o[1][i], o[2][i], o[3][i]);
+      rs += ok ? cs : 0.0f;
     } else if constexpr (MODE == MF_MAP) {
       const float s = ssim_px(e, o[0][i], o[1][i], o[2][i], o[3][i]);
       if (ok) map_px[static_cast<int64_t>(i) * Wout] = s;
@@ -574,7 +592,7 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     // everything up to 2 floor(H / 2).  Every row the chunk pools lies in one
     // of its H blocks.
     Pool pl = {};
-    if constexpr (MODE == MF_CS) {
+    if constexpr (MODE == MF_CS || MODE == MF_CSO) {
       pl.px = a.px;
       pl.py = a.py;
       pl.half = a.level_f16 != 0;
@@ -639,7 +657,7 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     // horizontal pass of block j (and its share of the pyramid)
     auto hpass = [&](int j, const Raw<SRC>& r) {
       const Frag f = prep(r, a.one);
-      if constexpr (MODE == MF_CS) {
+      if constexpr (MODE == MF_CS || MODE == MF_CSO) {
         if (a.px) pool_frag<PYR>(pl, r0 + MT * j + 4 * g, pcol, f);  // uniform branch
       }
       return hmfma<PYR>(f, w);
@@ -668,7 +686,7 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
       {
         stash_all<1, PYR>(hn, a.one, v);  // H_{b+1} next to H_b
         f4 o[4];
-        vblock<0, MODE == MF_REDUCE>(w, v, o, e.c2s);
+        vblock<0, MODE == MF_REDUCE || MODE == MF_CSO>(w, v, o, e.c2s);
         if (b + 2 <= nb) {  // uniform
           hn = hpass(b + 2, raw);
           load(b + 3, raw);
@@ -678,7 +696,7 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
       if (b + 1 < nb) {
         stash_all<0, PYR>(hn, a.one, v);  // H_{b+2} over H_b
         f4 o[4];
-        vblock<1, MODE == MF_REDUCE>(w, v, o, e.c2s);
+        vblock<1, MODE == MF_REDUCE || MODE == MF_CSO>(w, v, o, e.c2s);
         if (b + 3 <= nb) {
           hn = hpass(b + 3, raw);
           load(b + 4, raw);
@@ -698,7 +716,7 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     }
   } else {
     const double s = block_sum(acc, sred);
-    if (threadIdx.x == 0) a.partial[slot] = s;
+    if (threadIdx.x == 0) (MODE == MF_CSO ? a.partial_cs : a.partial)[slot] = s;
   }
 }
 
@@ -723,13 +741,16 @@ int occupancy() {
 }
 
 // The kernel of (source, mode): its occupancy (launch == false) or its launch.
-// float16 levels come only through the CS pass (fa_gpu_ssim_cs_ex).
+// Pyramid levels come only through the CS pass (fa_gpu_ssim_cs_ex).
 template <int SRC>
 int dispatch(int mode, bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
   if (mode == MF_CS) {
     if (!launch) return occupancy<SRC, MF_CS>();
     hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_CS>), grid, dim3(BLOCK), 0, st, a);
-  } else if constexpr (SRC != SRC_F16) {
+  } else if (mode == MF_CSO) {
+    if (!launch) return occupancy<SRC, MF_CSO>();
+    hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_CSO>), grid, dim3(BLOCK), 0, st, a);
+  } else if constexpr (SRC == SRC_U8) {
     if (mode == MF_MAP) {
       if (!launch) return occupancy<SRC, MF_MAP>();
       hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_MAP>), grid, dim3(BLOCK), 0, st, a);
@@ -755,9 +776,11 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   const int src = c.src == SsimMfmaCall::F32_LEVEL   ? SRC_F32
                   : c.src == SsimMfmaCall::F16_LEVEL ? SRC_F16
                                                      : SRC_U8;
-  const int mode = c.partial_cs ? MF_CS : c.map ? MF_MAP : MF_REDUCE;
-  if (src == SRC_F16 && mode != MF_CS) return FA_OK;
-  if (c.level_f16 && (src != SRC_U8 || mode != MF_CS)) return FA_OK;
+  // the CS pass, with (MF_CS) or without (MF_CSO, partial null) the SSIM sums
+  const int mode = c.partial_cs ? (c.partial ? MF_CS : MF_CSO) : c.map ? MF_MAP : MF_REDUCE;
+  const bool cs_pass = mode == MF_CS || mode == MF_CSO;
+  if (src != SRC_U8 && !cs_pass) return FA_OK;
+  if (c.level_f16 && (src != SRC_U8 || !cs_pass)) return FA_OK;
   // 16-byte loads (float32 and float16 levels) or 8-byte loads (uint8)
   const uintptr_t base_align = src == SRC_U8 ? 7 : 15;
   if ((reinterpret_cast<uintptr_t>(c.x) | reinterpret_cast<uintptr_t>(c.y)) & base_align)

@@ -577,9 +577,10 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
             for i in range(scales):
                 last = i == scales - 1
                 ldt = torch.float16 if u8 and i == 0 else pdt
+                # the SSIM sums only at the coarsest scale, cs below it
                 ps, pcs, sl, npx, cx, cy = backend.ssim_cs_partials(
                     cx, cy, win32, shift, C1, C2, None if last else ldt,
-                    luma=lw if i == 0 else None, u8_pyramid=u8 and i > 0)
+                    luma=lw if i == 0 else None, u8_pyramid=u8 and i > 0, ssim_sums=last)
                 parts.append(ps if last else pcs)
                 slots.append(sl)
                 npix.append(npx)

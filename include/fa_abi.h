@@ -236,7 +236,8 @@ FA_API int fa_gpu_ssim_ex(const void* x, const void* y, int dtype, int N, int C,
  * then correctly rounded).
  * out_s / out_cs: N * Cout plane means as in fa_gpu_ssim_cs, or both null:
  * then no finalize runs and the partial sums stay in partial / partial_cs for
- * fa_gpu_ms_ssim_reduce.  out_slots: host int, may be null unless both means
+ * fa_gpu_ms_ssim_reduce; partial may then be null too, and the pass forms
+ * the cs sums alone (MS-SSIM reads no SSIM sums below its coarsest scale).  out_slots: host int, may be null unless both means
  * are null; receives the number of slots per plane the launch used (each
  * plane's partial sums are packed at that stride from the start of the
  * buffer).  dtype: FA_F32 | FA_DTYPE_U8_PYRAMID marks a uint8 pyramid level,

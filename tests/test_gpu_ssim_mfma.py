@@ -229,6 +229,33 @@ def test_ms_ssim_pyramid_level_exact(gpu, w, pool, kernel):
     assert np.allclose(got_cs, cs_ref.mean(axis=(-2, -1)), rtol=1e-6, atol=0)
 
 
+@pytest.mark.parametrize("kernel", ["auto", "strip"])
+@pytest.mark.parametrize("w", [136, 134])
+def test_cs_sums_alone_uint8(gpu, kernel, w):
+    # uint8 input, the cs sums alone (partial null, as MS-SSIM asks below its
+    # coarsest scale) with the float16 level: cs matches the oracle, the
+    # level is exact
+    import contextlib
+
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((2, 3, 90, w), 7.0, seed=5)
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    n, c = a.shape[:2]
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    with _VectorAlu() if kernel == "strip" else contextlib.nullcontext():
+        ps, pcs, sl, npix, px, py = backend.ssim_cs_partials(
+            x, y, win, 127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, torch.float16,
+            ssim_sums=False)
+    assert ps is None and px.dtype == torch.float16
+    _, cs_ref = ref.ssim_maps(a.astype(float), b.astype(float))
+    cs_mean = pcs.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+    assert np.allclose(cs_mean, cs_ref.mean(axis=(-2, -1)).reshape(-1), rtol=REL, atol=0)
+    assert np.array_equal(px.cpu().numpy().astype(np.float64), ref.avg_pool2(a.astype(float)))
+    assert np.array_equal(py.cpu().numpy().astype(np.float64), ref.avg_pool2(b.astype(float)))
+
+
 def test_float16_level_only_below_uint8(gpu):
     # a float16 level is exact only for the 2 x 2 means of bytes: any other
     # input, or luma, is refused
@@ -275,17 +302,19 @@ def test_pyramid_level_flag_float16(gpu, kernel, w):
     assert np.array_equal(x.cpu().numpy().astype(np.float64), a)
     win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
     C1, C2 = (0.01 * 255) ** 2, (0.03 * 255) ** 2
-    with _VectorAlu() if kernel == "strip" else contextlib.nullcontext():
-        ps, pcs, sl, npix, px, py = backend.ssim_cs_partials(
-            x, y, win, 127.5, C1, C2, torch.float32, u8_pyramid=True)
-    s_mean = ps.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
-    cs_mean = pcs.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
     s_ref, cs_ref = ref.ssim_maps(a, b)
-    assert np.allclose(s_mean, s_ref.mean(axis=(-2, -1)).reshape(-1), rtol=REL, atol=0)
-    assert np.allclose(cs_mean, cs_ref.mean(axis=(-2, -1)).reshape(-1), rtol=REL, atol=0)
-    assert px.dtype == torch.float32
-    assert np.array_equal(px.cpu().numpy().astype(np.float64), ref.avg_pool2(a))
-    assert np.array_equal(py.cpu().numpy().astype(np.float64), ref.avg_pool2(b))
+    for sums in (True, False):  # with the SSIM sums, or the cs sums alone
+        with _VectorAlu() if kernel == "strip" else contextlib.nullcontext():
+            ps, pcs, sl, npix, px, py = backend.ssim_cs_partials(
+                x, y, win, 127.5, C1, C2, torch.float32, u8_pyramid=True, ssim_sums=sums)
+        cs_mean = pcs.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+        assert np.allclose(cs_mean, cs_ref.mean(axis=(-2, -1)).reshape(-1), rtol=REL, atol=0)
+        if sums:
+            s_mean = ps.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+            assert np.allclose(s_mean, s_ref.mean(axis=(-2, -1)).reshape(-1), rtol=REL, atol=0)
+        assert px.dtype == torch.float32
+        assert np.array_equal(px.cpu().numpy().astype(np.float64), ref.avg_pool2(a))
+        assert np.array_equal(py.cpu().numpy().astype(np.float64), ref.avg_pool2(b))
 
 
 @pytest.mark.parametrize("s", [1, 2, 4])
@@ -305,23 +334,24 @@ def test_pyramid_level_flag(gpu, s):
     y = torch.as_tensor(b, device=gpu)
     win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
     C1, C2 = (0.01 * 255) ** 2, (0.03 * 255) ** 2
-    outs = {}
-    for flag in (True, False):
-        ps, pcs, sl, npix, px, py = backend.ssim_cs_partials(
-            x, y, win, 127.5, C1, C2, torch.float32, u8_pyramid=flag)
-        # each plane's partials are packed at the used stride `sl`
-        s_mean = ps.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
-        cs_mean = pcs.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
-        outs[flag] = (s_mean, cs_mean, px.cpu().numpy(), py.cpu().numpy())
     s_ref, cs_ref = ref.ssim_maps(a.astype(np.float64), b.astype(np.float64))
     want_s = s_ref.mean(axis=(-2, -1)).reshape(-1)
     want_cs = cs_ref.mean(axis=(-2, -1)).reshape(-1)
     for flag in (True, False):
-        got_s, got_cs, px, py = outs[flag]
-        assert np.allclose(got_s, want_s, rtol=REL, atol=0), (flag, got_s, want_s)
-        assert np.allclose(got_cs, want_cs, rtol=REL, atol=0), (flag, got_cs, want_cs)
-        assert np.array_equal(px.astype(np.float64), ref.avg_pool2(a.astype(np.float64)))
-        assert np.array_equal(py.astype(np.float64), ref.avg_pool2(b.astype(np.float64)))
+        for sums in (True, False):  # with the SSIM sums, or the cs sums alone
+            ps, pcs, sl, npix, px, py = backend.ssim_cs_partials(
+                x, y, win, 127.5, C1, C2, torch.float32, u8_pyramid=flag, ssim_sums=sums)
+            assert (ps is None) == (not sums)
+            # each plane's partials are packed at the used stride `sl`
+            cs_mean = pcs.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+            assert np.allclose(cs_mean, want_cs, rtol=REL, atol=0), (flag, sums, cs_mean, want_cs)
+            if sums:
+                s_mean = ps.reshape(-1)[: n * c * sl].reshape(n * c, sl).sum(1).cpu().numpy() / npix
+                assert np.allclose(s_mean, want_s, rtol=REL, atol=0), (flag, s_mean, want_s)
+            assert np.array_equal(px.cpu().numpy().astype(np.float64),
+                                  ref.avg_pool2(a.astype(np.float64)))
+            assert np.array_equal(py.cpu().numpy().astype(np.float64),
+                                  ref.avg_pool2(b.astype(np.float64)))
 
 
 def test_pyramid_flag_is_an_ex_hint_only(gpu):
