@@ -475,18 +475,22 @@ __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, 
 // four samples of x' 2^-9 (uint8, float16 level) or of x' = hi + lo (float32
 // levels); the mean of four bytes, a multiple of 1/4, is exact in float16 too.
 struct Pool {
-  void* px;
-  void* py;
-  bool half;     // float16 level (uint8 input), else float32
-  int64_t off;   // this plane's first element
-  int Wd;        // level width, floor(W / 2)
-  int row_end;   // first input row this chunk does not pool
-  bool lane_on;  // this lane stores pooled column c0/2 + n (inside the level)
-  h8 pm;         // the column-pair matrix fragment
+  char* bx;        // this plane's level of x and y, at this chunk's first level row
+  char* by;
+  int rows;        // level rows this chunk writes (its input rows / 2)
+  uint32_t rstep;  // bytes per level row
+  uint32_t lo;     // this lane's byte offset in a block's level rows (row 2g,
+                   // its column), or out of every buffer's range when it stores nothing
+  bool half;       // float16 level (uint8 input), else float32
+  h8 pm;           // the column-pair matrix fragment
 };
 
+// Stores through buffer resources whose base is the block's first level row
+// (scalar) and whose range ends at the last row this chunk writes: the lane's
+// offset is fixed, so a store costs no vector address arithmetic, and the range
+// check drops the rows past the chunk and the lanes that store nothing.
 template <bool PYR>
-__device__ inline void pool_frag(const Pool& pl, int row0, uint32_t pcol, const Frag& f) {
+__device__ inline void pool_frag(const Pool& pl, int j, const Frag& f) {
   const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 sx = mfma(f.x, pl.pm, z);
   f4 sy = mfma(f.y, pl.pm, z);
@@ -494,25 +498,25 @@ __device__ inline void pool_frag(const Pool& pl, int row0, uint32_t pcol, const 
     sx = mfma(f.xl, pl.pm, sx);
     sy = mfma(f.yl, pl.pm, sy);
   }
-  // a sum of four is (S - 512) 2^-9 (uint8) or S - 512: the mean S / 4 is
-  // sum * k + 128
+  // a sum of four is (S - 512) 2^-9 (uint8, float16 level) or S - 512: the
+  // mean S / 4 is sum * k + 128
   constexpr float k = PYR ? 0.25f : 128.0f;
-  if (pl.lane_on) {
+  const int row = MT / 2 * j;  // the block's first level row, in this chunk
+  const uint32_t boff = static_cast<uint32_t>(row) * pl.rstep;
+  const int range = max(pl.rows - row, 0) * static_cast<int>(pl.rstep);
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(pl.bx + boff, 0, range, MF_RSRC_WORD3);
+  const auto ry = __builtin_amdgcn_make_buffer_rsrc(pl.by + boff, 0, range, MF_RSRC_WORD3);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int row = row0 + 2 * q;  // even; row_end is even, so row + 1 pools too
-      if (row < pl.row_end) {
-        const int64_t o = pl.off + static_cast<int64_t>(row >> 1) * pl.Wd + pcol;
-        const float mx = fmaf(sx[2 * q] + sx[2 * q + 1], k, 128.0f);
-        const float my = fmaf(sy[2 * q] + sy[2 * q + 1], k, 128.0f);
-        if (pl.half) {  // uniform
-          static_cast<_Float16*>(pl.px)[o] = static_cast<_Float16>(mx);
-          static_cast<_Float16*>(pl.py)[o] = static_cast<_Float16>(my);
-        } else {
-          static_cast<float*>(pl.px)[o] = mx;
-          static_cast<float*>(pl.py)[o] = my;
-        }
-      }
+  for (int q = 0; q < 2; ++q) {
+    const float mx = fmaf(sx[2 * q] + sx[2 * q + 1], k, 128.0f);
+    const float my = fmaf(sy[2 * q] + sy[2 * q + 1], k, 128.0f);
+    const int o = static_cast<int>(pl.lo + q * pl.rstep);  // level row 2g + q
+    if (pl.half) {  // uniform
+      __builtin_amdgcn_raw_buffer_store_b16(bc<unsigned short>(static_cast<_Float16>(mx)), rx, o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(bc<unsigned short>(static_cast<_Float16>(my)), ry, o, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(mx), rx, o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(my), ry, o, 0, 0);
     }
   }
 }
@@ -593,19 +597,25 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     // of its H blocks.
     Pool pl = {};
     if constexpr (MODE == MF_CS || MODE == MF_CSO) {
-      pl.px = a.px;
-      pl.py = a.py;
-      pl.half = a.level_f16 != 0;
-      pl.Wd = a.W / 2;
-      pl.off = static_cast<int64_t>(plane) * (a.H / 2) * pl.Wd;
-      pl.row_end = r0 + a.TH >= a.Hout ? 2 * (a.H / 2) : r0 + a.TH;
-      const bool last_wave = c0 + MT >= a.Wout;
-      pl.lane_on = a.px != nullptr && ((wave & 1) == 0 || last_wave) && c0 / 2 + n < pl.Wd;
+      if (a.px) {  // uniform
+        const int Wd = a.W / 2;
+        const int eb = a.level_f16 ? 2 : 4;
+        const int row_end = r0 + a.TH >= a.Hout ? 2 * (a.H / 2) : r0 + a.TH;
+        const int64_t first = (static_cast<int64_t>(plane) * (a.H / 2) + r0 / 2) * Wd * eb;
+        pl.bx = static_cast<char*>(a.px) + first;
+        pl.by = static_cast<char*>(a.py) + first;
+        pl.rows = row_end / 2 - r0 / 2;
+        pl.rstep = static_cast<uint32_t>(Wd * eb);
+        pl.half = a.level_f16 != 0;
+        const bool last_wave = c0 + MT >= a.Wout;
+        const bool lane_on = ((wave & 1) == 0 || last_wave) && c0 / 2 + n < Wd;
+        // 0x80000000 lies past every range (a plane's level is below 2^31 bytes)
+        pl.lo = lane_on ? static_cast<uint32_t>((2 * g * Wd + c0 / 2 + n) * eb) : 0x80000000u;
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         pl.pm[i] = static_cast<_Float16>(((8 * g + i) >> 1) == n ? 1.0f : 0.0f);
     }
-    const uint32_t pcol = static_cast<uint32_t>(c0 / 2 + n);
 
     // Rows past the image only feed output rows past Hout.  load(j) is called
     // for j = 0, 1, 2, ... in order, so the row offsets advance by 16 rows per
@@ -658,7 +668,7 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     auto hpass = [&](int j, const Raw<SRC>& r) {
       const Frag f = prep(r, a.one);
       if constexpr (MODE == MF_CS || MODE == MF_CSO) {
-        if (a.px) pool_frag<PYR>(pl, r0 + MT * j + 4 * g, pcol, f);  // uniform branch
+        if (a.px) pool_frag<PYR>(pl, j, f);  // uniform branch
       }
       return hmfma<PYR>(f, w);
     };
