@@ -86,8 +86,10 @@ __device__ inline typename std::conditional<FAST, float, double>::type one_minus
     const float Gs = G1 + G2;
     const float A = fmaf(2.0f, __builtin_amdgcn_sqrtf(G1 * G2), Gs);  // (g1 + g2)^2
     const float n = static_cast<float>(dm);
-    // the floor keeps 0 / 0 (flat, eps = 0) at 0; a non-zero dm implies A > 0
-    return (n * n) * __builtin_amdgcn_rcpf(fmaxf(A * (Gs + t_f), 1e-30f));
+    // e_f and t_f arrive floored at 1e-18 (gmsd_impl), so A (Gs + t_f) >=
+    // 6e-36, a normal float32: the reciprocal is finite and a flat pixel's
+    // 0 / 0 (eps = T = 0) comes out 0
+    return (n * n) * __builtin_amdgcn_rcpf(A * (Gs + t_f));
   } else {
     const double G1 = static_cast<double>(m1) + e_d;
     const double G2 = static_cast<double>(m2) + e_d;
@@ -324,12 +326,12 @@ __device__ inline void mag2(double gx1, double gy1, double gx2, double gy2, doub
 // Rows [row0, row0 + rows) of one strip of one plane, added to acc / acc2,
 // walked top-down, or bottom-up when `up` (uniform).  Walking up swaps the
 // window's top and bottom rows, which only flips the sign of gy: the
-// magnitudes, and so every term, are the same.
-template <class Src>
+// magnitudes, and so every term, are the same.  MAP: also write the q map.
+template <class Src, bool MAP>
 __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int row0, int rows,
                                 bool up, double& acc, double& acc2) {
   float* const map_plane =
-      a.map ? a.map + (static_cast<int64_t>(n) * a.Cout + c) * a.Hout * a.Wout : nullptr;
+      MAP ? a.map + (static_cast<int64_t>(n) * a.Cout + c) * a.Hout * a.Wout : nullptr;
   using S = typename Src::S;
   using Raw = typename Src::Raw;
   constexpr int NC = Src::NC;
@@ -360,13 +362,19 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
   src.samples(p1, xb, yb);
 
   using Acc = typename std::conditional<Src::FAST, float, double>::type;
-  // G_PD rows from `cur`, starting at row g of the run; the group's sums are
-  // formed at the accumulation type, then added in float64
-  auto group = [&](const Raw (&cur)[G_PD], int g) {
-    Acc gs = Acc(0), gs2 = Acc(0);
+  // G_PD rows from `cur`, starting at row g of the run (FULL: all G_PD lie in
+  // the run, so the body has no row test and the window rotates by renaming).
+  // Each column sums its own terms; a lane's columns past the strip or the
+  // image (ok false) hold finite garbage that the group drops once, by
+  // selection, instead of masking every term.  The sums are formed at the
+  // accumulation type, then added in float64.
+  auto group = [&](const Raw (&cur)[G_PD], int g, auto full) {
+    Acc gs[NC], gs2[NC];  // -0 + d is d exactly, so the first add folds away
+#pragma unroll
+    for (int k = 0; k < NC; ++k) gs[k] = gs2[k] = Acc(-0.0);
 #pragma unroll
     for (int i = 0; i < G_PD; ++i) {
-      if (g + i < rows) {  // uniform
+      if (decltype(full)::value || g + i < rows) {  // uniform
         S xc[NC], yc[NC];
         src.samples(cur[i], xc, yc);
         S gx1[NC], gy1[NC], gx2[NC], gy2[NC];
@@ -376,14 +384,14 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
         for (int k = 0; k < NC; ++k) {
           S m1, m2, dm;
           mag2(gx1[k], gy1[k], gx2[k], gy2[k], m1, m2, dm);
-          dm = ok[k] ? dm : S(0);
           const Acc d = one_minus_q<Src::FAST, S>(m1, m2, dm, a.eps2f, a.T2f, a.eps2, a.T2);
-          if (map_plane && ok[k])  // uniform test of the pointer
-            map_plane[static_cast<int64_t>(up ? row0 + rows - 1 - g - i : row0 + g + i) * a.Wout +
-                      col + k] =
-                static_cast<float>(1.0 - static_cast<double>(d));
-          gs += d;
-          gs2 = fma(d, d, gs2);
+          if constexpr (MAP) {
+            if (ok[k])
+              map_plane[static_cast<int64_t>(up ? row0 + rows - 1 - g - i : row0 + g + i) *
+                            a.Wout + col + k] = static_cast<float>(1.0 - static_cast<double>(d));
+          }
+          gs[k] += d;
+          gs2[k] = fma(d, d, gs2[k]);
         }
 #pragma unroll
         for (int k = 0; k < NC; ++k) {
@@ -394,22 +402,34 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
         }
       }
     }
-    acc += static_cast<double>(gs);
-    acc2 += static_cast<double>(gs2);
+    Acc s = Acc(0), s2 = Acc(0);
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      s += ok[k] ? gs[k] : Acc(0);
+      s2 += ok[k] ? gs2[k] : Acc(0);
+    }
+    acc += static_cast<double>(s);
+    acc2 += static_cast<double>(s2);
   };
 
   for (int g = 0; g < rows; g += 2 * G_PD) {
 #pragma unroll
     for (int i = 0; i < G_PD; ++i) bufB[i] = src.load(srow(2 + g + G_PD + i));
-    group(bufA, g);
+    if (g + G_PD <= rows)
+      group(bufA, g, std::true_type{});
+    else
+      group(bufA, g, std::false_type{});
     if (g + G_PD >= rows) break;
 #pragma unroll
     for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(srow(2 + g + 2 * G_PD + i));
-    group(bufB, g + G_PD);
+    if (g + 2 * G_PD <= rows)
+      group(bufB, g + G_PD, std::true_type{});
+    else
+      group(bufB, g + G_PD, std::false_type{});
   }
 }
 
-template <class Src>
+template <class Src, bool MAP>
 __global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
   // one task per workgroup: its four waves take four adjacent strips over the
   // same rows, so each input row is fetched as one contiguous stretch
@@ -436,7 +456,7 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
       const int row = static_cast<int>(rem - static_cast<int64_t>(grp) * a.Hout);
       const int len = static_cast<int>(min(e - s, static_cast<int64_t>(a.Hout - row)));
       const int strip = grp * WAVES_PER_BLOCK + wave;
-      if (strip < a.strips) gmsd_run<Src>(a, n, c, strip, row, len, false, acc, acc2);
+      if (strip < a.strips) gmsd_run<Src, MAP>(a, n, c, strip, row, len, false, acc, acc2);
       s += len;
     }
   } else {
@@ -449,7 +469,7 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
       const int rq = static_cast<int>(rem - static_cast<int64_t>(grp) * a.Hout);
       const int len = static_cast<int>(min(t - s, static_cast<int64_t>(rq + 1)));
       const int strip = grp * WAVES_PER_BLOCK + wave;
-      if (strip < a.strips) gmsd_run<Src>(a, n, c, strip, rq - len + 1, len, true, acc, acc2);
+      if (strip < a.strips) gmsd_run<Src, MAP>(a, n, c, strip, rq - len + 1, len, true, acc, acc2);
       t -= len;
     }
   }
@@ -681,21 +701,29 @@ static int gmsd_slots(const GGeom& g) {
 
 static bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
-// Workgroups per image: one round of resident workgroups over the whole
-// launch, no more than the workspace holds (a slot per wave) or than leaves a
-// workgroup G_MIN_ROWS rows.
-template <class Src>
-static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipStream_t st,
-                       int* wpi_used) {
+template <class Src, bool MAP>
+static int occupancy_gmsd() {
   static int wgs_per_cu = 0;  // occupancy of this kernel, queried once
   if (wgs_per_cu <= 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, reinterpret_cast<const void*>(&gmsd_kernel<Src>), BLOCK, 0) != hipSuccess ||
+            &v, reinterpret_cast<const void*>(&gmsd_kernel<Src, MAP>), BLOCK, 0) != hipSuccess ||
         v <= 0)
       v = 1;
     wgs_per_cu = v;
   }
+  return wgs_per_cu;
+}
+
+// Workgroups per image: one round of resident workgroups over the whole
+// launch, no more than the workspace holds (a slot per wave) or than leaves a
+// workgroup G_MIN_ROWS rows.  The kernel that writes the q map is its own
+// instantiation, so the statistics-only one carries no map test.
+template <class Src>
+static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipStream_t st,
+                       int* wpi_used) {
+  const bool map = a.map != nullptr;
+  const int wgs_per_cu = map ? occupancy_gmsd<Src, true>() : occupancy_gmsd<Src, false>();
   a.strips = (a.Wout + Src::OUTW - 1) / Src::OUTW;
   a.groups = (a.strips + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.rows_img = static_cast<int64_t>(a.Cout) * a.groups * a.Hout;
@@ -708,7 +736,12 @@ static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipSt
   if (tasks > INT32_MAX / WAVES_PER_BLOCK) return FA_E_SHAPE;
   a.wpi = static_cast<int>(wpi);
   a.tasks = static_cast<int>(tasks);
-  hipLaunchKernelGGL((gmsd_kernel<Src>), dim3(static_cast<unsigned>(tasks)), dim3(BLOCK), 0, st, a);
+  if (map)
+    hipLaunchKernelGGL((gmsd_kernel<Src, true>), dim3(static_cast<unsigned>(tasks)), dim3(BLOCK),
+                       0, st, a);
+  else
+    hipLaunchKernelGGL((gmsd_kernel<Src, false>), dim3(static_cast<unsigned>(tasks)), dim3(BLOCK),
+                       0, st, a);
   FA_LAUNCH_CHECK();
   *wpi_used = a.wpi * WAVES_PER_BLOCK;  // partial slots per image
   return FA_OK;
@@ -775,8 +808,13 @@ static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int 
   const double sc2 = downsample ? 144.0 : 9.0;  // 9 s^2
   a.T2 = Tc * sc2;
   a.eps2 = eps * sc2;
-  a.T2f = static_cast<float>(a.T2);
-  a.eps2f = static_cast<float>(a.eps2);
+  // The float32 path's denominators stay positive when eps and T are at least
+  // 1e-18 (see one_minus_q).  Only values in [0, 1e-18) are raised: the
+  // defaults are far above, and adding 1e-18 to G = gx^2 + gy^2 + eps moves a
+  // term by at most ~1e-9 relative even where G is tiny.
+  const auto floor18 = [](double v) { return static_cast<float>(v >= 0.0 && v < 1e-18 ? 1e-18 : v); };
+  a.T2f = floor18(a.T2);
+  a.eps2f = floor18(a.eps2);
   a.psum = psum;
   a.psumsq = psumsq;
   a.map = map_out;
