@@ -44,7 +44,7 @@
 
 namespace fa {
 
-constexpr int G_PD = 4;        // rows of loads in flight ahead of the window
+constexpr int G_PD = 3;        // rows of loads in flight ahead of the window
 constexpr int G_MIN_ROWS = 8;  // fewest rows a wave is given, where rows are scarce
 constexpr int G_SLOT_ROWS = 4; // workspace: one partial slot per 4 rows of a strip
 constexpr int G_OUTW_WIDE = 2 * WAVE - 2;  // output columns per wave, 2 columns per lane
@@ -75,17 +75,22 @@ struct GmsdArgs {
 };
 
 // d = 1 - q from the squared gradient magnitudes M1, M2 (without eps) and
-// their difference dm = M1 - M2 (exact for integer samples; zero for masked
-// columns, which then contribute d = 0).  float32 where FAST, else float64.
+// their difference dm = M1 - M2 (exact for integer samples).  float32 where
+// FAST, else float64.
 template <bool FAST, typename S>
 __device__ inline typename std::conditional<FAST, float, double>::type one_minus_q(
     S m1, S m2, S dm, float e_f, float t_f, double e_d, double t_d) {
   if constexpr (FAST) {
-    const float G1 = static_cast<float>(m1) + e_f;
-    const float G2 = static_cast<float>(m2) + e_f;
+    const float f1 = static_cast<float>(m1), f2 = static_cast<float>(m2);
+    const float G1 = f1 + e_f;
+    const float G2 = f2 + e_f;
     const float Gs = G1 + G2;
     const float A = fmaf(2.0f, __builtin_amdgcn_sqrtf(G1 * G2), Gs);  // (g1 + g2)^2
-    const float n = static_cast<float>(dm);
+    // integer magnitudes below 2^24 are exact in float32, so f1 - f2 is dm;
+    // above, both gradients are near their maximum, the rounding moves dm by
+    // at most 2, and where that is a large share of dm, d is below 1e-14.
+    // Other sources pass dm exactly.
+    const float n = std::is_integral<S>::value ? f1 - f2 : static_cast<float>(dm);
     // e_f and t_f arrive floored at 1e-18 (gmsd_impl), so A (Gs + t_f) >=
     // 6e-36, a normal float32: the reciprocal is finite and a flat pixel's
     // 0 / 0 (eps = T = 0) comes out 0
