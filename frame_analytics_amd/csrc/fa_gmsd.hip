@@ -44,11 +44,16 @@
 
 namespace fa {
 
-constexpr int G_PD = 3;        // rows of loads in flight ahead of the window
+constexpr int G_PD = 2;        // rows of loads in flight ahead of the window
 constexpr int G_MIN_ROWS = 8;  // fewest rows a wave is given, where rows are scarce
 constexpr int G_SLOT_ROWS = 4; // workspace: one partial slot per 4 rows of a strip
 constexpr int G_OUTW_WIDE = 2 * WAVE - 2;  // output columns per wave, 2 columns per lane
 constexpr int G_OUTW_NARROW = WAVE - 2;    // ... 1 column per lane
+// at most this many waves per SIMD in the one round of resident waves: more
+// waves give each wave a shorter run, whose prologue (two window rows, the
+// first loads' latency) and final reductions then weigh more; measured
+// slower at 7 and 8 on configs[4]
+constexpr int G_MAX_WAVES_PER_SIMD = 6;
 
 struct GView {
   int64_t sn, sc, sh;  // element strides of image, channel, row (columns are unit stride)
@@ -121,6 +126,7 @@ struct SrcU8Wide {
   static constexpr int OUTW = G_OUTW_WIDE;
   static constexpr int CH = LUMA ? 3 : 1;
   static constexpr bool FAST = true;
+  static constexpr bool PACKED = !LUMA;  // samples_xy / prewitt_xy
   using S = typename std::conditional<LUMA, double, int>::type;
   struct Raw {
     uint32_t w[2][CH][2];  // tensor, channel, input row of the pair
@@ -195,6 +201,24 @@ struct SrcU8Wide {
       }
     }
   }
+
+  // Column k's x sample in the low 16 bits of p[k], its y sample in the high
+  // 16 (each at most 4 * 255, so neither half carries into the other).  The x
+  // sample is two byte dot products; the y sample gathers its four bytes (two
+  // of each input row) with one byte permute and adds their sum, shifted up
+  // 16, to the x sample in one v_sad_hi_u8 (sum of |byte - 0| << 16, plus
+  // the accumulator).
+  __device__ inline void samples_xy(const Raw& v, uint32_t (&p)[NC]) const {
+    static_assert(!LUMA && NC == 2, "packed samples: uint8, two columns per lane");
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const uint32_t wk = k ? 0x01010000u : 0x00000101u;
+      const uint32_t sx = __builtin_amdgcn_udot4(v.w[0][0][1], wk,
+                                                 __builtin_amdgcn_udot4(v.w[0][0][0], wk, 0u, false), false);
+      const uint32_t yb = __builtin_amdgcn_perm(v.w[1][0][1], v.w[1][0][0], k ? 0x07060302u : 0x05040100u);
+      p[k] = __builtin_amdgcn_sad_hi_u8(yb, 0u, sx);
+    }
+  }
 };
 
 // Any element type, with or without downsampling, any strides: one sample
@@ -206,6 +230,7 @@ struct SrcGeneric {
   static constexpr int CH = LUMA ? 3 : 1;
   static constexpr int NV = DOWN ? 4 : 1;
   static constexpr bool FAST = std::is_same<T, uint8_t>::value || std::is_same<T, half_t>::value;
+  static constexpr bool PACKED = false;
   using S = double;
   struct Raw {
     T v[2][CH][NV];
@@ -321,6 +346,58 @@ __device__ inline void mag2(int gx1, int gy1, int gx2, int gy2, int& m1, int& m2
   m2 = __mul24(gx2, gx2) + __mul24(gy2, gy2);
   dm = m1 - m2;
 }
+// The Prewitt responses of both tensors at once: column k's samples of x and y
+// share one register (x low, y high half; see samples_xy), and the column
+// sums, row differences and their neighbours are formed on both halves by
+// packed 16-bit operations.  Every intermediate fits in int16: samples are at
+// most 1020, column sums 3060, row differences, gx and gy within +-3060.
+// M1 (x) and M2 (y) are then dot products of [gx, gy] with itself (the two
+// halves regathered by a byte permute), exact in int32.
+using short2_t = short __attribute__((ext_vector_type(2)));
+// v . v of two int16 lanes; the three-operand form with an inline zero (the
+// builtin's accumulating two-operand form costs a zeroing move per use)
+__device__ inline int sdot2_self(uint32_t v) {
+  int r;
+  asm("v_dot2_i32_i16 %0, %1, %1, 0" : "=v"(r) : "v"(v));
+  return r;
+}
+// a + b + c in one instruction (the compiler prefers two adds sharing a pair
+// sum across rows; on gfx950 every vector instruction of mixed code costs
+// about the same, so one is cheaper)
+__device__ inline uint32_t add3_u32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_add3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ inline void prewitt_xy(const uint32_t (&a)[2], const uint32_t (&b)[2],
+                                  const uint32_t (&c)[2], int (&m1)[2], int (&m2)[2]) {
+  uint32_t cs[2];
+  short2_t rd[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    cs[k] = add3_u32(a[k], b[k], c[k]);
+    rd[k] = __builtin_bit_cast(short2_t, a[k]) - __builtin_bit_cast(short2_t, c[k]);
+  }
+  // the next lane's two columns (zero past the wave: those columns are masked)
+  const short2_t ncs0 = __builtin_bit_cast(short2_t, wave_next(static_cast<int>(cs[0])));
+  const short2_t ncs1 = __builtin_bit_cast(short2_t, wave_next(static_cast<int>(cs[1])));
+  const short2_t nrd0 = __builtin_bit_cast(short2_t, wave_next(__builtin_bit_cast(int, rd[0])));
+  const short2_t nrd1 = __builtin_bit_cast(short2_t, wave_next(__builtin_bit_cast(int, rd[1])));
+  const short2_t gx0 = __builtin_bit_cast(short2_t, cs[0]) - ncs0;
+  const short2_t gx1 = __builtin_bit_cast(short2_t, cs[1]) - ncs1;
+  const short2_t t = rd[1] + nrd0;
+  const short2_t gy0 = rd[0] + t, gy1 = t + nrd1;
+  const short2_t gx[2] = {gx0, gx1}, gy[2] = {gy0, gy1};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t ux = __builtin_bit_cast(uint32_t, gx[k]), uy = __builtin_bit_cast(uint32_t, gy[k]);
+    const short2_t vx = __builtin_bit_cast(short2_t, __builtin_amdgcn_perm(uy, ux, 0x05040100u));
+    const short2_t vy = __builtin_bit_cast(short2_t, __builtin_amdgcn_perm(uy, ux, 0x07060302u));
+    m1[k] = sdot2_self(__builtin_bit_cast(uint32_t, vx));
+    m2[k] = sdot2_self(__builtin_bit_cast(uint32_t, vy));
+  }
+}
+
 __device__ inline void mag2(double gx1, double gy1, double gx2, double gy2, double& m1,
                             double& m2, double& dm) {
   m1 = fma(gx1, gx1, gy1 * gy1);
@@ -363,8 +440,14 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
 #pragma unroll
   for (int i = 0; i < G_PD; ++i) bufA[i] = src.load(srow(2 + i));
   S xa[NC], xb[NC], ya[NC], yb[NC];
-  src.samples(p0, xa, ya);
-  src.samples(p1, xb, yb);
+  uint32_t pa[NC], pb[NC];  // PACKED: x and y samples of a column in one register
+  if constexpr (Src::PACKED) {
+    src.samples_xy(p0, pa);
+    src.samples_xy(p1, pb);
+  } else {
+    src.samples(p0, xa, ya);
+    src.samples(p1, xb, yb);
+  }
 
   using Acc = typename std::conditional<Src::FAST, float, double>::type;
   // G_PD rows from `cur`, starting at row g of the run (FULL: all G_PD lie in
@@ -380,16 +463,35 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
 #pragma unroll
     for (int i = 0; i < G_PD; ++i) {
       if (decltype(full)::value || g + i < rows) {  // uniform
-        S xc[NC], yc[NC];
-        src.samples(cur[i], xc, yc);
-        S gx1[NC], gy1[NC], gx2[NC], gy2[NC];
-        prewitt<S, NC>(xa, xb, xc, gx1, gy1);
-        prewitt<S, NC>(ya, yb, yc, gx2, gy2);
+        S m1[NC], m2[NC], dm[NC];
+        if constexpr (Src::PACKED) {
+          uint32_t pc[NC];
+          src.samples_xy(cur[i], pc);
+          prewitt_xy(pa, pb, pc, m1, m2);
+#pragma unroll
+          for (int k = 0; k < NC; ++k) {
+            dm[k] = m1[k] - m2[k];
+            pa[k] = pb[k];
+            pb[k] = pc[k];
+          }
+        } else {
+          S xc[NC], yc[NC];
+          src.samples(cur[i], xc, yc);
+          S gx1[NC], gy1[NC], gx2[NC], gy2[NC];
+          prewitt<S, NC>(xa, xb, xc, gx1, gy1);
+          prewitt<S, NC>(ya, yb, yc, gx2, gy2);
+#pragma unroll
+          for (int k = 0; k < NC; ++k) {
+            mag2(gx1[k], gy1[k], gx2[k], gy2[k], m1[k], m2[k], dm[k]);
+            xa[k] = xb[k];
+            xb[k] = xc[k];
+            ya[k] = yb[k];
+            yb[k] = yc[k];
+          }
+        }
 #pragma unroll
         for (int k = 0; k < NC; ++k) {
-          S m1, m2, dm;
-          mag2(gx1[k], gy1[k], gx2[k], gy2[k], m1, m2, dm);
-          const Acc d = one_minus_q<Src::FAST, S>(m1, m2, dm, a.eps2f, a.T2f, a.eps2, a.T2);
+          const Acc d = one_minus_q<Src::FAST, S>(m1[k], m2[k], dm[k], a.eps2f, a.T2f, a.eps2, a.T2);
           if constexpr (MAP) {
             if (ok[k])
               map_plane[static_cast<int64_t>(up ? row0 + rows - 1 - g - i : row0 + g + i) *
@@ -397,13 +499,6 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
           }
           gs[k] += d;
           gs2[k] = fma(d, d, gs2[k]);
-        }
-#pragma unroll
-        for (int k = 0; k < NC; ++k) {
-          xa[k] = xb[k];
-          xb[k] = xc[k];
-          ya[k] = yb[k];
-          yb[k] = yc[k];
         }
       }
     }
@@ -728,7 +823,9 @@ template <class Src>
 static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipStream_t st,
                        int* wpi_used) {
   const bool map = a.map != nullptr;
-  const int wgs_per_cu = map ? occupancy_gmsd<Src, true>() : occupancy_gmsd<Src, false>();
+  // a workgroup is one wave on each of the CU's four SIMDs
+  const int wgs_per_cu = std::min(G_MAX_WAVES_PER_SIMD,
+                                  map ? occupancy_gmsd<Src, true>() : occupancy_gmsd<Src, false>());
   a.strips = (a.Wout + Src::OUTW - 1) / Src::OUTW;
   a.groups = (a.strips + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.rows_img = static_cast<int64_t>(a.Cout) * a.groups * a.Hout;
