@@ -346,6 +346,15 @@ __global__ __launch_bounds__(BLOCK) void pix_float_kernel(
 constexpr int SWEEP_UNROLL = FA_SWEEP_UNROLL;  // gridwide strides per round
 constexpr int SWEEP_BLOCK = FA_SWEEP_BLOCK;    // threads per workgroup (one per CU)
 constexpr int SWEEP_LDS_IMAGES = 32;           // batches up to this size sum waves in LDS
+// uint8 batches below this many bytes per tensor take the many-wave shape: 16
+// waves per CU with one 16-byte load in flight each per tensor, against 8
+// waves with two (the same bytes in flight, the same round).  Measured per
+// fa_gpu_pixel_reduce call, 8 / 16 / 24 x 3 x 1080 x 1920 and 5 / 6 / 7 x 3 x
+// 2160 x 3840: 8-15 % faster; 8 / 9 / 12 / 16 x 3 x 2160 x 3840 (199 MB and up
+// per tensor): 1.5-2.6 % slower, so those keep the two-load shape.
+constexpr int64_t SWEEP_MANY_WAVES_BELOW = 190000000;
+constexpr int SWEEP_MANY_BLOCK = 1024;
+constexpr int SWEEP_SLOTS_PER_CU = SWEEP_MANY_BLOCK / WAVE;  // workspace: the larger shape
 
 template <typename T, int OP>
 struct VecAcc {
@@ -515,34 +524,45 @@ __global__ __launch_bounds__(NT) void pix_sweep_kernel(
   }
 }
 
+// One sweep launch of shape (U, NT) over G workgroups, or 0 when a round of
+// it would span more than one image (the kernel touches at most two per
+// round; smaller images take the per-image grid).  Returns the partial columns
+// per image it writes: G for up to SWEEP_LDS_IMAGES images, G * NT / WAVE
+// beyond (packed at that stride).
+template <typename T, int OP, int U, int NT>
+static int launch_sweep_shape(hipStream_t st, const void* a, const void* b, int64_t n_images,
+                              int64_t nv, int64_t G, double param, void* partial) {
+  if (nv < static_cast<int64_t>(U) * G * NT) return 0;
+  const dim3 grid(static_cast<unsigned>(G));
+  if (n_images <= SWEEP_LDS_IMAGES) {
+    hipLaunchKernelGGL((pix_sweep_kernel<T, OP, true, U, NT>), grid, dim3(NT), 0, st,
+                       static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
+                       static_cast<int>(n_images), param, partial);
+    return static_cast<int>(G);
+  }
+  hipLaunchKernelGGL((pix_sweep_kernel<T, OP, false, U, NT>), grid, dim3(NT), 0, st,
+                     static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
+                     static_cast<int>(n_images), param, partial);
+  return static_cast<int>(G * (NT / WAVE));
+}
+
 // Launch of the sweep when it applies: 16-byte aligned bases, whole vectors
-// per image, bpi a multiple of the waves per workgroup (one workgroup per WPB
-// slots) and at least U gridwide strides per image.  Returns the partial
-// columns per image it writes (G for up to SWEEP_LDS_IMAGES images, bpi
-// beyond), or 0 when it does not apply and nothing was launched.
+// per image, bpi a multiple of SWEEP_SLOTS_PER_CU (one workgroup per CU) and
+// at least one round per image.  Returns the partial columns per image it
+// writes, or 0 when it does not apply and nothing was launched.
 template <typename T, int OP>
 static int launch_sweep(hipStream_t st, const void* a, const void* b, int64_t n_images,
                         int64_t per, int bpi, double param, void* partial) {
   constexpr int64_t E = 16 / static_cast<int64_t>(sizeof(T));
   const uintptr_t bases = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
-  constexpr int WPB = SWEEP_BLOCK / WAVE;
-  if ((bases & 15) != 0 || per % E != 0 || bpi % WPB != 0) return 0;
+  if ((bases & 15) != 0 || per % E != 0 || bpi % SWEEP_SLOTS_PER_CU != 0) return 0;
   const int64_t nv = per / E;
-  const int64_t G = bpi / WPB;
-  // the kernel needs a round to span no more than one image (so it touches
-  // at most two); smaller images take the per-image grid
-  if (nv < SWEEP_UNROLL * G * SWEEP_BLOCK) return 0;
-  const dim3 grid(static_cast<unsigned>(G));
-  if (n_images <= SWEEP_LDS_IMAGES) {
-    hipLaunchKernelGGL((pix_sweep_kernel<T, OP, true>), grid, dim3(SWEEP_BLOCK), 0, st,
-                       static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
-                       static_cast<int>(n_images), param, partial);
-    return static_cast<int>(G);
-  }
-  hipLaunchKernelGGL((pix_sweep_kernel<T, OP, false>), grid, dim3(SWEEP_BLOCK), 0, st,
-                     static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
-                     static_cast<int>(n_images), param, partial);
-  return bpi;
+  const int64_t G = bpi / SWEEP_SLOTS_PER_CU;
+  if (std::is_same<T, uint8_t>::value && per * n_images < SWEEP_MANY_WAVES_BELOW)
+    return launch_sweep_shape<T, OP, 1, SWEEP_MANY_BLOCK>(st, a, b, n_images, nv, G, param,
+                                                          partial);
+  return launch_sweep_shape<T, OP, SWEEP_UNROLL, SWEEP_BLOCK>(st, a, b, n_images, nv, G, param,
+                                                              partial);
 }
 
 template <typename T>
@@ -962,8 +982,8 @@ FA_API int fa_gpu_pixel_workspace(int64_t n_images, int64_t n_per_image,
   if (n_images <= 0 || n_per_image <= 0 || n_images > 65535) return FA_E_SHAPE;
   const int64_t cus = cu_count(device);
   if (n_per_image >= PIX_SWEEP_MIN_ELEMS) {
-    // the sweep: one workgroup per CU, one partial per wave
-    *out_bpi = static_cast<int>(cus * (SWEEP_BLOCK / WAVE));
+    // the sweep: one workgroup per CU, one partial per wave of its larger shape
+    *out_bpi = static_cast<int>(cus * SWEEP_SLOTS_PER_CU);
     return FA_OK;
   }
   const int64_t by_device = std::max<int64_t>(1, cus * PIX_WG_PER_CU / n_images);

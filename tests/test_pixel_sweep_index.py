@@ -78,7 +78,10 @@ def simulate_sweep(nv: int, n_images: int, G: int, NT: int, U: int):
 
 CASES = [
     # (nv, n_images, G, NT, U)
-    (1_555_200, 8, 256, 512, 2),   # configs[2] on a 256-CU part, the shipped shape
+    (1_555_200, 8, 256, 512, 2),   # configs[2] on a 256-CU part, the large-batch shape
+    (388_800, 8, 256, 1024, 1),    # configs[4] 8x3x1080x1920 uint8, the many-wave shape
+    (262_144, 3, 256, 1024, 1),    # many-wave shape, exactly one round per image
+    (300_001, 33, 256, 1024, 1),   # many-wave shape past the LDS image limit
     (1_555_200, 8, 256, 256, 4),   # the 4 x 256 launch shape
     (1_555_200, 8, 256, 512, 4),   # 4 x 512: a short last round, waves finish a round early
     (268_125, 3, 256, 256, 4),     # 3x3x1100x1300 uint8
