@@ -884,7 +884,8 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   // on emptying SIMDs -- lasts one small chunk instead of one of the uniform
   // size.  Keeping the chunk count, the first half of a column's chunks get
   // weight 1 and the rest 0.4 (on configs[1] 17,17,17,16 blocks become
-  // 24,24,10,9: 77.9 against 79.6 us, the same work and workgroup count).
+  // 24,24,10,9: 82.1 against 84.3 us per call over rotated input pairs, the
+  // same work and workgroup count).
   // It needs each XCD's range of tiles to hold whole planes (the count of
   // planes a multiple of 8); walked plane by plane instead it measured slower.
   if (best_chunks >= 2 && planes % NUM_XCD == 0) {
