@@ -259,6 +259,12 @@ struct SsimPol {
     }
   }
 
+  // emit reads nothing that the strip engine could load ahead of it (the
+  // upstream map of MODE_PREP stays a load in emit: prefetching it would
+  // take the float64 kernel past 256 registers, one wave per SIMD)
+  struct EIn {};
+  __device__ inline EIn emit_load(int, int) const { return EIn{}; }
+
   // Per output pixel, from the four filtered moments v = (E x', E y', E x'y',
   // E (x'-y')^2) with x' = x - shift, u = E x':
   //   A1 = 2 mu_x mu_y + C1 = 2 ux uy + 2 shift (ux + uy) + (2 shift^2 + C1)
@@ -266,7 +272,7 @@ struct SsimPol {
   //   A2 = 2 sigma_xy + C2,  sigma_xy = E x'y' - ux uy
   //   B2 = sigma_x^2 + sigma_y^2 + C2 = E (x'-y')^2 + A2 - (ux - uy)^2
   // `valid` masks lanes whose column lies outside the map.
-  __device__ inline void emit(int orow, int ocol, const CT* v, bool valid) {
+  __device__ inline void emit(int orow, int ocol, const CT* v, bool valid, const EIn&, int) {
     const CT ux = v[0];
     const CT uy = v[1];
     const CT p = ux * uy;
@@ -288,10 +294,13 @@ struct SsimPol {
     } else if (valid) {
       const CT mx = ux + shift;
       const CT my = uy + shift;
-      const CT iB1 = CT(1) / B1;
-      const CT iB2 = CT(1) / B2;
-      const CT S = A1 * A2 * iB1 * iB2;
-      const CT k = CT(2) * A2 * iB1 * iB2;
+      // one division, 1 / (B1 B2), and each reciprocal from it by a product
+      // (B1 >= C1 and B2 >= C2 keep the product far from under- and overflow)
+      const CT inv = CT(1) / (B1 * B2);
+      const CT iB1 = B2 * inv;
+      const CT iB2 = B1 * inv;
+      const CT S = A1 * A2 * inv;
+      const CT k = CT(2) * A2 * inv;
       const CT dmux = k * (my - mx * A1 * iB1);
       const CT dmuy = k * (mx - my * A1 * iB1);
       const int64_t idx = out_off + static_cast<int64_t>(orow) * Wout + ocol;
@@ -472,7 +481,7 @@ struct ScatterPol {
   const T* __restrict__ x;
   const T* __restrict__ y;
   int64_t img_off;
-  int W;
+  int H, W;
   double shift;
   T* __restrict__ dx;
   T* __restrict__ dy;
@@ -525,14 +534,63 @@ struct ScatterPol {
                           : static_cast<double>(static_cast<const float*>(g)[o]));
   }
 
-  __device__ inline void emit(int orow, int ocol, const double* v, bool valid) {
+  // Without dy, what emit reads for a lane's COLS_PER_LANE outputs of one
+  // row -- x, y and the pyramid gradient of the 2x2 blocks they belong to
+  // (the lane's first column is even: outputs k = 0, 1 share block 0, k = 2,
+  // 3 block 1) -- is loaded a phase ahead by the strip engine.  With dy the
+  // second set of registers would take the kernel past 256 (one wave per
+  // SIMD), so emit loads it itself.
+  static constexpr bool PRE = !DY;
+  struct EInPre {
+    T x[COLS_PER_LANE], y[COLS_PER_LANE];
+    double g[2];
+  };
+  struct EInNone {};
+  using EIn = typename std::conditional<PRE, EInPre, EInNone>::type;
+
+  __device__ inline EIn emit_load(int orow, int ocol) const {
+    EIn e;
+    if constexpr (PRE) {
+      const int r = orow < H ? orow : H - 1;
+      const int64_t base = img_off + static_cast<int64_t>(r) * W;
+#pragma unroll
+      for (int k = 0; k < COLS_PER_LANE; ++k) {
+        const int c = ocol + k < W ? ocol + k : W - 1;
+        e.x[k] = x[base + c];
+        e.y[k] = y[base + c];
+      }
+      e.g[0] = 0.0;
+      e.g[1] = 0.0;
+      if (gpx && Hp > 0 && Wp > 0) {  // uniform
+        const int pr = orow >> 1;
+        const int64_t prow = gp_off + static_cast<int64_t>(pr < Hp ? pr : Hp - 1) * Wp;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int pc = (ocol >> 1) + j;
+          const int64_t o = prow + (pc < Wp ? pc : Wp - 1);
+          const double t = gp_f64 ? static_cast<const double*>(gpx)[o]
+                                  : static_cast<double>(static_cast<const float*>(gpx)[o]);
+          e.g[j] = pr < Hp && pc < Wp ? 0.25 * t : 0.0;
+        }
+      }
+    }
+    return e;
+  }
+
+  __device__ inline void emit(int orow, int ocol, const double* v, bool valid, const EIn& e,
+                              int k) {
     if (!valid) return;
     const int64_t o = img_off + static_cast<int64_t>(orow) * W + ocol;
-    const double xv = static_cast<double>(x[o]) - shift;
-    const double yv = static_cast<double>(y[o]) - shift;
-    if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + pyr_grad(gpx, orow, ocol));
-    if constexpr (DY)
+    if constexpr (PRE) {
+      const double xv = static_cast<double>(e.x[k]) - shift;
+      const double yv = static_cast<double>(e.y[k]) - shift;
+      if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + e.g[k >> 1]);
+    } else {
+      const double xv = static_cast<double>(x[o]) - shift;
+      const double yv = static_cast<double>(y[o]) - shift;
+      if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + pyr_grad(gpx, orow, ocol));
       dy[o] = static_cast<T>(2.0 * yv * v[0] + xv * v[1] + v[3] + pyr_grad(gpy, orow, ocol));
+    }
   }
 };
 
@@ -558,6 +616,7 @@ __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
   pol.x = static_cast<const T*>(a.x);
   pol.y = static_cast<const T*>(a.y);
   pol.img_off = static_cast<int64_t>(plane) * a.H * a.W;
+  pol.H = a.H;
   pol.W = a.W;
   pol.shift = a.shift;
   pol.dx = static_cast<T*>(a.dx);

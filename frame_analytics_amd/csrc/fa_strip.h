@@ -23,15 +23,17 @@
 // What the lane loads (Pol::set_column once, Pol::load(row) per row; loads are
 // branch free, out-of-grid rows and columns are clamped or zeroed by the
 // policy), what it does with each raw row besides (Pol::pool: the MS-SSIM
-// pyramid step rides along, one (even, odd) row pair at a time), which moments it forms and what happens to each output pixel
-// (Pol::emit with a validity flag, Pol::end_row after each lane's four) is a
-// policy (see fa_ssim.hip): the SSIM forward (4 moments, float32 or
+// pyramid step rides along, one (even, odd) row pair at a time), which
+// moments it forms and what happens to each output pixel (Pol::emit with a
+// validity flag and what Pol::emit_load fetched for it a phase earlier,
+// Pol::end_row after each lane's four) is a policy (see fa_ssim.hip): the SSIM forward (4 moments, float32 or
 // float64), the backward coefficient pass, and the backward scatter (the
 // coefficient maps filtered back onto the full grid, which is the same
 // correlation with the input origin moved back by KW-1 and zero padding).
 #pragma once
 
 #include "fa_common.h"
+#include "fa_widen.h"
 
 namespace fa {
 
@@ -78,9 +80,14 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
   constexpr int VN = LdsVec<CT>::N;
   constexpr int NREAD = 16 / VN;  // 16-byte LDS reads per plane per lane
 
+  // float64 taps take their weights from scalar registers (22 vector
+  // registers fewer): widen_uniform converts on the scalar unit.
   CT w[KW];
 #pragma unroll
-  for (int j = 0; j < KW; ++j) w[j] = static_cast<CT>(win[j]);
+  for (int j = 0; j < KW; ++j) {
+    if constexpr (sizeof(CT) == 8) w[j] = widen_uniform(win[j]);
+    else w[j] = static_cast<CT>(win[j]);
+  }
 
   const int lane = threadIdx.x;
   const int col0 = strip * OUTW;          // first output column of the strip
@@ -121,6 +128,15 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
   const int hrow = threadIdx.x / WAVE;          // phase row of this wave
   const int oc_l = COLS_PER_LANE * (threadIdx.x % WAVE);  // strip-local output column
 
+  // What emit reads from memory for the lane's outputs (Pol::EIn: the input
+  // samples of the scatter, an upstream gradient map) is loaded one phase
+  // ahead, so its latency hides behind the next phase's vertical taps
+  // instead of stalling the horizontal pass.  Pol::emit_load clamps its
+  // addresses into the grid; rows and columns past it are never emitted.
+  using EIn = typename Pol::EIn;
+  static_assert(OUTW % 2 == 0, "a lane's first output column is even");
+  EIn ein = pol.emit_load(r0 + hrow, col0 + oc_l);
+
   for (int qc = 0; qc < nph; qc += NCYC) {
 #pragma unroll
     for (int u = 0; u < NCYC; ++u) {
@@ -136,17 +152,29 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
         for (int i = 0; i < PH; ++i) pend[i] = pol.load(in_row0 + KW - 1 + (q + 1) * PH + i);
 
         // ---- vertical taps, from the register ring ----------------------
+        // Ring row by ring row: the products a policy forms from a row (the
+        // float64 ring keeps x', y' only) are formed once and die at once,
+        // instead of staying live for all PH output rows that use them.
+        // Each output row still adds its taps in the order j = 0 .. KW-1.
         CT (*dst)[NP][HROW] = sbuf[q & 1];
+        CT v[PH][NP];
 #pragma unroll
-        for (int i = 0; i < PH; ++i) {
-          CT v[NP];
+        for (int i = 0; i < PH; ++i)
 #pragma unroll
-          for (int p = 0; p < NP; ++p) v[p] = CT(0);
+          for (int p = 0; p < NP; ++p) v[i][p] = CT(0);
 #pragma unroll
-          for (int j = 0; j < KW; ++j) pol.vtap(w[j], ring[(u * PH + i + j) % RS], v);
+        for (int r = 0; r < KW - 1 + PH; ++r) {
 #pragma unroll
-          for (int p = 0; p < NP; ++p) dst[i][p][lane] = v[p];
+          for (int i = 0; i < PH; ++i) {
+            const int j = r - i;
+            if (j >= 0 && j < KW) pol.vtap(w[j], ring[(u * PH + r) % RS], v[i]);
+          }
         }
+#pragma unroll
+        for (int i = 0; i < PH; ++i)
+#pragma unroll
+          for (int p = 0; p < NP; ++p) dst[i][p][lane] = v[i][p];
+        const EIn ein_next = pol.emit_load(r0 + (q + 1) * PH + hrow, col0 + oc_l);
         __syncthreads();
 
         // ---- horizontal taps, from LDS ----------------------------------
@@ -170,13 +198,24 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
               h[k][p] = a;
             }
           }
+          // float64: the sums are formed here, before the emits.  Left to
+          // itself the compiler sinks each column's taps into its emit's
+          // validity branch, which keeps every plane's 14 LDS values live
+          // until the last column (~70 registers more).
+          if constexpr (sizeof(CT) == 8) {
+#pragma unroll
+            for (int k = 0; k < COLS_PER_LANE; ++k)
+#pragma unroll
+              for (int p = 0; p < NP; ++p) asm volatile("" : "+v"(h[k][p]));
+          }
 #pragma unroll
           for (int k = 0; k < COLS_PER_LANE; ++k) {
             const int oc = col0 + oc_l + k;
-            pol.emit(r0 + orow_l, oc, h[k], oc_l + k < OUTW && oc < out_W);
+            pol.emit(r0 + orow_l, oc, h[k], oc_l + k < OUTW && oc < out_W, ein, k);
           }
           pol.end_row();
         }
+        ein = ein_next;
       }
     }
   }
