@@ -245,17 +245,26 @@ struct SsimPol {
     }
   }
 
-  // v += w * (x', y', x'y', (x'-y')^2) of one ring row
-  __device__ inline void vtap(CT w, const RT* m, CT* v) const {
-    v[0] = fma(w, m[0], v[0]);
-    v[1] = fma(w, m[1], v[1]);
-    if constexpr (NR == 4) {
+  // v += w * (x', y', x'y', (x'-y')^2) of one ring row.  At float64 the four
+  // moments pass through LDS in two sub-phases (x', y', then the products),
+  // halving the LDS per workgroup; s is the sub-phase (a constant once the
+  // engine's sub-phase loop is unrolled) and v holds that sub-phase's two.
+  static constexpr int NSUB = sizeof(CT) == 8 ? 2 : 1;
+  __device__ inline void vtap(CT w, const RT* m, CT* v, int s) const {
+    if constexpr (NSUB == 2) {
+      if (s == 0) {
+        v[0] = fma(w, m[0], v[0]);
+        v[1] = fma(w, m[1], v[1]);
+      } else {
+        const CT d = m[0] - m[1];
+        v[0] = fma(w, m[0] * m[1], v[0]);
+        v[1] = fma(w, d * d, v[1]);
+      }
+    } else {
+      v[0] = fma(w, m[0], v[0]);
+      v[1] = fma(w, m[1], v[1]);
       v[2] = fma(w, m[2], v[2]);
       v[3] = fma(w, m[3], v[3]);
-    } else {
-      const CT d = m[0] - m[1];
-      v[2] = fma(w, m[0] * m[1], v[2]);
-      v[3] = fma(w, d * d, v[3]);
     }
   }
 
@@ -341,7 +350,8 @@ struct SsimPol {
 
 template <typename T, typename CT, int MODE, int KW, bool LUMA = false>
 __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
-  __shared__ CT sbuf[2][PH][4][HROW];
+  using Pol = SsimPol<T, CT, MODE, LUMA>;
+  __shared__ CT sbuf[2][PH][Pol::NP / Pol::NSUB][HROW];
   __shared__ double sred[2 * WAVES_PER_BLOCK];
 
   const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
@@ -350,7 +360,6 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   const int chunk = tile / a.strips;
   const int strip = tile - chunk * a.strips;
 
-  using Pol = SsimPol<T, CT, MODE, LUMA>;
   Pol pol;
   {
     const int n = plane / a.Cout;
@@ -516,7 +525,11 @@ struct ScatterPol {
     for (int p = 0; p < NP; ++p) m[p] = r.v[p];
   }
 
-  __device__ inline void vtap(double w, const float* m, double* v) const {
+  // One LDS pass for all maps: splitting the four maps of dy in two halves
+  // the LDS per workgroup but takes the kernel to 189 registers, which
+  // holds it at two waves per SIMD all the same.
+  static constexpr int NSUB = 1;
+  __device__ inline void vtap(double w, const float* m, double* v, int) const {
 #pragma unroll
     for (int p = 0; p < NP; ++p) v[p] = fma(w, static_cast<double>(m[p]), v[p]);
   }
@@ -597,7 +610,7 @@ struct ScatterPol {
 template <typename T, int KW, bool DY>
 __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
   constexpr int NP = ScatterPol<T, DY>::NP;
-  __shared__ double sbuf[2][PH][NP][HROW];
+  __shared__ double sbuf[2][PH][NP / ScatterPol<T, DY>::NSUB][HROW];
 
   const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
   const int plane = t / a.bpp;

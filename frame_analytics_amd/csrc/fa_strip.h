@@ -69,10 +69,13 @@ template <class Pol, int KW>
 __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
                                     int off, int out_H, int out_W, int TH,
                                     int strip, int chunk,
-                                    typename Pol::CT (*sbuf)[PH][Pol::NP][HROW]) {
+                                    typename Pol::CT (*sbuf)[PH][Pol::NP / Pol::NSUB][HROW]) {
   using CT = typename Pol::CT;
   using Raw = typename Pol::Raw;
   constexpr int NP = Pol::NP;
+  constexpr int NSUB = Pol::NSUB;  // LDS sub-phases per phase
+  constexpr int NPL = NP / NSUB;   // moments per sub-phase
+  static_assert(NP % NSUB == 0, "sub-phases split the moments evenly");
   constexpr int OUTW = StripGeom<KW>::OUTW;
   constexpr int RS = StripGeom<KW>::RS;
   constexpr int NCYC = StripGeom<KW>::NCYC;
@@ -107,8 +110,9 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
   static_assert(KW % 2 == 1 && PH % 2 == 0, "row pairs must not straddle a phase");
   // The ring holds what the policy keeps per input row (Pol::NR values of
   // Pol::RT; Pol::moments fills a row, Pol::vtap adds one tap's weighted
-  // moments): the NP moments themselves, or fewer, narrower values the tap
-  // expands exactly, which frees registers for the float64 kernels.
+  // moments of sub-phase s): the NP moments themselves, or fewer, narrower
+  // values the tap expands exactly, which frees registers for the float64
+  // kernels.
   using RT = typename Pol::RT;
   constexpr int NR = Pol::NR;
   RT ring[RS][NR];
@@ -151,53 +155,64 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
 #pragma unroll
         for (int i = 0; i < PH; ++i) pend[i] = pol.load(in_row0 + KW - 1 + (q + 1) * PH + i);
 
-        // ---- vertical taps, from the register ring ----------------------
-        // Ring row by ring row: the products a policy forms from a row (the
-        // float64 ring keeps x', y' only) are formed once and die at once,
-        // instead of staying live for all PH output rows that use them.
-        // Each output row still adds its taps in the order j = 0 .. KW-1.
-        CT (*dst)[NP][HROW] = sbuf[q & 1];
-        CT v[PH][NP];
+        // The NP moments go through LDS in NSUB sub-phases of NPL each,
+        // alternating the two buffers: one barrier per sub-phase.  (The
+        // float64 forward splits its four moments in two, which halves its
+        // LDS per workgroup and lets more workgroups share a CU.)
+        const int orow_l = q * PH + hrow;
+        const bool out_lane = orow_l < rows_here && oc_l < OUTW;
+        CT h[COLS_PER_LANE][NP];
+        EIn ein_next;
 #pragma unroll
-        for (int i = 0; i < PH; ++i)
+        for (int s = 0; s < NSUB; ++s) {
+          // ---- vertical taps, from the register ring --------------------
+          // Ring row by ring row: the products a policy forms from a row
+          // (the float64 ring keeps x', y' only) are formed once and die at
+          // once.  Each output row still adds its taps in the order
+          // j = 0 .. KW-1.
+          CT (*dst)[NPL][HROW] = sbuf[(q * NSUB + s) & 1];
+          CT v[PH][NPL];
 #pragma unroll
-          for (int p = 0; p < NP; ++p) v[i][p] = CT(0);
+          for (int i = 0; i < PH; ++i)
 #pragma unroll
-        for (int r = 0; r < KW - 1 + PH; ++r) {
+            for (int p = 0; p < NPL; ++p) v[i][p] = CT(0);
 #pragma unroll
-          for (int i = 0; i < PH; ++i) {
-            const int j = r - i;
-            if (j >= 0 && j < KW) pol.vtap(w[j], ring[(u * PH + r) % RS], v[i]);
+          for (int r = 0; r < KW - 1 + PH; ++r) {
+#pragma unroll
+            for (int i = 0; i < PH; ++i) {
+              const int j = r - i;
+              if (j >= 0 && j < KW) pol.vtap(w[j], ring[(u * PH + r) % RS], v[i], s);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < PH; ++i)
+#pragma unroll
+            for (int p = 0; p < NPL; ++p) dst[i][p][lane] = v[i][p];
+          if (s == NSUB - 1) ein_next = pol.emit_load(r0 + (q + 1) * PH + hrow, col0 + oc_l);
+          __syncthreads();
+
+          // ---- horizontal taps, from LDS --------------------------------
+          if (out_lane) {
+#pragma unroll
+            for (int p = 0; p < NPL; ++p) {
+              CT in[16];
+              const V16* src = reinterpret_cast<const V16*>(&dst[hrow][p][oc_l]);
+#pragma unroll
+              for (int r = 0; r < NREAD; ++r) {
+                const V16 t = src[r];
+                __builtin_memcpy(&in[r * VN], &t, sizeof(V16));
+              }
+#pragma unroll
+              for (int k = 0; k < COLS_PER_LANE; ++k) {
+                CT a = CT(0);
+#pragma unroll
+                for (int j = 0; j < KW; ++j) a = fma(w[j], in[k + j], a);
+                h[k][s * NPL + p] = a;
+              }
+            }
           }
         }
-#pragma unroll
-        for (int i = 0; i < PH; ++i)
-#pragma unroll
-          for (int p = 0; p < NP; ++p) dst[i][p][lane] = v[i][p];
-        const EIn ein_next = pol.emit_load(r0 + (q + 1) * PH + hrow, col0 + oc_l);
-        __syncthreads();
-
-        // ---- horizontal taps, from LDS ----------------------------------
-        const int orow_l = q * PH + hrow;
-        if (orow_l < rows_here && oc_l < OUTW) {
-          CT h[COLS_PER_LANE][NP];
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            CT in[16];
-            const V16* src = reinterpret_cast<const V16*>(&dst[hrow][p][oc_l]);
-#pragma unroll
-            for (int r = 0; r < NREAD; ++r) {
-              const V16 t = src[r];
-              __builtin_memcpy(&in[r * VN], &t, sizeof(V16));
-            }
-#pragma unroll
-            for (int k = 0; k < COLS_PER_LANE; ++k) {
-              CT a = CT(0);
-#pragma unroll
-              for (int j = 0; j < KW; ++j) a = fma(w[j], in[k + j], a);
-              h[k][p] = a;
-            }
-          }
+        if (out_lane) {
           // float64: the sums are formed here, before the emits.  Left to
           // itself the compiler sinks each column's taps into its emit's
           // validity branch, which keeps every plane's 14 LDS values live
