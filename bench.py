@@ -506,6 +506,13 @@ def main():
 
     _clock_warmup(torch, loss_step, LEG_WARMUP_S)
     c3_ms = _time_steps(torch, loss_step, reps, 5) / reps * 1e3
+    # The same step with the autograd engine running the backward in the
+    # calling thread: by default it hands a GPU graph to its device thread and
+    # waits, and on these hosts that round trip costs more than the step's
+    # kernels (~0.15 ms of host time per step against ~85 us of kernels).
+    with torch.autograd.set_multithreading_enabled(False):
+        _clock_warmup(torch, loss_step, LEG_WARMUP_S)
+        c3_inline_ms = _time_steps(torch, loss_step, reps, 5) / reps * 1e3
     del x3, y3
 
     # ---------------- PSNR, configs[2] ---------------------------------- #
@@ -593,7 +600,8 @@ def main():
         },
         "configs4": c4,
         "configs3": {"workload": "1 - ssim(x, y) forward + backward, 16x3x256x256 float32",
-                     "ms_per_step": round(c3_ms, 4)},
+                     "ms_per_step": round(c3_ms, 4),
+                     "ms_per_step_backward_in_calling_thread": round(c3_inline_ms, 4)},
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
         "cpu_configs0": None if args.no_cpu_baseline else cpu_configs0(),
     }
