@@ -456,8 +456,20 @@ def main():
     mfma_tf = (None if mfma_count is None
                else round(mfma_count * MFMA_FLOP / (k_ms * 1e-3) / 1e12, 2))
 
-    # ---------------- configs[4]: MS-SSIM and GMSD on the same pairs ---- #
+    # configs[1]'s other two outputs: per-image values and the float32 map
+    # (8x3x1070x1910, 196 MB written per call besides the 99.5 MB read)
     reps = max(20, args.steps // 10)
+    c1 = {"workload": "fa.ssim on configs[1], 4 resident pairs rotated"}
+    map_bytes = 4.0 * n * c * (h - 10) * (w - 10)
+    for key, fn in (
+            ("none_ms", lambda i: fa.ssim(*pairs[i % 4], data_range=255.0, reduction="none")),
+            ("map_ms", lambda i: fa.ssim(*pairs[i % 4], data_range=255.0, return_map=True))):
+        _clock_warmup(torch, fn, LEG_WARMUP_S)
+        c1[key] = round(_time_steps(torch, fn, reps, 5) / reps * 1e3, 4)
+    c1["map_GBps"] = round((bytes_per_launch + map_bytes) / (c1["map_ms"] * 1e-3) / 1e9, 1)
+    torch.cuda.empty_cache()  # the maps' 196 MB blocks go back before the next legs
+
+    # ---------------- configs[4]: MS-SSIM and GMSD on the same pairs ---- #
     c4 = {"workload": "8x3x1080x1920 uint8 (configs[4]), 4 resident pairs rotated"}
     for key, fn in (
             ("ms_ssim_ms", lambda i: fa.ms_ssim(*pairs[i % 4], data_range=255.0)),
@@ -602,6 +614,7 @@ def main():
         "configs3": {"workload": "1 - ssim(x, y) forward + backward, 16x3x256x256 float32",
                      "ms_per_step": round(c3_ms, 4),
                      "ms_per_step_backward_in_calling_thread": round(c3_inline_ms, 4)},
+        "configs1_other_outputs": c1,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
         "cpu_configs0": None if args.no_cpu_baseline else cpu_configs0(),
     }

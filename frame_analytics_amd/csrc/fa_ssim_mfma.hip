@@ -442,10 +442,11 @@ __device__ inline void ssim_cs_px(const Epi& e, float U, float V, float X, float
 
 // Adds this lane's four outputs (rows row0 .. row0 + 3 of its column) to the
 // lane's float64 sums (MF_CSO: the cs values into acc); `full` (uniform) says
-// the whole 16 x 16 block lies inside the map.
+// the whole 16 x 16 block lies inside the map.  MF_MAP also returns the four
+// values in mv; the caller stores them (MF_MAP's stores in the kernel).
 template <int MODE, bool FULL>
 __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, bool col_ok,
-                              float* map_px, int Wout, double& acc, double& acc_cs) {
+                              float (&mv)[4], double& acc, double& acc_cs) {
   float rs = 0.0f, rcs = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -460,7 +461,7 @@ __device__ inline void finish(const Epi& e, const f4* o, int row0, int row_end, 
       rs += ok ? cs : 0.0f;
     } else if constexpr (MODE == MF_MAP) {
       const float s = ssim_px(e, o[0][i], o[1][i], o[2][i], o[3][i]);
-      if (ok) map_px[static_cast<int64_t>(i) * Wout] = s;
+      mv[i] = s;  // stored by the caller, after the branch (see MapOut)
       rs += ok ? s : 0.0f;
     } else {
       const float s = ssim_px_folded(e, o[0][i], o[1][i], o[2][i], o[3][i]);
@@ -485,16 +486,23 @@ struct Pool {
   uint32_t rstep;  // bytes per level row
   uint32_t lo;     // this lane's byte offset in a block's level rows (row 2g,
                    // its column), or out of every buffer's range when it stores nothing
-  bool half;       // float16 level (uint8 input), else float32
   h8 pm;           // the column-pair matrix fragment
 };
 
-// Stores through buffer resources whose base is the block's first level row
-// (scalar) and whose range ends at the last row this chunk writes: the lane's
-// offset is fixed, so a store costs no vector address arithmetic, and the range
-// check drops the rows past the chunk and the lanes that store nothing.
-template <bool PYR>
-__device__ inline void pool_frag(const Pool& pl, int j, const Frag& f) {
+// The 2 x 2 means of one block's level rows 2g and 2g + 1 (this lane's
+// column), x and y: float32, or (HALF) float16 packed in pairs, which keeps
+// them in two registers while they wait for the next block's loads.
+template <bool HALF>
+struct PoolOut {
+  float mx[2], my[2];
+};
+template <>
+struct PoolOut<true> {
+  uint32_t hx, hy;  // rows 2g (low half) and 2g + 1 (high half)
+};
+
+template <bool PYR, bool HALF>
+__device__ inline PoolOut<HALF> pool_frag(const Pool& pl, const Frag& f) {
   const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 sx = mfma(f.x, pl.pm, z);
   f4 sy = mfma(f.y, pl.pm, z);
@@ -505,6 +513,34 @@ __device__ inline void pool_frag(const Pool& pl, int j, const Frag& f) {
   // a sum of four is (S - 512) 2^-9 (uint8, float16 level) or S - 512: the
   // mean S / 4 is sum * k + 128
   constexpr float k = PYR ? 0.25f : 128.0f;
+  float mx[2], my[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    mx[q] = fmaf(sx[2 * q] + sx[2 * q + 1], k, 128.0f);
+    my[q] = fmaf(sy[2 * q] + sy[2 * q + 1], k, 128.0f);
+  }
+  PoolOut<HALF> po;
+  if constexpr (HALF) {
+    // exact: multiples of 1/4 in [0, 255]
+    po.hx = bc<uint32_t>(h2{static_cast<_Float16>(mx[0]), static_cast<_Float16>(mx[1])});
+    po.hy = bc<uint32_t>(h2{static_cast<_Float16>(my[0]), static_cast<_Float16>(my[1])});
+  } else {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      po.mx[q] = mx[q];
+      po.my[q] = my[q];
+    }
+  }
+  return po;
+}
+
+// Stores block j's means through buffer resources whose base is the block's
+// first level row (scalar) and whose range ends at the last row this chunk
+// writes: the lane's offset is fixed, so a store costs no vector address
+// arithmetic, and the range check drops the rows past the chunk and the lanes
+// that store nothing.  Four stores in every block.
+template <bool HALF>
+__device__ inline void pool_store(const Pool& pl, int j, const PoolOut<HALF>& po) {
   const int row = MT / 2 * j;  // the block's first level row, in this chunk
   const uint32_t boff = static_cast<uint32_t>(row) * pl.rstep;
   const int range = max(pl.rows - row, 0) * static_cast<int>(pl.rstep);
@@ -512,15 +548,14 @@ __device__ inline void pool_frag(const Pool& pl, int j, const Frag& f) {
   const auto ry = __builtin_amdgcn_make_buffer_rsrc(pl.by + boff, 0, range, MF_RSRC_WORD3);
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const float mx = fmaf(sx[2 * q] + sx[2 * q + 1], k, 128.0f);
-    const float my = fmaf(sy[2 * q] + sy[2 * q + 1], k, 128.0f);
     const int o = static_cast<int>(pl.lo + q * pl.rstep);  // level row 2g + q
-    if (pl.half) {  // uniform
-      __builtin_amdgcn_raw_buffer_store_b16(bc<unsigned short>(static_cast<_Float16>(mx)), rx, o, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b16(bc<unsigned short>(static_cast<_Float16>(my)), ry, o, 0, 0);
+    if constexpr (HALF) {
+      const int sh = 16 * q;
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(po.hx >> sh), rx, o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(po.hy >> sh), ry, o, 0, 0);
     } else {
-      __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(mx), rx, o, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(my), ry, o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(po.mx[q]), rx, o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(po.my[q]), ry, o, 0, 0);
     }
   }
 }
@@ -548,12 +583,24 @@ __device__ inline void vblock(const Weights& w, const VState& v, f4* o, float c2
   for (int q = 0; q < 4; ++q) o[q] = mfma(ah, bc<h8>(v.lo[q]), o[q]);
 }
 
+// What a CS pass writes besides its sums: no level, the next pyramid level in
+// float32, or in float16 (uint8 input only).
+enum { LVL_NONE = 0, LVL_F32 = 1, LVL_F16 = 2 };
+
 // uint8 and float16 levels: 4 waves per SIMD (128 VGPRs) fit without spills
-// and beat 3.
-template <int SRC, int MODE>
+// and beat 3; the uint8 cs-only pass writing a float32 level (which MS-SSIM
+// does not use: its first level is float16) needs more and runs 3.  LVL (CS
+// modes): the pyramid level the pass writes.
+template <int SRC, int MODE, int LVL>
 __global__ __launch_bounds__(BLOCK)
-__attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kernel(MfArgs a) {
+__attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1
+                                   : (SRC == SRC_U8 && MODE == MF_CSO && LVL == LVL_F32) ? 3
+                                                                                       : 4)))
+void ssim_mfma_kernel(MfArgs a) {
   constexpr bool PYR = SRC == SRC_F32;  // float32 samples: hi + lo operands
+  constexpr bool LEVEL = LVL != LVL_NONE;
+  static_assert(!LEVEL || MODE == MF_CS || MODE == MF_CSO, "levels come from the CS pass");
+  static_assert(LVL != LVL_F16 || SRC == SRC_U8, "float16 levels below uint8 input only");
   __shared__ double sred[2 * WAVES_PER_BLOCK];
   __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
   const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
@@ -574,7 +621,9 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     strip = tl - chunk * a.strips;
   }
   const int tile = chunk * a.strips + strip;
-  const int wave = static_cast<int>(threadIdx.x) / WAVE;
+  // uniform (a scalar register): every branch on the wave's columns is a
+  // scalar branch, so each path issues the same loads and stores
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / WAVE);
   const int lane = static_cast<int>(threadIdx.x) % WAVE;
   const int g = lane >> 4;
   const int n = lane & 15;
@@ -601,9 +650,14 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     const float k1 = 2.0f * 128.0f * 128.0f + a.C1;
     const Epi e = {k1, a.C2, 256.0f * k1, 256.0f * a.C2};
     const bool col_ok = c0 + n < a.Wout;
-    float* map_col = nullptr;
-    if constexpr (MODE == MF_MAP)
-      map_col = a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout + c0 + n;
+    // MF_MAP: the plane's map and the lane's fixed offset in a block (the host
+    // keeps a plane's map below 2^31 bytes)
+    float* const map_plane =
+        MODE == MF_MAP ? a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout : nullptr;
+    const uint32_t map_row = static_cast<uint32_t>(a.Wout) * 4u;
+    const uint32_t map_lane =
+        col_ok ? static_cast<uint32_t>(4 * g) * map_row + static_cast<uint32_t>(c0 + n) * 4u
+               : 0x80000000u;
 
     // The pyramid level: a wave's 32-column window pools to 16 columns, its
     // own 8 (c0/2 .. c0/2 + 7) and its right neighbour's 8.  Even waves store
@@ -614,17 +668,16 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     // everything up to 2 floor(H / 2).  Every row the chunk pools lies in one
     // of its H blocks.
     Pool pl = {};
-    if constexpr (MODE == MF_CS || MODE == MF_CSO) {
-      if (a.px) {  // uniform
+    if constexpr (LEVEL) {
+      {
         const int Wd = a.W / 2;
-        const int eb = a.level_f16 ? 2 : 4;
+        const int eb = LVL == LVL_F16 ? 2 : 4;
         const int row_end = r_lim >= a.Hout ? 2 * (a.H / 2) : r_lim;
         const int64_t first = (static_cast<int64_t>(plane) * (a.H / 2) + r0 / 2) * Wd * eb;
         pl.bx = static_cast<char*>(a.px) + first;
         pl.by = static_cast<char*>(a.py) + first;
         pl.rows = row_end / 2 - r0 / 2;
         pl.rstep = static_cast<uint32_t>(Wd * eb);
-        pl.half = a.level_f16 != 0;
         const bool last_wave = c0 + MT >= a.Wout;
         const bool lane_on = ((wave & 1) == 0 || last_wave) && c0 / 2 + n < Wd;
         // 0x80000000 lies past every range (a plane's level is below 2^31 bytes)
@@ -656,7 +709,13 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
     const int ext_x = (a.H - 1) * static_cast<int>(a.xsh) + a.W;
     const int ext_y = (a.H - 1) * static_cast<int>(a.ysh) + a.W;
     int bx = r0 * static_cast<int>(a.xsh), by = r0 * static_cast<int>(a.ysh);
-    auto load = [&](int, Raw<SRC>& r) {
+    const int nb = (r_end - r0 + MT - 1) / MT;  // output blocks; H blocks 0 .. nb
+    // Every step issues its load, whether or not its block is used, so that
+    // every path through the loop issues the same memory operations (the
+    // compiler then waits for the loads alone, see MapOut); a block past nb
+    // gets an empty range (uint8, float16: nothing is read) or re-reads the
+    // clamped last row (float32 levels).
+    auto load = [&](int j, Raw<SRC>& r) {
       if constexpr (PYR) {
         r.x0 = *reinterpret_cast<const float4*>(xp + xo);
         r.x1 = *reinterpret_cast<const float4*>(xp + xo + 4);
@@ -665,10 +724,11 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
         xo = min(xo + xstep, xmax);
         yo = min(yo + ystep, ymax);
       } else {
+        const bool live = j <= nb;  // uniform
         const auto rx = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<E*>(xp + bx), 0, max(ext_x - bx, 0) * EB, MF_RSRC_WORD3);
+            const_cast<E*>(xp + bx), 0, live ? max(ext_x - bx, 0) * EB : 0, MF_RSRC_WORD3);
         const auto ry = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<E*>(yp + by), 0, max(ext_y - by, 0) * EB, MF_RSRC_WORD3);
+            const_cast<E*>(yp + by), 0, live ? max(ext_y - by, 0) * EB : 0, MF_RSRC_WORD3);
         if constexpr (SRC == SRC_F16) {
           r.x = bc<u4>(__builtin_amdgcn_raw_buffer_load_b128(rx, vx, 0, 0));
           r.y = bc<u4>(__builtin_amdgcn_raw_buffer_load_b128(ry, vy, 0, 0));
@@ -682,55 +742,108 @@ __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1 : 4))) void ssim_mfma_kern
         by += static_cast<int>(ystep);
       }
     };
-    // horizontal pass of block j (and its share of the pyramid)
+    // horizontal pass of block j, and (LEVEL) its share of the pyramid, which
+    // the caller stores after issuing the next block's loads (pool_store)
+    // LATE: the level of block j waits in registers for the next block's
+    // loads and is stored after them.  The uint8 cs-only pass with a float32
+    // level has no four registers to spare (it would spill) and stores it
+    // inside hpass, before those loads.
+    constexpr bool HALF = LVL == LVL_F16;
+    constexpr bool LATE = LEVEL && !(SRC == SRC_U8 && MODE == MF_CSO && LVL == LVL_F32);
+    // GUARD: a step past the last block skips its loads and stores along
+    // with its horizontal pass.  Both forms give the compiler the same
+    // memory operations behind every wait (it waits with vmcnt(4) where a
+    // step stores); they differ in the registers the compiler ends up with:
+    // the guarded form keeps the uint8 kernels within 128 without spills,
+    // the unguarded one the float16 and float32 level kernels.
+    constexpr bool GUARD = SRC == SRC_U8;
+    PoolOut<HALF> po = {};
     auto hpass = [&](int j, const Raw<SRC>& r) {
       const Frag f = prep(r, a.one);
-      if constexpr (MODE == MF_CS || MODE == MF_CSO) {
-        if (a.px) pool_frag<PYR>(pl, j, f);  // uniform branch
+      if constexpr (LEVEL) {
+        po = pool_frag<PYR, HALF>(pl, f);
+        if constexpr (!LATE) pool_store<HALF>(pl, j, po);
       }
       return hmfma<PYR>(f, w);
     };
+    auto level_store = [&](int j) {
+      if constexpr (LATE) pool_store<HALF>(pl, j, po);
+    };
     auto epilogue = [&](int b, const f4* o) {
       const int row0 = r0 + MT * b + 4 * g;
-      float* mp = MODE == MF_MAP ? map_col + static_cast<int64_t>(row0) * a.Wout : nullptr;
+      float mv[4];
       if (r0 + MT * (b + 1) <= r_end && c0 + MT <= a.Wout)  // uniform: the whole block
-        finish<MODE, true>(e, o, row0, r_end, col_ok, mp, a.Wout, acc, acc_cs);
+        finish<MODE, true>(e, o, row0, r_end, col_ok, mv, acc, acc_cs);
       else
-        finish<MODE, false>(e, o, row0, r_end, col_ok, mp, a.Wout, acc, acc_cs);
+        finish<MODE, false>(e, o, row0, r_end, col_ok, mv, acc, acc_cs);
+      if constexpr (MODE == MF_MAP) {
+        // MF_MAP's stores: through a buffer resource whose base is the
+        // block's first map row (scalar) and whose range ends at the chunk's
+        // last row, at the lane's fixed offset of row 4g (0x80000000, past
+        // every range, for lanes whose column lies outside the map), so the
+        // range check drops the rows past the chunk and the columns past the
+        // map.  They sit outside the branch above: every path then issues the
+        // same four stores, and the compiler waits for the next block's loads
+        // alone (vmcnt(4)).  A store on some paths only made it wait for every
+        // store in flight (vmcnt(0)), which exposed the write latency once per
+        // block.
+        const int rb = r0 + MT * b;
+        const auto r = __builtin_amdgcn_make_buffer_rsrc(
+            map_plane + static_cast<int64_t>(rb) * a.Wout, 0,
+            max(r_end - rb, 0) * static_cast<int>(map_row), MF_RSRC_WORD3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(mv[i]), r, map_lane + i * map_row, 0, 0);
+      }
     };
 
     // Software pipeline: the horizontal MFMAs of block j + 2 are issued
     // between the vertical MFMAs of step j and its epilogue, so the matrix
     // cores and the vector ALU overlap within the wave too.
-    const int nb = (r_end - r0 + MT - 1) / MT;  // output blocks; H blocks 0 .. nb
+    //
+    // Memory order per step: the wait for block j's loads (in hpass), the
+    // loads of block j + 1, then the step's stores (the level of block j,
+    // the map of the step's output block).  The stores are unconditional
+    // (the range checks drop what lies past the chunk), so on every path into
+    // the next step's wait four stores follow the loads it waits for, and the
+    // compiler waits with vmcnt(4): the stores stay in flight.  The first
+    // step (peeled) is the only one whose loads may have nothing behind them.
     VState v;
     Raw<SRC> raw;
     load(0, raw);
     stash_all<0, PYR>(hpass(0, raw), a.one, v);
     load(1, raw);
+    level_store(0);
     HAcc hn = hpass(1, raw);
     load(2, raw);
-    for (int b = 0; b < nb; b += 2) {
-      {
-        stash_all<1, PYR>(hn, a.one, v);  // H_{b+1} next to H_b
-        f4 o[4];
-        vblock<0, MODE == MF_REDUCE || MODE == MF_CSO>(w, v, o, e.c2s);
+    level_store(1);
+    // step with output block b: PAR 0 finds H_b in the first half of the
+    // vertical operand and puts H_{b+1} in the second, PAR 1 the reverse
+    auto step = [&](int b, auto par) {
+      constexpr int PAR = decltype(par)::value;
+      stash_all<1 - PAR, PYR>(hn, a.one, v);  // H_{b+1} into the half H_{b-1} held
+      f4 o[4];
+      vblock<PAR, MODE == MF_REDUCE || MODE == MF_CSO>(w, v, o, e.c2s);
+      if constexpr (GUARD) {
         if (b + 2 <= nb) {  // uniform
           hn = hpass(b + 2, raw);
           load(b + 3, raw);
+          level_store(b + 2);
         }
-        epilogue(b, o);
+      } else {
+        if (b + 2 <= nb) hn = hpass(b + 2, raw);  // uniform
+        load(b + 3, raw);
+        level_store(b + 2);
       }
-      if (b + 1 < nb) {
-        stash_all<0, PYR>(hn, a.one, v);  // H_{b+2} over H_b
-        f4 o[4];
-        vblock<1, MODE == MF_REDUCE || MODE == MF_CSO>(w, v, o, e.c2s);
-        if (b + 3 <= nb) {
-          hn = hpass(b + 3, raw);
-          load(b + 4, raw);
-        }
-        epilogue(b + 1, o);
-      }
+      epilogue(b, o);
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    step(0, P0{});  // nb >= 1; with nb == 0 its sums and stores would be dropped
+    for (int b = 1; b < nb; b += 2) {
+      step(b, P1{});
+      if (b + 1 >= nb) break;
+      step(b + 1, P0{});
     }
   }
   // packed: each image owns C * tiles consecutive slots, as the finalize reads them
@@ -754,13 +867,14 @@ bool mfma_enabled() {
   return !(e && e[0] == '0');
 }
 
-template <int SRC, int MODE>
+template <int SRC, int MODE, int LVL>
 int occupancy() {
   static int occ = 0;
   if (occ <= 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, reinterpret_cast<const void*>(&ssim_mfma_kernel<SRC, MODE>), BLOCK, 0) != hipSuccess ||
+            &v, reinterpret_cast<const void*>(&ssim_mfma_kernel<SRC, MODE, LVL>), BLOCK, 0) !=
+            hipSuccess ||
         v <= 0)
       v = 1;
     occ = v;
@@ -768,24 +882,32 @@ int occupancy() {
   return occ;
 }
 
-// The kernel of (source, mode): its occupancy (launch == false) or its launch.
+// The kernel of (source, mode, level): its occupancy (launch == false) or its
+// launch.
+template <int SRC, int MODE, int LVL>
+int run(bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
+  if (!launch) return occupancy<SRC, MODE, LVL>();
+  hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MODE, LVL>), grid, dim3(BLOCK), 0, st, a);
+  return 0;
+}
+
+template <int SRC, int MODE>
+int run_cs(bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
+  if (!a.px) return run<SRC, MODE, LVL_NONE>(launch, grid, st, a);
+  if constexpr (SRC == SRC_U8) {
+    if (a.level_f16) return run<SRC, MODE, LVL_F16>(launch, grid, st, a);
+  }
+  return run<SRC, MODE, LVL_F32>(launch, grid, st, a);
+}
+
 // Pyramid levels come only through the CS pass (fa_gpu_ssim_cs_ex).
 template <int SRC>
 int dispatch(int mode, bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
-  if (mode == MF_CS) {
-    if (!launch) return occupancy<SRC, MF_CS>();
-    hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_CS>), grid, dim3(BLOCK), 0, st, a);
-  } else if (mode == MF_CSO) {
-    if (!launch) return occupancy<SRC, MF_CSO>();
-    hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_CSO>), grid, dim3(BLOCK), 0, st, a);
-  } else if constexpr (SRC == SRC_U8) {
-    if (mode == MF_MAP) {
-      if (!launch) return occupancy<SRC, MF_MAP>();
-      hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_MAP>), grid, dim3(BLOCK), 0, st, a);
-    } else {
-      if (!launch) return occupancy<SRC, MF_REDUCE>();
-      hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MF_REDUCE>), grid, dim3(BLOCK), 0, st, a);
-    }
+  if (mode == MF_CS) return run_cs<SRC, MF_CS>(launch, grid, st, a);
+  if (mode == MF_CSO) return run_cs<SRC, MF_CSO>(launch, grid, st, a);
+  if constexpr (SRC == SRC_U8) {
+    if (mode == MF_MAP) return run<SRC, MF_MAP, LVL_NONE>(launch, grid, st, a);
+    return run<SRC, MF_REDUCE, LVL_NONE>(launch, grid, st, a);
   }
   return 0;
 }
@@ -824,6 +946,8 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   // the last output row (their range check stops them at the plane's end)
   const int64_t eb = src == SRC_F32 ? 4 : src == SRC_F16 ? 2 : 1;
   if ((static_cast<int64_t>(c.H) + 48) * std::max(c.xsh, c.ysh) * eb > INT32_MAX) return FA_OK;
+  // the map is written through buffer resources with 32-bit offsets in a plane
+  if (mode == MF_MAP && static_cast<int64_t>(c.Hout) * c.Wout * 4 > INT32_MAX) return FA_OK;
 
   MfArgs a = {};
   a.x = c.x;

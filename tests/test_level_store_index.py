@@ -9,7 +9,8 @@ and the hardware drops every store whose offset is not below the range.  This
 model replays that arithmetic for every workgroup, wave, block and lane of a
 launch -- every uniform chunk height the host may pick, and the big-then-small
 chunk lists it builds from them -- and checks that each element of each
-plane's level is written, and only from inside that plane.
+plane's level is written, and only from inside that plane, and that the
+stores of the steps past a chunk's last block write nothing.
 """
 
 from __future__ import annotations
@@ -79,7 +80,11 @@ def level_writes(N, C, H, W, K, TH, eb, short_rows=0, col_shift=0, nbig=None, TH
                     lo = np.where(lane_on, (2 * g * Wd + c0 // 2 + n + col_shift) * eb,
                                   0x80000000)
                     lo = np.broadcast_to(lo, (4, 16))
-                    for j in range(nb + 1):  # H blocks 0 .. nb
+                    # H blocks 0 .. nb, and the two steps past the last
+                    # block, whose stores the float16 / float32 level passes
+                    # issue anyway (with the previous block's values): the
+                    # range check must drop every one of those
+                    for j in range(nb + 3):
                         row = MT // 2 * j
                         rng = max(rows - short_rows - row, 0) * rstep
                         for q in range(2):
@@ -87,6 +92,8 @@ def level_writes(N, C, H, W, K, TH, eb, short_rows=0, col_shift=0, nbig=None, TH
                             kept = o < rng  # the range check (unsigned offsets)
                             if not kept.any():
                                 continue
+                            if j > nb:
+                                return count, False
                             assert np.all(o[kept] % eb == 0)
                             elem = first + row * Wd + o[kept] // eb
                             lo_plane, hi_plane = plane * Hd * Wd, (plane + 1) * Hd * Wd
