@@ -8,6 +8,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fa_abi.h"
 
 namespace fa {
@@ -211,6 +213,28 @@ int launch_finalize(const void* partial, bool exact, int nrows, int ncols,
                     double* out_per_row, double* out_total,
                     double* out_psnr_per_row, double* out_psnr_total,
                     hipStream_t st);
+
+// Stores a lane may or may not make, issued on every path: a buffer resource
+// over one output row (scalar base, range: the row's bytes, or nothing for a
+// null output) and the lane's byte offset in it, or 0x80000000 -- past every
+// range -- where the lane has nothing to store, so the range check drops it.
+template <typename E>
+__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(E* row, int ncols) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<typename std::remove_const<E>::type*>(row), 0,
+                                           row ? ncols * static_cast<int>(sizeof(E)) : 0,
+                                           0x00020000);
+}
+template <typename E>
+__device__ inline uint32_t lane_off(int col, bool on) {
+  return on ? static_cast<uint32_t>(col) * static_cast<uint32_t>(sizeof(E)) : 0x80000000u;
+}
+__device__ inline void row_store(float v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+}
+__device__ inline void row_store(double v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, 0);
+}
 
 }  // namespace fa
 

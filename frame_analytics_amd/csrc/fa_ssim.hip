@@ -292,15 +292,17 @@ struct SsimPol {
     const CT B2 = fma(-du, du, v[3] + A2);
     if constexpr (MODE == MODE_REDUCE || MODE == MODE_MAP) {
       const CT s = quot(A1 * A2, B1 * B2);
-      if constexpr (MODE == MODE_MAP) {
-        if (valid) map[out_off + static_cast<int64_t>(orow) * Wout + ocol] = static_cast<float>(s);
-      }
+      if constexpr (MODE == MODE_MAP)
+        row_store(static_cast<float>(s), row_rsrc(map + out_off + static_cast<int64_t>(orow) * Wout, Wout),
+                  lane_off<float>(ocol, valid));
       row_s += valid ? s : CT(0);
     } else if constexpr (MODE == MODE_CS) {
       const CT inv = quot(CT(1), B1 * B2);
       row_s += valid ? A1 * A2 * inv : CT(0);
       row_cs += valid ? A2 * B1 * inv : CT(0);
     } else if (valid) {
+      // the backward coefficients keep their guarded stores: issued on every
+      // path (row_store) they measured slower (configs[3] 27.0 -> 32.3 us)
       const CT mx = ux + shift;
       const CT my = uy + shift;
       // one division, 1 / (B1 B2), and each reciprocal from it by a product
@@ -592,13 +594,16 @@ struct ScatterPol {
 
   __device__ inline void emit(int orow, int ocol, const double* v, bool valid, const EIn& e,
                               int k) {
-    if (!valid) return;
-    const int64_t o = img_off + static_cast<int64_t>(orow) * W + ocol;
     if constexpr (PRE) {
+      // every lane stores, through a row buffer resource (see row_store)
       const double xv = static_cast<double>(e.x[k]) - shift;
       const double yv = static_cast<double>(e.y[k]) - shift;
-      if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + e.g[k >> 1]);
+      row_store(static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + e.g[k >> 1]),
+                row_rsrc(dx ? dx + img_off + static_cast<int64_t>(orow) * W : nullptr, W),
+                lane_off<T>(ocol, valid));
     } else {
+      if (!valid) return;
+      const int64_t o = img_off + static_cast<int64_t>(orow) * W + ocol;
       const double xv = static_cast<double>(x[o]) - shift;
       const double yv = static_cast<double>(y[o]) - shift;
       if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + pyr_grad(gpx, orow, ocol));

@@ -129,7 +129,10 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
 #pragma unroll
   for (int i = 0; i < PH; ++i) pend[i] = pol.load(in_row0 + KW - 1 + i);
 
-  const int hrow = threadIdx.x / WAVE;          // phase row of this wave
+  // phase row of this wave, in a scalar register: the row of every output a
+  // wave emits is uniform, so a policy can address its output row with a
+  // scalar buffer resource
+  const int hrow = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / WAVE);
   const int oc_l = COLS_PER_LANE * (threadIdx.x % WAVE);  // strip-local output column
 
   // What emit reads from memory for the lane's outputs (Pol::EIn: the input
@@ -192,7 +195,13 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
           __syncthreads();
 
           // ---- horizontal taps, from LDS --------------------------------
-          if (out_lane) {
+          // Every lane runs them (a lane past the strip's outputs reads
+          // columns up to oc_l + 15 < HROW) and every lane emits, with
+          // `valid` false where there is no output: the policies' stores are
+          // then issued on every path, so the wait for the next phase's loads
+          // does not wait for them (a store on some paths only made the
+          // compiler wait for every store in flight).
+          {
 #pragma unroll
             for (int p = 0; p < NPL; ++p) {
               CT in[16];
@@ -212,7 +221,7 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
             }
           }
         }
-        if (out_lane) {
+        {
           // float64: the sums are formed here, before the emits.  Left to
           // itself the compiler sinks each column's taps into its emit's
           // validity branch, which keeps every plane's 14 LDS values live
@@ -226,7 +235,7 @@ __device__ inline void strip_engine(Pol& pol, const float* __restrict__ win,
 #pragma unroll
           for (int k = 0; k < COLS_PER_LANE; ++k) {
             const int oc = col0 + oc_l + k;
-            pol.emit(r0 + orow_l, oc, h[k], oc_l + k < OUTW && oc < out_W, ein, k);
+            pol.emit(r0 + orow_l, oc, h[k], out_lane && oc_l + k < OUTW && oc < out_W, ein, k);
           }
           pol.end_row();
         }
