@@ -65,6 +65,8 @@ SIGNATURES = {
     "fa_gpu_ms_ssim_reduce": ([_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _P], _I),
     "fa_gpu_ssim_noalloc":
         ([_P, _P, _I, _I, _I, _I, _I, _P, _I, _D, _D, _D, _P, _P, _P, _I, _P], _I),
+    "fa_gpu_pixel_reduce_once":
+        ([_P, _P, _I, _L, _L, _I, _D, _D, _P, _I, _P, _P, _P, _P, _P, _I, _P], _I),
     "fa_gpu_ssim_cs_backward_ex":
         ([_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _D, _D, _D, _P, _P, _I, _P, _P, _P,
           _I, _P], _I),

@@ -321,6 +321,29 @@ def workspace_slots(kind: str, a: int, b: int, c: int) -> int:
 # --------------------------------------------------------------------------- #
 
 
+#: uint64 words of fa_gpu_pixel_reduce_once's accumulator (FA_PIXEL_ACC_WORDS)
+_PIXEL_ACC_WORDS = (32 + 1) * 16
+#: (device, raw stream) -> that stream's accumulator, zero between calls
+_pixel_acc: dict = {}
+
+
+def _pixel_acc_for(device: torch.device, dev: int, stream: int) -> Optional[torch.Tensor]:
+    """The zeroed accumulator that lets exact uint8 reductions finish inside
+    their one sweep launch (``fa_gpu_pixel_reduce_once``).  Each call leaves it
+    zero again, so one buffer serves every call on its stream, in stream
+    order; calls on another stream get their own.  Under graph capture there
+    is none (the call takes the two-launch form): a graph's replays could
+    overlap eager calls of the stream that recorded it."""
+    if torch._C._cuda_isCurrentStreamCapturing():
+        return None
+    key = (dev, stream)
+    acc = _pixel_acc.get(key)
+    if acc is None:
+        acc = torch.zeros(_PIXEL_ACC_WORDS, dtype=torch.int64, device=device)
+        _pixel_acc[key] = acc
+    return acc
+
+
 def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
               param: float, per_image: bool, psnr_bias: float,
               luma: Optional[tuple] = None) -> torch.Tensor:
@@ -341,8 +364,10 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
     slot = (2 if psnr_bias != _PSNR_NONE else 0) + (0 if per_image else 1)
     sinks = [_ptr(out) if i == slot else None for i in range(4)]
     if luma is None and xs is None and ys is None:
-        _run("fa_gpu_pixel_reduce", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op,
-             float(param), float(psnr_bias), _ptr(partial), bpi, *sinks, dev, stream)
+        acc = _pixel_acc_for(x.device, dev, stream) if x.dtype == torch.uint8 else None
+        _run("fa_gpu_pixel_reduce_once", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op,
+             float(param), float(psnr_bias), _ptr(partial), bpi, _ptr(acc), *sinks, dev,
+             stream)
     else:
         _run("fa_gpu_pixel_reduce_ex", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w,
              xs, ys, _luma_arg(luma), op, float(param), float(psnr_bias), _ptr(partial), bpi,

@@ -425,10 +425,64 @@ struct VecAcc {
   }
 };
 
-template <typename T, int OP, bool LDSP, int U = SWEEP_UNROLL, int NT = SWEEP_BLOCK>
+// --------------------------------------------------------------------------
+// The single-launch finish of the exact uint8 sums (fa_gpu_pixel_reduce_once).
+//
+// Each workgroup adds its per-image sums, and its sum over the whole batch,
+// to caller-owned accumulator words with ONE returning device-scope atomic
+// per word that also counts the contribution: a word holds
+// (sum << FIN_COUNT_BITS) + count.  The atomic's return value is the word
+// before this add, so the workgroup whose add brings a word's count to
+// gridDim.x holds that word's complete sum in registers (every other
+// contribution is ordered before its own on that word) and finishes it
+// itself: the mean, the dB, and a reset of the word to zero.  The image words
+// and the batch word are added by different lanes of one instruction, so the
+// call's tail is one atomic round trip.  No fence and no cache write-back is
+// needed: nothing is read except through the returning atomics.  Each word
+// sits on its own 128-byte line.
+//
+// The host allows the form only where every packed sum fits: the batch's
+// n_total * max_term < 2^(64 - FIN_COUNT_BITS), which bounds the images too.
+// --------------------------------------------------------------------------
+constexpr int FIN_COUNT_BITS = 12;  // contributions per word: gridDim.x <= 4095
+constexpr int FIN_STRIDE = 16;      // uint64 words between accumulators (128 bytes)
+static_assert(FA_PIXEL_ACC_WORDS == (SWEEP_LDS_IMAGES + 1) * FIN_STRIDE,
+              "the ABI's accumulator size");
+
+struct SweepFin {
+  uint64_t* acc;  // (n_images + 1) * FIN_STRIDE words, zero on entry and on exit
+  double n_per_image, n_total, psnr_bias;
+  double *out_per_image, *out_total, *out_psnr_per_image, *out_psnr_total;
+};
+
+// Thread-level: adds workgroup sum `t` to word `i` (image i, or the batch when
+// i == n_images) and finishes the word when this is its last contribution.
+__device__ inline void fin_word(const SweepFin& f, int i, int n_images, uint64_t t) {
+  uint64_t* w = f.acc + static_cast<int64_t>(i) * FIN_STRIDE;
+  const uint64_t old = __hip_atomic_fetch_add(w, (t << FIN_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+  constexpr uint64_t CM = (uint64_t(1) << FIN_COUNT_BITS) - 1;
+  if ((old & CM) + 1u != gridDim.x) return;
+  __hip_atomic_store(w, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool batch = i == n_images;
+  const double v = static_cast<double>((old >> FIN_COUNT_BITS) + t) /
+                   (batch ? f.n_total : f.n_per_image);
+  double* mean = batch ? f.out_total : (f.out_per_image ? f.out_per_image + i : nullptr);
+  double* db = batch ? f.out_psnr_total
+                     : (f.out_psnr_per_image ? f.out_psnr_per_image + i : nullptr);
+  if (mean) *mean = v;
+  if (f.psnr_bias != FA_PSNR_NONE && db) *db = f.psnr_bias - 10.0 * log10(v);
+}
+
+// FIN (exact uint8 sums, LDSP only): the workgroup finishes through
+// fin_word instead of writing partials; each wave also keeps its sum over the
+// whole batch for the batch word.
+template <typename T, int OP, bool LDSP, int U = SWEEP_UNROLL, int NT = SWEEP_BLOCK,
+          bool FIN = false>
 __global__ __launch_bounds__(NT) void pix_sweep_kernel(
     const uint4* __restrict__ a, const uint4* __restrict__ b, int64_t nv, int n_images,
-    double param, void* __restrict__ partial) {
+    double param, void* __restrict__ partial, SweepFin fin) {
+  static_assert(!FIN || (LDSP && VecAcc<T, OP>::EXACT), "the one-launch finish takes exact sums");
   using Acc = VecAcc<T, OP>;
   constexpr int WPB = NT / WAVE;
   // LDSP: the waves' image sums wait in LDS and each workgroup writes one
@@ -436,6 +490,8 @@ __global__ __launch_bounds__(NT) void pix_sweep_kernel(
   // then reads G instead of G * WPB per image); otherwise every wave writes
   // its own, partial[img * G * WPB + wave].
   __shared__ uint64_t s_p[LDSP ? SWEEP_LDS_IMAGES * WPB : 1];
+  __shared__ uint64_t s_all[FIN ? WPB : 1];
+  uint64_t wave_all = 0;  // FIN: this wave's sum over the batch
   const int64_t gs = static_cast<int64_t>(gridDim.x) * NT;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
   const int64_t w0 = t0 - (threadIdx.x & (WAVE - 1));  // lane 0 of this wave
@@ -503,6 +559,7 @@ __global__ __launch_bounds__(NT) void pix_sweep_kernel(
     const int64_t next = base + U * gs + w0;
     while (img < n_images && next >= edge) {
       const uint64_t bits = cur.wave_bits();
+      if constexpr (FIN) wave_all += bits;
       if (lead) {
         if constexpr (LDSP) s_p[img * WPB + wave] = bits;
         else reinterpret_cast<uint64_t*>(partial)[img * bpi + wslot] = bits;
@@ -513,13 +570,28 @@ __global__ __launch_bounds__(NT) void pix_sweep_kernel(
       edge += nv;
     }
   }
+  if constexpr (FIN) {
+    if (lead) s_all[wave] = wave_all;
+  }
   if constexpr (LDSP) {
     __syncthreads();  // every wave has left the walk
     for (int i = static_cast<int>(threadIdx.x); i < n_images; i += NT) {
       uint64_t t = s_p[i * WPB];
 #pragma unroll
       for (int w = 1; w < WPB; ++w) t = Acc::add_bits(t, s_p[i * WPB + w]);
-      reinterpret_cast<uint64_t*>(partial)[static_cast<int64_t>(i) * gridDim.x + blockIdx.x] = t;
+      if constexpr (FIN) fin_word(fin, i, n_images, t);
+      else reinterpret_cast<uint64_t*>(partial)[static_cast<int64_t>(i) * gridDim.x + blockIdx.x] = t;
+    }
+    if constexpr (FIN) {
+      // the batch word, from a lane of the first wave that no image took
+      // (n_images <= SWEEP_LDS_IMAGES < WAVE)
+      const bool any_total = fin.out_total || (fin.psnr_bias != FA_PSNR_NONE && fin.out_psnr_total);
+      if (static_cast<int>(threadIdx.x) == n_images && any_total) {
+        uint64_t t = s_all[0];
+#pragma unroll
+        for (int w = 1; w < WPB; ++w) t += s_all[w];
+        fin_word(fin, n_images, n_images, t);
+      }
     }
   }
 }
@@ -529,30 +601,43 @@ __global__ __launch_bounds__(NT) void pix_sweep_kernel(
 // round; smaller images take the per-image grid).  Returns the partial columns
 // per image it writes: G for up to SWEEP_LDS_IMAGES images, G * NT / WAVE
 // beyond (packed at that stride).
+// With `fin` (exact sums of at most SWEEP_LDS_IMAGES images only) the launch
+// finishes the call itself and returns -1.
 template <typename T, int OP, int U, int NT>
 static int launch_sweep_shape(hipStream_t st, const void* a, const void* b, int64_t n_images,
-                              int64_t nv, int64_t G, double param, void* partial) {
+                              int64_t nv, int64_t G, double param, void* partial,
+                              const SweepFin* fin) {
   if (nv < static_cast<int64_t>(U) * G * NT) return 0;
   const dim3 grid(static_cast<unsigned>(G));
+  const uint4* va = static_cast<const uint4*>(a);
+  const uint4* vb = static_cast<const uint4*>(b);
+  const int ni = static_cast<int>(n_images);
+  if constexpr (VecAcc<T, OP>::EXACT) {
+    if (fin) {
+      hipLaunchKernelGGL((pix_sweep_kernel<T, OP, true, U, NT, true>), grid, dim3(NT), 0, st,
+                         va, vb, nv, ni, param, partial, *fin);
+      return -1;
+    }
+  }
   if (n_images <= SWEEP_LDS_IMAGES) {
-    hipLaunchKernelGGL((pix_sweep_kernel<T, OP, true, U, NT>), grid, dim3(NT), 0, st,
-                       static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
-                       static_cast<int>(n_images), param, partial);
+    hipLaunchKernelGGL((pix_sweep_kernel<T, OP, true, U, NT>), grid, dim3(NT), 0, st, va, vb,
+                       nv, ni, param, partial, SweepFin{});
     return static_cast<int>(G);
   }
-  hipLaunchKernelGGL((pix_sweep_kernel<T, OP, false, U, NT>), grid, dim3(NT), 0, st,
-                     static_cast<const uint4*>(a), static_cast<const uint4*>(b), nv,
-                     static_cast<int>(n_images), param, partial);
+  hipLaunchKernelGGL((pix_sweep_kernel<T, OP, false, U, NT>), grid, dim3(NT), 0, st, va, vb, nv,
+                     ni, param, partial, SweepFin{});
   return static_cast<int>(G * (NT / WAVE));
 }
 
 // Launch of the sweep when it applies: 16-byte aligned bases, whole vectors
 // per image, bpi a multiple of SWEEP_SLOTS_PER_CU (one workgroup per CU) and
 // at least one round per image.  Returns the partial columns per image it
-// writes, or 0 when it does not apply and nothing was launched.
+// writes, -1 when it finished the call through `fin`, or 0 when it does not
+// apply and nothing was launched.
 template <typename T, int OP>
 static int launch_sweep(hipStream_t st, const void* a, const void* b, int64_t n_images,
-                        int64_t per, int bpi, double param, void* partial) {
+                        int64_t per, int bpi, double param, void* partial,
+                        const SweepFin* fin) {
   constexpr int64_t E = 16 / static_cast<int64_t>(sizeof(T));
   const uintptr_t bases = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
   if ((bases & 15) != 0 || per % E != 0 || bpi % SWEEP_SLOTS_PER_CU != 0) return 0;
@@ -560,20 +645,20 @@ static int launch_sweep(hipStream_t st, const void* a, const void* b, int64_t n_
   const int64_t G = bpi / SWEEP_SLOTS_PER_CU;
   if (std::is_same<T, uint8_t>::value && per * n_images < SWEEP_MANY_WAVES_BELOW)
     return launch_sweep_shape<T, OP, 1, SWEEP_MANY_BLOCK>(st, a, b, n_images, nv, G, param,
-                                                          partial);
+                                                          partial, fin);
   return launch_sweep_shape<T, OP, SWEEP_UNROLL, SWEEP_BLOCK>(st, a, b, n_images, nv, G, param,
-                                                              partial);
+                                                              partial, fin);
 }
 
 template <typename T>
 static int launch_sweep_op(int op, hipStream_t st, const void* a, const void* b,
                            int64_t n_images, int64_t per, int bpi, double param,
-                           void* partial) {
+                           void* partial, const SweepFin* fin = nullptr) {
   switch (op) {
-    case FA_OP_MSE: return launch_sweep<T, FA_OP_MSE>(st, a, b, n_images, per, bpi, param, partial);
-    case FA_OP_L1: return launch_sweep<T, FA_OP_L1>(st, a, b, n_images, per, bpi, param, partial);
-    case FA_OP_CHARB: return launch_sweep<T, FA_OP_CHARB>(st, a, b, n_images, per, bpi, param, partial);
-    default: return launch_sweep<T, FA_OP_HUBER>(st, a, b, n_images, per, bpi, param, partial);
+    case FA_OP_MSE: return launch_sweep<T, FA_OP_MSE>(st, a, b, n_images, per, bpi, param, partial, fin);
+    case FA_OP_L1: return launch_sweep<T, FA_OP_L1>(st, a, b, n_images, per, bpi, param, partial, fin);
+    case FA_OP_CHARB: return launch_sweep<T, FA_OP_CHARB>(st, a, b, n_images, per, bpi, param, partial, nullptr);
+    default: return launch_sweep<T, FA_OP_HUBER>(st, a, b, n_images, per, bpi, param, partial, nullptr);
   }
 }
 
@@ -1001,6 +1086,20 @@ FA_API int fa_gpu_pixel_reduce(const void* a, const void* b, int dtype,
                                double* out_total, double* out_psnr_per_image,
                                double* out_psnr_total, int device,
                                void* stream) {
+  return fa_gpu_pixel_reduce_once(a, b, dtype, n_images, n_per_image, op, param, psnr_bias,
+                                  partial, bpi, nullptr, out_per_image, out_total,
+                                  out_psnr_per_image, out_psnr_total, device, stream);
+}
+
+// No counterpart in the reference: fa_gpu_pixel_reduce whose exact uint8 sums
+// (MSE / PSNR / L1 over the sweep) finish inside the sweep launch through
+// `acc`, a caller-owned zeroed buffer the call leaves zeroed.
+FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
+                                    int64_t n_images, int64_t n_per_image, int op,
+                                    double param, double psnr_bias, double* partial,
+                                    int bpi, uint64_t* acc, double* out_per_image,
+                                    double* out_total, double* out_psnr_per_image,
+                                    double* out_psnr_total, int device, void* stream) {
   if (!a || !b || !partial) return FA_E_ARG;
   if (op < 0 || op > 3) return FA_E_OP;
   if (n_images <= 0 || n_per_image <= 0 || bpi <= 0) return FA_E_SHAPE;
@@ -1010,10 +1109,41 @@ FA_API int fa_gpu_pixel_reduce(const void* a, const void* b, int dtype,
   const dim3 grid(static_cast<unsigned>(bpi), static_cast<unsigned>(n_images));
   const uintptr_t rel = reinterpret_cast<uintptr_t>(a) - reinterpret_cast<uintptr_t>(b);
 
+  // the one-launch finish: exact uint8 sums, a wanted output, and every
+  // packed word within its bits (the batch's sum below 2^52, so each image's
+  // is too; the contribution count below 2^12)
+  SweepFin fin = {};
+  const SweepFin* pfin = nullptr;
+  const bool want = out_per_image || out_total ||
+                    (psnr_bias != FA_PSNR_NONE && (out_psnr_per_image || out_psnr_total));
+  if (acc && want && dtype == FA_U8 && (op == FA_OP_MSE || op == FA_OP_L1) &&
+      n_images <= SWEEP_LDS_IMAGES && bpi / SWEEP_SLOTS_PER_CU < (1 << FIN_COUNT_BITS)) {
+    const int64_t term = op == FA_OP_MSE ? 255 * 255 : 255;
+    const int64_t lim = (int64_t(1) << (64 - FIN_COUNT_BITS)) / term;
+    if (n_per_image < lim / n_images) {
+      fin.acc = acc;
+      fin.n_per_image = static_cast<double>(n_per_image);
+      fin.n_total = static_cast<double>(n_per_image) * static_cast<double>(n_images);
+      fin.psnr_bias = psnr_bias;
+      fin.out_per_image = out_per_image;
+      fin.out_total = out_total;
+      fin.out_psnr_per_image = out_psnr_per_image;
+      fin.out_psnr_total = out_psnr_total;
+      pfin = &fin;
+    }
+  }
+
   bool exact = false;
   int swept = 0;  // partial columns per image the sweep wrote, 0 if it did not run
   switch (dtype) {
-    case FA_U8: swept = launch_sweep_op<uint8_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
+    case FA_U8:
+      swept = launch_sweep_op<uint8_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial,
+                                       pfin);
+      if (swept < 0) {  // finished inside the sweep
+        FA_LAUNCH_CHECK();
+        return FA_OK;
+      }
+      break;
     case FA_F16: swept = launch_sweep_op<half_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
     case FA_BF16: swept = launch_sweep_op<bf16_t>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;
     case FA_F32: swept = launch_sweep_op<float>(op, st, a, b, n_images, n_per_image, bpi, param, partial); break;

@@ -350,6 +350,29 @@ FA_API int fa_gpu_ssim_noalloc(const void* x, const void* y, int dtype, int N,
                                float* map_out, double* out_per_image,
                                double* out_total, int device, void* stream);
 
+/*
+ * No counterpart in the reference, whose pixel reductions always end in a
+ * separate finalize launch (fa_cuda.cu:1150-1155).  fa_gpu_pixel_reduce (same
+ * arguments, same results bit for bit) plus `acc`: FA_PIXEL_ACC_WORDS uint64
+ * of device memory that is zero when the call starts and that the call leaves
+ * zero when it completes.  Where the sums are exact -- dtype FA_U8, op
+ * FA_OP_MSE or FA_OP_L1, contiguous batches the one-workgroup-per-CU sweep
+ * takes (images of >= 4 Mi elements, 16-byte aligned), at most 32 images --
+ * the sweep finishes the call itself: each workgroup adds its per-image sums
+ * to `acc` with returning device-scope atomics, and the workgroup that adds
+ * an image's last sum writes that image's outputs (and the batch's, after the
+ * batch's last image).  One launch instead of two.  Every other call ignores
+ * `acc` (it may be null) and runs as fa_gpu_pixel_reduce.  `acc` is state of
+ * one stream: calls that may overlap (two streams) need one buffer each.
+ */
+#define FA_PIXEL_ACC_WORDS ((32 + 1) * 16)
+FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
+                                    int64_t n_images, int64_t n_per_image, int op,
+                                    double param, double psnr_bias, double* partial,
+                                    int bpi, uint64_t* acc, double* out_per_image,
+                                    double* out_total, double* out_psnr_per_image,
+                                    double* out_psnr_total, int device, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -39,7 +39,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 20  # 12 reference entry points + 8 extensions
+    assert len(decl) == 21  # 12 reference entry points + 9 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -106,6 +106,11 @@ def test_argument_validation_before_any_gpu_work(lib):
                                    None, None, None, None, 0, None) == 4  # FA_E_OP
     assert lib.fa_gpu_pixel_reduce(p, p, 0, 0, 16, 0, 0.0, -1e300, p, 1,
                                    None, None, None, None, 0, None) == 2
+    once = lib.fa_gpu_pixel_reduce_once
+    assert once(p, p, 0, 1, 16, 0, 0.0, -1e300, None, 1, p, p, None, None, None, 0, None) == 5
+    assert once(p, p, 0, 1, 16, 4, 0.0, -1e300, p, 1, p, p, None, None, None, 0, None) == 4
+    assert once(p, p, 0, 70000, 16, 0, 0.0, -1e300, p, 1, p, p, None, None, None, 0,
+                None) == 2
     assert lib.fa_gpu_ssim(p, p, 0, 1, 1, 64, 64, p, 12, 0.5, 1e-4, 9e-4, None, p, 1,
                            None, None, 0, None) == 3
     assert lib.fa_gpu_ssim(p, p, 0, 1, 1, 64, 64, p, 11, 0.5, 1e-4, 9e-4, None, p, 99,

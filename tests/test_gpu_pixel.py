@@ -310,3 +310,107 @@ def test_any_workspace_size_exact(gpu, n):
                               None, 0, stream)
         assert rc == 0, (bpi, rc)
         assert np.array_equal(out.cpu().numpy(), want), bpi
+
+
+def _reduce(name, x, y, op, n, per, bpi, acc, sinks, stream):
+    from frame_analytics_amd import backend
+
+    part = torch.empty((n, bpi), dtype=torch.float64, device=x.device)
+    args = [x.data_ptr(), y.data_ptr(), 0, n, per, op, 0.0,
+            10.0 * math.log10(255.0 ** 2), part.data_ptr(), bpi]
+    if name == "fa_gpu_pixel_reduce_once":
+        args.append(None if acc is None else acc.data_ptr())
+    rc = backend.call_gpu(name, *args, *[s.data_ptr() for s in sinks], 0, stream)
+    assert rc == 0, (name, n, per, bpi, rc)
+
+
+@pytest.mark.parametrize("n,hw,bpis", [
+    (1, (2048, 2048), (None, 16, 64, 65536, 1000)),
+    (5, (2048, 2048), (None, 16, 4080)),
+    (32, (2048, 2048), (None,)),            # the largest batch the one-launch form takes
+    (33, (2048, 2048), (None,)),            # beyond it: two launches, acc untouched
+    (32, (64, 1024), (16, 32)),             # small images, few workgroups
+    (7, (1100, 1300), (None, 48)),          # a round straddles two images
+])
+def test_single_launch_finish_matches_two_launches(gpu, n, hw, bpis):
+    """fa_gpu_pixel_reduce_once: the exact uint8 MSE / L1 sums finished inside
+    the sweep by returning atomics give the same per-image and total values,
+    and the same dB, bit for bit, as fa_gpu_pixel_reduce (itself exact against
+    the oracle's integer sums), for workspace shapes that take the one-launch
+    form and ones that do not; the accumulator is zero after every call,
+    including a second, smaller call on the same buffer."""
+    from frame_analytics_amd import backend
+
+    g = torch.Generator(device=gpu)
+    g.manual_seed(n * 7 + hw[0])
+    shape = (n, 1) + hw
+    x = torch.randint(0, 256, shape, dtype=torch.uint8, device=gpu, generator=g)
+    y = (x.to(torch.int16) + torch.randint(-9, 10, shape, dtype=torch.int16, device=gpu,
+                                           generator=g)).clamp(0, 255).to(torch.uint8)
+    per = hw[0] * hw[1]
+    stream = torch.cuda.current_stream().cuda_stream
+    acc = torch.zeros(backend._PIXEL_ACC_WORDS, dtype=torch.int64, device=gpu)
+    a_np, b_np = x.cpu().numpy(), y.cpu().numpy()
+    for op, isum in ((0, ref.sse_u8(a_np, b_np, per_image=True)),
+                     (1, ref.sad_u8(a_np, b_np, per_image=True))):
+        isum = [int(v) for v in isum]
+        want = np.asarray(isum, dtype=np.float64) / float(per)
+        for bpi in bpis:
+            bpi = backend.workspace_slots("pixel", n, per, 0) if bpi is None else bpi
+            for m in (n, max(1, n - 2)):  # a second, smaller call on the same acc
+                xs, ys = x[:m], y[:m]
+                two = [torch.full((m,), -1.0, dtype=torch.float64, device=gpu),
+                       torch.full((), -1.0, dtype=torch.float64, device=gpu),
+                       torch.full((m,), -1.0, dtype=torch.float64, device=gpu),
+                       torch.full((), -1.0, dtype=torch.float64, device=gpu)]
+                one = [t.clone() for t in two]
+                _reduce("fa_gpu_pixel_reduce", xs, ys, op, m, per, bpi, None, two, stream)
+                _reduce("fa_gpu_pixel_reduce_once", xs, ys, op, m, per, bpi, acc, one, stream)
+                for t1, t2 in zip(one, two):
+                    assert torch.equal(t1, t2), (op, bpi, m, t1, t2)
+                assert np.array_equal(one[0].cpu().numpy(), want[:m]), (op, bpi, m)
+                assert float(one[1]) == float(sum(isum[:m])) / float(per * m)
+                assert not bool(acc.any()), (op, bpi, m, acc.nonzero())
+            # only the total wanted, then only per-image values: the image
+            # finishers still run, and the total word is left zero either way
+            for pick in ((1,), (0,), (3,), (2,)):
+                outs = [torch.full((n,) if i % 2 == 0 else (), -1.0, dtype=torch.float64,
+                                   device=gpu) for i in range(4)]
+                sinks = [outs[i] if i in pick else None for i in range(4)]
+                part = torch.empty((n, bpi), dtype=torch.float64, device=gpu)
+                rc = backend.call_gpu(
+                    "fa_gpu_pixel_reduce_once", x.data_ptr(), y.data_ptr(), 0, n, per, op, 0.0,
+                    10.0 * math.log10(255.0 ** 2), part.data_ptr(), bpi, acc.data_ptr(),
+                    *[None if s is None else s.data_ptr() for s in sinks], 0, stream)
+                assert rc == 0
+                if 0 in pick:
+                    assert np.array_equal(outs[0].cpu().numpy(), want)
+                if 1 in pick:
+                    assert float(outs[1]) == float(sum(isum)) / float(per * n)
+                assert not bool(acc.any()), (op, bpi, pick)
+
+
+def test_single_launch_finish_per_stream(gpu):
+    """fa.mse / fa.psnr on two streams at once: each stream has its own
+    accumulator, so interleaved calls stay exact."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((3, 1, 2048, 2048), 7.0, seed=11)
+    c, d = u8_pair((2, 3, 1100, 1300), 3.0, seed=12)
+    ta, tb, tc, td = (_t(v, gpu) for v in (a, b, c, d))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(4):
+        with torch.cuda.stream(s1):
+            outs.append(("ab", fa.mse(ta, tb, reduction="none")))
+        with torch.cuda.stream(s2):
+            outs.append(("cd", fa.mse(tc, td, reduction="none")))
+    torch.cuda.synchronize()
+    for key, o in outs:
+        want = ref.mse(a, b, "none") if key == "ab" else ref.mse(c, d, "none")
+        assert np.array_equal(o.cpu().numpy(), want), key
+    keys = [k for k in backend._pixel_acc if k[1] in (s1.cuda_stream, s2.cuda_stream)]
+    assert len(keys) == 2
+    for k in keys:
+        assert not bool(backend._pixel_acc[k].any())
