@@ -321,26 +321,27 @@ def workspace_slots(kind: str, a: int, b: int, c: int) -> int:
 # --------------------------------------------------------------------------- #
 
 
-#: uint64 words of fa_gpu_pixel_reduce_once's accumulator (FA_PIXEL_ACC_WORDS)
-_PIXEL_ACC_WORDS = (32 + 1) * 16
-#: (device, raw stream) -> that stream's accumulator, zero between calls
-_pixel_acc: dict = {}
+#: uint64 words of the one-launch entry points' accumulators
+#: (FA_PIXEL_ACC_WORDS, FA_GMSD_ACC_WORDS)
+_ACC_WORDS = {"pixel": (32 + 1) * 16, "gmsd": (3 * 64 + 2) * 16}
+#: (kind, device, raw stream) -> that stream's accumulator, zero between calls
+_stream_acc: dict = {}
 
 
-def _pixel_acc_for(device: torch.device, dev: int, stream: int) -> Optional[torch.Tensor]:
-    """The zeroed accumulator that lets exact uint8 reductions finish inside
-    their one sweep launch (``fa_gpu_pixel_reduce_once``).  Each call leaves it
-    zero again, so one buffer serves every call on its stream, in stream
-    order; calls on another stream get their own.  Under graph capture there
-    is none (the call takes the two-launch form): a graph's replays could
-    overlap eager calls of the stream that recorded it."""
+def _acc_for(kind: str, device: torch.device, dev: int, stream: int) -> Optional[torch.Tensor]:
+    """The zeroed accumulator that lets a reduction finish inside its one
+    launch (``fa_gpu_pixel_reduce_once``, ``fa_gpu_gmsd_once``).  Each call
+    leaves it zero again, so one buffer serves every call on its stream, in
+    stream order; calls on another stream get their own.  Under graph capture
+    there is none (the call takes its two-launch form): a graph's replays
+    could overlap eager calls of the stream that recorded it."""
     if torch._C._cuda_isCurrentStreamCapturing():
         return None
-    key = (dev, stream)
-    acc = _pixel_acc.get(key)
+    key = (kind, dev, stream)
+    acc = _stream_acc.get(key)
     if acc is None:
-        acc = torch.zeros(_PIXEL_ACC_WORDS, dtype=torch.int64, device=device)
-        _pixel_acc[key] = acc
+        acc = torch.zeros(_ACC_WORDS[kind], dtype=torch.int64, device=device)
+        _stream_acc[key] = acc
     return acc
 
 
@@ -364,7 +365,7 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
     slot = (2 if psnr_bias != _PSNR_NONE else 0) + (0 if per_image else 1)
     sinks = [_ptr(out) if i == slot else None for i in range(4)]
     if luma is None and xs is None and ys is None:
-        acc = _pixel_acc_for(x.device, dev, stream) if x.dtype == torch.uint8 else None
+        acc = _acc_for("pixel", x.device, dev, stream) if x.dtype == torch.uint8 else None
         _run("fa_gpu_pixel_reduce_once", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op,
              float(param), float(psnr_bias), _ptr(partial), bpi, _ptr(acc), *sinks, dev,
              stream)
@@ -764,12 +765,13 @@ def try_gmsd(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float, downsamp
 def _gmsd_native(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float,
                  downsample: bool, luma: Optional[tuple] = None, want_map: bool = False):
     """``(gms_mean, gmsd)`` per image, float64 -- plus the float32 q map when
-    ``want_map`` -- or ``None`` if unavailable.
+    ``want_map``, or else their two batch means as a third, (2,) tensor -- or
+    ``None`` if unavailable.
 
     ``luma`` = (kr, kg, kb[, offset]) makes the kernel read the three channels
     and form the luma plane itself; cropped views are read in place through
-    their strides (``fa_gpu_gmsd_ex``).  CPU tensors run ``fa_cpu_gmsd``
-    (statistics only: no luma, no map).
+    their strides (``fa_gpu_gmsd_ex`` / ``fa_gpu_gmsd_once``).  CPU tensors
+    run ``fa_cpu_gmsd`` (statistics only: no luma, no map).
     """
     n, c, h, w = (int(v) for v in x.shape)
     hd, wd = (h // 2, w // 2) if downsample else (h, w)
@@ -791,29 +793,40 @@ def _gmsd_native(x: torch.Tensor, y: torch.Tensor, *, T: float, eps: float,
     x, xs = _view_strides(x)
     y, ys = _view_strides(y)
     planes = n * (1 if luma is not None else c)
-    mean, std, qmap = _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes,
-                                   want_map, hd, wd)
-    return (mean, std, qmap) if want_map else (mean, std)
+    return _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, wd)
 
 
-def _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, wd):
+def _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, wd,
+                 separate=False):
+    """``(mean, std, qmap)`` with the map, else ``(mean, std, batch)``: the
+    batch means of both.  Without the map the statistics come from
+    ``fa_gpu_gmsd_once``, which finishes a uint8 call inside its one launch.
+    ``separate``: mean and std in allocations of their own (autograd outputs),
+    not views of one."""
     n, c, h, w = (int(v) for v in x.shape)
     bpp = workspace_slots("gmsd", h, w, int(bool(downsample)))
     dev, stream = _site(x)
-    # one allocation for both workspaces and one for both outputs (each torch
+    # one allocation for both workspaces and one for the outputs (each torch
     # allocation is ~1.7 us of host time)
     psum, psumsq = _f64(x.device, 2, planes, bpp).unbind(0)
-    mean, std = _f64(x.device, 2, n).unbind(0)
-    qmap = (torch.empty((n, planes // n, hd - 2, wd - 2), dtype=torch.float32,
-                        device=x.device) if want_map else None)
     head = (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w)
     consts = (float(T), float(eps), int(bool(downsample)))
-    sums = (_ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(std), dev, stream)
-    if luma is None and xs is None and ys is None and qmap is None:
-        _run("fa_gpu_gmsd", *head, *consts, *sums)
+    if want_map:
+        mean, std = _f64(x.device, 2, n).unbind(0)
+        qmap = torch.empty((n, planes // n, hd - 2, wd - 2), dtype=torch.float32,
+                           device=x.device)
+        _run("fa_gpu_gmsd_ex", *head, xs, ys, _luma_arg(luma), *consts, _ptr(qmap),
+             _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(std), dev, stream)
+        return mean, std, qmap
+    if separate:
+        mean, std, batch = _f64(x.device, n), _f64(x.device, n), None
     else:
-        _run("fa_gpu_gmsd_ex", *head, xs, ys, _luma_arg(luma), *consts, _ptr(qmap), *sums)
-    return mean, std, qmap
+        out = _f64(x.device, 2 * n + 2)
+        mean, std, batch = out[:n], out[n:2 * n], out[2 * n:]
+    acc = _acc_for("gmsd", x.device, dev, stream) if x.dtype == torch.uint8 else None
+    _run("fa_gpu_gmsd_once", *head, xs, ys, _luma_arg(luma), *consts, _ptr(psum),
+         _ptr(psumsq), bpp, _ptr(acc), _ptr(mean), _ptr(std), _ptr(batch), dev, stream)
+    return mean, std, batch
 
 
 def gmsd_autograd_available(x: torch.Tensor, y: torch.Tensor) -> bool:
@@ -827,7 +840,7 @@ def gmsd_stats_fwd(x, y, T, eps, downsample):
     n, c, h, w = (int(v) for v in x.shape)
     hd, wd = (h // 2, w // 2) if downsample else (h, w)
     mean, std, _ = _gmsd_launch(x, y, None, None, None, T, eps, downsample, n * c, False,
-                                hd, wd)
+                                hd, wd, separate=True)
     return mean, std
 
 

@@ -77,6 +77,12 @@ struct GmsdArgs {
   double* psum;
   double* psumsq;
   float* map;                // optional q map, [N * Cout, Hout, Wout]
+  // the one-launch finish (gmsd_kernel<..., FIN>): accumulator words, the
+  // fixed-point scale 2^F of the per-image sums and its inverse, and outputs
+  uint64_t* acc;
+  double fscale, finv, npix;
+  double *out_mean, *out_std, *out_batch;
+  int N;
 };
 
 // d = 1 - q from the squared gradient magnitudes M1, M2 (without eps) and
@@ -96,9 +102,10 @@ __device__ inline typename std::conditional<FAST, float, double>::type one_minus
     // at most 2, and where that is a large share of dm, d is below 1e-14.
     // Other sources pass dm exactly.
     const float n = std::is_integral<S>::value ? f1 - f2 : static_cast<float>(dm);
-    // e_f and t_f arrive floored at 1e-18 (gmsd_impl), so A (Gs + t_f) >=
-    // 6e-36, a normal float32: the reciprocal is finite and a flat pixel's
-    // 0 / 0 (eps = T = 0) comes out 0
+    // positive e_f and t_f arrive floored at 1e-18 (gmsd_impl), so where
+    // either is positive A (Gs + t_f) >= 1e-36, a normal float32, and the
+    // reciprocal is finite; with both zero a flat pixel's 0 * rcp(0) is NaN,
+    // the reference's 0 / 0
     return (n * n) * __builtin_amdgcn_rcpf(A * (Gs + t_f));
   } else {
     const double G1 = static_cast<double>(m1) + e_d;
@@ -106,7 +113,7 @@ __device__ inline typename std::conditional<FAST, float, double>::type one_minus
     const double Gs = G1 + G2;
     const double A = fma(2.0, sqrt(G1 * G2), Gs);
     const double n = static_cast<double>(dm);
-    return dm != S(0) ? (n * n) / (A * (Gs + t_d)) : 0.0;
+    return (n * n) / (A * (Gs + t_d));  // 0 / 0 = NaN on a flat patch with T = eps = 0
   }
 }
 
@@ -126,6 +133,7 @@ struct SrcU8Wide {
   static constexpr int OUTW = G_OUTW_WIDE;
   static constexpr int CH = LUMA ? 3 : 1;
   static constexpr bool FAST = true;
+  static constexpr bool U8IN = true;     // uint8 input: every sample finite
   static constexpr bool PACKED = !LUMA;  // samples_xy / prewitt_xy
   using S = typename std::conditional<LUMA, double, int>::type;
   struct Raw {
@@ -230,6 +238,7 @@ struct SrcGeneric {
   static constexpr int CH = LUMA ? 3 : 1;
   static constexpr int NV = DOWN ? 4 : 1;
   static constexpr bool FAST = std::is_same<T, uint8_t>::value || std::is_same<T, half_t>::value;
+  static constexpr bool U8IN = std::is_same<T, uint8_t>::value;
   static constexpr bool PACKED = false;
   using S = double;
   struct Raw {
@@ -529,7 +538,94 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
   }
 }
 
-template <class Src, bool MAP>
+// --------------------------------------------------------------------------
+// The one-launch finish (fa_gpu_gmsd_once), for uint8 input with T or eps
+// positive, where every d = 1 - q is finite and in [0, 1].
+//
+// A workgroup's sums of d and d^2 go to two accumulator words of its image as
+// fixed-point integers, round(sum * 2^F) with F = 52 - bits(pixels per image
+// + 1), packed with a contribution count: word = (value << GF_COUNT_BITS) +
+// count.  One returning device-scope atomic per word adds both at once, and
+// integer addition does not depend on the order, so the result is the same
+// from run to run.  The workgroup whose add brings a word's count to the
+// image's workgroup count holds that word's complete sum.  The two words of
+// an image may be completed by different workgroups, which meet on a third
+// word: each exchanges its completed value (with a presence bit and a bit
+// saying which sum it is) into it, and the one that gets the other's value
+// back holds both, writes the image's mean q = 1 - mean d and population
+// std q = std d, and resets the meeting word.  It then adds the two results,
+// in fixed point with 2^45, to two batch words counted in images, whose
+// finishers write the batch means.  Every word is reset to zero by the one
+// that completes it, so the buffer is zero again when the call ends.  Words
+// sit on their own 128-byte lines.
+//
+// Each workgroup's rounding is at most 2^-(F+1) on a sum below 2^(52-F), so
+// the per-image sums keep ~2^-52 relative accuracy times the workgroup count.
+// --------------------------------------------------------------------------
+constexpr int GF_COUNT_BITS = 12;  // workgroups per image: < 4096
+constexpr int GF_STRIDE = 16;      // uint64 words between accumulators (128 bytes)
+constexpr int GF_MAX_IMAGES = 64;
+constexpr int GF_BATCH_BITS = 45;  // fixed-point bits of the batch sums (<= 64 images in [0, 1])
+constexpr uint64_t GF_PRESENT = uint64_t(1) << 62;
+constexpr uint64_t GF_IS_SQ = uint64_t(1) << 61;
+static_assert(FA_GMSD_ACC_WORDS == (3 * GF_MAX_IMAGES + 2) * GF_STRIDE,
+              "the ABI's accumulator size");
+
+__device__ inline uint64_t gf_add(uint64_t* p, uint64_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t gf_swap(uint64_t* p, uint64_t v) {
+  return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void gf_zero(uint64_t* p) {
+  __hip_atomic_store(p, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Mean q and population std q of an image from its sums of d = 1 - q.  A NaN
+// variance (a NaN q, e.g. a flat patch with T = eps = 0) stays NaN.
+__device__ inline void gmsd_stats(double sa, double sb, double npix, double* mean,
+                                  double* sd) {
+  const double md = sa / npix;  // mean of d = 1 - q
+  const double var = sb / npix - md * md;
+  *mean = 1.0 - md;
+  *sd = sqrt(var < 0.0 ? 0.0 : var);
+}
+
+// Lane `which` (0: sum d, 1: sum d^2) of image n adds the workgroup's `v`.
+__device__ inline void gmsd_finish(const GmsdArgs& a, int n, int which, double v) {
+  constexpr uint64_t CM = (uint64_t(1) << GF_COUNT_BITS) - 1;
+  uint64_t* w = a.acc + static_cast<int64_t>(3 * n + which) * GF_STRIDE;
+  const uint64_t f = static_cast<uint64_t>(__double2ll_rn(v * a.fscale));
+  const uint64_t old = gf_add(w, (f << GF_COUNT_BITS) + 1u);
+  if ((old & CM) + 1u != static_cast<uint64_t>(a.wpi)) return;
+  gf_zero(w);
+  const uint64_t mine = (old >> GF_COUNT_BITS) + f;
+  uint64_t* meet = a.acc + static_cast<int64_t>(3 * n + 2) * GF_STRIDE;
+  const uint64_t other = gf_swap(meet, mine | GF_PRESENT | (which ? GF_IS_SQ : 0));
+  if (!(other & GF_PRESENT)) return;  // the other sum is not complete yet
+  gf_zero(meet);
+  const uint64_t ov = other & (GF_IS_SQ - 1);
+  const double sd = static_cast<double>(which ? ov : mine) * a.finv;
+  const double sd2 = static_cast<double>(which ? mine : ov) * a.finv;
+  double mq, sq;
+  gmsd_stats(sd, sd2, a.npix, &mq, &sq);
+  a.out_mean[n] = mq;
+  a.out_std[n] = sq;
+  if (!a.out_batch) return;
+  const double bs = static_cast<double>(uint64_t(1) << GF_BATCH_BITS);
+  double r[2] = {mq, sq};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    uint64_t* b = a.acc + static_cast<int64_t>(3 * GF_MAX_IMAGES + k) * GF_STRIDE;
+    const uint64_t fb = static_cast<uint64_t>(__double2ll_rn(r[k] * bs));
+    const uint64_t ob = gf_add(b, (fb << GF_COUNT_BITS) + 1u);
+    if ((ob & CM) + 1u != static_cast<uint64_t>(a.N)) continue;
+    gf_zero(b);
+    a.out_batch[k] = static_cast<double>((ob >> GF_COUNT_BITS) + fb) / bs / a.N;
+  }
+}
+
+template <class Src, bool MAP, bool FIN = false>
 __global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
   // one task per workgroup: its four waves take four adjacent strips over the
   // same rows, so each input row is fetched as one contiguous stretch
@@ -575,7 +671,21 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
   }
   acc = wave_sum(acc);
   acc2 = wave_sum(acc2);
-  if (lane == 0) {
+  if constexpr (FIN) {
+    // the workgroup's two sums, in wave order, then one lane per word
+    __shared__ double s_f[2 * WAVES_PER_BLOCK];
+    if (lane == 0) {
+      s_f[wave] = acc;
+      s_f[WAVES_PER_BLOCK + wave] = acc2;
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+      double v = 0.0;
+#pragma unroll
+      for (int w = 0; w < WAVES_PER_BLOCK; ++w) v += s_f[threadIdx.x * WAVES_PER_BLOCK + w];
+      gmsd_finish(a, n, static_cast<int>(threadIdx.x), v);
+    }
+  } else if (lane == 0) {
     const int slot = task * WAVES_PER_BLOCK + wave;
     a.psum[slot] = acc;
     a.psumsq[slot] = acc2;
@@ -584,23 +694,44 @@ __global__ __launch_bounds__(BLOCK) void gmsd_kernel(GmsdArgs a) {
 
 // Block b reduces image b: mean and population standard deviation of its map
 // (reference fa_cuda.cu:1005-1026), from the sums of d = 1 - q.
+// A NaN variance (a NaN q, e.g. a flat patch with T = eps = 0) stays NaN, as
+// the reference's portable statistics give (functional.py:959-971); its
+// CUDA finalize clamps it to 0 instead.  With out_batch, block N (one more)
+// forms the batch means of both statistics from the per-image sums, in image
+// order.
 __global__ __launch_bounds__(BLOCK) void gmsd_finalize_kernel(
     const double* __restrict__ psum, const double* __restrict__ psumsq, int ncols,
-    double npix, double* __restrict__ out_mean, double* __restrict__ out_std) {
+    double npix, double* __restrict__ out_mean, double* __restrict__ out_std, int N,
+    double* __restrict__ out_batch) {
   __shared__ double smem[2 * WAVES_PER_BLOCK];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * ncols;
-  double a = 0.0, b = 0.0;
-  for (int i = threadIdx.x; i < ncols; i += BLOCK) {
-    a += psum[base + i];
-    b += psumsq[base + i];
+  const bool batch = static_cast<int>(blockIdx.x) == N;
+  double bm = 0.0, bs = 0.0;
+  for (int img = batch ? 0 : blockIdx.x; img < (batch ? N : static_cast<int>(blockIdx.x) + 1);
+       ++img) {  // uniform
+    const int64_t base = static_cast<int64_t>(img) * ncols;
+    double a = 0.0, b = 0.0;
+    for (int i = threadIdx.x; i < ncols; i += BLOCK) {
+      a += psum[base + i];
+      b += psumsq[base + i];
+    }
+    double sa = 0.0, sb = 0.0;
+    block_sum2(a, b, smem, &sa, &sb);
+    __syncthreads();  // smem is reused by the next image
+    if (threadIdx.x == 0) {
+      double m, sd;
+      gmsd_stats(sa, sb, npix, &m, &sd);
+      if (batch) {
+        bm += m;
+        bs += sd;
+      } else {
+        out_mean[img] = m;
+        out_std[img] = sd;
+      }
+    }
   }
-  double sa = 0.0, sb = 0.0;
-  block_sum2(a, b, smem, &sa, &sb);
-  if (threadIdx.x == 0) {
-    const double md = sa / npix;  // mean of d = 1 - q
-    const double var = sb / npix - md * md;
-    out_mean[blockIdx.x] = 1.0 - md;
-    out_std[blockIdx.x] = sqrt(var > 0.0 ? var : 0.0);
+  if (batch && threadIdx.x == 0) {
+    out_batch[0] = bm / N;
+    out_batch[1] = bs / N;
   }
 }
 
@@ -801,13 +932,13 @@ static int gmsd_slots(const GGeom& g) {
 
 static bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
-template <class Src, bool MAP>
+template <class Src, bool MAP, bool FIN = false>
 static int occupancy_gmsd() {
   static int wgs_per_cu = 0;  // occupancy of this kernel, queried once
   if (wgs_per_cu <= 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, reinterpret_cast<const void*>(&gmsd_kernel<Src, MAP>), BLOCK, 0) != hipSuccess ||
+            &v, reinterpret_cast<const void*>(&gmsd_kernel<Src, MAP, FIN>), BLOCK, 0) != hipSuccess ||
         v <= 0)
       v = 1;
     wgs_per_cu = v;
@@ -818,14 +949,19 @@ static int occupancy_gmsd() {
 // Workgroups per image: one round of resident workgroups over the whole
 // launch, no more than the workspace holds (a slot per wave) or than leaves a
 // workgroup G_MIN_ROWS rows.  The kernel that writes the q map is its own
-// instantiation, so the statistics-only one carries no map test.
+// instantiation, so the statistics-only one carries no map test.  With
+// a.acc set (and no map) the launch finishes the call itself when its
+// workgroups per image fit the finish's count bits: *wpi_used is then 0.
 template <class Src>
 static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipStream_t st,
                        int* wpi_used) {
   const bool map = a.map != nullptr;
+  const bool fin_ok = Src::U8IN && a.acc && !map;
   // a workgroup is one wave on each of the CU's four SIMDs
-  const int wgs_per_cu = std::min(G_MAX_WAVES_PER_SIMD,
-                                  map ? occupancy_gmsd<Src, true>() : occupancy_gmsd<Src, false>());
+  const int wgs_per_cu = std::min(
+      G_MAX_WAVES_PER_SIMD, map ? occupancy_gmsd<Src, true>()
+                                : (fin_ok ? occupancy_gmsd<Src, false, true>()
+                                          : occupancy_gmsd<Src, false>()));
   a.strips = (a.Wout + Src::OUTW - 1) / Src::OUTW;
   a.groups = (a.strips + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
   a.rows_img = static_cast<int64_t>(a.Cout) * a.groups * a.Hout;
@@ -838,6 +974,15 @@ static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipSt
   if (tasks > INT32_MAX / WAVES_PER_BLOCK) return FA_E_SHAPE;
   a.wpi = static_cast<int>(wpi);
   a.tasks = static_cast<int>(tasks);
+  if constexpr (Src::U8IN) {
+    if (fin_ok && wpi < (1 << GF_COUNT_BITS)) {
+      hipLaunchKernelGGL((gmsd_kernel<Src, false, true>), dim3(static_cast<unsigned>(tasks)),
+                         dim3(BLOCK), 0, st, a);
+      FA_LAUNCH_CHECK();
+      *wpi_used = 0;
+      return FA_OK;
+    }
+  }
   if (map)
     hipLaunchKernelGGL((gmsd_kernel<Src, true>), dim3(static_cast<unsigned>(tasks)), dim3(BLOCK),
                        0, st, a);
@@ -878,7 +1023,8 @@ static int dispatch_gmsd(int dtype, const GmsdArgs& a, const GLaunch& l, bool do
 static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int H, int W,
                      const int64_t* xs, const int64_t* ys, const double* luma, double Tc,
                      double eps, int downsample, float* map_out, double* psum, double* psumsq,
-                     int bpp, double* out_mean, double* out_std, int device, void* stream) {
+                     int bpp, double* out_mean, double* out_std, int device, void* stream,
+                     uint64_t* acc = nullptr, double* out_batch = nullptr) {
   if (!x || !y || !psum || !psumsq || !out_mean || !out_std) return FA_E_ARG;
   if (N <= 0 || C <= 0) return FA_E_SHAPE;
   if (dtype < FA_U8 || dtype > FA_F64) return FA_E_DTYPE;
@@ -910,16 +1056,37 @@ static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int 
   const double sc2 = downsample ? 144.0 : 9.0;  // 9 s^2
   a.T2 = Tc * sc2;
   a.eps2 = eps * sc2;
-  // The float32 path's denominators stay positive when eps and T are at least
-  // 1e-18 (see one_minus_q).  Only values in [0, 1e-18) are raised: the
-  // defaults are far above, and adding 1e-18 to G = gx^2 + gy^2 + eps moves a
-  // term by at most ~1e-9 relative even where G is tiny.
-  const auto floor18 = [](double v) { return static_cast<float>(v >= 0.0 && v < 1e-18 ? 1e-18 : v); };
+  // The float32 path's denominators stay positive when eps or T is positive
+  // and at least 1e-18 (see one_minus_q), so positive values below 1e-18 are
+  // raised to it: the defaults are far above, and adding 1e-18 to G = gx^2 +
+  // gy^2 + eps moves a term by at most ~1e-9 relative even where G is tiny.
+  // Zero stays zero: with T = eps = 0 a flat pixel is 0 / 0 = NaN, as in the
+  // reference (fa_cuda.cu:987-988, functional.py:950-956).
+  const auto floor18 = [](double v) { return static_cast<float>(v > 0.0 && v < 1e-18 ? 1e-18 : v); };
   a.T2f = floor18(a.T2);
   a.eps2f = floor18(a.eps2);
   a.psum = psum;
   a.psumsq = psumsq;
   a.map = map_out;
+  // the one-launch finish: uint8 input (finite samples), T or eps positive
+  // (every d finite), statistics only, at most GF_MAX_IMAGES images; the
+  // fixed-point scale leaves a sum of d (or d^2) over the image, each at most
+  // 1 (plus float32 rounding), below 2^(64 - GF_COUNT_BITS)
+  const double npix = static_cast<double>(g.Hout) * g.Wout * a.Cout;
+  if (acc && dtype == FA_U8 && !map_out && N <= GF_MAX_IMAGES && (a.T2f > 0.0f || a.eps2f > 0.0f)) {
+    int bits = 1;
+    while (bits < 40 && std::ldexp(1.0, bits) <= 2.0 * npix) ++bits;
+    if (bits < 40) {
+      a.acc = acc;
+      a.fscale = std::ldexp(1.0, 64 - GF_COUNT_BITS - bits);
+      a.finv = std::ldexp(1.0, bits - (64 - GF_COUNT_BITS));
+      a.npix = npix;
+      a.out_mean = out_mean;
+      a.out_std = out_std;
+      a.out_batch = out_batch;
+      a.N = N;
+    }
+  }
   const bool down = downsample != 0;
   // the dword path: uint8, downsampled, every row of every plane 4-byte aligned
   // (buffer addressing: a plane's rows must lie within 2^31 bytes of its base)
@@ -937,10 +1104,11 @@ static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int 
   const int r = luma ? dispatch_gmsd<true>(dtype, a, l, down, wide, &wpi)
                      : dispatch_gmsd<false>(dtype, a, l, down, wide, &wpi);
   if (r != FA_OK) return r;
+  if (wpi == 0) return FA_OK;  // finished inside the launch
   // each image owns wpi consecutive slots, one per wave
-  hipLaunchKernelGGL(gmsd_finalize_kernel, dim3(static_cast<unsigned>(N)), dim3(BLOCK), 0, st,
-                     psum, psumsq, wpi,
-                     static_cast<double>(g.Hout) * g.Wout * a.Cout, out_mean, out_std);
+  hipLaunchKernelGGL(gmsd_finalize_kernel, dim3(static_cast<unsigned>(N + (out_batch ? 1 : 0))),
+                     dim3(BLOCK), 0, st, psum, psumsq, wpi, npix, out_mean, out_std, N,
+                     out_batch);
   FA_LAUNCH_CHECK();
   return FA_OK;
 }
@@ -980,6 +1148,20 @@ FA_API int fa_gpu_gmsd_ex(const void* x, const void* y, int dtype, int N, int C,
                           int device, void* stream) {
   return gmsd_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, Tc, eps, downsample,
                    map_out, psum, psumsq, bpp, out_mean, out_std, device, stream);
+}
+
+// No counterpart in the reference, whose GMSD ends in a finalize launch
+// (fa_cuda.cu:1460-1465) and takes batch means with torch (functional.py:1082):
+// fa_gpu_gmsd_ex without the map, finished inside the launch where it can be.
+FA_API int fa_gpu_gmsd_once(const void* x, const void* y, int dtype, int N, int C, int H,
+                            int W, const int64_t* x_strides, const int64_t* y_strides,
+                            const double* luma, double Tc, double eps, int downsample,
+                            double* psum, double* psumsq, int bpp, uint64_t* acc,
+                            double* out_mean, double* out_std, double* out_batch, int device,
+                            void* stream) {
+  return gmsd_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, Tc, eps, downsample,
+                   nullptr, psum, psumsq, bpp, out_mean, out_std, device, stream, acc,
+                   out_batch);
 }
 
 // No counterpart in the reference: its GMS / GMSD losses differentiate the

@@ -740,7 +740,10 @@ def gms(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None,
                             crop_border, reduction, return_map, backend_hint)
     if q is not None:
         return q
-    return stats[0] if reduction == "none" else stats[0].mean()
+    if reduction == "none":
+        return stats[0]
+    # the native statistics come with their batch means, formed in the kernel
+    return stats[2][0] if len(stats) > 2 and stats[2] is not None else stats[0].mean()
 
 
 def gmsd(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None,
@@ -753,7 +756,9 @@ def gmsd(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = None
                             crop_border, reduction, return_map, backend_hint)
     if q is not None:
         return q
-    return stats[1] if reduction == "none" else stats[1].mean()
+    if reduction == "none":
+        return stats[1]
+    return stats[2][1] if len(stats) > 2 and stats[2] is not None else stats[1].mean()
 
 
 # --------------------------------------------------------------------------- #

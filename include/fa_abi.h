@@ -373,6 +373,33 @@ FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
                                     double* out_total, double* out_psnr_per_image,
                                     double* out_psnr_total, int device, void* stream);
 
+/*
+ * No counterpart in the reference, whose GMSD ends in a finalize launch
+ * (fa_cuda.cu:1460-1465) and whose batch means are torch ops
+ * (functional.py:1082).  fa_gpu_gmsd_ex without the map (same arguments and
+ * per-image results), plus
+ *   acc: FA_GMSD_ACC_WORDS uint64 of device memory, zero when the call starts,
+ *     left zero when it completes (state of one stream, like
+ *     fa_gpu_pixel_reduce_once's);
+ *   out_batch: optional double[2], the batch means of out_mean and out_std.
+ * For uint8 input with T or eps positive and N <= 64, the kernel finishes
+ * the call itself: each workgroup adds its sums of d = 1 - q and d^2 to
+ * `acc` as round-to-nearest fixed-point integers (so the result does not
+ * depend on the order of the adds) with returning device-scope atomics, and
+ * the workgroups that complete an image's sums write its statistics (the
+ * batch means likewise).  The per-image values then differ from
+ * fa_gpu_gmsd's fixed-order float64 sums by the fixed-point rounding, about
+ * 2^-52 relative per workgroup.  Every other call runs fa_gpu_gmsd_ex's
+ * launches (plus one block for out_batch) and ignores `acc`.
+ */
+#define FA_GMSD_ACC_WORDS ((3 * 64 + 2) * 16)
+FA_API int fa_gpu_gmsd_once(const void* x, const void* y, int dtype, int N, int C, int H,
+                            int W, const int64_t* x_strides, const int64_t* y_strides,
+                            const double* luma, double Tc, double eps, int downsample,
+                            double* psum, double* psumsq, int bpp, uint64_t* acc,
+                            double* out_mean, double* out_std, double* out_batch, int device,
+                            void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -436,3 +436,111 @@ def test_fused_pyramid_level_gradient(gpu, dt):
         want = base.double() + spread(r)
         err = (got.double() - want).abs().max() / want.abs().max()
         assert err <= tol, (dt, float(err))
+
+
+def _gmsd_call(name, x, y, T, eps, down, acc=None, batch=False, luma=None):
+    """fa_gpu_gmsd (or fa_gpu_gmsd_once with ``acc``) through the C ABI:
+    (mean, std[, batch means]) as float64 numpy arrays."""
+    import ctypes
+
+    from frame_analytics_amd import backend
+
+    n, c, h, w = (int(v) for v in x.shape)
+    bpp = backend.workspace_slots("gmsd", h, w, int(down))
+    planes = n * (1 if luma else c)
+    ps = torch.full((2, planes, bpp), -7.0, dtype=torch.float64, device=x.device)
+    out = torch.full((2 * n + 2,), -7.0, dtype=torch.float64, device=x.device)
+    stream = torch.cuda.current_stream().cuda_stream
+    head = (x.data_ptr(), y.data_ptr(), backend._DTYPE_CODE[x.dtype], n, c, h, w)
+    lw = None if luma is None else (ctypes.c_double * 3)(*luma)
+    if name == "fa_gpu_gmsd":
+        rc = backend.call_gpu(name, *head, float(T), float(eps), int(down), ps[0].data_ptr(),
+                              ps[1].data_ptr(), bpp, out.data_ptr(), out[n:].data_ptr(), 0,
+                              stream)
+    else:
+        rc = backend.call_gpu(name, *head, None, None, lw, float(T), float(eps), int(down),
+                              ps[0].data_ptr(), ps[1].data_ptr(), bpp,
+                              None if acc is None else acc.data_ptr(), out.data_ptr(),
+                              out[n:].data_ptr(), out[2 * n:].data_ptr() if batch else None,
+                              0, stream)
+    assert rc == 0, (name, rc)
+    o = out.cpu().numpy()
+    return o[:n], o[n:2 * n], o[2 * n:]
+
+
+@pytest.mark.parametrize("shape,down", [((1, 1, 200, 232), True), ((8, 3, 1080, 1920), True),
+                                        ((5, 3, 130, 150), False), ((64, 1, 96, 80), True),
+                                        ((65, 1, 40, 48), True)])
+def test_gmsd_one_launch_matches_two_launches(gpu, shape, down):
+    """fa_gpu_gmsd_once: per-image statistics whose sums went through the
+    fixed-point atomics agree with fa_gpu_gmsd's fixed-order float64 sums --
+    mean q to 1e-12 relative, std q to 1e-10 (each workgroup's sum of d^2 is
+    rounded to 2^-30 at 1080p; over ~200 workgroups that is ~1e-11 of the
+    variance, which the E[d^2] - E[d]^2 cancellation carries into the std) --
+    and with the oracle to the 1e-6 bar; its batch means
+    match the means of the per-image values; the same call twice gives the
+    same bits (the adds' order does not matter); the accumulator is zero
+    after every call, including a second, smaller call on it.  N = 65 is
+    past the one-launch form: the two-launch path with the batch block."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair(shape, 9.0, seed=shape[0] * 31 + shape[2])
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    T, eps = 170.0, (1e-6 * 255.0) ** 2
+    acc = torch.zeros(backend._ACC_WORDS["gmsd"], dtype=torch.int64, device=gpu)
+    m2, s2, _ = _gmsd_call("fa_gpu_gmsd", x, y, T, eps, down)
+    m1, s1, bt = _gmsd_call("fa_gpu_gmsd_once", x, y, T, eps, down, acc=acc, batch=True)
+    assert not bool(acc.any())
+    assert np.all(np.abs(m1 - m2) <= 1e-12 * np.abs(m2)), (m1, m2)
+    assert np.all(np.abs(s1 - s2) <= 1e-10 * np.abs(s2)), (s1, s2)
+    assert abs(bt[0] - m1.mean()) <= 1e-12 * abs(m1.mean())
+    assert abs(bt[1] - s1.mean()) <= 1e-12 * abs(s1.mean())
+    again = _gmsd_call("fa_gpu_gmsd_once", x, y, T, eps, down, acc=acc, batch=True)
+    for u, v in zip((m1, s1, bt), again):
+        assert np.array_equal(u, v)
+    k = max(1, shape[0] // 2)
+    mk, sk, _ = _gmsd_call("fa_gpu_gmsd_once", x[:k], y[:k], T, eps, down, acc=acc)
+    assert not bool(acc.any())
+    assert np.all(np.abs(sk - s2[:k]) <= 1e-9 * np.abs(s2[:k]))
+    i = shape[0] - 1
+    m0, s0 = ref.gmsd_stats(a[i:i + 1], b[i:i + 1], 255.0, downsample=down)
+    assert _rel(float(s1[i]), float(s0[0])) <= REL and _rel(float(m1[i]), float(m0[0])) <= REL
+    # luma, through the same one-launch finish
+    lw = (0.299, 0.587, 0.114)
+    if shape[1] == 3:
+        ml, sl, _ = _gmsd_call("fa_gpu_gmsd_once", x, y, T, eps, down, acc=acc, luma=lw)
+        al = ref.rgb_to_luma(a[:1].astype(np.float64), "bt601")
+        bl = ref.rgb_to_luma(b[:1].astype(np.float64), "bt601")
+        _, sr = ref.gmsd_stats(al, bl, 255.0, downsample=down)
+        assert _rel(float(sl[0]), float(sr[0])) <= REL
+        assert not bool(acc.any())
+
+
+@pytest.mark.parametrize("dt", [torch.uint8, torch.float16, torch.float32, torch.float64])
+def test_gmsd_flat_patch_without_T_and_eps_is_nan(gpu, dt):
+    """T = eps = 0: a flat patch is 0 / 0 in q, so its image's statistics are
+    NaN, as the oracle (and the reference's portable statistics) give; an
+    image without a flat patch stays finite and matches the oracle; T = 0
+    with eps > 0 stays finite too."""
+    a, b = _plane_pair(120, 136, seed=5)
+    a2, b2 = a.copy(), b.copy()
+    a2[20:60, 30:80] = 100.0  # the same flat patch in both
+    b2[20:60, 30:80] = 100.0
+    xa = np.stack([a2, a])[:, None]
+    xb = np.stack([b2, b])[:, None]
+    x = torch.as_tensor(xa, dtype=dt, device=gpu)
+    y = torch.as_tensor(xb, dtype=dt, device=gpu)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        m0, s0 = ref.gmsd_stats(xa, xb, 255.0, T=0.0, eps=0.0)
+    assert np.isnan(m0[0]) and np.isnan(s0[0]) and np.isfinite(s0[1])
+    got_s = fa.gmsd(x, y, data_range=255.0, T=0.0, eps=0.0, reduction="none").cpu().numpy()
+    got_m = fa.gms(x, y, data_range=255.0, T=0.0, eps=0.0, reduction="none").cpu().numpy()
+    assert np.isnan(got_s[0]) and np.isnan(got_m[0]), (got_s, got_m)
+    assert _rel(float(got_s[1]), float(s0[1])) <= REL and _rel(float(got_m[1]), float(m0[1])) <= REL
+    assert np.isnan(float(fa.gmsd(x, y, data_range=255.0, T=0.0, eps=0.0)))
+    if dt != torch.float64:  # (a float64 map is the portable path's, not a kernel's)
+        qmap = fa.gms(x, y, data_range=255.0, T=0.0, eps=0.0, return_map=True).cpu().numpy()
+        assert np.isnan(qmap[0]).any() and not np.isnan(qmap[1]).any()
+    m1, s1 = ref.gmsd_stats(xa, xb, 255.0, T=0.0, eps=1e-30)
+    got = fa.gmsd(x, y, data_range=255.0, T=0.0, eps=1e-30, reduction="none").cpu().numpy()
+    assert np.all(np.isfinite(got)) and np.all(np.abs(got - s1) <= REL * np.abs(s1)), (got, s1)

@@ -349,7 +349,7 @@ def test_single_launch_finish_matches_two_launches(gpu, n, hw, bpis):
                                            generator=g)).clamp(0, 255).to(torch.uint8)
     per = hw[0] * hw[1]
     stream = torch.cuda.current_stream().cuda_stream
-    acc = torch.zeros(backend._PIXEL_ACC_WORDS, dtype=torch.int64, device=gpu)
+    acc = torch.zeros(backend._ACC_WORDS["pixel"], dtype=torch.int64, device=gpu)
     a_np, b_np = x.cpu().numpy(), y.cpu().numpy()
     for op, isum in ((0, ref.sse_u8(a_np, b_np, per_image=True)),
                      (1, ref.sad_u8(a_np, b_np, per_image=True))):
@@ -410,7 +410,8 @@ def test_single_launch_finish_per_stream(gpu):
     for key, o in outs:
         want = ref.mse(a, b, "none") if key == "ab" else ref.mse(c, d, "none")
         assert np.array_equal(o.cpu().numpy(), want), key
-    keys = [k for k in backend._pixel_acc if k[1] in (s1.cuda_stream, s2.cuda_stream)]
+    keys = [k for k in backend._stream_acc
+            if k[0] == "pixel" and k[2] in (s1.cuda_stream, s2.cuda_stream)]
     assert len(keys) == 2
     for k in keys:
-        assert not bool(backend._pixel_acc[k].any())
+        assert not bool(backend._stream_acc[k].any())
