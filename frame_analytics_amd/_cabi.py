@@ -70,6 +70,9 @@ SIGNATURES = {
     "fa_gpu_gmsd_once":
         ([_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _D, _D, _I, _P, _P, _I, _P, _P, _P, _P, _I,
           _P], _I),
+    "fa_gpu_ssim_once":
+        ([_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _D, _D, _D, _P, _P, _I, _P, _P, _P,
+          _I, _P], _I),
     "fa_gpu_ssim_cs_backward_ex":
         ([_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _D, _D, _D, _P, _P, _I, _P, _P, _P,
           _I, _P], _I),

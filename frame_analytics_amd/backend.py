@@ -322,8 +322,8 @@ def workspace_slots(kind: str, a: int, b: int, c: int) -> int:
 
 
 #: uint64 words of the one-launch entry points' accumulators
-#: (FA_PIXEL_ACC_WORDS, FA_GMSD_ACC_WORDS)
-_ACC_WORDS = {"pixel": (32 + 1) * 16, "gmsd": (3 * 64 + 2) * 16}
+#: (FA_PIXEL_ACC_WORDS, FA_GMSD_ACC_WORDS, FA_SSIM_ACC_WORDS)
+_ACC_WORDS = {"pixel": (32 + 1) * 16, "gmsd": (3 * 64 + 2) * 16, "ssim": (256 + 1) * 16}
 #: (kind, device, raw stream) -> that stream's accumulator, zero between calls
 _stream_acc: dict = {}
 
@@ -571,7 +571,11 @@ def _ssim_native(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: floa
     head = (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w)
     tail = (_ptr(win), win_size, float(shift), float(C1), float(C2), _ptr(smap),
             _ptr(partial), bpp, _ptr(per_image), _ptr(total), dev, stream)
-    if luma is None and xs is None and ys is None:
+    if smap is None:
+        acc = _acc_for("ssim", x.device, dev, stream) if x.dtype == torch.uint8 else None
+        _run("fa_gpu_ssim_once", *head, xs, ys, _luma_arg(luma), *tail[:8], _ptr(acc),
+             *tail[8:])
+    elif luma is None and xs is None and ys is None:
         _run("fa_gpu_ssim", *head, *tail)
     else:
         _run("fa_gpu_ssim_ex", *head, xs, ys, _luma_arg(luma), *tail)

@@ -1015,7 +1015,7 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
                      const int64_t* xs, const int64_t* ys, const double* luma,
                      const float* win, int K, double shift, double C1, double C2,
                      float* map_out, double* partial, int bpp, double* out_per_image,
-                     double* out_total, int device, void* stream) {
+                     double* out_total, int device, void* stream, uint64_t* acc = nullptr) {
   if (!x || !y || !win || !partial) return FA_E_ARG;
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
@@ -1048,9 +1048,10 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
     // allows (fa_ssim_mfma.hip); otherwise the strip kernel below
     const SsimMfmaCall mc = {x, y, SsimMfmaCall::U8, a.xsn, a.xsc, a.ysn, a.ysc, a.xsh, a.ysh,
                              N, C, H, W, Hout, Wout, K, win, C1, C2, map_out, partial, bpp,
-                             nullptr, nullptr, nullptr, false};
+                             nullptr, nullptr, nullptr, false, acc, out_per_image, out_total};
     rc = ssim_mfma(mc, device, st, &tiles);
     if (rc != FA_OK) return rc;
+    if (tiles < 0) return FA_OK;  // the launch finished the call
   }
   if (tiles == 0) {
     rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, lm, a, planes, device, st)
@@ -1162,6 +1163,19 @@ FA_API int fa_gpu_ssim_ex(const void* x, const void* y, int dtype, int N, int C,
                           void* stream) {
   return ssim_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, win, K, shift, C1, C2,
                    map_out, partial, bpp, out_per_image, out_total, device, stream);
+}
+
+// No counterpart in the reference, whose SSIM ends in a finalize launch
+// (fa_cuda.cu:1218-1222): fa_gpu_ssim_ex, finished inside the matrix-core
+// launch where it can be (include/fa_abi.h states where).
+FA_API int fa_gpu_ssim_once(const void* x, const void* y, int dtype, int N, int C, int H,
+                            int W, const int64_t* x_strides, const int64_t* y_strides,
+                            const double* luma, const float* win, int K, double shift,
+                            double C1, double C2, float* map_out, double* partial, int bpp,
+                            uint64_t* acc, double* out_per_image, double* out_total,
+                            int device, void* stream) {
+  return ssim_impl(x, y, dtype, N, C, H, W, x_strides, y_strides, luma, win, K, shift, C1, C2,
+                   map_out, partial, bpp, out_per_image, out_total, device, stream, acc);
 }
 
 // reference: fa_cuda.cu:1235-1283 (fa_cuda_ssim_cs)

@@ -33,6 +33,12 @@ struct SsimMfmaCall {
   void* px;
   void* py;
   bool level_f16;
+  // the one-launch finish (forward over uint8 planes, no map): a zeroed
+  // accumulator of FA_SSIM_ACC_WORDS words the launch leaves zeroed, and the
+  // outputs it then writes itself (either may be null, not both)
+  uint64_t* acc;
+  double* out_per_image;
+  double* out_total;
 };
 
 // Launches the matrix-core SSIM forward (or CS pass) when the call fits it
@@ -41,7 +47,8 @@ struct SsimMfmaCall {
 // output planes).  Returns FA_OK and
 // sets *tiles (partial slots used per plane) when it launched; returns FA_OK
 // with *tiles = 0 when the call does not fit, so the caller runs the
-// vector-ALU strip kernel instead.
+// vector-ALU strip kernel instead.  With c.acc set, a launch that finished
+// the call itself (no finalize needed) sets *tiles = -1.
 int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles);
 
 }  // namespace fa

@@ -96,7 +96,56 @@ struct MfArgs {
   void* px;             // MF_CS, MF_CSO: optional pyramid level (2 x 2 means),
   void* py;             //   float32, or float16 (level_f16, uint8 input)
   int level_f16;
+  // the one-launch finish (ssim_mfma_kernel<..., FIN>)
+  uint64_t* acc;
+  double fscale, finv, npix_img, npix_all;
+  double *out_per_image, *out_total;
+  int N;
 };
+
+// --------------------------------------------------------------------------
+// The one-launch finish of the uint8 forward (fa_gpu_ssim_once).
+//
+// Each workgroup adds its sum of the SSIM map to its image's accumulator word
+// as a signed fixed-point integer, round(sum * 2^F), packed with a
+// contribution count: word = (value << MF_COUNT_BITS) + count, in two's
+// complement (the count stays in the low bits whatever the sign of the sum,
+// and an arithmetic shift recovers the sum).  One returning device-scope
+// atomic adds both; integer addition does not depend on the order, so the
+// result is the same from run to run.  The workgroup whose add completes an
+// image's count (C * tiles workgroups) holds the image's sum, writes its mean,
+// resets the word, and adds the image's integer sum to the batch word, counted
+// in images, whose completer writes the batch mean.  F = 51 - bits(2 N pixels
+// per image) keeps every packed sum within the word.  Words sit on their own
+// 128-byte lines.
+// --------------------------------------------------------------------------
+constexpr int MF_COUNT_BITS = 12;
+constexpr int MF_STRIDE = 16;
+constexpr int MF_FIN_MAX_IMAGES = 256;
+static_assert(FA_SSIM_ACC_WORDS == (MF_FIN_MAX_IMAGES + 1) * MF_STRIDE,
+              "the ABI's accumulator size");
+
+__device__ inline void mf_finish(const MfArgs& a, int img, int wg_per_image, double s) {
+  constexpr uint64_t CM = (uint64_t(1) << MF_COUNT_BITS) - 1;
+  uint64_t* w = a.acc + static_cast<int64_t>(img) * MF_STRIDE;
+  const int64_t f = __double2ll_rn(s * a.fscale);
+  const uint64_t old = __hip_atomic_fetch_add(
+      w, (static_cast<uint64_t>(f) << MF_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
+      __HIP_MEMORY_SCOPE_AGENT);
+  if ((old & CM) + 1u != static_cast<uint64_t>(wg_per_image)) return;
+  __hip_atomic_store(w, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t tot = (static_cast<int64_t>(old) >> MF_COUNT_BITS) + f;
+  if (a.out_per_image) a.out_per_image[img] = static_cast<double>(tot) * a.finv / a.npix_img;
+  if (!a.out_total) return;
+  uint64_t* wb = a.acc + static_cast<int64_t>(MF_FIN_MAX_IMAGES) * MF_STRIDE;
+  const uint64_t ob = __hip_atomic_fetch_add(
+      wb, (static_cast<uint64_t>(tot) << MF_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
+      __HIP_MEMORY_SCOPE_AGENT);
+  if ((ob & CM) + 1u != static_cast<uint64_t>(a.N)) return;
+  __hip_atomic_store(wb, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t all = (static_cast<int64_t>(ob) >> MF_COUNT_BITS) + tot;
+  *a.out_total = static_cast<double>(all) * a.finv / a.npix_all;
+}
 
 __device__ inline f4 mfma(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -591,7 +640,7 @@ enum { LVL_NONE = 0, LVL_F32 = 1, LVL_F16 = 2 };
 // and beat 3; the uint8 cs-only pass writing a float32 level (which MS-SSIM
 // does not use: its first level is float16) needs more and runs 3.  LVL (CS
 // modes): the pyramid level the pass writes.
-template <int SRC, int MODE, int LVL>
+template <int SRC, int MODE, int LVL, bool FIN = false>
 __global__ __launch_bounds__(BLOCK)
 __attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1
                                    : (SRC == SRC_U8 && MODE == MF_CSO && LVL == LVL_F32) ? 3
@@ -600,6 +649,7 @@ void ssim_mfma_kernel(MfArgs a) {
   constexpr bool PYR = SRC == SRC_F32;  // float32 samples: hi + lo operands
   constexpr bool LEVEL = LVL != LVL_NONE;
   static_assert(!LEVEL || MODE == MF_CS || MODE == MF_CSO, "levels come from the CS pass");
+  static_assert(!FIN || (MODE == MF_REDUCE && SRC == SRC_U8), "the finish: uint8 forward sums");
   static_assert(LVL != LVL_F16 || SRC == SRC_U8, "float16 levels below uint8 input only");
   __shared__ double sred[2 * WAVES_PER_BLOCK];
   __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
@@ -857,7 +907,11 @@ void ssim_mfma_kernel(MfArgs a) {
     }
   } else {
     const double s = block_sum(acc, sred);
-    if (threadIdx.x == 0) (MODE == MF_CSO ? a.partial_cs : a.partial)[slot] = s;
+    if constexpr (FIN) {
+      if (threadIdx.x == 0) mf_finish(a, plane / a.C, a.C * a.tiles, s);
+    } else if (threadIdx.x == 0) {
+      (MODE == MF_CSO ? a.partial_cs : a.partial)[slot] = s;
+    }
   }
 }
 
@@ -867,14 +921,14 @@ bool mfma_enabled() {
   return !(e && e[0] == '0');
 }
 
-template <int SRC, int MODE, int LVL>
+template <int SRC, int MODE, int LVL, bool FIN = false>
 int occupancy() {
   static int occ = 0;
   if (occ <= 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, reinterpret_cast<const void*>(&ssim_mfma_kernel<SRC, MODE, LVL>), BLOCK, 0) !=
-            hipSuccess ||
+            &v, reinterpret_cast<const void*>(&ssim_mfma_kernel<SRC, MODE, LVL, FIN>), BLOCK,
+            0) != hipSuccess ||
         v <= 0)
       v = 1;
     occ = v;
@@ -886,6 +940,13 @@ int occupancy() {
 // launch.
 template <int SRC, int MODE, int LVL>
 int run(bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
+  if constexpr (SRC == SRC_U8 && MODE == MF_REDUCE) {
+    if (a.acc) {
+      if (!launch) return occupancy<SRC, MODE, LVL, true>();
+      hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MODE, LVL, true>), grid, dim3(BLOCK), 0, st, a);
+      return 0;
+    }
+  }
   if (!launch) return occupancy<SRC, MODE, LVL>();
   hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MODE, LVL>), grid, dim3(BLOCK), 0, st, a);
   return 0;
@@ -944,6 +1005,9 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
     if (v % 8 != 0) return FA_OK;
   // 32-bit offsets within a plane: the buffer loads run up to 47 rows past
   // the last output row (their range check stops them at the plane's end)
+  // the finish takes the uint8 forward's sums with a wanted output
+  const bool fin = c.acc && src == SRC_U8 && mode == MF_REDUCE && c.N <= MF_FIN_MAX_IMAGES &&
+                   (c.out_per_image || c.out_total);
   const int64_t eb = src == SRC_F32 ? 4 : src == SRC_F16 ? 2 : 1;
   if ((static_cast<int64_t>(c.H) + 48) * std::max(c.xsh, c.ysh) * eb > INT32_MAX) return FA_OK;
   // the map is written through buffer resources with 32-bit offsets in a plane
@@ -1030,9 +1094,25 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   }
   const int64_t wgs = planes * a.tiles;
   if (wgs > INT32_MAX) return FA_OK;
+  // the one-launch finish, where its counts fit: C * tiles workgroups per
+  // image and N images below 2^MF_COUNT_BITS (the tile plan above is the same
+  // either way: the finish's kernel has the same occupancy)
+  if (fin && static_cast<int64_t>(c.C) * a.tiles < (1 << MF_COUNT_BITS)) {
+    a.acc = c.acc;
+    a.out_per_image = c.out_per_image;
+    a.out_total = c.out_total;
+    a.N = c.N;
+    a.npix_img = static_cast<double>(c.Hout) * c.Wout * c.C;
+    a.npix_all = a.npix_img * c.N;
+    int bits = 1;
+    while (bits < 50 && std::ldexp(1.0, bits) <= 2.0 * a.npix_all) ++bits;
+    a.fscale = std::ldexp(1.0, 51 - bits);
+    a.finv = std::ldexp(1.0, bits - 51);
+    if (bits >= 40) a.acc = nullptr;  // (never at real sizes) too few fraction bits left
+  }
   dispatch(src, mode, true, dim3(static_cast<unsigned>(wgs)), st, a);
   FA_LAUNCH_CHECK();
-  *tiles = a.tiles;
+  *tiles = a.acc ? -1 : a.tiles;
   return FA_OK;
 }
 

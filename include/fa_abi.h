@@ -400,6 +400,30 @@ FA_API int fa_gpu_gmsd_once(const void* x, const void* y, int dtype, int N, int 
                             double* out_mean, double* out_std, double* out_batch, int device,
                             void* stream);
 
+/*
+ * No counterpart in the reference, whose SSIM ends in a finalize launch
+ * (fa_cuda.cu:1218-1222).  fa_gpu_ssim_ex (same arguments and results), plus
+ * acc: FA_SSIM_ACC_WORDS uint64 of device memory, zero when the call starts
+ * and left zero when it completes (state of one stream, like
+ * fa_gpu_pixel_reduce_once's).  Where the forward runs on the matrix cores
+ * (uint8 planes without luma, 8-sample aligned rows; see fa_gpu_ssim) with
+ * no map, N <= 256 and a mean wanted, the launch finishes the call itself:
+ * each workgroup adds its sum of the map to `acc` as a round-to-nearest
+ * signed fixed-point integer (so the result does not depend on the order of
+ * the adds) with returning device-scope atomics, and the workgroups that
+ * complete an image's sum, and the batch's, write the means.  They differ
+ * from fa_gpu_ssim's fixed-order float64 sums by that rounding, ~1e-13
+ * relative at 1080p.  Every other call runs as fa_gpu_ssim_ex and ignores
+ * `acc`.
+ */
+#define FA_SSIM_ACC_WORDS ((256 + 1) * 16)
+FA_API int fa_gpu_ssim_once(const void* x, const void* y, int dtype, int N, int C, int H,
+                            int W, const int64_t* x_strides, const int64_t* y_strides,
+                            const double* luma, const float* win, int K, double shift,
+                            double C1, double C2, float* map_out, double* partial, int bpp,
+                            uint64_t* acc, double* out_per_image, double* out_total,
+                            int device, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

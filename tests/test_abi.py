@@ -39,7 +39,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 22  # 12 reference entry points + 10 extensions
+    assert len(decl) == 23  # 12 reference entry points + 11 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name

@@ -372,3 +372,64 @@ def test_pyramid_flag_is_an_ex_hint_only(gpu):
     with pytest.raises(ValueError):
         backend.ssim_cs_partials(x.double(), x.double(), win, 0.5, 1e-4, 9e-4, None,
                                  u8_pyramid=True)
+
+
+def _ssim_abi(name, x, y, win, acc=None, K=11, L=255.0, per_image=True, total=True):
+    """fa_gpu_ssim (or fa_gpu_ssim_once with ``acc``) with both mean sinks:
+    (per-image means, batch mean) as numpy float64."""
+    from frame_analytics_amd import backend
+
+    n, c, h, w = (int(v) for v in x.shape)
+    bpp = backend.workspace_slots("ssim", h, w, K)
+    part = torch.full((n * c, bpp), -3.0, dtype=torch.float64, device=x.device)
+    out = torch.full((n + 1,), -3.0, dtype=torch.float64, device=x.device)
+    stream = torch.cuda.current_stream().cuda_stream
+    head = (x.data_ptr(), y.data_ptr(), 0, n, c, h, w)
+    consts = (win.data_ptr(), K, L / 2, (0.01 * L) ** 2, (0.03 * L) ** 2, None,
+              part.data_ptr(), bpp)
+    sinks = (out.data_ptr() if per_image else None, out[n:].data_ptr() if total else None)
+    if name == "fa_gpu_ssim":
+        rc = backend.call_gpu(name, *head, *consts, *sinks, 0, stream)
+    else:
+        rc = backend.call_gpu(name, *head, None, None, None, *consts,
+                              None if acc is None else acc.data_ptr(), *sinks, 0, stream)
+    assert rc == 0, (name, rc)
+    o = out.cpu().numpy()
+    return o[:n], o[n]
+
+
+@pytest.mark.parametrize("shape", [(8, 3, 1080, 1920), (1, 1, 96, 128), (3, 2, 200, 256),
+                                   (256, 1, 24, 32), (257, 1, 24, 32)])
+def test_one_launch_finish_matches_finalize(gpu, shape):
+    """fa_gpu_ssim_once on the matrix-core forward: the per-image and batch
+    means its workgroups finish through fixed-point atomics agree with
+    fa_gpu_ssim's fixed-order float64 finalize to 1e-12 relative (the
+    rounding is 2^-24 per workgroup sum at configs[1]), repeat bit for bit,
+    and leave the accumulator zero, also over a second, smaller call and with
+    only one of the two sinks.  257 images is past the one-launch form."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair(shape, 8.0, seed=shape[0] + shape[2])
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    acc = torch.zeros(backend._ACC_WORDS["ssim"], dtype=torch.int64, device=gpu)
+    p2, t2 = _ssim_abi("fa_gpu_ssim", x, y, win)
+    p1, t1 = _ssim_abi("fa_gpu_ssim_once", x, y, win, acc)
+    assert not bool(acc.any())
+    assert np.all(np.abs(p1 - p2) <= 1e-12 * np.abs(p2)), (p1, p2)
+    assert abs(t1 - t2) <= 1e-12 * abs(t2), (t1, t2)
+    q1, u1 = _ssim_abi("fa_gpu_ssim_once", x, y, win, acc)
+    assert np.array_equal(p1, q1) and t1 == u1
+    k = max(1, shape[0] // 2)
+    pk, tk = _ssim_abi("fa_gpu_ssim_once", x[:k], y[:k], win, acc)
+    assert not bool(acc.any())
+    assert np.all(np.abs(pk - p2[:k]) <= 1e-12 * np.abs(p2[:k]))
+    for pi, to in ((True, False), (False, True)):
+        pj, tj = _ssim_abi("fa_gpu_ssim_once", x, y, win, acc, per_image=pi, total=to)
+        assert not bool(acc.any()), (pi, to)
+        if pi:
+            assert np.array_equal(pj, p1)
+        else:
+            assert tj == t1
+    want = ref.ssim(a[:1].astype(np.float64), b[:1].astype(np.float64), 255.0)
+    assert _rel(float(p1[0]), float(want)) <= REL
