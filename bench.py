@@ -23,6 +23,12 @@ counted as float32 operations per output pixel -- is reported beside the HBM
 figure.  ``traffic`` is filled from the committed rocprofv3 PMC summary when
 present.
 
+Besides: ``latency_single_frame`` (per-call ms at 512^2 and one 1080p frame,
+beside the reference's RTX 3090 row), ``streaming`` (``StreamingMetrics``
+frames per second at 1080p RGB, host-in and resident) and ``peak_memory_MiB``
+(device memory a call allocates above its inputs, forward and loss step at
+1080p x8) -- the reference's own measurements of this path.
+
 ``cpu_baseline`` times the reference's own CPU kernels (oracle/_ref, compiled
 from the reference sources) on a bounded sample of the same workload, on all
 host cores.  ``cpu_configs0`` runs configs[0] (1x3x512x512 uint8) through the
@@ -398,6 +404,144 @@ def trace_leg(name, steps, warmup):
     print(json.dumps({"leg": name, "steps": steps, "ms_per_step": round(ms, 4)}), flush=True)
 
 
+def _frames(torch, shape, dev, seed, sigma=8.0):
+    """One resident uint8 pair of ``shape`` (the BASELINE.json generator)."""
+    return _pairs(torch, shape, sigma, 1, dev, seed)[0]
+
+
+# The reference's per-call table (README.md:53-59, RTX 3090), ms: SSIM and
+# PSNR on one channel (its bench/bench.py:188), MS-SSIM / GMSD / L1 on three
+# (bench/bench_training.py:127,232,269).
+REF_LATENCY_MS = {
+    "ssim": {"512": 0.024, "1080p": 0.085}, "psnr": {"512": 0.020, "1080p": 0.028},
+    "ms_ssim": {"512": 0.331, "1080p": 0.512}, "gmsd": {"512": 0.023, "1080p": 0.055},
+    "l1": {"512": 0.021, "1080p": 0.026},
+}
+
+
+def latency_legs(torch, fa, dev):
+    """Per-call milliseconds of single frames, the reference's timer (fastest
+    of 5 batches of 20 calls between synchronisations), beside its RTX 3090
+    row.  Small frames are where fixed costs show: launches and the Python
+    path."""
+    out = {"workload": "one frame per call: ssim / psnr 1 channel, ms_ssim / gmsd / l1 "
+                       "3 channels (the reference's bench channel counts), uint8"}
+    calls = {"ssim": lambda a, b: fa.ssim(a, b, data_range=255.0),
+             "psnr": lambda a, b: fa.psnr(a, b, data_range=255.0),
+             "ms_ssim": lambda a, b: fa.ms_ssim(a, b, data_range=255.0),
+             "gmsd": lambda a, b: fa.gmsd(a, b, data_range=255.0),
+             "l1": lambda a, b: fa.l1(a, b)}
+    for size, (h, w) in (("512", (512, 512)), ("1080p", (1080, 1920))):
+        pairs = {c: _frames(torch, (1, c, h, w), dev, seed=40 + c) for c in (1, 3)}
+        for name, fn in calls.items():
+            a, b = pairs[1 if name in ("ssim", "psnr") else 3]
+            f = (lambda i, fn=fn, a=a, b=b: fn(a, b))
+            _clock_warmup(torch, f, 0.1)
+            out.setdefault(name, {})[size] = round(_leg_ms(torch, f, 20, 5), 4)
+    out["reference_rtx3090_ms"] = REF_LATENCY_MS
+    return out
+
+
+def streaming_leg(torch, fa, dev, frames=300):
+    """``StreamingMetrics`` at 1080p RGB (mse + psnr + ssim as one captured HIP
+    graph): host uint8 frames in, Python floats out, and the reference's
+    resident comparison (fa.ssim + fa.psnr on resident frames), as its
+    bench/bench.py:302-335 times them."""
+    h, w = 1080, 1920
+    g = torch.Generator()
+    g.manual_seed(5)
+    host = []
+    for _ in range(4):
+        a = torch.randint(0, 256, (3, h, w), dtype=torch.uint8, generator=g)
+        n = torch.round(torch.randn((3, h, w), generator=g) * 8.0).to(torch.int16)
+        host.append((a, (a.to(torch.int16) + n).clamp(0, 255).to(torch.uint8)))
+    sm = fa.StreamingMetrics((1, 3, h, w), device=dev, dtype=torch.uint8, data_range=255.0)
+    for i in range(16):
+        sm.update(*host[i % 4])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(frames):
+        sm.update(*host[i % 4])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ra, rb = host[0][0].to(dev)[None], host[0][1].to(dev)[None]
+    for _ in range(16):
+        fa.ssim(ra, rb, data_range=255.0)
+        fa.psnr(ra, rb, data_range=255.0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(frames):
+        fa.ssim(ra, rb, data_range=255.0)
+        fa.psnr(ra, rb, data_range=255.0)
+    torch.cuda.synchronize()
+    dt2 = time.perf_counter() - t0
+    return {"workload": f"{frames} frames of 1080p RGB uint8",
+            "graph_captured": bool(sm.graph_captured),
+            "host_in_fps": round(frames / dt, 1),
+            "resident_fps": round(frames / dt2, 1),
+            "reference_rtx3090_fps": {"host_in": 931, "resident": 2941}}
+
+
+def memory_legs(torch, fa, dev):
+    """Peak device allocation of one call above its inputs, MiB (the
+    reference's cuda_peak, bench/bench_memory.py:56-86: warm first, then
+    max_memory_allocated over the call against what was allocated before),
+    at 1080p x8 RGB, beside its RTX 3090 figures (README.md:95-115,150-165)."""
+    import gc
+
+    mib = float(1 << 20)
+
+    def peak(fn, setup=None):
+        fn()
+        if setup is not None:
+            setup()
+        torch.cuda.synchronize()
+        gc.collect()
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        before = torch.cuda.memory_allocated()
+        out = fn()
+        torch.cuda.synchronize()
+        v = (torch.cuda.max_memory_allocated() - before) / mib
+        del out
+        return round(v, 3)
+
+    x8, y8 = _frames(torch, SSIM_SHAPE, dev, seed=9)
+    res = {"workload": "8x3x1080x1920: forward on uint8, loss step (forward + backward) "
+                       "on float32 frames / 255"}
+    with torch.no_grad():
+        res["forward"] = {
+            "ssim": peak(lambda: fa.ssim(x8, y8, data_range=255.0)),
+            "ms_ssim": peak(lambda: fa.ms_ssim(x8, y8, data_range=255.0)),
+            "gmsd": peak(lambda: fa.gmsd(x8, y8, data_range=255.0)),
+            "psnr": peak(lambda: fa.psnr(x8, y8, data_range=255.0)),
+        }
+    x = (x8.float() / 255.0).requires_grad_(True)
+    y = y8.float() / 255.0
+    del x8, y8
+
+    def step(fn):
+        def run():
+            loss = fn()
+            loss.backward()
+            return loss
+        return run
+
+    def drop_grad():
+        x.grad = None
+
+    res["loss_step"] = {
+        "ssim": peak(step(lambda: 1.0 - fa.ssim(x, y, data_range=1.0)), drop_grad),
+        "ms_ssim": peak(step(lambda: 1.0 - fa.ms_ssim(x, y, data_range=1.0)), drop_grad),
+    }
+    res["reference_rtx3090_MiB"] = {"forward": {"ssim": 0.19, "ms_ssim": 120, "gmsd": 0.19,
+                                                "psnr": 0.007},
+                                    "loss_step": {"ssim": 752, "ms_ssim": 942}}
+    del x, y
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -539,8 +683,7 @@ def main():
         return fa.psnr(a, b, data_range=255.0)
 
     _clock_warmup(torch, psnr_step, LEG_WARMUP_S)
-    p_el = _time_steps(torch, psnr_step, args.steps, args.warmup)
-    p_ms = p_el / args.steps * 1e3
+    p_ms = _leg_ms(torch, psnr_step, reps, 5)
     pbytes = 2.0 * ppairs[0][0].numel()
     bpi = backend.workspace_slots("pixel", pn, per, 0)
     ppart = torch.empty((pn, bpi), dtype=torch.float64, device=dev)
@@ -574,6 +717,10 @@ def main():
     torch.cuda.empty_cache()
     torch.cuda.empty_cache()
 
+    latency = latency_legs(torch, fa, dev)
+    streaming = streaming_leg(torch, fa, dev)
+    memory = memory_legs(torch, fa, dev)
+
     line = {
         "metric": "SSIM Gpixel/s at 1080p x8 uint8 (configs[1]); PSNR 4K x8 HBM GB/s beside it",
         "value": round(gpix, 3),
@@ -585,7 +732,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(gpix / BASELINE_GPIXS, 3),
-        "dtype": "f32",
+        # the input samples; the kernel multiplies exact fp16 hi + lo pieces
+        # of them on the matrix cores and accumulates in float32
+        "dtype": "u8",
+        "operands": "fp16 hi+lo split operands (v_mfma_f32_16x16x32_f16), f32 accumulate",
         "data": "synthetic uint8 (BASELINE.json generator, 4 resident pairs rotated); "
                 f"{args.clock_warmup:g} s clock warm-up ({warm_calls} untimed steps) before "
                 f"the warm-up steps; {LEG_WARMUP_S:g} s of untimed calls before each "
@@ -619,6 +769,7 @@ def main():
             "workload": "psnr 8x3x2160x3840 uint8 (configs[2]), 2 resident pairs rotated",
             "ms_per_step": round(p_ms, 4),
             "GBps_end_to_end": round(pbytes / (p_ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak_end_to_end": round(pbytes / (p_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "kernel": "pix_sweep_kernel<uint8,MSE>",
             "kernel_ms": round(pk_ms, 4),
             "GBps_kernel": round(pbytes / (pk_ms * 1e-3) / 1e9, 1),
@@ -635,6 +786,9 @@ def main():
                      "ms_per_step": round(c3_ms, 4),
                      "ms_per_step_backward_in_calling_thread": round(c3_inline_ms, 4)},
         "configs1_other_outputs": c1,
+        "latency_single_frame": latency,
+        "streaming": streaming,
+        "peak_memory_MiB": memory,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
         "cpu_configs0": None if args.no_cpu_baseline else cpu_configs0(),
     }
