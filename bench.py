@@ -314,8 +314,9 @@ def profile_sequence(launches=20):
     """A fixed launch sequence for rocprofv3 counter runs (``--profile``):
     a torch copy of exactly 256 MiB (the FETCH_SIZE / WRITE_SIZE calibration:
     256 MiB read, 256 MiB written), then `launches` launches each of the SSIM
-    strip kernel, the GMSD kernel and the PSNR pixel
-    kernel, through the C ABI, rotating resident input pairs."""
+    kernel (configs[1]; reduction, then with the float32 map), the GMSD kernel
+    (configs[4]) and the PSNR pixel kernel, through the C ABI,
+    rotating resident input pairs."""
     import torch
 
     import frame_analytics_amd as fa
@@ -343,6 +344,15 @@ def profile_sequence(launches=20):
                                127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, None,
                                partial.data_ptr(), bpp, None, None, 0, stream) == 0
     torch.cuda.synchronize()
+    # the same kernel writing the float32 map (configs[1], return_map=True)
+    smap = torch.empty((n, c, h - 10, w - 10), dtype=torch.float32, device=dev)
+    for i in range(launches):
+        a, b = pairs[i % 4]
+        assert lib.fa_gpu_ssim(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, win.data_ptr(), 11,
+                               127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, smap.data_ptr(),
+                               partial.data_ptr(), bpp, None, None, 0, stream) == 0
+    torch.cuda.synchronize()
+    del smap
     # GMSD (configs[4]: downsample, per-channel pooled) on the same pairs
     gbpp = backend.workspace_slots("gmsd", h, w, 1)
     ps = torch.empty((n * c, gbpp), dtype=torch.float64, device=dev)

@@ -1083,14 +1083,21 @@ std::atomic<double*> g_scratch[NOALLOC_MAX_DEVICES];
 
 // The device address of the current device's `scratch`, asked once per device
 // (hipGetSymbolAddress with that device current) and kept.  The array's name
-// is a host-side stand-in in host code and is never passed to a kernel.
-int scratch_on_current_device(double** out) {
+// is a host-side stand-in in host code and is never passed to a kernel.  The
+// lookup may load the code object, which has no place in a graph capture:
+// a first call on a device whose stream is capturing gets FA_E_ARG before any
+// other HIP call (one eager call on the device must come first).
+int scratch_on_current_device(hipStream_t st, double** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return -static_cast<int>(e);
   if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return FA_E_ARG;
   double* p = g_scratch[dev].load(std::memory_order_acquire);
   if (p == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cap);
+    if (e != hipSuccess) return -static_cast<int>(e);
+    if (cap != hipStreamCaptureStatusNone) return FA_E_ARG;
     void* q = nullptr;
     e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return -static_cast<int>(e);
@@ -1126,7 +1133,7 @@ FA_API int fa_gpu_ssim_noalloc(const void* x, const void* y, int dtype, int N, i
   double* partial = nullptr;
   {
     FA_DEVICE_SCOPE(device);
-    rc = scratch_on_current_device(&partial);
+    rc = scratch_on_current_device(static_cast<hipStream_t>(stream), &partial);
     if (rc != FA_OK) return rc;
   }
   return ssim_impl(x, y, dtype, N, C, H, W, nullptr, nullptr, nullptr, win, K, shift, C1, C2,

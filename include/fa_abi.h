@@ -341,7 +341,11 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials,
  * plane, fa_gpu_ssim_workspace) > FA_NOALLOC_SLOTS returns FA_E_SCRATCH
  * before touching the GPU (e.g. up to ~480 1080p planes at K = 11).
  * Calls on one GPU share its scratch: calls that overlap on one GPU (two
- * streams, two threads) race and must be serialised by the caller.
+ * streams, two threads) race and must be serialised by the caller.  The first
+ * call on a device looks up the scratch array's address there (which may
+ * load the code object); made on a stream under graph capture it returns
+ * FA_E_ARG and does nothing, so one eager call on the device must come before
+ * a capture.  After it the entry point can be captured and replayed.
  */
 #define FA_NOALLOC_SLOTS (1 << 20)
 FA_API int fa_gpu_ssim_noalloc(const void* x, const void* y, int dtype, int N,

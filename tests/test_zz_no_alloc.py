@@ -122,3 +122,44 @@ def test_noalloc_rejects_oversize_before_the_gpu(gpu):
                           11, 127.5, C1, C2, None, None, None, 0, None)
     assert rc == 8  # FA_E_SCRATCH
     assert b"scratch" in backend.load().gpu.fa_gpu_error_string(8)
+
+
+def test_noalloc_captured_in_a_graph_and_replayed(gpu):
+    """After one eager call on the device, fa_gpu_ssim_noalloc is captured
+    into a HIP graph (torch.cuda.CUDAGraph) over static input and output
+    buffers; each replay on new frames -- with eager calls of the library
+    between replays -- gives fa_gpu_ssim's eager means bit for bit."""
+    from frame_analytics_amd import backend
+
+    shape = (2, 3, 256, 384)
+    a0, b0 = u8_pair(shape, 9.0, seed=20)
+    x = torch.from_numpy(a0).to(gpu)
+    y = torch.from_numpy(b0).to(gpu)
+    n, c, h, w = shape
+    per, tot, _ = _outputs(x, False)
+    win = _window(gpu)
+
+    def call(stream):
+        return backend.call_gpu("fa_gpu_ssim_noalloc", x.data_ptr(), y.data_ptr(), 0, n, c, h,
+                                w, win.data_ptr(), 11, 127.5, C1, C2, None, per.data_ptr(),
+                                tot.data_ptr(), 0, stream)
+
+    assert call(torch.cuda.current_stream().cuda_stream) == 0  # the eager first call
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert call(torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    for k in range(3):
+        a, b = u8_pair(shape, 6.0 + 3 * k, seed=21 + k)
+        print(f"graph replay {k}", flush=True)
+        x.copy_(torch.from_numpy(a))
+        y.copy_(torch.from_numpy(b))
+        graph.replay()
+        got = (per.clone(), tot.clone())
+        torch.cuda.synchronize()
+        want = _with_workspace(x, y, False)  # eager, between the replays
+        torch.cuda.synchronize()
+        _same(got, want[:2])
+        o = ref.ssim(a[:1], b[:1], 255.0)
+        assert abs(float(got[0][0]) - o) <= 1e-6 * o
