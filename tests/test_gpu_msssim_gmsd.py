@@ -113,6 +113,23 @@ def test_ms_ssim_one_reduction_matches_per_scale_means(gpu, weights, luma):
     assert abs(float(tot) - want.mean()) < 1e-14
 
 
+@pytest.mark.parametrize("n", [1, 8, 69])
+def test_ms_ssim_batch_equals_single_images(gpu, n):
+    """The inference reduction (fa_gpu_ms_ssim_reduce) over a batch gives each
+    image the value a one-image call gives it, to 1e-14, and the batch mean
+    of them; 69 RGB images at 5 scales are 1035 (plane, scale) terms."""
+    a, b = u8_pair((n, 3, 176, 184), 9.0, seed=n)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    per = fa.ms_ssim(x, y, data_range=255.0, reduction="none").cpu().numpy()
+    for i in sorted({0, n // 2, n - 1}):
+        one = float(fa.ms_ssim(x[i:i + 1], y[i:i + 1], data_range=255.0))
+        assert abs(one - per[i]) < 1e-14, (i, one, per[i])
+    assert abs(float(fa.ms_ssim(x, y, data_range=255.0)) - per.mean()) < 1e-14
+    if n == 1:
+        want = ref.ms_ssim(a.astype(np.float64), b.astype(np.float64), 255.0)
+        assert _rel(float(per[0]), float(want)) <= REL
+
+
 def test_ms_ssim_nan_propagates_like_torch(gpu):
     """A NaN sample makes MS-SSIM NaN on every path: the fused inference
     reduction (fa_gpu_ms_ssim_reduce) clamps like torch's clamp_min, which
