@@ -14,9 +14,9 @@ Also reported: PSNR on configs[2] (8x3x2160x3840 uint8), as achieved GB/s at 2
 bytes per sample and its fraction of the 8 TB/s HBM peak.
 
 ``roofline`` is measured live for the dominant kernel (the matrix-core SSIM
-kernel, ssim_u8_mfma_kernel): its launches are bracketed with HIP events on the
-stream they run on, through the C ABI with no finalize sinks, so the average is
-that kernel alone.  The algorithmic bytes are 2 B per input sample; the kernel
+kernel, which an fa.ssim call runs as its only launch: it also finishes the
+mean): its launches through the C ABI (fa_gpu_ssim_once) are bracketed with
+HIP events on the stream they run on, so the average is that kernel alone.  The algorithmic bytes are 2 B per input sample; the kernel
 is bound by instruction issue (vector ALU and matrix cores together), so its
 arithmetic -- the two 11-tap passes over four moments and the SSIM formula,
 counted as float32 operations per output pixel -- is reported beside the HBM
@@ -41,6 +41,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -314,9 +315,9 @@ def profile_sequence(launches=20):
     """A fixed launch sequence for rocprofv3 counter runs (``--profile``):
     a torch copy of exactly 256 MiB (the FETCH_SIZE / WRITE_SIZE calibration:
     256 MiB read, 256 MiB written), then `launches` launches each of the SSIM
-    kernel (configs[1]; reduction, then with the float32 map), the GMSD kernel
-    (configs[4]) and the PSNR pixel kernel, through the C ABI,
-    rotating resident input pairs."""
+    kernel (configs[1]; the one-launch mean, then with the float32 map), the
+    GMSD kernel (configs[4], one launch) and the PSNR pixel kernel (configs[2],
+    one launch), through the C ABI, rotating resident input pairs."""
     import torch
 
     import frame_analytics_amd as fa
@@ -338,11 +339,14 @@ def profile_sequence(launches=20):
     win = fa.gaussian_window_1d(11, 1.5, device=dev, dtype=torch.float32)
     bpp = backend.workspace_slots("ssim", h, w, 11)
     partial = torch.empty((n * c, bpp), dtype=torch.float64, device=dev)
+    acc = torch.zeros(backend._ACC_WORDS["ssim"], dtype=torch.int64, device=dev)
+    tot = torch.empty((), dtype=torch.float64, device=dev)
     for i in range(launches):
         a, b = pairs[i % 4]
-        assert lib.fa_gpu_ssim(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, win.data_ptr(), 11,
-                               127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, None,
-                               partial.data_ptr(), bpp, None, None, 0, stream) == 0
+        assert lib.fa_gpu_ssim_once(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, None, None, None,
+                                    win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
+                                    (0.03 * 255) ** 2, None, partial.data_ptr(), bpp,
+                                    acc.data_ptr(), None, tot.data_ptr(), 0, stream) == 0
     torch.cuda.synchronize()
     # the same kernel writing the float32 map (configs[1], return_map=True)
     smap = torch.empty((n, c, h - 10, w - 10), dtype=torch.float32, device=dev)
@@ -359,11 +363,13 @@ def profile_sequence(launches=20):
     ps2 = torch.empty_like(ps)
     gm = torch.empty(n, dtype=torch.float64, device=dev)
     gs = torch.empty_like(gm)
+    gacc = torch.zeros(backend._ACC_WORDS["gmsd"], dtype=torch.int64, device=dev)
     for i in range(launches):
         a, b = pairs[i % 4]
-        assert lib.fa_gpu_gmsd(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, 170.0, (255e-6) ** 2,
-                               1, ps.data_ptr(), ps2.data_ptr(), gbpp, gm.data_ptr(),
-                               gs.data_ptr(), 0, stream) == 0
+        assert lib.fa_gpu_gmsd_once(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, None, None, None,
+                                    170.0, (255e-6) ** 2, 1, ps.data_ptr(), ps2.data_ptr(), gbpp,
+                                    gacc.data_ptr(), gm.data_ptr(), gs.data_ptr(), None, 0,
+                                    stream) == 0
     torch.cuda.synchronize()
     del pairs, partial, ps, ps2
 
@@ -372,11 +378,14 @@ def profile_sequence(launches=20):
     per = ppairs[0][0].numel() // pn
     bpi = backend.workspace_slots("pixel", pn, per, 0)
     ppart = torch.empty((pn, bpi), dtype=torch.float64, device=dev)
+    pacc = torch.zeros(backend._ACC_WORDS["pixel"], dtype=torch.int64, device=dev)
+    pdb = torch.empty((), dtype=torch.float64, device=dev)
     for i in range(launches):
         a, b = ppairs[i % 2]
-        assert lib.fa_gpu_pixel_reduce(a.data_ptr(), b.data_ptr(), 0, pn, per, 0, 0.0, -1e300,
-                                       ppart.data_ptr(), bpi, None, None, None, None, 0,
-                                       stream) == 0
+        assert lib.fa_gpu_pixel_reduce_once(a.data_ptr(), b.data_ptr(), 0, pn, per, 0, 0.0,
+                                            10.0 * math.log10(255.0 ** 2), ppart.data_ptr(), bpi,
+                                            pacc.data_ptr(), None, None, None, pdb.data_ptr(), 0,
+                                            stream) == 0
     torch.cuda.synchronize()
     print("profile sequence done", flush=True)
 
@@ -608,11 +617,17 @@ def main():
     partial = torch.empty((n * c, bpp), dtype=torch.float64, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
 
+    # the kernel an fa.ssim call runs, alone: fa_gpu_ssim_once finishes the
+    # batch mean inside its one launch
+    acc = torch.zeros(backend._ACC_WORDS["ssim"], dtype=torch.int64, device=dev)
+    ktot = torch.empty((), dtype=torch.float64, device=dev)
+
     def ssim_kernel(i):
         a, b = pairs[i % len(pairs)]
-        rc = lib.fa_gpu_ssim(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, win.data_ptr(), 11,
-                             127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2, None,
-                             partial.data_ptr(), bpp, None, None, 0, stream)
+        rc = lib.fa_gpu_ssim_once(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, None, None, None,
+                                  win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
+                                  (0.03 * 255) ** 2, None, partial.data_ptr(), bpp,
+                                  acc.data_ptr(), None, ktot.data_ptr(), 0, stream)
         assert rc == 0, rc
 
     k_ms = _kernel_ms(torch, ssim_kernel, 200)
@@ -698,10 +713,17 @@ def main():
     bpi = backend.workspace_slots("pixel", pn, per, 0)
     ppart = torch.empty((pn, bpi), dtype=torch.float64, device=dev)
 
+    # the one launch an fa.psnr call makes (the sweep that also finishes the
+    # batch's dB), alone
+    pacc = torch.zeros(backend._ACC_WORDS["pixel"], dtype=torch.int64, device=dev)
+    pdb = torch.empty((), dtype=torch.float64, device=dev)
+
     def psnr_kernel(i):
         a, b = ppairs[i % len(ppairs)]
-        rc = lib.fa_gpu_pixel_reduce(a.data_ptr(), b.data_ptr(), 0, pn, per, 0, 0.0, -1e300,
-                                     ppart.data_ptr(), bpi, None, None, None, None, 0, stream)
+        rc = lib.fa_gpu_pixel_reduce_once(a.data_ptr(), b.data_ptr(), 0, pn, per, 0, 0.0,
+                                          10.0 * math.log10(255.0 ** 2), ppart.data_ptr(), bpi,
+                                          pacc.data_ptr(), None, None, None, pdb.data_ptr(), 0,
+                                          stream)
         assert rc == 0, rc
 
     pk_ms = _kernel_ms(torch, psnr_kernel, 200)
@@ -762,7 +784,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _pmc_value("traffic_bytes_per_launch"),
-            "kernel": "ssim_mfma_kernel<REDUCE> (v_mfma_f32_16x16x32_f16 passes)",
+            "kernel": "ssim_mfma_kernel<uint8,REDUCE,finish> (v_mfma_f32_16x16x32_f16 passes)",
             "kernel_ms": round(k_ms, 4),
             "limiter": "instruction issue (VALU + MFMA), not HBM",
             # the filter and formula work as float32 operations per output
@@ -780,7 +802,7 @@ def main():
             "ms_per_step": round(p_ms, 4),
             "GBps_end_to_end": round(pbytes / (p_ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak_end_to_end": round(pbytes / (p_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "kernel": "pix_sweep_kernel<uint8,MSE>",
+            "kernel": "pix_sweep_kernel<uint8,MSE> finishing the dB in its launch",
             "kernel_ms": round(pk_ms, 4),
             "GBps_kernel": round(pbytes / (pk_ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(pbytes / (pk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

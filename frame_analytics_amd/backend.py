@@ -865,6 +865,39 @@ def gmsd_stats_bwd(x, y, mean, std, g_mean, g_std, T, eps, downsample, need_dx, 
     return dx, dy
 
 
+@functools.lru_cache(maxsize=256)
+def _ms_workspace_bytes(code: int, n: int, c: int, h: int, w: int, k: int, m: int,
+                        luma: bool) -> int:
+    """Bytes of fa_gpu_ms_ssim's workspace for one call shape (asked once per
+    shape, so a graph capture never issues the query)."""
+    out = ctypes.c_int64(0)
+    _run("fa_gpu_ms_ssim_workspace", code, n, c, h, w, k, m, int(luma), ctypes.byref(out))
+    return int(out.value)
+
+
+def ms_ssim_fused(x, y, win, shift, C1, C2, weights, luma=None, per_image=False):
+    """Inference MS-SSIM in one C-ABI call (``fa_gpu_ms_ssim``): every scale's
+    fused pass and the reduction, launched back to back from the library, over
+    one workspace allocation; per-image values (``per_image``) or their
+    batch mean."""
+    win = _win32(win)
+    n, c, h, w = (int(v) for v in x.shape)
+    k = int(win.numel())
+    m = len(weights)
+    x, xs = _view_strides(x)
+    y, ys = _view_strides(y)
+    code = _DTYPE_CODE[x.dtype]
+    nbytes = _ms_workspace_bytes(code, n, c, h, w, k, m, luma is not None)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    out = _f64(x.device, n) if per_image else _f64(x.device)
+    wts = (ctypes.c_double * m)(*[float(v) for v in weights])
+    dev, stream = _site(x)
+    _run("fa_gpu_ms_ssim", _ptr(x), _ptr(y), code, n, c, h, w, xs, ys, _luma_arg(luma),
+         _ptr(win), k, float(shift), float(C1), float(C2), wts, m, _ptr(ws), nbytes,
+         _ptr(out) if per_image else None, None if per_image else _ptr(out), dev, stream)
+    return out
+
+
 def ms_ssim_reduce(partials, slots, npix, weights, n: int, c: int, per_image: bool):
     """MS-SSIM's per-scale plane reductions, clamp / power / product and the
     channel and batch means in two launches (``fa_gpu_ms_ssim_reduce``) from

@@ -1067,6 +1067,90 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
                          out_per_image, out_total, nullptr, nullptr, st);
 }
 
+// MS-SSIM's reduction (fa_gpu_ms_ssim_reduce, and the end of fa_gpu_ms_ssim).
+static int ms_reduce_impl(const double* const* partials, const int* slots, const double* npix,
+                          const double* weights, int M, int N, int C, double* plane_scratch,
+                          double* out_per_image, double* out_total, int device, void* stream) {
+  if (!partials || !slots || !npix || !weights || !plane_scratch) return FA_E_ARG;
+  if (M <= 0 || M > MS_MAX_SCALES || N <= 0 || C <= 0) return FA_E_SHAPE;
+  if (!out_per_image && !out_total) return FA_E_ARG;
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  if (planes > INT32_MAX) return FA_E_SHAPE;
+  MsParts parts = {};
+  for (int m = 0; m < M; ++m) {
+    if (!partials[m]) return FA_E_ARG;
+    if (slots[m] <= 0 || !(npix[m] > 0.0)) return FA_E_SHAPE;
+    parts.p[m] = partials[m];
+    parts.slots[m] = slots[m];
+    parts.npix[m] = npix[m];
+    parts.w[m] = weights[m];
+  }
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(ms_term_kernel, dim3(static_cast<unsigned>(planes), M), dim3(BLOCK), 0, st,
+                     parts, plane_scratch);
+  FA_LAUNCH_CHECK();
+  hipLaunchKernelGGL(ms_finish_kernel, dim3(1), dim3(BLOCK), 0, st, M, N, C, plane_scratch,
+                     out_per_image, out_total);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
+}
+
+// The layout of fa_gpu_ms_ssim's workspace and the per-scale shapes and
+// element types: the exact pyramid of the inference path (float16 first level
+// and float32 below it under uint8 input, float64 under floating input or a
+// luma plane), each scale's partial sums (the cs sums, and the SSIM sums at
+// the coarsest scale) and the reduction's scratch, every piece 256-byte
+// aligned.  Every scale's shape is checked here, before anything runs.
+struct MsPlan {
+  int M, cout;
+  int H[MS_MAX_SCALES], W[MS_MAX_SCALES], bpp[MS_MAX_SCALES];
+  int in_dtype[MS_MAX_SCALES];     // dtype code of scale i's input
+  int level_dtype[MS_MAX_SCALES];  // element type of level i (i >= 1)
+  int64_t level_x[MS_MAX_SCALES], level_y[MS_MAX_SCALES];  // byte offsets (i >= 1)
+  int64_t pcs[MS_MAX_SCALES], ps_last, scratch, total;
+};
+
+static int ms_plan(int dtype, int N, int C, int H, int W, int K, int M, bool luma, MsPlan* p) {
+  if (dtype < FA_U8 || dtype > FA_F64) return FA_E_DTYPE;
+  if (M <= 0 || M > MS_MAX_SCALES || N <= 0 || C <= 0) return FA_E_SHAPE;
+  if (luma && C != 3) return FA_E_SHAPE;
+  p->M = M;
+  p->cout = luma ? 1 : C;
+  const int64_t planes = static_cast<int64_t>(N) * p->cout;
+  const bool u8 = dtype == FA_U8 && !luma;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  for (int i = 0; i < M; ++i) {
+    p->H[i] = i == 0 ? H : p->H[i - 1] / 2;
+    p->W[i] = i == 0 ? W : p->W[i - 1] / 2;
+    int Hout = 0, Wout = 0;
+    const int rc = ssim_shape(N, i == 0 ? C : p->cout, p->H[i], p->W[i], K, &Hout, &Wout);
+    if (rc != FA_OK) return rc;
+    p->bpp[i] = ssim_slots(Hout, Wout, K);
+    if (i > 0) {
+      p->level_dtype[i] = u8 ? (i == 1 ? FA_F16 : FA_F32) : FA_F64;
+      p->in_dtype[i] = u8 ? (p->level_dtype[i] | FA_DTYPE_U8_PYRAMID) : FA_F64;
+      const int64_t eb = p->level_dtype[i] == FA_F16 ? 2 : p->level_dtype[i] == FA_F32 ? 4 : 8;
+      const int64_t lb = planes * p->H[i] * p->W[i] * eb;
+      p->level_x[i] = take(lb);
+      p->level_y[i] = take(lb);
+    } else {
+      p->in_dtype[i] = dtype;
+      p->level_dtype[i] = dtype;
+    }
+    p->pcs[i] = take(planes * p->bpp[i] * 8);
+  }
+  p->ps_last = take(planes * p->bpp[M - 1] * 8);
+  p->scratch = take(static_cast<int64_t>(M) * planes * 8);
+  p->total = off;
+  return FA_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Fixed scratch for fa_gpu_ssim_noalloc: the float64 partial sums of one
 // call (N * C * slots per plane), in a file-scope device array.  Every GPU the
@@ -1293,29 +1377,63 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials, const int* slots
                                  const double* npix, const double* weights, int M, int N,
                                  int C, double* plane_scratch, double* out_per_image,
                                  double* out_total, int device, void* stream) {
-  if (!partials || !slots || !npix || !weights || !plane_scratch) return FA_E_ARG;
-  if (M <= 0 || M > MS_MAX_SCALES || N <= 0 || C <= 0) return FA_E_SHAPE;
-  if (!out_per_image && !out_total) return FA_E_ARG;
-  const int64_t planes = static_cast<int64_t>(N) * C;
-  if (planes > INT32_MAX) return FA_E_SHAPE;
-  MsParts parts = {};
-  for (int m = 0; m < M; ++m) {
-    if (!partials[m]) return FA_E_ARG;
-    if (slots[m] <= 0 || !(npix[m] > 0.0)) return FA_E_SHAPE;
-    parts.p[m] = partials[m];
-    parts.slots[m] = slots[m];
-    parts.npix[m] = npix[m];
-    parts.w[m] = weights[m];
-  }
-  FA_DEVICE_SCOPE(device);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(ms_term_kernel, dim3(static_cast<unsigned>(planes), M), dim3(BLOCK), 0, st,
-                     parts, plane_scratch);
-  FA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(ms_finish_kernel, dim3(1), dim3(BLOCK), 0, st, M, N, C, plane_scratch,
-                     out_per_image, out_total);
-  FA_LAUNCH_CHECK();
+  return ms_reduce_impl(partials, slots, npix, weights, M, N, C, plane_scratch, out_per_image,
+                        out_total, device, stream);
+}
+
+// No counterpart in the reference, whose MS-SSIM is a Python loop over the
+// scales with torch pooling between them (functional.py:874-901).  The
+// workspace of one fa_gpu_ms_ssim call.
+FA_API int fa_gpu_ms_ssim_workspace(int dtype, int N, int C, int H, int W, int K, int M,
+                                    int luma, int64_t* out_bytes) {
+  if (!out_bytes) return FA_E_ARG;
+  MsPlan p;
+  const int rc = ms_plan(dtype, N, C, H, W, K, M, luma != 0, &p);
+  if (rc != FA_OK) return rc;
+  *out_bytes = p.total;
   return FA_OK;
+}
+
+// No counterpart in the reference (see fa_gpu_ms_ssim_workspace): the whole
+// inference MS-SSIM in one call -- every scale's fused CS pass (which also
+// writes the next pyramid level) and the reduction, launched back to back.
+FA_API int fa_gpu_ms_ssim(const void* x, const void* y, int dtype, int N, int C, int H, int W,
+                          const int64_t* x_strides, const int64_t* y_strides,
+                          const double* luma, const float* win, int K, double shift,
+                          double C1, double C2, const double* weights, int M, void* workspace,
+                          int64_t workspace_bytes, double* out_per_image, double* out_total,
+                          int device, void* stream) {
+  if (!x || !y || !win || !weights || !workspace) return FA_E_ARG;
+  if (!out_per_image && !out_total) return FA_E_ARG;
+  if (luma && C != 3) return FA_E_SHAPE;
+  MsPlan p;
+  int rc = ms_plan(dtype, N, C, H, W, K, M, luma != nullptr, &p);
+  if (rc != FA_OK) return rc;
+  if (workspace_bytes < p.total) return FA_E_ARG;
+  char* ws = static_cast<char*>(workspace);
+  const double* parts[MS_MAX_SCALES];
+  int slots[MS_MAX_SCALES];
+  double npix[MS_MAX_SCALES];
+  for (int i = 0; i < M; ++i) {
+    const bool last = i == M - 1;
+    const void* xi = i == 0 ? x : ws + p.level_x[i];
+    const void* yi = i == 0 ? y : ws + p.level_y[i];
+    double* pcs = reinterpret_cast<double*>(ws + p.pcs[i]);
+    double* ps = last ? reinterpret_cast<double*>(ws + p.ps_last) : nullptr;
+    void* px = last ? nullptr : ws + p.level_x[i + 1];
+    void* py = last ? nullptr : ws + p.level_y[i + 1];
+    rc = ssim_cs_impl(xi, yi, p.in_dtype[i], N, i == 0 ? C : p.cout, p.H[i], p.W[i],
+                      i == 0 ? x_strides : nullptr, i == 0 ? y_strides : nullptr,
+                      i == 0 ? luma : nullptr, win, K, shift, C1, C2, ps, pcs, p.bpp[i], nullptr,
+                      nullptr, &slots[i], px, py, last ? FA_F64 : p.level_dtype[i + 1], device,
+                      stream);
+    if (rc != FA_OK) return rc;
+    parts[i] = last ? ps : pcs;
+    npix[i] = static_cast<double>(p.H[i] - K + 1) * (p.W[i] - K + 1);
+  }
+  return ms_reduce_impl(parts, slots, npix, weights, M, N, p.cout,
+                        reinterpret_cast<double*>(ws + p.scratch), out_per_image, out_total,
+                        device, stream);
 }
 
 }  // extern "C"

@@ -566,26 +566,13 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
         consts = (shift, C1, C2)
         cx, cy = x4, y4
         if not grad and len(w) <= 8:
-            # inference: every scale leaves its partial sums, and one reduction
-            # finishes all scales (plane terms, product, channel and batch means)
-            # The levels below uint8 input are exact 2x2 means of bytes, which
-            # the native side may treat as such (matrix-core kernel); the first
-            # (multiples of 1/4 in [0, 255]) is exact in float16, half the bytes
-            # to write and read, the deeper ones in float32.
-            u8 = x4.dtype == torch.uint8 and lw is None
-            parts, slots, npix = [], [], []
-            for i in range(scales):
-                last = i == scales - 1
-                ldt = torch.float16 if u8 and i == 0 else pdt
-                # the SSIM sums only at the coarsest scale, cs below it
-                ps, pcs, sl, npx, cx, cy = backend.ssim_cs_partials(
-                    cx, cy, win32, shift, C1, C2, None if last else ldt,
-                    luma=lw if i == 0 else None, u8_pyramid=u8 and i > 0, ssim_sums=last)
-                parts.append(ps if last else pcs)
-                slots.append(sl)
-                npix.append(npx)
-            return backend.ms_ssim_reduce(parts, slots, npix, w, n, c,
-                                          per_image=reduction == "none")
+            # inference: one library call runs every scale's fused pass (cs
+            # sums, the SSIM sums at the coarsest scale, the next exact level:
+            # float16 for the first level and float32 below it under uint8,
+            # float64 otherwise) and the reduction (plane terms, product,
+            # channel and batch means), with no host work between launches
+            return backend.ms_ssim_fused(x4, y4, win32, shift, C1, C2, w, luma=lw,
+                                         per_image=reduction == "none")
         for i in range(scales):
             last = i == scales - 1
             if grad:

@@ -331,6 +331,30 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials,
                                  double* out_total, int device, void* stream);
 
 /*
+ * No counterpart in the reference, whose MS-SSIM is a Python loop over the
+ * scales with torch pooling between them (functional.py:874-901).  The
+ * inference MS-SSIM in one call: for each of the M (<= 8) scales the fused
+ * pass of fa_gpu_ssim_cs_ex (the cs sums; the SSIM sums at the coarsest
+ * scale; the next pyramid level, exact: float16 for the first level and
+ * float32 below it under uint8 input, float64 under floating input or a luma
+ * plane), then the reduction of fa_gpu_ms_ssim_reduce, launched back to back
+ * with no host work between them.  x / y: N x C x H x W of any dtype, with
+ * optional strides and luma as in fa_gpu_ssim_ex; weights: host array of M.
+ * workspace: at least fa_gpu_ms_ssim_workspace's bytes of device memory
+ * (levels, partial sums, scratch).  Every scale's shape is checked before
+ * anything is launched.  out_per_image (N) / out_total (1) float64: either
+ * may be null, not both.
+ */
+FA_API int fa_gpu_ms_ssim_workspace(int dtype, int N, int C, int H, int W, int K, int M,
+                                    int luma, int64_t* out_bytes);
+FA_API int fa_gpu_ms_ssim(const void* x, const void* y, int dtype, int N, int C, int H, int W,
+                          const int64_t* x_strides, const int64_t* y_strides,
+                          const double* luma, const float* win, int K, double shift,
+                          double C1, double C2, const double* weights, int M, void* workspace,
+                          int64_t workspace_bytes, double* out_per_image, double* out_total,
+                          int device, void* stream);
+
+/*
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory -- code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc: fa_gpu_ssim (same arguments, same results, the same

@@ -39,7 +39,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 23  # 12 reference entry points + 11 extensions
+    assert len(decl) == 25  # 12 reference entry points + 13 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name
@@ -94,6 +94,18 @@ def test_workspace_queries(lib):
     assert lib.fa_gpu_gmsd_workspace(1080, 1920, 1, ctypes.byref(out)) == 0
     assert out.value == 16 * 135  # 538x958 output: 62-column strips, 4-row tiles
     assert lib.fa_gpu_gmsd_workspace(5, 5, 1, ctypes.byref(out)) == 2
+    # fa_gpu_ms_ssim's workspace: levels, partial sums and scratch, every scale checked
+    nb = ctypes.c_int64(0)
+    assert lib.fa_gpu_ms_ssim_workspace(0, 8, 3, 1080, 1920, 11, 5, 0, ctypes.byref(nb)) == 0
+    u8 = nb.value
+    # at least the float16 first level and the float32 second of both inputs
+    assert u8 >= 2 * 24 * (540 * 960 * 2 + 270 * 480 * 4)
+    assert lib.fa_gpu_ms_ssim_workspace(3, 8, 3, 1080, 1920, 11, 5, 0, ctypes.byref(nb)) == 0
+    assert nb.value > u8  # float64 levels under float32 input
+    assert lib.fa_gpu_ms_ssim_workspace(0, 1, 1, 160, 200, 11, 5, 0, ctypes.byref(nb)) == 2
+    assert lib.fa_gpu_ms_ssim_workspace(0, 1, 1, 176, 176, 11, 5, 0, ctypes.byref(nb)) == 0
+    assert lib.fa_gpu_ms_ssim_workspace(0, 1, 1, 176, 176, 11, 9, 0, ctypes.byref(nb)) == 2
+    assert lib.fa_gpu_ms_ssim_workspace(0, 1, 2, 176, 176, 11, 5, 1, ctypes.byref(nb)) == 2
 
 
 def test_argument_validation_before_any_gpu_work(lib):
@@ -106,6 +118,15 @@ def test_argument_validation_before_any_gpu_work(lib):
                                    None, None, None, None, 0, None) == 4  # FA_E_OP
     assert lib.fa_gpu_pixel_reduce(p, p, 0, 0, 16, 0, 0.0, -1e300, p, 1,
                                    None, None, None, None, 0, None) == 2
+    w5 = (ctypes.c_double * 5)(0.0448, 0.2856, 0.3001, 0.2363, 0.1333)
+    ms = lib.fa_gpu_ms_ssim
+    # a scale too small, and a workspace too small: refused before any launch
+    assert ms(p, p, 0, 1, 1, 160, 200, None, None, None, p, 11, 127.5, 6.5, 58.5, w5, 5, p,
+              1 << 40, p, None, 0, None) == 2
+    assert ms(p, p, 0, 1, 1, 176, 176, None, None, None, p, 11, 127.5, 6.5, 58.5, w5, 5, p,
+              16, p, None, 0, None) == 5
+    assert ms(p, p, 0, 1, 1, 176, 176, None, None, None, p, 11, 127.5, 6.5, 58.5, w5, 5, p,
+              1 << 40, None, None, 0, None) == 5  # no output
     once = lib.fa_gpu_pixel_reduce_once
     assert once(p, p, 0, 1, 16, 0, 0.0, -1e300, None, 1, p, p, None, None, None, 0, None) == 5
     assert once(p, p, 0, 1, 16, 4, 0.0, -1e300, p, 1, p, p, None, None, None, 0, None) == 4
