@@ -241,6 +241,16 @@ def call_gpu(name: str, *args) -> int:
     return int(code)
 
 
+def _run_or_needs_workspace(name: str, args_without, args_with) -> None:
+    """Call a one-launch entry point without its workspace first (it is not
+    read where the call finishes in its launch); when the library answers
+    FA_E_ARG -- it refuses before launching anything -- call it again with the
+    workspace that ``args_with()`` allocates."""
+    if call_gpu(name, *args_without) == 0:
+        return
+    _run(name, *args_with())
+
+
 def _run(name: str, *args) -> None:
     """:func:`call_gpu`, raising :class:`KernelError` on a non-zero status."""
     code = call_gpu(name, *args)
@@ -358,7 +368,6 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
     per = c * h * w
     dev, stream = _site(x)
     bpi = workspace_slots("pixel", n, per, dev)
-    partial = _f64(x.device, n, bpi)
     out = _f64(x.device, n) if per_image else _f64(x.device)
     # the four ABI sinks, in order: mean per image, mean total, dB per image,
     # dB total; exactly one is written
@@ -366,10 +375,18 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
     sinks = [_ptr(out) if i == slot else None for i in range(4)]
     if luma is None and xs is None and ys is None:
         acc = _acc_for("pixel", x.device, dev, stream) if x.dtype == torch.uint8 else None
-        _run("fa_gpu_pixel_reduce_once", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op,
-             float(param), float(psnr_bias), _ptr(partial), bpi, _ptr(acc), *sinks, dev,
-             stream)
+
+        def args(partial):
+            return (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, per, op, float(param),
+                    float(psnr_bias), partial, bpi, _ptr(acc), *sinks, dev, stream)
+
+        if acc is None:
+            _run("fa_gpu_pixel_reduce_once", *args(_ptr(_f64(x.device, n, bpi))))
+        else:
+            _run_or_needs_workspace("fa_gpu_pixel_reduce_once", args(None),
+                                    lambda: args(_ptr(_f64(x.device, n, bpi))))
     else:
+        partial = _f64(x.device, n, bpi)
         _run("fa_gpu_pixel_reduce_ex", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w,
              xs, ys, _luma_arg(luma), op, float(param), float(psnr_bias), _ptr(partial), bpi,
              *sinks, dev, stream)
@@ -558,7 +575,6 @@ def _ssim_native(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: floa
     planes = n * (1 if luma is not None else c)
     bpp = workspace_slots("ssim", h, w, win_size)
     dev, stream = _site(x)
-    partial = _f64(x.device, planes, bpp)
     # one sink: the float32 map, the per-image means or the batch mean
     smap = per_image = total = None
     if return_map:
@@ -569,16 +585,30 @@ def _ssim_native(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: floa
     else:
         total = _f64(x.device)
     head = (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w)
-    tail = (_ptr(win), win_size, float(shift), float(C1), float(C2), _ptr(smap),
-            _ptr(partial), bpp, _ptr(per_image), _ptr(total), dev, stream)
+
+    def tail(partial):
+        return (_ptr(win), win_size, float(shift), float(C1), float(C2), _ptr(smap), partial,
+                bpp, _ptr(per_image), _ptr(total), dev, stream)
+
     if smap is None:
         acc = _acc_for("ssim", x.device, dev, stream) if x.dtype == torch.uint8 else None
-        _run("fa_gpu_ssim_once", *head, xs, ys, _luma_arg(luma), *tail[:8], _ptr(acc),
-             *tail[8:])
-    elif luma is None and xs is None and ys is None:
-        _run("fa_gpu_ssim", *head, *tail)
+        lw = _luma_arg(luma)
+
+        def args(partial):
+            t = tail(partial)
+            return (*head, xs, ys, lw, *t[:8], _ptr(acc), *t[8:])
+
+        if acc is None:
+            _run("fa_gpu_ssim_once", *args(_ptr(_f64(x.device, planes, bpp))))
+        else:
+            _run_or_needs_workspace("fa_gpu_ssim_once", args(None),
+                                    lambda: args(_ptr(_f64(x.device, planes, bpp))))
+        return per_image if reduction == "none" else total
+    partial = _ptr(_f64(x.device, planes, bpp))
+    if luma is None and xs is None and ys is None:
+        _run("fa_gpu_ssim", *head, *tail(partial))
     else:
-        _run("fa_gpu_ssim_ex", *head, xs, ys, _luma_arg(luma), *tail)
+        _run("fa_gpu_ssim_ex", *head, xs, ys, _luma_arg(luma), *tail(partial))
     if return_map:
         return smap if dtype == torch.float32 else smap.to(dtype)
     return per_image if reduction == "none" else total
@@ -810,17 +840,21 @@ def _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, w
     n, c, h, w = (int(v) for v in x.shape)
     bpp = workspace_slots("gmsd", h, w, int(bool(downsample)))
     dev, stream = _site(x)
-    # one allocation for both workspaces and one for the outputs (each torch
-    # allocation is ~1.7 us of host time)
-    psum, psumsq = _f64(x.device, 2, planes, bpp).unbind(0)
     head = (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w)
     consts = (float(T), float(eps), int(bool(downsample)))
+
+    def workspaces():
+        # one allocation for both (each torch allocation is ~1.7 us of host time)
+        ps, pss = _f64(x.device, 2, planes, bpp).unbind(0)
+        return _ptr(ps), _ptr(pss)
+
     if want_map:
+        psum, psumsq = workspaces()
         mean, std = _f64(x.device, 2, n).unbind(0)
         qmap = torch.empty((n, planes // n, hd - 2, wd - 2), dtype=torch.float32,
                            device=x.device)
         _run("fa_gpu_gmsd_ex", *head, xs, ys, _luma_arg(luma), *consts, _ptr(qmap),
-             _ptr(psum), _ptr(psumsq), bpp, _ptr(mean), _ptr(std), dev, stream)
+             psum, psumsq, bpp, _ptr(mean), _ptr(std), dev, stream)
         return mean, std, qmap
     if separate:
         mean, std, batch = _f64(x.device, n), _f64(x.device, n), None
@@ -828,8 +862,17 @@ def _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, w
         out = _f64(x.device, 2 * n + 2)
         mean, std, batch = out[:n], out[n:2 * n], out[2 * n:]
     acc = _acc_for("gmsd", x.device, dev, stream) if x.dtype == torch.uint8 else None
-    _run("fa_gpu_gmsd_once", *head, xs, ys, _luma_arg(luma), *consts, _ptr(psum),
-         _ptr(psumsq), bpp, _ptr(acc), _ptr(mean), _ptr(std), _ptr(batch), dev, stream)
+    lw = _luma_arg(luma)
+
+    def args(ws):
+        return (*head, xs, ys, lw, *consts, *ws, bpp, _ptr(acc), _ptr(mean), _ptr(std),
+                _ptr(batch), dev, stream)
+
+    if acc is None:
+        _run("fa_gpu_gmsd_once", *args(workspaces()))
+    else:
+        _run_or_needs_workspace("fa_gpu_gmsd_once", args((None, None)),
+                                lambda: args(workspaces()))
     return mean, std, batch
 
 

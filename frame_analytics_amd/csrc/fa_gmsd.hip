@@ -974,6 +974,8 @@ static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipSt
   if (tasks > INT32_MAX / WAVES_PER_BLOCK) return FA_E_SHAPE;
   a.wpi = static_cast<int>(wpi);
   a.tasks = static_cast<int>(tasks);
+  if ((!a.psum || !a.psumsq) && !(Src::U8IN && fin_ok && wpi < (1 << GF_COUNT_BITS)))
+    return FA_E_ARG;
   if constexpr (Src::U8IN) {
     if (fin_ok && wpi < (1 << GF_COUNT_BITS)) {
       hipLaunchKernelGGL((gmsd_kernel<Src, false, true>), dim3(static_cast<unsigned>(tasks)),
@@ -1025,7 +1027,10 @@ static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int 
                      double eps, int downsample, float* map_out, double* psum, double* psumsq,
                      int bpp, double* out_mean, double* out_std, int device, void* stream,
                      uint64_t* acc = nullptr, double* out_batch = nullptr) {
-  if (!x || !y || !psum || !psumsq || !out_mean || !out_std) return FA_E_ARG;
+  // null psum / psumsq are enough only where the launch finishes the call
+  // (launch_gmsd refuses them otherwise, before launching)
+  if (!x || !y || !out_mean || !out_std) return FA_E_ARG;
+  if ((!psum || !psumsq) && !acc) return FA_E_ARG;
   if (N <= 0 || C <= 0) return FA_E_SHAPE;
   if (dtype < FA_U8 || dtype > FA_F64) return FA_E_DTYPE;
   if (luma && C != 3) return FA_E_SHAPE;

@@ -629,6 +629,20 @@ static int launch_sweep_shape(hipStream_t st, const void* a, const void* b, int6
   return static_cast<int>(G * (NT / WAVE));
 }
 
+// Whether launch_sweep<T, OP> launches (the same tests, nothing launched).
+template <typename T>
+static bool sweep_applies(const void* a, const void* b, int64_t n_images, int64_t per,
+                          int bpi) {
+  constexpr int64_t E = 16 / static_cast<int64_t>(sizeof(T));
+  const uintptr_t bases = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
+  if ((bases & 15) != 0 || per % E != 0 || bpi % SWEEP_SLOTS_PER_CU != 0) return false;
+  const int64_t nv = per / E;
+  const int64_t G = bpi / SWEEP_SLOTS_PER_CU;
+  if (std::is_same<T, uint8_t>::value && per * n_images < SWEEP_MANY_WAVES_BELOW)
+    return nv >= G * SWEEP_MANY_BLOCK;
+  return nv >= static_cast<int64_t>(SWEEP_UNROLL) * G * SWEEP_BLOCK;
+}
+
 // Launch of the sweep when it applies: 16-byte aligned bases, whole vectors
 // per image, bpi a multiple of SWEEP_SLOTS_PER_CU (one workgroup per CU) and
 // at least one round per image.  Returns the partial columns per image it
@@ -1100,12 +1114,10 @@ FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
                                     int bpi, uint64_t* acc, double* out_per_image,
                                     double* out_total, double* out_psnr_per_image,
                                     double* out_psnr_total, int device, void* stream) {
-  if (!a || !b || !partial) return FA_E_ARG;
+  if (!a || !b || (!partial && !acc)) return FA_E_ARG;
   if (op < 0 || op > 3) return FA_E_OP;
   if (n_images <= 0 || n_per_image <= 0 || bpi <= 0) return FA_E_SHAPE;
   if (n_images > 65535 || static_cast<int64_t>(bpi) * BLOCK > INT32_MAX) return FA_E_SHAPE;
-  FA_DEVICE_SCOPE(device);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(bpi), static_cast<unsigned>(n_images));
   const uintptr_t rel = reinterpret_cast<uintptr_t>(a) - reinterpret_cast<uintptr_t>(b);
 
@@ -1132,6 +1144,11 @@ FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
       pfin = &fin;
     }
   }
+  // a null workspace is enough only for the one-launch form
+  if (!partial && !(pfin && sweep_applies<uint8_t>(a, b, n_images, n_per_image, bpi)))
+    return FA_E_ARG;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
 
   bool exact = false;
   int swept = 0;  // partial columns per image the sweep wrote, 0 if it did not run

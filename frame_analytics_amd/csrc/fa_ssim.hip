@@ -1016,7 +1016,9 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
                      const float* win, int K, double shift, double C1, double C2,
                      float* map_out, double* partial, int bpp, double* out_per_image,
                      double* out_total, int device, void* stream, uint64_t* acc = nullptr) {
-  if (!x || !y || !win || !partial) return FA_E_ARG;
+  // a null workspace is enough only where the matrix-core launch finishes the
+  // call (ssim_mfma refuses it otherwise, before launching)
+  if (!x || !y || !win || (!partial && !acc)) return FA_E_ARG;
   int Hout = 0, Wout = 0;
   int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
   if (rc != FA_OK) return rc;
@@ -1053,6 +1055,7 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
     if (rc != FA_OK) return rc;
     if (tiles < 0) return FA_OK;  // the launch finished the call
   }
+  if (!partial) return FA_E_ARG;  // nothing launched: the strip kernel needs the workspace
   if (tiles == 0) {
     rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, lm, a, planes, device, st)
                  : launch_ssim<MODE_REDUCE>(dtype, K, lm, a, planes, device, st);

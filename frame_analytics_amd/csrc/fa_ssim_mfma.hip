@@ -1110,6 +1110,9 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
     a.finv = std::ldexp(1.0, bits - 51);
     if (bits >= 40) a.acc = nullptr;  // (never at real sizes) too few fraction bits left
   }
+  // the forward's only launch without a workspace is the finish (the CS pass
+  // forming the cs sums alone has a null `partial` of its own)
+  if (!cs_pass && !a.acc && !c.partial) return FA_E_ARG;
   dispatch(src, mode, true, dim3(static_cast<unsigned>(wgs)), st, a);
   FA_LAUNCH_CHECK();
   *tiles = a.acc ? -1 : a.tiles;

@@ -392,6 +392,9 @@ FA_API int fa_gpu_ssim_noalloc(const void* x, const void* y, int dtype, int N,
  * batch's last image).  One launch instead of two.  Every other call ignores
  * `acc` (it may be null) and runs as fa_gpu_pixel_reduce.  `acc` is state of
  * one stream: calls that may overlap (two streams) need one buffer each.
+ * `partial` may be null for a call that takes the one-launch form (it is not
+ * read); a call with a null `partial` that cannot returns FA_E_ARG before
+ * launching anything.
  */
 #define FA_PIXEL_ACC_WORDS ((32 + 1) * 16)
 FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
@@ -418,7 +421,9 @@ FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
  * batch means likewise).  The per-image values then differ from
  * fa_gpu_gmsd's fixed-order float64 sums by the fixed-point rounding, about
  * 2^-52 relative per workgroup.  Every other call runs fa_gpu_gmsd_ex's
- * launches (plus one block for out_batch) and ignores `acc`.
+ * launches (plus one block for out_batch) and ignores `acc`.  psum / psumsq
+ * may be null for a call that finishes in its launch; one with them null that
+ * cannot returns FA_E_ARG before launching anything.
  */
 #define FA_GMSD_ACC_WORDS ((3 * 64 + 2) * 16)
 FA_API int fa_gpu_gmsd_once(const void* x, const void* y, int dtype, int N, int C, int H,
@@ -442,7 +447,8 @@ FA_API int fa_gpu_gmsd_once(const void* x, const void* y, int dtype, int N, int 
  * complete an image's sum, and the batch's, write the means.  They differ
  * from fa_gpu_ssim's fixed-order float64 sums by that rounding, ~1e-13
  * relative at 1080p.  Every other call runs as fa_gpu_ssim_ex and ignores
- * `acc`.
+ * `acc`.  `partial` may be null for a call that finishes in its launch; one
+ * with a null `partial` that cannot returns FA_E_ARG before launching anything.
  */
 #define FA_SSIM_ACC_WORDS ((256 + 1) * 16)
 FA_API int fa_gpu_ssim_once(const void* x, const void* y, int dtype, int N, int C, int H,

@@ -561,3 +561,31 @@ def test_gmsd_flat_patch_without_T_and_eps_is_nan(gpu, dt):
     m1, s1 = ref.gmsd_stats(xa, xb, 255.0, T=0.0, eps=1e-30)
     got = fa.gmsd(x, y, data_range=255.0, T=0.0, eps=1e-30, reduction="none").cpu().numpy()
     assert np.all(np.isfinite(got)) and np.all(np.abs(got - s1) <= REL * np.abs(s1)), (got, s1)
+
+
+def test_gmsd_one_launch_without_workspace(gpu):
+    """fa_gpu_gmsd_once with null psum / psumsq: the launch that finishes the
+    call does not read them (same statistics); with T = eps = 0 (no one-launch
+    form) the call returns FA_E_ARG and writes nothing."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((2, 3, 240, 320), 9.0, seed=5)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    acc = torch.zeros(backend._ACC_WORDS["gmsd"], dtype=torch.int64, device=gpu)
+    m2, s2, _ = _gmsd_call("fa_gpu_gmsd", x, y, 170.0, 6.5e-8, True)
+    bpp = backend.workspace_slots("gmsd", 240, 320, 1)
+    st = torch.cuda.current_stream().cuda_stream
+    for T, eps, ok in ((170.0, 6.5e-8, True), (0.0, 0.0, False)):
+        out = torch.full((4,), -7.0, dtype=torch.float64, device=gpu)
+        rc = backend.call_gpu("fa_gpu_gmsd_once", x.data_ptr(), y.data_ptr(), 0, 2, 3, 240, 320,
+                              None, None, None, T, eps, 1, None, None, bpp, acc.data_ptr(),
+                              out.data_ptr(), out[2:].data_ptr(), None, 0, st)
+        torch.cuda.synchronize()
+        if ok:
+            assert rc == 0
+            o = out.cpu().numpy()
+            assert np.all(np.abs(o[:2] - m2) <= 1e-12 * np.abs(m2))
+            assert np.all(np.abs(o[2:] - s2) <= 1e-10 * np.abs(s2))
+        else:
+            assert rc == 5 and bool((out == -7.0).all()), rc
+        assert not bool(acc.any())

@@ -415,3 +415,32 @@ def test_single_launch_finish_per_stream(gpu):
     assert len(keys) == 2
     for k in keys:
         assert not bool(backend._stream_acc[k].any())
+
+
+def test_single_launch_without_workspace(gpu):
+    """fa_gpu_pixel_reduce_once with a null `partial`: where the call finishes
+    in the sweep the workspace is not read and the values are the same; where
+    it cannot (a workspace shape the sweep does not take, an op without exact
+    sums) the call returns FA_E_ARG and writes nothing."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((3, 1, 2048, 2048), 6.0, seed=31)
+    x, y = _t(a, gpu), _t(b, gpu)
+    n, per = 3, 2048 * 2048
+    st = torch.cuda.current_stream().cuda_stream
+    acc = torch.zeros(backend._ACC_WORDS["pixel"], dtype=torch.int64, device=gpu)
+    bias = 10.0 * math.log10(255.0 ** 2)
+    bpi = backend.workspace_slots("pixel", n, per, 0)
+    for op, bp, ok in ((0, bpi, True), (1, bpi, True), (0, 1000, False), (2, bpi, False)):
+        out = torch.full((n,), -1.0, dtype=torch.float64, device=gpu)
+        rc = backend.call_gpu("fa_gpu_pixel_reduce_once", x.data_ptr(), y.data_ptr(), 0, n, per,
+                              op, 1e-6, bias, None, bp, acc.data_ptr(), out.data_ptr(), None,
+                              None, None, 0, st)
+        torch.cuda.synchronize()
+        if ok:
+            assert rc == 0
+            want = ref.mse(a, b, "none") if op == 0 else ref.l1(a, b, "none")
+            assert np.array_equal(out.cpu().numpy(), want)
+        else:
+            assert rc == 5 and bool((out == -1.0).all()), (op, bp, rc)
+        assert not bool(acc.any())

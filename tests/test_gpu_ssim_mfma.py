@@ -433,3 +433,37 @@ def test_one_launch_finish_matches_finalize(gpu, shape):
             assert tj == t1
     want = ref.ssim(a[:1].astype(np.float64), b[:1].astype(np.float64), 255.0)
     assert _rel(float(p1[0]), float(want)) <= REL
+
+
+def test_one_launch_finish_without_workspace(gpu):
+    """fa_gpu_ssim_once with a null `partial`: the matrix-core launch that
+    finishes the call does not read it (same means); a float32 call, which the
+    strip kernel serves, and a map call return FA_E_ARG and write nothing."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((2, 3, 200, 256), 8.0, seed=77)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    acc = torch.zeros(backend._ACC_WORDS["ssim"], dtype=torch.int64, device=gpu)
+    want_p, want_t = _ssim_abi("fa_gpu_ssim", x, y, win)
+    st = torch.cuda.current_stream().cuda_stream
+    bpp = backend.workspace_slots("ssim", 200, 256, 11)
+    for xx, yy, code, with_map, ok in ((x, y, 0, False, True), (x.float(), y.float(), 3, False, False),
+                                       (x, y, 0, True, False)):
+        out = torch.full((3,), -3.0, dtype=torch.float64, device=gpu)
+        smap = (torch.empty((2, 3, 190, 246), dtype=torch.float32, device=gpu)
+                if with_map else None)
+        rc = backend.call_gpu("fa_gpu_ssim_once", xx.data_ptr(), yy.data_ptr(), code, 2, 3, 200,
+                              256, None, None, None, win.data_ptr(), 11, 127.5,
+                              (0.01 * 255) ** 2, (0.03 * 255) ** 2,
+                              None if smap is None else smap.data_ptr(), None, bpp,
+                              acc.data_ptr(), out.data_ptr(), out[2:].data_ptr(), 0, st)
+        torch.cuda.synchronize()
+        if ok:
+            assert rc == 0
+            o = out.cpu().numpy()
+            assert np.all(np.abs(o[:2] - want_p) <= 1e-12 * np.abs(want_p))
+            assert abs(o[2] - want_t) <= 1e-12 * abs(want_t)
+        else:
+            assert rc == 5 and bool((out == -3.0).all()), (code, with_map, rc)
+        assert not bool(acc.any())
