@@ -332,15 +332,17 @@ def workspace_slots(kind: str, a: int, b: int, c: int) -> int:
 
 
 #: uint64 words of the one-launch entry points' accumulators
-#: (FA_PIXEL_ACC_WORDS, FA_GMSD_ACC_WORDS, FA_SSIM_ACC_WORDS)
-_ACC_WORDS = {"pixel": (32 + 1) * 16, "gmsd": (3 * 64 + 2) * 16, "ssim": (256 + 1) * 16}
+#: (FA_PIXEL_ACC_WORDS, FA_GMSD_ACC_WORDS, FA_SSIM_ACC_WORDS, FA_MS_SSIM_ACC_WORDS)
+_ACC_WORDS = {"pixel": (32 + 1) * 16, "gmsd": (3 * 64 + 2) * 16, "ssim": (256 + 1) * 16,
+              "ms": (8 * 256 + 1) * 16}
 #: (kind, device, raw stream) -> that stream's accumulator, zero between calls
 _stream_acc: dict = {}
 
 
 def _acc_for(kind: str, device: torch.device, dev: int, stream: int) -> Optional[torch.Tensor]:
     """The zeroed accumulator that lets a reduction finish inside its one
-    launch (``fa_gpu_pixel_reduce_once``, ``fa_gpu_gmsd_once``).  Each call
+    launch (``fa_gpu_pixel_reduce_once``, ``fa_gpu_gmsd_once``,
+    ``fa_gpu_ssim_once``, ``fa_gpu_ms_ssim``).  Each call
     leaves it zero again, so one buffer serves every call on its stream, in
     stream order; calls on another stream get their own.  Under graph capture
     there is none (the call takes its two-launch form): a graph's replays
@@ -922,7 +924,9 @@ def ms_ssim_fused(x, y, win, shift, C1, C2, weights, luma=None, per_image=False)
     """Inference MS-SSIM in one C-ABI call (``fa_gpu_ms_ssim``): every scale's
     fused pass and the reduction, launched back to back from the library, over
     one workspace allocation; per-image values (``per_image``) or their
-    batch mean."""
+    batch mean.  With the stream's accumulator (none under graph capture) a
+    uint8 call whose scales all fit the matrix-core kernel runs in three
+    launches, the reduction finished in the last."""
     win = _win32(win)
     n, c, h, w = (int(v) for v in x.shape)
     k = int(win.numel())
@@ -935,9 +939,12 @@ def ms_ssim_fused(x, y, win, shift, C1, C2, weights, luma=None, per_image=False)
     out = _f64(x.device, n) if per_image else _f64(x.device)
     wts = (ctypes.c_double * m)(*[float(v) for v in weights])
     dev, stream = _site(x)
+    acc = _acc_for("ms", x.device, dev, stream) if x.dtype == torch.uint8 and luma is None \
+        else None
     _run("fa_gpu_ms_ssim", _ptr(x), _ptr(y), code, n, c, h, w, xs, ys, _luma_arg(luma),
          _ptr(win), k, float(shift), float(C1), float(C2), wts, m, _ptr(ws), nbytes,
-         _ptr(out) if per_image else None, None if per_image else _ptr(out), dev, stream)
+         _ptr(acc) if acc is not None else None, _ptr(out) if per_image else None,
+         None if per_image else _ptr(out), dev, stream)
     return out
 
 

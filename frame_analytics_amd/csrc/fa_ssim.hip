@@ -1404,8 +1404,8 @@ FA_API int fa_gpu_ms_ssim(const void* x, const void* y, int dtype, int N, int C,
                           const int64_t* x_strides, const int64_t* y_strides,
                           const double* luma, const float* win, int K, double shift,
                           double C1, double C2, const double* weights, int M, void* workspace,
-                          int64_t workspace_bytes, double* out_per_image, double* out_total,
-                          int device, void* stream) {
+                          int64_t workspace_bytes, uint64_t* acc, double* out_per_image,
+                          double* out_total, int device, void* stream) {
   if (!x || !y || !win || !weights || !workspace) return FA_E_ARG;
   if (!out_per_image && !out_total) return FA_E_ARG;
   if (luma && C != 3) return FA_E_SHAPE;
@@ -1414,6 +1414,44 @@ FA_API int fa_gpu_ms_ssim(const void* x, const void* y, int dtype, int N, int C,
   if (rc != FA_OK) return rc;
   if (workspace_bytes < p.total) return FA_E_ARG;
   char* ws = static_cast<char*>(workspace);
+  if (acc && dtype == FA_U8 && !luma) {
+    // three launches, the reduction finished in the last (ssim_mfma_ms)
+    SsimArgs v = {};
+    rc = set_views(v, C, H, W, x_strides, y_strides, nullptr);
+    if (rc != FA_OK) return rc;
+    SsimMfmaMs mc = {};
+    mc.x = x;
+    mc.y = y;
+    mc.xsn = v.xsn;
+    mc.xsc = v.xsc;
+    mc.ysn = v.ysn;
+    mc.ysc = v.ysc;
+    mc.xsh = v.xsh;
+    mc.ysh = v.ysh;
+    mc.N = N;
+    mc.C = C;
+    mc.H = H;
+    mc.W = W;
+    mc.K = K;
+    mc.M = M;
+    mc.win = win;
+    mc.C1 = C1;
+    mc.C2 = C2;
+    mc.weights = weights;
+    for (int i = 1; i < M; ++i) {
+      mc.lx[i] = ws + p.level_x[i];
+      mc.ly[i] = ws + p.level_y[i];
+    }
+    mc.words = acc;
+    mc.out_per_image = out_per_image;
+    mc.out_total = out_total;
+    bool done = false;
+    {
+      FA_DEVICE_SCOPE(device);
+      rc = ssim_mfma_ms(mc, device, static_cast<hipStream_t>(stream), &done);
+    }
+    if (rc != FA_OK || done) return rc;
+  }
   const double* parts[MS_MAX_SCALES];
   int slots[MS_MAX_SCALES];
   double npix[MS_MAX_SCALES];

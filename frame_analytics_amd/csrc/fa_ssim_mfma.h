@@ -51,4 +51,30 @@ struct SsimMfmaCall {
 // the call itself (no finalize needed) sets *tiles = -1.
 int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles);
 
+// Inference MS-SSIM over uint8 planes without luma, M (3 .. 5) scales, in
+// three launches: scale 0 (writing the float16 level 1), scale 1 (writing the
+// float32 levels 2, 3 and 4), and scales 2 .. M - 1 side by side in one
+// launch whose last workgroup also finishes the reduction from the
+// per-(scale, plane) fixed-point sums every launch adds to `words`.
+struct SsimMfmaMs {
+  const void* x;
+  const void* y;
+  int64_t xsn, xsc, ysn, ysc;  // image and channel strides of the input (elements)
+  int xsh, ysh;                // row strides
+  int N, C, H, W, K, M;
+  const float* win;            // the 1-D window, K floats on the device
+  double C1, C2;
+  const double* weights;       // host, M exponents
+  void* lx[8];                 // level i >= 1 of x and y: floor(H / 2^i) x
+  void* ly[8];                 //   floor(W / 2^i) per plane, float16 (i = 1), float32
+  uint64_t* words;             // FA_MS_SSIM_ACC_WORDS, zero; left zero
+  double* out_per_image;
+  double* out_total;
+};
+
+// Launches it when every scale fits (ssim_mfma's layout rules at each scale,
+// N * C <= 256, C1 and C2 positive) and sets *done; otherwise launches nothing
+// and leaves *done false, for the per-scale path.
+int ssim_mfma_ms(const SsimMfmaMs& c, int device, hipStream_t st, bool* done);
+
 }  // namespace fa

@@ -96,7 +96,10 @@ struct MfArgs {
   void* px;             // MF_CS, MF_CSO: optional pyramid level (2 x 2 means),
   void* py;             //   float32, or float16 (level_f16, uint8 input)
   int level_f16;
-  // the one-launch finish (ssim_mfma_kernel<..., FIN>)
+  void* dpx[2];         // LVL_F32D: the two levels below px / py (float32, either
+  void* dpy[2];         //   pair may be null)
+  // the one-launch finish (ssim_mfma_kernel<..., FIN_SSIM>); FIN_MS uses acc
+  // (this scale's words) and fscale
   uint64_t* acc;
   double fscale, finv, npix_img, npix_all;
   double *out_per_image, *out_total;
@@ -145,6 +148,16 @@ __device__ inline void mf_finish(const MfArgs& a, int img, int wg_per_image, dou
   __hip_atomic_store(wb, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int64_t all = (static_cast<int64_t>(ob) >> MF_COUNT_BITS) + tot;
   *a.out_total = static_cast<double>(all) * a.finv / a.npix_all;
+}
+
+// MS-SSIM's words: one per (scale, plane), each workgroup adding its sum of
+// the plane's cs (or, at the coarsest scale, SSIM) values packed as mf_finish
+// packs them, round(sum * 2^F) << MF_COUNT_BITS plus a count of 1, with
+// F = 51 - bits(2 * output pixels of the plane at that scale).
+__device__ inline uint64_t ms_add(uint64_t* w, double s, double fscale) {
+  const int64_t f = __double2ll_rn(s * fscale);
+  return __hip_atomic_fetch_add(w, (static_cast<uint64_t>(f) << MF_COUNT_BITS) + 1u,
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ inline f4 mfma(h8 a, h8 b, f4 c) {
@@ -536,7 +549,25 @@ struct Pool {
   uint32_t lo;     // this lane's byte offset in a block's level rows (row 2g,
                    // its column), or out of every buffer's range when it stores nothing
   h8 pm;           // the column-pair matrix fragment
+  // LVL_F32D: the two levels below, as bx / by .. lo above (a block's 16 input
+  // rows hold 4 rows of the first and 2 of the second)
+  char *dx[2], *dy[2];
+  int drows[2];
+  uint32_t dstep[2], dlo[2];
 };
+
+// Lane exchanges of the deep levels' sums: v_mov_b32 with DPP quad_perm
+// [1,0,3,2] / [2,3,0,1] (lanes n ^ 1, n ^ 2 in a row of 16) and a
+// ds_swizzle in bit-mask mode with xor mask 16 (lane l ^ 16 in each half).
+__device__ inline float lane_xor1(float v) {
+  return bc<float>(__builtin_amdgcn_mov_dpp(bc<int>(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ inline float lane_xor2(float v) {
+  return bc<float>(__builtin_amdgcn_mov_dpp(bc<int>(v), 0x4E, 0xF, 0xF, false));
+}
+__device__ inline float lane_xor16(float v) {
+  return bc<float>(__builtin_amdgcn_ds_swizzle(bc<int>(v), 0x401F));
+}
 
 // The 2 x 2 means of one block's level rows 2g and 2g + 1 (this lane's
 // column), x and y: float32, or (HALF) float16 packed in pairs, which keeps
@@ -609,6 +640,31 @@ __device__ inline void pool_store(const Pool& pl, int j, const PoolOut<HALF>& po
   }
 }
 
+// LVL_F32D: the two levels below a float32 level from the same block's
+// means.  Lane (g, n) holds the level's rows 2g, 2g + 1 in column n; the sum
+// of both rows over lanes n, n ^ 1 is 4 means of the next level down (its row
+// g, column n / 2), and over the quad of lanes and g, g ^ 1 it is 16 means of
+// the one below (row g / 2, column n / 4).  Every sum is exact: multiples of
+// 1/16 below 2^12.  Stored like pool_store: four stores in every block.
+__device__ inline void pool_store_deep(const Pool& pl, int j, const PoolOut<false>& po) {
+  const float tx = po.mx[0] + po.mx[1], ty = po.my[0] + po.my[1];
+  const float px = tx + lane_xor1(tx), py = ty + lane_xor1(ty);
+  const float qx = px + lane_xor2(px), qy = py + lane_xor2(py);
+  const float rx = qx + lane_xor16(qx), ry = qy + lane_xor16(qy);
+  const float vx[2] = {px * 0.25f, rx * 0.0625f};
+  const float vy[2] = {py * 0.25f, ry * 0.0625f};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const int row = (MT / 4 >> d) * j;  // the block's first row of that level, in this chunk
+    const uint32_t boff = static_cast<uint32_t>(row) * pl.dstep[d];
+    const int range = max(pl.drows[d] - row, 0) * static_cast<int>(pl.dstep[d]);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc(pl.dx[d] + boff, 0, range, MF_RSRC_WORD3);
+    const auto ry = __builtin_amdgcn_make_buffer_rsrc(pl.dy[d] + boff, 0, range, MF_RSRC_WORD3);
+    __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(vx[d]), rx, static_cast<int>(pl.dlo[d]), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(vy[d]), ry, static_cast<int>(pl.dlo[d]), 0, 0);
+  }
+}
+
 // FOLD: the x'y' sums start at c2s (ssim_px_folded).
 template <int PAR, bool FOLD>
 __device__ inline void vblock(const Weights& w, const VState& v, f4* o, float c2s) {
@@ -634,26 +690,23 @@ __device__ inline void vblock(const Weights& w, const VState& v, f4* o, float c2
 
 // What a CS pass writes besides its sums: no level, the next pyramid level in
 // float32, or in float16 (uint8 input only).
-enum { LVL_NONE = 0, LVL_F32 = 1, LVL_F16 = 2 };
+// LVL_F32D: the float32 level and the two below it (the float16 level's
+// pass of a uint8 pyramid, so that the coarser scales can run side by side).
+enum { LVL_NONE = 0, LVL_F32 = 1, LVL_F16 = 2, LVL_F32D = 3 };
 
-// uint8 and float16 levels: 4 waves per SIMD (128 VGPRs) fit without spills
-// and beat 3; the uint8 cs-only pass writing a float32 level (which MS-SSIM
-// does not use: its first level is float16) needs more and runs 3.  LVL (CS
-// modes): the pyramid level the pass writes.
-template <int SRC, int MODE, int LVL, bool FIN = false>
-__global__ __launch_bounds__(BLOCK)
-__attribute__((amdgpu_waves_per_eu(SRC == SRC_F32 ? 1
-                                   : (SRC == SRC_U8 && MODE == MF_CSO && LVL == LVL_F32) ? 3
-                                                                                       : 4)))
-void ssim_mfma_kernel(MfArgs a) {
+// One workgroup's tile t of a launch over the planes of `a`: its 16-row
+// blocks, walked down its chunk of its column strip by the four waves, each
+// lane's sums added to acc (and acc_cs, MF_CS).  The tile's plane and its
+// index within the plane come back for the caller's reduction.
+template <int SRC, int MODE, int LVL>
+__device__ __attribute__((always_inline)) inline void mf_walk(
+    const MfArgs& a, int t, float (&swin)[WAVES_PER_BLOCK][WIN_LEN], double& acc,
+    double& acc_cs, int& plane_out, int& tile_out) {
   constexpr bool PYR = SRC == SRC_F32;  // float32 samples: hi + lo operands
   constexpr bool LEVEL = LVL != LVL_NONE;
   static_assert(!LEVEL || MODE == MF_CS || MODE == MF_CSO, "levels come from the CS pass");
-  static_assert(!FIN || (MODE == MF_REDUCE && SRC == SRC_U8), "the finish: uint8 forward sums");
   static_assert(LVL != LVL_F16 || SRC == SRC_U8, "float16 levels below uint8 input only");
-  __shared__ double sred[2 * WAVES_PER_BLOCK];
-  __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
-  const int t = static_cast<int>(xcd_tile(blockIdx.x, gridDim.x));
+  static_assert(LVL != LVL_F32D || SRC == SRC_F16, "deep levels: the float16 level's pass");
   int plane, chunk, strip;
   if (a.xcd_planes > 0) {
     const int per = a.xcd_planes * a.tiles;  // the tiles of one XCD (xcd_tile)
@@ -681,8 +734,9 @@ void ssim_mfma_kernel(MfArgs a) {
   const int r0 = chunk < a.nbig ? chunk * a.TH : a.nbig * a.TH + (chunk - a.nbig) * a.THs;
   const int r_lim = r0 + (chunk < a.nbig ? a.TH : a.THs);  // the chunk's end row
   const int r_end = min(r_lim, a.Hout);
+  plane_out = plane;
+  tile_out = tile;
 
-  double acc = 0.0, acc_cs = 0.0;
   if (c0 < a.Wout) {  // uniform per wave
     const int img = plane / a.C;
     const int ch = plane - img * a.C;
@@ -729,9 +783,33 @@ void ssim_mfma_kernel(MfArgs a) {
         pl.rows = row_end / 2 - r0 / 2;
         pl.rstep = static_cast<uint32_t>(Wd * eb);
         const bool last_wave = c0 + MT >= a.Wout;
-        const bool lane_on = ((wave & 1) == 0 || last_wave) && c0 / 2 + n < Wd;
+        const bool wave_on = (wave & 1) == 0 || last_wave;
+        const bool lane_on = wave_on && c0 / 2 + n < Wd;
         // 0x80000000 lies past every range (a plane's level is below 2^31 bytes)
         pl.lo = lane_on ? static_cast<uint32_t>((2 * g * Wd + c0 / 2 + n) * eb) : 0x80000000u;
+        if constexpr (LVL == LVL_F32D) {
+          // level d + 2 below the input (d = 0, 1): W / 2^(d+2) columns (W % 8
+          // == 0), floor(H / 2^(d+2)) rows; this chunk's rows r0 / 2^(d+2) ..;
+          // lane (g, n) stores row g >> d, column (c0 / 2 + n) >> (d + 1)
+          // when n (and, d = 1, g) is the first of its group
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const int sh = d + 2;
+            const int Wl = a.W >> sh;
+            const int end = r_lim >= a.Hout ? (a.H >> sh) : (r_lim >> sh);
+            const bool have = a.dpx[d] != nullptr;
+            const int64_t at = (static_cast<int64_t>(plane) * (a.H >> sh) + (r0 >> sh)) * Wl * 4;
+            pl.dx[d] = static_cast<char*>(have ? a.dpx[d] : a.px) + (have ? at : 0);
+            pl.dy[d] = static_cast<char*>(have ? a.dpy[d] : a.py) + (have ? at : 0);
+            pl.drows[d] = have ? end - (r0 >> sh) : 0;
+            pl.dstep[d] = static_cast<uint32_t>(Wl * 4);
+            const int col = (c0 / 2 + n) >> (d + 1);
+            const bool first = (n & ((2 << d) - 1)) == 0 && (d == 0 || (g & 1) == 0);
+            pl.dlo[d] = wave_on && first && col < Wl
+                            ? static_cast<uint32_t>(((g >> d) * Wl + col) * 4)
+                            : 0x80000000u;
+          }
+        }
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -818,6 +896,7 @@ void ssim_mfma_kernel(MfArgs a) {
     };
     auto level_store = [&](int j) {
       if constexpr (LATE) pool_store<HALF>(pl, j, po);
+      if constexpr (LVL == LVL_F32D) pool_store_deep(pl, j, po);
     };
     auto epilogue = [&](int b, const f4* o) {
       const int row0 = r0 + MT * b + 4 * g;
@@ -896,6 +975,35 @@ void ssim_mfma_kernel(MfArgs a) {
       step(b + 1, P0{});
     }
   }
+}
+
+// What a launch does with its workgroups' sums: store them as partial slots
+// (FIN_NONE), finish the uint8 forward's means (FIN_SSIM, mf_finish), or add
+// them to MS-SSIM's per-(scale, plane) words (FIN_MS, ms_add).
+enum { FIN_NONE = 0, FIN_SSIM = 1, FIN_MS = 2 };
+
+// uint8 and float16 levels: 4 waves per SIMD (128 VGPRs) fit without spills
+// and beat 3; the uint8 cs-only pass writing a float32 level (which MS-SSIM
+// does not use: its first level is float16) needs more and runs 3, and so
+// does the float16 level's pass writing three levels (which spills at 128;
+// at 1080p its 720 workgroups fit 3 per CU anyway).  LVL (CS modes): the
+// pyramid level the pass writes.
+template <int SRC, int MODE, int LVL, int FIN = FIN_NONE>
+__global__ __launch_bounds__(BLOCK)
+__attribute__((amdgpu_waves_per_eu(
+    SRC == SRC_F32 ? 1
+    : ((SRC == SRC_U8 && MODE == MF_CSO && LVL == LVL_F32) || LVL == LVL_F32D) ? 3
+                                                                             : 4)))
+void ssim_mfma_kernel(MfArgs a) {
+  static_assert(FIN != FIN_SSIM || (MODE == MF_REDUCE && SRC == SRC_U8),
+                "the finish: uint8 forward sums");
+  static_assert(FIN != FIN_MS || MODE == MF_CSO, "MS-SSIM's words: the cs sums of a scale");
+  __shared__ double sred[2 * WAVES_PER_BLOCK];
+  __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
+  double acc = 0.0, acc_cs = 0.0;
+  int plane = 0, tile = 0;
+  mf_walk<SRC, MODE, LVL>(a, static_cast<int>(xcd_tile(blockIdx.x, gridDim.x)), swin, acc,
+                          acc_cs, plane, tile);
   // packed: each image owns C * tiles consecutive slots, as the finalize reads them
   const int64_t slot = static_cast<int64_t>(plane) * a.tiles + tile;
   if constexpr (MODE == MF_CS) {
@@ -907,12 +1015,122 @@ void ssim_mfma_kernel(MfArgs a) {
     }
   } else {
     const double s = block_sum(acc, sred);
-    if constexpr (FIN) {
+    if constexpr (FIN == FIN_SSIM) {
       if (threadIdx.x == 0) mf_finish(a, plane / a.C, a.C * a.tiles, s);
+    } else if constexpr (FIN == FIN_MS) {
+      if (threadIdx.x == 0) ms_add(a.acc + static_cast<int64_t>(plane) * MF_STRIDE, s, a.fscale);
     } else if (threadIdx.x == 0) {
       (MODE == MF_CSO ? a.partial_cs : a.partial)[slot] = s;
     }
   }
+}
+
+// MS-SSIM's coarse scales (2 .. M - 1 of a uint8 pyramid, float32 levels) in
+// one launch, and the reduction of every scale after them.  The scales'
+// workgroups follow each other in the grid (coarser last, so their short
+// tiles fill the end of the launch); each adds its cs sum (the coarsest
+// scale: its SSIM sum) to its (scale, plane) word with a returning atomic.
+// The workgroup whose add completes a word's count (the scale's tiles per
+// plane) adds 1 to the launch's counter; the one that completes the counter
+// holds the only view in which every word is whole -- the scales before this
+// launch added theirs in earlier launches on the stream -- and turns them into
+// the result: each plane's means, clamped at zero and raised to the scale's
+// weight, multiplied over the scales (reference functional.py:897-901), the
+// channel mean of each image and the mean over the batch, as ms_term_kernel and
+// ms_finish_kernel do from partial sums.  It reads the words with atomic
+// exchanges of zero and resets the counter, so the accumulator is zero again
+// for the next call.  A returning atomic has been performed where every agent
+// sees it once its value is back, so a count that completes has every add of
+// that word behind it.
+constexpr int MS_TAIL_MAX = 3;         // scales 2 .. 4 of a five-scale pyramid
+constexpr int MS_WORD_SCALES = 8;
+constexpr int MS_FIN_MAX_PLANES = 256;
+static_assert(FA_MS_SSIM_ACC_WORDS == (MS_WORD_SCALES * MS_FIN_MAX_PLANES + 1) * MF_STRIDE,
+              "the ABI's accumulator size");
+
+struct MfTail {
+  MfArgs s[MS_TAIL_MAX];
+  int n, first;                 // scales first .. first + n - 1 in this launch
+  int wg_end[MS_TAIL_MAX];      // end of each scale's workgroups in the grid
+  int M, N, C, planes;
+  uint64_t* words;              // word (m, plane) at (m * planes + plane) * MF_STRIDE,
+                                // the launch's counter after M * planes of them
+  double finv[MS_WORD_SCALES];  // 2^-F of every scale's words
+  double npix[MS_WORD_SCALES];  // output pixels of a plane at each scale
+  double w[MS_WORD_SCALES];     // the scales' exponents
+  double *out_per_image, *out_total;
+};
+
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(1)))
+void ssim_mfma_tail_kernel(MfTail m) {
+  __shared__ double sred[2 * WAVES_PER_BLOCK];
+  __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
+  __shared__ double sterm[(2 + MS_TAIL_MAX) * MS_FIN_MAX_PLANES];
+  __shared__ int sfin;
+  const int b = static_cast<int>(blockIdx.x);
+  int k = 0;
+  while (k + 1 < m.n && b >= m.wg_end[k]) ++k;
+  k = __builtin_amdgcn_readfirstlane(k);
+  const MfArgs& a = m.s[k];
+  double acc = 0.0, acc_cs = 0.0;
+  int plane = 0, tile = 0;
+  // the coarsest scale's SSIM values, the cs values of the others, with the
+  // per-pixel arithmetic of the per-scale passes (MF_CS there, MF_CSO's folded
+  // form here); either way the sum the word takes ends up in acc
+  const int t = b - (k > 0 ? m.wg_end[k - 1] : 0);
+  if (k == m.n - 1)
+    mf_walk<SRC_F32, MF_CS, LVL_NONE>(a, t, swin, acc, acc_cs, plane, tile);
+  else
+    mf_walk<SRC_F32, MF_CSO, LVL_NONE>(a, t, swin, acc, acc_cs, plane, tile);
+  const double s = block_sum(acc, sred);
+  const int64_t planes = m.planes;
+  if (threadIdx.x == 0) {
+    constexpr uint64_t CM = (uint64_t(1) << MF_COUNT_BITS) - 1;
+    const int64_t sc = m.first + k;
+    const uint64_t old = ms_add(m.words + (sc * planes + plane) * MF_STRIDE, s, a.fscale);
+    int fin = 0;
+    if ((old & CM) + 1u == static_cast<uint64_t>(a.tiles)) {
+      uint64_t* cnt = m.words + static_cast<int64_t>(m.M) * planes * MF_STRIDE;
+      const uint64_t c = __hip_atomic_fetch_add(cnt, uint64_t(1), __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      if (c + 1u == static_cast<uint64_t>(m.n) * planes) {
+        __hip_atomic_store(cnt, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fin = 1;
+      }
+    }
+    sfin = fin;
+  }
+  __syncthreads();
+  if (!sfin) return;
+  // one word per thread (every exchange of the workgroup in flight at once):
+  // word i is scale i / planes, plane i % planes; its term into sterm[i]
+  const int64_t words = static_cast<int64_t>(m.M) * planes;
+  for (int64_t i = threadIdx.x; i < words; i += BLOCK) {
+    const int sc = static_cast<int>(i / planes);
+    const uint64_t v = __hip_atomic_exchange(m.words + i * MF_STRIDE, uint64_t(0),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const double mean =
+        static_cast<double>(static_cast<int64_t>(v) >> MF_COUNT_BITS) * m.finv[sc] / m.npix[sc];
+    sterm[i] = pow(mean > 0.0 ? mean : 0.0, m.w[sc]);
+  }
+  __syncthreads();
+  // each plane's product over the scales, in scale order, into sterm[plane]
+  for (int64_t p = threadIdx.x; p < planes; p += BLOCK) {
+    double prod = 1.0;
+    for (int sc = 0; sc < m.M; ++sc) prod *= sterm[sc * planes + p];
+    sterm[p] = prod;
+  }
+  __syncthreads();
+  double tot = 0.0;
+  for (int n = threadIdx.x; n < m.N; n += BLOCK) {
+    double img = 0.0;
+    for (int c = 0; c < m.C; ++c) img += sterm[n * m.C + c];
+    img /= static_cast<double>(m.C);
+    if (m.out_per_image) m.out_per_image[n] = img;
+    tot += img;
+  }
+  tot = block_sum(tot, sred);
+  if (threadIdx.x == 0 && m.out_total) *m.out_total = tot / static_cast<double>(m.N);
 }
 
 // FA_SSIM_MFMA=0 in the environment selects the vector-ALU kernel instead.
@@ -921,7 +1139,7 @@ bool mfma_enabled() {
   return !(e && e[0] == '0');
 }
 
-template <int SRC, int MODE, int LVL, bool FIN = false>
+template <int SRC, int MODE, int LVL, int FIN = FIN_NONE>
 int occupancy() {
   static int occ = 0;
   if (occ <= 0) {
@@ -942,8 +1160,9 @@ template <int SRC, int MODE, int LVL>
 int run(bool launch, dim3 grid, hipStream_t st, const MfArgs& a) {
   if constexpr (SRC == SRC_U8 && MODE == MF_REDUCE) {
     if (a.acc) {
-      if (!launch) return occupancy<SRC, MODE, LVL, true>();
-      hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MODE, LVL, true>), grid, dim3(BLOCK), 0, st, a);
+      if (!launch) return occupancy<SRC, MODE, LVL, FIN_SSIM>();
+      hipLaunchKernelGGL((ssim_mfma_kernel<SRC, MODE, LVL, FIN_SSIM>), grid, dim3(BLOCK), 0, st,
+                         a);
       return 0;
     }
   }
@@ -981,38 +1200,31 @@ int dispatch(int src, int mode, bool launch, dim3 grid, hipStream_t st, const Mf
 
 }  // namespace
 
-int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
-  *tiles = 0;
-  if (!mfma_enabled() || c.K > MF_MAX_K || c.W % 8 != 0 || c.W < 8) return FA_OK;
-  const int src = c.src == SsimMfmaCall::F32_LEVEL   ? SRC_F32
-                  : c.src == SsimMfmaCall::F16_LEVEL ? SRC_F16
-                                                     : SRC_U8;
-  // the CS pass, with (MF_CS) or without (MF_CSO, partial null) the SSIM sums
-  const int mode = c.partial_cs ? (c.partial ? MF_CS : MF_CSO) : c.map ? MF_MAP : MF_REDUCE;
-  const bool cs_pass = mode == MF_CS || mode == MF_CSO;
-  if (src != SRC_U8 && !cs_pass) return FA_OK;
-  if (c.level_f16 && (src != SRC_U8 || !cs_pass)) return FA_OK;
-  // 16-byte loads (float32 and float16 levels) or 8-byte loads (uint8)
+namespace {
+
+// The layout checks every matrix-core launch shares: rows and planes aligned
+// to 8 samples, 8-byte (uint8) or 16-byte (levels) aligned bases, 16-byte
+// aligned pyramid outputs, K <= 16, and the 32-bit offsets within a plane.
+bool mfma_fits(const SsimMfmaCall& c, int src, int mode) {
+  if (c.K > MF_MAX_K || c.W % 8 != 0 || c.W < 8) return false;
   const uintptr_t base_align = src == SRC_U8 ? 7 : 15;
   if ((reinterpret_cast<uintptr_t>(c.x) | reinterpret_cast<uintptr_t>(c.y)) & base_align)
-    return FA_OK;
-  // float4 stores into the pyramid level (W % 8 == 0 makes every row of it
-  // a multiple of 16 bytes)
+    return false;
   if (c.px && ((reinterpret_cast<uintptr_t>(c.px) | reinterpret_cast<uintptr_t>(c.py)) & 15))
-    return FA_OK;
+    return false;
   const int64_t s[6] = {c.xsn, c.xsc, c.ysn, c.ysc, c.xsh, c.ysh};
   for (int64_t v : s)
-    if (v % 8 != 0) return FA_OK;
-  // 32-bit offsets within a plane: the buffer loads run up to 47 rows past
-  // the last output row (their range check stops them at the plane's end)
-  // the finish takes the uint8 forward's sums with a wanted output
-  const bool fin = c.acc && src == SRC_U8 && mode == MF_REDUCE && c.N <= MF_FIN_MAX_IMAGES &&
-                   (c.out_per_image || c.out_total);
+    if (v % 8 != 0) return false;
+  // the buffer loads run up to 47 rows past the last output row (their range
+  // check stops them at the plane's end)
   const int64_t eb = src == SRC_F32 ? 4 : src == SRC_F16 ? 2 : 1;
-  if ((static_cast<int64_t>(c.H) + 48) * std::max(c.xsh, c.ysh) * eb > INT32_MAX) return FA_OK;
+  if ((static_cast<int64_t>(c.H) + 48) * std::max(c.xsh, c.ysh) * eb > INT32_MAX) return false;
   // the map is written through buffer resources with 32-bit offsets in a plane
-  if (mode == MF_MAP && static_cast<int64_t>(c.Hout) * c.Wout * 4 > INT32_MAX) return FA_OK;
+  if (mode == MF_MAP && static_cast<int64_t>(c.Hout) * c.Wout * 4 > INT32_MAX) return false;
+  return true;
+}
 
+MfArgs args_of(const SsimMfmaCall& c) {
   MfArgs a = {};
   a.x = c.x;
   a.y = c.y;
@@ -1038,20 +1250,32 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   a.px = c.px;
   a.py = c.py;
   a.level_f16 = c.level_f16 ? 1 : 0;
+  return a;
+}
 
-  // Rows per chunk (a multiple of 16): the fewest rounds of resident
-  // workgroups times the work of one, charging the extra 16-row block of
-  // horizontal work each chunk starts with at 10 rows.
-  const int occ = dispatch(src, mode, false, dim3(1), st, a);
-  const int64_t resident = static_cast<int64_t>(cu_count(device)) * occ;
-  const int64_t planes = static_cast<int64_t>(c.N) * c.C;
-  const int strips = (c.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
-  const int blocks = (c.Hout + MT - 1) / MT;
+// Rows per chunk (a multiple of 16): the fewest rounds of resident
+// workgroups times the work of one, charging the extra 16-row block of
+// horizontal work each chunk starts with at 10 rows, with at most max_tiles
+// tiles per plane.  False when nothing fits.
+//
+// big_small: big chunks first, small ones last.  Workgroups start in tile
+// order on each XCD, so the drain at the end of the launch -- the last
+// workgroups running on emptying SIMDs -- lasts one small chunk instead of one
+// of the uniform size.  Keeping the chunk count, the first half of a column's
+// chunks get weight 1 and the rest 0.4 (on configs[1] 17,17,17,16 blocks
+// become 24,24,10,9: 82.1 against 84.3 us per call over rotated input pairs,
+// the same work and workgroup count).  It needs each XCD's range of tiles to
+// hold whole planes (the count of planes a multiple of 8); walked plane by
+// plane instead it measured slower.
+bool plan_tiles(MfArgs& a, int64_t planes, int64_t resident, int64_t max_tiles,
+                bool big_small) {
+  const int strips = (a.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
+  const int blocks = (a.Hout + MT - 1) / MT;
   int best_th = 0, best_chunks = 0;
   int64_t best_cost = INT64_MAX;
   for (int m = blocks; m >= 1; --m) {
     const int chunks = (blocks + m - 1) / m;
-    if (static_cast<int64_t>(strips) * chunks > c.bpp) break;  // fewer rows: more slots
+    if (static_cast<int64_t>(strips) * chunks > max_tiles) break;  // fewer rows: more tiles
     const int64_t wgs = planes * strips * chunks;
     const int64_t cost = ((wgs + resident - 1) / resident) * (MT * m + 10);
     if (cost < best_cost) {
@@ -1060,30 +1284,21 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
       best_chunks = chunks;
     }
   }
-  if (best_th == 0) return FA_OK;
+  if (best_th == 0) return false;
   a.TH = best_th;
   a.strips = strips;
   a.tiles = strips * best_chunks;
   a.nbig = best_chunks;
   a.THs = best_th;
   a.xcd_planes = 0;
-  // Big chunks first, small ones last: workgroups start in tile order on each
-  // XCD, so the drain at the end of the launch -- the last workgroups running
-  // on emptying SIMDs -- lasts one small chunk instead of one of the uniform
-  // size.  Keeping the chunk count, the first half of a column's chunks get
-  // weight 1 and the rest 0.4 (on configs[1] 17,17,17,16 blocks become
-  // 24,24,10,9: 82.1 against 84.3 us per call over rotated input pairs, the
-  // same work and workgroup count).
-  // It needs each XCD's range of tiles to hold whole planes (the count of
-  // planes a multiple of 8); walked plane by plane instead it measured slower.
-  if (best_chunks >= 2 && planes % NUM_XCD == 0) {
+  if (big_small && best_chunks >= 2 && planes % NUM_XCD == 0) {
     const int nb = (best_chunks + 1) / 2;
     const int ns = best_chunks - nb;
     const int big = static_cast<int>(std::lround(blocks / (nb + 0.4 * ns)));
     if (big * nb < blocks) {
       const int small = (blocks - big * nb + ns - 1) / ns;
       const int chunks = nb + (blocks - big * nb + small - 1) / small;
-      if (small >= 1 && small < big && static_cast<int64_t>(strips) * chunks <= c.bpp) {
+      if (small >= 1 && small < big && static_cast<int64_t>(strips) * chunks <= max_tiles) {
         a.TH = MT * big;
         a.nbig = nb;
         a.THs = MT * small;
@@ -1092,8 +1307,51 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
       }
     }
   }
+  return planes * a.tiles <= INT32_MAX;
+}
+
+// 2^F and 2^-F of a fixed-point sum of values in [-1, 1] over npix pixels:
+// F = 51 - bits(2 npix) keeps the packed sum within its word.
+void fixed_scale(double npix, double* fscale, double* finv) {
+  int bits = 1;
+  while (bits < 50 && std::ldexp(1.0, bits) <= 2.0 * npix) ++bits;
+  *fscale = std::ldexp(1.0, 51 - bits);
+  *finv = std::ldexp(1.0, bits - 51);
+}
+
+template <class K>
+int occupancy_of(K kernel) {
+  int v = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, reinterpret_cast<const void*>(kernel),
+                                                   BLOCK, 0) != hipSuccess ||
+      v <= 0)
+    v = 1;
+  return v;
+}
+
+}  // namespace
+
+int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
+  *tiles = 0;
+  if (!mfma_enabled()) return FA_OK;
+  const int src = c.src == SsimMfmaCall::F32_LEVEL   ? SRC_F32
+                  : c.src == SsimMfmaCall::F16_LEVEL ? SRC_F16
+                                                     : SRC_U8;
+  // the CS pass, with (MF_CS) or without (MF_CSO, partial null) the SSIM sums
+  const int mode = c.partial_cs ? (c.partial ? MF_CS : MF_CSO) : c.map ? MF_MAP : MF_REDUCE;
+  const bool cs_pass = mode == MF_CS || mode == MF_CSO;
+  if (src != SRC_U8 && !cs_pass) return FA_OK;
+  if (c.level_f16 && (src != SRC_U8 || !cs_pass)) return FA_OK;
+  if (!mfma_fits(c, src, mode)) return FA_OK;
+  // the finish takes the uint8 forward's sums with a wanted output
+  const bool fin = c.acc && src == SRC_U8 && mode == MF_REDUCE && c.N <= MF_FIN_MAX_IMAGES &&
+                   (c.out_per_image || c.out_total);
+  MfArgs a = args_of(c);
+  const int occ = dispatch(src, mode, false, dim3(1), st, a);
+  const int64_t planes = static_cast<int64_t>(c.N) * c.C;
+  if (!plan_tiles(a, planes, static_cast<int64_t>(cu_count(device)) * occ, c.bpp, true))
+    return FA_OK;
   const int64_t wgs = planes * a.tiles;
-  if (wgs > INT32_MAX) return FA_OK;
   // the one-launch finish, where its counts fit: C * tiles workgroups per
   // image and N images below 2^MF_COUNT_BITS (the tile plan above is the same
   // either way: the finish's kernel has the same occupancy)
@@ -1116,6 +1374,149 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   dispatch(src, mode, true, dim3(static_cast<unsigned>(wgs)), st, a);
   FA_LAUNCH_CHECK();
   *tiles = a.acc ? -1 : a.tiles;
+  return FA_OK;
+}
+
+int ssim_mfma_ms(const SsimMfmaMs& c, int device, hipStream_t st, bool* done) {
+  *done = false;
+  const int M = c.M;
+  const int64_t planes = static_cast<int64_t>(c.N) * c.C;
+  if (!mfma_enabled() || !c.words || M < 3 || M > 2 + MS_TAIL_MAX) return FA_OK;
+  if (planes > MS_FIN_MAX_PLANES || !(c.C1 > 0.0) || !(c.C2 > 0.0)) return FA_OK;
+  if (!c.out_per_image && !c.out_total) return FA_OK;
+  // every scale's call, checked before anything is launched
+  MfArgs a[2 + MS_TAIL_MAX];
+  double finv[MS_WORD_SCALES] = {}, npix[MS_WORD_SCALES] = {};
+  int H = c.H, W = c.W;
+  for (int i = 0; i < M; ++i) {
+    SsimMfmaCall k = {};
+    k.x = i == 0 ? c.x : c.lx[i];
+    k.y = i == 0 ? c.y : c.ly[i];
+    k.src = i == 0 ? SsimMfmaCall::U8 : i == 1 ? SsimMfmaCall::F16_LEVEL : SsimMfmaCall::F32_LEVEL;
+    const int64_t plane = static_cast<int64_t>(H) * W;
+    k.xsn = i == 0 ? c.xsn : plane * c.C;
+    k.xsc = i == 0 ? c.xsc : plane;
+    k.ysn = i == 0 ? c.ysn : plane * c.C;
+    k.ysc = i == 0 ? c.ysc : plane;
+    k.xsh = i == 0 ? c.xsh : W;
+    k.ysh = i == 0 ? c.ysh : W;
+    k.N = c.N;
+    k.C = c.C;
+    k.H = H;
+    k.W = W;
+    k.Hout = H - c.K + 1;
+    k.Wout = W - c.K + 1;
+    k.K = c.K;
+    k.win = c.win;
+    k.C1 = c.C1;
+    k.C2 = c.C2;
+    // the next level: float16 below the uint8 input, float32 below that
+    if (i + 1 < M && i <= 1) {
+      k.px = c.lx[i + 1];
+      k.py = c.ly[i + 1];
+      k.level_f16 = i == 0;
+    }
+    const int src = i == 0 ? SRC_U8 : i == 1 ? SRC_F16 : SRC_F32;
+    if (k.Hout < 1 || k.Wout < 1 || !mfma_fits(k, src, i + 1 < M ? MF_CSO : MF_CS)) return FA_OK;
+    if (i == 1)
+      for (int d = 0; d < 2; ++d)
+        if (3 + d < M && (reinterpret_cast<uintptr_t>(c.lx[3 + d]) |
+                          reinterpret_cast<uintptr_t>(c.ly[3 + d])) & 15)
+          return FA_OK;
+    a[i] = args_of(k);
+    npix[i] = static_cast<double>(k.Hout) * k.Wout;
+    fixed_scale(npix[i], &a[i].fscale, &finv[i]);
+    a[i].acc = c.words + static_cast<int64_t>(i) * planes * MF_STRIDE;
+    H /= 2;
+    W /= 2;
+  }
+  // scale 1 also writes the levels of scales 3 and 4
+  for (int d = 0; d < 2; ++d) {
+    a[1].dpx[d] = 3 + d < M ? c.lx[3 + d] : nullptr;
+    a[1].dpy[d] = 3 + d < M ? c.ly[3 + d] : nullptr;
+  }
+  const int64_t cus = cu_count(device);
+  auto k0 = ssim_mfma_kernel<SRC_U8, MF_CSO, LVL_F16, FIN_MS>;
+  auto k1 = ssim_mfma_kernel<SRC_F16, MF_CSO, LVL_F32D, FIN_MS>;
+  static const int occ0 = occupancy_of(k0), occ1 = occupancy_of(k1),
+                   occt = occupancy_of(ssim_mfma_tail_kernel);
+  // the counts of every word (tiles per plane) stay below 2^MF_COUNT_BITS
+  constexpr int64_t max_tiles = (1 << MF_COUNT_BITS) - 1;
+  if (!plan_tiles(a[0], planes, cus * occ0, max_tiles, true) ||
+      !plan_tiles(a[1], planes, cus * occ1, max_tiles, true))
+    return FA_OK;
+  // The coarse scales share one round of resident workgroups: starting from
+  // one chunk per column, the scale with the longest chunks is split once
+  // more while the launch still fits the round (on configs[4]: 3, 1 and 2
+  // chunks, 720 of 768 workgroups).  Measured: these passes are bound by
+  // instruction issue, so more workgroups than the round holds only add the
+  // extra block of rows each chunk starts with; planned one scale at a time
+  // (each with the whole round) the launch took 27.6 us, planned together
+  // 22-24.
+  MfTail t = {};
+  t.n = M - 2;
+  t.first = 2;
+  int chunks[MS_TAIL_MAX], blocks[MS_TAIL_MAX];
+  int64_t cols[MS_TAIL_MAX], wgs = 0;
+  for (int k = 0; k < t.n; ++k) {
+    MfArgs& s = a[2 + k];
+    s.strips = (s.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
+    blocks[k] = (s.Hout + MT - 1) / MT;
+    cols[k] = planes * s.strips;
+    chunks[k] = 1;
+    wgs += cols[k];
+  }
+  const int64_t round = cus * occt;
+  for (;;) {
+    int pick = -1, longest = 0;
+    for (int k = 0; k < t.n; ++k) {
+      const int len = (blocks[k] + chunks[k] - 1) / chunks[k];
+      if (len > 1 && len > longest && wgs + cols[k] <= round) {
+        longest = len;
+        pick = k;
+      }
+    }
+    if (pick < 0) break;
+    ++chunks[pick];
+    wgs += cols[pick];
+  }
+  wgs = 0;
+  for (int k = 0; k < t.n; ++k) {
+    MfArgs& s = a[2 + k];
+    const int m = (blocks[k] + chunks[k] - 1) / chunks[k];  // blocks per chunk
+    const int ch = (blocks[k] + m - 1) / m;
+    s.TH = s.THs = MT * m;
+    s.nbig = ch;
+    s.tiles = s.strips * ch;
+    s.xcd_planes = 0;
+    if (s.tiles > max_tiles) return FA_OK;
+    wgs += planes * s.tiles;
+    if (wgs > INT32_MAX) return FA_OK;
+    t.s[k] = s;
+    t.wg_end[k] = static_cast<int>(wgs);
+  }
+  t.M = M;
+  t.N = c.N;
+  t.C = c.C;
+  t.planes = static_cast<int>(planes);
+  t.words = c.words;
+  for (int i = 0; i < M; ++i) {
+    t.finv[i] = finv[i];
+    t.npix[i] = npix[i];
+    t.w[i] = c.weights[i];
+  }
+  t.out_per_image = c.out_per_image;
+  t.out_total = c.out_total;
+  hipLaunchKernelGGL(k0, dim3(static_cast<unsigned>(planes * a[0].tiles)), dim3(BLOCK), 0, st,
+                     a[0]);
+  FA_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k1, dim3(static_cast<unsigned>(planes * a[1].tiles)), dim3(BLOCK), 0, st,
+                     a[1]);
+  FA_LAUNCH_CHECK();
+  hipLaunchKernelGGL(ssim_mfma_tail_kernel, dim3(static_cast<unsigned>(wgs)), dim3(BLOCK), 0,
+                     st, t);
+  FA_LAUNCH_CHECK();
+  *done = true;
   return FA_OK;
 }
 

@@ -344,15 +344,27 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials,
  * (levels, partial sums, scratch).  Every scale's shape is checked before
  * anything is launched.  out_per_image (N) / out_total (1) float64: either
  * may be null, not both.
+ *
+ * acc: null, or FA_MS_SSIM_ACC_WORDS uint64 of device memory, zero when the
+ * call starts; the call leaves it zero.  With it, uint8 input without luma
+ * whose every scale fits the matrix-core kernel (widths a multiple of 8 at
+ * every scale, e.g. W % 128 == 0 at M = 5; K <= 16; C1, C2 > 0; N * C <= 256;
+ * 3 <= M <= 5) runs as three launches: scale 0, scale 1 (which also writes
+ * levels 3 and 4), and scales 2 .. M - 1 side by side in one launch whose last
+ * workgroup finishes the reduction from per-(scale, plane) fixed-point sums
+ * (about 1e-13 relative from the float64 reduction, the same bits run to run).
+ * Other calls ignore acc.  `acc` is state of one stream: calls that overlap
+ * on it (two streams, graph replays beside eager calls) race.
  */
+#define FA_MS_SSIM_ACC_WORDS ((8 * 256 + 1) * 16)
 FA_API int fa_gpu_ms_ssim_workspace(int dtype, int N, int C, int H, int W, int K, int M,
                                     int luma, int64_t* out_bytes);
 FA_API int fa_gpu_ms_ssim(const void* x, const void* y, int dtype, int N, int C, int H, int W,
                           const int64_t* x_strides, const int64_t* y_strides,
                           const double* luma, const float* win, int K, double shift,
                           double C1, double C2, const double* weights, int M, void* workspace,
-                          int64_t workspace_bytes, double* out_per_image, double* out_total,
-                          int device, void* stream);
+                          int64_t workspace_bytes, uint64_t* acc, double* out_per_image,
+                          double* out_total, int device, void* stream);
 
 /*
  * No counterpart in the reference.  For callers that cannot allocate device

@@ -122,11 +122,11 @@ def test_argument_validation_before_any_gpu_work(lib):
     ms = lib.fa_gpu_ms_ssim
     # a scale too small, and a workspace too small: refused before any launch
     assert ms(p, p, 0, 1, 1, 160, 200, None, None, None, p, 11, 127.5, 6.5, 58.5, w5, 5, p,
-              1 << 40, p, None, 0, None) == 2
+              1 << 40, None, p, None, 0, None) == 2
     assert ms(p, p, 0, 1, 1, 176, 176, None, None, None, p, 11, 127.5, 6.5, 58.5, w5, 5, p,
-              16, p, None, 0, None) == 5
+              16, None, p, None, 0, None) == 5
     assert ms(p, p, 0, 1, 1, 176, 176, None, None, None, p, 11, 127.5, 6.5, 58.5, w5, 5, p,
-              1 << 40, None, None, 0, None) == 5  # no output
+              1 << 40, p, None, None, 0, None) == 5  # no output
     once = lib.fa_gpu_pixel_reduce_once
     assert once(p, p, 0, 1, 16, 0, 0.0, -1e300, None, 1, p, p, None, None, None, 0, None) == 5
     assert once(p, p, 0, 1, 16, 4, 0.0, -1e300, p, 1, p, p, None, None, None, 0, None) == 4

@@ -153,6 +153,78 @@ def test_ms_ssim_too_small(gpu):
     assert float(fa.ms_ssim(z, z, data_range=1.0)) == pytest.approx(1.0)
 
 
+def _ms_call(x, y, weights, k=11, acc=None):
+    """fa_gpu_ms_ssim through the C ABI over a workspace filled with 0xFF:
+    (per-image values, batch mean, the workspace afterwards)."""
+    import ctypes
+
+    from frame_analytics_amd import backend
+    from frame_analytics_amd.functional import gaussian_window_1d
+
+    n, c, h, w = (int(v) for v in x.shape)
+    m = len(weights)
+    win = gaussian_window_1d(k, 1.5, device=x.device, dtype=torch.float32)
+    nb = ctypes.c_int64(0)
+    assert backend.call_gpu("fa_gpu_ms_ssim_workspace", 0, n, c, h, w, k, m, 0,
+                            ctypes.byref(nb)) == 0
+    ws = torch.full((nb.value,), 0xFF, dtype=torch.uint8, device=x.device)
+    out = torch.full((n + 1,), -7.0, dtype=torch.float64, device=x.device)
+    x, xs = backend._view_strides(x)
+    y, ys = backend._view_strides(y)
+    wts = (ctypes.c_double * m)(*[float(v) for v in weights])
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = backend.call_gpu("fa_gpu_ms_ssim", x.data_ptr(), y.data_ptr(), 0, n, c, h, w, xs, ys,
+                          None, win.data_ptr(), k, 127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2,
+                          wts, m, ws.data_ptr(), nb.value,
+                          None if acc is None else acc.data_ptr(), out.data_ptr(),
+                          out[n:].data_ptr(), 0, stream)
+    assert rc == 0, rc
+    o = out.cpu().numpy()
+    return o[:n], float(o[n]), ws
+
+
+@pytest.mark.parametrize("shape,weights,k,crop", [
+    ((3, 3, 517, 512), None, 11, False),
+    ((2, 1, 256, 640), (0.3, 0.3, 0.4), 11, False),
+    ((2, 3, 384, 384), (0.1, 0.2, 0.3, 0.4), 7, True),
+])
+def test_ms_ssim_three_launch_path(gpu, shape, weights, k, crop):
+    """uint8 MS-SSIM with the stream's accumulator: scale 0, scale 1 (which
+    also writes the levels of scales 3 and 4), then the coarse scales side by
+    side in one launch whose last workgroup finishes the reduction from
+    fixed-point sums.  Against the per-scale path (no accumulator) to 1e-12
+    relative and against the oracle to the bar, on two calls in a row; each
+    call leaves the accumulator zero and never writes the per-scale path's
+    reduction scratch (the workspace's last region, which that path fills)."""
+    from frame_analytics_amd import backend
+    from frame_analytics_amd.functional import MS_SSIM_WEIGHTS
+
+    w = tuple(MS_SSIM_WEIGHTS) if weights is None else weights
+    n, c, h, wd = shape
+    if crop:
+        a, b = u8_pair((n, c, h + 16, wd + 24), 9.0, seed=5)
+        x = torch.from_numpy(a).to(gpu)[..., 5:5 + h, 8:8 + wd]
+        y = torch.from_numpy(b).to(gpu)[..., 5:5 + h, 8:8 + wd]
+    else:
+        a, b = u8_pair(shape, 9.0, seed=5)
+        x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    m = len(w)
+    scratch = m * n * c * 8
+    start = -((scratch + 255) // 256 * 256)  # the reduction's scratch, last in the workspace
+    per0, tot0, ws0 = _ms_call(x, y, w, k)
+    assert not bool((ws0[start:start + scratch] == 0xFF).all())
+    acc = torch.zeros(backend._ACC_WORDS["ms"], dtype=torch.int64, device=gpu)
+    for _ in range(2):
+        per, tot, ws = _ms_call(x, y, w, k, acc=acc)
+        assert bool((ws[start:start + scratch] == 0xFF).all())
+        assert int((acc != 0).sum()) == 0
+        assert np.all(np.abs(per - per0) <= 1e-12 * np.abs(per0)), (per, per0)
+        assert abs(tot - tot0) <= 1e-12 * abs(tot0), (tot, tot0)
+    want = ref.ms_ssim(x.cpu().numpy().astype(np.float64), y.cpu().numpy().astype(np.float64),
+                       255.0, win_size=k, weights=w, reduction="none")
+    assert np.all(np.abs(per - want) <= REL * np.abs(want)), (per, want)
+
+
 @pytest.mark.parametrize("shape", [(1, 1, 192, 192), (2, 3, 180, 200)])
 @pytest.mark.parametrize("wrt", [("x",), ("x", "y")])
 def test_ms_ssim_backward_matches_oracle(gpu, shape, wrt):
