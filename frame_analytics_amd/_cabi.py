@@ -77,6 +77,11 @@ SIGNATURES = {
     "fa_gpu_ms_ssim":
         ([_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _D, _D, _D, _P, _I, _P, _L, _P, _P,
           _P, _I, _P], _I),
+    "fa_gpu_ssim_cs_coef":
+        ([_P, _P, _I, _I, _I, _I, _I, _P, _I, _D, _D, _D, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P,
+          _I, _I, _P], _I),
+    "fa_gpu_ssim_cs_scatter":
+        ([_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _D, _P, _I, _P, _P, _I, _P, _P, _I, _P], _I),
     "fa_gpu_ssim_cs_backward_ex":
         ([_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _D, _D, _D, _P, _P, _I, _P, _P, _P,
           _I, _P], _I),

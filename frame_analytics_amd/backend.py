@@ -729,6 +729,57 @@ def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy,
     return dx, dy
 
 
+def ssim_cs_coef_forward(x, y, win, shift, C1, C2, unit_s, pool_dtype, need_dy):
+    """A training step's CS pass in float64 (``fa_gpu_ssim_cs_coef``): the
+    plane means ``(s, cs)``, the next pyramid level when ``pool_dtype`` is
+    given, and the backward's coefficient maps for a unit gradient of the SSIM
+    means (``unit_s``) or of the cs means, 3 (4 with ``need_dy``) float32 per
+    output pixel.  Returns ``(s, cs, px, py, aux)``."""
+    x, y, win = _contig(x), _contig(y), _win32(win)
+    n, c, h, w = (int(v) for v in x.shape)
+    k = int(win.numel())
+    planes = n * c
+    bpp = workspace_slots("ssim", h, w, k)
+    partial, partial_cs = _f64(x.device, planes, bpp), _f64(x.device, planes, bpp)
+    s, cs = _f64(x.device, planes), _f64(x.device, planes)
+    px = py = None
+    if pool_dtype is not None:
+        px = torch.empty((n, c, h // 2, w // 2), dtype=pool_dtype, device=x.device)
+        py = torch.empty_like(px)
+    aux = torch.empty((4 if need_dy else 3, planes, h - k + 1, w - k + 1), device=x.device,
+                      dtype=torch.float32)
+    dev, stream = _site(x)
+    pcode = _DTYPE_CODE[pool_dtype if pool_dtype is not None else torch.float64]
+    _run("fa_gpu_ssim_cs_coef", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), k,
+         float(shift), float(C1), float(C2), int(bool(unit_s)), _ptr(partial), _ptr(partial_cs),
+         bpp, _ptr(s), _ptr(cs), _ptr(px), _ptr(py), pcode, _ptr(aux), int(bool(need_dy)),
+         dev, stream)
+    return s, cs, px, py, aux
+
+
+def ssim_cs_scatter(x, y, g, aux, win, shift, need_dx, need_dy, gpx=None, gpy=None):
+    """Gradients from ``ssim_cs_coef_forward``'s maps: each plane's share times
+    ``g[plane]`` (the upstream gradient of the plane mean the maps were made
+    for), plus a quarter of the pyramid level's gradient ``gpx`` / ``gpy``."""
+    x, y, win = _contig(x), _contig(y), _win32(win)
+    n, c, h, w = (int(v) for v in x.shape)
+    k = int(win.numel())
+    gf = g.to(torch.float32).contiguous().reshape(-1)
+    dx = torch.empty_like(x) if need_dx else None
+    dy = torch.empty_like(y) if need_dy else None
+    gpx = _contig(gpx) if (gpx is not None and need_dx) else None
+    gpy = _contig(gpy) if (gpy is not None and need_dy) else None
+    if gpx is not None and gpy is not None and gpx.dtype != gpy.dtype:
+        gpy = gpy.to(gpx.dtype)
+    gp = gpx if gpx is not None else gpy
+    gp_code = _DTYPE_CODE[gp.dtype if gp is not None else torch.float64]
+    dev, stream = _site(x)
+    _run("fa_gpu_ssim_cs_scatter", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], _ptr(gf), _ptr(win), k,
+         n, c, h, w, float(shift), _ptr(aux), int(aux.shape[0] == 4), _ptr(gpx), _ptr(gpy),
+         gp_code, _ptr(dx), _ptr(dy), dev, stream)
+    return dx, dy
+
+
 def ssim_cs_pool_available(x: torch.Tensor, y: torch.Tensor, win_size: int) -> bool:
     """Can the native MS-SSIM scale step (CS means + fused pyramid) serve x, y?"""
     return (x.is_cuda and x.dim() == 4 and x.dtype in _SUPPORTED and y.dtype == x.dtype

@@ -30,7 +30,13 @@
 
 namespace fa {
 
-enum { MODE_REDUCE = 0, MODE_MAP = 1, MODE_CS = 2, MODE_PREP = 3, MODE_PREP_CS = 4 };
+// MODE_CSF: the CS pass of a training step, in float64, which also writes
+// the coefficient maps of MODE_PREP_CS for a unit gradient of one plane mean
+// (the SSIM means or the cs means, SsimArgs::unit_s): MS-SSIM's loss reads
+// only one of them at each scale, so the maps the backward needs are these
+// times that plane's upstream gradient, and no coefficient pass runs there.
+enum { MODE_REDUCE = 0, MODE_MAP = 1, MODE_CS = 2, MODE_PREP = 3, MODE_PREP_CS = 4,
+       MODE_CSF = 5 };
 
 // Output rows per workgroup (TH), a multiple of 4 up to 128.  A workgroup
 // walks its rows in sequence and re-reads K-1 halo rows, so a launch trades
@@ -111,6 +117,7 @@ struct SsimArgs {
   double gnorm;         // MODE_PREP(_CS): 1/(npix*planes) or 1/npix
   const float* gs;      // MODE_PREP_CS: per-plane dL/d(mean ssim)
   const float* gcs;     // MODE_PREP_CS: per-plane dL/d(mean cs)
+  int unit_s;           // MODE_CSF: maps for d(mean ssim) = 1 (1) or d(mean cs) = 1 (0)
   float* ob;
   float* oc;
   float* otx;
@@ -204,7 +211,7 @@ struct SsimPol {
   // even lane.  The engine hands both rows of a pair at once, so there is no
   // row-parity branch and no state between calls.
   __device__ inline void pool2(int row, const Raw& a, const Raw& b) {
-    if constexpr (MODE == MODE_CS) {
+    if constexpr (MODE == MODE_CS || MODE == MODE_CSF) {
       // prow1 is even, so row < prow1 covers row + 1 too
       if (!pool_on || row < prow0 || row >= prow1) return;  // uniform
       PA sx = static_cast<PA>(a.x) + static_cast<PA>(b.x);
@@ -300,6 +307,32 @@ struct SsimPol {
       const CT inv = quot(CT(1), B1 * B2);
       row_s += valid ? A1 * A2 * inv : CT(0);
       row_cs += valid ? A2 * B1 * inv : CT(0);
+    } else if constexpr (MODE == MODE_CSF) {
+      // the plane sums of MODE_CS, and the MODE_PREP_CS coefficients below
+      // with (gS, gCS) = (1 / npix, 0) or (0, 1 / npix)
+      const CT inv = CT(1) / (B1 * B2);
+      const CT S = A1 * A2 * inv;
+      const CT CS = A2 * B1 * inv;
+      row_s += valid ? S : CT(0);
+      row_cs += valid ? CS : CT(0);
+      if (valid) {
+        const CT mx = ux + shift;
+        const CT my = uy + shift;
+        const CT iB1 = B2 * inv;
+        const CT iB2 = B1 * inv;
+        const CT k = CT(2) * A2 * inv;
+        const int64_t idx = out_off + static_cast<int64_t>(orow) * Wout + ocol;
+        const CT b = -(gS * S + gCS * CS) * iB2;
+        const CT c = CT(2) * (gS * A1 * iB1 + gCS) * iB2;
+        const CT dmux = k * (my - mx * A1 * iB1);
+        ob[idx] = static_cast<float>(b);
+        oc[idx] = static_cast<float>(c);
+        otx[idx] = static_cast<float>(gS * dmux - CT(2) * b * ux - c * uy);
+        if (oty) {
+          const CT dmuy = k * (mx - my * A1 * iB1);
+          oty[idx] = static_cast<float>(gS * dmuy - CT(2) * b * uy - c * ux);
+        }
+      }
     } else if (valid) {
       // the backward coefficients keep their guarded stores: issued on every
       // path (row_store) they measured slower (configs[3] 27.0 -> 32.3 us)
@@ -403,6 +436,10 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
     pol.gS = static_cast<CT>(a.gs[plane]) * static_cast<CT>(a.gnorm);
     pol.gCS = static_cast<CT>(a.gcs[plane]) * static_cast<CT>(a.gnorm);
   }
+  if constexpr (MODE == MODE_CSF) {
+    pol.gS = a.unit_s ? static_cast<CT>(a.gnorm) : CT(0);
+    pol.gCS = a.unit_s ? CT(0) : static_cast<CT>(a.gnorm);
+  }
   pol.k1 = static_cast<CT>(2.0 * a.shift * a.shift + a.C1);
   pol.row_s = CT(0);
   pol.row_cs = CT(0);
@@ -411,7 +448,7 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   pol.px = a.px;
   pol.py = a.py;
   pol.pool_on = false;
-  if constexpr (MODE == MODE_CS) {
+  if constexpr (MODE == MODE_CS || MODE == MODE_CSF) {
     if (a.px) {
       // rows and columns of the output map this workgroup owns, extended to
       // the image edge (2 * floor(H/2), 2 * floor(W/2)) in the last chunk /
@@ -442,7 +479,7 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   if constexpr (MODE == MODE_REDUCE || MODE == MODE_MAP) {
     const double s = block_sum(pol.acc_s, sred);
     if (threadIdx.x == 0) a.partial[slot] = s;
-  } else if constexpr (MODE == MODE_CS) {
+  } else if constexpr (MODE == MODE_CS || MODE == MODE_CSF) {
     double s = 0.0, scs = 0.0;
     block_sum2(pol.acc_s, pol.acc_cs, sred, &s, &scs);
     if (threadIdx.x == 0) {
@@ -471,6 +508,8 @@ struct ScatterArgs {
   const void* gpx;  // optional gradient of the next pyramid level (2x2 means)
   const void* gpy;
   int gp_f64;       // its element type: float64 (1) or float32 (0)
+  const float* gscale;  // optional per-plane factor of the coefficient maps'
+                        // share (maps written by MODE_CSF for a unit gradient)
 };
 
 template <typename T, bool DY>
@@ -499,6 +538,7 @@ struct ScatterPol {
   const void* gpx;
   const void* gpy;
   bool gp_f64;
+  double gmul;       // this plane's factor of the maps' share (1 without gscale)
   int Hp, Wp;        // pyramid level grid: floor(H/2) x floor(W/2)
   int64_t gp_off;    // this plane of the pyramid gradient
 
@@ -598,7 +638,7 @@ struct ScatterPol {
       // every lane stores, through a row buffer resource (see row_store)
       const double xv = static_cast<double>(e.x[k]) - shift;
       const double yv = static_cast<double>(e.y[k]) - shift;
-      row_store(static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + e.g[k >> 1]),
+      row_store(static_cast<T>(gmul * (2.0 * xv * v[0] + yv * v[1] + v[2]) + e.g[k >> 1]),
                 row_rsrc(dx ? dx + img_off + static_cast<int64_t>(orow) * W : nullptr, W),
                 lane_off<T>(ocol, valid));
     } else {
@@ -606,8 +646,11 @@ struct ScatterPol {
       const int64_t o = img_off + static_cast<int64_t>(orow) * W + ocol;
       const double xv = static_cast<double>(x[o]) - shift;
       const double yv = static_cast<double>(y[o]) - shift;
-      if (dx) dx[o] = static_cast<T>(2.0 * xv * v[0] + yv * v[1] + v[2] + pyr_grad(gpx, orow, ocol));
-      dy[o] = static_cast<T>(2.0 * yv * v[0] + xv * v[1] + v[3] + pyr_grad(gpy, orow, ocol));
+      if (dx)
+        dx[o] = static_cast<T>(gmul * (2.0 * xv * v[0] + yv * v[1] + v[2]) +
+                               pyr_grad(gpx, orow, ocol));
+      dy[o] = static_cast<T>(gmul * (2.0 * yv * v[0] + xv * v[1] + v[3]) +
+                             pyr_grad(gpy, orow, ocol));
     }
   }
 };
@@ -642,6 +685,8 @@ __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
   pol.gpx = a.gpx;
   pol.gpy = a.gpy;
   pol.gp_f64 = a.gp_f64 != 0;
+  // x * 1.0 is x: without gscale the results are those of the plain scatter
+  pol.gmul = a.gscale ? static_cast<double>(a.gscale[plane]) : 1.0;
   pol.Hp = a.H / 2;
   pol.Wp = a.W / 2;
   pol.gp_off = static_cast<int64_t>(plane) * pol.Hp * pol.Wp;
@@ -867,6 +912,43 @@ static int set_views(SsimArgs& a, int C, int H, int W, const int64_t* xs, const 
   return FA_OK;
 }
 
+// The scatter of coefficient maps `aux` (b, c, tx and, with aux_dy, ty, each
+// N * C * Hout * Wout float32) onto dx / dy, optionally scaled per plane by
+// gscale, plus a quarter of the pyramid level's gradient over each 2x2 block.
+template <typename T>
+static int scatter_impl(const T* x, const T* y, const float* gscale, const float* win, int K,
+                        int N, int C, int H, int W, double shift, const float* aux, bool aux_dy,
+                        const void* gpx, const void* gpy, int gp_dtype, T* dx, T* dy,
+                        int device, hipStream_t st) {
+  int Hout = 0, Wout = 0;
+  const int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  if (dy && !aux_dy) return FA_E_ARG;
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  const int64_t aux_stride = planes * Hout * Wout;
+  ScatterArgs s = {};
+  s.x = x;
+  s.y = y;
+  s.ab = aux;
+  s.ac = aux + aux_stride;
+  s.atx = aux + 2 * aux_stride;
+  s.aty = aux_dy ? aux + 3 * aux_stride : nullptr;
+  s.dx = dx;
+  s.dy = dy;
+  s.win = win;
+  s.H = H;
+  s.W = W;
+  s.Hout = Hout;
+  s.Wout = Wout;
+  s.shift = shift;
+  s.gpx = gpx;
+  s.gpy = gpy;
+  s.gp_f64 = gp_dtype == FA_F64 ? 1 : 0;
+  s.gscale = gscale;
+  return dy ? launch_scatter_k<T, true>(K, s, planes, device, st)
+            : launch_scatter_k<T, false>(K, s, planes, device, st);
+}
+
 // The coefficient pass plus the scatter, shared by the backward entry points.
 // T is the element type of x, y, dx and dy (float, or double for the float64
 // MS-SSIM pyramid levels); the arithmetic is float64 either way.
@@ -910,27 +992,8 @@ static int ssim_backward_impl(const T* x, const T* y, const float* dmap,
   a.oty = dy ? aux + 3 * aux_stride : nullptr;
   rc = launch_ssim_k<T, double, MODE>(K, a, planes, device, st);
   if (rc != FA_OK) return rc;
-
-  ScatterArgs s = {};
-  s.x = x;
-  s.y = y;
-  s.ab = a.ob;
-  s.ac = a.oc;
-  s.atx = a.otx;
-  s.aty = a.oty;
-  s.dx = dx;
-  s.dy = dy;
-  s.win = win;
-  s.H = H;
-  s.W = W;
-  s.Hout = Hout;
-  s.Wout = Wout;
-  s.shift = shift;
-  s.gpx = gpx;
-  s.gpy = gpy;
-  s.gp_f64 = gp_dtype == FA_F64 ? 1 : 0;
-  return dy ? launch_scatter_k<T, true>(K, s, planes, device, st)
-            : launch_scatter_k<T, false>(K, s, planes, device, st);
+  return scatter_impl<T>(x, y, nullptr, win, K, N, C, H, W, shift, aux, dy != nullptr, gpx, gpy,
+                         gp_dtype, dx, dy, device, st);
 }
 
 // fa_gpu_ssim_cs over views, with optional luma and, when px / py are not
@@ -1372,6 +1435,91 @@ FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
       static_cast<const double*>(x), static_cast<const double*>(y), nullptr, nullptr, gs, gcs,
       win, K, N, C, H, W, shift, C1, C2, aux, static_cast<double*>(dx),
       static_cast<double*>(dy), gpx, gpy, gp_dtype, device, st);
+}
+
+// No counterpart in the reference, whose MS-SSIM training path runs the CS
+// forward of every scale and, in the backward, a coefficient pass before the
+// scatter (fa_cuda.cu:655-784 per scale).  MS-SSIM's loss reads one plane
+// mean per scale (cs below the coarsest, SSIM there), so this CS pass in
+// float64 also writes the coefficient maps for a unit gradient of that mean
+// (unit_s: of the SSIM means, else of the cs means); fa_gpu_ssim_cs_scatter
+// then scales them by each plane's upstream gradient.
+FA_API int fa_gpu_ssim_cs_coef(const void* x, const void* y, int dtype, int N, int C, int H,
+                               int W, const float* win, int K, double shift, double C1,
+                               double C2, int unit_s, double* partial, double* partial_cs,
+                               int bpp, double* out_s, double* out_cs, void* px, void* py,
+                               int pool_dtype, float* aux, int aux_dy, int device,
+                               void* stream) {
+  if (!x || !y || !win || !partial || !partial_cs || !out_s || !out_cs || !aux)
+    return FA_E_ARG;
+  if (dtype != FA_F32 && dtype != FA_F64) return FA_E_DTYPE;
+  if ((px == nullptr) != (py == nullptr)) return FA_E_ARG;
+  if (px && pool_dtype != FA_F32 && pool_dtype != FA_F64) return FA_E_DTYPE;
+  int Hout = 0, Wout = 0;
+  int rc = ssim_shape(N, C, H, W, K, &Hout, &Wout);
+  if (rc != FA_OK) return rc;
+  if (bpp != ssim_slots(Hout, Wout, K)) return FA_E_ARG;
+  SsimArgs a = {};
+  rc = set_views(a, C, H, W, nullptr, nullptr, nullptr);
+  if (rc != FA_OK) return rc;
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  const int64_t npix = static_cast<int64_t>(Hout) * Wout;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  a.x = x;
+  a.y = y;
+  a.H = H;
+  a.W = W;
+  a.Hout = Hout;
+  a.Wout = Wout;
+  a.shift = shift;
+  a.C1 = C1;
+  a.C2 = C2;
+  a.win = win;
+  a.partial = partial;
+  a.partial_cs = partial_cs;
+  a.px = px;
+  a.py = py;
+  a.pool_f64 = pool_dtype == FA_F64 ? 1 : 0;
+  a.gnorm = 1.0 / static_cast<double>(npix);
+  a.unit_s = unit_s ? 1 : 0;
+  a.ob = aux;
+  a.oc = aux + planes * npix;
+  a.otx = aux + 2 * planes * npix;
+  a.oty = aux_dy ? aux + 3 * planes * npix : nullptr;
+  rc = dtype == FA_F32 ? launch_ssim_k<float, double, MODE_CSF>(K, a, planes, device, st)
+                       : launch_ssim_k<double, double, MODE_CSF>(K, a, planes, device, st);
+  if (rc != FA_OK) return rc;
+  hipLaunchKernelGGL(planes2_kernel, dim3(static_cast<unsigned>(planes)), dim3(BLOCK), 0, st,
+                     partial, partial_cs, a.bpp, static_cast<double>(npix), out_s, out_cs);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
+}
+
+// No counterpart in the reference (see fa_gpu_ssim_cs_coef): the scatter of
+// that pass's maps `aux`, times gscale[plane] (the plane mean's upstream
+// gradient, N * C float32), plus a quarter of the pyramid level's gradient
+// (gpx / gpy of gp_dtype, either may be null) over each 2x2 block.
+FA_API int fa_gpu_ssim_cs_scatter(const void* x, const void* y, int dtype, const float* gscale,
+                                  const float* win, int K, int N, int C, int H, int W,
+                                  double shift, const float* aux, int aux_dy, const void* gpx,
+                                  const void* gpy, int gp_dtype, void* dx, void* dy, int device,
+                                  void* stream) {
+  if (!x || !y || !gscale || !win || !aux) return FA_E_ARG;
+  if (!dx && !dy) return FA_E_ARG;
+  if (dy && !aux_dy) return FA_E_ARG;
+  if (dtype != FA_F32 && dtype != FA_F64) return FA_E_DTYPE;
+  if ((gpx || gpy) && gp_dtype != FA_F32 && gp_dtype != FA_F64) return FA_E_DTYPE;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FA_F32)
+    return scatter_impl<float>(static_cast<const float*>(x), static_cast<const float*>(y), gscale,
+                               win, K, N, C, H, W, shift, aux, aux_dy != 0, gpx, gpy, gp_dtype,
+                               static_cast<float*>(dx), static_cast<float*>(dy), device, st);
+  return scatter_impl<double>(static_cast<const double*>(x), static_cast<const double*>(y),
+                              gscale, win, K, N, C, H, W, shift, aux, aux_dy != 0, gpx, gpy,
+                              gp_dtype, static_cast<double*>(dx), static_cast<double*>(dy),
+                              device, st);
 }
 
 // No counterpart in the reference, which reduces each MS-SSIM scale in its own

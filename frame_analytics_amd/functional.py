@@ -333,25 +333,43 @@ class _NativeSSIM(torch.autograd.Function):
       (ssim, cs) gradient (``fa_gpu_ssim_cs_backward_ex``), so a scale costs
       one forward and two backward launches whatever reaches it.
 
-    Only x, y and the window are kept; the backward recomputes the moments
-    from them (the reference keeps the same memory profile,
-    functional.py:521-572 and :749-783).  ``consts`` is (shift, C1, C2).
+    x, y and the window are kept and the backward recomputes the moments from
+    them (the reference keeps the same memory profile, functional.py:521-572
+    and :749-783) -- except where the caller says which plane mean its loss
+    reads (``use``, "s" or "cs": MS-SSIM reads cs below its coarsest scale and
+    SSIM there) and the input is float32 or float64.  Then the forward runs in
+    float64 and also writes the backward's coefficient maps for a unit
+    gradient of that mean (``fa_gpu_ssim_cs_coef``, 3 float32 per output
+    pixel, 4 when y needs a gradient, kept until the backward), and the
+    backward is the scatter alone, each plane scaled by its upstream gradient
+    (``fa_gpu_ssim_cs_scatter``); a backward that receives the other mean's
+    gradient too recomputes, as without ``use``.  ``consts`` is (shift, C1,
+    C2).
     """
 
     @staticmethod
-    def forward(ctx, x, y, win, consts, form, pool_dtype):
+    def forward(ctx, x, y, win, consts, form, pool_dtype, use=None):
         from . import backend
 
         shift, C1, C2 = consts
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(x, y, win)
-        ctx.consts, ctx.form = consts, form
+        ctx.consts, ctx.form, ctx.aux, ctx.use = consts, form, None, use
         if form in ("mean", "map"):
             res = backend.ssim_fused(x, y, win, shift, C1, C2, form == "map")
             return res[2] if form == "map" else res[1]
-        if form == "cs":
+        need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if (use is not None and (need_dx or need_dy)
+                and x.dtype in (torch.float32, torch.float64)):
+            s, cs, px, py, ctx.aux = backend.ssim_cs_coef_forward(
+                x, y, win, shift, C1, C2, use == "s",
+                pool_dtype if form == "cs+pool" else None, need_dy)
+            if form == "cs":
+                return s, cs
+        elif form == "cs":
             return backend.ssim_cs_forward(x, y, win, shift, C1, C2)
-        s, cs, px, py = backend.ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype)
+        else:
+            s, cs, px, py = backend.ssim_cs_forward(x, y, win, shift, C1, C2, pool_dtype)
         # a level of an input that needs no gradient needs none either: without
         # this the next scale would compute (and this one spread) its gradient
         for level, wanted in ((px, ctx.needs_input_grad[0]), (py, ctx.needs_input_grad[1])):
@@ -365,7 +383,7 @@ class _NativeSSIM(torch.autograd.Function):
 
         _reject_double_backward()
         need_dx, need_dy = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        nothing = (None,) * 6
+        nothing = (None,) * 7
         if not (need_dx or need_dy) or all(g is None for g in grads):
             return nothing
         x, y, win = ctx.saved_tensors
@@ -378,9 +396,17 @@ class _NativeSSIM(torch.autograd.Function):
                                            need_dx, need_dy)
         else:
             planes = x.shape[0] * x.shape[1]
+            g_px, g_py = grads[2:4] if ctx.form == "cs+pool" else (None, None)
+            g_used, g_other = (grads[0], grads[1]) if ctx.use == "s" else (grads[1], grads[0])
+            if ctx.aux is not None and g_other is None:
+                if g_used is None:
+                    g_used = x.new_zeros(planes, dtype=torch.float32)
+                dx, dy = backend.ssim_cs_scatter(x, y, g_used, ctx.aux, win, shift, need_dx,
+                                                 need_dy, g_px, g_py)
+                ctx.aux = None
+                return (dx if need_dx else None, dy if need_dy else None) + nothing[2:]
             g_s, g_cs = (g if g is not None else x.new_zeros(planes, dtype=torch.float32)
                          for g in grads[:2])
-            g_px, g_py = grads[2:4] if ctx.form == "cs+pool" else (None, None)
             dx, dy = backend.ssim_cs_backward(x, y, g_s, g_cs, win, shift, C1, C2,
                                               need_dx, need_dy, g_px, g_py)
         return (dx if need_dx else None, dy if need_dy else None) + nothing[2:]
@@ -576,10 +602,12 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
         for i in range(scales):
             last = i == scales - 1
             if grad:
+                # the loss reads the SSIM means at the coarsest scale, cs below
                 if last:
-                    s, cs = _NativeSSIM.apply(cx, cy, win32, consts, "cs", None)
+                    s, cs = _NativeSSIM.apply(cx, cy, win32, consts, "cs", None, "s")
                 else:
-                    s, cs, cx, cy = _NativeSSIM.apply(cx, cy, win32, consts, "cs+pool", pdt)
+                    s, cs, cx, cy = _NativeSSIM.apply(cx, cy, win32, consts, "cs+pool", pdt,
+                                                      "cs")
             else:
                 out = backend.ssim_cs_pool(cx, cy, win32, shift, C1, C2,
                                            None if last else pdt, luma=lw if i == 0 else None)

@@ -293,6 +293,43 @@ FA_API int fa_gpu_ssim_cs_backward_ex(const void* x, const void* y, int dtype,
                                       int device, void* stream);
 
 /*
+ * No counterpart in the reference, whose MS-SSIM training path runs the CS
+ * forward of every scale and, in the backward, a coefficient pass before the
+ * scatter (fa_cuda.cu:655-784 per scale).  MS-SSIM's loss reads one plane mean
+ * per scale (cs below the coarsest scale, SSIM there), and the coefficient
+ * maps are linear in that mean's gradient.  This pass is the CS forward of
+ * fa_gpu_ssim_cs_ex in float64 (x / y of `dtype` FA_F32 or FA_F64, contiguous
+ * N x C x H x W, no luma) -- plane means out_s / out_cs (N * C float64) from
+ * `partial` / `partial_cs` (bpp slots per plane, fa_gpu_ssim_workspace), and
+ * optionally the next pyramid level px / py of `pool_dtype` (FA_F32 or
+ * FA_F64) -- which also writes into `aux` the coefficient maps of
+ * fa_gpu_ssim_cs_backward for a unit gradient of the SSIM means (unit_s != 0)
+ * or of the cs means (unit_s == 0): b, c, tx and, with aux_dy, ty, each
+ * N * C * Hout * Wout float32.
+ */
+FA_API int fa_gpu_ssim_cs_coef(const void* x, const void* y, int dtype, int N,
+                               int C, int H, int W, const float* win, int K,
+                               double shift, double C1, double C2, int unit_s,
+                               double* partial, double* partial_cs, int bpp,
+                               double* out_s, double* out_cs, void* px,
+                               void* py, int pool_dtype, float* aux,
+                               int aux_dy, int device, void* stream);
+
+/*
+ * No counterpart in the reference (see fa_gpu_ssim_cs_coef).  The scatter of
+ * fa_gpu_ssim_cs_backward over the maps fa_gpu_ssim_cs_coef wrote, each
+ * plane's share times gscale[plane] (N * C float32: the upstream gradient of
+ * that plane's mean), plus the pyramid level's gradient gpx / gpy as in
+ * fa_gpu_ssim_cs_backward_ex.  dy needs maps written with aux_dy.
+ */
+FA_API int fa_gpu_ssim_cs_scatter(const void* x, const void* y, int dtype,
+                                  const float* gscale, const float* win, int K,
+                                  int N, int C, int H, int W, double shift,
+                                  const float* aux, int aux_dy, const void* gpx,
+                                  const void* gpy, int gp_dtype, void* dx,
+                                  void* dy, int device, void* stream);
+
+/*
  * No counterpart in the reference, whose GMS / GMSD losses differentiate the
  * portable PyTorch path (modules.py:183-184).  Gradients of
  *   L = sum_n g_mean[n] * mean_n(q) + g_std[n] * std_n(q)

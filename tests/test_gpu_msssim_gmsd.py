@@ -244,6 +244,49 @@ def test_ms_ssim_backward_matches_oracle(gpu, shape, wrt):
         assert err <= REL, err
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+@pytest.mark.parametrize("unit_s", [False, True])
+@pytest.mark.parametrize("need_dy", [False, True])
+def test_cs_coef_scatter_matches_recomputed_backward(gpu, dt, unit_s, need_dy):
+    """The training CS pass that also writes unit-gradient coefficient maps
+    (fa_gpu_ssim_cs_coef) and the scatter that scales them per plane
+    (fa_gpu_ssim_cs_scatter) against the CS forward and the recomputing
+    backward (fa_gpu_ssim_cs_backward_ex) with the same gradient: plane means
+    to 1e-6 of the float32 forward (1e-12 of the float64 one), the pyramid
+    levels bit for bit, dx / dy to 1e-6 max-normwise (both paths round the
+    maps to float32: one the unit maps, the other the scaled ones), with and
+    without the level's gradient."""
+    from frame_analytics_amd import backend
+    from frame_analytics_amd.functional import gaussian_window_1d
+
+    xa, ya = float_pair((2, 3, 100, 124), 0.05, seed=7)
+    x = torch.from_numpy(xa).to(device=gpu, dtype=dt)
+    y = torch.from_numpy(ya).to(device=gpu, dtype=dt)
+    win = gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    consts = (0.5, (0.01) ** 2, (0.03) ** 2)
+    s0, cs0, px0, py0 = backend.ssim_cs_forward(x, y, win, *consts, torch.float64)
+    s1, cs1, px1, py1, aux = backend.ssim_cs_coef_forward(x, y, win, *consts, unit_s,
+                                                          torch.float64, need_dy)
+    tol = 1e-6 if dt == torch.float32 else 1e-12
+    for a, b in ((s1, s0), (cs1, cs0)):
+        assert float(((a - b).abs() / b.abs()).max()) <= tol
+    assert torch.equal(px1, px0) and torch.equal(py1, py0)
+    g = torch.linspace(-1.5, 2.0, 6, device=gpu, dtype=torch.float64)
+    zero = torch.zeros_like(g)
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    for gp in (None, torch.randn(px0.shape, generator=gen, dtype=torch.float64).to(gpu)):
+        gpy = gp if need_dy else None
+        dx, dy = backend.ssim_cs_scatter(x, y, g, aux, win, consts[0], True, need_dy, gp, gpy)
+        wx, wy = backend.ssim_cs_backward(x, y, g if unit_s else zero, zero if unit_s else g,
+                                          win, *consts, True, need_dy, gp, gpy)
+        for got, want in ((dx, wx), (dy, wy)):
+            assert (got is None) == (want is None)
+            if want is None:
+                continue
+            err = float((got - want).abs().max() / want.abs().max())
+            assert err <= 1e-6, err
+
+
 # --------------------------------------------------------------------------- #
 # GMSD / GMS
 # --------------------------------------------------------------------------- #
