@@ -281,6 +281,11 @@ struct Weights {
 // are unconditional.
 constexpr int WIN_PAD = 16, WIN_LEN = 48;
 
+// Row pitch (floats) of the map's LDS staging: 64 columns and 4 of padding,
+// which spreads a wave's writes (rows 4g + i, columns n) and its row reads
+// over distinct banks.
+constexpr int MAP_PITCH = 68;
+
 __device__ inline void stage_window(const float* win, int K, float* sw, int lane) {
   if (lane < WIN_LEN) {
     const int d = lane - WIN_PAD;
@@ -701,7 +706,7 @@ enum { LVL_NONE = 0, LVL_F32 = 1, LVL_F16 = 2, LVL_F32D = 3 };
 template <int SRC, int MODE, int LVL>
 __device__ __attribute__((always_inline)) inline void mf_walk(
     const MfArgs& a, int t, float (&swin)[WAVES_PER_BLOCK][WIN_LEN], double& acc,
-    double& acc_cs, int& plane_out, int& tile_out) {
+    double& acc_cs, int& plane_out, int& tile_out, float* smap = nullptr) {
   constexpr bool PYR = SRC == SRC_F32;  // float32 samples: hi + lo operands
   constexpr bool LEVEL = LVL != LVL_NONE;
   static_assert(!LEVEL || MODE == MF_CS || MODE == MF_CSO, "levels come from the CS pass");
@@ -737,7 +742,10 @@ __device__ __attribute__((always_inline)) inline void mf_walk(
   plane_out = plane;
   tile_out = tile;
 
-  if (c0 < a.Wout) {  // uniform per wave
+  // uniform per wave; the map kernel runs every wave of the workgroup (their
+  // steps meet at a barrier, see the map's stores), a wave past the map with
+  // its loads clamped into the image and its outputs masked
+  if (MODE == MF_MAP || c0 < a.Wout) {
     const int img = plane / a.C;
     const int ch = plane - img * a.C;
     // element pointers of this plane (uint8 samples, or pyramid samples)
@@ -754,14 +762,15 @@ __device__ __attribute__((always_inline)) inline void mf_walk(
     const float k1 = 2.0f * 128.0f * 128.0f + a.C1;
     const Epi e = {k1, a.C2, 256.0f * k1, 256.0f * a.C2};
     const bool col_ok = c0 + n < a.Wout;
-    // MF_MAP: the plane's map and the lane's fixed offset in a block (the host
+    // MF_MAP: the plane's map, and the lane's column in its workgroup's 64
+    // (0x80000000, past every range, where that lies outside the map; the host
     // keeps a plane's map below 2^31 bytes)
     float* const map_plane =
         MODE == MF_MAP ? a.map + static_cast<int64_t>(plane) * a.Hout * a.Wout : nullptr;
     const uint32_t map_row = static_cast<uint32_t>(a.Wout) * 4u;
-    const uint32_t map_lane =
-        col_ok ? static_cast<uint32_t>(4 * g) * map_row + static_cast<uint32_t>(c0 + n) * 4u
-               : 0x80000000u;
+    const int wg_col = strip * WAVES_PER_BLOCK * MT + lane;
+    const uint32_t wg_col_off =
+        wg_col < a.Wout ? static_cast<uint32_t>(wg_col) * 4u : 0x80000000u;
 
     // The pyramid level: a wave's 32-column window pools to 16 columns, its
     // own 8 (c0/2 .. c0/2 + 7) and its right neighbour's 8.  Even waves store
@@ -906,23 +915,36 @@ __device__ __attribute__((always_inline)) inline void mf_walk(
       else
         finish<MODE, false>(e, o, row0, r_end, col_ok, mv, acc, acc_cs);
       if constexpr (MODE == MF_MAP) {
-        // MF_MAP's stores: through a buffer resource whose base is the
-        // block's first map row (scalar) and whose range ends at the chunk's
-        // last row, at the lane's fixed offset of row 4g (0x80000000, past
-        // every range, for lanes whose column lies outside the map), so the
-        // range check drops the rows past the chunk and the columns past the
-        // map.  They sit outside the branch above: every path then issues the
-        // same four stores, and the compiler waits for the next block's loads
-        // alone (vmcnt(4)).  A store on some paths only made it wait for every
-        // store in flight (vmcnt(0)), which exposed the write latency once per
-        // block.
+        // MF_MAP's stores.  A lane holds rows 4g .. 4g+3 of one column, so
+        // stored straight from the fragment each store instruction covers 64
+        // bytes of four rows, most pieces split over two 128-byte lines (map
+        // rows of 7640 bytes at configs[1]); the texture units then spent ~51
+        // cycles per store and were 83 % busy.  Instead the four waves stage
+        // the workgroup's 16 x 64 block in LDS (rows padded to 68 floats:
+        // conflict-free both ways, double-buffered so one barrier per step
+        // suffices) and each wave stores four whole rows, 256 contiguous
+        // bytes per instruction.  The barrier waits for LDS only: a fence
+        // there would wait for the next block's loads in flight.  The stores
+        // go through a buffer resource whose base is the block's first map row
+        // (scalar) and whose range ends at the chunk's last row, so the range
+        // check drops the rows past the chunk (and the 0x80000000 offsets the
+        // columns past the map); they are issued on every path, so the
+        // compiler waits for the next block's loads alone (vmcnt(4)).
         const int rb = r0 + MT * b;
         const auto r = __builtin_amdgcn_make_buffer_rsrc(
             map_plane + static_cast<int64_t>(rb) * a.Wout, 0,
             max(r_end - rb, 0) * static_cast<int>(map_row), MF_RSRC_WORD3);
+        float* stg = smap + (b & 1) * (MT * MAP_PITCH);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(mv[i]), r, map_lane + i * map_row, 0, 0);
+        for (int i = 0; i < 4; ++i) stg[(4 * g + i) * MAP_PITCH + MT * wave + n] = mv[i];
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int row = 4 * wave + k;
+          __builtin_amdgcn_raw_buffer_store_b32(bc<uint32_t>(stg[row * MAP_PITCH + lane]), r,
+                                                static_cast<uint32_t>(row) * map_row + wg_col_off,
+                                                0, 0);
+        }
       }
     };
 
@@ -1000,10 +1022,11 @@ void ssim_mfma_kernel(MfArgs a) {
   static_assert(FIN != FIN_MS || MODE == MF_CSO, "MS-SSIM's words: the cs sums of a scale");
   __shared__ double sred[2 * WAVES_PER_BLOCK];
   __shared__ float swin[WAVES_PER_BLOCK][WIN_LEN];
+  __shared__ float smap[MODE == MF_MAP ? 2 * MT * MAP_PITCH : 1];  // the map's staging
   double acc = 0.0, acc_cs = 0.0;
   int plane = 0, tile = 0;
   mf_walk<SRC, MODE, LVL>(a, static_cast<int>(xcd_tile(blockIdx.x, gridDim.x)), swin, acc,
-                          acc_cs, plane, tile);
+                          acc_cs, plane, tile, smap);
   // packed: each image owns C * tiles consecutive slots, as the finalize reads them
   const int64_t slot = static_cast<int64_t>(plane) * a.tiles + tile;
   if constexpr (MODE == MF_CS) {

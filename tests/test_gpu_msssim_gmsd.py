@@ -287,6 +287,26 @@ def test_cs_coef_scatter_matches_recomputed_backward(gpu, dt, unit_s, need_dy):
             assert err <= 1e-6, err
 
 
+def test_cs_coef_path_falls_back_when_both_means_get_gradients(gpu):
+    """A loss that reads both plane means of a scale made with ``use="cs"``
+    (not MS-SSIM's) gets the recomputing backward: its gradient equals the one
+    of the same loss without ``use``."""
+    from frame_analytics_amd.functional import _NativeSSIM, gaussian_window_1d
+
+    xa, ya = float_pair((1, 2, 64, 72), 0.05, seed=9)
+    win = gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
+    consts = (0.5, (0.01) ** 2, (0.03) ** 2)
+    grads = []
+    for use in ("cs", None):
+        x = torch.from_numpy(xa).to(gpu).requires_grad_(True)
+        y = torch.from_numpy(ya).to(gpu)
+        s, cs, px, _ = _NativeSSIM.apply(x, y, win, consts, "cs+pool", torch.float64, use)
+        (s.sum() + 2.0 * cs.sum() + px.sum()).backward()
+        grads.append(x.grad.double())
+    err = float((grads[0] - grads[1]).abs().max() / grads[1].abs().max())
+    assert err <= 1e-6, err
+
+
 # --------------------------------------------------------------------------- #
 # GMSD / GMS
 # --------------------------------------------------------------------------- #
