@@ -183,6 +183,26 @@ def _ms_call(x, y, weights, k=11, acc=None):
     return o[:n], float(o[n]), ws
 
 
+def test_ms_ssim_three_launch_path_declines_past_its_limits(gpu):
+    """With the accumulator, calls the three-launch path does not take run the
+    per-scale path and give its result bit for bit, leaving the accumulator
+    zero: more than 256 planes (86 RGB images), six scales, and a width whose
+    first level is not a multiple of 8 (360 -> 180)."""
+    from frame_analytics_amd import backend
+
+    acc = torch.zeros(backend._ACC_WORDS["ms"], dtype=torch.int64, device=gpu)
+    cases = [((86, 3, 256, 256), (0.0448, 0.2856, 0.3001, 0.2363, 0.1333)),
+             ((1, 3, 704, 704), (0.1, 0.1, 0.2, 0.2, 0.2, 0.2)),
+             ((2, 3, 352, 360), (0.0448, 0.2856, 0.3001, 0.2363, 0.1333))]
+    for shape, w in cases:
+        a, b = u8_pair(shape, 9.0, seed=shape[0])
+        x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+        per0, tot0, _ = _ms_call(x, y, w)
+        per1, tot1, _ = _ms_call(x, y, w, acc=acc)
+        assert np.array_equal(per0, per1) and tot0 == tot1, shape
+        assert int((acc != 0).sum()) == 0
+
+
 @pytest.mark.parametrize("shape,weights,k,crop", [
     ((3, 3, 517, 512), None, 11, False),
     ((2, 1, 256, 640), (0.3, 0.3, 0.4), 11, False),
