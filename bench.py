@@ -27,7 +27,10 @@ Besides: ``latency_single_frame`` (per-call ms at 512^2 and one 1080p frame,
 beside the reference's RTX 3090 row), ``streaming`` (``StreamingMetrics``
 frames per second at 1080p RGB, host-in and resident) and ``peak_memory_MiB``
 (device memory a call allocates above its inputs, forward and loss step at
-1080p x8) -- the reference's own measurements of this path.
+1080p x8) -- the reference's own measurements of this path.  The MS-SSIM loss
+step is timed and measured twice: as shipped (the training forward keeps the
+backward's coefficient maps) and with FA_MS_SSIM_RECOMPUTE=1 (recomputed in the
+backward, the reference's memory profile).
 
 ``cpu_baseline`` times the reference's own CPU kernels (oracle/_ref, compiled
 from the reference sources) on a bounded sample of the same workload, on all
@@ -553,6 +556,13 @@ def memory_legs(torch, fa, dev):
         "ssim": peak(step(lambda: 1.0 - fa.ssim(x, y, data_range=1.0)), drop_grad),
         "ms_ssim": peak(step(lambda: 1.0 - fa.ms_ssim(x, y, data_range=1.0)), drop_grad),
     }
+    # with the coefficient maps recomputed in the backward (FA_MS_SSIM_RECOMPUTE=1)
+    os.environ["FA_MS_SSIM_RECOMPUTE"] = "1"
+    try:
+        res["loss_step"]["ms_ssim_recompute"] = peak(
+            step(lambda: 1.0 - fa.ms_ssim(x, y, data_range=1.0)), drop_grad)
+    finally:
+        os.environ.pop("FA_MS_SSIM_RECOMPUTE", None)
     res["reference_rtx3090_MiB"] = {"forward": {"ssim": 0.19, "ms_ssim": 120, "gmsd": 0.19,
                                                 "psnr": 0.007},
                                     "loss_step": {"ssim": 752, "ms_ssim": 942}}
@@ -670,6 +680,14 @@ def main():
     _clock_warmup(torch, msssim_loss_step, LEG_WARMUP_S)
     c4["ms_ssim_loss_fwd_bwd_fp32_ms"] = round(
         _leg_ms(torch, msssim_loss_step, lreps, 2), 3)
+    # the same step with the coefficient maps recomputed in the backward (the
+    # reference's memory profile, FA_MS_SSIM_RECOMPUTE=1)
+    os.environ["FA_MS_SSIM_RECOMPUTE"] = "1"
+    try:
+        c4["ms_ssim_loss_fwd_bwd_fp32_recompute_ms"] = round(
+            _leg_ms(torch, msssim_loss_step, lreps, 2), 3)
+    finally:
+        os.environ.pop("FA_MS_SSIM_RECOMPUTE", None)
     del xl, yl
     # the reference's published RTX 3090 figures for the same calls (its README)
     c4["reference_rtx3090_ms"] = {"ms_ssim": 3.088, "gmsd": 0.313, "l1": 0.115,

@@ -729,6 +729,14 @@ def ssim_cs_backward(x, y, gs, gcs, win, shift, C1, C2, need_dx, need_dy,
     return dx, dy
 
 
+def ms_ssim_keeps_coefficients() -> bool:
+    """Whether MS-SSIM's training forward writes the backward's coefficient
+    maps and keeps them until the backward (faster; peak memory one set of
+    float32 maps per scale higher).  ``FA_MS_SSIM_RECOMPUTE=1`` recomputes
+    them in the backward instead, as the reference does."""
+    return os.environ.get("FA_MS_SSIM_RECOMPUTE", "0").lower() not in ("1", "on", "true", "yes")
+
+
 def ssim_cs_coef_forward(x, y, win, shift, C1, C2, unit_s, pool_dtype, need_dy):
     """A training step's CS pass in float64 (``fa_gpu_ssim_cs_coef``): the
     plane means ``(s, cs)``, the next pyramid level when ``pool_dtype`` is

@@ -603,11 +603,13 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
             last = i == scales - 1
             if grad:
                 # the loss reads the SSIM means at the coarsest scale, cs below
+                keep = backend.ms_ssim_keeps_coefficients()
                 if last:
-                    s, cs = _NativeSSIM.apply(cx, cy, win32, consts, "cs", None, "s")
+                    s, cs = _NativeSSIM.apply(cx, cy, win32, consts, "cs", None,
+                                              "s" if keep else None)
                 else:
                     s, cs, cx, cy = _NativeSSIM.apply(cx, cy, win32, consts, "cs+pool", pdt,
-                                                      "cs")
+                                                      "cs" if keep else None)
             else:
                 out = backend.ssim_cs_pool(cx, cy, win32, shift, C1, C2,
                                            None if last else pdt, luma=lw if i == 0 else None)

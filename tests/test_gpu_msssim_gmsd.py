@@ -245,12 +245,16 @@ def test_ms_ssim_three_launch_path(gpu, shape, weights, k, crop):
     assert np.all(np.abs(per - want) <= REL * np.abs(want)), (per, want)
 
 
+@pytest.mark.parametrize("recompute", ["0", "1"])
 @pytest.mark.parametrize("shape", [(1, 1, 192, 192), (2, 3, 180, 200)])
 @pytest.mark.parametrize("wrt", [("x",), ("x", "y")])
-def test_ms_ssim_backward_matches_oracle(gpu, shape, wrt):
+def test_ms_ssim_backward_matches_oracle(gpu, shape, wrt, recompute, monkeypatch):
     """dL/dx and dL/dy of 1 - ms_ssim against the oracle's closed-form float64
     MS-SSIM adjoint (oracle.ms_ssim_grad, itself pinned by central differences
-    of the float64 forward), 1e-6 max-normwise."""
+    of the float64 forward), 1e-6 max-normwise: with the coefficient maps
+    written by the forward (the default) and recomputed in the backward
+    (FA_MS_SSIM_RECOMPUTE=1)."""
+    monkeypatch.setenv("FA_MS_SSIM_RECOMPUTE", recompute)
     xa, ya = float_pair(shape, 0.05, seed=shape[-1])
     x = torch.from_numpy(xa).to(gpu).requires_grad_("x" in wrt)
     y = torch.from_numpy(ya).to(gpu).requires_grad_("y" in wrt)
