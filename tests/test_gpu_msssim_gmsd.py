@@ -183,6 +183,30 @@ def _ms_call(x, y, weights, k=11, acc=None):
     return o[:n], float(o[n]), ws
 
 
+def test_ms_ssim_three_launch_path_at_256_planes(gpu):
+    """The three-launch path at its plane limit (256 planes: every slot of the
+    final workgroup's term array in use), against the per-scale path to 1e-12
+    and two of its images against the oracle."""
+    from frame_analytics_amd import backend
+    from frame_analytics_amd.functional import MS_SSIM_WEIGHTS
+
+    a, b = u8_pair((256, 1, 256, 256), 9.0, seed=256)
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    w = tuple(MS_SSIM_WEIGHTS)
+    acc = torch.zeros(backend._ACC_WORDS["ms"], dtype=torch.int64, device=gpu)
+    per0, tot0, _ = _ms_call(x, y, w)
+    per, tot, ws = _ms_call(x, y, w, acc=acc)
+    scratch = len(w) * 256 * 8
+    start = -((scratch + 255) // 256 * 256)
+    assert bool((ws[start:start + scratch] == 0xFF).all())  # the three-launch path ran
+    assert int((acc != 0).sum()) == 0
+    assert np.all(np.abs(per - per0) <= 1e-12 * np.abs(per0))
+    assert abs(tot - tot0) <= 1e-12 * abs(tot0)
+    for i in (0, 255):
+        want = ref.ms_ssim(a[i:i + 1].astype(np.float64), b[i:i + 1].astype(np.float64), 255.0)
+        assert _rel(float(per[i]), float(want)) <= REL, (i, per[i], want)
+
+
 def test_ms_ssim_three_launch_path_declines_past_its_limits(gpu):
     """With the accumulator, calls the three-launch path does not take run the
     per-scale path and give its result bit for bit, leaving the accumulator
