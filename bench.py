@@ -319,8 +319,9 @@ def profile_sequence(launches=20):
     a torch copy of exactly 256 MiB (the FETCH_SIZE / WRITE_SIZE calibration:
     256 MiB read, 256 MiB written), then `launches` launches each of the SSIM
     kernel (configs[1]; the one-launch mean, then with the float32 map), the
-    GMSD kernel (configs[4], one launch) and the PSNR pixel kernel (configs[2],
-    one launch), through the C ABI, rotating resident input pairs."""
+    GMSD kernel (configs[4], one launch), MS-SSIM (configs[4], three launches)
+    and the PSNR pixel kernel (configs[2], one launch), through the C ABI,
+    rotating resident input pairs."""
     import torch
 
     import frame_analytics_amd as fa
@@ -374,7 +375,22 @@ def profile_sequence(launches=20):
                                     gacc.data_ptr(), gm.data_ptr(), gs.data_ptr(), None, 0,
                                     stream) == 0
     torch.cuda.synchronize()
-    del pairs, partial, ps, ps2
+    # MS-SSIM (configs[4], 5 scales: the three-launch form with the stream's
+    # accumulator, fa.ms_ssim's inference call) on the same pairs
+    from frame_analytics_amd.functional import MS_SSIM_WEIGHTS
+
+    mbytes = backend._ms_workspace_bytes(0, n, c, h, w, 11, 5, False)
+    mws = torch.empty(mbytes, dtype=torch.uint8, device=dev)
+    macc = torch.zeros(backend._ACC_WORDS["ms"], dtype=torch.int64, device=dev)
+    wts = (ctypes.c_double * 5)(*MS_SSIM_WEIGHTS)
+    for i in range(launches):
+        a, b = pairs[i % 4]
+        assert lib.fa_gpu_ms_ssim(a.data_ptr(), b.data_ptr(), 0, n, c, h, w, None, None, None,
+                                  win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2,
+                                  (0.03 * 255) ** 2, wts, 5, mws.data_ptr(), mbytes,
+                                  macc.data_ptr(), None, tot.data_ptr(), 0, stream) == 0
+    torch.cuda.synchronize()
+    del pairs, partial, ps, ps2, mws
 
     ppairs = _pairs(torch, PSNR_SHAPE, 4.0, 2, dev, seed=2)
     pn = PSNR_SHAPE[0]
