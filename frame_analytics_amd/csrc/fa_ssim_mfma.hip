@@ -1289,7 +1289,9 @@ MfArgs args_of(const SsimMfmaCall& c) {
 // become 24,24,10,9: 82.1 against 84.3 us per call over rotated input pairs,
 // the same work and workgroup count).  It needs each XCD's range of tiles to
 // hold whole planes (the count of planes a multiple of 8); walked plane by
-// plane instead it measured slower.
+// plane instead it measured slower.  A launch that fits one round of
+// resident workgroups has no drain to shorten -- every chunk starts at once
+// and the longest sets the time -- so it keeps uniform chunks.
 bool plan_tiles(MfArgs& a, int64_t planes, int64_t resident, int64_t max_tiles,
                 bool big_small) {
   const int strips = (a.Wout + WAVES_PER_BLOCK * MT - 1) / (WAVES_PER_BLOCK * MT);
@@ -1314,7 +1316,8 @@ bool plan_tiles(MfArgs& a, int64_t planes, int64_t resident, int64_t max_tiles,
   a.nbig = best_chunks;
   a.THs = best_th;
   a.xcd_planes = 0;
-  if (big_small && best_chunks >= 2 && planes % NUM_XCD == 0) {
+  if (big_small && best_chunks >= 2 && planes % NUM_XCD == 0 &&
+      planes * strips * best_chunks > resident) {
     const int nb = (best_chunks + 1) / 2;
     const int ns = best_chunks - nb;
     const int big = static_cast<int>(std::lround(blocks / (nb + 0.4 * ns)));
