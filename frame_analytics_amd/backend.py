@@ -241,14 +241,33 @@ def call_gpu(name: str, *args) -> int:
     return int(code)
 
 
-def _run_or_needs_workspace(name: str, args_without, args_with) -> None:
+_FA_E_ARG = 5  # include/fa_abi.h: a refusal made before anything was launched
+
+
+def _run_or_needs_workspace(name: str, args_without, args_with, acc=None) -> None:
     """Call a one-launch entry point without its workspace first (it is not
     read where the call finishes in its launch); when the library answers
     FA_E_ARG -- it refuses before launching anything -- call it again with the
-    workspace that ``args_with()`` allocates."""
-    if call_gpu(name, *args_without) == 0:
+    workspace that ``args_with()`` allocates.  Any other failure raises, and
+    drops the stream's accumulator ``acc`` (:func:`_forget_acc`)."""
+    code = call_gpu(name, *args_without)
+    if code == 0:
         return
-    _run(name, *args_with())
+    if code == _FA_E_ARG:
+        code = call_gpu(name, *args_with())
+        if code == 0:
+            return
+    _forget_acc(acc)
+    raise KernelError(f"{name}: " + status_text(code, _ext.gpu if _ext else None))
+
+
+def _run_acc(name: str, acc, *args) -> None:
+    """:func:`_run` for a call handed the stream's accumulator ``acc``: a
+    failure drops it (:func:`_forget_acc`) before raising."""
+    code = call_gpu(name, *args)
+    if code:
+        _forget_acc(acc)
+        raise KernelError(f"{name}: " + status_text(code, _ext.gpu if _ext else None))
 
 
 def _run(name: str, *args) -> None:
@@ -357,6 +376,18 @@ def _acc_for(kind: str, device: torch.device, dev: int, stream: int) -> Optional
     return acc
 
 
+def _forget_acc(acc: Optional[torch.Tensor]) -> None:
+    """Drop a stream's accumulator after a call that failed with it: a call
+    that stopped between two of its launches (MS-SSIM makes three) can leave
+    words of it non-zero, and every later call on the stream counts from zero.
+    The next call allocates a new, zeroed one."""
+    if acc is None:
+        return
+    for key, t in list(_stream_acc.items()):
+        if t is acc:
+            del _stream_acc[key]
+
+
 def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
               param: float, per_image: bool, psnr_bias: float,
               luma: Optional[tuple] = None) -> torch.Tensor:
@@ -386,7 +417,7 @@ def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,
             _run("fa_gpu_pixel_reduce_once", *args(_ptr(_f64(x.device, n, bpi))))
         else:
             _run_or_needs_workspace("fa_gpu_pixel_reduce_once", args(None),
-                                    lambda: args(_ptr(_f64(x.device, n, bpi))))
+                                    lambda: args(_ptr(_f64(x.device, n, bpi))), acc)
     else:
         partial = _f64(x.device, n, bpi)
         _run("fa_gpu_pixel_reduce_ex", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w,
@@ -604,7 +635,7 @@ def _ssim_native(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: floa
             _run("fa_gpu_ssim_once", *args(_ptr(_f64(x.device, planes, bpp))))
         else:
             _run_or_needs_workspace("fa_gpu_ssim_once", args(None),
-                                    lambda: args(_ptr(_f64(x.device, planes, bpp))))
+                                    lambda: args(_ptr(_f64(x.device, planes, bpp))), acc)
         return per_image if reduction == "none" else total
     partial = _ptr(_f64(x.device, planes, bpp))
     if luma is None and xs is None and ys is None:
@@ -933,7 +964,7 @@ def _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, w
         _run("fa_gpu_gmsd_once", *args(workspaces()))
     else:
         _run_or_needs_workspace("fa_gpu_gmsd_once", args((None, None)),
-                                lambda: args(workspaces()))
+                                lambda: args(workspaces()), acc)
     return mean, std, batch
 
 
@@ -1000,10 +1031,10 @@ def ms_ssim_fused(x, y, win, shift, C1, C2, weights, luma=None, per_image=False)
     dev, stream = _site(x)
     acc = _acc_for("ms", x.device, dev, stream) if x.dtype == torch.uint8 and luma is None \
         else None
-    _run("fa_gpu_ms_ssim", _ptr(x), _ptr(y), code, n, c, h, w, xs, ys, _luma_arg(luma),
-         _ptr(win), k, float(shift), float(C1), float(C2), wts, m, _ptr(ws), nbytes,
-         _ptr(acc) if acc is not None else None, _ptr(out) if per_image else None,
-         None if per_image else _ptr(out), dev, stream)
+    _run_acc("fa_gpu_ms_ssim", acc, _ptr(x), _ptr(y), code, n, c, h, w, xs, ys,
+             _luma_arg(luma), _ptr(win), k, float(shift), float(C1), float(C2), wts, m,
+             _ptr(ws), nbytes, _ptr(acc) if acc is not None else None,
+             _ptr(out) if per_image else None, None if per_image else _ptr(out), dev, stream)
     return out
 
 

@@ -169,3 +169,43 @@ def test_declined_kernel_warns_once_and_falls_back(monkeypatch):
     with warnings.catch_warnings():
         warnings.simplefilter("error")
         assert abs(float(fa.mse(x, y)) - float(want)) < 1e-9  # warned once only
+
+
+def test_failed_one_launch_call_drops_the_stream_accumulator(monkeypatch):
+    """A one-launch call keeps its stream's accumulator zero between calls;
+    one that fails may have stopped between launches (MS-SSIM makes three),
+    so the backend drops that accumulator and the next call starts on a new
+    one.  FA_E_ARG (refused before any launch) retries with the workspace and
+    keeps it.  No kernel runs: the library calls are replaced."""
+    from frame_analytics_amd import backend
+
+    acc = torch.zeros(8, dtype=torch.int64)
+    key = ("ms", 0, 12345)
+    monkeypatch.setattr(backend, "_stream_acc", {key: acc})
+    codes = []
+    monkeypatch.setattr(backend, "call_gpu", lambda name, *args: codes.pop(0))
+
+    codes[:] = [5, 0]  # refused without the workspace, done with it
+    backend._run_or_needs_workspace("fa_gpu_ssim_once", (), lambda: (), acc)
+    assert backend._stream_acc.get(key) is acc and not codes
+
+    codes[:] = [5, 6]  # refused, then failed with the workspace
+    with pytest.raises(backend.KernelError):
+        backend._run_or_needs_workspace("fa_gpu_ssim_once", (), lambda: (), acc)
+    assert key not in backend._stream_acc and not codes
+
+    backend._stream_acc[key] = acc
+    codes[:] = [6]  # failed outright: no retry
+    with pytest.raises(backend.KernelError):
+        backend._run_or_needs_workspace("fa_gpu_ssim_once", (), lambda: (), acc)
+    assert key not in backend._stream_acc and not codes
+
+    backend._stream_acc[key] = acc
+    codes[:] = [6]
+    with pytest.raises(backend.KernelError):
+        backend._run_acc("fa_gpu_ms_ssim", acc)
+    assert key not in backend._stream_acc
+    codes[:] = [0]
+    backend._stream_acc[key] = acc
+    backend._run_acc("fa_gpu_ms_ssim", acc)
+    assert backend._stream_acc.get(key) is acc
