@@ -391,7 +391,9 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials,
  * workgroup finishes the reduction from per-(scale, plane) fixed-point sums
  * (about 1e-13 relative from the float64 reduction, the same bits run to run).
  * Other calls ignore acc.  `acc` is state of one stream: calls that overlap
- * on it (two streams, graph replays beside eager calls) race.
+ * on it (two streams, graph replays beside eager calls) race.  After a
+ * non-zero status its contents are unknown (a failure between the launches
+ * leaves words set): zero it again before the next call.
  */
 #define FA_MS_SSIM_ACC_WORDS ((8 * 256 + 1) * 16)
 FA_API int fa_gpu_ms_ssim_workspace(int dtype, int N, int C, int H, int W, int K, int M,
