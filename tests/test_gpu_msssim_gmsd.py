@@ -772,3 +772,44 @@ def test_gmsd_one_launch_without_workspace(gpu):
         else:
             assert rc == 5 and bool((out == -7.0).all()), rc
         assert not bool(acc.any())
+
+
+def test_one_launch_finishes_on_two_streams(gpu):
+    """fa.ssim, fa.gmsd and fa.ms_ssim (uint8: the one-launch SSIM and GMSD
+    forms, MS-SSIM's three launches) interleaved on two streams: each stream
+    has its own accumulator, so every value matches the same call made alone
+    on the default stream bit for bit (the fixed-point sums do not depend on
+    the order), and both streams' accumulators are zero afterwards."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((2, 3, 256, 384), 6.0, seed=41)
+    c, d = u8_pair((1, 3, 320, 512), 9.0, seed=42)
+    ta, tb, tc, td = (torch.from_numpy(v).to(gpu) for v in (a, b, c, d))
+    calls = {
+        "ssim": lambda x, y: fa.ssim(x, y, data_range=255.0, reduction="none"),
+        "gmsd": lambda x, y: fa.gmsd(x, y, data_range=255.0, reduction="none"),
+        "ms_ssim": lambda x, y: fa.ms_ssim(x, y, data_range=255.0, reduction="none"),
+    }
+    alone = {(k, p): f(*xy).cpu() for k, f in calls.items()
+             for p, xy in (("ab", (ta, tb)), ("cd", (tc, td)))}
+    # the values are the oracle's too (MS-SSIM's three-launch sums: 1e-12)
+    assert np.allclose(alone["ms_ssim", "ab"].numpy(), ref.ms_ssim(a, b, 255.0, reduction="none"),
+                       rtol=REL, atol=0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(3):
+        for k, f in calls.items():
+            with torch.cuda.stream(s1):
+                outs.append((k, "ab", f(ta, tb)))
+            with torch.cuda.stream(s2):
+                outs.append((k, "cd", f(tc, td)))
+    torch.cuda.synchronize()
+    for k, p, o in outs:
+        assert torch.equal(o.cpu(), alone[k, p]), (k, p)
+    kinds = {"ssim", "gmsd", "ms"}
+    keys = [key for key in backend._stream_acc
+            if key[0] in kinds and key[2] in (s1.cuda_stream, s2.cuda_stream)]
+    assert len(keys) == 6, keys
+    for key in keys:
+        assert not bool(backend._stream_acc[key].any()), key
