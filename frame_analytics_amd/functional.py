@@ -502,11 +502,50 @@ def _scale_exponents(weights: Tuple[float, ...], device: str) -> torch.Tensor:
     return torch.tensor(weights, dtype=torch.float64).view(-1, 1, 1).to(torch.device(device))
 
 
+@functools.lru_cache(maxsize=16)
+def _cofactor_mask(m: int, device: str) -> torch.Tensor:
+    """``(m, m, 1, 1)`` bool, true on the diagonal: row k masks factor k."""
+    return torch.eye(m, dtype=torch.bool).view(m, m, 1, 1).to(torch.device(device))
+
+
+class _CombineScales(torch.autograd.Function):
+    """The product of :func:`_combine_scales` with a backward that never waits
+    for the host.  torch's ``prod`` backward counts the zero factors with a
+    device-to-host read, so a training step would stop there until the device
+    caught up and issue every later launch of its backward behind the host;
+    here each factor's gradient takes the product of the other factors (a
+    masked product, exact where factors are zero) and the derivatives of the
+    clamp and the power as torch forms them: no gradient where t < 0 or the
+    exponent is 0, inf for a zero factor under a fractional exponent.  The
+    backward recomputes from the saved input, so its operations differentiate
+    again under ``create_graph``."""
+
+    @staticmethod
+    def forward(ctx, stacked, expo):
+        ctx.save_for_backward(stacked, expo)
+        return stacked.clamp_min(0.0).pow(expo).prod(dim=0)
+
+    @staticmethod
+    def backward(ctx, g):
+        stacked, expo = ctx.saved_tensors
+        t = stacked.clamp_min(0.0)
+        p = t.pow(expo)
+        m = p.shape[0]
+        others = p.unsqueeze(0).expand(m, *p.shape).masked_fill(
+            _cofactor_mask(m, str(p.device)), 1.0).prod(dim=1)
+        dpow = torch.where(expo == 0.0, 0.0, expo * t.pow(expo - 1.0))
+        grad = torch.where(stacked >= 0.0, (g * others) * dpow, 0.0)
+        return grad.to(stacked.dtype), None
+
+
 def _combine_scales(terms, weights, device) -> torch.Tensor:
     """Per plane: prod_j max(t_j, 0)^w_j over the stacked ``(N, C)`` terms (a
     fractional power of a negative factor is not real, hence the clamp)."""
-    stacked = torch.stack(terms).clamp_min(0.0)
-    return stacked.pow(_scale_exponents(tuple(weights), str(device))).prod(dim=0)
+    expo = _scale_exponents(tuple(weights), str(device))
+    stacked = torch.stack(terms)
+    if torch.is_grad_enabled() and stacked.requires_grad:
+        return _CombineScales.apply(stacked, expo)
+    return stacked.clamp_min(0.0).pow(expo).prod(dim=0)
 
 
 def _ssim_cs_pair(x4, y4, win, wdt, shift, C1, C2, backend_hint):

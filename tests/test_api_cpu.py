@@ -209,3 +209,50 @@ def test_failed_one_launch_call_drops_the_stream_accumulator(monkeypatch):
     backend._stream_acc[key] = acc
     backend._run_acc("fa_gpu_ms_ssim", acc)
     assert backend._stream_acc.get(key) is acc
+
+
+def test_scale_product_gradient_matches_torch_autograd():
+    """MS-SSIM's scale product (clamp at zero, power, product over the scales)
+    differentiated without the host read torch's prod backward makes: the
+    same gradient as torch's autograd of the plain expression, including
+    negative, zero and NaN terms, zero exponents and a zero factor under a
+    fractional exponent (inf), and again under create_graph."""
+    from frame_analytics_amd.functional import _CombineScales
+
+    g = torch.Generator().manual_seed(5)
+    base = torch.rand((5, 3, 4), generator=g, dtype=torch.float64) * 1.2 - 0.1
+    base[0, 0, 0] = 0.0          # a zero factor, fractional exponent: inf
+    base[1, 1, 1] = -0.3         # clamped: no gradient through it
+    base[2, 2, 2] = float("nan")
+    base[3, 0, 3] = 0.0
+    for expo_v in ((0.0448, 0.2856, 0.3001, 0.2363, 0.1333), (0.5, 0.0, 1.0, 2.0, 0.25)):
+        expo = torch.tensor(expo_v, dtype=torch.float64).view(-1, 1, 1)
+        upstream = torch.rand((3, 4), generator=g, dtype=torch.float64)
+        a = base.clone().requires_grad_(True)
+        b = base.clone().requires_grad_(True)
+        want_v = a.clamp_min(0.0).pow(expo).prod(dim=0)
+        got_v = _CombineScales.apply(b, expo)
+        assert torch.equal(torch.nan_to_num(got_v, nan=-7.0), torch.nan_to_num(want_v, nan=-7.0))
+        (want,) = torch.autograd.grad(want_v, a, upstream)
+        (got,) = torch.autograd.grad(got_v, b, upstream)
+        assert torch.equal(torch.isnan(got), torch.isnan(want))
+        assert torch.equal(torch.isinf(got), torch.isinf(want))
+        fin = torch.isfinite(want)
+        assert torch.allclose(got[fin], want[fin], rtol=1e-14, atol=0)
+    # float32 terms: the gradient comes back float32, like the input
+    a32 = base.abs().float().clamp_min(0.01).requires_grad_(True)
+    expo = torch.tensor(MS_W, dtype=torch.float64).view(-1, 1, 1)
+    (g32,) = torch.autograd.grad(_CombineScales.apply(a32, expo).sum(), a32)
+    assert g32.dtype == torch.float32
+    # second derivative, on strictly positive terms (finite everywhere)
+    pos = (base.abs() + 0.05).nan_to_num(0.5)
+    a = pos.clone().requires_grad_(True)
+    b = pos.clone().requires_grad_(True)
+    (ga,) = torch.autograd.grad(a.clamp_min(0.0).pow(expo).prod(dim=0).sum(), a, create_graph=True)
+    (gb,) = torch.autograd.grad(_CombineScales.apply(b, expo).sum(), b, create_graph=True)
+    (ha,) = torch.autograd.grad((ga * ga).sum(), a)
+    (hb,) = torch.autograd.grad((gb * gb).sum(), b)
+    assert torch.allclose(hb, ha, rtol=1e-12, atol=0)
+
+
+MS_W = (0.0448, 0.2856, 0.3001, 0.2363, 0.1333)
