@@ -63,6 +63,8 @@ SIGNATURES = {
     "fa_gpu_gmsd_backward":
         ([_P, _P, _I, _I, _I, _I, _I, _D, _D, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P], _I),
     "fa_gpu_ms_ssim_reduce": ([_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _P], _I),
+    "fa_gpu_ms_ssim_head": ([_P, _I, _I, _I, _P, _P, _P, _I, _P], _I),
+    "fa_gpu_ms_ssim_head_backward": ([_P, _I, _I, _I, _P, _P, _P, _P, _I, _P], _I),
     "fa_gpu_ssim_noalloc":
         ([_P, _P, _I, _I, _I, _I, _I, _P, _I, _D, _D, _D, _P, _P, _P, _I, _P], _I),
     "fa_gpu_pixel_reduce_once":

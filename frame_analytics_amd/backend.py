@@ -803,7 +803,7 @@ def ssim_cs_scatter(x, y, g, aux, win, shift, need_dx, need_dy, gpx=None, gpy=No
     x, y, win = _contig(x), _contig(y), _win32(win)
     n, c, h, w = (int(v) for v in x.shape)
     k = int(win.numel())
-    gf = g.to(torch.float32).contiguous().reshape(-1)
+    gf = _contig(g.to(torch.float64)).reshape(-1)
     dx = torch.empty_like(x) if need_dx else None
     dy = torch.empty_like(y) if need_dy else None
     gpx = _contig(gpx) if (gpx is not None and need_dx) else None
@@ -1036,6 +1036,46 @@ def ms_ssim_fused(x, y, win, shift, C1, C2, weights, luma=None, per_image=False)
              _ptr(ws), nbytes, _ptr(acc) if acc is not None else None,
              _ptr(out) if per_image else None, None if per_image else _ptr(out), dev, stream)
     return out
+
+
+def ms_head_available(terms) -> bool:
+    """Can ``fa_gpu_ms_ssim_head`` combine these ``(N, C)`` plane means?"""
+    t0 = terms[0]
+    return (0 < len(terms) <= 8 and t0.is_cuda and t0.dim() == 2
+            and all(t.dtype == torch.float64 and t.is_contiguous() and t.shape == t0.shape
+                    and t.device == t0.device for t in terms)
+            and _gpu_ext(t0) is not None)
+
+
+def ms_head(terms, weights, per_image: bool) -> torch.Tensor:
+    """MS-SSIM's head over formed plane means (``fa_gpu_ms_ssim_head``): the
+    per-image values ``(N,)`` or their batch mean (a 0-d tensor)."""
+    m = len(terms)
+    n, c = (int(v) for v in terms[0].shape)
+    ptrs = (ctypes.c_void_p * m)(*[t.data_ptr() for t in terms])
+    wts = (ctypes.c_double * m)(*[float(v) for v in weights])
+    out = _f64(terms[0].device, n) if per_image else _f64(terms[0].device)
+    dev, stream = _site(terms[0])
+    _run("fa_gpu_ms_ssim_head", ptrs, m, n, c, wts, _ptr(out) if per_image else None,
+         None if per_image else _ptr(out), dev, stream)
+    return out
+
+
+def ms_head_backward(terms, weights, per_image: bool, g, needs):
+    """Each scale's gradient of its plane means from the upstream gradient
+    ``g`` of :func:`ms_head`'s output (``fa_gpu_ms_ssim_head_backward``); None
+    where ``needs`` says no."""
+    m = len(terms)
+    n, c = (int(v) for v in terms[0].shape)
+    g = _contig(g.to(torch.float64))
+    grads = [torch.empty_like(t) if need else None for t, need in zip(terms, needs)]
+    ptrs = (ctypes.c_void_p * m)(*[t.data_ptr() for t in terms])
+    gptrs = (ctypes.c_void_p * m)(*[_ptr(v) for v in grads])
+    wts = (ctypes.c_double * m)(*[float(v) for v in weights])
+    dev, stream = _site(terms[0])
+    _run("fa_gpu_ms_ssim_head_backward", ptrs, m, n, c, wts, _ptr(g) if per_image else None,
+         None if per_image else _ptr(g), gptrs, dev, stream)
+    return grads
 
 
 def ms_ssim_reduce(partials, slots, npix, weights, n: int, c: int, per_image: bool):

@@ -508,7 +508,7 @@ struct ScatterArgs {
   const void* gpx;  // optional gradient of the next pyramid level (2x2 means)
   const void* gpy;
   int gp_f64;       // its element type: float64 (1) or float32 (0)
-  const float* gscale;  // optional per-plane factor of the coefficient maps'
+  const double* gscale;  // optional per-plane factor of the coefficient maps'
                         // share (maps written by MODE_CSF for a unit gradient)
 };
 
@@ -686,7 +686,7 @@ __global__ __launch_bounds__(BLOCK) void scatter_kernel(ScatterArgs a) {
   pol.gpy = a.gpy;
   pol.gp_f64 = a.gp_f64 != 0;
   // x * 1.0 is x: without gscale the results are those of the plain scatter
-  pol.gmul = a.gscale ? static_cast<double>(a.gscale[plane]) : 1.0;
+  pol.gmul = a.gscale ? a.gscale[plane] : 1.0;
   pol.Hp = a.H / 2;
   pol.Wp = a.W / 2;
   pol.gp_off = static_cast<int64_t>(plane) * pol.Hp * pol.Wp;
@@ -773,6 +773,80 @@ __global__ __launch_bounds__(BLOCK) void ms_finish_kernel(int M, int N, int C,
   }
   tot = block_sum(tot, smem);
   if (threadIdx.x == 0 && out_total) *out_total = tot / static_cast<double>(N);
+}
+
+// MS-SSIM's head over plane means that are already formed (the training
+// path, where each scale's means are outputs of its own pass): per plane the
+// product over the scales of max(t_m, 0)^w_m, the mean over the C channels of
+// each image and the batch mean (fa_gpu_ms_ssim_head), and the gradient of
+// every scale's plane means from the upstream gradient of either mean
+// (fa_gpu_ms_ssim_head_backward).  The clamp and the power differentiate as
+// torch's clamp_min and pow do (reference functional.py:897-901 combines the
+// scales with them): no gradient where t < 0 (or t is NaN) or w = 0, and
+// w * 0^(w - 1) = inf for a zero factor under a fractional weight.
+struct MsHead {
+  const double* t[MS_MAX_SCALES];  // scale m's plane means, N * C each
+  double w[MS_MAX_SCALES];
+  int M, N, C;
+};
+
+struct MsHeadGrads {
+  double* g[MS_MAX_SCALES];  // scale m's gradient, N * C (null: not wanted)
+};
+
+__device__ inline double ms_clamp0(double v) { return (v != v) ? v : (v > 0.0 ? v : 0.0); }
+
+__global__ __launch_bounds__(BLOCK) void ms_head_kernel(MsHead h,
+                                                        double* __restrict__ out_per_image,
+                                                        double* __restrict__ out_total) {
+  __shared__ double smem[WAVES_PER_BLOCK];
+  double tot = 0.0;
+  for (int n = threadIdx.x; n < h.N; n += BLOCK) {
+    double img = 0.0;
+    for (int c = 0; c < h.C; ++c) {
+      const int64_t p = static_cast<int64_t>(n) * h.C + c;
+      double prod = 1.0;
+#pragma unroll
+      for (int m = 0; m < MS_MAX_SCALES; ++m)
+        if (m < h.M) prod *= pow(ms_clamp0(h.t[m][p]), h.w[m]);
+      img += prod;
+    }
+    img /= static_cast<double>(h.C);
+    if (out_per_image) out_per_image[n] = img;
+    tot += img;
+  }
+  tot = block_sum(tot, smem);
+  if (threadIdx.x == 0 && out_total) *out_total = tot / static_cast<double>(h.N);
+}
+
+// One thread per plane.  g_per_image (N) or g_total (1): the upstream gradient
+// of the per-image values or of the batch mean.
+__global__ __launch_bounds__(BLOCK) void ms_head_backward_kernel(
+    MsHead h, const double* __restrict__ g_per_image, const double* __restrict__ g_total,
+    MsHeadGrads out) {
+  const int64_t planes = static_cast<int64_t>(h.N) * h.C;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * BLOCK + threadIdx.x;
+  if (p >= planes) return;
+  const int n = static_cast<int>(p / h.C);
+  // the means' backward: 1 / N, then 1 / C, as torch's mean backward divides
+  const double gi = g_per_image ? g_per_image[n] : g_total[0] / static_cast<double>(h.N);
+  const double gp = gi / static_cast<double>(h.C);
+  double t[MS_MAX_SCALES], f[MS_MAX_SCALES];
+#pragma unroll
+  for (int m = 0; m < MS_MAX_SCALES; ++m) {
+    t[m] = m < h.M ? h.t[m][p] : 1.0;
+    f[m] = m < h.M ? pow(ms_clamp0(t[m]), h.w[m]) : 1.0;
+  }
+#pragma unroll
+  for (int m = 0; m < MS_MAX_SCALES; ++m) {
+    if (m >= h.M || !out.g[m]) continue;
+    double others = 1.0;  // the product of the other factors, exact where some are zero
+#pragma unroll
+    for (int k = 0; k < MS_MAX_SCALES; ++k)
+      if (k != m) others *= f[k];
+    const double dpow = h.w[m] == 0.0 ? 0.0 : h.w[m] * pow(ms_clamp0(t[m]), h.w[m] - 1.0);
+    out.g[m][p] = t[m] >= 0.0 ? (gp * others) * dpow : 0.0;
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -916,7 +990,7 @@ static int set_views(SsimArgs& a, int C, int H, int W, const int64_t* xs, const 
 // N * C * Hout * Wout float32) onto dx / dy, optionally scaled per plane by
 // gscale, plus a quarter of the pyramid level's gradient over each 2x2 block.
 template <typename T>
-static int scatter_impl(const T* x, const T* y, const float* gscale, const float* win, int K,
+static int scatter_impl(const T* x, const T* y, const double* gscale, const float* win, int K,
                         int N, int C, int H, int W, double shift, const float* aux, bool aux_dy,
                         const void* gpx, const void* gpy, int gp_dtype, T* dx, T* dy,
                         int device, hipStream_t st) {
@@ -1500,7 +1574,7 @@ FA_API int fa_gpu_ssim_cs_coef(const void* x, const void* y, int dtype, int N, i
 // that pass's maps `aux`, times gscale[plane] (the plane mean's upstream
 // gradient, N * C float32), plus a quarter of the pyramid level's gradient
 // (gpx / gpy of gp_dtype, either may be null) over each 2x2 block.
-FA_API int fa_gpu_ssim_cs_scatter(const void* x, const void* y, int dtype, const float* gscale,
+FA_API int fa_gpu_ssim_cs_scatter(const void* x, const void* y, int dtype, const double* gscale,
                                   const float* win, int K, int N, int C, int H, int W,
                                   double shift, const float* aux, int aux_dy, const void* gpx,
                                   const void* gpy, int gp_dtype, void* dx, void* dy, int device,
@@ -1530,6 +1604,61 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials, const int* slots
                                  double* out_total, int device, void* stream) {
   return ms_reduce_impl(partials, slots, npix, weights, M, N, C, plane_scratch, out_per_image,
                         out_total, device, stream);
+}
+
+// Checks and packs fa_gpu_ms_ssim_head(_backward)'s scale arrays.
+static int ms_head_args(const double* const* terms, const double* weights, int M, int N, int C,
+                        MsHead* h) {
+  if (!terms || !weights) return FA_E_ARG;
+  if (M <= 0 || M > MS_MAX_SCALES || N <= 0 || C <= 0) return FA_E_SHAPE;
+  if (static_cast<int64_t>(N) * C > static_cast<int64_t>(INT32_MAX) - BLOCK) return FA_E_SHAPE;
+  *h = MsHead{};
+  for (int m = 0; m < M; ++m) {
+    if (!terms[m]) return FA_E_ARG;
+    h->t[m] = terms[m];
+    h->w[m] = weights[m];
+  }
+  h->M = M;
+  h->N = N;
+  h->C = C;
+  return FA_OK;
+}
+
+// No counterpart in the reference, which combines the MS-SSIM scales with
+// torch ops (functional.py:897-901): about six launches forward and twenty
+// backward per training step, here one each.
+FA_API int fa_gpu_ms_ssim_head(const double* const* terms, int M, int N, int C,
+                               const double* weights, double* out_per_image, double* out_total,
+                               int device, void* stream) {
+  MsHead h;
+  const int rc = ms_head_args(terms, weights, M, N, C, &h);
+  if (rc != FA_OK) return rc;
+  if (!out_per_image && !out_total) return FA_E_ARG;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(ms_head_kernel, dim3(1), dim3(BLOCK), 0, st, h, out_per_image, out_total);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
+}
+
+// No counterpart in the reference (see fa_gpu_ms_ssim_head).
+FA_API int fa_gpu_ms_ssim_head_backward(const double* const* terms, int M, int N, int C,
+                                        const double* weights, const double* g_per_image,
+                                        const double* g_total, double* const* g_terms,
+                                        int device, void* stream) {
+  MsHead h;
+  const int rc = ms_head_args(terms, weights, M, N, C, &h);
+  if (rc != FA_OK) return rc;
+  if (!g_terms || (g_per_image == nullptr) == (g_total == nullptr)) return FA_E_ARG;
+  MsHeadGrads g = {};
+  for (int m = 0; m < M; ++m) g.g[m] = g_terms[m];
+  const int64_t planes = static_cast<int64_t>(N) * C;
+  FA_DEVICE_SCOPE(device);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(ms_head_backward_kernel, dim3(static_cast<unsigned>((planes + BLOCK - 1) / BLOCK)),
+                     dim3(BLOCK), 0, st, h, g_per_image, g_total, g);
+  FA_LAUNCH_CHECK();
+  return FA_OK;
 }
 
 // No counterpart in the reference, whose MS-SSIM is a Python loop over the

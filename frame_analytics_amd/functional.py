@@ -538,6 +538,38 @@ class _CombineScales(torch.autograd.Function):
         return grad.to(stacked.dtype), None
 
 
+class _MsHead(torch.autograd.Function):
+    """MS-SSIM's head over the scales' ``(N, C)`` plane means on the GPU: the
+    scale product, the channel mean and (``per_image`` false) the batch mean
+    in one launch (``fa_gpu_ms_ssim_head``), and every scale's gradient in
+    one launch back (``fa_gpu_ms_ssim_head_backward``), where the same torch
+    expression (:func:`_combine_scales`, then the means) takes about six
+    launches forward and twenty back per training step.  The derivatives are
+    torch's (the clamp, the power, the product, the means); like the scales'
+    fused backward it is not twice differentiable."""
+
+    @staticmethod
+    def forward(ctx, weights, per_image, *terms):
+        from . import backend
+
+        ctx.save_for_backward(*terms)
+        ctx.weights, ctx.per_image = weights, per_image
+        ctx.set_materialize_grads(False)
+        return backend.ms_head(terms, weights, per_image)
+
+    @staticmethod
+    def backward(ctx, g):
+        from . import backend
+
+        _reject_double_backward()
+        terms = ctx.saved_tensors
+        needs = ctx.needs_input_grad[2:]
+        if g is None or not any(needs):
+            return (None, None) + (None,) * len(terms)
+        grads = backend.ms_head_backward(terms, ctx.weights, ctx.per_image, g, needs)
+        return (None, None, *grads)
+
+
 def _combine_scales(terms, weights, device) -> torch.Tensor:
     """Per plane: prod_j max(t_j, 0)^w_j over the stacked ``(N, C)`` terms (a
     fractional power of a negative factor is not real, hence the clamp)."""
@@ -666,6 +698,8 @@ def ms_ssim(x: torch.Tensor, y: torch.Tensor, *, data_range: Optional[float] = N
                 cy = F.avg_pool2d(cy.to(wdt), 2)
             s, cs = _ssim_cs_pair(cx, cy, win, wdt, shift, C1, C2, backend_hint)
             terms.append(s if i == scales - 1 else cs)
+    if native and grad and backend.ms_head_available(terms):
+        return _MsHead.apply(w, reduction == "none", *terms)
     per_image = _combine_scales(terms, w, x4.device).mean(dim=1)  # channels after the product
     return per_image if reduction == "none" else per_image.mean()
 

@@ -318,12 +318,12 @@ FA_API int fa_gpu_ssim_cs_coef(const void* x, const void* y, int dtype, int N,
 /*
  * No counterpart in the reference (see fa_gpu_ssim_cs_coef).  The scatter of
  * fa_gpu_ssim_cs_backward over the maps fa_gpu_ssim_cs_coef wrote, each
- * plane's share times gscale[plane] (N * C float32: the upstream gradient of
+ * plane's share times gscale[plane] (N * C float64: the upstream gradient of
  * that plane's mean), plus the pyramid level's gradient gpx / gpy as in
  * fa_gpu_ssim_cs_backward_ex.  dy needs maps written with aux_dy.
  */
 FA_API int fa_gpu_ssim_cs_scatter(const void* x, const void* y, int dtype,
-                                  const float* gscale, const float* win, int K,
+                                  const double* gscale, const float* win, int K,
                                   int N, int C, int H, int W, double shift,
                                   const float* aux, int aux_dy, const void* gpx,
                                   const void* gpy, int gp_dtype, void* dx,
@@ -366,6 +366,40 @@ FA_API int fa_gpu_ms_ssim_reduce(const double* const* partials,
                                  const double* weights, int M, int N, int C,
                                  double* plane_scratch, double* out_per_image,
                                  double* out_total, int device, void* stream);
+
+/*
+ * No counterpart in the reference, which combines the MS-SSIM scales with
+ * torch ops (functional.py:897-901).  The same head as the end of
+ * fa_gpu_ms_ssim_reduce over plane means that are already formed (the
+ * training path, where each scale's means come out of its own pass): per
+ * plane prod_j max(t_j, 0)^w_j (a NaN mean stays NaN), the mean over the C
+ * channels of each image and the batch mean of those, in one launch.
+ *   terms: host array of M (<= 8) device pointers, scale j's plane means
+ *     (N * C float64: cs below the coarsest scale, SSIM at it);
+ *   weights: host array of M;
+ *   out_per_image (N) / out_total (1) float64: either may be null, not both.
+ */
+FA_API int fa_gpu_ms_ssim_head(const double* const* terms, int M, int N, int C,
+                               const double* weights, double* out_per_image,
+                               double* out_total, int device, void* stream);
+
+/*
+ * No counterpart in the reference (see fa_gpu_ms_ssim_head).  Its gradient,
+ * in one launch: from the upstream gradient of the per-image values
+ * (g_per_image, N float64) or of the batch mean (g_total, 1 float64; exactly
+ * one of the two), each scale's gradient of its plane means into g_terms[j]
+ * (host array of M device pointers, N * C float64 each; a null entry is not
+ * written).  The clamp and the power differentiate as torch's clamp_min and
+ * pow: 0 where t_j < 0, t_j is NaN or w_j = 0, and inf for a zero mean under
+ * a fractional weight; the product's derivative multiplies the other factors
+ * (exact where some are zero).
+ */
+FA_API int fa_gpu_ms_ssim_head_backward(const double* const* terms, int M,
+                                        int N, int C, const double* weights,
+                                        const double* g_per_image,
+                                        const double* g_total,
+                                        double* const* g_terms, int device,
+                                        void* stream);
 
 /*
  * No counterpart in the reference, whose MS-SSIM is a Python loop over the

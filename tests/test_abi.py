@@ -39,7 +39,7 @@ def lib():
 
 def test_header_and_binder_agree():
     decl = _declared()
-    assert len(decl) == 27  # 12 reference entry points + 15 extensions
+    assert len(decl) == 29  # 12 reference entry points + 17 extensions
     assert set(decl) == set(_cabi.SIGNATURES)
     for name, n in decl.items():
         assert len(_cabi.SIGNATURES[name][0]) == n, name

@@ -813,3 +813,72 @@ def test_one_launch_finishes_on_two_streams(gpu):
     assert len(keys) == 6, keys
     for key in keys:
         assert not bool(backend._stream_acc[key].any()), key
+
+
+@pytest.mark.parametrize("per_image", [False, True])
+@pytest.mark.parametrize("weights", [(0.0448, 0.2856, 0.3001, 0.2363, 0.1333), (0.5, 0.0, 1.0)])
+def test_ms_head_matches_the_torch_expression(gpu, per_image, weights):
+    """fa_gpu_ms_ssim_head and its backward (the training path's scale
+    product, channel mean and batch mean in one launch each way) against
+    torch's autograd of the same expression on the same float64 plane means:
+    values and gradients to 1e-14 relative, with zero, negative and NaN means,
+    a zero weight, and one scale that needs no gradient; NaN and inf land
+    where torch puts them."""
+    from frame_analytics_amd.functional import _MsHead
+
+    m, n, c = len(weights), 3, 4
+    gen = torch.Generator().manual_seed(17 + m)
+    base = (torch.rand((m, n, c), generator=gen, dtype=torch.float64) * 1.1 - 0.05)
+    base[0, 0, 0] = 0.0            # zero factor under a fractional weight: inf
+    base[1, 1, 2] = -0.2           # clamped: no gradient through it
+    base[m - 1, 2, 3] = float("nan")
+    base = base.to(gpu)
+    expo = torch.tensor(weights, dtype=torch.float64, device=gpu).view(-1, 1, 1)
+    ref_terms = [base[i].clone().requires_grad_(True) for i in range(m)]
+    got_terms = [base[i].clone().requires_grad_(i != 1) for i in range(m)]
+    prod = torch.stack(ref_terms).clamp_min(0.0).pow(expo).prod(dim=0).mean(dim=1)
+    want = prod if per_image else prod.mean()
+    got = _MsHead.apply(tuple(weights), per_image, *got_terms)
+    assert got.shape == want.shape and got.dtype == torch.float64
+    w_, g_ = want.detach().cpu(), got.detach().cpu()
+    assert torch.equal(torch.isnan(g_), torch.isnan(w_))
+    fin = torch.isfinite(w_)
+    assert torch.allclose(g_[fin], w_[fin], rtol=1e-14, atol=0)
+    up = torch.rand(want.shape, generator=gen, dtype=torch.float64).to(gpu) + 0.5
+    want_g = torch.autograd.grad(want, ref_terms, up)
+    got_g = torch.autograd.grad(got, [t for t in got_terms if t.requires_grad], up)
+    want_g = [v for i, v in enumerate(want_g) if i != 1]
+    for i, (a, b) in enumerate(zip(got_g, want_g)):
+        a, b = a.cpu(), b.cpu()
+        assert torch.equal(torch.isnan(a), torch.isnan(b)), i
+        assert torch.equal(torch.isinf(a), torch.isinf(b)), i
+        f = torch.isfinite(b)
+        assert torch.allclose(a[f], b[f], rtol=1e-14, atol=1e-300), i
+
+
+def test_ms_ssim_training_path_uses_the_head(gpu):
+    """fa.ms_ssim with a gradient combines the scales in the head's two
+    launches (no torch product in the graph) and its value and gradient
+    match the same loss combined by the torch expression."""
+    from frame_analytics_amd import backend, functional
+
+    a, b = u8_pair((2, 3, 192, 224), 8.0, seed=23)
+    x0 = torch.from_numpy(a).to(gpu).float() / 255.0
+    y = torch.from_numpy(b).to(gpu).float() / 255.0
+    x = x0.clone().requires_grad_(True)
+    before = backend.native_calls["fa_gpu_ms_ssim_head_backward"]
+    loss = 1.0 - fa.ms_ssim(x, y, data_range=1.0)
+    loss.backward()
+    assert backend.native_calls["fa_gpu_ms_ssim_head_backward"] == before + 1
+    xr = x0.clone().requires_grad_(True)
+    orig = backend.ms_head_available
+    try:
+        backend.ms_head_available = lambda terms: False  # the torch expression instead
+        loss_r = 1.0 - fa.ms_ssim(xr, y, data_range=1.0)
+        loss_r.backward()
+    finally:
+        backend.ms_head_available = orig
+    assert abs(float(loss.detach()) - float(loss_r.detach())) <= 1e-14
+    err = float((x.grad - xr.grad).abs().max() / xr.grad.abs().max())
+    assert err <= 1e-12, err
+    del functional
