@@ -796,57 +796,101 @@ struct MsHeadGrads {
 
 __device__ inline double ms_clamp0(double v) { return (v != v) ? v : (v > 0.0 ? v : 0.0); }
 
+// The forward's factors wait in LDS, MS_HEAD_LDS doubles: whole images of
+// planes at a time (every thread one factor, every factor's power computed
+// at once instead of in one thread's chain).
+constexpr int MS_HEAD_LDS = BLOCK * MS_MAX_SCALES;
+
+// One workgroup.  A chunk of images: each thread raises one (scale, plane)
+// mean to its weight, then each plane's product, then each image's channel
+// mean; thread i keeps images i, i + BLOCK, ... of every chunk for the batch
+// sum, so the sum's order does not depend on timing.  Images whose C * M
+// factors exceed the LDS take the slow path (one thread per image).
 __global__ __launch_bounds__(BLOCK) void ms_head_kernel(MsHead h,
                                                         double* __restrict__ out_per_image,
                                                         double* __restrict__ out_total) {
+  __shared__ double sf[MS_HEAD_LDS];
   __shared__ double smem[WAVES_PER_BLOCK];
+  const int64_t per_img = static_cast<int64_t>(h.C) * h.M;  // factors of one image
+  const int ci = per_img <= MS_HEAD_LDS ? static_cast<int>(MS_HEAD_LDS / per_img) : 0;  // images per chunk
   double tot = 0.0;
-  for (int n = threadIdx.x; n < h.N; n += BLOCK) {
-    double img = 0.0;
-    for (int c = 0; c < h.C; ++c) {
-      const int64_t p = static_cast<int64_t>(n) * h.C + c;
-      double prod = 1.0;
-#pragma unroll
-      for (int m = 0; m < MS_MAX_SCALES; ++m)
-        if (m < h.M) prod *= pow(ms_clamp0(h.t[m][p]), h.w[m]);
-      img += prod;
+  if (ci == 0) {
+    for (int n = threadIdx.x; n < h.N; n += BLOCK) {
+      double img = 0.0;
+      for (int c = 0; c < h.C; ++c) {
+        const int64_t p = static_cast<int64_t>(n) * h.C + c;
+        double prod = 1.0;
+        for (int m = 0; m < h.M; ++m) prod *= pow(ms_clamp0(h.t[m][p]), h.w[m]);
+        img += prod;
+      }
+      img /= static_cast<double>(h.C);
+      if (out_per_image) out_per_image[n] = img;
+      tot += img;
     }
-    img /= static_cast<double>(h.C);
-    if (out_per_image) out_per_image[n] = img;
-    tot += img;
+  } else {
+    for (int n0 = 0; n0 < h.N; n0 += ci) {
+      const int nimg = min(ci, h.N - n0);
+      const int cp = nimg * h.C;  // planes of the chunk
+      const int64_t p0 = static_cast<int64_t>(n0) * h.C;
+      for (int i = threadIdx.x; i < cp * h.M; i += BLOCK) {
+        const int m = i / cp;
+        sf[i] = pow(ms_clamp0(h.t[m][p0 + (i - m * cp)]), h.w[m]);
+      }
+      __syncthreads();
+      for (int q = threadIdx.x; q < cp; q += BLOCK) {  // column q is this thread's alone
+        double prod = sf[q];
+        for (int m = 1; m < h.M; ++m) prod *= sf[m * cp + q];
+        sf[q] = prod;
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < nimg; i += BLOCK) {
+        double img = 0.0;
+        for (int c = 0; c < h.C; ++c) img += sf[i * h.C + c];
+        img /= static_cast<double>(h.C);
+        if (out_per_image) out_per_image[n0 + i] = img;
+        tot += img;
+      }
+      __syncthreads();  // the next chunk overwrites sf
+    }
   }
   tot = block_sum(tot, smem);
   if (threadIdx.x == 0 && out_total) *out_total = tot / static_cast<double>(h.N);
 }
 
-// One thread per plane.  g_per_image (N) or g_total (1): the upstream gradient
-// of the per-image values or of the batch mean.
+// BLOCK / MS_MAX_SCALES planes per workgroup, thread (q, m) = (tid / 8,
+// tid % 8): the factor and the power's derivative of scale m's mean of plane
+// q; the factors meet in LDS for each thread's product of the others.
+// g_per_image (N) or g_total (1): the upstream gradient of the per-image
+// values or of the batch mean.
+constexpr int MS_HEAD_BW_PLANES = BLOCK / MS_MAX_SCALES;
+
 __global__ __launch_bounds__(BLOCK) void ms_head_backward_kernel(
     MsHead h, const double* __restrict__ g_per_image, const double* __restrict__ g_total,
     MsHeadGrads out) {
-  const int64_t planes = static_cast<int64_t>(h.N) * h.C;
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * BLOCK + threadIdx.x;
-  if (p >= planes) return;
-  const int n = static_cast<int>(p / h.C);
+  __shared__ double sf[MS_HEAD_BW_PLANES][MS_MAX_SCALES];
+  const int planes = h.N * h.C;  // <= INT32_MAX - BLOCK (host check)
+  const int q = static_cast<int>(threadIdx.x) / MS_MAX_SCALES;
+  const int m = static_cast<int>(threadIdx.x) % MS_MAX_SCALES;
+  const int p = static_cast<int>(blockIdx.x) * MS_HEAD_BW_PLANES + q;
+  const bool live = p < planes && m < h.M;
+  double t = 1.0, f = 1.0;
+  if (live) {
+    t = h.t[m][p];
+    f = pow(ms_clamp0(t), h.w[m]);
+  }
+  sf[q][m] = f;  // 1.0 for the scales past M
+  __syncthreads();
+  if (!live || !out.g[m]) return;
+  const int n = p / h.C;
   // the means' backward: 1 / N, then 1 / C, as torch's mean backward divides
   const double gi = g_per_image ? g_per_image[n] : g_total[0] / static_cast<double>(h.N);
   const double gp = gi / static_cast<double>(h.C);
-  double t[MS_MAX_SCALES], f[MS_MAX_SCALES];
+  double others = 1.0;  // the product of the other factors, exact where some are zero
 #pragma unroll
-  for (int m = 0; m < MS_MAX_SCALES; ++m) {
-    t[m] = m < h.M ? h.t[m][p] : 1.0;
-    f[m] = m < h.M ? pow(ms_clamp0(t[m]), h.w[m]) : 1.0;
-  }
-#pragma unroll
-  for (int m = 0; m < MS_MAX_SCALES; ++m) {
-    if (m >= h.M || !out.g[m]) continue;
-    double others = 1.0;  // the product of the other factors, exact where some are zero
-#pragma unroll
-    for (int k = 0; k < MS_MAX_SCALES; ++k)
-      if (k != m) others *= f[k];
-    const double dpow = h.w[m] == 0.0 ? 0.0 : h.w[m] * pow(ms_clamp0(t[m]), h.w[m] - 1.0);
-    out.g[m][p] = t[m] >= 0.0 ? (gp * others) * dpow : 0.0;
-  }
+  for (int k = 0; k < MS_MAX_SCALES; ++k)
+    if (k != m) others *= sf[q][k];
+  const double dpow = h.w[m] == 0.0 ? 0.0 : h.w[m] * pow(ms_clamp0(t), h.w[m] - 1.0);
+  out.g[m][p] = t >= 0.0 ? (gp * others) * dpow : 0.0;
 }
 
 // --------------------------------------------------------------------------
@@ -1655,7 +1699,8 @@ FA_API int fa_gpu_ms_ssim_head_backward(const double* const* terms, int M, int N
   const int64_t planes = static_cast<int64_t>(N) * C;
   FA_DEVICE_SCOPE(device);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(ms_head_backward_kernel, dim3(static_cast<unsigned>((planes + BLOCK - 1) / BLOCK)),
+  hipLaunchKernelGGL(ms_head_backward_kernel,
+                     dim3(static_cast<unsigned>((planes + MS_HEAD_BW_PLANES - 1) / MS_HEAD_BW_PLANES)),
                      dim3(BLOCK), 0, st, h, g_per_image, g_total, g);
   FA_LAUNCH_CHECK();
   return FA_OK;
