@@ -1369,9 +1369,12 @@ int ssim_mfma(const SsimMfmaCall& c, int device, hipStream_t st, int* tiles) {
   if (src != SRC_U8 && !cs_pass) return FA_OK;
   if (c.level_f16 && (src != SRC_U8 || !cs_pass)) return FA_OK;
   if (!mfma_fits(c, src, mode)) return FA_OK;
-  // the finish takes the uint8 forward's sums with a wanted output
+  // the finish takes the uint8 forward's sums with a wanted output, where no
+  // SSIM value can be NaN (C1, C2 > 0: with a zero constant a flat patch is
+  // 0 / 0, which a fixed-point word cannot carry; the two-launch form's float64
+  // sums pass it on, as the reference does)
   const bool fin = c.acc && src == SRC_U8 && mode == MF_REDUCE && c.N <= MF_FIN_MAX_IMAGES &&
-                   (c.out_per_image || c.out_total);
+                   (c.out_per_image || c.out_total) && c.C1 > 0.0 && c.C2 > 0.0;
   MfArgs a = args_of(c);
   const int occ = dispatch(src, mode, false, dim3(1), st, a);
   const int64_t planes = static_cast<int64_t>(c.N) * c.C;

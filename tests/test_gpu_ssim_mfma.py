@@ -467,3 +467,29 @@ def test_one_launch_finish_without_workspace(gpu):
         else:
             assert rc == 5 and bool((out == -3.0).all()), (code, with_map, rc)
         assert not bool(acc.any())
+
+
+def test_zero_constants_keep_nan_like_the_reference(gpu):
+    """uint8 SSIM with K = (0, 0): a patch flat in both frames is 0 / 0, NaN,
+    and the reference's mean carries it (functional.py's float sums).  fa.ssim
+    on uint8 hands the call its stream's accumulator, whose fixed-point words
+    cannot hold NaN, so the one-launch finish declines such calls and the
+    two-launch form returns NaN for that image and the batch; an image
+    without a flat patch stays finite and matches the oracle, and the
+    accumulator stays zero."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((2, 1, 96, 128), 8.0, seed=5)
+    a[0, 0, 20:60, 30:80] = 100
+    b[0, 0, 20:60, 30:80] = 100
+    x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    want = ref.ssim(a.astype(np.float64), b.astype(np.float64), 255.0, K=(0.0, 0.0),
+                    reduction="none")
+    assert np.isnan(want[0]) and np.isfinite(want[1])
+    per = fa.ssim(x, y, data_range=255.0, K=(0.0, 0.0), reduction="none").cpu().numpy()
+    tot = float(fa.ssim(x, y, data_range=255.0, K=(0.0, 0.0)))
+    assert np.isnan(per[0]) and np.isnan(tot)
+    assert _rel(float(per[1]), float(want[1])) <= REL
+    st = torch.cuda.current_stream().cuda_stream
+    acc = backend._stream_acc.get(("ssim", 0, st))
+    assert acc is not None and not bool(acc.any())
