@@ -503,14 +503,29 @@ def ssim_fused(x: torch.Tensor, y: torch.Tensor, win: torch.Tensor,
     k = int(win.numel())
     bpp = workspace_slots("ssim", h, w, k)
     dev, stream = _site(x)
-    partial = _f64(x.device, n * c, bpp)
     per_image, total = _f64(x.device, n), _f64(x.device)
-    smap = (torch.empty((n, c, h - k + 1, w - k + 1), device=x.device, dtype=torch.float32)
-            if want_map else None)
+    if not want_map:
+        # the means finished in the forward's launch where it can (the stream's
+        # accumulator; none under graph capture)
+        acc = _acc_for("ssim", x.device, dev, stream)
+
+        def args(partial):
+            return (_ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, None, None, None,
+                    _ptr(win), k, float(shift), float(C1), float(C2), None, partial, bpp,
+                    _ptr(acc), _ptr(per_image), _ptr(total), dev, stream)
+
+        if acc is None:
+            _run("fa_gpu_ssim_once", *args(_ptr(_f64(x.device, n * c, bpp))))
+        else:
+            _run_or_needs_workspace("fa_gpu_ssim_once", args(None),
+                                    lambda: args(_ptr(_f64(x.device, n * c, bpp))), acc)
+        return [per_image, total]
+    partial = _f64(x.device, n * c, bpp)
+    smap = torch.empty((n, c, h - k + 1, w - k + 1), device=x.device, dtype=torch.float32)
     _run("fa_gpu_ssim", _ptr(x), _ptr(y), _DTYPE_CODE[x.dtype], n, c, h, w, _ptr(win), k,
          float(shift), float(C1), float(C2), _ptr(smap), _ptr(partial), bpp,
          _ptr(per_image), _ptr(total), dev, stream)
-    return [per_image, total, smap] if want_map else [per_image, total]
+    return [per_image, total, smap]
 
 
 def _grad_buffers(x, y, k, need_dx, need_dy):
@@ -624,7 +639,7 @@ def _ssim_native(x: torch.Tensor, y: torch.Tensor, *, win_size: int, sigma: floa
                 bpp, _ptr(per_image), _ptr(total), dev, stream)
 
     if smap is None:
-        acc = _acc_for("ssim", x.device, dev, stream) if x.dtype == torch.uint8 else None
+        acc = _acc_for("ssim", x.device, dev, stream)
         lw = _luma_arg(luma)
 
         def args(partial):

@@ -236,6 +236,73 @@ __device__ inline void row_store(double v, __amdgpu_buffer_rsrc_t r, uint32_t of
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, 0);
 }
 
+// --------------------------------------------------------------------------
+// The one-launch finish of the SSIM forwards (fa_gpu_ssim_once: the uint8
+// matrix-core kernel and the strip kernel).
+//
+// Each workgroup adds its sum of the SSIM map to its image's accumulator word
+// as a signed fixed-point integer, round(sum * 2^F), packed with a
+// contribution count: word = (value << SSIM_FIN_COUNT_BITS) + count, in two's
+// complement (the count stays in the low bits whatever the sign of the sum,
+// and an arithmetic shift recovers the sum).  One returning device-scope
+// atomic adds both; integer addition does not depend on the order, so the
+// result is the same from run to run.  The workgroup whose add completes an
+// image's count (C * tiles workgroups) holds the image's sum, writes its mean,
+// resets the word, and adds the image's integer sum to the batch word, counted
+// in images, whose completer writes the batch mean.  F = 51 - bits(2 N pixels
+// per image) keeps every packed sum within the word (SSIM values lie in
+// [-1, 1] where C1, C2 > 0; the host takes the finish only then).  Words sit
+// on their own 128-byte lines.
+// --------------------------------------------------------------------------
+constexpr int SSIM_FIN_COUNT_BITS = 12;
+constexpr int SSIM_FIN_STRIDE = 16;
+constexpr int SSIM_FIN_MAX_IMAGES = 256;
+static_assert(FA_SSIM_ACC_WORDS == (SSIM_FIN_MAX_IMAGES + 1) * SSIM_FIN_STRIDE,
+              "the ABI's accumulator size");
+
+struct SsimFin {
+  uint64_t* acc;              // FA_SSIM_ACC_WORDS, zero; left zero
+  double fscale, finv;        // 2^F and 2^-F
+  double npix_img, npix_all;  // output pixels of one image, of the batch
+  int N;
+  double* out_per_image;
+  double* out_total;
+};
+
+// The host's F for a batch of npix_all output pixels; false where too few
+// fraction bits would be left (never at real sizes).
+inline bool ssim_fin_scale(SsimFin& f) {
+  int bits = 1;
+  while (bits < 50 && static_cast<double>(int64_t(1) << bits) <= 2.0 * f.npix_all) ++bits;
+  f.fscale = static_cast<double>(int64_t(1) << (51 - bits));
+  f.finv = 1.0 / f.fscale;
+  return bits < 40;
+}
+
+// Thread-level: workgroup sum `s` of image `img`, whose words take
+// `wg_per_image` contributions.
+__device__ inline void ssim_fin_add(const SsimFin& f, int img, int wg_per_image, double s) {
+  constexpr uint64_t CM = (uint64_t(1) << SSIM_FIN_COUNT_BITS) - 1;
+  uint64_t* w = f.acc + static_cast<int64_t>(img) * SSIM_FIN_STRIDE;
+  const int64_t q = __double2ll_rn(s * f.fscale);
+  const uint64_t old = __hip_atomic_fetch_add(
+      w, (static_cast<uint64_t>(q) << SSIM_FIN_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
+      __HIP_MEMORY_SCOPE_AGENT);
+  if ((old & CM) + 1u != static_cast<uint64_t>(wg_per_image)) return;
+  __hip_atomic_store(w, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t tot = (static_cast<int64_t>(old) >> SSIM_FIN_COUNT_BITS) + q;
+  if (f.out_per_image) f.out_per_image[img] = static_cast<double>(tot) * f.finv / f.npix_img;
+  if (!f.out_total) return;
+  uint64_t* wb = f.acc + static_cast<int64_t>(SSIM_FIN_MAX_IMAGES) * SSIM_FIN_STRIDE;
+  const uint64_t ob = __hip_atomic_fetch_add(
+      wb, (static_cast<uint64_t>(tot) << SSIM_FIN_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
+      __HIP_MEMORY_SCOPE_AGENT);
+  if ((ob & CM) + 1u != static_cast<uint64_t>(f.N)) return;
+  __hip_atomic_store(wb, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t all = (static_cast<int64_t>(ob) >> SSIM_FIN_COUNT_BITS) + tot;
+  *f.out_total = static_cast<double>(all) * f.finv / f.npix_all;
+}
+
 }  // namespace fa
 
 #define FA_DEVICE_SCOPE(DEV)                                             \

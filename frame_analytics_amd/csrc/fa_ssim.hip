@@ -111,6 +111,8 @@ struct SsimArgs {
   const float* win;
   float* map;           // MODE_MAP
   double* partial;      // MODE_REDUCE / MAP / CS
+  SsimFin fin;          // MODE_REDUCE: with fin.acc, the one-launch finish
+                        //   (ssim_fin_add) in place of the partial slots
   double* partial_cs;   // MODE_CS
   const float* dmap;    // MODE_PREP: full upstream map, or null
   const float* gscalar; // MODE_PREP: device scalar used when dmap is null
@@ -476,7 +478,13 @@ __global__ __launch_bounds__(BLOCK) FA_SSIM_ATTR void ssim_kernel(SsimArgs a) {
   strip_engine<Pol, KW>(pol, a.win, 0, a.Hout, a.Wout, a.TH, strip, chunk, sbuf);
 
   const int64_t slot = static_cast<int64_t>(plane) * a.bpp + tile;
-  if constexpr (MODE == MODE_REDUCE || MODE == MODE_MAP) {
+  if constexpr (MODE == MODE_REDUCE) {
+    const double s = block_sum(pol.acc_s, sred);
+    if (threadIdx.x == 0) {
+      if (a.fin.acc) ssim_fin_add(a.fin, plane / a.Cout, a.Cout * a.bpp, s);
+      else a.partial[slot] = s;
+    }
+  } else if constexpr (MODE == MODE_MAP) {
     const double s = block_sum(pol.acc_s, sred);
     if (threadIdx.x == 0) a.partial[slot] = s;
   } else if constexpr (MODE == MODE_CS || MODE == MODE_CSF) {
@@ -912,6 +920,21 @@ static int grid_of(int64_t planes, int64_t per_plane, dim3* grid) {
   return FA_OK;
 }
 
+// The plan of a launch, checked once its tiles are known: other launches
+// need nothing more; an SSIM forward that asked for the one-launch finish
+// needs its counts to fit (Cout * tiles contributions per image word), and
+// without the finish, the partial slots (false: refused, nothing launched).
+template <typename Args>
+static bool strip_plan_ok(Args&) {
+  return true;
+}
+static bool strip_plan_ok(SsimArgs& a) {
+  if (!a.fin.acc) return true;
+  if (static_cast<int64_t>(a.Cout) * a.bpp < (int64_t(1) << SSIM_FIN_COUNT_BITS)) return true;
+  a.fin.acc = nullptr;
+  return a.partial != nullptr;
+}
+
 // Tiles `kern` over `planes` planes of an out_H x out_W grid for its
 // occupancy `occ` and launches it; a.TH / a.strips / a.bpp report the tiling.
 template <typename Args>
@@ -921,6 +944,7 @@ static int launch_strips(void (*kern)(Args), int occ, Args& a, int64_t planes, i
   a.TH = t.TH;
   a.strips = t.strips;
   a.bpp = t.tiles;
+  if (!strip_plan_ok(a)) return FA_E_ARG;  // nothing launched
   dim3 grid;
   const int rc = grid_of(planes, t.tiles, &grid);
   if (rc != FA_OK) return rc;
@@ -1236,12 +1260,29 @@ static int ssim_impl(const void* x, const void* y, int dtype, int N, int C, int 
     if (rc != FA_OK) return rc;
     if (tiles < 0) return FA_OK;  // the launch finished the call
   }
-  if (!partial) return FA_E_ARG;  // nothing launched: the strip kernel needs the workspace
   if (tiles == 0) {
+    // the strip kernel's own one-launch finish: the mean alone, as the
+    // matrix-core kernel's (at most SSIM_FIN_MAX_IMAGES images, C1, C2 > 0 so
+    // that no SSIM value is NaN); launch_strips drops it where the counts do
+    // not fit, and then needs the workspace
+    if (acc && !map_out && N <= SSIM_FIN_MAX_IMAGES && (out_per_image || out_total) &&
+        C1 > 0.0 && C2 > 0.0) {
+      a.fin.acc = acc;
+      a.fin.N = N;
+      a.fin.npix_img = static_cast<double>(Hout) * Wout * Cout;
+      a.fin.npix_all = a.fin.npix_img * N;
+      a.fin.out_per_image = out_per_image;
+      a.fin.out_total = out_total;
+      if (!ssim_fin_scale(a.fin)) a.fin.acc = nullptr;
+    }
+    if (!partial && !a.fin.acc) return FA_E_ARG;  // nothing launched
     rc = map_out ? launch_ssim<MODE_MAP>(dtype, K, lm, a, planes, device, st)
                  : launch_ssim<MODE_REDUCE>(dtype, K, lm, a, planes, device, st);
     if (rc != FA_OK) return rc;
+    if (a.fin.acc) return FA_OK;  // the launch finished the call
     tiles = a.bpp;
+  } else if (!partial) {
+    return FA_E_ARG;
   }
 
   // each image owns Cout * tiles consecutive slots of `partial`

@@ -106,48 +106,17 @@ struct MfArgs {
   int N;
 };
 
-// --------------------------------------------------------------------------
-// The one-launch finish of the uint8 forward (fa_gpu_ssim_once).
-//
-// Each workgroup adds its sum of the SSIM map to its image's accumulator word
-// as a signed fixed-point integer, round(sum * 2^F), packed with a
-// contribution count: word = (value << MF_COUNT_BITS) + count, in two's
-// complement (the count stays in the low bits whatever the sign of the sum,
-// and an arithmetic shift recovers the sum).  One returning device-scope
-// atomic adds both; integer addition does not depend on the order, so the
-// result is the same from run to run.  The workgroup whose add completes an
-// image's count (C * tiles workgroups) holds the image's sum, writes its mean,
-// resets the word, and adds the image's integer sum to the batch word, counted
-// in images, whose completer writes the batch mean.  F = 51 - bits(2 N pixels
-// per image) keeps every packed sum within the word.  Words sit on their own
-// 128-byte lines.
-// --------------------------------------------------------------------------
-constexpr int MF_COUNT_BITS = 12;
-constexpr int MF_STRIDE = 16;
-constexpr int MF_FIN_MAX_IMAGES = 256;
-static_assert(FA_SSIM_ACC_WORDS == (MF_FIN_MAX_IMAGES + 1) * MF_STRIDE,
-              "the ABI's accumulator size");
+// The one-launch finish of the uint8 forward (fa_gpu_ssim_once): the packed
+// fixed-point words of ssim_fin_add (fa_common.h), which the strip kernel's
+// finish shares.
+constexpr int MF_COUNT_BITS = SSIM_FIN_COUNT_BITS;
+constexpr int MF_STRIDE = SSIM_FIN_STRIDE;
+constexpr int MF_FIN_MAX_IMAGES = SSIM_FIN_MAX_IMAGES;
 
 __device__ inline void mf_finish(const MfArgs& a, int img, int wg_per_image, double s) {
-  constexpr uint64_t CM = (uint64_t(1) << MF_COUNT_BITS) - 1;
-  uint64_t* w = a.acc + static_cast<int64_t>(img) * MF_STRIDE;
-  const int64_t f = __double2ll_rn(s * a.fscale);
-  const uint64_t old = __hip_atomic_fetch_add(
-      w, (static_cast<uint64_t>(f) << MF_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
-      __HIP_MEMORY_SCOPE_AGENT);
-  if ((old & CM) + 1u != static_cast<uint64_t>(wg_per_image)) return;
-  __hip_atomic_store(w, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int64_t tot = (static_cast<int64_t>(old) >> MF_COUNT_BITS) + f;
-  if (a.out_per_image) a.out_per_image[img] = static_cast<double>(tot) * a.finv / a.npix_img;
-  if (!a.out_total) return;
-  uint64_t* wb = a.acc + static_cast<int64_t>(MF_FIN_MAX_IMAGES) * MF_STRIDE;
-  const uint64_t ob = __hip_atomic_fetch_add(
-      wb, (static_cast<uint64_t>(tot) << MF_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
-      __HIP_MEMORY_SCOPE_AGENT);
-  if ((ob & CM) + 1u != static_cast<uint64_t>(a.N)) return;
-  __hip_atomic_store(wb, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int64_t all = (static_cast<int64_t>(ob) >> MF_COUNT_BITS) + tot;
-  *a.out_total = static_cast<double>(all) * a.finv / a.npix_all;
+  const SsimFin f = {a.acc, a.fscale, a.finv, a.npix_img, a.npix_all, a.N, a.out_per_image,
+                     a.out_total};
+  ssim_fin_add(f, img, wg_per_image, s);
 }
 
 // MS-SSIM's words: one per (scale, plane), each workgroup adding its sum of

@@ -523,9 +523,11 @@ FA_API int fa_gpu_gmsd_once(const void* x, const void* y, int dtype, int N, int 
  * (fa_cuda.cu:1218-1222).  fa_gpu_ssim_ex (same arguments and results), plus
  * acc: FA_SSIM_ACC_WORDS uint64 of device memory, zero when the call starts
  * and left zero when it completes (state of one stream, like
- * fa_gpu_pixel_reduce_once's).  Where the forward runs on the matrix cores
- * (uint8 planes without luma, 8-sample aligned rows; see fa_gpu_ssim) with
- * no map, N <= 256 and a mean wanted, the launch finishes the call itself:
+ * fa_gpu_pixel_reduce_once's).  A call with no map, N <= 256, a mean
+ * wanted and C1, C2 > 0 (so that no SSIM value is NaN) finishes in its one
+ * launch -- the matrix-core forward's (uint8 planes without luma, 8-sample
+ * aligned rows; see fa_gpu_ssim) or the strip kernel's (every other input,
+ * luma and views included, while C_out * tiles per image stays below 4096):
  * each workgroup adds its sum of the map to `acc` as a round-to-nearest
  * signed fixed-point integer (so the result does not depend on the order of
  * the adds) with returning device-scope atomics, and the workgroups that

@@ -7,6 +7,8 @@ own gate is 5e-5, validate.py:25).
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -222,3 +224,81 @@ def test_autocast_does_not_move_the_metric(gpu, dt, fn):
     assert x.grad is not None and torch.isfinite(x.grad).all()
     with torch.no_grad(), torch.autocast("cuda", dtype=dt):
         assert abs(float(call(x, y, data_range=1.0)) - plain) <= 1e-6 * max(abs(plain), 1e-3)
+
+
+_DT = {torch.uint8: 0, torch.float16: 1, torch.bfloat16: 2, torch.float32: 3, torch.float64: 4}
+
+
+def _ssim_call(name, x, y, acc=None, luma=None, K=11, L=255.0, partial=True):
+    """fa_gpu_ssim_ex, or fa_gpu_ssim_once with ``acc``, on views of x / y
+    (element strides passed through) with optional luma: (status,
+    per-image means, batch mean) as numpy float64."""
+    from frame_analytics_amd import backend
+
+    n, c, h, w = (int(v) for v in x.shape)
+    cout = 1 if luma is not None else c
+    bpp = backend.workspace_slots("ssim", h, w, K)
+    part = (torch.full((n * cout, bpp), -3.0, dtype=torch.float64, device=x.device)
+            if partial else None)
+    out = torch.full((n + 1,), -3.0, dtype=torch.float64, device=x.device)
+    st = torch.cuda.current_stream().cuda_stream
+    win = fa.gaussian_window_1d(K, 1.5, device=x.device, dtype=torch.float32)
+    xs = (ctypes.c_int64 * 3)(x.stride(0), x.stride(1), x.stride(2))
+    ys = (ctypes.c_int64 * 3)(y.stride(0), y.stride(1), y.stride(2))
+    lw = (ctypes.c_double * 4)(*luma) if luma is not None else None
+    args = [x.data_ptr(), y.data_ptr(), _DT[x.dtype], n, c, h, w, xs, ys, lw, win.data_ptr(), K,
+            L / 2, (0.01 * L) ** 2, (0.03 * L) ** 2, None,
+            None if part is None else part.data_ptr(), bpp]
+    if name == "fa_gpu_ssim_once":
+        args.append(None if acc is None else acc.data_ptr())
+    rc = backend.call_gpu(name, *args, out.data_ptr(), out[n:].data_ptr(), 0, st)
+    o = out.cpu().numpy()
+    return rc, o[:n], o[n]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float64, torch.float16, torch.bfloat16])
+def test_strip_one_launch_finish(gpu, dt):
+    """The strip kernel's one-launch finish (fa_gpu_ssim_once over float
+    input): per-image and batch means within 1e-12 of fa_gpu_ssim_ex's float64
+    finalize, the same bits on a repeat, the accumulator zero after every
+    call (a second, smaller call included), with a null workspace (the launch
+    does not read it), over cropped views and with luma formed in the kernel;
+    the oracle agrees.  A call whose counts do not fit the words (C * tiles
+    per image >= 4096) takes the workspace and the two-launch form."""
+    from frame_analytics_amd import backend
+
+    g = torch.Generator(device="cpu").manual_seed(31)
+    base = torch.rand((3, 3, 150, 212), generator=g, dtype=torch.float64) * 255.0
+    noisy = (base + 9.0 * torch.randn(base.shape, generator=g, dtype=torch.float64)).clamp(0, 255)
+    x, y = base.to(gpu, dt), noisy.to(gpu, dt)
+    acc = torch.zeros(backend._ACC_WORDS["ssim"], dtype=torch.int64, device=gpu)
+    bt601 = (0.299, 0.587, 0.114, 0.0)
+    for xx, yy, luma in ((x, y, None), (x[:, :, 3:-2, 5:-4], y[:, :, 3:-2, 5:-4], None),
+                         (x, y, bt601)):
+        rc2, p2, t2 = _ssim_call("fa_gpu_ssim_ex", xx, yy, luma=luma)
+        rc1, p1, t1 = _ssim_call("fa_gpu_ssim_once", xx, yy, acc, luma=luma, partial=False)
+        assert rc1 == 0 and rc2 == 0
+        assert not bool(acc.any())
+        assert np.all(np.abs(p1 - p2) <= 1e-12 * np.abs(p2)), (p1, p2)
+        assert abs(t1 - t2) <= 1e-12 * abs(t2)
+        _, q1, u1 = _ssim_call("fa_gpu_ssim_once", xx, yy, acc, luma=luma, partial=False)
+        assert np.array_equal(p1, q1) and t1 == u1
+        _, pk, tk = _ssim_call("fa_gpu_ssim_once", xx[:1], yy[:1], acc, luma=luma, partial=False)
+        assert not bool(acc.any())
+        assert abs(pk[0] - p2[0]) <= 1e-12 * abs(p2[0])
+    xo = x.double().cpu().numpy()
+    yo = y.double().cpu().numpy()
+    _, p1, _ = _ssim_call("fa_gpu_ssim_once", x, y, acc, partial=False)
+    want = ref.ssim(xo, yo, 255.0, reduction="none")
+    assert np.all(np.abs(p1 - want) <= 1e-6 * np.abs(want))
+    if dt == torch.float32:
+        # 4096 channels of one image (one tile per 24 x 24 plane): 4096
+        # contributions per word is past 4095, so the call needs the
+        # workspace (refused without it)
+        wide_x = torch.rand((1, 4096, 24, 24), generator=g, dtype=torch.float64).to(gpu, dt) * 255
+        wide_y = (wide_x + 5.0).clamp(0, 255)
+        rc0, _, _ = _ssim_call("fa_gpu_ssim_once", wide_x, wide_y, acc, partial=False)
+        rcw, pw, tw = _ssim_call("fa_gpu_ssim_once", wide_x, wide_y, acc)
+        _, pr, tr = _ssim_call("fa_gpu_ssim_ex", wide_x, wide_y)
+        assert (rc0, rcw) == (5, 0) and np.array_equal(pw, pr) and tw == tr
+        assert not bool(acc.any())

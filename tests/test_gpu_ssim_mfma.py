@@ -436,20 +436,32 @@ def test_one_launch_finish_matches_finalize(gpu, shape):
 
 
 def test_one_launch_finish_without_workspace(gpu):
-    """fa_gpu_ssim_once with a null `partial`: the matrix-core launch that
-    finishes the call does not read it (same means); a float32 call, which the
-    strip kernel serves, and a map call return FA_E_ARG and write nothing."""
+    """fa_gpu_ssim_once with a null `partial`: the launch that finishes the
+    call does not read it (same means), the matrix-core kernel's for uint8 and
+    the strip kernel's for float32; a map call returns FA_E_ARG and writes
+    nothing."""
     from frame_analytics_amd import backend
 
     a, b = u8_pair((2, 3, 200, 256), 8.0, seed=77)
     x, y = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
     win = fa.gaussian_window_1d(11, 1.5, device=gpu, dtype=torch.float32)
     acc = torch.zeros(backend._ACC_WORDS["ssim"], dtype=torch.int64, device=gpu)
-    want_p, want_t = _ssim_abi("fa_gpu_ssim", x, y, win)
     st = torch.cuda.current_stream().cuda_stream
     bpp = backend.workspace_slots("ssim", 200, 256, 11)
-    for xx, yy, code, with_map, ok in ((x, y, 0, False, True), (x.float(), y.float(), 3, False, False),
+
+    def two_launch(xx, yy, code):
+        part = torch.empty((6, bpp), dtype=torch.float64, device=gpu)
+        out = torch.empty((3,), dtype=torch.float64, device=gpu)
+        assert backend.call_gpu("fa_gpu_ssim", xx.data_ptr(), yy.data_ptr(), code, 2, 3, 200, 256,
+                                win.data_ptr(), 11, 127.5, (0.01 * 255) ** 2, (0.03 * 255) ** 2,
+                                None, part.data_ptr(), bpp, out.data_ptr(), out[2:].data_ptr(),
+                                0, st) == 0
+        o = out.cpu().numpy()
+        return o[:2], o[2]
+
+    for xx, yy, code, with_map, ok in ((x, y, 0, False, True), (x.float(), y.float(), 3, False, True),
                                        (x, y, 0, True, False)):
+        want_p, want_t = two_launch(xx, yy, code)
         out = torch.full((3,), -3.0, dtype=torch.float64, device=gpu)
         smap = (torch.empty((2, 3, 190, 246), dtype=torch.float32, device=gpu)
                 if with_map else None)
