@@ -253,6 +253,15 @@ __device__ inline void row_store(double v, __amdgpu_buffer_rsrc_t r, uint32_t of
 // per image) keeps every packed sum within the word (SSIM values lie in
 // [-1, 1] where C1, C2 > 0; the host takes the finish only then).  Words sit
 // on their own 128-byte lines.
+//
+// Floating input can hold NaN or inf, which make SSIM values NaN, and a
+// fixed-point word cannot: a workgroup whose sum is not finite adds 0 to the
+// value and sets the word's flag, the next word of its line, with a returning
+// atomic whose value it waits for before its count add; the completer then
+// reads and clears the flag by an exchange and writes NaN, as the reference's
+// float mean would be (and the batch's flag likewise).  A flag set before a
+// count add is performed before it, so the completer, whose add saw every
+// count, sees every flag.
 // --------------------------------------------------------------------------
 constexpr int SSIM_FIN_COUNT_BITS = 12;
 constexpr int SSIM_FIN_STRIDE = 16;
@@ -281,26 +290,47 @@ inline bool ssim_fin_scale(SsimFin& f) {
 
 // Thread-level: workgroup sum `s` of image `img`, whose words take
 // `wg_per_image` contributions.
+// Sets the flag word `flag` and waits for the atomic's return, so that it is
+// performed before anything the thread issues after.
+__device__ inline void ssim_fin_flag(uint64_t* flag) {
+  const uint64_t r = __hip_atomic_fetch_or(flag, uint64_t(1), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(r));  // the value is used: the add below issues after it is back
+}
+
+__device__ inline bool ssim_fin_flagged(uint64_t* flag) {
+  return __hip_atomic_exchange(flag, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
+// Thread-level: workgroup sum `s` of image `img`, whose words take
+// `wg_per_image` contributions.
 __device__ inline void ssim_fin_add(const SsimFin& f, int img, int wg_per_image, double s) {
   constexpr uint64_t CM = (uint64_t(1) << SSIM_FIN_COUNT_BITS) - 1;
+  constexpr double NaN = __builtin_nan("");
   uint64_t* w = f.acc + static_cast<int64_t>(img) * SSIM_FIN_STRIDE;
-  const int64_t q = __double2ll_rn(s * f.fscale);
+  const bool finite = __builtin_isfinite(s);
+  if (!finite) ssim_fin_flag(w + 1);
+  const int64_t q = finite ? __double2ll_rn(s * f.fscale) : 0;
   const uint64_t old = __hip_atomic_fetch_add(
       w, (static_cast<uint64_t>(q) << SSIM_FIN_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
       __HIP_MEMORY_SCOPE_AGENT);
   if ((old & CM) + 1u != static_cast<uint64_t>(wg_per_image)) return;
   __hip_atomic_store(w, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool nan_img = ssim_fin_flagged(w + 1);
   const int64_t tot = (static_cast<int64_t>(old) >> SSIM_FIN_COUNT_BITS) + q;
-  if (f.out_per_image) f.out_per_image[img] = static_cast<double>(tot) * f.finv / f.npix_img;
+  if (f.out_per_image)
+    f.out_per_image[img] = nan_img ? NaN : static_cast<double>(tot) * f.finv / f.npix_img;
   if (!f.out_total) return;
   uint64_t* wb = f.acc + static_cast<int64_t>(SSIM_FIN_MAX_IMAGES) * SSIM_FIN_STRIDE;
+  if (nan_img) ssim_fin_flag(wb + 1);
   const uint64_t ob = __hip_atomic_fetch_add(
       wb, (static_cast<uint64_t>(tot) << SSIM_FIN_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
       __HIP_MEMORY_SCOPE_AGENT);
   if ((ob & CM) + 1u != static_cast<uint64_t>(f.N)) return;
   __hip_atomic_store(wb, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool nan_all = ssim_fin_flagged(wb + 1);
   const int64_t all = (static_cast<int64_t>(ob) >> SSIM_FIN_COUNT_BITS) + tot;
-  *f.out_total = static_cast<double>(all) * f.finv / f.npix_all;
+  *f.out_total = nan_all ? NaN : static_cast<double>(all) * f.finv / f.npix_all;
 }
 
 }  // namespace fa

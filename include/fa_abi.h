@@ -533,7 +533,10 @@ FA_API int fa_gpu_gmsd_once(const void* x, const void* y, int dtype, int N, int 
  * the adds) with returning device-scope atomics, and the workgroups that
  * complete an image's sum, and the batch's, write the means.  They differ
  * from fa_gpu_ssim's fixed-order float64 sums by that rounding, ~1e-13
- * relative at 1080p.  Every other call runs as fa_gpu_ssim_ex and ignores
+ * relative at 1080p.  A workgroup sum that is not finite (NaN or inf in
+ * floating input) sets a flag beside the image's word instead, and that
+ * image's mean and the batch mean come out NaN, as the float64 sums would.
+ * Every other call runs as fa_gpu_ssim_ex and ignores
  * `acc`.  `partial` may be null for a call that finishes in its launch; one
  * with a null `partial` that cannot returns FA_E_ARG before launching anything.
  */

@@ -302,3 +302,38 @@ def test_strip_one_launch_finish(gpu, dt):
         _, pr, tr = _ssim_call("fa_gpu_ssim_ex", wide_x, wide_y)
         assert (rc0, rcw) == (5, 0) and np.array_equal(pw, pr) and tw == tr
         assert not bool(acc.any())
+
+
+def test_strip_one_launch_finish_carries_nan(gpu):
+    """Floating input can hold NaN and inf, which make SSIM values NaN; the
+    one-launch finish flags such a workgroup sum instead of packing it, so an
+    image with a NaN or an inf sample comes out NaN, as do the batch mean and
+    the two-launch form and the oracle, while the other image stays finite;
+    the accumulator and its flags are zero afterwards, and a clean call right
+    after gives finite means again."""
+    from frame_analytics_amd import backend
+
+    g = torch.Generator(device="cpu").manual_seed(8)
+    base = torch.rand((3, 1, 96, 128), generator=g, dtype=torch.float64) * 255.0
+    noisy = (base + 6.0 * torch.randn(base.shape, generator=g, dtype=torch.float64)).clamp(0, 255)
+    x, y = base.to(gpu, torch.float32), noisy.to(gpu, torch.float32)
+    xb = x.clone()
+    xb[0, 0, 40, 50] = float("nan")
+    xb[2, 0, 10, 100] = float("inf")
+    acc = torch.zeros(backend._ACC_WORDS["ssim"], dtype=torch.int64, device=gpu)
+    rc1, p1, t1 = _ssim_call("fa_gpu_ssim_once", xb, y, acc, partial=False)
+    rc2, p2, t2 = _ssim_call("fa_gpu_ssim_ex", xb, y)
+    assert rc1 == 0 and rc2 == 0
+    want = ref.ssim(xb.double().cpu().numpy(), y.double().cpu().numpy(), 255.0, reduction="none")
+    for got in (p1, p2, want):
+        assert np.isnan(got[0]) and np.isnan(got[2]) and np.isfinite(got[1])
+    assert np.isnan(t1) and np.isnan(t2)
+    assert abs(p1[1] - p2[1]) <= 1e-12 * abs(p2[1])
+    assert not bool(acc.any())
+    _, pc, tc = _ssim_call("fa_gpu_ssim_once", x, y, acc, partial=False)
+    assert np.all(np.isfinite(pc)) and np.isfinite(tc)
+    assert not bool(acc.any())
+    # through the public call: fa.ssim hands the stream's accumulator
+    per = fa.ssim(xb, y, data_range=255.0, reduction="none").cpu().numpy()
+    assert np.isnan(per[0]) and np.isnan(per[2]) and abs(per[1] - p2[1]) <= 1e-12 * abs(p2[1])
+    assert np.isnan(float(fa.ssim(xb, y, data_range=255.0)))
