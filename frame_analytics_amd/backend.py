@@ -31,6 +31,7 @@ path, which is the reference's own behaviour on such hosts.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import functools
 import os
@@ -356,6 +357,25 @@ _ACC_WORDS = {"pixel": (32 + 1) * 16, "gmsd": (3 * 64 + 2) * 16, "ssim": (256 + 
               "ms": (8 * 256 + 1) * 16}
 #: (kind, device, raw stream) -> that stream's accumulator, zero between calls
 _stream_acc: dict = {}
+#: (kind, device) -> accumulator of one HIP graph's calls alone (see
+#: private_accumulators); None outside such a scope
+_private_acc: Optional[dict] = None
+
+
+@contextlib.contextmanager
+def private_accumulators(store: dict):
+    """Within this scope the one-launch entry points take their accumulators
+    from ``store`` (made on first use, outside capture), in graph capture
+    too.  For a graph whose replays share those buffers with nothing else
+    (``StreamingMetrics``: its warm-up and its capture run in this scope, and
+    then only its replays use them), so the captured calls can finish in their
+    one launch; each replay leaves them zero, like an eager call."""
+    global _private_acc
+    prev, _private_acc = _private_acc, store
+    try:
+        yield store
+    finally:
+        _private_acc = prev
 
 
 def _acc_for(kind: str, device: torch.device, dev: int, stream: int) -> Optional[torch.Tensor]:
@@ -365,8 +385,18 @@ def _acc_for(kind: str, device: torch.device, dev: int, stream: int) -> Optional
     leaves it zero again, so one buffer serves every call on its stream, in
     stream order; calls on another stream get their own.  Under graph capture
     there is none (the call takes its two-launch form): a graph's replays
-    could overlap eager calls of the stream that recorded it."""
-    if torch._C._cuda_isCurrentStreamCapturing():
+    could overlap eager calls of the stream that recorded it -- unless the
+    capture runs in :func:`private_accumulators`, whose buffers are the
+    graph's alone."""
+    capturing = torch._C._cuda_isCurrentStreamCapturing()
+    store = _private_acc
+    if store is not None:
+        acc = store.get((kind, dev))
+        if acc is None and not capturing:
+            acc = torch.zeros(_ACC_WORDS[kind], dtype=torch.int64, device=device)
+            store[(kind, dev)] = acc
+        return acc
+    if capturing:
         return None
     key = (kind, dev, stream)
     acc = _stream_acc.get(key)
@@ -383,9 +413,10 @@ def _forget_acc(acc: Optional[torch.Tensor]) -> None:
     The next call allocates a new, zeroed one."""
     if acc is None:
         return
-    for key, t in list(_stream_acc.items()):
-        if t is acc:
-            del _stream_acc[key]
+    for store in (_stream_acc, _private_acc or {}):
+        for key, t in list(store.items()):
+            if t is acc:
+                del store[key]
 
 
 def pixel_gpu(ext: _Native, x: torch.Tensor, y: torch.Tensor, *, op: int,

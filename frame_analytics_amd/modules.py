@@ -295,14 +295,19 @@ class StreamingMetrics:
         return done, values
 
     def _capture(self) -> None:
+        from . import backend
+
         side = torch.cuda.Stream(self.device)
+        # the graph's own accumulators: only its replays use them, so the
+        # captured metrics finish in their one launch (made in the warm-up)
+        self._accs: dict = {}
         try:
-            with torch.cuda.device(self.device):
+            with torch.cuda.device(self.device), backend.private_accumulators(self._accs):
                 self.ref.zero_()
                 self.dist.zero_()
                 side.wait_stream(torch.cuda.current_stream(self.device))
                 with torch.cuda.stream(side):
-                    self._evaluate()  # pool, workspace and window caches
+                    self._evaluate()  # pool, workspace, window caches, accumulators
                 side.synchronize()
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, stream=side):
@@ -311,6 +316,7 @@ class StreamingMetrics:
             self._graph, self._outs = graph, outs
         except Exception as exc:  # an eager scorer still works
             self._graph = self._outs = None
+            self._accs = {}
             self.capture_error = f"{type(exc).__name__}: {exc}"
 
     # -- staging ------------------------------------------------------------- #

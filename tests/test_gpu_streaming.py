@@ -66,3 +66,34 @@ def test_streaming_from_device_tensors(gpu):
     out = sm.update(ta, tb, as_float=False)
     assert isinstance(out["ssim"], torch.Tensor)
     assert float(out["mse"]) == ref.mse(a, b)
+
+
+def test_streaming_graph_finishes_in_its_launches(gpu):
+    """At 1080p RGB every captured metric takes its one-launch form (the pixel
+    sweep's, the matrix-core SSIM's, GMSD's, MS-SSIM's three launches) on the
+    graph's own accumulators: replays match eager calls made between them (on
+    the stream's shared accumulators) to 1e-12, and every private accumulator
+    is zero after each replay."""
+    from frame_analytics_amd import backend
+
+    metrics = ("mse", "psnr", "ssim", "ms_ssim", "gmsd")
+    shape = (1, 3, 1080, 1920)
+    sm = fa.StreamingMetrics(shape, device="cuda", dtype=torch.uint8, data_range=255.0,
+                             metrics=metrics)
+    assert sm.graph_captured
+    assert {k[0] for k in sm._accs} == {"pixel", "ssim", "gmsd", "ms"}
+    for seed in range(3):
+        a, b = u8_pair(shape, 5.0 + 3 * seed, seed=200 + seed)
+        got = sm.update(a, b)
+        torch.cuda.synchronize()
+        assert not any(bool(t.any()) for t in sm._accs.values()), seed
+        ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+        want = {"mse": float(fa.mse(ta, tb)), "psnr": float(fa.psnr(ta, tb, data_range=255.0)),
+                "ssim": float(fa.ssim(ta, tb, data_range=255.0)),
+                "ms_ssim": float(fa.ms_ssim(ta, tb, data_range=255.0)),
+                "gmsd": float(fa.gmsd(ta, tb, data_range=255.0))}
+        for k in metrics:
+            assert abs(got[k] - want[k]) <= 1e-12 * max(1.0, abs(want[k])), (seed, k, got[k], want[k])
+        assert got["mse"] == ref.mse(a, b)
+    shared = list(backend._stream_acc.values())
+    assert not any(t is u for t in sm._accs.values() for u in shared)
