@@ -999,7 +999,7 @@ def _gmsd_launch(x, y, xs, ys, luma, T, eps, downsample, planes, want_map, hd, w
     else:
         out = _f64(x.device, 2 * n + 2)
         mean, std, batch = out[:n], out[n:2 * n], out[2 * n:]
-    acc = _acc_for("gmsd", x.device, dev, stream) if x.dtype == torch.uint8 else None
+    acc = _acc_for("gmsd", x.device, dev, stream)
     lw = _luma_arg(luma)
 
     def args(ws):

@@ -133,7 +133,6 @@ struct SrcU8Wide {
   static constexpr int OUTW = G_OUTW_WIDE;
   static constexpr int CH = LUMA ? 3 : 1;
   static constexpr bool FAST = true;
-  static constexpr bool U8IN = true;     // uint8 input: every sample finite
   static constexpr bool PACKED = !LUMA;  // samples_xy / prewitt_xy
   using S = typename std::conditional<LUMA, double, int>::type;
   struct Raw {
@@ -238,7 +237,6 @@ struct SrcGeneric {
   static constexpr int CH = LUMA ? 3 : 1;
   static constexpr int NV = DOWN ? 4 : 1;
   static constexpr bool FAST = std::is_same<T, uint8_t>::value || std::is_same<T, half_t>::value;
-  static constexpr bool U8IN = std::is_same<T, uint8_t>::value;
   static constexpr bool PACKED = false;
   using S = double;
   struct Raw {
@@ -539,8 +537,8 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
 }
 
 // --------------------------------------------------------------------------
-// The one-launch finish (fa_gpu_gmsd_once), for uint8 input with T or eps
-// positive, where every d = 1 - q is finite and in [0, 1].
+// The one-launch finish (fa_gpu_gmsd_once), with T or eps positive, where the
+// d = 1 - q of finite samples are in [0, 1].
 //
 // A workgroup's sums of d and d^2 go to two accumulator words of its image as
 // fixed-point integers, round(sum * 2^F) with F = 52 - bits(pixels per image
@@ -561,6 +559,14 @@ __device__ inline void gmsd_run(const GmsdArgs& a, int n, int c, int strip, int 
 //
 // Each workgroup's rounding is at most 2^-(F+1) on a sum below 2^(52-F), so
 // the per-image sums keep ~2^-52 relative accuracy times the workgroup count.
+//
+// Floating input can hold NaN or inf, which make d NaN; a fixed-point word
+// cannot carry it.  A lane whose sum is not finite adds 0 and first sets a
+// flag, the second word of the image's meeting line, with a returning atomic
+// it waits for; the meeting's completer, whose view has every add of both
+// words behind it (and so every flag set before them), reads and clears the
+// flag by an exchange and writes NaN for both statistics, as the reference's
+// float statistics would be; the batch words carry flags the same way.
 // --------------------------------------------------------------------------
 constexpr int GF_COUNT_BITS = 12;  // workgroups per image: < 4096
 constexpr int GF_STRIDE = 16;      // uint64 words between accumulators (128 bytes)
@@ -580,6 +586,13 @@ __device__ inline uint64_t gf_swap(uint64_t* p, uint64_t v) {
 __device__ inline void gf_zero(uint64_t* p) {
   __hip_atomic_store(p, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Sets flag word p and waits for the atomic's return, so that it is performed
+// before anything the thread issues after it.
+__device__ inline void gf_flag(uint64_t* p) {
+  const uint64_t r = __hip_atomic_fetch_or(p, uint64_t(1), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(r));
+}
 
 // Mean q and population std q of an image from its sums of d = 1 - q.  A NaN
 // variance (a NaN q, e.g. a flat patch with T = eps = 0) stays NaN.
@@ -594,21 +607,26 @@ __device__ inline void gmsd_stats(double sa, double sb, double npix, double* mea
 // Lane `which` (0: sum d, 1: sum d^2) of image n adds the workgroup's `v`.
 __device__ inline void gmsd_finish(const GmsdArgs& a, int n, int which, double v) {
   constexpr uint64_t CM = (uint64_t(1) << GF_COUNT_BITS) - 1;
+  constexpr double NaN = __builtin_nan("");
   uint64_t* w = a.acc + static_cast<int64_t>(3 * n + which) * GF_STRIDE;
-  const uint64_t f = static_cast<uint64_t>(__double2ll_rn(v * a.fscale));
+  uint64_t* meet = a.acc + static_cast<int64_t>(3 * n + 2) * GF_STRIDE;
+  const bool finite = __builtin_isfinite(v);
+  if (!finite) gf_flag(meet + 1);
+  const uint64_t f = finite ? static_cast<uint64_t>(__double2ll_rn(v * a.fscale)) : 0u;
   const uint64_t old = gf_add(w, (f << GF_COUNT_BITS) + 1u);
   if ((old & CM) + 1u != static_cast<uint64_t>(a.wpi)) return;
   gf_zero(w);
   const uint64_t mine = (old >> GF_COUNT_BITS) + f;
-  uint64_t* meet = a.acc + static_cast<int64_t>(3 * n + 2) * GF_STRIDE;
   const uint64_t other = gf_swap(meet, mine | GF_PRESENT | (which ? GF_IS_SQ : 0));
   if (!(other & GF_PRESENT)) return;  // the other sum is not complete yet
   gf_zero(meet);
+  const bool nan_img = gf_swap(meet + 1, 0) != 0;
   const uint64_t ov = other & (GF_IS_SQ - 1);
   const double sd = static_cast<double>(which ? ov : mine) * a.finv;
   const double sd2 = static_cast<double>(which ? mine : ov) * a.finv;
   double mq, sq;
   gmsd_stats(sd, sd2, a.npix, &mq, &sq);
+  if (nan_img) mq = sq = NaN;
   a.out_mean[n] = mq;
   a.out_std[n] = sq;
   if (!a.out_batch) return;
@@ -617,11 +635,13 @@ __device__ inline void gmsd_finish(const GmsdArgs& a, int n, int which, double v
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     uint64_t* b = a.acc + static_cast<int64_t>(3 * GF_MAX_IMAGES + k) * GF_STRIDE;
-    const uint64_t fb = static_cast<uint64_t>(__double2ll_rn(r[k] * bs));
+    if (nan_img) gf_flag(b + 1);
+    const uint64_t fb = nan_img ? 0u : static_cast<uint64_t>(__double2ll_rn(r[k] * bs));
     const uint64_t ob = gf_add(b, (fb << GF_COUNT_BITS) + 1u);
     if ((ob & CM) + 1u != static_cast<uint64_t>(a.N)) continue;
     gf_zero(b);
-    a.out_batch[k] = static_cast<double>((ob >> GF_COUNT_BITS) + fb) / bs / a.N;
+    const bool nan_all = gf_swap(b + 1, 0) != 0;
+    a.out_batch[k] = nan_all ? NaN : static_cast<double>((ob >> GF_COUNT_BITS) + fb) / bs / a.N;
   }
 }
 
@@ -956,7 +976,7 @@ template <class Src>
 static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipStream_t st,
                        int* wpi_used) {
   const bool map = a.map != nullptr;
-  const bool fin_ok = Src::U8IN && a.acc && !map;
+  const bool fin_ok = a.acc && !map;
   // a workgroup is one wave on each of the CU's four SIMDs
   const int wgs_per_cu = std::min(
       G_MAX_WAVES_PER_SIMD, map ? occupancy_gmsd<Src, true>()
@@ -974,16 +994,13 @@ static int launch_gmsd(GmsdArgs a, int N, int slots_per_image, int device, hipSt
   if (tasks > INT32_MAX / WAVES_PER_BLOCK) return FA_E_SHAPE;
   a.wpi = static_cast<int>(wpi);
   a.tasks = static_cast<int>(tasks);
-  if ((!a.psum || !a.psumsq) && !(Src::U8IN && fin_ok && wpi < (1 << GF_COUNT_BITS)))
-    return FA_E_ARG;
-  if constexpr (Src::U8IN) {
-    if (fin_ok && wpi < (1 << GF_COUNT_BITS)) {
-      hipLaunchKernelGGL((gmsd_kernel<Src, false, true>), dim3(static_cast<unsigned>(tasks)),
-                         dim3(BLOCK), 0, st, a);
-      FA_LAUNCH_CHECK();
-      *wpi_used = 0;
-      return FA_OK;
-    }
+  if ((!a.psum || !a.psumsq) && !(fin_ok && wpi < (1 << GF_COUNT_BITS))) return FA_E_ARG;
+  if (fin_ok && wpi < (1 << GF_COUNT_BITS)) {
+    hipLaunchKernelGGL((gmsd_kernel<Src, false, true>), dim3(static_cast<unsigned>(tasks)),
+                       dim3(BLOCK), 0, st, a);
+    FA_LAUNCH_CHECK();
+    *wpi_used = 0;
+    return FA_OK;
   }
   if (map)
     hipLaunchKernelGGL((gmsd_kernel<Src, true>), dim3(static_cast<unsigned>(tasks)), dim3(BLOCK),
@@ -1073,12 +1090,13 @@ static int gmsd_impl(const void* x, const void* y, int dtype, int N, int C, int 
   a.psum = psum;
   a.psumsq = psumsq;
   a.map = map_out;
-  // the one-launch finish: uint8 input (finite samples), T or eps positive
-  // (every d finite), statistics only, at most GF_MAX_IMAGES images; the
-  // fixed-point scale leaves a sum of d (or d^2) over the image, each at most
-  // 1 (plus float32 rounding), below 2^(64 - GF_COUNT_BITS)
+  // the one-launch finish: T or eps positive (the d of finite samples in
+  // [0, 1]; NaN and inf samples flag their image, see gmsd_finish), statistics
+  // only, at most GF_MAX_IMAGES images; the fixed-point scale leaves a sum of d
+  // (or d^2) over the image, each at most 1 (plus float32 rounding), below
+  // 2^(64 - GF_COUNT_BITS)
   const double npix = static_cast<double>(g.Hout) * g.Wout * a.Cout;
-  if (acc && dtype == FA_U8 && !map_out && N <= GF_MAX_IMAGES && (a.T2f > 0.0f || a.eps2f > 0.0f)) {
+  if (acc && !map_out && N <= GF_MAX_IMAGES && (a.T2f > 0.0f || a.eps2f > 0.0f)) {
     int bits = 1;
     while (bits < 40 && std::ldexp(1.0, bits) <= 2.0 * npix) ++bits;
     if (bits < 40) {

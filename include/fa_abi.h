@@ -498,8 +498,10 @@ FA_API int fa_gpu_pixel_reduce_once(const void* a, const void* b, int dtype,
  *     left zero when it completes (state of one stream, like
  *     fa_gpu_pixel_reduce_once's);
  *   out_batch: optional double[2], the batch means of out_mean and out_std.
- * For uint8 input with T or eps positive and N <= 64, the kernel finishes
- * the call itself: each workgroup adds its sums of d = 1 - q and d^2 to
+ * Without the map, with T or eps positive and N <= 64, the kernel finishes
+ * the call itself (any input dtype; a NaN or inf sample flags its image,
+ * whose statistics and the batch means then come out NaN, as the float64
+ * sums would): each workgroup adds its sums of d = 1 - q and d^2 to
  * `acc` as round-to-nearest fixed-point integers (so the result does not
  * depend on the order of the adds) with returning device-scope atomics, and
  * the workgroups that complete an image's sums write its statistics (the

@@ -885,3 +885,48 @@ def test_ms_ssim_training_path_uses_the_head(gpu):
     err = float((x.grad - xr.grad).abs().max() / xr.grad.abs().max())
     assert err <= 1e-12, err
     del functional
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32, torch.float64])
+def test_gmsd_one_launch_floating_input(gpu, dt):
+    """fa_gpu_gmsd_once over floating input finishes in its launch as over
+    uint8: statistics within 1e-12 (mean) / 1e-10 (std) of the two-launch
+    form, the same bits twice, the batch means, the oracle to 1e-6, the
+    accumulator zero; and a NaN or an inf sample makes its image's
+    statistics and the batch means NaN (the two-launch form and the oracle
+    agree) while the other image stays finite."""
+    from frame_analytics_amd import backend
+
+    a, b = u8_pair((3, 3, 200, 264), 9.0, seed=61)
+    x = torch.from_numpy(a).to(gpu).to(dt)
+    y = torch.from_numpy(b).to(gpu).to(dt)
+    T, eps = 170.0, (1e-6 * 255.0) ** 2
+    acc = torch.zeros(backend._ACC_WORDS["gmsd"], dtype=torch.int64, device=gpu)
+    m2, s2, _ = _gmsd_call("fa_gpu_gmsd", x, y, T, eps, True)
+    m1, s1, bt = _gmsd_call("fa_gpu_gmsd_once", x, y, T, eps, True, acc=acc, batch=True)
+    assert not bool(acc.any())
+    assert np.all(np.abs(m1 - m2) <= 1e-12 * np.abs(m2)), (m1, m2)
+    assert np.all(np.abs(s1 - s2) <= 1e-10 * np.abs(s2)), (s1, s2)
+    assert abs(bt[0] - m1.mean()) <= 1e-12 * abs(m1.mean())
+    again = _gmsd_call("fa_gpu_gmsd_once", x, y, T, eps, True, acc=acc, batch=True)
+    for u, v in zip((m1, s1, bt), again):
+        assert np.array_equal(u, v)
+    xo, yo = x.double().cpu().numpy(), y.double().cpu().numpy()
+    m0, s0 = ref.gmsd_stats(xo, yo, 255.0)
+    assert np.all(np.abs(s1 - s0) <= REL * np.abs(s0)) and np.all(np.abs(m1 - m0) <= REL * np.abs(m0))
+    xb = x.clone()
+    xb[0, 1, 50, 60] = float("nan")
+    xb[2, 0, 10, 200] = float("inf")
+    mb, sb, bb = _gmsd_call("fa_gpu_gmsd_once", xb, y, T, eps, True, acc=acc, batch=True)
+    mr, sr, _ = _gmsd_call("fa_gpu_gmsd", xb, y, T, eps, True)
+    assert not bool(acc.any())
+    for got in (mb, sb, mr, sr):
+        assert np.isnan(got[0]) and np.isnan(got[2]) and np.isfinite(got[1])
+    assert np.isnan(bb[0]) and np.isnan(bb[1])
+    assert abs(mb[1] - mr[1]) <= 1e-12 * abs(mr[1]) and abs(sb[1] - sr[1]) <= 1e-10 * abs(sr[1])
+    with np.errstate(invalid="ignore"):
+        mo, so = ref.gmsd_stats(xb.double().cpu().numpy(), yo, 255.0)
+    assert np.isnan(mo[0]) and np.isnan(so[2])
+    # a clean call after them on the same accumulator
+    mc, sc, _ = _gmsd_call("fa_gpu_gmsd_once", x, y, T, eps, True, acc=acc)
+    assert np.array_equal(mc, m1) and np.array_equal(sc, s1)
