@@ -35,6 +35,7 @@ import contextlib
 import ctypes
 import functools
 import os
+import threading
 import warnings
 from collections import Counter
 from typing import Any, Optional
@@ -357,9 +358,9 @@ _ACC_WORDS = {"pixel": (32 + 1) * 16, "gmsd": (3 * 64 + 2) * 16, "ssim": (256 + 
               "ms": (8 * 256 + 1) * 16}
 #: (kind, device, raw stream) -> that stream's accumulator, zero between calls
 _stream_acc: dict = {}
-#: (kind, device) -> accumulator of one HIP graph's calls alone (see
-#: private_accumulators); None outside such a scope
-_private_acc: Optional[dict] = None
+#: per thread: (kind, device) -> accumulator of one HIP graph's calls alone
+#: (see private_accumulators); unset outside such a scope
+_private = threading.local()
 
 
 @contextlib.contextmanager
@@ -369,13 +370,15 @@ def private_accumulators(store: dict):
     too.  For a graph whose replays share those buffers with nothing else
     (``StreamingMetrics``: its warm-up and its capture run in this scope, and
     then only its replays use them), so the captured calls can finish in their
-    one launch; each replay leaves them zero, like an eager call."""
-    global _private_acc
-    prev, _private_acc = _private_acc, store
+    one launch; each replay leaves them zero, like an eager call.  The scope
+    is the calling thread's: calls from other threads keep their streams'
+    shared accumulators."""
+    prev = getattr(_private, "store", None)
+    _private.store = store
     try:
         yield store
     finally:
-        _private_acc = prev
+        _private.store = prev
 
 
 def _acc_for(kind: str, device: torch.device, dev: int, stream: int) -> Optional[torch.Tensor]:
@@ -389,7 +392,7 @@ def _acc_for(kind: str, device: torch.device, dev: int, stream: int) -> Optional
     capture runs in :func:`private_accumulators`, whose buffers are the
     graph's alone."""
     capturing = torch._C._cuda_isCurrentStreamCapturing()
-    store = _private_acc
+    store = getattr(_private, "store", None)
     if store is not None:
         acc = store.get((kind, dev))
         if acc is None and not capturing:
@@ -413,7 +416,7 @@ def _forget_acc(acc: Optional[torch.Tensor]) -> None:
     The next call allocates a new, zeroed one."""
     if acc is None:
         return
-    for store in (_stream_acc, _private_acc or {}):
+    for store in (_stream_acc, getattr(_private, "store", None) or {}):
         for key, t in list(store.items()):
             if t is acc:
                 del store[key]

@@ -256,3 +256,23 @@ def test_scale_product_gradient_matches_torch_autograd():
 
 
 MS_W = (0.0448, 0.2856, 0.3001, 0.2363, 0.1333)
+
+
+def test_private_accumulator_scope_is_per_thread():
+    """backend.private_accumulators (a graph's own accumulators) applies to
+    the thread that opened it: another thread's calls meanwhile keep their
+    streams' shared accumulators, and the scope ends with its block."""
+    import threading
+
+    from frame_analytics_amd import backend
+
+    seen = {}
+    mine: dict = {}
+    with backend.private_accumulators(mine):
+        assert getattr(backend._private, "store", None) is mine
+        t = threading.Thread(target=lambda: seen.setdefault(
+            "other", getattr(backend._private, "store", None)))
+        t.start()
+        t.join()
+    assert seen["other"] is None
+    assert getattr(backend._private, "store", None) is None
