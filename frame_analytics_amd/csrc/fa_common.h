@@ -290,15 +290,17 @@ inline bool ssim_fin_scale(SsimFin& f) {
 
 // Thread-level: workgroup sum `s` of image `img`, whose words take
 // `wg_per_image` contributions.
-// Sets the flag word `flag` and waits for the atomic's return, so that it is
-// performed before anything the thread issues after.
-__device__ inline void ssim_fin_flag(uint64_t* flag) {
+// The NaN flags of the one-launch finishes (SSIM here, GMSD in fa_gmsd.hip).
+// fin_flag_set sets flag word `flag` and waits for the atomic's return, so
+// that it is performed before anything the thread issues after it;
+// fin_flag_take reads and clears it.
+__device__ inline void fin_flag_set(uint64_t* flag) {
   const uint64_t r = __hip_atomic_fetch_or(flag, uint64_t(1), __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("" ::"v"(r));  // the value is used: the add below issues after it is back
+  asm volatile("" ::"v"(r));  // the value is used: what follows issues after it is back
 }
 
-__device__ inline bool ssim_fin_flagged(uint64_t* flag) {
+__device__ inline bool fin_flag_take(uint64_t* flag) {
   return __hip_atomic_exchange(flag, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
@@ -309,26 +311,26 @@ __device__ inline void ssim_fin_add(const SsimFin& f, int img, int wg_per_image,
   constexpr double NaN = __builtin_nan("");
   uint64_t* w = f.acc + static_cast<int64_t>(img) * SSIM_FIN_STRIDE;
   const bool finite = __builtin_isfinite(s);
-  if (!finite) ssim_fin_flag(w + 1);
+  if (!finite) fin_flag_set(w + 1);
   const int64_t q = finite ? __double2ll_rn(s * f.fscale) : 0;
   const uint64_t old = __hip_atomic_fetch_add(
       w, (static_cast<uint64_t>(q) << SSIM_FIN_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
       __HIP_MEMORY_SCOPE_AGENT);
   if ((old & CM) + 1u != static_cast<uint64_t>(wg_per_image)) return;
   __hip_atomic_store(w, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const bool nan_img = ssim_fin_flagged(w + 1);
+  const bool nan_img = fin_flag_take(w + 1);
   const int64_t tot = (static_cast<int64_t>(old) >> SSIM_FIN_COUNT_BITS) + q;
   if (f.out_per_image)
     f.out_per_image[img] = nan_img ? NaN : static_cast<double>(tot) * f.finv / f.npix_img;
   if (!f.out_total) return;
   uint64_t* wb = f.acc + static_cast<int64_t>(SSIM_FIN_MAX_IMAGES) * SSIM_FIN_STRIDE;
-  if (nan_img) ssim_fin_flag(wb + 1);
+  if (nan_img) fin_flag_set(wb + 1);
   const uint64_t ob = __hip_atomic_fetch_add(
       wb, (static_cast<uint64_t>(tot) << SSIM_FIN_COUNT_BITS) + 1u, __ATOMIC_RELAXED,
       __HIP_MEMORY_SCOPE_AGENT);
   if ((ob & CM) + 1u != static_cast<uint64_t>(f.N)) return;
   __hip_atomic_store(wb, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const bool nan_all = ssim_fin_flagged(wb + 1);
+  const bool nan_all = fin_flag_take(wb + 1);
   const int64_t all = (static_cast<int64_t>(ob) >> SSIM_FIN_COUNT_BITS) + tot;
   *f.out_total = nan_all ? NaN : static_cast<double>(all) * f.finv / f.npix_all;
 }

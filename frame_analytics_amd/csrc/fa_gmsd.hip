@@ -586,13 +586,7 @@ __device__ inline uint64_t gf_swap(uint64_t* p, uint64_t v) {
 __device__ inline void gf_zero(uint64_t* p) {
   __hip_atomic_store(p, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Sets flag word p and waits for the atomic's return, so that it is performed
-// before anything the thread issues after it.
-__device__ inline void gf_flag(uint64_t* p) {
-  const uint64_t r = __hip_atomic_fetch_or(p, uint64_t(1), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("" ::"v"(r));
-}
+
 
 // Mean q and population std q of an image from its sums of d = 1 - q.  A NaN
 // variance (a NaN q, e.g. a flat patch with T = eps = 0) stays NaN.
@@ -611,7 +605,7 @@ __device__ inline void gmsd_finish(const GmsdArgs& a, int n, int which, double v
   uint64_t* w = a.acc + static_cast<int64_t>(3 * n + which) * GF_STRIDE;
   uint64_t* meet = a.acc + static_cast<int64_t>(3 * n + 2) * GF_STRIDE;
   const bool finite = __builtin_isfinite(v);
-  if (!finite) gf_flag(meet + 1);
+  if (!finite) fin_flag_set(meet + 1);
   const uint64_t f = finite ? static_cast<uint64_t>(__double2ll_rn(v * a.fscale)) : 0u;
   const uint64_t old = gf_add(w, (f << GF_COUNT_BITS) + 1u);
   if ((old & CM) + 1u != static_cast<uint64_t>(a.wpi)) return;
@@ -620,7 +614,7 @@ __device__ inline void gmsd_finish(const GmsdArgs& a, int n, int which, double v
   const uint64_t other = gf_swap(meet, mine | GF_PRESENT | (which ? GF_IS_SQ : 0));
   if (!(other & GF_PRESENT)) return;  // the other sum is not complete yet
   gf_zero(meet);
-  const bool nan_img = gf_swap(meet + 1, 0) != 0;
+  const bool nan_img = fin_flag_take(meet + 1);
   const uint64_t ov = other & (GF_IS_SQ - 1);
   const double sd = static_cast<double>(which ? ov : mine) * a.finv;
   const double sd2 = static_cast<double>(which ? mine : ov) * a.finv;
@@ -635,12 +629,12 @@ __device__ inline void gmsd_finish(const GmsdArgs& a, int n, int which, double v
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     uint64_t* b = a.acc + static_cast<int64_t>(3 * GF_MAX_IMAGES + k) * GF_STRIDE;
-    if (nan_img) gf_flag(b + 1);
+    if (nan_img) fin_flag_set(b + 1);
     const uint64_t fb = nan_img ? 0u : static_cast<uint64_t>(__double2ll_rn(r[k] * bs));
     const uint64_t ob = gf_add(b, (fb << GF_COUNT_BITS) + 1u);
     if ((ob & CM) + 1u != static_cast<uint64_t>(a.N)) continue;
     gf_zero(b);
-    const bool nan_all = gf_swap(b + 1, 0) != 0;
+    const bool nan_all = fin_flag_take(b + 1);
     a.out_batch[k] = nan_all ? NaN : static_cast<double>((ob >> GF_COUNT_BITS) + fb) / bs / a.N;
   }
 }
