@@ -59,3 +59,43 @@ def test_random_shapes(gpu, seed):
         gm = fa.gms(x, y, data_range=255.0, reduction="none").cpu().numpy()
         assert np.all(np.abs(gs - s) <= REL * np.abs(s)), (shape, gs, s)
         assert np.all(np.abs(gm - m) <= REL * np.abs(m)), (shape, gm, m)
+
+
+_FLOATS = [torch.float16, torch.bfloat16, torch.float32, torch.float64]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_floating(gpu, seed):
+    """Floating input over seeded random shapes, through the public calls,
+    which hand the stream's accumulator to the one-launch finishes (the SSIM
+    strip kernel's, GMSD's): a random dtype, sometimes a cropped view, and for
+    three channels sometimes BT.601 luma formed in the kernel; SSIM and GMSD
+    per image within 1e-6 of the oracle on the same (rounded) samples, and the
+    accumulators zero afterwards."""
+    from frame_analytics_amd import backend
+
+    rng = np.random.default_rng(5000 + seed)
+    a, b = _case(seed + 40)
+    dt = _FLOATS[int(rng.integers(0, len(_FLOATS)))]
+    x = torch.from_numpy(a).to(gpu).to(dt)
+    y = torch.from_numpy(b).to(gpu).to(dt)
+    if seed % 3 == 1 and x.shape[-2] > 20 and x.shape[-1] > 20:
+        x, y = x[..., 2:-3, 1:-2], y[..., 2:-3, 1:-2]  # views, read in place
+    luma = "bt601" if (x.shape[1] == 3 and seed % 2 == 0) else None
+    xo, yo = x.double().cpu().numpy(), y.double().cpu().numpy()
+    if luma:
+        xo, yo = ref.rgb_to_luma(xo, "bt601"), ref.rgb_to_luma(yo, "bt601")
+    got = fa.ssim(x, y, data_range=255.0, reduction="none", luma=luma).cpu().numpy()
+    want = ref.ssim(xo, yo, 255.0, reduction="none")
+    assert np.all(np.abs(got - want) <= REL * np.abs(want)), (dt, x.shape, luma, got, want)
+    if x.shape[-2] >= 6 and x.shape[-1] >= 6:
+        m, s = ref.gmsd_stats(xo, yo, 255.0)
+        gs = fa.gmsd(x, y, data_range=255.0, reduction="none", luma=luma).cpu().numpy()
+        gm = fa.gms(x, y, data_range=255.0, reduction="none", luma=luma).cpu().numpy()
+        assert np.all(np.abs(gs - s) <= REL * np.abs(s)), (dt, x.shape, luma, gs, s)
+        assert np.all(np.abs(gm - m) <= REL * np.abs(m)), (dt, x.shape, luma, gm, m)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream().cuda_stream
+    for kind in ("ssim", "gmsd"):
+        acc = backend._stream_acc.get((kind, 0, st))
+        assert acc is None or not bool(acc.any()), kind
