@@ -79,7 +79,11 @@ def compile_flags() -> List[str]:
              # CDNA4 packed-FP32 forms stay off: plain float code only.
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              # MFMA accumulators in VGPRs: no v_accvgpr_read copies before the VALU uses them
-             "-mllvm", "-amdgpu-mfma-vgpr-form"]
+             "-mllvm", "-amdgpu-mfma-vgpr-form",
+             # every device atomic here is issued by one lane at an address of
+             # its own: the wave-aggregating atomic optimizer only wraps each in a
+             # readfirstlane and a wait, serialising the finishes' returning atomics
+             "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
     for a in archs():
         flags.append(f"--offload-arch={a}")
     return flags

@@ -625,17 +625,25 @@ __device__ inline void gmsd_finish(const GmsdArgs& a, int n, int which, double v
   a.out_std[n] = sq;
   if (!a.out_batch) return;
   const double bs = static_cast<double>(uint64_t(1) << GF_BATCH_BITS);
-  double r[2] = {mq, sq};
+  const double r[2] = {mq, sq};
+  uint64_t* b[2];
+  uint64_t fb[2], ob[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    uint64_t* b = a.acc + static_cast<int64_t>(3 * GF_MAX_IMAGES + k) * GF_STRIDE;
-    if (nan_img) fin_flag_set(b + 1);
-    const uint64_t fb = nan_img ? 0u : static_cast<uint64_t>(__double2ll_rn(r[k] * bs));
-    const uint64_t ob = gf_add(b, (fb << GF_COUNT_BITS) + 1u);
-    if ((ob & CM) + 1u != static_cast<uint64_t>(a.N)) continue;
-    gf_zero(b);
-    const bool nan_all = fin_flag_take(b + 1);
-    a.out_batch[k] = nan_all ? NaN : static_cast<double>((ob >> GF_COUNT_BITS) + fb) / bs / a.N;
+    b[k] = a.acc + static_cast<int64_t>(3 * GF_MAX_IMAGES + k) * GF_STRIDE;
+    if (nan_img) fin_flag_set(b[k] + 1);
+    fb[k] = nan_img ? 0u : static_cast<uint64_t>(__double2ll_rn(r[k] * bs));
+  }
+  // both batch adds in flight at once: neither waits for the other's return
+#pragma unroll
+  for (int k = 0; k < 2; ++k) ob[k] = gf_add(b[k], (fb[k] << GF_COUNT_BITS) + 1u);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if ((ob[k] & CM) + 1u != static_cast<uint64_t>(a.N)) continue;
+    gf_zero(b[k]);
+    const bool nan_all = fin_flag_take(b[k] + 1);
+    a.out_batch[k] =
+        nan_all ? NaN : static_cast<double>((ob[k] >> GF_COUNT_BITS) + fb[k]) / bs / a.N;
   }
 }
 
