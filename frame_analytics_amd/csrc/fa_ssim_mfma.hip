@@ -1195,11 +1195,14 @@ int dispatch(int src, int mode, bool launch, dim3 grid, hipStream_t st, const Mf
 namespace {
 
 // The layout checks every matrix-core launch shares: rows and planes aligned
-// to 8 samples, 8-byte (uint8) or 16-byte (levels) aligned bases, 16-byte
+// to 8 samples, 4-byte (uint8) or 16-byte (levels) aligned bases, 16-byte
 // aligned pyramid outputs, K <= 16, and the 32-bit offsets within a plane.
+// uint8 samples are read as 8-byte buffer loads at multiples of 8 bytes from
+// the base, so a 4-byte aligned base (a crop of 4 pixels, say) keeps every
+// load dword-aligned, which is all a multi-dword buffer access requires.
 bool mfma_fits(const SsimMfmaCall& c, int src, int mode) {
   if (c.K > MF_MAX_K || c.W % 8 != 0 || c.W < 8) return false;
-  const uintptr_t base_align = src == SRC_U8 ? 7 : 15;
+  const uintptr_t base_align = src == SRC_U8 ? 3 : 15;
   if ((reinterpret_cast<uintptr_t>(c.x) | reinterpret_cast<uintptr_t>(c.y)) & base_align)
     return false;
   if (c.px && ((reinterpret_cast<uintptr_t>(c.px) | reinterpret_cast<uintptr_t>(c.py)) & 15))

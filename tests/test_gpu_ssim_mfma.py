@@ -154,16 +154,44 @@ def test_data_range(gpu, L):
 
 
 def test_views_aligned_and_not(gpu):
-    # crops read in place: an 8-aligned crop stays on the matrix cores,
-    # a 4-pixel one moves to the strip kernel; both match the oracle
+    # crops read in place: crops of 8 and 4 pixels (bases 8- and 4-byte
+    # aligned, widths multiples of 8) stay on the matrix cores, so each gives
+    # the bits of the same crop copied out contiguously; a 2-pixel crop (width
+    # 156) moves to the strip kernel; all match the oracle
     a, b = u8_pair((2, 3, 96, 160), 9.0, seed=13)
     x = torch.as_tensor(a, device=gpu)
     y = torch.as_tensor(b, device=gpu)
-    for c in (8, 4):
+    for c in (8, 4, 2):
         want = ref.ssim(a[..., c:-c, c:-c], b[..., c:-c, c:-c], 255.0, reduction="none")
         got = fa.ssim(x, y, data_range=255.0, crop_border=c, reduction="none").cpu().numpy()
         for g, w in zip(got, want):
             assert _rel(float(g), float(w)) <= REL, (c, g, w)
+        if c % 4 == 0:
+            xc = x[..., c:-c, c:-c].contiguous()
+            yc = y[..., c:-c, c:-c].contiguous()
+            copy = fa.ssim(xc, yc, data_range=255.0, reduction="none").cpu().numpy()
+            assert np.array_equal(got, copy), (c, got, copy)
+            with _VectorAlu():
+                alu = fa.ssim(x, y, data_range=255.0, crop_border=c,
+                              reduction="none").cpu().numpy()
+            assert not np.array_equal(got, alu), c  # the strip kernel's bits differ
+
+
+def test_ms_ssim_four_pixel_crop_in_place(gpu):
+    # a 4-pixel crop of 264-wide frames: a 4-byte aligned base, and every
+    # scale's width (256 .. 16) a multiple of 8, so the crop read in place
+    # takes the three-launch matrix-core path and gives the bits of the
+    # contiguous copy
+    a, b = u8_pair((2, 3, 200, 264), 9.0, seed=21)
+    x = torch.as_tensor(a, device=gpu)
+    y = torch.as_tensor(b, device=gpu)
+    got = fa.ms_ssim(x, y, data_range=255.0, crop_border=4, reduction="none").cpu().numpy()
+    copy = fa.ms_ssim(x[..., 4:-4, 4:-4].contiguous(), y[..., 4:-4, 4:-4].contiguous(),
+                      data_range=255.0, reduction="none").cpu().numpy()
+    assert np.array_equal(got, copy), (got, copy)
+    want = ref.ms_ssim(a[..., 4:-4, 4:-4], b[..., 4:-4, 4:-4], 255.0, reduction="none")
+    for g, w in zip(got, want):
+        assert _rel(float(g), float(w)) <= REL, (g, w)
 
 
 # MS-SSIM over uint8: scale 0 (SSIM and cs sums plus the first pyramid level,
