@@ -288,8 +288,6 @@ inline bool ssim_fin_scale(SsimFin& f) {
   return bits < 40;
 }
 
-// Thread-level: workgroup sum `s` of image `img`, whose words take
-// `wg_per_image` contributions.
 // The NaN flags of the one-launch finishes (SSIM here, GMSD in fa_gmsd.hip).
 // fin_flag_set sets flag word `flag` and waits for the atomic's return, so
 // that it is performed before anything the thread issues after it;
