@@ -99,3 +99,40 @@ def test_random_shapes_floating(gpu, seed):
     for kind in ("ssim", "gmsd"):
         acc = backend._stream_acc.get((kind, 0, st))
         assert acc is None or not bool(acc.any()), kind
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_uint8_views(gpu, seed):
+    """uint8 views cut from larger frames at random offsets, read in place: a
+    base aligned to 1, 2, 4 or 8 bytes, a width that is a multiple of 8 or
+    not.  SSIM per image within 1e-6 of the oracle, PSNR to 1e-12; where the
+    base is 4-byte aligned and the width a multiple of 8 the view takes the
+    matrix-core kernel, as its contiguous copy does, and the two agree bit
+    for bit."""
+    rng = np.random.default_rng(7000 + seed)
+    n = int(rng.integers(1, 3))
+    c = int(rng.choice([1, 3]))
+    H0 = int(rng.integers(30, 140))
+    W0 = 8 * int(rng.integers(6, 40))
+    a = rng.integers(0, 256, (n, c, H0, W0)).astype(np.float64)
+    b = np.clip(a + rng.normal(0.0, 6.0, a.shape), 0, 255).round()
+    a, b = a.astype(np.uint8), b.astype(np.uint8)
+    top = int(rng.integers(0, 8))
+    left = [0, 4, 2, 1, 4, 3, 0, 4, 6, 4][seed]
+    w = W0 - left - int(rng.integers(0, 16))
+    if seed % 2 == 0:
+        w -= w % 8  # a multiple of 8
+    h = H0 - top - int(rng.integers(0, 8))
+    xv = torch.from_numpy(a).to(gpu)[..., top:top + h, left:left + w]
+    yv = torch.from_numpy(b).to(gpu)[..., top:top + h, left:left + w]
+    av, bv = a[..., top:top + h, left:left + w], b[..., top:top + h, left:left + w]
+    got = fa.ssim(xv, yv, data_range=255.0, reduction="none").cpu().numpy()
+    want = ref.ssim(av, bv, 255.0, reduction="none")
+    assert np.all(np.abs(got - want) <= REL * np.abs(want)), (left, w, got, want)
+    if left % 4 == 0 and w % 8 == 0:
+        copy = fa.ssim(xv.contiguous(), yv.contiguous(), data_range=255.0,
+                       reduction="none").cpu().numpy()
+        assert np.array_equal(got, copy), (left, w, got, copy)
+    pw = ref.psnr(av, bv, 255.0, reduction="none")
+    pg = fa.psnr(xv, yv, data_range=255.0, reduction="none").cpu().numpy()
+    assert np.all(np.abs(pg - pw) <= 1e-12 * np.abs(pw)), (left, w, pg, pw)
